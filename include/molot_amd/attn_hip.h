@@ -1,0 +1,152 @@
+/*
+ * molot_amd: MI355X (gfx950) fused RoPE + GQA decode attention, C ABI.
+ *
+ * Drop-in boundary for the single-token decode-attention step of the Molot
+ * runtime.  Every entry point takes plain pointers and sizes, is asynchronous
+ * on the HIP stream it is given (`stream` is a hipStream_t; NULL = the null
+ * stream), and returns 0 or a non-zero status (molot_hip_strerror() names
+ * it): no exceptions cross this ABI.  Device buffers are allocated and owned
+ * by the caller; the library never frees or retains them.  The library keeps
+ * one internal workspace per device (split-K partials, grown on demand).
+ *
+ * Layouts (d = head dim, element type fp32 or bf16 per `kv_dtype`):
+ *   q, o            [nq][d] fp32, query head h uses KV head h / (nq/nkv)
+ *   KV cache        token-major [cap][nkv*d]: slot t of head h at
+ *                   t*nkv*d + h*d  (include/molot/attn.h:122-124,
+ *                   include/molot/forward.h:48-51)
+ *   head-major      [nkv][n][d] (include/molot/attn.h:111-112)
+ *   paged           [block][nkv][page][d], block_table[b][max_blocks]
+ *                   (no reference counterpart: the reference cache is not
+ *                   paged)
+ * Semantics (include/molot/attn.h:125-177): n = valid slots after the
+ * append, window <= 0 attends [0, n), otherwise [t0, n) with
+ * t0 = max(0, pos_cur - window + 1); an empty range yields o = 0.
+ */
+#ifndef MOLOT_AMD_ATTN_HIP_H_
+#define MOLOT_AMD_ATTN_HIP_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* KV element types. */
+#define MOLOT_KV_F32 0
+#define MOLOT_KV_BF16 1 /* RNE-rounded as include/molot/quant.h:192-198 */
+
+/* Status codes besides hipError_t values (which are positive). */
+#define MOLOT_OK 0
+#define MOLOT_EINVAL (-22)  /* bad shape / argument */
+#define MOLOT_ENOTSUP (-95) /* shape the kernels are not built for */
+#define MOLOT_ENOSPC (-28)  /* append beyond the cache capacity */
+
+const char* molot_hip_strerror(int status);
+/* Library version string ("molot_amd <major>.<minor>"). */
+const char* molot_hip_version(void);
+
+/* Host-side table: out[i] = 1 / base^(2i/d), i < d/2, computed in fp32 with
+ * powf.  Replaces rope_inv_freq, include/molot/attn.h:31-33 (same formula as
+ * the per-layer table of include/molot/model.h:546). */
+void molot_rope_inv_freq(float base, int d, float* out);
+
+/* In-place RoPE of `nheads` consecutive heads of x[nheads][d] at position
+ * `pos` (NEOX half-split pairs (i, i+d/2), fp32 angle pos*inv_freq[i]).
+ * Replaces rope_apply, include/molot/attn.h:19-28, as called per head at
+ * include/molot/forward.h:556-558 and :566-568.  inv_freq: device [d/2]. */
+int molot_hip_rope_apply(float* x, int nheads, int d, int pos, const float* inv_freq,
+                         void* stream);
+
+/* RoPE prologue + KV append of one decode step:
+ *   rotate q[nq][d] in place; rotate k_new[nkv][d] (input, not modified) and
+ *   store it, with v_new[nkv][d], into slot `slot` of the token-major cache
+ *   K/V (fp32, or bf16 RNE when kv_dtype == MOLOT_KV_BF16).
+ * Replaces include/molot/forward.h:556-558 (rope q), :566-568 (rope k) and
+ * :571-575 (memcpy append).  The capacity check of forward.h:570 ("KV cache
+ * full") is the caller's, as in the reference (see the C++ DeviceKV).
+ * Stream-ordered before any attention launched afterwards on `stream`. */
+int molot_hip_rope_append(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                          int nq, int nkv, int d, int slot, int pos, const float* inv_freq,
+                          int kv_dtype, void* stream);
+
+/* GQA decode attention over the token-major cache [n][nkv*qhd].
+ * Replaces attn_decode_gqa_cache, include/molot/attn.h:125-127 (call site
+ * include/molot/forward.h:589-590); the ThreadPool argument has no
+ * counterpart.  K/V element type per kv_dtype (the reference is fp32). */
+int molot_hip_attn_decode_gqa_cache(const float* Q, const void* K, const void* V, float* O,
+                                    int nq, int nkv, int n, int qhd, float scale, int pos_cur,
+                                    int window, int kv_dtype, void* stream);
+
+/* GQA decode attention over the head-major layout [nkv][n][d], full prefix.
+ * Replaces attn_decode_gqa, include/molot/attn.h:111-120 (the layout of the
+ * reference benchmark, bench/bench.cc:357-383). */
+int molot_hip_attn_decode_gqa(const float* Q, const void* K, const void* V, float* O, int nq,
+                              int nkv, int n, int d, float scale, int kv_dtype, void* stream);
+
+/* Head-major layout with a sliding window.
+ * Replaces attn_decode_gqa_win, include/molot/attn.h:178-187. */
+int molot_hip_attn_decode_gqa_win(const float* Q, const void* K, const void* V, float* O, int nq,
+                                  int nkv, int n, int d, float scale, int pos_cur, int window,
+                                  int kv_dtype, void* stream);
+
+/* One head, contiguous K/V [n][d], with window.
+ * Replaces attn_decode_head_win, include/molot/attn.h:57-101 (and
+ * attn_decode_head, :104-107, with pos_cur = n, window = 0). */
+int molot_hip_attn_decode_head_win(const float* Q, const void* K, const void* V, float* out,
+                                   int n, int d, float scale, int pos_cur, int window,
+                                   int kv_dtype, void* stream);
+
+/* General strided form behind all of the above: row t of KV head h at
+ * element offset t*tok_stride + h*head_stride. */
+int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, float* O, int nq,
+                                  int nkv, int n, int d, int64_t tok_stride, int64_t head_stride,
+                                  float scale, int pos_cur, int window, int kv_dtype,
+                                  void* stream);
+
+/* One full decode layer-step: molot_hip_rope_append into slot `slot`, then
+ * attention over n = slot + 1 at pos_cur = pos.  q is rotated in place and
+ * O receives the attention output.  Replaces the block
+ * include/molot/forward.h:556-591 for a layer that owns its KV. */
+int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                          float* O, int nq, int nkv, int d, int slot, int pos,
+                          const float* inv_freq, float scale, int window, int kv_dtype,
+                          void* stream);
+
+/* Batched decode over a paged cache (continuous batching; no reference
+ * counterpart).  Q/O [B][nq][d] fp32; K/V pages [num_blocks][nkv][page][d];
+ * sequence b attends slots [t0_b, seq_lens[b]) through
+ * block_table[b*max_blocks + t/page], with pos_cur = pos[b] (seq_lens[b]-1
+ * when pos is NULL).  All index arrays are device int32. */
+int molot_hip_attn_decode_paged(const float* Q, const void* K, const void* V, float* O,
+                                const int32_t* block_table, const int32_t* seq_lens,
+                                const int32_t* pos, int B, int max_blocks, int max_seq_len,
+                                int nq, int nkv, int d, int page, float scale, int window,
+                                int kv_dtype, void* stream);
+
+/* RoPE + append for the paged cache: q[B][nq][d] rotated in place at pos[b];
+ * k_new/v_new [B][nkv][d] (k rotated) written to slot seq_lens[b]-1 of
+ * sequence b through its block table. */
+int molot_hip_rope_append_paged(float* q, const float* k_new, const float* v_new, void* K,
+                                void* V, const int32_t* block_table, const int32_t* seq_lens,
+                                const int32_t* pos, int B, int max_blocks, int nq, int nkv, int d,
+                                int page, const float* inv_freq, int kv_dtype, void* stream);
+
+/* Softmax exponential used by the attention kernels, applied elementwise
+ * (x, y device [n]).  Counterpart of exp_avx512_ps, include/molot/norm.h:35-47,
+ * exposed so its accuracy can be checked against the reference's
+ * known-answer points (bench/bench.cc:220-234). */
+int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream);
+
+/* Split-K tuning knob (0 = automatic): tokens per workgroup chunk.  Applies
+ * to subsequent launches from this process. */
+void molot_hip_set_split_chunk(int tokens);
+
+/* Launch geometry the attention entry points would use for a problem:
+ * writes the number of context chunks per KV head and tokens per chunk. */
+int molot_hip_split_plan(int nkv, int n_att, int d, int kv_dtype, int* nchunks, int* chunk);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* MOLOT_AMD_ATTN_HIP_H_ */

@@ -1,0 +1,250 @@
+"""Python host interface of the decode-attention path, over the C ABI.
+
+Names, argument order and meaning follow the reference's C++ interface
+(include/molot/attn.h, include/molot/forward.h) so tests read like the
+reference's own checks; tensors are torch device tensors (torch supplies
+device memory and the current HIP stream, nothing else).  Every call is
+asynchronous on the current stream, like the C ABI.
+
+Shapes are validated here before any pointer crosses the ABI, so a kernel
+never sees a buffer smaller than the shape it is told.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import lib as _lib
+from .lib import KV_BF16, KV_F32, check
+
+__all__ = [
+    "KV_F32", "KV_BF16", "rope_inv_freq", "rope_apply", "rope_append", "attn_decode_gqa_cache",
+    "attn_decode_gqa", "attn_decode_gqa_win", "attn_decode_head", "attn_decode_head_win",
+    "attn_decode_strided", "decode_step", "attn_decode_paged", "rope_append_paged", "vexp",
+    "split_plan", "set_split_chunk", "KVCache", "kv_dtype_of",
+]
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _need(t: torch.Tensor, name: str, dtype=None, min_numel: int = 0) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a device tensor, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if dtype is not None and t.dtype not in (dtype if isinstance(dtype, tuple) else (dtype,)):
+        raise TypeError(f"{name}: dtype {t.dtype} not supported")
+    if t.numel() < min_numel:
+        raise ValueError(f"{name}: holds {t.numel()} elements, shape needs {min_numel}")
+
+
+def kv_dtype_of(t: torch.Tensor) -> int:
+    """KV element code of a cache tensor (fp32, or bf16 stored as bf16/int16 bits)."""
+    if t.dtype == torch.float32:
+        return KV_F32
+    if t.dtype in (torch.bfloat16, torch.int16, torch.uint16):
+        return KV_BF16
+    raise TypeError(f"KV cache dtype {t.dtype} not supported (float32 or bfloat16)")
+
+
+_KV_DTYPES = (torch.float32, torch.bfloat16, torch.int16, torch.uint16)
+
+
+def rope_inv_freq(base: float, d: int) -> torch.Tensor:
+    """Host fp32 table 1/base^(2i/d), i < d/2 (include/molot/attn.h:31-33)."""
+    out = (ctypes.c_float * (d // 2))()
+    _lib.load().molot_rope_inv_freq(float(base), int(d), out)
+    return torch.tensor(list(out), dtype=torch.float32)
+
+
+def rope_apply(x: torch.Tensor, pos: int, inv_freq: torch.Tensor) -> torch.Tensor:
+    """In-place NEOX RoPE of every head of x[..., d] (include/molot/attn.h:19-28)."""
+    d = x.shape[-1]
+    _need(x, "x", torch.float32)
+    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    nheads = x.numel() // d
+    check(_lib.load().molot_hip_rope_apply(_ptr(x), nheads, d, int(pos), _ptr(inv_freq),
+                                           _stream()), "rope_apply")
+    return x
+
+
+def rope_append(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq, cap=None):
+    """RoPE q (in place) and k_new, append k/v at `slot` (forward.h:556-575)."""
+    kvd = kv_dtype_of(K)
+    cap = K.numel() // (nkv * d) if cap is None else cap
+    if slot < 0 or slot >= cap:
+        raise RuntimeError("fwd: KV cache full")  # forward.h:570
+    _need(q, "q", torch.float32, nq * d)
+    _need(k_new, "k_new", torch.float32, nkv * d)
+    _need(v_new, "v_new", torch.float32, nkv * d)
+    _need(K, "K", _KV_DTYPES, (slot + 1) * nkv * d)
+    _need(V, "V", K.dtype, (slot + 1) * nkv * d)
+    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    check(_lib.load().molot_hip_rope_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V),
+                                            nq, nkv, d, int(slot), int(pos), _ptr(inv_freq), kvd,
+                                            _stream()), "rope_append")
+
+
+def attn_decode_strided(Q, K, V, O, nq, nkv, n, d, tok_stride, head_stride, scale, pos_cur,
+                        window):
+    """Attention with row t of KV head h at t*tok_stride + h*head_stride."""
+    kvd = kv_dtype_of(K)
+    _need(Q, "Q", torch.float32, nq * d)
+    _need(O, "O", torch.float32, nq * d)
+    if n > 0:
+        span = (n - 1) * tok_stride + (nkv - 1) * head_stride + d
+        _need(K, "K", _KV_DTYPES, span)
+        _need(V, "V", K.dtype, span)
+    check(_lib.load().molot_hip_attn_decode_strided(
+        _ptr(Q), _ptr(K), _ptr(V), _ptr(O), nq, nkv, int(n), d, int(tok_stride), int(head_stride),
+        float(scale), int(pos_cur), int(window), kvd, _stream()), "attn_decode")
+    return O
+
+
+def attn_decode_gqa_cache(Q, K, V, O, nq, nkv, n, qhd, scale, pos_cur, window):
+    """GQA decode over the token-major cache [n][nkv*qhd] (attn.h:125-177)."""
+    return attn_decode_strided(Q, K, V, O, nq, nkv, n, qhd, nkv * qhd, qhd, scale, pos_cur,
+                               window)
+
+
+def attn_decode_gqa(Q, K, V, O, nq, nkv, n, d, scale):
+    """GQA decode over the head-major layout [nkv][n][d] (attn.h:111-120)."""
+    return attn_decode_strided(Q, K, V, O, nq, nkv, n, d, d, n * d, scale, n, 0)
+
+
+def attn_decode_gqa_win(Q, K, V, O, nq, nkv, n, d, scale, pos_cur, window):
+    """Head-major GQA decode with a sliding window (attn.h:178-187)."""
+    return attn_decode_strided(Q, K, V, O, nq, nkv, n, d, d, n * d, scale, pos_cur, window)
+
+
+def attn_decode_head_win(Q, K, V, out, n, d, scale, pos_cur, window):
+    """One head over contiguous K/V [n][d] (attn.h:57-101)."""
+    return attn_decode_strided(Q, K, V, out, 1, 1, n, d, d, n * d, scale, pos_cur, window)
+
+
+def attn_decode_head(Q, K, V, out, n, d, scale):
+    """One head, full prefix (attn.h:104-107)."""
+    return attn_decode_head_win(Q, K, V, out, n, d, scale, n if n > 0 else 0, 0)
+
+
+def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale, window):
+    """forward.h:556-591 for one layer: rope + append at `slot`, attention over slot+1."""
+    rope_append(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq)
+    _need(O, "O", torch.float32, nq * d)
+    return attn_decode_gqa_cache(q, K, V, O, nq, nkv, slot + 1, d, scale, pos, window)
+
+
+def _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V):
+    _need(block_table, "block_table", torch.int32, B * max_blocks)
+    _need(seq_lens, "seq_lens", torch.int32, B)
+    if pos is not None:
+        _need(pos, "pos", torch.int32, B)
+    nblocks = K.numel() // (nkv * page * d)
+    _need(K, "K", _KV_DTYPES, nblocks * nkv * page * d)
+    _need(V, "V", K.dtype, nblocks * nkv * page * d)
+    # host-side bounds check of every block id a kernel can reach
+    lens = seq_lens.cpu()
+    if int(lens.min()) < 0 or int(lens.max()) > max_blocks * page:
+        raise ValueError("seq_lens outside [0, max_blocks*page]")
+    bt = block_table.view(B, max_blocks).cpu()
+    for b in range(B):
+        used = (int(lens[b]) + page - 1) // page
+        if used and (int(bt[b, :used].min()) < 0 or int(bt[b, :used].max()) >= nblocks):
+            raise ValueError(f"block_table row {b} names a block outside the pool")
+    return int(lens.max()) if B else 0
+
+
+def attn_decode_paged(Q, K, V, O, block_table, seq_lens, pos, B, max_blocks, nq, nkv, d, page,
+                      scale, window=0):
+    """Batched decode over a paged cache [blocks][nkv][page][d] (no reference counterpart)."""
+    kvd = kv_dtype_of(K)
+    _need(Q, "Q", torch.float32, B * nq * d)
+    _need(O, "O", torch.float32, B * nq * d)
+    max_len = _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V)
+    check(_lib.load().molot_hip_attn_decode_paged(
+        _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(block_table), _ptr(seq_lens), _ptr(pos), B,
+        max_blocks, max_len, nq, nkv, d, page, float(scale), int(window), kvd, _stream()),
+        "attn_decode_paged")
+    return O
+
+
+def rope_append_paged(q, k_new, v_new, K, V, block_table, seq_lens, pos, B, max_blocks, nq, nkv,
+                      d, page, inv_freq):
+    """RoPE + append of one token per sequence into its page slot seq_lens[b]-1."""
+    kvd = kv_dtype_of(K)
+    _need(q, "q", torch.float32, B * nq * d)
+    _need(k_new, "k_new", torch.float32, B * nkv * d)
+    _need(v_new, "v_new", torch.float32, B * nkv * d)
+    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V)
+    if B and int(seq_lens.min()) < 1:
+        raise ValueError("rope_append_paged: every sequence needs seq_lens >= 1")
+    check(_lib.load().molot_hip_rope_append_paged(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(block_table), _ptr(seq_lens),
+        _ptr(pos), B, max_blocks, nq, nkv, d, page, _ptr(inv_freq), kvd, _stream()),
+        "rope_append_paged")
+
+
+def vexp(x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+    """The attention softmax's exp, elementwise (counterpart of norm.h:35-47)."""
+    _need(x, "x", torch.float32)
+    y = torch.empty_like(x) if y is None else y
+    _need(y, "y", torch.float32, x.numel())
+    check(_lib.load().molot_hip_vexp(_ptr(x), _ptr(y), x.numel(), _stream()), "vexp")
+    return y
+
+
+def split_plan(nkv: int, n_att: int, d: int = 128, kv_dtype: int = KV_F32):
+    nch, ch = ctypes.c_int(), ctypes.c_int()
+    check(_lib.load().molot_hip_split_plan(nkv, n_att, d, kv_dtype, ctypes.byref(nch),
+                                           ctypes.byref(ch)), "split_plan")
+    return nch.value, ch.value
+
+
+def set_split_chunk(tokens: int) -> None:
+    _lib.load().molot_hip_set_split_chunk(int(tokens))
+
+
+class KVCache:
+    """Device KV cache of one layer: [cap][nkv*hd] (forward.h:48-51, 104-110).
+
+    ``append`` mirrors forward.h:566-575 (rope k, copy k/v into slot n, n++),
+    fused with the RoPE of q; ``attend`` is forward.h:589-590.
+    """
+
+    def __init__(self, cap: int, nkv: int, hd: int, kv_dtype: int = KV_F32, device="cuda"):
+        dt = torch.float32 if kv_dtype == KV_F32 else torch.bfloat16
+        self.cap, self.nkv, self.hd, self.n = cap, nkv, hd, 0
+        self.k = torch.zeros(cap * nkv * hd, dtype=dt, device=device)
+        self.v = torch.zeros(cap * nkv * hd, dtype=dt, device=device)
+
+    def reset(self) -> None:
+        self.n = 0  # molot_chat.cc /reset: n = 0
+
+    def append(self, q, k_new, v_new, nq, pos, inv_freq) -> None:
+        if self.n >= self.cap:
+            raise RuntimeError("fwd: KV cache full")
+        rope_append(q, k_new, v_new, self.k, self.v, nq, self.nkv, self.hd, self.n, pos,
+                    inv_freq, cap=self.cap)
+        self.n += 1
+
+    def attend(self, q, O, nq, scale, pos_cur, window=0):
+        if self.n == 0:
+            raise RuntimeError("fwd: shared KV empty")  # forward.h:580
+        return attn_decode_gqa_cache(q, self.k, self.v, O, nq, self.nkv, self.n, self.hd, scale,
+                                     pos_cur, window)
+
+
+def default_scale(d: int) -> float:
+    """1/sqrt(head_dim) (forward.h:170-173 when attn_scale_one is off)."""
+    return 1.0 / math.sqrt(d)

@@ -1,0 +1,76 @@
+"""Build recipes for the native parts of molot_amd (run on the CPU host).
+
+``build_all()`` compiles, in-tree:
+  molot_amd/libmolot_amd.so   HIP kernels + C ABI (hipcc, gfx950)
+  molot_amd/test_attn_cpp     C++ self-check of the header-only C++ layer
+                              (include/molot_amd/attn.hpp), linked to the above
+The oracle (oracle/Makefile) is test infrastructure and is built by
+``__graft_entry__.build()`` next to these, never by the product path.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "molot_amd")
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB = os.path.join(PKG, "libmolot_amd.so")
+CPP_TEST = os.path.join(PKG, "test_attn_cpp")
+ARCH = os.environ.get("MOLOT_OFFLOAD_ARCH", "gfx950")
+
+# Packed-FP32 VALU forms are kept out of the generated code: -packed-fp32-ops.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build molot_amd)")
+
+
+def _run(cmd: list[str]) -> None:
+    print("+", " ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+
+
+def build_library() -> str:
+    srcs = [os.path.join(CSRC, "attn_decode.hip")]
+    tmp = LIB + ".tmp"
+    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+def build_cpp_test() -> str:
+    src = os.path.join(ROOT, "tests", "cpp", "test_attn_cpp.cpp")
+    oracle_inc = os.path.join(ROOT, "oracle")
+    tmp = CPP_TEST + ".tmp"
+    _run([_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{oracle_inc}", src, "-o", tmp,
+          f"-L{PKG}", "-lmolot_amd", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN",
+          os.path.join(ROOT, "oracle", "liboracle.so"),
+          f"-Wl,-rpath,{os.path.join(ROOT, 'oracle')}"])
+    os.replace(tmp, CPP_TEST)
+    return CPP_TEST
+
+
+def build_all() -> None:
+    build_library()
+    if os.path.exists(os.path.join(ROOT, "tests", "cpp", "test_attn_cpp.cpp")):
+        build_cpp_test()
+
+
+if __name__ == "__main__":
+    build_all()
+    sys.exit(0)

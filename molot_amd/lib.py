@@ -1,0 +1,99 @@
+"""ctypes binding of libmolot_amd.so (the C ABI in include/molot_amd/attn_hip.h).
+
+The library is built in-tree by ``__graft_entry__.build()`` (or
+``python -m molot_amd.build``).  There is no fallback: if the library is
+missing, ``load()`` raises, so every caller of the product path fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmolot_amd.so")
+
+KV_F32 = 0
+KV_BF16 = 1
+
+OK = 0
+EINVAL = -22
+ENOTSUP = -95
+ENOSPC = -28
+
+_lock = threading.Lock()
+_lib = None
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_I64 = ctypes.c_int64
+
+# name -> argtypes (all return int status unless listed in _VOID / _STR)
+_SIGS = {
+    "molot_hip_rope_apply": [_P, _I, _I, _I, _P, _P],
+    "molot_hip_rope_append": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _I, _P],
+    "molot_hip_attn_decode_gqa_cache": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P],
+    "molot_hip_attn_decode_gqa": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _P],
+    "molot_hip_attn_decode_gqa_win": [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _P],
+    "molot_hip_attn_decode_head_win": [_P, _P, _P, _P, _I, _I, _F, _I, _I, _I, _P],
+    "molot_hip_attn_decode_strided": [_P, _P, _P, _P, _I, _I, _I, _I, _I64, _I64, _F, _I, _I,
+                                      _I, _P],
+    "molot_hip_decode_step": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _I, _P],
+    "molot_hip_attn_decode_paged": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
+                                    _I, _I, _P],
+    "molot_hip_rope_append_paged": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P,
+                                    _I, _P],
+    "molot_hip_vexp": [_P, _P, _I64, _P],
+    "molot_hip_split_plan": [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)],
+}
+_VOID = {
+    "molot_rope_inv_freq": [_F, _I, ctypes.POINTER(ctypes.c_float)],
+    "molot_hip_set_split_chunk": [_I],
+}
+_STR = {
+    "molot_hip_strerror": [_I],
+    "molot_hip_version": [],
+}
+
+# Every symbol include/molot_amd/attn_hip.h declares.
+EXPORTS = sorted(list(_SIGS) + list(_VOID) + list(_STR))
+
+
+def load() -> ctypes.CDLL:
+    """Load libmolot_amd.so once; raise if it has not been built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"molot_amd: native library not built ({LIB_PATH}); run "
+                "`python -c 'import __graft_entry__ as g; g.build()'`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        for name, args in _VOID.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = None
+        for name, args in _STR.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_char_p
+        _lib = lib
+        return lib
+
+
+class MolotHipError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        msg = load().molot_hip_strerror(status).decode()
+        super().__init__(f"{what}: {msg} (status {status})")
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        raise MolotHipError(status, what)

@@ -1,0 +1,250 @@
+"""CPU oracle for the decode-attention path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this package, and only as the checker (or as the timed CPU baseline);
+the product path (molot_amd) never calls it.
+
+Two native libraries, built by oracle/Makefile:
+  liboracle.so          restatement of the reference algorithm in plain C
+                        (attn_oracle.c, each function citing the reference
+                        file:line it follows) + a float64 brute force
+  _ref/libmolot_ref.so  the reference's own headers compiled where they lie
+                        (ref_shim.cc); optional -- present only where the
+                        reference tree was available at build time, and
+                        usable only on an AVX512F host
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(_HERE, "liboracle.so")
+REF_SO = os.path.join(_HERE, "_ref", "libmolot_ref.so")
+
+KV_F32 = 0
+KV_BF16 = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_D = ctypes.c_double
+_I64 = ctypes.c_int64
+
+_lib = None
+_ref = None
+
+
+def _p(a):
+    return ctypes.c_void_p(0 if a is None else a.ctypes.data)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(ORACLE_SO):
+            raise RuntimeError(f"oracle not built: {ORACLE_SO} (make -C oracle)")
+        L = ctypes.CDLL(ORACLE_SO)
+        sig = {
+            "orc_rope_inv_freq": (None, [_F, _I, _P]),
+            "orc_rope_apply": (None, [_P, _I, _I, _P]),
+            "orc_rope_apply_heads": (None, [_P, _I, _I, _I, _P]),
+            "orc_vexp16": (None, [_P, _P]),
+            "orc_vexp": (None, [_P, _P, _I64]),
+            "orc_dot": (_F, [_P, _P, _I]),
+            "orc_f32_to_bf16_array": (None, [_P, _P, _I64]),
+            "orc_attn_decode": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I, _I64, _I64,
+                                       _I64, _P, _I, _I]),
+            "orc_attn_decode_gqa_cache": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _I]),
+            "orc_attn_decode_paged": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                             _F, _I, _I, _I]),
+            "orc_decode_step": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _I,
+                                       _I]),
+            "orc_attn_decode_f64": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _D, _I, _I, _I, _I64,
+                                           _I64, _I64, _P, _I, _I]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def host_has_avx512f() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            return " avx512f" in f.read()
+    except OSError:
+        return False
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO) and host_has_avx512f()
+
+
+def ref() -> ctypes.CDLL:
+    """The compiled reference headers (raises if unavailable on this host)."""
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError("reference library unavailable (not built, or host lacks AVX512F)")
+        R = ctypes.CDLL(REF_SO)
+        sig = {
+            "ref_pool_create": (_P, [_I]),
+            "ref_pool_destroy": (None, [_P]),
+            "ref_pool_size": (_I, [_P]),
+            "ref_pool_cover": (None, [_P, _I64, _P]),
+            "ref_rope_inv_freq": (None, [_F, _I, _P]),
+            "ref_rope_apply": (None, [_P, _I, _I, _P]),
+            "ref_exp16": (None, [_P, _P]),
+            "ref_dot": (_F, [_P, _P, _I]),
+            "ref_fp32_to_bf16": (ctypes.c_uint16, [_F]),
+            "ref_bf16_to_fp32": (_F, [ctypes.c_uint16]),
+            "ref_attn_decode_head_win": (None, [_P, _P, _P, _P, _I, _I, _F, _I, _I]),
+            "ref_attn_decode_head": (None, [_P, _P, _P, _P, _I, _I, _F]),
+            "ref_attn_decode_gqa": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
+            "ref_attn_decode_gqa_cache": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P]),
+            "ref_attn_decode_gqa_win": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P]),
+            "ref_decode_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _F, _I,
+                                     _P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(R, name)
+            fn.restype = res
+            fn.argtypes = args
+        _ref = R
+    return _ref
+
+
+class RefPool:
+    """The reference's ThreadPool (thread_pool.h:17-126) with n threads."""
+
+    def __init__(self, nthreads: int = 0):
+        self.h = ref().ref_pool_create(int(nthreads))
+
+    def size(self) -> int:
+        return ref().ref_pool_size(self.h)
+
+    def close(self) -> None:
+        if self.h:
+            ref().ref_pool_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+
+# ---------------------------------------------------------------------------
+# restatement (liboracle.so)
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def rope_inv_freq(base: float, d: int) -> np.ndarray:
+    out = np.empty(d // 2, dtype=np.float32)
+    lib().orc_rope_inv_freq(float(base), int(d), _p(out))
+    return out
+
+
+def rope_apply(x: np.ndarray, pos: int, inv_freq: np.ndarray) -> np.ndarray:
+    """Returns a rotated copy of x[..., d] (every head)."""
+    y = _f32(x).copy()
+    d = y.shape[-1]
+    lib().orc_rope_apply_heads(_p(y), y.size // d, d, int(pos), _p(_f32(inv_freq)))
+    return y
+
+
+def vexp(x: np.ndarray) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().orc_vexp(_p(x), _p(y), x.size)
+    return y
+
+
+def dot(a: np.ndarray, b: np.ndarray) -> float:
+    a, b = _f32(a), _f32(b)
+    return float(lib().orc_dot(_p(a), _p(b), a.size))
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_bf16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def _kv_code(K: np.ndarray) -> int:
+    if K.dtype == np.float32:
+        return KV_F32
+    if K.dtype == np.uint16:
+        return KV_BF16
+    raise TypeError(f"KV dtype {K.dtype}: float32 or uint16 (bf16 bits)")
+
+
+def attn_decode(Q, K, V, nq, nkv, n, d, scale, pos_cur, window, tok_stride, head_stride,
+                block_stride=0, block_table=None, page=0, nthreads=0) -> np.ndarray:
+    """fp32 restatement of attn.h:125-177 over a strided / paged K,V."""
+    Q = _f32(Q)
+    K = np.ascontiguousarray(K)
+    V = np.ascontiguousarray(V)
+    bt = None if block_table is None else np.ascontiguousarray(block_table, dtype=np.int32)
+    O = np.empty((nq, d), dtype=np.float32)
+    lib().orc_attn_decode(_p(Q), _p(K), _p(V), _p(O), nq, nkv, int(n), d, float(scale),
+                          int(pos_cur), int(window), _kv_code(K), int(tok_stride),
+                          int(head_stride), int(block_stride), _p(bt), int(page), int(nthreads))
+    return O
+
+
+def attn_decode_gqa_cache(Q, K, V, nq, nkv, n, qhd, scale, pos_cur, window, nthreads=0):
+    return attn_decode(Q, K, V, nq, nkv, n, qhd, scale, pos_cur, window, nkv * qhd, qhd,
+                       nthreads=nthreads)
+
+
+def attn_decode_f64(Q, K, V, nq, nkv, n, d, scale, pos_cur, window, tok_stride, head_stride,
+                    block_stride=0, block_table=None, page=0, nthreads=0) -> np.ndarray:
+    """float64 brute force (formulation of bench/bench.cc:195-213)."""
+    Q = _f32(Q)
+    K = np.ascontiguousarray(K)
+    V = np.ascontiguousarray(V)
+    bt = None if block_table is None else np.ascontiguousarray(block_table, dtype=np.int32)
+    O = np.empty((nq, d), dtype=np.float64)
+    lib().orc_attn_decode_f64(_p(Q), _p(K), _p(V), _p(O), nq, nkv, int(n), d, float(scale),
+                              int(pos_cur), int(window), _kv_code(K), int(tok_stride),
+                              int(head_stride), int(block_stride), _p(bt), int(page),
+                              int(nthreads))
+    return O
+
+
+def attn_decode_paged(Q, Kp, Vp, block_table, seq_lens, pos, B, max_blocks, nq, nkv, d, page,
+                      scale, window=0, nthreads=0) -> np.ndarray:
+    Q = _f32(Q)
+    Kp = np.ascontiguousarray(Kp)
+    Vp = np.ascontiguousarray(Vp)
+    bt = np.ascontiguousarray(block_table, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    ps = None if pos is None else np.ascontiguousarray(pos, dtype=np.int32)
+    O = np.empty((B, nq, d), dtype=np.float32)
+    lib().orc_attn_decode_paged(_p(Q), _p(Kp), _p(Vp), _p(O), _p(bt), _p(sl), _p(ps), B,
+                                max_blocks, nq, nkv, d, page, float(scale), int(window),
+                                _kv_code(Kp), int(nthreads))
+    return O
+
+
+def decode_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, slot, pos, inv_freq, scale, window,
+                nthreads=0):
+    """forward.h:556-591: returns (q_rot, k_rot, O); Kc/Vc are updated in place."""
+    q = _f32(q).copy()
+    k = _f32(k_new).copy()
+    v = _f32(v_new)
+    O = np.empty((nq, d), dtype=np.float32)
+    lib().orc_decode_step(_p(q), _p(k), _p(v), _p(Kc), _p(Vc), _p(O), nq, nkv, d, int(slot),
+                          int(pos), _p(_f32(inv_freq)), float(scale), int(window), _kv_code(Kc),
+                          int(nthreads))
+    return q, k, O

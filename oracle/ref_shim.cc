@@ -1,0 +1,92 @@
+// C-ABI exports over the reference's own header-only implementation.
+//
+// TEST INFRASTRUCTURE ONLY.  This file contains no reference code: it
+// #includes the reference headers where they lie (-I<reference>/include, see
+// oracle/Makefile) and exports their functions unchanged so the restatement
+// in attn_oracle.c can be checked against them, and so bench.py can time the
+// reference's own CPU path as its cpu_baseline.  The built library goes to
+// oracle/_ref/ (git-ignored).
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+
+#include "molot/attn.h"
+#include "molot/norm.h"
+#include "molot/quant.h"
+#include "molot/thread_pool.h"
+
+extern "C" {
+
+void* ref_pool_create(int nthreads) { return new molot::ThreadPool(nthreads); }
+void ref_pool_destroy(void* p) { delete static_cast<molot::ThreadPool*>(p); }
+int ref_pool_size(void* p) { return static_cast<molot::ThreadPool*>(p)->size(); }
+
+// ThreadPool::parallel_for coverage probe (bench/bench.cc:59-66 style):
+// writes 1 into seen[i] for every index the pool visits.
+void ref_pool_cover(void* p, int64_t n, int32_t* seen) {
+  static_cast<molot::ThreadPool*>(p)->parallel_for(n, [&](int, int64_t i) { seen[i] += 1; });
+}
+
+void ref_rope_inv_freq(float base, int d, float* out) { molot::rope_inv_freq(base, d, out); }
+
+void ref_rope_apply(float* x, int d, int pos, const float* inv_freq) {
+  molot::rope_apply(x, d, pos, inv_freq);
+}
+
+void ref_exp16(const float* in, float* out) {
+  _mm512_storeu_ps(out, molot::exp_avx512_ps(_mm512_loadu_ps(in)));
+}
+
+float ref_dot(const float* a, const float* b, int n) { return molot::dot_fp32_avx512(a, b, n); }
+
+uint16_t ref_fp32_to_bf16(float f) { return molot::fp32_to_bf16(f); }
+float ref_bf16_to_fp32(uint16_t b) { return molot::bf16_to_fp32(b); }
+
+void ref_attn_decode_head_win(const float* Q, const float* K, const float* V, float* out, int n,
+                              int d, float scale, int pos_cur, int window) {
+  molot::attn_decode_head_win(Q, K, V, out, n, d, scale, pos_cur, window);
+}
+
+void ref_attn_decode_head(const float* Q, const float* K, const float* V, float* out, int n,
+                          int d, float scale) {
+  molot::attn_decode_head(Q, K, V, out, n, d, scale);
+}
+
+void ref_attn_decode_gqa(const float* Q, const float* K, const float* V, float* O, int nq, int nkv,
+                         int n, int d, float scale, void* pool) {
+  molot::attn_decode_gqa(Q, K, V, O, nq, nkv, n, d, scale,
+                         *static_cast<molot::ThreadPool*>(pool));
+}
+
+void ref_attn_decode_gqa_cache(const float* Q, const float* K, const float* V, float* O, int nq,
+                               int nkv, int n, int qhd, float scale, int pos_cur, int window,
+                               void* pool) {
+  molot::attn_decode_gqa_cache(Q, K, V, O, nq, nkv, n, qhd, scale, pos_cur, window,
+                               *static_cast<molot::ThreadPool*>(pool));
+}
+
+void ref_attn_decode_gqa_win(const float* Q, const float* K, const float* V, float* O, int nq,
+                             int nkv, int n, int d, float scale, int pos_cur, int window,
+                             void* pool) {
+  molot::attn_decode_gqa_win(Q, K, V, O, nq, nkv, n, d, scale, pos_cur, window,
+                             *static_cast<molot::ThreadPool*>(pool));
+}
+
+// The decode-attention block of Runner::forward_token (forward.h:556-591)
+// for one layer with its own KV: rope q heads, rope k heads, append k/v at
+// slot `slot` of the [cap][nkv*d] cache, attention over n = slot + 1.
+// Returns 0, or -1 where forward.h:570 would throw "KV cache full".
+int ref_decode_step(float* q, float* k, const float* v, float* Kc, float* Vc, float* O, int nq,
+                    int nkv, int d, int slot, int cap, int pos, const float* inv_freq, float scale,
+                    int window, void* pool) {
+  for (int hh = 0; hh < nq; ++hh) molot::rope_apply(q + (size_t)hh * d, d, pos, inv_freq);
+  for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(k + (size_t)hh * d, d, pos, inv_freq);
+  if (slot >= cap) return -1;
+  std::memcpy(Kc + (size_t)slot * nkv * d, k, (size_t)nkv * d * 4);
+  std::memcpy(Vc + (size_t)slot * nkv * d, v, (size_t)nkv * d * 4);
+  molot::attn_decode_gqa_cache(q, Kc, Vc, O, nq, nkv, slot + 1, d, scale, pos, window,
+                               *static_cast<molot::ThreadPool*>(pool));
+  return 0;
+}
+
+}  // extern "C"

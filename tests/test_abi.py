@@ -1,0 +1,108 @@
+"""The C ABI boundary, checked on the CPU (no compute call needs a GPU here).
+
+- libmolot_amd.so loads and exports every function include/molot_amd/attn_hip.h
+  declares (and the Python binding knows each one);
+- host-only functions (status strings, version, the RoPE table) work;
+- argument validation rejects bad shapes with status codes before anything
+  touches the device.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from molot_amd import lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "molot_amd", "attn_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(molot_\w+)\s*\(", text)))
+
+
+def test_header_declarations_match_binding():
+    decl = declared_functions()
+    assert decl == sorted(L.EXPORTS), set(decl) ^ set(L.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], check=True,
+                         capture_output=True, text=True).stdout
+    exported = set(re.findall(r" T (\w+)", out))
+    missing = [f for f in declared_functions() if f not in exported]
+    assert not missing, missing
+
+
+def test_library_loads_and_binds():
+    lib = L.load()
+    for name in L.EXPORTS:
+        assert callable(getattr(lib, name))
+    assert lib.molot_hip_version().decode().startswith("molot_amd")
+
+
+def test_status_strings():
+    lib = L.load()
+    assert lib.molot_hip_strerror(0) == b"ok"
+    assert b"invalid" in lib.molot_hip_strerror(L.EINVAL)
+    assert b"unsupported" in lib.molot_hip_strerror(L.ENOTSUP)
+    assert b"full" in lib.molot_hip_strerror(L.ENOSPC)
+
+
+@pytest.mark.parametrize("base,d", [(500000.0, 128), (10000.0, 256), (10000.0, 64)])
+def test_host_inv_freq_matches_oracle(base, d):
+    out = (ctypes.c_float * (d // 2))()
+    L.load().molot_rope_inv_freq(base, d, out)
+    got = np.frombuffer(out, dtype=np.float32)
+    assert np.array_equal(got, oracle.rope_inv_freq(base, d))
+
+
+def _p(v=0x1000):  # a dummy non-null pointer: never dereferenced on these paths
+    return ctypes.c_void_p(v)
+
+
+def test_validation_before_launch():
+    lib = L.load()
+    s = ctypes.c_void_p(0)
+    # nq not a multiple of nkv
+    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 6, 4, 10, 128, 0.1, 9, 0,
+                                               0, s) == L.EINVAL
+    # unknown kv dtype
+    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, 128, 0.1, 9, 0,
+                                               7, s) == L.EINVAL
+    # head dim without kernels
+    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, 96, 0.1, 9, 0,
+                                               0, s) == L.ENOTSUP
+    # null output
+    assert lib.molot_hip_attn_decode_strided(_p(), _p(), _p(), None, 8, 4, 10, 128, 512, 128,
+                                             0.1, 9, 0, 0, s) == L.EINVAL
+    # misaligned K (16-byte vector loads)
+    assert lib.molot_hip_attn_decode_strided(_p(), _p(0x1004), _p(), _p(), 8, 4, 10, 128, 512,
+                                             128, 0.1, 9, 0, 0, s) == L.EINVAL
+    # odd head dim for RoPE, negative slot
+    assert lib.molot_hip_rope_apply(_p(), 4, 127, 3, _p(), s) == L.EINVAL
+    assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 4, 128, -1, 3, _p(), 0,
+                                     s) == L.EINVAL
+    # paged: page size must be a power of two; lengths must fit the table
+    assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 2, 4, 40, 8,
+                                           4, 128, 12, 0.1, 0, 0, s) == L.EINVAL
+    assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 2, 4, 100, 8,
+                                           4, 128, 16, 0.1, 0, 0, s) == L.EINVAL
+    nch, ch = ctypes.c_int(), ctypes.c_int()
+    assert lib.molot_hip_split_plan(0, 10, 128, 0, ctypes.byref(nch), ctypes.byref(ch)) == L.EINVAL
+
+
+def test_python_layer_checks_sizes_without_gpu():
+    """Host-side size checks run before any pointer is passed."""
+    import torch
+    from molot_amd import attn
+
+    cpu = torch.zeros(10)
+    with pytest.raises(ValueError, match="device tensor"):
+        attn.attn_decode_gqa_cache(cpu, cpu, cpu, cpu, 1, 1, 10, 128, 0.1, 9, 0)

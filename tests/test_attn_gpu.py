@@ -1,0 +1,461 @@
+"""Parity of the HIP decode-attention path with the oracle (MI355X only).
+
+Every call goes through the C ABI (molot_amd.attn -> libmolot_amd.so).
+Bars: normwise max|gpu-ref|/max|ref| <= 1e-5 for fp32
+KV; for bf16 KV <= 1e-5 against the oracle run on the same bf16 values and
+<= 2e-2 against the fp32 originals.  RoPE outputs within a few ulp; the KV
+append is bit-exact.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import normwise_err
+from gpu_util import dev, dev_bf16, host, make_decode, oracle_decode, widen
+from molot_amd import attn
+from molot_amd.synth import Stream, bf16_to_f32, f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 2e-2
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden(name):
+    with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def run_decode_gpu(p):
+    """rope+append+attention on the GPU; returns (q_rot, K_after, V_after, O)."""
+    q = dev(p.q)
+    K = dev_bf16(p.K) if p.kv_dtype else dev(p.K)
+    V = dev_bf16(p.V) if p.kv_dtype else dev(p.V)
+    O = torch.empty((p.nq, p.d), dtype=torch.float32, device="cuda")
+    attn.decode_step(q, dev(p.k_new), dev(p.v_new), K, V, O, p.nq, p.nkv, p.d, p.pos, p.pos,
+                     dev(p.inv_freq), p.scale, p.window)
+    if p.kv_dtype:
+        Kh = host(K.view(torch.int16)).view(np.uint16)
+        Vh = host(V.view(torch.int16)).view(np.uint16)
+    else:
+        Kh, Vh = host(K), host(V)
+    return host(q), Kh, Vh, host(O)
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures written from the compiled reference
+
+@pytest.mark.parametrize("name", ["decode_step_g4_d128", "decode_step_win_d256",
+                                  "decode_step_g8_d64_scale1"])
+def test_golden_decode_step(gpu, name):
+    announce(name)
+    g = golden(name)
+    nq, nkv, d, pos = int(g["nq"]), int(g["nkv"]), int(g["d"]), int(g["pos"])
+    K = np.zeros((pos + 1, nkv * d), np.float32)
+    V = np.zeros_like(K)
+    K[:pos], V[:pos] = g["K"], g["V"]
+    q, Kd, Vd = dev(g["q"]), dev(K), dev(V)
+    O = torch.empty((nq, d), dtype=torch.float32, device="cuda")
+    attn.decode_step(q, dev(g["k_new"]), dev(g["v_new"]), Kd, Vd, O, nq, nkv, d, pos, pos,
+                     dev(g["inv_freq"]), float(g["scale"]), int(g["window"]))
+    np.testing.assert_allclose(host(q), g["q_rot"], atol=2e-6)
+    Kh, Vh = host(Kd), host(Vd)
+    np.testing.assert_allclose(Kh[pos], g["k_rot"].reshape(-1), atol=2e-6)
+    np.testing.assert_array_equal(Vh[pos], g["v_new"].reshape(-1))
+    np.testing.assert_array_equal(Kh[:pos], g["K"])  # nothing else written
+    assert normwise_err(host(O), g["O"]) < FP32_TOL
+
+
+def test_golden_head(gpu):
+    g = golden("head_bench_check")
+    n, d = int(g["n"]), int(g["d"])
+    O = torch.empty(d, dtype=torch.float32, device="cuda")
+    attn.attn_decode_head(dev(g["Q"]), dev(g["K"]), dev(g["V"]), O, n, d, float(g["scale"]))
+    o = host(O)
+    assert np.max(np.abs(o - g["O"])) < 1e-3  # bench/bench.cc:216 bar
+    assert normwise_err(o, g["O"]) < FP32_TOL
+
+
+@pytest.mark.parametrize("name", ["gqa_headmajor_d64", "gqa_win_headmajor_d64"])
+def test_golden_headmajor(gpu, name):
+    g = golden(name)
+    nq, nkv, n, d = (int(g[k]) for k in ("nq", "nkv", "n", "d"))
+    O = torch.empty((nq, d), dtype=torch.float32, device="cuda")
+    if int(g["window"]) > 0:
+        attn.attn_decode_gqa_win(dev(g["Q"]), dev(g["K"]), dev(g["V"]), O, nq, nkv, n, d,
+                                 float(g["scale"]), int(g["pos_cur"]), int(g["window"]))
+    else:
+        attn.attn_decode_gqa(dev(g["Q"]), dev(g["K"]), dev(g["V"]), O, nq, nkv, n, d,
+                             float(g["scale"]))
+    assert normwise_err(host(O), g["O"]) < FP32_TOL
+
+
+def test_golden_bf16_cache(gpu):
+    g = golden("bf16_cache_g8_d128")
+    nq, nkv, n, d = (int(g[k]) for k in ("nq", "nkv", "n", "d"))
+    O = torch.empty((nq, d), dtype=torch.float32, device="cuda")
+    attn.attn_decode_gqa_cache(dev(g["Q"]), dev_bf16(g["K_bf16"]), dev_bf16(g["V_bf16"]), O, nq,
+                               nkv, n, d, float(g["scale"]), n - 1, 0)
+    assert normwise_err(host(O), g["O"]) < FP32_TOL
+
+
+@pytest.mark.parametrize("name", ["rope_d128_theta5e5", "rope_d256_theta1e4"])
+def test_golden_rope(gpu, name):
+    g = golden(name)
+    inv = dev(g["inv_freq"])
+    for i, pos in enumerate(g["positions"]):
+        x = dev(g["X"][i])
+        attn.rope_apply(x, int(pos), inv)
+        y = host(x)
+        assert np.max(np.abs(y - g["Y"][i])) <= 4e-7 * max(1.0, float(np.max(np.abs(g["Y"][i]))))
+
+
+def test_vexp_known_answers(gpu):
+    """bench/bench.cc:220-234 on the GPU softmax exp: relerr < 1e-5."""
+    kat = np.array([-87., -20., -10., -5., -3., -2., -1.5, -1., -0.75, -0.5, -0.25, -0.1, -0.01,
+                    0., 1., 50.], np.float32)
+    y = host(attn.vexp(dev(kat)))
+    ref = np.exp(kat.astype(np.float64))
+    assert np.max(np.abs(y - ref) / ref) < 1e-5
+    g = golden("vexp_points")
+    yg = host(attn.vexp(dev(g["X"])))
+    x = g["X"].astype(np.float64)
+    inside = (x >= -87.3) & (x <= 88.0)  # both sides representable as normal floats
+    np.testing.assert_allclose(yg[inside], np.exp(x[inside]), rtol=1e-5)
+
+
+def test_inv_freq_host_table(gpu):
+    for base, d in ((500000.0, 128), (10000.0, 256)):
+        got = attn.rope_inv_freq(base, d).numpy()
+        np.testing.assert_array_equal(got, oracle.rope_inv_freq(base, d))
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs at full size against the oracle
+
+def check_decode(p, tol=FP32_TOL, label=""):
+    q_rot, K_after, V_after, O = run_decode_gpu(p)
+    oq, ok, oO, oK, oV = oracle_decode(p)
+    np.testing.assert_allclose(q_rot, oq, atol=4e-6, rtol=2e-6)
+    np.testing.assert_array_equal(V_after[p.pos], oV[p.pos])
+    if p.kv_dtype == 0:
+        np.testing.assert_allclose(K_after[p.pos], oK[p.pos], atol=4e-6, rtol=2e-6)
+    else:  # bf16 rounding of a value that may differ by an ulp before rounding
+        kd = np.abs(bf16_to_f32(K_after[p.pos]) - bf16_to_f32(oK[p.pos]))
+        assert np.max(kd) <= 8e-3 * max(1.0, float(np.max(np.abs(bf16_to_f32(oK[p.pos])))))
+    np.testing.assert_array_equal(K_after[:p.pos], p.K[:p.pos])
+    err = normwise_err(O, oO)
+    # float64 brute force on the same (rotated, appended) inputs: separates the
+    # kernel's rounding from the fp32 oracle's own sequential-sum rounding
+    f64 = oracle.attn_decode_f64(oq, oK, oV, p.nq, p.nkv, p.pos + 1, p.d, p.scale, p.pos,
+                                 p.window, p.nkv * p.d, p.d)
+    e_gpu, e_orc = normwise_err(O, f64), normwise_err(oO, f64)
+    print(f"{label} normwise err vs oracle {err:.3e}; vs f64: gpu {e_gpu:.3e} oracle {e_orc:.3e}",
+          flush=True)
+    if p.kv_dtype == 0:
+        assert err < tol
+    else:
+        assert err < BF16_TOL  # north_star bar for bf16 KV
+        assert e_gpu < FP32_TOL  # and the kernel itself is fp32-accurate on those values
+    return O
+
+
+def test_c1_llama8b_ctx4096(gpu):
+    announce("c1 32q/8kv/d128 pos 4096 fp32")
+    check_decode(make_decode(32, 8, 128, 4096, base=500000.0), label="c1")
+
+
+def test_c2_llama8b_ctx16384(gpu):
+    announce("c2 32q/8kv/d128 pos 16384 fp32")
+    check_decode(make_decode(32, 8, 128, 16384, base=500000.0), label="c2")
+
+
+def test_c3_sliding_window(gpu):
+    announce("c3 8q/4kv/d256 pos 32768 window 1024 fp32")
+    check_decode(make_decode(8, 4, 256, 32768, base=10000.0, window=1024), label="c3")
+
+
+def test_c5_70b_ctx131072_bf16(gpu):
+    announce("c5 64q/8kv/d128 pos 131072 bf16 sigma 0.5")
+    p = make_decode(64, 8, 128, 131072, base=500000.0, sigma_kv=0.5, bf16=True)
+    O = check_decode(p, label="c5 vs oracle on bf16 values")
+    # against fp32 originals: regenerate them from the same stream positions
+    st = Stream(1234)
+    st.normal((64, 128)), st.normal((8, 128)), st.normal((8, 128))
+    Kf = np.zeros((p.pos + 1, 8 * 128), np.float32)
+    Vf = np.zeros_like(Kf)
+    Kf[:p.pos] = st.normal((p.pos, 1024), 0.5)
+    Vf[:p.pos] = st.normal((p.pos, 1024), 0.5)
+    _, _, Of = oracle.decode_step(p.q, p.k_new, p.v_new, Kf, Vf, 64, 8, 128, p.pos, p.pos,
+                                  p.inv_freq, p.scale, 0)
+    assert normwise_err(O, Of) < BF16_TOL
+
+
+# ---------------------------------------------------------------------------
+# shapes, windows, ragged lengths, chunking
+
+@pytest.mark.parametrize("nq,nkv,d", [(32, 8, 128), (8, 4, 256), (64, 8, 128), (16, 16, 64),
+                                      (24, 8, 128), (16, 1, 128), (32, 2, 64), (12, 4, 256)])
+@pytest.mark.parametrize("pos", [0, 1, 15, 16, 63, 64, 65, 1000, 2049])
+def test_shapes_and_ragged_lengths(gpu, nq, nkv, d, pos):
+    announce(f"shape {nq}/{nkv}/{d} pos {pos}")
+    check_decode(make_decode(nq, nkv, d, pos, seed=pos + 7 * nq + d), label="shape")
+
+
+@pytest.mark.parametrize("window", [1, 2, 17, 64, 1000, 5000])
+def test_windows(gpu, window):
+    announce(f"window {window}")
+    check_decode(make_decode(8, 4, 256, 3000, base=10000.0, window=window, seed=window),
+                 label="window")
+
+
+@pytest.mark.parametrize("chunk", [16, 64, 256, 1024])
+def test_forced_chunk_sizes(gpu, chunk):
+    announce(f"chunk {chunk}")
+    attn.set_split_chunk(chunk)
+    try:
+        check_decode(make_decode(32, 8, 128, 5000, seed=chunk), label=f"chunk{chunk}")
+        check_decode(make_decode(64, 8, 128, 700, seed=chunk + 1, bf16=True), label="bf16")
+    finally:
+        attn.set_split_chunk(0)
+
+
+@pytest.mark.parametrize("nq,nkv,d,pos", [(32, 8, 128, 3000), (8, 1, 64, 999), (8, 4, 256, 555),
+                                          (4, 4, 128, 1)])
+def test_bf16_cache_shapes(gpu, nq, nkv, d, pos):
+    announce(f"bf16 {nq}/{nkv}/{d} pos {pos}")
+    check_decode(make_decode(nq, nkv, d, pos, seed=pos, bf16=True), label="bf16")
+
+
+def test_empty_window_gives_zero(gpu):
+    st = Stream(3)
+    Q = dev(st.normal((4, 128)))
+    K = dev(st.normal((50, 2 * 128)))
+    O = torch.full((4, 128), 7.0, device="cuda")
+    attn.attn_decode_gqa_cache(Q, K, K, O, 4, 2, 50, 128, 0.1, 500, 10)  # t0 = 491 > n
+    assert np.all(host(O) == 0)
+
+
+def test_headmajor_equals_token_major(gpu):
+    st = Stream(4)
+    nq, nkv, d, n = 32, 8, 128, 3333
+    Q = st.normal((nq, d))
+    K = st.normal((n, nkv * d))
+    V = st.normal((n, nkv * d))
+    O1 = torch.empty((nq, d), device="cuda")
+    O2 = torch.empty((nq, d), device="cuda")
+    attn.attn_decode_gqa_cache(dev(Q), dev(K), dev(V), O1, nq, nkv, n, d, 0.088, n - 1, 0)
+    Kh = np.ascontiguousarray(K.reshape(n, nkv, d).transpose(1, 0, 2))
+    Vh = np.ascontiguousarray(V.reshape(n, nkv, d).transpose(1, 0, 2))
+    attn.attn_decode_gqa(dev(Q), dev(Kh), dev(Vh), O2, nq, nkv, n, d, 0.088)
+    o1, o2 = host(O1), host(O2)
+    assert normwise_err(o2, o1) < 1e-6
+    R = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.088, n - 1, 0)
+    assert normwise_err(o1, R) < FP32_TOL
+
+
+# ---------------------------------------------------------------------------
+# size-independent properties at the headline size
+
+def test_properties_at_16k(gpu):
+    announce("properties at n=16385")
+    st = Stream(5)
+    nq, nkv, d, n = 32, 8, 128, 16385
+    Q = st.normal((nq, d))
+    K = st.normal((n, nkv * d))
+    V = np.full((n, nkv * d), -1.25, np.float32)
+    O = torch.empty((nq, d), device="cuda")
+    attn.attn_decode_gqa_cache(dev(Q), dev(K), dev(V), O, nq, nkv, n, d, 0.088, n - 1, 0)
+    np.testing.assert_allclose(host(O), -1.25, rtol=1e-6)  # constant V
+    # GQA mapping: V of kv head j is j+1 everywhere -> O[h] = h//4 + 1
+    Vj = np.repeat(np.arange(1, nkv + 1, dtype=np.float32), d)[None, :].repeat(n, 0)
+    attn.attn_decode_gqa_cache(dev(Q), dev(K), dev(Vj), O, nq, nkv, n, d, 0.088, n - 1, 0)
+    np.testing.assert_allclose(host(O), (np.arange(nq) // 4 + 1)[:, None].repeat(d, 1),
+                               rtol=1e-6)
+    # permutation of (K_t, V_t) pairs
+    V = st.normal((n, nkv * d))
+    perm = st.permutation(n)
+    O2 = torch.empty_like(O)
+    attn.attn_decode_gqa_cache(dev(Q), dev(K), dev(V), O, nq, nkv, n, d, 0.088, n - 1, 0)
+    attn.attn_decode_gqa_cache(dev(Q), dev(K[perm]), dev(V[perm]), O2, nq, nkv, n, d, 0.088,
+                               n - 1, 0)
+    assert normwise_err(host(O2), host(O)) < 2e-6
+    # window == slicing
+    w = 1000
+    attn.attn_decode_gqa_cache(dev(Q), dev(K), dev(V), O, nq, nkv, n, d, 0.088, n - 1, w)
+    attn.attn_decode_gqa_cache(dev(Q), dev(K[n - w:]), dev(V[n - w:]), O2, nq, nkv, w, d, 0.088,
+                               w - 1, 0)
+    assert normwise_err(host(O), host(O2)) < 2e-6
+
+
+def test_non_default_stream(gpu):
+    s = torch.cuda.Stream()
+    p = make_decode(32, 8, 128, 2000, seed=9)
+    with torch.cuda.stream(s):
+        q_rot, _, _, O = run_decode_gpu(p)
+    _, _, oO, _, _ = oracle_decode(p)
+    assert normwise_err(O, oO) < FP32_TOL
+
+
+def test_repeated_calls_are_deterministic(gpu):
+    p = make_decode(32, 8, 128, 4096, seed=10)
+    Q = dev(oracle.rope_apply(p.q, p.pos, p.inv_freq))
+    K, V = dev(p.K), dev(p.V)
+    outs = []
+    for _ in range(3):
+        O = torch.empty((32, 128), device="cuda")
+        attn.attn_decode_gqa_cache(Q, K, V, O, 32, 8, p.pos, 128, p.scale, p.pos - 1, 0)
+        outs.append(host(O))
+    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+
+
+# ---------------------------------------------------------------------------
+# paged, batched (config 4 and smaller)
+
+def make_paged(B, nq, nkv, d, lmin, lmax, page=16, seed=1234, bf16=True, spare_blocks=7):
+    st = Stream(seed)
+    q = st.normal((B, nq, d))
+    k_new = st.normal((B, nkv, d))
+    v_new = st.normal((B, nkv, d))
+    L = st.uniform_int(lmin, lmax, B).astype(np.int32)  # context before the new token
+    n = L + 1
+    blocks = (n + page - 1) // page
+    nblk = int(blocks.sum()) + spare_blocks
+    perm = st.permutation(nblk)
+    max_blocks = int(blocks.max())
+    bt = np.zeros((B, max_blocks), np.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :blocks[b]] = perm[o:o + blocks[b]]
+        o += blocks[b]
+    Kp = st.normal((nblk, nkv, page, d))
+    Vp = st.normal((nblk, nkv, page, d))
+    if bf16:
+        Kp, Vp = f32_to_bf16(Kp), f32_to_bf16(Vp)
+    return dict(q=q, k_new=k_new, v_new=v_new, n=n, bt=bt, Kp=Kp, Vp=Vp, page=page,
+                max_blocks=max_blocks, B=B, nq=nq, nkv=nkv, d=d)
+
+
+def run_paged(P, inv, scale, window=0, pos=None):
+    bf = P["Kp"].dtype == np.uint16
+    K = dev_bf16(P["Kp"]) if bf else dev(P["Kp"])
+    V = dev_bf16(P["Vp"]) if bf else dev(P["Vp"])
+    q = dev(P["q"])
+    bt, sl = dev(P["bt"].reshape(-1)), dev(P["n"])
+    pd = None if pos is None else dev(pos)
+    attn.rope_append_paged(q, dev(P["k_new"]), dev(P["v_new"]), K, V, bt, sl, pd, P["B"],
+                           P["max_blocks"], P["nq"], P["nkv"], P["d"], P["page"], dev(inv))
+    O = torch.empty((P["B"], P["nq"], P["d"]), device="cuda")
+    attn.attn_decode_paged(q, K, V, O, bt, sl, pd, P["B"], P["max_blocks"], P["nq"], P["nkv"],
+                           P["d"], P["page"], scale, window)
+    if bf:
+        Kh = host(K.view(torch.int16)).view(np.uint16)
+        Vh = host(V.view(torch.int16)).view(np.uint16)
+    else:
+        Kh, Vh = host(K), host(V)
+    return host(q), Kh, Vh, host(O)
+
+
+def oracle_paged(P, inv, scale, window=0, pos=None):
+    Kp, Vp = P["Kp"].copy(), P["Vp"].copy()
+    B, nq, nkv, d, page = P["B"], P["nq"], P["nkv"], P["d"], P["page"]
+    q = np.empty_like(P["q"])
+    for b in range(B):
+        n = int(P["n"][b])
+        p = n - 1 if pos is None else int(pos[b])
+        q[b] = oracle.rope_apply(P["q"][b], p, inv)
+        k = oracle.rope_apply(P["k_new"][b], p, inv)
+        slot = n - 1
+        blk = P["bt"][b, slot // page]
+        if Kp.dtype == np.uint16:
+            Kp[blk, :, slot % page] = oracle.f32_to_bf16(k)
+            Vp[blk, :, slot % page] = oracle.f32_to_bf16(P["v_new"][b])
+        else:
+            Kp[blk, :, slot % page] = k
+            Vp[blk, :, slot % page] = P["v_new"][b]
+    O = oracle.attn_decode_paged(q, Kp, Vp, P["bt"], P["n"], pos, B, P["max_blocks"], nq, nkv, d,
+                                 page, scale, window)
+    return q, Kp, Vp, O
+
+
+def test_c4_continuous_batching_paged_bf16(gpu):
+    announce("c4 64 seqs U[512,8192] paged16 shuffled bf16")
+    P = make_paged(64, 32, 8, 128, 512, 8192)
+    inv = oracle.rope_inv_freq(500000.0, 128)
+    s = 1 / math.sqrt(128)
+    q, Kh, Vh, O = run_paged(P, inv, s)
+    oq, oK, oV, oO = oracle_paged(P, inv, s)
+    np.testing.assert_allclose(q, oq, atol=4e-6, rtol=2e-6)
+    np.testing.assert_array_equal(Vh, oV)
+    err = normwise_err(O, oO)
+    print(f"c4 normwise err {err:.3e}", flush=True)
+    assert err < FP32_TOL
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("window", [0, 40])
+def test_paged_small_ragged(gpu, bf16, window):
+    P = make_paged(9, 8, 2, 64, 0, 300, seed=77 + window, bf16=bf16)
+    inv = oracle.rope_inv_freq(10000.0, 64)
+    q, Kh, Vh, O = run_paged(P, inv, 0.125, window)
+    oq, oK, oV, oO = oracle_paged(P, inv, 0.125, window)
+    assert normwise_err(O, oO) < FP32_TOL
+
+
+def test_paged_matches_contiguous(gpu):
+    """The same logical cache through a shuffled block table or contiguous."""
+    st = Stream(6)
+    nq, nkv, d, n, page = 32, 8, 128, 1234, 16
+    Q = st.normal((nq, d))
+    K = st.normal((n, nkv * d))
+    V = st.normal((n, nkv * d))
+    nblk = (n + page - 1) // page
+    perm = st.permutation(nblk)
+    Kp = np.zeros((nblk, nkv, page, d), np.float32)
+    Vp = np.zeros_like(Kp)
+    for i in range(nblk):
+        rows = slice(i * page, min(n, (i + 1) * page))
+        m = rows.stop - rows.start
+        Kp[perm[i], :, :m] = K[rows].reshape(m, nkv, d).transpose(1, 0, 2)
+        Vp[perm[i], :, :m] = V[rows].reshape(m, nkv, d).transpose(1, 0, 2)
+    O1 = torch.empty((nq, d), device="cuda")
+    O2 = torch.empty((1, nq, d), device="cuda")
+    attn.attn_decode_gqa_cache(dev(Q), dev(K), dev(V), O1, nq, nkv, n, d, 0.088, n - 1, 0)
+    attn.attn_decode_paged(dev(Q), dev(Kp), dev(Vp), O2, dev(perm), dev(np.array([n], np.int32)),
+                           None, 1, nblk, nq, nkv, d, page, 0.088)
+    assert normwise_err(host(O2)[0], host(O1)) < 1e-6
+
+
+# ---------------------------------------------------------------------------
+# errors reported through the ABI, never a launch
+
+def test_error_codes(gpu):
+    from molot_amd.lib import MolotHipError
+    st = Stream(8)
+    Q = dev(st.normal((6, 96)))
+    K = dev(st.normal((10, 4 * 96)))
+    O = torch.empty((6, 96), device="cuda")
+    with pytest.raises(MolotHipError) as e:  # nq % nkv != 0
+        attn.attn_decode_gqa_cache(Q, K, K, O, 6, 4, 10, 96, 0.1, 9, 0)
+    assert e.value.status == -22
+    Q2 = dev(st.normal((4, 96)))
+    with pytest.raises(MolotHipError) as e:  # head dim 96 not built
+        attn.attn_decode_gqa_cache(Q2, K, K, O, 4, 4, 10, 96, 0.1, 9, 0)
+    assert e.value.status == -95
+    cache = attn.KVCache(2, 2, 64)
+    inv = dev(oracle.rope_inv_freq(10000.0, 64))
+    q = dev(st.normal((4, 64)))
+    kn = dev(st.normal((2, 64)))
+    cache.append(q, kn, kn, 4, 0, inv)
+    cache.append(q, kn, kn, 4, 1, inv)
+    with pytest.raises(RuntimeError, match="KV cache full"):  # forward.h:570
+        cache.append(q, kn, kn, 4, 2, inv)

@@ -1,0 +1,430 @@
+"""Pin the CPU oracle before it is trusted to judge the GPU path.
+
+Each oracle function is checked against something other than its own
+formula: the reference's known-answer points and attention check
+(bench/bench.cc:186-234), the reference's outputs (golden fixtures written
+from the compiled reference headers, and the compiled reference itself where
+it is available), a float64 brute force, and closed-form invariants chosen so
+that a plausible mistake (wrong RoPE pairing, sign, GQA index, dropped
+window, missing normalisation) fails one of them.
+"""
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import normwise_err
+from molot_amd.synth import Stream, bf16_to_f32, f32_to_bf16
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden(name):
+    with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def kv_token_major(st, n, nkv, d, sigma=1.0):
+    return st.normal((n, nkv * d), sigma), st.normal((n, nkv * d), sigma)
+
+
+# ---------------------------------------------------------------------------
+# a5 vexp: bench/bench.cc:220-234 known-answer points, relerr < 1e-5
+
+KAT = np.array([-87., -20., -10., -5., -3., -2., -1.5, -1., -0.75, -0.5, -0.25, -0.1, -0.01, 0.,
+                1., 50.], np.float32)
+
+
+def test_vexp_known_answers():
+    y = oracle.vexp(KAT)
+    ref = np.exp(KAT.astype(np.float64))
+    rel = np.max(np.abs(y - ref) / (ref + 1e-30))
+    assert rel < 1e-5, rel
+
+
+def test_vexp_golden_points():
+    g = golden("vexp_points")
+    y = oracle.vexp(g["X"])
+    # restated Taylor-5 vs the reference's compiled exp_avx512_ps; the reference
+    # is built with -ffast-math, which flushes denormal results to zero, so
+    # results below FLT_MIN may differ by a denormal
+    np.testing.assert_allclose(y, g["Y"], rtol=2e-7, atol=1.2e-38)
+
+
+def test_vexp_clamps_like_reference():
+    y = oracle.vexp(np.array([-1000., 1000.], np.float32))
+    assert y[0] == pytest.approx(math.exp(-88), rel=1e-5)
+    assert y[1] == pytest.approx(math.exp(88), rel=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# a4 dot
+
+def test_dot_matches_double():
+    st = Stream(5)
+    for n in (1, 15, 16, 17, 128, 131, 256):
+        a, b = st.normal(n), st.normal(n)
+        ref = float(np.dot(a.astype(np.float64), b.astype(np.float64)))
+        assert oracle.dot(a, b) == pytest.approx(ref, rel=1e-5, abs=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# a1/a2 RoPE
+
+def test_inv_freq_closed_form():
+    for base, d in ((500000.0, 128), (10000.0, 256), (10000.0, 64)):
+        got = oracle.rope_inv_freq(base, d)
+        ref = 1.0 / np.power(float(base), 2.0 * np.arange(d // 2) / d)
+        np.testing.assert_allclose(got, ref, rtol=3e-7)
+        assert got[0] == 1.0
+
+
+def rope_f64(x, pos, inv):
+    """NEOX half-split rotation in float64 with the fp32 angle pos*inv_freq."""
+    d = x.shape[-1]
+    h = d // 2
+    ang = (np.float32(pos) * inv.astype(np.float32)).astype(np.float64)
+    c, s = np.cos(ang), np.sin(ang)
+    x = x.astype(np.float64)
+    y = np.empty_like(x)
+    y[..., :h] = x[..., :h] * c - x[..., h:] * s
+    y[..., h:] = x[..., :h] * s + x[..., h:] * c
+    return y
+
+
+def rope_adjacent_f64(x, pos, inv):
+    """The (2i, 2i+1) pairing of the dead qk_dot_rope (attn.h:37-52) -- a planted
+    mistake: the checks below must tell it apart from rope_apply."""
+    ang = (np.float32(pos) * inv.astype(np.float32)).astype(np.float64)
+    c, s = np.cos(ang), np.sin(ang)
+    x = x.astype(np.float64)
+    y = np.empty_like(x)
+    y[..., 0::2] = x[..., 0::2] * c - x[..., 1::2] * s
+    y[..., 1::2] = x[..., 0::2] * s + x[..., 1::2] * c
+    return y
+
+
+@pytest.mark.parametrize("name", ["rope_d128_theta5e5", "rope_d256_theta1e4"])
+def test_rope_golden_and_closed_form(name):
+    g = golden(name)
+    inv = g["inv_freq"]
+    for i, pos in enumerate(g["positions"]):
+        got = oracle.rope_apply(g["X"][i], int(pos), inv)
+        # reference output (compiled rope_apply): within 2 ulp-scale of the data
+        assert np.max(np.abs(got - g["Y"][i])) <= 4e-7 * max(1.0, np.max(np.abs(g["Y"][i])))
+        # closed form in float64 on the same fp32 angle
+        f64 = rope_f64(g["X"][i], int(pos), inv)
+        assert np.max(np.abs(got - f64)) < 2e-6
+        if pos > 0:
+            wrong = rope_adjacent_f64(g["X"][i], int(pos), inv)
+            assert np.max(np.abs(wrong - g["Y"][i])) > 1e-2  # the planted mistake is caught
+
+
+def test_inv_freq_golden_ulps():
+    """The reference table is built under -ffast-math, where GCC may lower
+    pow(base, e) through exp/log; its bits then differ from a correctly
+    rounded powf by an ulp.  The path takes the table as an input, so the
+    drop-in passes the caller's bits through unchanged; the formula only has
+    to agree to ~2 ulp."""
+    for name, base, d in (("rope_d128_theta5e5", 500000.0, 128), ("rope_d256_theta1e4", 10000.0,
+                                                                    256)):
+        g = golden(name)
+        np.testing.assert_allclose(oracle.rope_inv_freq(base, d), g["inv_freq"], rtol=2.5e-7,
+                                   atol=0)
+
+
+def test_rope_invariants():
+    st = Stream(7)
+    d = 128
+    inv = oracle.rope_inv_freq(500000.0, d)
+    x = st.normal((4, d))
+    # pos 0 is the identity, bit for bit
+    assert np.array_equal(oracle.rope_apply(x, 0, inv), x)
+    # each pair's norm is preserved
+    y = oracle.rope_apply(x, 12345, inv)
+    n0 = x[:, :64] ** 2 + x[:, 64:] ** 2
+    n1 = y[:, :64].astype(np.float64) ** 2 + y[:, 64:].astype(np.float64) ** 2
+    np.testing.assert_allclose(n1, n0, rtol=2e-6, atol=1e-6)
+    # <R_p q, R_p' k> depends only on p - p'
+    q, k = st.normal(d), st.normal(d)
+    a = float(np.dot(oracle.rope_apply(q, 100, inv).astype(np.float64),
+                     oracle.rope_apply(k, 37, inv)))
+    b = float(np.dot(oracle.rope_apply(q, 63, inv).astype(np.float64), k))
+    assert a == pytest.approx(b, rel=1e-4, abs=1e-4)
+    # composition R_a R_b = R_{a+b}
+    ab = oracle.rope_apply(oracle.rope_apply(x, 20, inv), 22, inv)
+    np.testing.assert_allclose(ab, oracle.rope_apply(x, 42, inv), atol=2e-5)
+
+
+# ---------------------------------------------------------------------------
+# bf16 rounding (quant.h:192-198)
+
+def test_bf16_rne_points():
+    bits = np.array([0x3F800000, 0x3F808000, 0x3F818000, 0x3F80FFFF, 0x3F808001, 0xBF808000],
+                    np.uint32)
+    want = np.array([0x3F80, 0x3F80, 0x3F82, 0x3F81, 0x3F81, 0xBF80], np.uint16)
+    x = bits.view(np.float32)
+    assert np.array_equal(oracle.f32_to_bf16(x), want)
+    assert np.array_equal(f32_to_bf16(x), want)
+    assert np.array_equal(bf16_to_f32(want), (want.astype(np.uint32) << 16).view(np.float32))
+
+
+def test_bf16_golden_rounding():
+    g = golden("bf16_cache_g8_d128")
+    assert np.array_equal(oracle.f32_to_bf16(g["K_f32"]), g["K_bf16"])
+    assert np.array_equal(f32_to_bf16(g["V_f32"]), g["V_bf16"])
+
+
+# ---------------------------------------------------------------------------
+# a6-a10 attention
+
+def test_attention_bench_check():
+    """bench/bench.cc:186-218: single head, n=512, d=128, N(0,1)*0.2, max-abs < 1e-3
+    against the double-precision formulation (here ~1e-7 is reached)."""
+    st = Stream(1234)
+    n, d = 512, 128
+    Q = st.normal(d, 0.2)
+    K = st.normal((n, d), 0.2)
+    V = st.normal((n, d), 0.2)
+    s = 1 / math.sqrt(d)
+    O = oracle.attn_decode(Q, K, V, 1, 1, n, d, s, n, 0, d, n * d)
+    R = oracle.attn_decode_f64(Q, K, V, 1, 1, n, d, s, n, 0, d, n * d)
+    assert np.max(np.abs(O - R)) < 1e-3
+    assert normwise_err(O, R) < 1e-5
+
+
+@pytest.mark.parametrize("name", ["decode_step_g4_d128", "decode_step_win_d256",
+                                  "decode_step_g8_d64_scale1"])
+def test_decode_step_golden(name):
+    g = golden(name)
+    nq, nkv, d, pos = int(g["nq"]), int(g["nkv"]), int(g["d"]), int(g["pos"])
+    Kc = np.zeros((pos + 1, nkv * d), np.float32)
+    Vc = np.zeros_like(Kc)
+    Kc[:pos] = g["K"]
+    Vc[:pos] = g["V"]
+    q_rot, k_rot, O = oracle.decode_step(g["q"], g["k_new"], g["v_new"], Kc, Vc, nq, nkv, d, pos,
+                                         pos, g["inv_freq"], float(g["scale"]), int(g["window"]))
+    np.testing.assert_allclose(q_rot, g["q_rot"], atol=2e-6)
+    np.testing.assert_allclose(k_rot, g["k_rot"], atol=2e-6)
+    np.testing.assert_array_equal(Kc[pos], k_rot.reshape(-1))
+    np.testing.assert_array_equal(Vc[pos], g["v_new"].reshape(-1))
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+def test_head_golden():
+    g = golden("head_bench_check")
+    n, d = int(g["n"]), int(g["d"])
+    O = oracle.attn_decode(g["Q"], g["K"], g["V"], 1, 1, n, d, float(g["scale"]), n, 0, d, n * d)
+    assert normwise_err(O[0], g["O"]) < 2e-6
+
+
+@pytest.mark.parametrize("name", ["gqa_headmajor_d64", "gqa_win_headmajor_d64"])
+def test_headmajor_golden(name):
+    g = golden(name)
+    nq, nkv, n, d = (int(g[k]) for k in ("nq", "nkv", "n", "d"))
+    O = oracle.attn_decode(g["Q"], g["K"], g["V"], nq, nkv, n, d, float(g["scale"]),
+                           int(g["pos_cur"]), int(g["window"]), d, n * d)
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+def test_bf16_golden_attention():
+    g = golden("bf16_cache_g8_d128")
+    nq, nkv, n, d = (int(g[k]) for k in ("nq", "nkv", "n", "d"))
+    O = oracle.attn_decode(g["Q"], g["K_bf16"], g["V_bf16"], nq, nkv, n, d, float(g["scale"]),
+                           n - 1, 0, nkv * d, d)
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+@pytest.mark.parametrize("nq,nkv,d,n,window", [(32, 8, 128, 4097, 0), (8, 4, 256, 3000, 1024),
+                                               (64, 8, 128, 2500, 0), (4, 4, 64, 333, 7)])
+def test_restatement_vs_f64(nq, nkv, d, n, window):
+    st = Stream(nq * 1000 + n)
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d)
+    s = 1 / math.sqrt(d)
+    O = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, s, n - 1, window)
+    R = oracle.attn_decode_f64(Q, K, V, nq, nkv, n, d, s, n - 1, window, nkv * d, d)
+    assert normwise_err(O, R) < 1e-5
+
+
+# closed-form attention properties -------------------------------------------
+
+def test_constant_v_gives_constant_output():
+    st = Stream(21)
+    nq, nkv, d, n = 8, 2, 128, 300
+    Q = st.normal((nq, d))
+    K = st.normal((n, nkv * d))
+    V = np.full((n, nkv * d), 0.375, np.float32)
+    O = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.1, n - 1, 0)
+    np.testing.assert_allclose(O, 0.375, rtol=2e-6)
+
+
+def test_equal_keys_give_mean_of_window():
+    st = Stream(22)
+    nq, nkv, d, n, w = 4, 1, 64, 200, 50
+    Q = st.normal((nq, d))
+    K = np.tile(st.normal((1, d)), (n, 1))
+    V = st.normal((n, d))
+    O = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.3, n - 1, w)
+    want = V[n - w:].astype(np.float64).mean(axis=0)
+    np.testing.assert_allclose(O, np.tile(want, (nq, 1)), atol=2e-6)
+
+
+def test_dominant_key_selects_its_value():
+    st = Stream(23)
+    nq, nkv, d, n = 2, 1, 64, 100
+    Q = st.normal((nq, d))
+    K = st.normal((n, d)) * 0.01
+    K[37] = Q[0] * 50  # score ~ 50*|q|^2*scale >> others for head 0
+    V = st.normal((n, d))
+    O = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 1.0, n - 1, 0)
+    np.testing.assert_allclose(O[0], V[37], atol=1e-5)
+
+
+def test_gqa_head_mapping():
+    """query head h reads KV head h // (nq/nkv) (attn.h:131)."""
+    st = Stream(24)
+    nq, nkv, d, n = 12, 3, 64, 50
+    Q = st.normal((nq, d))
+    K = st.normal((n, nkv * d))
+    V = np.zeros((n, nkv, d), np.float32)
+    for j in range(nkv):
+        V[:, j, :] = j + 1
+    O = oracle.attn_decode_gqa_cache(Q, K, V.reshape(n, -1), nq, nkv, n, d, 0.2, n - 1, 0)
+    for h in range(nq):
+        np.testing.assert_allclose(O[h], h // (nq // nkv) + 1, rtol=2e-6)
+
+
+def test_window_equals_sliced_full_attention():
+    st = Stream(25)
+    nq, nkv, d, n, w = 8, 4, 256, 500, 64
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d)
+    full_w = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.06, n - 1, w)
+    sliced = oracle.attn_decode_gqa_cache(Q, K[n - w:], V[n - w:], nq, nkv, w, d, 0.06, w - 1, 0)
+    np.testing.assert_array_equal(full_w, sliced)
+    # window >= n and window <= 0 are the full prefix
+    a = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.06, n - 1, 0)
+    b = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.06, n - 1, n + 5)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_empty_range_gives_zero():
+    st = Stream(26)
+    Q = st.normal((2, 64))
+    K = st.normal((10, 64))
+    O = oracle.attn_decode_gqa_cache(Q, K, K, 2, 1, 10, 64, 0.1, 100, 5)  # t0 = 96 > n
+    assert np.all(O == 0)
+
+
+def test_permutation_invariance():
+    st = Stream(27)
+    nq, nkv, d, n = 8, 2, 128, 700
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d)
+    perm = st.permutation(n)
+    a = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.09, n - 1, 0)
+    b = oracle.attn_decode_gqa_cache(Q, K[perm], V[perm], nq, nkv, n, d, 0.09, n - 1, 0)
+    assert normwise_err(b, a) < 2e-6
+
+
+def test_layouts_agree():
+    """token-major [n][nkv*d], head-major [nkv][n][d] and paged are one computation."""
+    st = Stream(28)
+    nq, nkv, d, n, page = 8, 2, 64, 333, 16
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d)
+    tm = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.1, n - 1, 0)
+    Kh = np.ascontiguousarray(K.reshape(n, nkv, d).transpose(1, 0, 2))
+    Vh = np.ascontiguousarray(V.reshape(n, nkv, d).transpose(1, 0, 2))
+    hm = oracle.attn_decode(Q, Kh, Vh, nq, nkv, n, d, 0.1, n - 1, 0, d, n * d)
+    np.testing.assert_array_equal(tm, hm)
+    nblk = (n + page - 1) // page
+    perm = st.permutation(nblk + 5)[:nblk]
+    Kp = np.zeros((nblk + 5, nkv, page, d), np.float32)
+    Vp = np.zeros_like(Kp)
+    for i in range(nblk):
+        rows = slice(i * page, min(n, (i + 1) * page))
+        m = rows.stop - rows.start
+        Kp[perm[i], :, :m] = K[rows].reshape(m, nkv, d).transpose(1, 0, 2)
+        Vp[perm[i], :, :m] = V[rows].reshape(m, nkv, d).transpose(1, 0, 2)
+    pg = oracle.attn_decode_paged(Q, Kp, Vp, perm.reshape(1, -1), np.array([n]), None, 1, nblk,
+                                  nq, nkv, d, page, 0.1)
+    np.testing.assert_array_equal(pg[0], tm)
+
+
+def test_thread_count_invariance():
+    st = Stream(29)
+    nq, nkv, d, n = 32, 8, 128, 1000
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d)
+    a = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.08, n - 1, 0, nthreads=1)
+    b = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, 0.08, n - 1, 0, nthreads=5)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_planted_missing_normalisation_is_caught():
+    """A variant that skips 1/den must fail the f64 comparison the GPU is held to."""
+    st = Stream(30)
+    nq, nkv, d, n = 4, 1, 64, 64
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d)
+    R = oracle.attn_decode_f64(Q, K, V, nq, nkv, n, d, 0.125, n - 1, 0, nkv * d, d)
+    s = (Q.astype(np.float64) @ K.astype(np.float64).T) * 0.125
+    e = np.exp(s - s.max(axis=1, keepdims=True))
+    unnormalised = e @ V.astype(np.float64)
+    assert normwise_err(unnormalised, R) > 1e-2
+
+
+def test_golden_fixture_set_present():
+    names = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(GOLDEN, "*.npz")))
+    assert len(names) >= 10, names
+
+
+# ---------------------------------------------------------------------------
+# against the compiled reference, where it is available on this host
+
+needs_ref = pytest.mark.skipif(not oracle.ref_available(),
+                               reason="compiled reference not available on this host")
+
+
+@needs_ref
+def test_ref_pool_coverage():
+    """bench/bench.cc:59-66: parallel_for touches every index exactly once."""
+    with oracle.RefPool(4) as pool:
+        seen = np.zeros(100000, np.int32)
+        oracle.ref().ref_pool_cover(pool.h, seen.size, oracle._p(seen))
+        assert np.all(seen == 1)
+
+
+@needs_ref
+@pytest.mark.parametrize("nq,nkv,d,n,window,pos_cur", [(32, 8, 128, 4097, 0, 4096),
+                                                       (8, 4, 256, 2100, 1024, 2099),
+                                                       (8, 8, 64, 17, 0, 16),
+                                                       (16, 2, 128, 1, 0, 0)])
+def test_restatement_vs_reference(nq, nkv, d, n, window, pos_cur):
+    st = Stream(n + d)
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d)
+    s = 1 / math.sqrt(d)
+    O = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, s, pos_cur, window)
+    R = np.empty_like(O)
+    with oracle.RefPool(4) as pool:
+        oracle.ref().ref_attn_decode_gqa_cache(oracle._p(Q), oracle._p(K), oracle._p(V),
+                                               oracle._p(R), nq, nkv, n, d, s, pos_cur, window,
+                                               pool.h)
+    assert normwise_err(O, R) < 2e-6
+
+
+@needs_ref
+def test_vexp_vs_reference_random():
+    st = Stream(31)
+    x = (st.normal(4096) * 20).clip(-100, 100).astype(np.float32)
+    y = oracle.vexp(x)
+    r = np.empty_like(x)
+    for i in range(0, x.size, 16):
+        oracle.ref().ref_exp16(oracle._p(x[i:i + 16]), oracle._p(r[i:i + 16]))
+    np.testing.assert_allclose(y, r, rtol=2e-7, atol=1.2e-38)  # reference flushes denormals
