@@ -123,6 +123,18 @@ int molot_hip_attn_decode_paged(const float* Q, const void* K, const void* V, fl
                                 int nq, int nkv, int d, int page, float scale, int window,
                                 int kv_dtype, void* stream);
 
+/* One fused decode step per sequence over the paged cache: RoPE of q (in
+ * place) and of k_new, append of k/v at slot seq_lens[b]-1 of sequence b,
+ * attention over [t0_b, seq_lens[b]).  seq_lens counts the new token.  The
+ * batched counterpart of molot_hip_decode_step (include/molot/forward.h:556-591
+ * per sequence; the paged cache has no reference counterpart). */
+int molot_hip_decode_step_paged(float* q, const float* k_new, const float* v_new, void* K,
+                                void* V, float* O, const int32_t* block_table,
+                                const int32_t* seq_lens, const int32_t* pos, int B,
+                                int max_blocks, int max_seq_len, int nq, int nkv, int d, int page,
+                                const float* inv_freq, float scale, int window, int kv_dtype,
+                                void* stream);
+
 /* RoPE + append for the paged cache: q[B][nq][d] rotated in place at pos[b];
  * k_new/v_new [B][nkv][d] (k rotated) written to slot seq_lens[b]-1 of
  * sequence b through its block table. */
@@ -140,6 +152,11 @@ int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream);
 /* Split-K tuning knob (0 = automatic): tokens per workgroup chunk.  Applies
  * to subsequent launches from this process. */
 void molot_hip_set_split_chunk(int tokens);
+
+/* Tuning knobs for measurement sweeps (0 = default): workgroups per CU of
+ * the split-K launch, and an alternative work mapping of the 32q/8kv/d128
+ * fp32 kernels (1..3).  Process-wide; apply to subsequent launches. */
+void molot_hip_set_tuning(int wgs_per_cu, int variant);
 
 /* Launch geometry the attention entry points would use for a problem:
  * writes the number of context chunks per KV head and tokens per chunk. */

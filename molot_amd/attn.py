@@ -22,7 +22,8 @@ from .lib import KV_BF16, KV_F32, check
 __all__ = [
     "KV_F32", "KV_BF16", "rope_inv_freq", "rope_apply", "rope_append", "attn_decode_gqa_cache",
     "attn_decode_gqa", "attn_decode_gqa_win", "attn_decode_head", "attn_decode_head_win",
-    "attn_decode_strided", "decode_step", "attn_decode_paged", "rope_append_paged", "vexp",
+    "attn_decode_strided", "decode_step", "attn_decode_paged", "decode_step_paged",
+    "rope_append_paged", "vexp",
     "split_plan", "set_split_chunk", "KVCache", "kv_dtype_of",
 ]
 
@@ -138,10 +139,23 @@ def attn_decode_head(Q, K, V, out, n, d, scale):
 
 
 def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale, window):
-    """forward.h:556-591 for one layer: rope + append at `slot`, attention over slot+1."""
-    rope_append(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq)
+    """forward.h:556-591 for one layer in one fused launch: RoPE of q (in place)
+    and k_new, append of k/v at `slot`, attention over slot+1 at pos_cur=pos."""
+    kvd = kv_dtype_of(K)
+    cap = K.numel() // (nkv * d)
+    if slot < 0 or slot >= cap:
+        raise RuntimeError("fwd: KV cache full")  # forward.h:570
+    _need(q, "q", torch.float32, nq * d)
+    _need(k_new, "k_new", torch.float32, nkv * d)
+    _need(v_new, "v_new", torch.float32, nkv * d)
+    _need(K, "K", _KV_DTYPES, (slot + 1) * nkv * d)
+    _need(V, "V", K.dtype, (slot + 1) * nkv * d)
     _need(O, "O", torch.float32, nq * d)
-    return attn_decode_gqa_cache(q, K, V, O, nq, nkv, slot + 1, d, scale, pos, window)
+    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    check(_lib.load().molot_hip_decode_step(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), nq, nkv, d, int(slot),
+        int(pos), _ptr(inv_freq), float(scale), int(window), kvd, _stream()), "decode_step")
+    return O
 
 
 def _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V):
@@ -175,6 +189,27 @@ def attn_decode_paged(Q, K, V, O, block_table, seq_lens, pos, B, max_blocks, nq,
         _ptr(Q), _ptr(K), _ptr(V), _ptr(O), _ptr(block_table), _ptr(seq_lens), _ptr(pos), B,
         max_blocks, max_len, nq, nkv, d, page, float(scale), int(window), kvd, _stream()),
         "attn_decode_paged")
+    return O
+
+
+def decode_step_paged(q, k_new, v_new, K, V, O, block_table, seq_lens, pos, B, max_blocks, nq,
+                      nkv, d, page, inv_freq, scale, window=0):
+    """Fused RoPE + append + attention for B sequences over a paged cache.
+
+    seq_lens[b] counts the new token, which lands in slot seq_lens[b]-1."""
+    kvd = kv_dtype_of(K)
+    _need(q, "q", torch.float32, B * nq * d)
+    _need(O, "O", torch.float32, B * nq * d)
+    _need(k_new, "k_new", torch.float32, B * nkv * d)
+    _need(v_new, "v_new", torch.float32, B * nkv * d)
+    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    max_len = _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V)
+    if B and int(seq_lens.min()) < 1:
+        raise ValueError("decode_step_paged: every sequence needs seq_lens >= 1")
+    check(_lib.load().molot_hip_decode_step_paged(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), _ptr(block_table),
+        _ptr(seq_lens), _ptr(pos), B, max_blocks, max_len, nq, nkv, d, page, _ptr(inv_freq),
+        float(scale), int(window), kvd, _stream()), "decode_step_paged")
     return O
 
 

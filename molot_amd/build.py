@@ -46,7 +46,7 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_library() -> str:
-    srcs = [os.path.join(CSRC, "attn_decode.hip")]
+    srcs = [os.path.join(CSRC, "attn_decode.hip"), os.path.join(CSRC, "probe.hip")]
     tmp = LIB + ".tmp"
     _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
     os.replace(tmp, LIB)

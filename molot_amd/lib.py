@@ -42,21 +42,27 @@ _SIGS = {
     "molot_hip_decode_step": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _I, _P],
     "molot_hip_attn_decode_paged": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                                     _I, _I, _P],
+    "molot_hip_decode_step_paged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                    _I, _P, _F, _I, _I, _P],
     "molot_hip_rope_append_paged": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P,
                                     _I, _P],
     "molot_hip_vexp": [_P, _P, _I64, _P],
     "molot_hip_split_plan": [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)],
+    # include/molot_amd/probe.h
+    "molot_probe_read": [_P, _I64, _P, _I64, _P],
+    "molot_probe_copy": [_P, _P, _I64, _P],
 }
 _VOID = {
     "molot_rope_inv_freq": [_F, _I, ctypes.POINTER(ctypes.c_float)],
     "molot_hip_set_split_chunk": [_I],
+    "molot_hip_set_tuning": [_I, _I],
 }
 _STR = {
     "molot_hip_strerror": [_I],
     "molot_hip_version": [],
 }
 
-# Every symbol include/molot_amd/attn_hip.h declares.
+# Every function include/molot_amd/*.h declares.
 EXPORTS = sorted(list(_SIGS) + list(_VOID) + list(_STR))
 
 

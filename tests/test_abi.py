@@ -7,6 +7,7 @@
   touches the device.
 """
 import ctypes
+import glob
 import os
 import re
 import subprocess
@@ -18,13 +19,15 @@ import oracle
 from molot_amd import lib as L
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "molot_amd", "attn_hip.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "molot_amd", "*.h")))
 
 
 def declared_functions():
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(molot_\w+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names.update(re.findall(r"\b(molot_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_header_declarations_match_binding():

@@ -411,6 +411,83 @@ def test_paged_small_ragged(gpu, bf16, window):
     assert normwise_err(O, oO) < FP32_TOL
 
 
+def run_paged_fused(P, inv, scale, window=0):
+    bf = P["Kp"].dtype == np.uint16
+    K = dev_bf16(P["Kp"]) if bf else dev(P["Kp"])
+    V = dev_bf16(P["Vp"]) if bf else dev(P["Vp"])
+    q = dev(P["q"])
+    O = torch.empty((P["B"], P["nq"], P["d"]), device="cuda")
+    attn.decode_step_paged(q, dev(P["k_new"]), dev(P["v_new"]), K, V, O,
+                           dev(P["bt"].reshape(-1)), dev(P["n"]), None, P["B"], P["max_blocks"],
+                           P["nq"], P["nkv"], P["d"], P["page"], dev(inv), scale, window)
+    if bf:
+        Kh = host(K.view(torch.int16)).view(np.uint16)
+        Vh = host(V.view(torch.int16)).view(np.uint16)
+    else:
+        Kh, Vh = host(K), host(V)
+    return host(q), Kh, Vh, host(O)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("window", [0, 100])
+def test_paged_fused_step(gpu, bf16, window):
+    """molot_hip_decode_step_paged (one launch) == oracle rope + append + attention."""
+    announce(f"paged fused bf16={bf16} window={window}")
+    P = make_paged(17, 32, 8, 128, 0, 2000, seed=5 + window, bf16=bf16)
+    inv = oracle.rope_inv_freq(500000.0, 128)
+    s = 1 / math.sqrt(128)
+    q, Kh, Vh, O = run_paged_fused(P, inv, s, window)
+    oq, oK, oV, oO = oracle_paged(P, inv, s, window)
+    np.testing.assert_allclose(q, oq, atol=4e-6, rtol=2e-6)
+    np.testing.assert_array_equal(Vh, oV)
+    assert normwise_err(O, oO) < FP32_TOL
+
+
+def test_c4_fused_step(gpu):
+    announce("c4 fused decode_step_paged")
+    P = make_paged(64, 32, 8, 128, 512, 8192)
+    inv = oracle.rope_inv_freq(500000.0, 128)
+    s = 1 / math.sqrt(128)
+    q, Kh, Vh, O = run_paged_fused(P, inv, s)
+    oq, oK, oV, oO = oracle_paged(P, inv, s)
+    np.testing.assert_array_equal(Vh, oV)
+    assert normwise_err(O, oO) < FP32_TOL
+
+
+def test_graph_replays_match_eager(gpu):
+    """The fused step captured in a HIP graph: every replay (with eager work and
+    synchronisations between replays) equals the eager result.  Exercises the
+    self-resetting completion counters across launches."""
+    p = make_decode(32, 8, 128, 6000, seed=12)
+    q0 = dev(p.q)
+    K, V = dev(p.K), dev(p.V)
+    kn, vn, inv = dev(p.k_new), dev(p.v_new), dev(p.inv_freq)
+    O = torch.empty((32, 128), device="cuda")
+    q = q0.clone()
+    attn.decode_step(q, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
+    eager = host(O)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        q.copy_(q0)
+        attn.decode_step(q, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    qg = q0.clone()
+    with torch.cuda.graph(g, stream=s):
+        attn.decode_step(qg, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
+    for r in range(5):
+        qg.copy_(q0)
+        O.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(O), eager), f"replay {r}"
+        # eager work in between replays
+        attn.attn_decode_gqa_cache(q, K, V, O, 32, 8, p.pos + 1, 128, p.scale, p.pos, 0)
+        torch.cuda.synchronize()
+
+
 def test_paged_matches_contiguous(gpu):
     """The same logical cache through a shuffled block table or contiguous."""
     st = Stream(6)
