@@ -1,0 +1,209 @@
+// Header-only C++ layer over the molot_amd C ABI (include/molot_amd/attn_hip.h).
+//
+// Drop-ins with the reference's own signatures, for a Molot-style host
+// forward pass whose KV cache lives in device memory:
+//   molot::amd::attn_decode_gqa_cache  <- include/molot/attn.h:125-127
+//   molot::amd::attn_decode_gqa        <- include/molot/attn.h:111-113
+//   molot::amd::rope_apply             <- include/molot/attn.h:19
+//   molot::amd::rope_inv_freq          <- include/molot/attn.h:31
+//   molot::amd::DeviceKV               <- Runner::KVC, include/molot/forward.h:48-51,
+//                                         with the decode block forward.h:556-591
+// The reference's ThreadPool& argument is accepted and ignored.  Calls are
+// synchronous like the reference's (outputs are valid on return); Q/O may be
+// host or device pointers (host ones are staged through per-thread device
+// buffers), K/V must be device pointers.  Errors throw std::runtime_error, as
+// the reference's caller does (forward.h:570, :580).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstddef>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "molot_amd/attn_hip.h"
+
+namespace molot {
+class ThreadPool;  // the reference's pool type (include/molot/thread_pool.h)
+}
+
+namespace molot::amd {
+
+inline void check(int status, const char* what) {
+  if (status != 0) throw std::runtime_error(std::string(what) + ": " + molot_hip_strerror(status));
+}
+
+inline void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// True for device (or managed) memory, false for host memory.
+inline bool is_device_ptr(const void* p) {
+  hipPointerAttribute_t attr;
+  if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
+    (void)hipGetLastError();  // unregistered host memory reports an error
+    return false;
+  }
+  return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
+}
+
+// Per-thread device staging for host-side q / o (small: nq * d floats).
+class Staging {
+ public:
+  ~Staging() {
+    if (buf_) (void)hipFree(buf_);
+  }
+  float* get(size_t floats) {
+    if (floats > cap_) {
+      if (buf_) check_hip(hipFree(buf_), "hipFree");
+      buf_ = nullptr;
+      check_hip(hipMalloc(&buf_, floats * sizeof(float)), "hipMalloc");
+      cap_ = floats;
+    }
+    return static_cast<float*>(buf_);
+  }
+  static Staging& local() {
+    static thread_local Staging s;
+    return s;
+  }
+
+ private:
+  void* buf_ = nullptr;
+  size_t cap_ = 0;
+};
+
+// Device view of q and o: the caller's pointers if they are device memory,
+// staged copies otherwise.  `sync_out` copies o back and waits.
+struct QOView {
+  const float* q;
+  float* o;
+  float* q_host_rot = nullptr;  // host q to receive the rotated q (decode step)
+  const float* q_in;
+  float* o_out;
+  size_t qn, on;
+  bool q_dev, o_dev;
+  float* stage = nullptr;
+
+  QOView(const float* Q, float* O, size_t qfloats, size_t ofloats, hipStream_t s)
+      : q_in(Q), o_out(O), qn(qfloats), on(ofloats) {
+    q_dev = is_device_ptr(Q);
+    o_dev = is_device_ptr(O);
+    q = Q;
+    o = O;
+    if (!q_dev || !o_dev) stage = Staging::local().get(qfloats + ofloats);
+    if (!q_dev) {
+      check_hip(hipMemcpyAsync(stage, Q, qn * sizeof(float), hipMemcpyHostToDevice, s), "H2D q");
+      q = stage;
+    }
+    if (!o_dev) o = stage + qfloats;
+  }
+  void finish(hipStream_t s) {
+    if (!o_dev)
+      check_hip(hipMemcpyAsync(o_out, o, on * sizeof(float), hipMemcpyDeviceToHost, s), "D2H o");
+    if (q_host_rot)
+      check_hip(hipMemcpyAsync(q_host_rot, q, qn * sizeof(float), hipMemcpyDeviceToHost, s),
+                "D2H q");
+    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  }
+};
+
+// attn.h:31-33
+inline void rope_inv_freq(float base, int d, float* out) { molot_rope_inv_freq(base, d, out); }
+
+// attn.h:19-28 on one device-resident head x[d]; inv_freq is a device table.
+inline void rope_apply(float* x, int d, int pos, const float* inv_freq, hipStream_t s = nullptr) {
+  check(molot_hip_rope_apply(x, 1, d, pos, inv_freq, s), "rope_apply");
+  check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+// attn.h:125-127: K, V device pointers to the [n][nkv*qhd] fp32 cache.
+inline void attn_decode_gqa_cache(const float* Q, const float* K, const float* V, float* O, int nq,
+                                  int nkv, int n, int qhd, float scale, int pos_cur, int window,
+                                  ThreadPool& /*pool*/, hipStream_t s = nullptr) {
+  QOView v(Q, O, (size_t)nq * qhd, (size_t)nq * qhd, s);
+  check(molot_hip_attn_decode_gqa_cache(v.q, K, V, v.o, nq, nkv, n, qhd, scale, pos_cur, window,
+                                        MOLOT_KV_F32, s),
+        "attn_decode_gqa_cache");
+  v.finish(s);
+}
+
+// attn.h:111-113: head-major [nkv][n][d] device K, V.
+inline void attn_decode_gqa(const float* Q, const float* K, const float* V, float* O, int nq,
+                            int nkv, int n, int d, float scale, ThreadPool& /*pool*/,
+                            hipStream_t s = nullptr) {
+  QOView v(Q, O, (size_t)nq * d, (size_t)nq * d, s);
+  check(molot_hip_attn_decode_gqa(v.q, K, V, v.o, nq, nkv, n, d, scale, MOLOT_KV_F32, s),
+        "attn_decode_gqa");
+  v.finish(s);
+}
+
+// Device KV cache of one layer (Runner::KVC, forward.h:48-51) with the
+// decode-attention block of forward.h:556-591 in one fused launch.
+class DeviceKV {
+ public:
+  int n = 0, cap = 0, nkv = 0, hd = 0, kv_dtype = MOLOT_KV_F32;
+  void* k = nullptr;  // [cap][nkv*hd]
+  void* v = nullptr;
+
+  DeviceKV(int cap_, int nkv_, int hd_, int kv_dtype_ = MOLOT_KV_F32)
+      : cap(cap_), nkv(nkv_), hd(hd_), kv_dtype(kv_dtype_) {
+    const size_t bytes = (size_t)cap * nkv * hd * (kv_dtype == MOLOT_KV_F32 ? 4 : 2);
+    check_hip(hipMalloc(&k, bytes), "hipMalloc K");
+    check_hip(hipMalloc(&v, bytes), "hipMalloc V");
+    check_hip(hipMemset(k, 0, bytes), "hipMemset K");
+    check_hip(hipMemset(v, 0, bytes), "hipMemset V");
+  }
+  ~DeviceKV() {
+    if (k) (void)hipFree(k);
+    if (v) (void)hipFree(v);
+  }
+  DeviceKV(const DeviceKV&) = delete;
+  DeviceKV& operator=(const DeviceKV&) = delete;
+
+  void reset() { n = 0; }  // molot_chat.cc /reset
+
+  // forward.h:556-591 for a layer that owns its KV: q (nq heads) rotated in
+  // place, k rotated and appended with v at slot n, n++, then attention into
+  // ao.  q, k, v, ao may be host or device pointers; inv_freq is a device
+  // table of hd/2 floats (the layer's L.freq).
+  void decode(float* q, const float* knew, const float* vnew, float* ao, int nq, int pos,
+              const float* inv_freq, float scale, int window, hipStream_t s = nullptr) {
+    if (n >= cap) throw std::runtime_error("fwd: KV cache full");  // forward.h:570
+    const size_t qf = (size_t)nq * hd, kf = (size_t)nkv * hd;
+    QOView view(q, ao, qf, qf, s);
+    if (!view.q_dev) view.q_host_rot = q;
+    const float* kd = knew;
+    const float* vd = vnew;
+    float* kv_stage = nullptr;
+    if (!is_device_ptr(knew) || !is_device_ptr(vnew)) {
+      kv_stage = kv_staging_.get(2 * kf);
+      check_hip(hipMemcpyAsync(kv_stage, knew, kf * 4, hipMemcpyHostToDevice, s), "H2D k");
+      check_hip(hipMemcpyAsync(kv_stage + kf, vnew, kf * 4, hipMemcpyHostToDevice, s), "H2D v");
+      kd = kv_stage;
+      vd = kv_stage + kf;
+    }
+    check(molot_hip_decode_step(const_cast<float*>(view.q), kd, vd, k, v, view.o, nq, nkv, hd, n,
+                                pos, inv_freq, scale, window, kv_dtype, s),
+          "decode_step");
+    ++n;
+    view.finish(s);
+  }
+
+  // forward.h:589-590 alone (e.g. a layer reading this cache as shared KV).
+  void attend(const float* q, float* ao, int nq, float scale, int pos_cur, int window,
+              hipStream_t s = nullptr) const {
+    if (n == 0) throw std::runtime_error("fwd: shared KV empty");  // forward.h:580
+    QOView view(q, ao, (size_t)nq * hd, (size_t)nq * hd, s);
+    check(molot_hip_attn_decode_gqa_cache(view.q, k, v, view.o, nq, nkv, n, hd, scale, pos_cur,
+                                          window, kv_dtype, s),
+          "attn_decode_gqa_cache");
+    view.finish(s);
+  }
+
+ private:
+  Staging kv_staging_;
+};
+
+}  // namespace molot::amd

@@ -2,8 +2,9 @@
 
 ``build_all()`` compiles, in-tree:
   molot_amd/libmolot_amd.so   HIP kernels + C ABI (hipcc, gfx950)
-  molot_amd/test_attn_cpp     C++ self-check of the header-only C++ layer
+  tests/cpp/test_attn_cpp      C++ self-check of the header-only C++ layer
                               (include/molot_amd/attn.hpp), linked to the above
+                              and to the oracle (its checker)
 The oracle (oracle/Makefile) is test infrastructure and is built by
 ``__graft_entry__.build()`` next to these, never by the product path.
 """
@@ -19,7 +20,7 @@ PKG = os.path.join(ROOT, "molot_amd")
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libmolot_amd.so")
-CPP_TEST = os.path.join(PKG, "test_attn_cpp")
+CPP_TEST = os.path.join(ROOT, "tests", "cpp", "test_attn_cpp")
 ARCH = os.environ.get("MOLOT_OFFLOAD_ARCH", "gfx950")
 
 # Packed-FP32 VALU forms are kept out of the generated code: -packed-fp32-ops.
@@ -57,10 +58,10 @@ def build_cpp_test() -> str:
     src = os.path.join(ROOT, "tests", "cpp", "test_attn_cpp.cpp")
     oracle_inc = os.path.join(ROOT, "oracle")
     tmp = CPP_TEST + ".tmp"
+    # rpaths relative to the binary, so the tree can move (the GPU box copies it)
     _run([_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{oracle_inc}", src, "-o", tmp,
-          f"-L{PKG}", "-lmolot_amd", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN",
-          os.path.join(ROOT, "oracle", "liboracle.so"),
-          f"-Wl,-rpath,{os.path.join(ROOT, 'oracle')}"])
+          f"-L{PKG}", "-lmolot_amd", f"-L{os.path.join(ROOT, 'oracle')}", "-loracle",
+          "-Wl,-rpath,$ORIGIN/../../molot_amd", "-Wl,-rpath,$ORIGIN/../../oracle"])
     os.replace(tmp, CPP_TEST)
     return CPP_TEST
 

@@ -34,6 +34,8 @@
  * relative-position property, constant V, equal keys, window == slice,
  * permutation invariance, layout invariance).
  */
+#include "attn_oracle.h"
+
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -42,9 +44,6 @@
 #ifdef _OPENMP
 #include <omp.h>
 #endif
-
-#define ORC_KV_F32 0
-#define ORC_KV_BF16 1
 
 /* ------------------------------------------------------------------ */
 /* bf16 helpers: include/molot/quant.h:186-198 (RNE, no NaN special case) */

@@ -1,0 +1,148 @@
+// Self-check of the header-only C++ layer (include/molot_amd/attn.hpp) on the
+// GPU, in the style of the reference's own self-checking benchmark
+// (bench/bench.cc:35-43: CHECK counts failures, exit status 1 on any).
+// The checker is the CPU oracle (oracle/attn_oracle.c), linked as a test
+// dependency.  Run by tests/test_cpp_layer.py.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <vector>
+
+#include "attn_oracle.h"
+#include "molot_amd/attn.hpp"
+
+static int failures = 0;
+#define CHECK(cond, ...)                      \
+  do {                                        \
+    if (!(cond)) {                            \
+      ++failures;                             \
+      std::printf("FAIL %d: ", __LINE__);     \
+      std::printf(__VA_ARGS__);               \
+      std::printf("\n");                      \
+    }                                         \
+  } while (0)
+
+// splitmix64 -> Box-Muller, the repo's generator (molot_amd/synth.py)
+struct Rng {
+  uint64_t s, i = 0;
+  explicit Rng(uint64_t seed) : s(seed) {}
+  uint64_t next() {
+    uint64_t z = s + (++i) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  void normal(std::vector<float>& v) {
+    for (size_t k = 0; k < v.size(); k += 2) {
+      const double u1 = ((double)(next() >> 11) + 1.0) / 9007199254740992.0;
+      const double u2 = (double)(next() >> 11) / 9007199254740992.0;
+      const double r = std::sqrt(-2.0 * std::log(u1));
+      v[k] = (float)(r * std::cos(2 * M_PI * u2));
+      if (k + 1 < v.size()) v[k + 1] = (float)(r * std::sin(2 * M_PI * u2));
+    }
+  }
+};
+
+static double normwise(const std::vector<float>& got, const std::vector<float>& ref) {
+  double num = 0, den = 0;
+  for (size_t i = 0; i < ref.size(); ++i) {
+    num = std::fmax(num, std::fabs((double)got[i] - ref[i]));
+    den = std::fmax(den, std::fabs((double)ref[i]));
+  }
+  return den > 0 ? num / den : num;
+}
+
+int main() {
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+    std::printf("no GPU\n");
+    return 2;
+  }
+  molot::ThreadPool* no_pool = nullptr;  // the reference's pool: accepted, unused
+
+  // ---- 1. DeviceKV: 64 consecutive decode steps vs the oracle's forward.h block ----
+  {
+    const int nq = 8, nkv = 2, d = 128, cap = 80, steps = 64;
+    const float scale = 1.0f / std::sqrt((float)d);
+    std::vector<float> inv(d / 2);
+    molot::amd::rope_inv_freq(500000.0f, d, inv.data());
+    float* inv_d = nullptr;
+    molot::amd::check_hip(hipMalloc(&inv_d, inv.size() * 4), "hipMalloc");
+    molot::amd::check_hip(hipMemcpy(inv_d, inv.data(), inv.size() * 4, hipMemcpyHostToDevice), "");
+    molot::amd::DeviceKV kv(cap, nkv, d);
+    std::vector<float> Kref((size_t)cap * nkv * d, 0.f), Vref((size_t)cap * nkv * d, 0.f);
+    Rng rng(42);
+    double worst = 0;
+    for (int pos = 0; pos < steps; ++pos) {
+      std::vector<float> q(nq * d), k(nkv * d), v(nkv * d), ao(nq * d), ao_ref(nq * d);
+      rng.normal(q);
+      rng.normal(k);
+      rng.normal(v);
+      std::vector<float> q_ref = q, k_ref = k;
+      kv.decode(q.data(), k.data(), v.data(), ao.data(), nq, pos, inv_d, scale, 0);
+      orc_decode_step(q_ref.data(), k_ref.data(), v.data(), Kref.data(), Vref.data(),
+                      ao_ref.data(), nq, nkv, d, pos, pos, inv.data(), scale, 0, ORC_KV_F32, 1);
+      worst = std::fmax(worst, normwise(ao, ao_ref));
+      CHECK(normwise(q, q_ref) < 1e-6, "rotated q differs at pos %d", pos);
+    }
+    CHECK(kv.n == steps, "cache length %d", kv.n);
+    CHECK(worst < 1e-5, "DeviceKV decode normwise err %g", worst);
+    std::printf("[%s] DeviceKV %d decode steps: max normwise err %.2e\n",
+                worst < 1e-5 ? "ok" : "FAIL", steps, worst);
+    // the cache holds exactly what the oracle appended
+    std::vector<float> Kd((size_t)steps * nkv * d);
+    molot::amd::check_hip(hipMemcpy(Kd.data(), kv.k, Kd.size() * 4, hipMemcpyDeviceToHost), "");
+    double kerr = 0;
+    for (size_t i = 0; i < Kd.size(); ++i) kerr = std::fmax(kerr, std::fabs(Kd[i] - Kref[i]));
+    CHECK(kerr < 1e-5, "appended K differs by %g", kerr);
+
+    // ---- 2. attn.h drop-in on the same cache, host q/o, sliding window ----
+    std::vector<float> q(nq * d), o(nq * d), o_ref(nq * d);
+    rng.normal(q);
+    molot::amd::attn_decode_gqa_cache(q.data(), (const float*)kv.k, (const float*)kv.v, o.data(),
+                                      nq, nkv, kv.n, d, scale, kv.n - 1, 17, *no_pool);
+    orc_attn_decode_gqa_cache(q.data(), Kref.data(), Vref.data(), o_ref.data(), nq, nkv, kv.n, d,
+                              scale, kv.n - 1, 17, 1);
+    const double e2 = normwise(o, o_ref);
+    CHECK(e2 < 1e-5, "attn_decode_gqa_cache drop-in err %g", e2);
+    std::printf("[%s] attn_decode_gqa_cache drop-in (window 17): err %.2e\n",
+                e2 < 1e-5 ? "ok" : "FAIL", e2);
+
+    // ---- 3. cache full throws, as forward.h:570 ----
+    bool threw = false;
+    molot::amd::DeviceKV small(1, nkv, d);
+    std::vector<float> qq(nq * d, 0.1f), kk(nkv * d, 0.2f), vv(nkv * d, 0.3f), oo(nq * d);
+    small.decode(qq.data(), kk.data(), vv.data(), oo.data(), nq, 0, inv_d, scale, 0);
+    try {
+      small.decode(qq.data(), kk.data(), vv.data(), oo.data(), nq, 1, inv_d, scale, 0);
+    } catch (const std::runtime_error& e) {
+      threw = std::string(e.what()).find("KV cache full") != std::string::npos;
+    }
+    CHECK(threw, "second append into a 1-slot cache did not throw");
+    // one token attends only to itself: o = v
+    double e3 = 0;
+    for (int h = 0; h < nq; ++h)
+      for (int j = 0; j < d; ++j) e3 = std::fmax(e3, std::fabs(oo[h * d + j] - 0.3f));
+    CHECK(e3 < 1e-6, "single-token attention err %g", e3);
+    std::printf("[%s] cache-full error and single-token output\n", threw && e3 < 1e-6 ? "ok" : "FAIL");
+    (void)hipFree(inv_d);
+  }
+
+  // ---- 4. unsupported head dim surfaces as std::runtime_error ----
+  {
+    bool threw = false;
+    try {
+      float* dq = nullptr;
+      molot::amd::check_hip(hipMalloc(&dq, 4 * 96 * 4), "");
+      molot::amd::attn_decode_gqa_cache(dq, dq, dq, dq, 4, 4, 1, 96, 0.1f, 0, 0, *no_pool);
+    } catch (const std::runtime_error& e) {
+      threw = std::string(e.what()).find("unsupported") != std::string::npos;
+    }
+    CHECK(threw, "head dim 96 did not raise");
+    std::printf("[%s] unsupported head dim raises\n", threw ? "ok" : "FAIL");
+  }
+
+  std::printf("%s (%d failures)\n", failures ? "FAILED" : "PASSED", failures);
+  return failures ? 1 : 0;
+}
