@@ -40,6 +40,7 @@ extern "C" {
 #define MOLOT_EINVAL (-22)  /* bad shape / argument */
 #define MOLOT_ENOTSUP (-95) /* shape the kernels are not built for */
 #define MOLOT_ENOSPC (-28)  /* append beyond the cache capacity */
+#define MOLOT_ENOWS (-16)   /* workspace not sized for a launch being captured in a graph */
 
 const char* molot_hip_strerror(int status);
 /* Library version string ("molot_amd <major>.<minor>"). */
@@ -155,8 +156,28 @@ void molot_hip_set_split_chunk(int tokens);
 
 /* Tuning knobs for measurement sweeps (0 = default): workgroups per CU of
  * the split-K launch, and an alternative work mapping of the 32q/8kv/d128
- * fp32 kernels (1..3).  Process-wide; apply to subsequent launches. */
+ * fp32 kernels (1..6).  Process-wide; apply to subsequent launches. */
 void molot_hip_set_tuning(int wgs_per_cu, int variant);
+
+/* Order in which the waves of a workgroup take their chunk's row blocks.
+ * dynamic = 1 (default): a wave takes the next free block when it has one
+ * to spare, so faster-served waves take more; the fp32 summation order then
+ * varies from run to run (results agree to rounding).  dynamic = 0: a fixed
+ * order, bit-identical from run to run.  Process-wide. */
+void molot_hip_set_block_order(int dynamic);
+
+/* Launch profiling, the counterpart of the reference's MOLOT_PROFILE
+ * attention timer (include/molot/forward.h:114-137, :588-591).
+ * molot_hip_profile_begin(max_launches) starts recording: each attention
+ * entry launched afterwards (outside graph capture, up to max_launches) has
+ * its kernels launched with start/stop HIP events stamped by the dispatch
+ * itself (hipExtLaunchKernelGGL).  molot_hip_profile_end() stops,
+ * waits for the recorded events and returns the summed durations (ms) of
+ * the attention kernel (*attn_ms over *launches launches) and of the
+ * split-K combine kernel (*combine_ms over *combines launches that needed
+ * one).  Process-wide; meant for measurement, not for concurrent callers. */
+int molot_hip_profile_begin(int max_launches);
+int molot_hip_profile_end(float* attn_ms, float* combine_ms, int* launches, int* combines);
 
 /* Launch geometry the attention entry points would use for a problem:
  * writes the number of context chunks per KV head and tokens per chunk. */

@@ -31,6 +31,9 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # single-lane atomics only: no wave-level scan around them (it would wait
+    # for an atomic's return right where it is issued)
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
 ]
 
 

@@ -16,6 +16,7 @@
 //   combine_kernel       log-sum-exp merge of the chunk partials.
 //
 // All shapes are validated on the host before any launch.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -25,6 +26,7 @@
 #include <map>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 #include "molot_amd/attn_hip.h"
 
@@ -93,6 +95,17 @@ __device__ __forceinline__ float dpp_f(float x) {
 }
 
 template <int N>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (N >= 2) v = fmaxf(v, dpp_f<0xB1>(v));
+  if constexpr (N >= 4) v = fmaxf(v, dpp_f<0x4E>(v));
+  if constexpr (N >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+  if constexpr (N >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+template <int N>
 __device__ __forceinline__ float group_sum(float v) {
   if constexpr (N >= 2) v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
   if constexpr (N >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -101,21 +114,6 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (N >= 32) v += __shfl_xor(v, 16);
   if constexpr (N >= 64) v += __shfl_xor(v, 32);
   return v;
-}
-
-// Cross-workgroup hand-off of the split-K partials.  The L2 of each XCD is
-// not coherent with the others, and an agent-scope fence writes back and
-// invalidates a whole L2, which would disturb every workgroup streaming KV
-// through it.  The partials therefore travel per access at device scope:
-// stores are written through to the device coherence point (sc1), each
-// thread waits for its stores to complete before the workgroup's counter
-// increment (a device-coherent atomic), and the finishing workgroup reads
-// them back with device-scope loads (sc1), which do not hit stale lines.
-__device__ __forceinline__ void store_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float load_dev(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // exp used by the softmax (full-accuracy device expf).
@@ -201,48 +199,63 @@ __global__ void rope_append_kernel(RopeArgs a) {
 //
 // Grid (chunks, nkv * subgroups, sequences).  Workgroup (c, h/sub, b) owns the
 // context rows [tb, tb + cnt) of KV head h and the GH query heads
-// hq0 .. hq0+GH-1 of that head's group:
-//   1. prologue: q of the GH heads into LDS; with ROPE, rotated there, and the
-//      workgroup holding the chunk that contains the new token rotates k_new,
-//      rounds k/v to the cache type, keeps them in LDS and (subgroup 0)
-//      stores them into the cache slot n-1;
-//   2. every wave streams its blocks of RB rows: 16-byte loads of the block's
-//      K and V rows are issued together; scores of the GH heads per K row
-//      (LPR lanes per row, DPP sums); online softmax per wave (running max,
-//      rescale of the accumulators); probabilities through a per-wave LDS
-//      slice to the PV lanes (LPR2 lanes per V row, 16 bytes each);
-//   3. the new token (ROPE, last chunk) is folded in by wave 0 from LDS;
-//   4. the waves' (max, sum, o) are merged through LDS; a single-chunk
-//      problem writes o / sum directly, otherwise the chunk partial goes to
-//      the workspace and the workgroup that finishes a head group last (a
-//      self-resetting counter) merges all chunk partials of that group with
-//      log-sum-exp weights, writes O and, with ROPE, the rotated q.
+// hq0 .. hq0+GH-1 of that head's group; the workgroups sharing (b, h/sub)
+// form a "slot".
+//   1. prologue: the first block(s) of K/V rows of every wave, then q of the
+//      GH heads into LDS; with ROPE, q is rotated there, and the workgroup
+//      holding the chunk that contains the new token rotates k_new and
+//      rounds k/v to the cache type in LDS.  Every wave issues the same
+//      loads on every path and the barriers order LDS only, so nothing waits
+//      for the K/V blocks in flight before it has to;
+//   2. every wave streams blocks of RB rows (NBUF blocks in flight); blocks
+//      past the first NBUF per wave are claimed from a workgroup counter in
+//      LDS, so waves that are served faster take more.  Scores of the GH
+//      heads per K row (LPR lanes per row, DPP sums); online softmax per
+//      wave (running max, rescale of the accumulators); probabilities through
+//      a per-wave LDS slice to the PV lanes (LPR2 lanes per V row, 16 bytes
+//      each);
+//   3. the new token (ROPE, last chunk): stored into the cache slot n-1 by
+//      subgroup 0 (no workgroup reads that slot in this launch) and folded in
+//      by wave 0 from LDS;
+//   4. the waves' (max, sum, o) are merged through LDS; every thread derives
+//      its own outputs' chunk partial.  A single-chunk problem writes
+//      o / sum (and the rotated q) directly;
+//   5. otherwise the chunk partial (o, max, sum) goes to the workspace, and
+//      combine_kernel, launched next on the same stream, merges the chunks
+//      of every slot with log-sum-exp weights and writes O (and, with ROPE,
+//      the rotated q, which chunk 0 leaves in the workspace: q is rotated in
+//      place, so it is written back only after every workgroup has read it).
 struct AttnArgs {
   const float* q;        // [B][nq][D]; un-rotated when the kernel applies RoPE
-  float* q_out;          // [B][nq][D] rotated q (ROPE), written by the finishing workgroup
+  float* q_out;          // [B][nq][D] rotated q (ROPE); written after every read of q
   const float* k_new;    // [B][nkv][D] fp32 (ROPE)
   const float* v_new;    // [B][nkv][D] fp32 (ROPE)
   void* k;               // KV cache
   void* v;
   const float* inv_freq; // [D/2] (ROPE)
   float* o;              // [B][nq][D]
-  float* part_o;         // [B][nq][nchunks][D]
-  float* part_ml;        // [B][nq][nchunks][2] = (max, sum)
-  int* counters;         // [B][nkv * subgroups], zero between launches
+  float* part_o;         // [slots][nchunks][GH*D] chunk partial o (split-K)
+  float* part_ml;        // [slots][nchunks][GH][2] chunk partial (max, sum)
+  float* qrot;           // [slots][GH*D] rotated q for the combine kernel (ROPE)
   const int32_t* block_table;
   const int32_t* seq_lens;
   const int32_t* pos_arr;
   int64_t tok_stride, head_stride, block_stride;
   int nq, nkv, n, t0, pos, chunk, nchunks, max_blocks, page_shift, window;
+  int dynamic;           // 1: waves claim blocks from a workgroup counter; 0: fixed order
   float scale;
 };
 
 // Work mapping of one kernel instance.
-//   LPR  lanes cooperating on one K row in the score loop (DPP sums across them)
-//   RB   rows per wave block (the block's K and V loads are issued together)
-//   NW   waves per workgroup
-template <int D, int GH, typename T, int LPR_, int RB_, int NW_>
+//   LPR   lanes cooperating on one K row in the score loop (DPP sums across them)
+//   RB    rows per wave block
+//   NW    waves per workgroup
+//   NBUF  blocks in flight per wave: 1 (load, then score) or 2 (one block is
+//         scored while the next one's loads are outstanding)
+template <int D, int GH, typename T, int LPR_, int RB_, int NW_, int NBUF_ = 1>
 struct Cfg {
+  static constexpr int NBUF = NBUF_;
+  static_assert(NBUF == 1 || NBUF == 2, "one or two blocks in flight");
   static constexpr int VW = KVT<T>::VW;
   static constexpr int LPR = LPR_;
   static constexpr int NV = D / (LPR * VW);  // 16-byte vectors per lane per K row
@@ -255,16 +268,20 @@ struct Cfg {
   static constexpr int VS = RB / RPI;  // V steps per block
   static constexpr int NW = NW_;
   static constexpr int NT = NW * 64;
+  static constexpr int P = GH * D;
+  // chunk partial: PP output pairs per thread (P > NT), Q threads per copy
+  static constexpr int PP = (P + NT - 1) / NT;
+  static constexpr int Q = P < NT ? P : NT;
   static_assert(NV >= 1 && D % (LPR * VW) == 0, "bad score mapping");
   static_assert(LPR2 <= 64 && 64 % LPR2 == 0, "bad PV mapping");
   static_assert(RB % RPS == 0 && RB % RPI == 0, "bad block");
+  static_assert(P % 64 == 0 || P <= NT, "pairs per phase");
 };
 
 // Default mapping: q registers (GH x D/LPR) kept at <= 32 where the 16-byte
-// vector allows it, then the largest block (<= 16 loads in flight per lane)
-// whose estimated register need keeps 4 waves per SIMD, else 2; 16 waves per
-// workgroup when the wave-merge buffer (NW*GH*D floats) and 4 waves/SIMD
-// allow, else 8 or 4.
+// vector allows it; one block in flight per wave; then the block size and
+// wave count with the most waves per SIMD (register estimate), preferring
+// 8-row blocks; one workgroup per CU (NW = 4 x waves per SIMD, at most 16).
 template <int D, int GH, typename T>
 struct Tune {
   static constexpr int VW = KVT<T>::VW;
@@ -277,22 +294,30 @@ struct Tune {
   static constexpr int NV = D / (LPR * VW);
   static constexpr int RPS = 64 / LPR, RPI = 64 / (D / VW);
   static constexpr int loads(int rb) { return (rb / RPS) * NV + rb / RPI; }
-  static constexpr int regs(int rb) {
-    return GH * NV * VW + GH * VW + 4 * loads(rb) + (rb / RPS) * GH + 3 * GH + 28;
+  static constexpr int regs(int rb) {  // one block of data + its addresses
+    return GH * NV * VW + GH * VW + 6 * loads(rb) + (rb / RPS) * GH + 3 * GH + 40;
   }
-  static constexpr bool ok(int rb, int cap) {
-    return rb % RPS == 0 && rb % RPI == 0 && loads(rb) <= 16 && regs(rb) <= cap;
+  static constexpr int wps(int rb) {
+    const int r = (regs(rb) + 7) / 8 * 8;
+    const int w = 512 / r;
+    return w > 4 ? 4 : w;
+  }
+  static constexpr bool ok(int rb) {
+    return rb % RPS == 0 && rb % RPI == 0 && loads(rb) <= 16 && wps(rb) >= 2;
   }
   static constexpr int rb() {
-    for (int cap : {128, 232})
-      for (int r : {32, 16, 8})
-        if (ok(r, cap)) return r;
+    int best = 0;
+    for (int r : {8, 16, 4})
+      if (ok(r) && (best == 0 || wps(r) > wps(best))) best = r;
+    if (best) return best;
     return RPS > RPI ? RPS : RPI;
   }
   static constexpr int RB = rb();
   static constexpr int nw() {
-    if (regs(RB) <= 128 && GH * D <= 512) return 16;
-    return GH * D <= 1024 ? 8 : 4;
+    const int w = wps(RB) >= 1 ? wps(RB) : 1;
+    int nw = 4 * w;
+    while (nw > 4 && nw * GH * D > 8192) nw -= 4;  // wave-merge buffer <= 32 KiB
+    return nw;
   }
   static constexpr int NW = nw();
   using C = Cfg<D, GH, T, LPR, RB, NW>;
@@ -300,9 +325,8 @@ struct Tune {
 
 // Dynamic LDS layout shared by host (size) and device (offsets), in floats.
 struct Lds {
-  int qs, cs, sn, knew, vnew, pw, wm, wl, wst, red, blk, flag, total;
-  __host__ __device__ Lds(int D, int GH, int NW, int RB, int nchunks, int chunk, int page_shift,
-                          bool paged) {
+  int qs, cs, sn, knew, vnew, pw, wm, wl, red, blk, misc, total;
+  __host__ __device__ Lds(int D, int GH, int NW, int RB, int chunk, int page_shift, bool paged) {
     int o = 0;
     qs = o; o += GH * D;
     cs = o; o += D / 2;
@@ -312,26 +336,46 @@ struct Lds {
     pw = o; o += NW * RB * GH;
     wm = o; o += NW * GH;
     wl = o; o += NW * GH;
-    wst = o; o += 2 * NW * GH + 2 * GH;  // wave weights + (M, L); later the combine's phase stats
-    red = o; o += NW * GH * D;
+    red = o; o += NW * GH * D;       // per-wave o
     blk = o; o += paged ? ((chunk >> page_shift) + 2) : 0;
-    flag = o; o += 4;
+    misc = o; o += 8;                // block claim counter
     total = o;
   }
 };
+
+
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for every outstanding global load and store of the thread
+// (s_waitcnt vmcnt(0)), which would stall the prologue on the K/V blocks
+// already in flight.  No global data crosses workgroups inside a launch
+// (the combine is a separate kernel).
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt at their maxima; gfx9
+// encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (((N >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
 __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   using V16 = typename KVT<T>::vec;
   constexpr int VW = C::VW, LPR = C::LPR, NV = C::NV, EPL = C::EPL, RPS = C::RPS;
   constexpr int LPR2 = C::LPR2, RPI = C::RPI, RB = C::RB, KS = C::KS, VS = C::VS;
-  constexpr int NW = C::NW, NT = C::NT;
+  constexpr int NW = C::NW, NT = C::NT, P = C::P;
 
   extern __shared__ float smem[];
-  const Lds L(D, GH, NW, RB, a.nchunks, a.chunk, a.page_shift, PAGED);
+  const Lds L(D, GH, NW, RB, a.chunk, a.page_shift, PAGED);
   float* qs = smem + L.qs;
   float* knew = smem + L.knew;
   float* vnew = smem + L.vnew;
+  int* misc = reinterpret_cast<int*>(smem + L.misc);
 
   const int c = blockIdx.x;
   const int G = a.nq / a.nkv;
@@ -342,7 +386,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const int b = blockIdx.z;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
 
   int n = a.n, t0 = a.t0, pos = a.pos;
   if constexpr (PAGED) {
@@ -360,7 +404,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (ROPE ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
-  if (c >= nch) {  // whole workgroup: chunk past this sequence's end
+  if (c >= nch) {  // whole workgroup: chunk past this sequence's end (never arrives)
     if (c == 0)    // empty attended range: o = 0 (include/molot/attn.h:162 with no rows)
       for (int i = tid; i < GH * D; i += NT) a.o[((int64_t)b * a.nq + hq0) * D + i] = 0.f;
     return;
@@ -368,20 +412,24 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const int tb = t0 + c * a.chunk;
   const int cntg = max(0, min(a.chunk, cend - tb));  // rows read from the cache
   const bool is_new = ROPE && c == nch - 1;          // this chunk folds in the new token
+  const bool split = nch > 1;
+  const int64_t slot = (int64_t)b * gridDim.y + blockIdx.y;
 
   const T* __restrict__ Kb = reinterpret_cast<const T*>(a.k);
   const T* __restrict__ Vb = reinterpret_cast<const T*>(a.v);
   const int64_t hoff = (int64_t)h * a.head_stride;
   const int64_t qrow0 = (int64_t)b * a.nq + hq0;
 
-  // ---- 1. prologue: block ids, the first block's loads, q (+ RoPE) ----
+  // ---- 1. prologue ----
   if constexpr (PAGED) {
     int32_t* sblk_w = reinterpret_cast<int32_t*>(smem + L.blk);
+    // the chunk's pages (at least the one holding row tb, which exists:
+    // tb <= n-1, so the clamped loads of an empty chunk stay in bounds)
     const int p0 = tb >> a.page_shift;
-    const int p1 = (tb + cntg - 1) >> a.page_shift;
-    for (int i = tid; cntg > 0 && i <= p1 - p0; i += NT)
+    const int p1 = max(p0, (tb + cntg - 1) >> a.page_shift);
+    for (int i = tid; i <= p1 - p0; i += NT)
       sblk_w[i] = a.block_table[(int64_t)b * a.max_blocks + p0 + i];
-    __syncthreads();
+    lds_barrier();
   }
   const int32_t* sblk = reinterpret_cast<const int32_t*>(smem + L.blk);
   auto row_ptr = [&](const T* base, int t) -> const T* {
@@ -397,114 +445,88 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const int rr = lane / LPR;   // scores: row of the group within a K step
   const int cs = lane % LPR2;  // PV: columns cs*VW .. cs*VW+VW-1
   const int rs = lane / LPR2;  // PV: row within a V step
-  V16 kr[KS][NV];
-  V16 vr[VS];
-  auto load_block = [&](int rbase) {
+  V16 kA[KS][NV], vA[VS], kB[KS][NV], vB[VS];
+  // Every wave issues the same sequence of global loads on every path: the
+  // compiler counts outstanding loads per path and, where paths merge with
+  // different counts, waits for all of them.  Rows past the chunk end (a
+  // partial block, or a block past the last) load the chunk's last row
+  // instead (row tb of an empty chunk): no branch around the loads, no extra
+  // HBM traffic (lines of a row already read), and a probability of
+  // e^-inf = 0 where they are scored at all.
+  const int rmax = max(cntg - 1, 0);
+  auto load_block = [&](V16 (&kr)[KS][NV], V16 (&vr)[VS], int rbase) {
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-      const int row = rbase + k * RPS + rr;
-      if (row < cntg) {
-        const T* p = row_ptr(Kb, tb + row);
+      const T* p = row_ptr(Kb, tb + min(rbase + k * RPS + rr, rmax));
 #pragma unroll
-        for (int v = 0; v < NV; ++v) kr[k][v] = load16(p + (v * LPR + s) * VW);
-      } else {
-#pragma unroll
-        for (int v = 0; v < NV; ++v) kr[k][v] = V16{0, 0, 0, 0};
-      }
+      for (int v = 0; v < NV; ++v) kr[k][v] = load16(p + (v * LPR + s) * VW);
     }
 #pragma unroll
-    for (int k = 0; k < VS; ++k) {
-      const int row = rbase + k * RPI + rs;
-      vr[k] = row < cntg ? load16(row_ptr(Vb, tb + row) + cs * VW) : V16{0, 0, 0, 0};
-    }
+    for (int k = 0; k < VS; ++k)
+      vr[k] = load16(row_ptr(Vb, tb + min(rbase + k * RPI + rs, rmax)) + cs * VW);
   };
   const int nblk = (cntg + RB - 1) / RB;
   // The prologue's own global loads go first: loads retire in order, so
-  // waiting for them does not also wait for the K/V block issued next.
+  // waiting for them does not also wait for the K/V blocks issued next.
   constexpr int QV = GH * D / 4;  // float4s of q of the group
   constexpr int QPT = (QV + NT - 1) / NT;
   static_assert(D <= NT, "one thread per head-dim element in the prologue");
   f32x4 qv[QPT];
 #pragma unroll
-  for (int u = 0; u < QPT; ++u) {
-    const int i = tid + u * NT;
-    if (i < QV) qv[u] = reinterpret_cast<const f32x4*>(a.q + qrow0 * D)[i];
-  }
+  for (int u = 0; u < QPT; ++u)
+    qv[u] = reinterpret_cast<const f32x4*>(a.q + qrow0 * D)[min(tid + u * NT, QV - 1)];
   float invf = 0.f, knv = 0.f, vnv = 0.f;
   if constexpr (ROPE) {
-    if (tid < D / 2) invf = a.inv_freq[tid];
-    if (is_new && tid < D) {
-      knv = a.k_new[((int64_t)b * a.nkv + h) * D + tid];
-      vnv = a.v_new[((int64_t)b * a.nkv + h) * D + tid];
-    }
+    invf = a.inv_freq[min(tid, D / 2 - 1)];
+    knv = a.k_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    vnv = a.v_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
   }
-  if (w < nblk) load_block(w * RB);  // in flight during the rest of the prologue
+  // each wave's first NBUF blocks: w (and w + NW); the rest are claimed
+  int bA = w, bB = w + NW;
+  load_block(kA, vA, bA * RB);
+  if constexpr (C::NBUF == 2) load_block(kB, vB, bB * RB);
+  if (tid == 0) {
+    misc[0] = C::NBUF * NW;  // next block to claim
+  }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
     const int i = tid + u * NT;
     if (i < QV) reinterpret_cast<f32x4*>(qs)[i] = qv[u];
   }
   if constexpr (ROPE) {
-    float* cs = smem + L.cs;
+    float* csn = smem + L.cs;
     float* sn = smem + L.sn;
     if (tid < D / 2) {
       const float ang = (float)pos * invf;
       double sd, cd;
       sincos((double)ang, &sd, &cd);
-      cs[tid] = (float)cd;
+      csn[tid] = (float)cd;
       sn[tid] = (float)sd;
     }
     if (is_new && tid < D) {
       knew[tid] = knv;
       vnew[tid] = vnv;
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
       const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
-      qs[g * D + j] = x0 * cs[j] - x1 * sn[j];
-      qs[g * D + j + D / 2] = x0 * sn[j] + x1 * cs[j];
+      qs[g * D + j] = x0 * csn[j] - x1 * sn[j];
+      qs[g * D + j + D / 2] = x0 * sn[j] + x1 * csn[j];
     }
     if (is_new) {
-      // the appended row as the cache will hold it: rotated k, k and v in the cache type
-      int64_t off;
-      const int slot = n - 1;
-      if constexpr (PAGED) {
-        const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot >> a.page_shift)];
-        off = blk * a.block_stride + hoff +
-              (int64_t)(slot & ((1 << a.page_shift) - 1)) * a.tok_stride;
-      } else {
-        off = (int64_t)slot * a.tok_stride + hoff;
-      }
+      // the appended row as the cache will hold it: rotated k, k and v
+      // rounded to the cache type (stored into the cache after the stream)
       for (int j = tid; j < D / 2; j += NT) {
         const float k0 = knew[j], k1 = knew[j + D / 2];
-        float r0 = k0 * cs[j] - k1 * sn[j];
-        float r1 = k0 * sn[j] + k1 * cs[j];
+        float r0 = k0 * csn[j] - k1 * sn[j];
+        float r1 = k0 * sn[j] + k1 * csn[j];
         float v0 = vnew[j], v1 = vnew[j + D / 2];
         if constexpr (sizeof(T) == 2) {
-          const uint16_t br0 = f32_to_bf16(r0), br1 = f32_to_bf16(r1);
-          const uint16_t bv0 = f32_to_bf16(v0), bv1 = f32_to_bf16(v1);
-          if (sub == 0) {
-            uint16_t* kd = reinterpret_cast<uint16_t*>(a.k) + off;
-            uint16_t* vd = reinterpret_cast<uint16_t*>(a.v) + off;
-            kd[j] = br0;
-            kd[j + D / 2] = br1;
-            vd[j] = bv0;
-            vd[j + D / 2] = bv1;
-          }
-          r0 = __uint_as_float((uint32_t)br0 << 16);
-          r1 = __uint_as_float((uint32_t)br1 << 16);
-          v0 = __uint_as_float((uint32_t)bv0 << 16);
-          v1 = __uint_as_float((uint32_t)bv1 << 16);
-        } else {
-          if (sub == 0) {
-            float* kd = reinterpret_cast<float*>(a.k) + off;
-            float* vd = reinterpret_cast<float*>(a.v) + off;
-            kd[j] = r0;
-            kd[j + D / 2] = r1;
-            vd[j] = v0;
-            vd[j + D / 2] = v1;
-          }
+          r0 = __uint_as_float((uint32_t)f32_to_bf16(r0) << 16);
+          r1 = __uint_as_float((uint32_t)f32_to_bf16(r1) << 16);
+          v0 = __uint_as_float((uint32_t)f32_to_bf16(v0) << 16);
+          v1 = __uint_as_float((uint32_t)f32_to_bf16(v1) << 16);
         }
         knew[j] = r0;
         knew[j + D / 2] = r1;
@@ -513,7 +535,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
 
   // q registers: lane s of a K row group holds elements (v*LPR + s)*VW + e
   float qr[GH][EPL];
@@ -540,10 +562,18 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int e = 0; e < VW; ++e) acc[g][e] = 0.f;
   }
-
-  for (int blk = w; blk < nblk; blk += NW) {
-    const int rbase = blk * RB;
-    if (blk != w) load_block(rbase);
+  int next_fixed = w + C::NBUF * NW;  // fixed order: wave w takes blocks w, w+NW, w+2NW, ...
+  auto claim = [&]() -> int {
+    if (!a.dynamic) {
+      const int v = next_fixed;
+      next_fixed += NW;
+      return v;
+    }
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&misc[0], 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  auto consume = [&](const V16 (&kr)[KS][NV], const V16 (&vr)[VS], int rbase) {
     // scores of this lane group's rows
     float sc[KS][GH];
     float bmax[GH];
@@ -606,9 +636,72 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       }
     }
     __builtin_amdgcn_wave_barrier();
+  };
+  // Two buffers, A and B, alternate: a block's successor is claimed before
+  // the block is consumed and loaded right after, so one block is always in
+  // flight while the other is scored.  On the path that continues, every
+  // load is unconditional (the exits drain the other buffer), so the
+  // compiler waits only for the buffer about to be consumed.  Claims are
+  // monotone: once a claim is past the end, every later one is too.
+  // The explicit waits state what the compiler cannot always derive at the
+  // rotated loop's header: the older buffer is complete while the younger
+  // buffer's LB loads stay in flight.
+  constexpr int LB = KS * NV + VS;  // loads per block
+  if constexpr (C::NBUF == 1) {
+    // one block in flight: score it, claim and load the next
+    while (bA < nblk) {
+      const int nx = claim();
+      consume(kA, vA, bA * RB);
+      bA = nx;
+      if (bA < nblk) load_block(kA, vA, bA * RB);
+    }
+  } else if (bA < nblk) {
+    if (bB >= nblk) {
+      consume(kA, vA, bA * RB);
+    } else {
+      for (;;) {
+        int nx = claim();
+        wait_vmcnt<LB>();
+        consume(kA, vA, bA * RB);
+        if (nx >= nblk) {
+          consume(kB, vB, bB * RB);
+          break;
+        }
+        bA = nx;
+        load_block(kA, vA, bA * RB);
+        nx = claim();
+        wait_vmcnt<LB>();
+        consume(kB, vB, bB * RB);
+        if (nx >= nblk) {
+          consume(kA, vA, bA * RB);
+          break;
+        }
+        bB = nx;
+        load_block(kB, vB, bB * RB);
+      }
+    }
   }
 
-  // ---- 3. the new token, from LDS ----
+  // ---- 3. the new token: appended to the cache (subgroup 0; no workgroup
+  // reads that slot in this launch) and folded in by wave 0 from LDS ----
+  if (is_new && sub == 0 && tid < D) {
+    const int slot_row = n - 1;
+    int64_t off;
+    if constexpr (PAGED) {
+      const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
+      off = blk * a.block_stride + hoff +
+            (int64_t)(slot_row & ((1 << a.page_shift) - 1)) * a.tok_stride;
+    } else {
+      off = (int64_t)slot_row * a.tok_stride + hoff;
+    }
+    if constexpr (sizeof(T) == 2) {  // exact bf16 values: the rounding returns their bits
+      reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
+      reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
+    } else {
+      reinterpret_cast<float*>(a.k)[off + tid] = knew[tid];
+      reinterpret_cast<float*>(a.v)[off + tid] = vnew[tid];
+    }
+  }
   if (is_new && w == 0) {
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
@@ -654,123 +747,195 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int e = 0; e < VW; ++e) red[(w * GH + g) * D + cs * VW + e] = acc[g][e];
   }
-  __syncthreads();
-  // chunk statistics per head: wave weights e^(m_w - M), chunk max M, sum L
-  float* wst = smem + L.wst;  // [GH][NW] weights | [GH] M | [GH] L
-  if (tid < GH) {
-    const int g = tid;
-    float m = wm[g];
+  lds_barrier();
+  // Every thread derives the chunk partial of its own output pairs from the
+  // wave partials (wave weights e^(m_w - M); waves without rows weigh
+  // e^-inf = 0).  Pairs: tid % Q + i*Q, i < PP; phase ph = tid / P.
+  constexpr int PP = C::PP, Q = C::Q;
+  const int ph = PP == 1 ? tid / P : 0;
+  int pr_[PP], g_[PP];
+  bool pv_[PP];
+  float po[PP], pm[PP], pl[PP];
+  // The 64 pairs of a wave lie in one head (D is a multiple of 64), so the
+  // wave weights are wave-uniform: lane ww < NW computes wave ww's weight,
+  // DPP/shuffle reductions give the chunk max and sum, and the weights reach
+  // every lane through readlane.
+  static_assert(D % 64 == 0 && NW <= 64, "wave-uniform head per 64 pairs");
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww) m = fmaxf(m, wm[ww * GH + g]);
-    float l = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) {
-      const float wgt = softmax_exp(wm[ww * GH + g] - m);  // waves without rows: e^-inf = 0
-      wst[g * NW + ww] = wgt;
-      l = fmaf(wgt, wl[ww * GH + g], l);
-    }
-    wst[GH * NW + g] = m;
-    wst[GH * NW + GH + g] = l;
-  }
-  __syncthreads();
-  const bool direct = nch == 1;
-  for (int idx = tid; idx < GH * D; idx += NT) {
-    const int g = idx / D;
+  for (int i = 0; i < PP; ++i) {
+    pr_[i] = tid % Q + i * Q;
+    pv_[i] = pr_[i] < P;
+    g_[i] = pv_[i] ? pr_[i] / D : 0;
+    const int g = __builtin_amdgcn_readfirstlane(g_[i]);
+    const float mw_l = lane < NW ? wm[lane * GH + g] : -INFINITY;
+    const float m = group_max<NW <= 16 ? 16 : 64>(mw_l);  // lanes >= NW hold -inf
+    const float e_l = lane < NW ? softmax_exp(mw_l - m) : 0.f;  // waves without rows: 0
+    const float l = group_sum<NW <= 16 ? 16 : 64>(lane < NW ? e_l * wl[lane * GH + g] : 0.f);
     float o = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) o = fmaf(wst[g * NW + ww], red[ww * GH * D + idx], o);
-    if (direct)
-      a.o[qrow0 * D + idx] = o / wst[GH * NW + GH + g];
-    else
-      store_dev(a.part_o + ((qrow0 + g) * a.nchunks + c) * D + (idx - g * D), o);
+    for (int ww = 0; ww < NW; ++ww)
+      o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e_l), ww)),
+               red[ww * P + (pv_[i] ? pr_[i] : 0)], o);
+    po[i] = o;
+    pm[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
+    pl[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(l)));
   }
-  if (direct) {
+  const bool lead = ph == 0;  // phase 0 threads own the chunk partial's outputs
+  if (!split) {
+#pragma unroll
+    for (int i = 0; i < PP; ++i)
+      if (lead && pv_[i]) a.o[qrow0 * D + pr_[i]] = po[i] / pl[i];
     if constexpr (ROPE) {
       if (a.q_out)
-        for (int i = tid; i < GH * D; i += NT) a.q_out[qrow0 * D + i] = qs[i];
+        for (int i = tid; i < P; i += NT) a.q_out[qrow0 * D + i] = qs[i];
     }
     return;
   }
-  if (tid < GH) {
-    float* ml = a.part_ml + ((qrow0 + tid) * a.nchunks + c) * 2;
-    store_dev(ml, wst[GH * NW + tid]);
-    store_dev(ml + 1, wst[GH * NW + GH + tid]);
-  }
 
-  // ---- 5. the workgroup finishing this head group merges all chunks ----
-  int* flag = reinterpret_cast<int*>(smem + L.flag);
-  __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores have completed
-  __syncthreads();
-  if (tid == 0) {
-    int* ctr = a.counters + (int64_t)b * gridDim.y + blockIdx.y;
-    const int done = atomicAdd(ctr, 1);
-    const bool last = done == nch - 1;
-    if (last) atomicExch(ctr, 0);  // ready for the next launch
-    flag[0] = last;
+  // ---- 5. the chunk partial for the combine kernel ----
+  // Plain stores: the combine kernel runs after this one on the same stream,
+  // so the kernel boundary orders them; no flag, counter or cleared memory
+  // is needed between the two launches.
+  float* po_s = a.part_o + (slot * a.nchunks + c) * P;
+  float* pml_s = a.part_ml + (slot * a.nchunks + c) * (GH * 2);
+#pragma unroll
+  for (int i = 0; i < PP; ++i) {
+    if (!(lead && pv_[i])) continue;
+    po_s[pr_[i]] = po[i];
+    if (pr_[i] - g_[i] * D == 0) {
+      pml_s[2 * g_[i]] = pm[i];
+      pml_s[2 * g_[i] + 1] = pl[i];
+    }
   }
-  __syncthreads();
-  if (!flag[0]) return;
+  if constexpr (ROPE) {  // the rotated q leaves through the combine kernel
+    if (c == 0 && a.q_out)
+      for (int i = tid; i < P; i += NT) a.qrot[slot * P + i] = qs[i];
+  }
+}
 
-  // Thread t owns output (g, j) of phase ph and merges chunks c = ph (mod PH)
-  // with its own running max: m, l and o of those chunks are loaded together
-  // (one round trip), then the PH phase results are merged through LDS.
-  constexpr int P = GH * D;
-  constexpr int PH = NT >= P ? (NT / P < NW ? NT / P : NW) : 1;  // PH*P <= NW*GH*D floats
-  float* pst = wst;  // [PH][GH][2] phase (max, sum); PH <= NW, wst holds 2*NW*GH + 2*GH floats
-  for (int t = tid; t < PH * P; t += NT) {
-    const int pair = t % P, ph = t / P;
-    const int g = pair / D, j = pair - g * D;
-    const float* src = a.part_o + (qrow0 + g) * a.nchunks * D + j;
-    const float* mls = a.part_ml + (qrow0 + g) * a.nchunks * 2;
-    float m = -INFINITY, acc = 0.f, lsum = 0.f;
-    for (int c0 = ph; c0 < nch; c0 += 8 * PH) {
-      float mv[8], lv[8], ov[8];
+// Log-sum-exp combine of the chunk partials of split-K launches.  Grid
+// (P/64, slots): a workgroup takes 64 output pairs of one head of a slot
+// (64 divides D) with 4 threads per pair, thread phase ph folding chunks
+// ph, ph+4, ...  The chunk weights e^(m_c - M) and the sum L are computed
+// once per workgroup into LDS; the first round of o loads is issued before
+// that, so a whole combine costs about one memory round trip.  Slots whose
+// sequence has a single chunk were written by the attention kernel itself.
+struct CombArgs {
+  const float* part_o;
+  const float* part_ml;
+  const float* qrot;
+  float* o;
+  float* q_out;
+  const int32_t* seq_lens;
+  const int32_t* pos_arr;
+  int nq, nkv, gh, nsub, d, nchunks, chunk, window, rope, paged;
+};
+
+constexpr int kCombThreads = 256;
+constexpr int kCombPairs = 64;                          // pairs per workgroup
+constexpr int kCombPhases = kCombThreads / kCombPairs;  // threads per pair
+constexpr int kCombRound = 8;                           // o loads in flight per thread
+constexpr int kMaxChunks = 4096;
+
+// Wave-wide max / sum with DPP only (no LDS round trips): the quad and
+// mirror steps reduce each row of 16 lanes, row_bcast:15 and row_bcast:31
+// carry the partial results up to lane 63, which readlane broadcasts.
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+  auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
+  v = op(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_f<0x141>(v));  // row_half_mirror
+  v = op(v, dpp_f<0x140>(v));  // row_mirror
+  // row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3; rows
+  // outside the mask keep their value (old = v)
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(MAX ? -INFINITY : 0.f),
+                                                       __float_as_int(v), 0x142, 0xA, 0xF,
+                                                       false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(MAX ? -INFINITY : 0.f),
+                                                       __float_as_int(v), 0x143, 0xC, 0xF,
+                                                       false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
+  __shared__ float wts[kMaxChunks];  // m_c, then the chunk weight e^(m_c - M)
+  __shared__ float lsv[kMaxChunks];  // l_c
+  __shared__ float s_l;              // L = sum_c e^(m_c - M) l_c
+  __shared__ float pacc[kCombThreads];
+  const int P = a.gh * a.d;
+  const int slot = blockIdx.y;
+  const int pb = blockIdx.x * kCombPairs;
+  const int t = threadIdx.x;
+  const int rows = a.nkv * a.nsub;  // slots per sequence
+  const int b = slot / rows, y = slot - b * rows;
+  int nch = a.nchunks;
+  if (a.paged) {  // this sequence's chunk count, as the attention kernel derives it
+    const int n = a.seq_lens[b];
+    const int pos = a.pos_arr ? a.pos_arr[b] : n - 1;
+    int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
+    if (t0 > n) t0 = n;
+    const int span = (a.rope ? n - 1 : n) - t0;
+    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.rope ? 1 : 0);
+    if (nch > a.nchunks) nch = a.nchunks;
+  }
+  if (nch <= 1) return;  // uniform over the workgroup
+  const int pl = t % kCombPairs, ph = t / kCombPairs;
+  const int pair = pb + pl;  // < P: P is a multiple of 64
+  const int g = pb / a.d;    // one head per workgroup
+  const float* po = a.part_o + (int64_t)slot * a.nchunks * P + pair;
+  const float* pml = a.part_ml + (int64_t)slot * a.nchunks * a.gh * 2 + 2 * g;
+  // first round of o loads, issued before the statistics
+  float ov[kCombRound];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int cc = c0 + u * PH;
-        const bool ok = cc < nch;
-        mv[u] = ok ? load_dev(mls + 2 * cc) : -INFINITY;
-        lv[u] = ok ? load_dev(mls + 2 * cc + 1) : 0.f;
-        ov[u] = ok ? load_dev(src + (int64_t)cc * D) : 0.f;
-      }
-      float mn = m;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) mn = fmaxf(mn, mv[u]);
-      const float alpha = softmax_exp(m - mn);  // m = -inf on the first pass -> 0
-      acc *= alpha;
-      lsum *= alpha;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float wgt = softmax_exp(mv[u] - mn);  // absent chunks: e^-inf = 0
-        acc = fmaf(wgt, ov[u], acc);
-        lsum = fmaf(wgt, lv[u], lsum);
-      }
-      m = mn;
+  for (int u = 0; u < kCombRound; ++u)
+    ov[u] = po[(int64_t)min(ph + kCombPhases * u, nch - 1) * P];
+  if (t < 64) {  // wave 0: chunk weights and L of head g (one global round trip)
+    float mloc = -INFINITY;
+    for (int cc = t; cc < nch; cc += 64) {
+      const float m = pml[(int64_t)cc * a.gh * 2];
+      wts[cc] = m;
+      lsv[cc] = pml[(int64_t)cc * a.gh * 2 + 1];
+      mloc = fmaxf(mloc, m);
     }
-    red[ph * P + pair] = acc;
-    if (j == 0) {
-      pst[(ph * GH + g) * 2] = m;
-      pst[(ph * GH + g) * 2 + 1] = lsum;
+    const float M = wave_reduce<true>(mloc);
+    float lloc = 0.f;
+    for (int cc = t; cc < nch; cc += 64) {  // the lane's own LDS entries
+      const float wgt = softmax_exp(wts[cc] - M);
+      wts[cc] = wgt;
+      lloc = fmaf(wgt, lsv[cc], lloc);
     }
+    const float Ls = wave_reduce<false>(lloc);
+    if (t == 0) s_l = Ls;
   }
   __syncthreads();
-  for (int pair = tid; pair < P; pair += NT) {
-    const int g = pair / D;
-    float M = pst[g * 2];
+  float acc = 0.f;
 #pragma unroll
-    for (int ph = 1; ph < PH; ++ph) M = fmaxf(M, pst[(ph * GH + g) * 2]);
-    float o = 0.f, l = 0.f;
-#pragma unroll
-    for (int ph = 0; ph < PH; ++ph) {
-      const float wgt = softmax_exp(pst[(ph * GH + g) * 2] - M);  // phases without chunks: 0
-      o = fmaf(wgt, red[ph * P + pair], o);
-      l = fmaf(wgt, pst[(ph * GH + g) * 2 + 1], l);
-    }
-    a.o[qrow0 * D + pair] = o / l;
+  for (int u = 0; u < kCombRound; ++u) {
+    const int cc = ph + kCombPhases * u;
+    if (cc < nch) acc = fmaf(wts[cc], ov[u], acc);
   }
-  if constexpr (ROPE) {
-    if (a.q_out)
-      for (int i = tid; i < GH * D; i += NT) a.q_out[qrow0 * D + i] = qs[i];
+  for (int c0 = ph + kCombPhases * kCombRound; c0 < nch; c0 += kCombPhases * kCombRound) {
+#pragma unroll
+    for (int u = 0; u < kCombRound; ++u)
+      ov[u] = po[(int64_t)min(c0 + kCombPhases * u, nch - 1) * P];
+#pragma unroll
+    for (int u = 0; u < kCombRound; ++u) {
+      const int cc = c0 + kCombPhases * u;
+      if (cc < nch) acc = fmaf(wts[cc], ov[u], acc);
+    }
+  }
+  pacc[t] = acc;
+  __syncthreads();
+  if (ph == 0) {
+    float o = acc;
+#pragma unroll
+    for (int q2 = 1; q2 < kCombPhases; ++q2) o += pacc[q2 * kCombPairs + pl];
+    const int G = a.nq / a.nkv;
+    const int h = y / a.nsub, sub = y - h * a.nsub;
+    const int64_t orow = ((int64_t)b * a.nq + h * G + sub * a.gh) * a.d;
+    a.o[orow + pair] = o / s_l;
+    if (a.rope && a.q_out) a.q_out[orow + pair] = a.qrot[(int64_t)slot * P + pair];
   }
 }
 
@@ -788,12 +953,44 @@ __global__ void zero_kernel(float* p, int64_t n) {
 // Host side.
 
 constexpr int kMaxChunk = 2048;
-constexpr int kMaxCounters = 1 << 16;  // (sequence, head group) pairs per launch
-constexpr size_t kCounterBytes = sizeof(int) * kMaxCounters;
+constexpr int kMaxSlots = 1 << 16;  // combine grid y: (sequence, head group) pairs per launch
 
 int g_split_chunk = 0;  // tokens per chunk, 0 = automatic
-int g_wgs_per_cu = 0;   // workgroups per CU, 0 = the variant's default
+int g_wgs_per_cu = 0;   // workgroups per CU, 0 = one
 int g_variant = 0;      // mapping variant of the 32q/8kv/d128 fp32 kernels (tuning sweeps)
+int g_dynamic = 1;      // block order: 1 = claimed by waves as they free up, 0 = fixed
+
+// Launch profiling (off by default): while on, every attention launch
+// outside graph capture goes through hipExtLaunchKernelGGL with a start and
+// a stop event per kernel, which HIP stamps from the dispatch itself (the
+// kernel's execution, without the gap before it).  molot_hip_profile_end()
+// waits for the events and returns the summed durations.
+struct ProfRec {
+  hipEvent_t a0, a1, c0, c1;  // attention kernel, combine kernel
+  bool combine;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+int g_prof_cap = 0;
+std::vector<ProfRec> g_prof;
+
+bool prof_active(void* stream) {
+  if (!g_prof_on) return false;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing((hipStream_t)stream, &cap) != hipSuccess) return false;
+  return cap == hipStreamCaptureStatusNone && (int)g_prof.size() < g_prof_cap;
+}
+
+hipEvent_t prof_event() {
+  hipEvent_t e = nullptr;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
+void prof_destroy(ProfRec& r) {
+  for (hipEvent_t e : {r.a0, r.a1, r.c0, r.c1})
+    if (e) (void)hipEventDestroy(e);
+}
 
 struct WsKey {
   int dev;
@@ -802,43 +999,40 @@ struct WsKey {
     return dev != o.dev ? dev < o.dev : stream < o.stream;
   }
 };
+// Per-(device, stream) workspace of the split-K partials, grown on demand.
+// The attention kernel fills it and the combine kernel, next on the same
+// stream, reads it, so it needs no clearing and holds nothing between
+// steps.  An outgrown buffer is retired, never freed: a graph captured
+// earlier on the stream still points at it (workspaces are small).
 struct WsBuf {
   void* ptr = nullptr;
   size_t bytes = 0;
 };
 std::mutex g_ws_mu;
 std::map<WsKey, WsBuf> g_ws;
+std::vector<void*> g_retired;
 
-// Per-(device, stream) workspace, grown on demand: [counters | partials].
-// The counters sit at offset 0 of every workspace, are zeroed once when it
-// is allocated and are left at zero by every launch (the finishing
-// workgroup resets its counter).  Growth waits for the stream so the old
-// buffer is idle when freed.
-int workspace(void* stream, size_t bytes, int** counters, float** partials) {
+int workspace(void* stream, size_t bytes, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
   std::lock_guard<std::mutex> lk(g_ws_mu);
   WsBuf& w = g_ws[WsKey{dev, stream}];
-  const size_t need = kCounterBytes + bytes;
-  if (w.bytes < need) {
-    if (w.ptr) {
-      e = hipStreamSynchronize((hipStream_t)stream);
-      if (e != hipSuccess) return (int)e;
-      e = hipFree(w.ptr);
-      if (e != hipSuccess) return (int)e;
-      w.ptr = nullptr;
-      w.bytes = 0;
-    }
-    const size_t want = need < (size_t)(8u << 20) ? (size_t)(8u << 20) : need;
-    e = hipMalloc(&w.ptr, want);
+  if (w.bytes < bytes) {
+    // a graph being captured cannot allocate: the caller sizes the
+    // workspace with one launch of the shape before capturing
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing((hipStream_t)stream, &cap);
     if (e != hipSuccess) return (int)e;
-    e = hipMemset(w.ptr, 0, kCounterBytes);
+    if (cap != hipStreamCaptureStatusNone) return MOLOT_ENOWS;
+    if (w.ptr) g_retired.push_back(w.ptr);
+    w = WsBuf{};
+    const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    e = hipMalloc(&w.ptr, want);
     if (e != hipSuccess) return (int)e;
     w.bytes = want;
   }
-  *counters = reinterpret_cast<int*>(w.ptr);
-  *partials = reinterpret_cast<float*>(reinterpret_cast<char*>(w.ptr) + kCounterBytes);
+  *out = w.ptr;
   return 0;
 }
 
@@ -863,9 +1057,8 @@ int pick_gh(int G) {
 }
 
 // Tokens per chunk: enough chunks that the launch holds `wpc` workgroups
-// per CU (all resident at once by default: 16 waves per CU), rounded up to a
-// multiple of `align` (= waves x rows per block) so every wave of a
-// workgroup gets the same number of blocks.
+// per CU (one by default: a workgroup fills its CU), rounded up to a
+// multiple of `align` rows.
 int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
   int chunk = g_split_chunk;
   if (chunk <= 0) {
@@ -880,20 +1073,94 @@ int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
   return chunk;
 }
 
+// Chunking + workspace of one launch.  `span` bounds every sequence's row
+// range tiled by chunks (cache rows only when the kernel folds in the new
+// token); B * nkv * subgroups slots share each chunk index.
 int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, bool paged, int align,
-                int wpc, void* stream);
+                void* stream) {
+  (void)paged;
+  const int rows = a.nkv * nsubs * B;
+  a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, 1);
+  a.nchunks = span > 0 ? (span + a.chunk - 1) / a.chunk : 1;
+  // bound the chunk count (grid x, and the combine's per-pair loop)
+  while (a.nchunks > kMaxChunks && a.chunk < kMaxChunk) {
+    a.chunk *= 2;
+    a.nchunks = (span + a.chunk - 1) / a.chunk;
+  }
+  if (a.nchunks > kMaxChunks) return MOLOT_ENOTSUP;
+  a.part_o = nullptr;
+  a.part_ml = nullptr;
+  a.qrot = nullptr;
+  if (a.nchunks == 1) return 0;  // single chunk: written directly, no combine
+  if ((long)rows > kMaxSlots) return MOLOT_ENOTSUP;
+  const size_t P = (size_t)gh * d;
+  const size_t po = (size_t)rows * a.nchunks * P;
+  const size_t pml = (size_t)rows * a.nchunks * gh * 2;
+  const size_t qr = (size_t)rows * P;
+  void* ws = nullptr;
+  const int st = workspace(stream, sizeof(float) * (po + pml + qr), &ws);
+  if (st) return st;
+  a.part_o = reinterpret_cast<float*>(ws);
+  a.part_ml = a.part_o + po;
+  a.qrot = a.part_ml + pml;
+  return 0;
+}
 
 template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
 int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
-  int st = plan_launch(a, D, span, GH, nsubs, B, PAGED, C::NW * C::RB,
-                       C::NW >= 16 ? 1 : 16 / C::NW, stream);
+  int st = plan_launch(a, D, span, GH, nsubs, B, PAGED, C::RB, stream);
   if (st) return st;
-  const Lds L(D, GH, C::NW, C::RB, a.nchunks, a.chunk, a.page_shift, PAGED);
+  const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED);
   const size_t lds = sizeof(float) * (size_t)L.total;
   if (lds > 65536) return (int)hipErrorInvalidConfiguration;
+  a.dynamic = g_dynamic;
+  std::lock_guard<std::mutex> plk(g_prof_mu);
+  const bool prof = prof_active(stream);
+  ProfRec pr{nullptr, nullptr, nullptr, nullptr, a.nchunks > 1};
   dim3 grid(a.nchunks, a.nkv * nsubs, B);
-  hipLaunchKernelGGL((attn_kernel<D, GH, T, PAGED, ROPE, C>), grid, dim3(C::NT), lds,
-                     (hipStream_t)stream, a);
+  if (prof) {
+    pr.a0 = prof_event();
+    pr.a1 = prof_event();
+    hipExtLaunchKernelGGL((attn_kernel<D, GH, T, PAGED, ROPE, C>), grid, dim3(C::NT), lds,
+                          (hipStream_t)stream, pr.a0, pr.a1, 0, a);
+  } else {
+    hipLaunchKernelGGL((attn_kernel<D, GH, T, PAGED, ROPE, C>), grid, dim3(C::NT), lds,
+                       (hipStream_t)stream, a);
+  }
+  st = (int)hipGetLastError();
+  if (st || a.nchunks == 1) {
+    if (prof) g_prof.push_back(pr);
+    return st;
+  }
+  CombArgs cb{};
+  cb.part_o = a.part_o;
+  cb.part_ml = a.part_ml;
+  cb.qrot = a.qrot;
+  cb.o = a.o;
+  cb.q_out = a.q_out;
+  cb.seq_lens = a.seq_lens;
+  cb.pos_arr = a.pos_arr;
+  cb.nq = a.nq;
+  cb.nkv = a.nkv;
+  cb.gh = GH;
+  cb.nsub = nsubs;
+  cb.d = D;
+  cb.nchunks = a.nchunks;
+  cb.chunk = a.chunk;
+  cb.window = a.window;
+  cb.rope = ROPE ? 1 : 0;
+  cb.paged = PAGED ? 1 : 0;
+  static_assert((GH * D) % kCombPairs == 0 && D % kCombPairs == 0, "combine tiling");
+  dim3 cgrid(GH * D / kCombPairs, a.nkv * nsubs * B);
+  if (prof) {
+    pr.c0 = prof_event();
+    pr.c1 = prof_event();
+    hipExtLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), 0, (hipStream_t)stream,
+                          pr.c0, pr.c1, 0, cb);
+    g_prof.push_back(pr);
+  } else {
+    hipLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), 0, (hipStream_t)stream, cb);
+  }
   return (int)hipGetLastError();
 }
 
@@ -901,9 +1168,12 @@ template <int D, int GH, typename T, bool PAGED, bool ROPE>
 int launch_attn(const AttnArgs& a, int span, int nsubs, int B, void* stream) {
   if constexpr (D == 128 && GH == 4 && sizeof(T) == 4 && !PAGED) {
     switch (g_variant) {  // alternative mappings of the headline shape, for sweeps
-      case 1: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 8, 8>>(a, span, nsubs, B, stream);
-      case 2: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 16, 8>>(a, span, nsubs, B, stream);
-      case 3: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 8, 16, 8>>(a, span, nsubs, B, stream);
+      case 1: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 16, 8>>(a, span, nsubs, B, stream);
+      case 2: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 8, 12>>(a, span, nsubs, B, stream);
+      case 3: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 4, 12, 2>>(a, span, nsubs, B, stream);
+      case 4: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 8, 8, 2>>(a, span, nsubs, B, stream);
+      case 5: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 4, 16>>(a, span, nsubs, B, stream);
+      case 6: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 8, 16>>(a, span, nsubs, B, stream);
       default: break;
     }
   }
@@ -958,35 +1228,6 @@ int zero_out(float* O, int64_t count, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
-// Chunking + workspace of one launch.  `span` bounds every sequence's row
-// range tiled by chunks (cache rows only when the kernel folds in the new
-// token); B * nkv * subgroups workgroups share each chunk index.
-int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, bool paged, int align,
-                int wpc, void* stream) {
-  const int rows = a.nkv * nsubs * B;
-  a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, wpc);
-  a.nchunks = span > 0 ? (span + a.chunk - 1) / a.chunk : 1;
-  // bound the chunk count (grid x, and the finishing workgroup's merge loop)
-  while (a.nchunks > 4096 && a.chunk < kMaxChunk) {
-    a.chunk *= 2;
-    a.nchunks = (span + a.chunk - 1) / a.chunk;
-  }
-  if (a.nchunks > 4096) return MOLOT_ENOTSUP;
-  a.part_o = nullptr;
-  a.part_ml = nullptr;
-  a.counters = nullptr;
-  if (a.nchunks == 1 && !paged) return 0;  // single chunk: written directly
-  if ((long)rows > kMaxCounters) return MOLOT_ENOTSUP;
-  const size_t po = (size_t)B * a.nq * a.nchunks * d;
-  const size_t pml = (size_t)B * a.nq * a.nchunks * 2;
-  float* part = nullptr;
-  const int st = workspace(stream, (po + pml) * sizeof(float), &a.counters, &part);
-  if (st) return st;
-  a.part_o = part;
-  a.part_ml = part + po;
-  return 0;
-}
-
 template <bool PAGED, bool ROPE>
 int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
   const int G = a.nq / a.nkv;
@@ -1007,6 +1248,9 @@ const char* molot_hip_strerror(int status) {
     case MOLOT_EINVAL: return "molot_amd: invalid argument";
     case MOLOT_ENOTSUP: return "molot_amd: unsupported shape (head dim must be 64, 128 or 256)";
     case MOLOT_ENOSPC: return "molot_amd: KV cache full";
+    case MOLOT_ENOWS:
+      return "molot_amd: workspace not sized for this shape on a capturing stream (launch the "
+             "shape once before capturing)";
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
   return "molot_amd: unknown status";
@@ -1033,6 +1277,58 @@ int molot_hip_split_plan(int nkv, int n_att, int d, int kv_dtype, int* nchunks, 
   *chunk = ch;
   *nchunks = n_att > 0 ? (n_att + ch - 1) / ch : 0;
   return 0;
+}
+
+void molot_hip_set_block_order(int dynamic) { g_dynamic = dynamic ? 1 : 0; }
+
+int molot_hip_profile_begin(int max_launches) {
+  if (max_launches <= 0) return MOLOT_EINVAL;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  for (ProfRec& r : g_prof) prof_destroy(r);
+  g_prof.clear();
+  g_prof.reserve(max_launches);
+  g_prof_cap = max_launches;
+  g_prof_on = true;
+  return 0;
+}
+
+int molot_hip_profile_end(float* attn_ms, float* combine_ms, int* launches, int* combines) {
+  if (!attn_ms || !combine_ms || !launches || !combines) return MOLOT_EINVAL;
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_on = false;
+  double ta = 0.0, tc = 0.0;
+  int n = 0, nc = 0, st = 0;
+  for (ProfRec& r : g_prof) {
+    if (!r.a0 || !r.a1 || (r.combine && (!r.c0 || !r.c1))) {
+      st = (int)hipErrorInvalidValue;
+      continue;
+    }
+    hipError_t e = hipEventSynchronize(r.combine ? r.c1 : r.a1);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.a0, r.a1);
+    if (e != hipSuccess) {
+      st = (int)e;
+      continue;
+    }
+    ta += ms;
+    ++n;
+    if (r.combine) {
+      e = hipEventElapsedTime(&ms, r.c0, r.c1);
+      if (e != hipSuccess) {
+        st = (int)e;
+        continue;
+      }
+      tc += ms;
+      ++nc;
+    }
+  }
+  for (ProfRec& r : g_prof) prof_destroy(r);
+  g_prof.clear();
+  *attn_ms = (float)ta;
+  *combine_ms = (float)tc;
+  *launches = n;
+  *combines = nc;
+  return st;
 }
 
 void molot_hip_set_tuning(int wgs_per_cu, int variant) {

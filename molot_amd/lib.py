@@ -20,6 +20,7 @@ OK = 0
 EINVAL = -22
 ENOTSUP = -95
 ENOSPC = -28
+ENOWS = -16
 
 _lock = threading.Lock()
 _lib = None
@@ -48,6 +49,9 @@ _SIGS = {
                                     _I, _P],
     "molot_hip_vexp": [_P, _P, _I64, _P],
     "molot_hip_split_plan": [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)],
+    "molot_hip_profile_begin": [_I],
+    "molot_hip_profile_end": [ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_I),
+                              ctypes.POINTER(_I)],
     # include/molot_amd/probe.h
     "molot_probe_read": [_P, _I64, _P, _I64, _P],
     "molot_probe_copy": [_P, _P, _I64, _P],
@@ -56,6 +60,7 @@ _VOID = {
     "molot_rope_inv_freq": [_F, _I, ctypes.POINTER(ctypes.c_float)],
     "molot_hip_set_split_chunk": [_I],
     "molot_hip_set_tuning": [_I, _I],
+    "molot_hip_set_block_order": [_I],
 }
 _STR = {
     "molot_hip_strerror": [_I],

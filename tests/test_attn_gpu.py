@@ -204,7 +204,8 @@ def test_c5_70b_ctx131072_bf16(gpu):
 # shapes, windows, ragged lengths, chunking
 
 @pytest.mark.parametrize("nq,nkv,d", [(32, 8, 128), (8, 4, 256), (64, 8, 128), (16, 16, 64),
-                                      (24, 8, 128), (16, 1, 128), (32, 2, 64), (12, 4, 256)])
+                                      (24, 8, 128), (16, 1, 128), (32, 2, 64), (12, 4, 256),
+                                      (16, 2, 256)])
 @pytest.mark.parametrize("pos", [0, 1, 15, 16, 63, 64, 65, 1000, 2049])
 def test_shapes_and_ragged_lengths(gpu, nq, nkv, d, pos):
     announce(f"shape {nq}/{nkv}/{d} pos {pos}")
@@ -297,6 +298,38 @@ def test_properties_at_16k(gpu):
     assert normwise_err(host(O), host(O2)) < 2e-6
 
 
+def test_fresh_stream_workspace(gpu):
+    """First launches on a brand-new stream: its workspace is created (and
+    cleared on that stream) by the first launch, then grown by a larger one;
+    both must match the oracle (the split-K bookkeeping starts from zero)."""
+    s = torch.cuda.Stream()
+    for pos, seed in ((3000, 21), (16384, 22), (16384, 23)):
+        p = make_decode(32, 8, 128, pos, seed=seed)
+        with torch.cuda.stream(s):
+            _, _, _, O = run_decode_gpu(p)
+        _, _, oO, _, _ = oracle_decode(p)
+        assert normwise_err(O, oO) < FP32_TOL, pos
+
+
+def test_capture_without_warmup_is_refused(gpu):
+    """Capturing a shape whose workspace does not exist yet on the capturing
+    stream is refused on the host (MOLOT_ENOWS) before anything is launched."""
+    from molot_amd.lib import ENOWS, MolotHipError
+    # 64 KV heads: more split-K slots than any earlier launch on a pooled stream
+    p = make_decode(64, 64, 64, 5000, base=10000.0, seed=24)
+    q, kn, vn = dev(p.q), dev(p.k_new), dev(p.v_new)
+    K, V, inv = dev(p.K), dev(p.V), dev(p.inv_freq)
+    O = torch.empty((64, 64), device="cuda")
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(MolotHipError) as e:
+        with torch.cuda.graph(g, stream=s):
+            attn.decode_step(q, kn, vn, K, V, O, 64, 64, 64, p.pos, p.pos, inv, p.scale, 0)
+    assert e.value.status == ENOWS
+    torch.cuda.synchronize()
+
+
 def test_non_default_stream(gpu):
     s = torch.cuda.Stream()
     p = make_decode(32, 8, 128, 2000, seed=9)
@@ -307,15 +340,29 @@ def test_non_default_stream(gpu):
 
 
 def test_repeated_calls_are_deterministic(gpu):
-    p = make_decode(32, 8, 128, 4096, seed=10)
+    """Fixed block order: bit-identical runs.  Dynamic order (the default):
+    runs agree to fp32 rounding of a different summation order."""
+    from molot_amd import lib as L
+    p = make_decode(32, 8, 128, 16384, seed=10)
     Q = dev(oracle.rope_apply(p.q, p.pos, p.inv_freq))
     K, V = dev(p.K), dev(p.V)
-    outs = []
-    for _ in range(3):
-        O = torch.empty((32, 128), device="cuda")
-        attn.attn_decode_gqa_cache(Q, K, V, O, 32, 8, p.pos, 128, p.scale, p.pos - 1, 0)
-        outs.append(host(O))
-    assert np.array_equal(outs[0], outs[1]) and np.array_equal(outs[1], outs[2])
+
+    def runs():
+        outs = []
+        for _ in range(3):
+            O = torch.empty((32, 128), device="cuda")
+            attn.attn_decode_gqa_cache(Q, K, V, O, 32, 8, p.pos, 128, p.scale, p.pos - 1, 0)
+            outs.append(host(O))
+        return outs
+
+    L.load().molot_hip_set_block_order(0)
+    try:
+        fixed = runs()
+    finally:
+        L.load().molot_hip_set_block_order(1)
+    assert np.array_equal(fixed[0], fixed[1]) and np.array_equal(fixed[1], fixed[2])
+    for o in runs():
+        assert normwise_err(o, fixed[0]) < 1e-6
 
 
 # ---------------------------------------------------------------------------
@@ -454,38 +501,49 @@ def test_c4_fused_step(gpu):
     assert normwise_err(O, oO) < FP32_TOL
 
 
-def test_graph_replays_match_eager(gpu):
+@pytest.mark.parametrize("dynamic", [0, 1])
+def test_graph_replays_match_eager(gpu, dynamic):
     """The fused step captured in a HIP graph: every replay (with eager work and
-    synchronisations between replays) equals the eager result.  Exercises the
-    self-resetting completion counters across launches."""
-    p = make_decode(32, 8, 128, 6000, seed=12)
-    q0 = dev(p.q)
-    K, V = dev(p.K), dev(p.V)
-    kn, vn, inv = dev(p.k_new), dev(p.v_new), dev(p.inv_freq)
-    O = torch.empty((32, 128), device="cuda")
-    q = q0.clone()
-    attn.decode_step(q, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
-    eager = host(O)
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        q.copy_(q0)
+    synchronisations between replays) equals the eager result -- bit for bit
+    with the fixed block order, to fp32 rounding with the dynamic one.
+    Exercises the per-slot arrival counters and epochs across launches."""
+    from molot_amd import lib as L
+    L.load().molot_hip_set_block_order(dynamic)
+    try:
+        p = make_decode(32, 8, 128, 6000, seed=12)
+        q0 = dev(p.q)
+        K, V = dev(p.K), dev(p.V)
+        kn, vn, inv = dev(p.k_new), dev(p.v_new), dev(p.inv_freq)
+        O = torch.empty((32, 128), device="cuda")
+        q = q0.clone()
         attn.decode_step(q, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    qg = q0.clone()
-    with torch.cuda.graph(g, stream=s):
-        attn.decode_step(qg, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
-    for r in range(5):
-        qg.copy_(q0)
-        O.fill_(float("nan"))
+        eager = host(O)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            q.copy_(q0)
+            attn.decode_step(q, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
         torch.cuda.synchronize()
-        g.replay()
-        torch.cuda.synchronize()
-        assert np.array_equal(host(O), eager), f"replay {r}"
-        # eager work in between replays
-        attn.attn_decode_gqa_cache(q, K, V, O, 32, 8, p.pos + 1, 128, p.scale, p.pos, 0)
-        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        qg = q0.clone()
+        with torch.cuda.graph(g, stream=s):
+            attn.decode_step(qg, kn, vn, K, V, O, 32, 8, 128, p.pos, p.pos, inv, p.scale, 0)
+        for r in range(5):
+            qg.copy_(q0)
+            O.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            got = host(O)
+            if dynamic:
+                assert normwise_err(got, eager) < 1e-6, f"replay {r}"
+            else:
+                assert np.array_equal(got, eager), f"replay {r}"
+            # eager work in between replays
+            attn.attn_decode_gqa_cache(q, K, V, O, 32, 8, p.pos + 1, 128, p.scale, p.pos, 0)
+            torch.cuda.synchronize()
+    finally:
+        L.load().molot_hip_set_block_order(1)
 
 
 def test_paged_matches_contiguous(gpu):
