@@ -5,15 +5,18 @@ Default workload = BASELINE.json configs[1] ("c2"): 32 query heads, 8 KV
 heads, head dim 128, fp32 token-major KV cache holding 16384 positions, one
 new token at pos 16384 (n = 16385 after the append), RoPE theta 500000,
 scale 1/sqrt(128), batch 1, q/K/V ~ N(0,1) from the repo's seeded generator.
+`--config c1|c3|c4|c5` measures the other BASELINE configs the same way
+(c4: 64 sequences over a paged bf16 cache, molot_hip_decode_step_paged).
 
 One step = one layer-step of the hot path through the C ABI
 (molot_hip_decode_step): RoPE of q and k, append of k/v into the cache,
-split-K attention (attn_kernel) and its log-sum-exp combine
-(combine_kernel), two launches on one stream.  Steps cycle over enough layers' KV caches
-(>= 1 GiB in total) that the 256 MB Infinity Cache cannot serve the stream:
-every step reads its layer's KV from HBM, as consecutive layers of a real
-decode do.  The K timed steps run as one HIP graph replay bracketed by
-events, inputs already resident in HBM.
+split-K attention (attn_kernel) and, when the context spans more than one
+chunk, its log-sum-exp combine (combine_kernel), launches on one stream.
+Steps cycle over enough layers' KV caches (>= 1 GiB of attended KV in
+total) that the 256 MB Infinity Cache cannot serve the stream: every step
+reads its layer's KV from HBM, as consecutive layers of a real decode do.
+The K timed steps run as one HIP graph replay bracketed by events, inputs
+already resident in HBM.
 
 value = unique KV bytes per step / time per step ("KV-stream GB/s").
 roofline = the dominant kernel, attn_kernel (RoPE, append and the split-K
@@ -23,7 +26,7 @@ hipExtLaunchKernelGGL while molot_hip_profile_* is on; eager launches on
 the bench stream after the timed region); achieved = the step's algorithmic
 bytes (all of which that kernel moves) / that duration; traffic =
 calibrated rocprofv3 FETCH_SIZE + WRITE_SIZE per launch
-(profiles/traffic.json).
+(profiles/traffic.json, per config).
 cpu_baseline = the reference's own attn.h decode step (oracle/_ref, built
 from the reference headers) on the host cores, same workload, bounded sample.
 """
@@ -36,24 +39,31 @@ import math
 import os
 import sys
 import time
+from types import SimpleNamespace
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
 METRIC = ("KV-stream HBM GB/s (% of peak) + µs/layer, 32q/8kv/d128 @16k ctx, 1 GPU")
+COLD_BYTES = 1 << 30  # attended KV cycled per timed pass (> 256 MB Infinity Cache)
 
 CONFIGS = {
-    # name: (nq, nkv, d, pos, theta, window, kv_dtype, sigma_kv)
-    "c1": (32, 8, 128, 4096, 500000.0, 0, 0, 1.0),
-    "c2": (32, 8, 128, 16384, 500000.0, 0, 0, 1.0),
-    "c3": (8, 4, 256, 32768, 10000.0, 1024, 0, 1.0),
-    "c5": (64, 8, 128, 131072, 500000.0, 0, 1, 0.5),
+    # contiguous token-major cache, batch 1
+    "c1": dict(nq=32, nkv=8, d=128, pos=4096, theta=500000.0, window=0, kvd=0, sigma=1.0),
+    "c2": dict(nq=32, nkv=8, d=128, pos=16384, theta=500000.0, window=0, kvd=0, sigma=1.0),
+    "c3": dict(nq=8, nkv=4, d=256, pos=32768, theta=10000.0, window=1024, kvd=0, sigma=1.0),
+    "c5": dict(nq=64, nkv=8, d=128, pos=131072, theta=500000.0, window=0, kvd=1, sigma=0.5),
+    # paged bf16 cache, 64 sequences of context U[512, 8192], shuffled 16-row pages
+    "c4": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=1, sigma=1.0, batch=64,
+               lmin=512, lmax=8192, page=16),
 }
 DESCR = {
     "c1": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 fp32 KV, pos 4096 (n=4097), batch 1",
     "c2": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 fp32 KV, ctx 16384 (n=16385), batch 1",
     "c3": "sliding-window GQA decode layer-step, 8q/4kv/d256 fp32 KV, pos 32768, window 1024",
+    "c4": "continuous-batching decode step, 64 sequences of ctx U[512,8192], 32q/8kv/d128, "
+          "bf16 KV in shuffled 16-token pages",
     "c5": "long-context GQA decode layer-step, 64q/8kv/d128 bf16 KV, pos 131072 (n=131073)",
 }
 
@@ -64,7 +74,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
-    ap.add_argument("--layers", type=int, default=0, help="KV caches to cycle (0 = auto, >=1 GiB)")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="KV caches to cycle (0 = auto, >= 1 GiB of attended KV)")
     ap.add_argument("--kernel-launches", type=int, default=200,
                     help="individually timed attention launches for the roofline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
@@ -74,6 +85,8 @@ def parse():
     ap.add_argument("--split-chunk", type=int, default=0, help="tokens per chunk (0 = auto)")
     ap.add_argument("--wgs-per-cu", type=int, default=0, help="workgroups per CU (0 = auto)")
     ap.add_argument("--variant", type=int, default=0, help="kernel mapping variant (0 = default)")
+    ap.add_argument("--block-order", type=int, default=1,
+                    help="1 = waves claim K/V blocks dynamically (default), 0 = fixed order")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
                     help="rocprofv3 PMC traffic summary (FETCH_SIZE/WRITE_SIZE per launch)")
     ap.add_argument("--pmc-run", action="store_true",
@@ -89,59 +102,51 @@ def log(args, *a):
 
 
 def algorithmic_bytes(nq, nkv, d, n_att, s_kv):
-    """Bytes one layer-step must move (decode-attention roofline):
+    """Bytes one sequence's layer-step must move (decode-attention roofline):
     KV stream 2*nkv*n_att*d*s_kv, q read + O write 2*nq*d*4, new k/v read as
-    fp32 and written at s_kv, the RoPE table d/2*4."""
+    fp32 and written at s_kv.  The RoPE table (d/2*4) is added once per step."""
     kv = 2 * nkv * n_att * d * s_kv
-    other = 2 * nq * d * 4 + 2 * nkv * d * (4 + s_kv) + (d // 2) * 4
+    other = 2 * nq * d * 4 + 2 * nkv * d * (4 + s_kv)
     return kv, kv + other
 
 
-def main() -> int:
-    args = parse()
-    if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by KV head across GPUs with no exchange (see DESIGN.md), "
-              "but nothing here launches on more than one device.", file=sys.stderr)
-        return 2
+def kernel_label(d, nq, nkv, kvd, paged, nchunks):
+    G = nq // nkv
+    gh = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
+    t = "float" if kvd == 0 else "bf16"
+    s = f"attn_kernel<{d},{gh},{t},paged={'true' if paged else 'false'},rope=true>"
+    return s + (" (then combine_kernel: split-K merge)" if nchunks > 1 else " (single chunk)")
 
-    import numpy as np
-    import torch
 
+# ---------------------------------------------------------------------------
+# workloads: inputs resident on the device, one step / attention-only launch,
+# byte counts and the CPU-baseline sample
+
+def contiguous_workload(args, cfg, lib, L, torch, np):
     from molot_amd import attn
-    from molot_amd import lib as L
     from molot_amd.synth import Stream, f32_to_bf16
 
-    if not torch.cuda.is_available():
-        print("bench.py: no GPU visible", file=sys.stderr)
-        return 1
-    lib = L.load()
-    torch.cuda.set_device(0)
-    if args.split_chunk:
-        attn.set_split_chunk(args.split_chunk)
-    if args.wgs_per_cu or args.variant:
-        lib.molot_hip_set_tuning(args.wgs_per_cu, args.variant)
-
-    nq, nkv, d, pos, theta, window, kvd, sigma = CONFIGS[args.config]
+    nq, nkv, d, pos = cfg["nq"], cfg["nkv"], cfg["d"], cfg["pos"]
+    theta, window, kvd, sigma = cfg["theta"], cfg["window"], cfg["kvd"], cfg["sigma"]
     s_kv = 4 if kvd == 0 else 2
     n = pos + 1
     t0 = max(0, pos - window + 1) if window > 0 else 0
     n_att = n - t0
     kv_bytes, step_bytes = algorithmic_bytes(nq, nkv, d, n_att, s_kv)
+    step_bytes += (d // 2) * 4
     cache_bytes = 2 * n * nkv * d * s_kv
-    layers = args.layers or max(2, math.ceil((1 << 30) / cache_bytes))
+    layers = args.layers or max(2, math.ceil(COLD_BYTES / kv_bytes))
     scale = 1.0 / math.sqrt(d)
 
-    # ---- inputs (seeded; one host draw, replicated per layer on the device) ----
-    t_setup = time.time()
     st = Stream(1234)
     q_h = st.normal((nq, d))
     k_h = st.normal((nkv, d))
     v_h = st.normal((nkv, d))
     K_h = np.zeros((n, nkv * d), np.float32)
     V_h = np.zeros_like(K_h)
-    K_h[:pos] = st.normal((pos, nkv * d), sigma)
-    V_h[:pos] = st.normal((pos, nkv * d), sigma)
+    # only the attended rows are drawn (a window's earlier rows are never read)
+    K_h[t0:pos] = st.normal((pos - t0, nkv * d), sigma)
+    V_h[t0:pos] = st.normal((pos - t0, nkv * d), sigma)
     dt = torch.float32 if kvd == 0 else torch.bfloat16
 
     def to_dev(a):
@@ -162,16 +167,11 @@ def main() -> int:
     O = torch.empty((nq, d), dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
     del K_h, V_h
-    log(args, f"setup {time.time() - t_setup:.1f}s: {args.config} layers={layers} "
-        f"cache={cache_bytes / 2**20:.0f} MiB/layer dtype={dt}")
 
     P = ctypes.c_void_p
     qp, kp, vp, ip, op = (P(t.data_ptr()) for t in (q, k_new, v_new, inv, O))
     Kp = [P(t.data_ptr()) for t in Ks]
     Vp = [P(t.data_ptr()) for t in Vs]
-
-    def cur_stream():
-        return P(torch.cuda.current_stream().cuda_stream)
 
     def step(i, stream):
         l = i % layers
@@ -187,10 +187,154 @@ def main() -> int:
         if rc:
             raise L.MolotHipError(rc, "attn_decode_gqa_cache")
 
-    nch = ctypes.c_int()
-    chk = ctypes.c_int()
-    # the fused step tiles the cached rows; the new token joins the last chunk
-    lib.molot_hip_split_plan(nkv, n_att - 1, d, kvd, ctypes.byref(nch), ctypes.byref(chk))
+    def cpu(args_):
+        return cpu_baseline_contiguous(args_, q_h, k_h, v_h, nq, nkv, d, pos, theta, window, kvd,
+                                       sigma, scale, kv_bytes)
+
+    return SimpleNamespace(
+        step=step, attention=attention, kv_bytes=kv_bytes, step_bytes=step_bytes, layers=layers,
+        cache_desc=f"cache={cache_bytes / 2**20:.0f} MiB/layer dtype={dt}", paged=False,
+        head_traffic=2 * nq * n_att * d * s_kv, cpu=cpu,
+        config={"nq": nq, "nkv": nkv, "head_dim": d, "pos": pos, "n": n, "window": window,
+                "rope_theta": theta, "batch": 1},
+        keep=(Ks, Vs, q, k_new, v_new, inv, O))
+
+
+def paged_workload(args, cfg, lib, L, torch, np):
+    """c4: B sequences with context U[lmin, lmax] from the seeded stream, one
+    new token each; bf16 K/V pages [block][nkv][page][d] behind a shuffled
+    block table (the tests' make_paged draws, same order and seed)."""
+    from molot_amd import attn
+    from molot_amd.synth import Stream, f32_to_bf16
+
+    nq, nkv, d, B, page = cfg["nq"], cfg["nkv"], cfg["d"], cfg["batch"], cfg["page"]
+    theta, window, kvd, sigma = cfg["theta"], cfg["window"], cfg["kvd"], cfg["sigma"]
+    assert kvd == 1 and window == 0
+    s_kv = 2
+    st = Stream(1234)
+    q_h = st.normal((B, nq, d))
+    k_h = st.normal((B, nkv, d))
+    v_h = st.normal((B, nkv, d))
+    Lc = st.uniform_int(cfg["lmin"], cfg["lmax"], B).astype(np.int32)  # context before the token
+    n = Lc + 1
+    blocks = (n + page - 1) // page
+    nblk = int(blocks.sum()) + 7
+    perm = st.permutation(nblk)
+    max_blocks = int(blocks.max())
+    bt = np.zeros((B, max_blocks), np.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :blocks[b]] = perm[o:o + blocks[b]]
+        o += blocks[b]
+    Kp_h = f32_to_bf16(st.normal((nblk, nkv, page, d), sigma))
+    Vp_h = f32_to_bf16(st.normal((nblk, nkv, page, d), sigma))
+
+    kv_bytes = 0
+    step_bytes = (d // 2) * 4 + int(blocks.sum()) * 4  # RoPE table + block-table entries
+    for b in range(B):
+        kv, tot = algorithmic_bytes(nq, nkv, d, int(n[b]), s_kv)
+        kv_bytes += kv
+        step_bytes += tot + 4  # + its seq_lens entry
+    cache_bytes = 2 * nblk * nkv * page * d * s_kv
+    layers = args.layers or max(2, math.ceil(COLD_BYTES / kv_bytes))
+    scale = 1.0 / math.sqrt(d)
+
+    def to_dev_bf16(a):
+        return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
+
+    K0, V0 = to_dev_bf16(Kp_h), to_dev_bf16(Vp_h)
+    Ks = [K0] + [torch.empty_like(K0) for _ in range(layers - 1)]
+    Vs = [V0] + [torch.empty_like(V0) for _ in range(layers - 1)]
+    for i in range(1, layers):
+        Ks[i].copy_(K0)
+        Vs[i].copy_(V0)
+    q = torch.from_numpy(q_h).cuda()
+    k_new = torch.from_numpy(k_h).cuda()
+    v_new = torch.from_numpy(v_h).cuda()
+    bt_d = torch.from_numpy(bt.reshape(-1)).cuda()
+    sl_d = torch.from_numpy(n.astype(np.int32)).cuda()
+    inv = attn.rope_inv_freq(theta, d).cuda()
+    O = torch.empty((B, nq, d), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    max_len = int(n.max())
+
+    P = ctypes.c_void_p
+    qp, kp, vp, ip, op, btp, slp = (P(t.data_ptr())
+                                    for t in (q, k_new, v_new, inv, O, bt_d, sl_d))
+    Kp = [P(t.data_ptr()) for t in Ks]
+    Vp = [P(t.data_ptr()) for t in Vs]
+
+    def step(i, stream):
+        l = i % layers
+        rc = lib.molot_hip_decode_step_paged(qp, kp, vp, Kp[l], Vp[l], op, btp, slp, None, B,
+                                             max_blocks, max_len, nq, nkv, d, page, ip, scale,
+                                             window, kvd, stream)
+        if rc:
+            raise L.MolotHipError(rc, "decode_step_paged")
+
+    def attention(i, stream):
+        l = i % layers
+        rc = lib.molot_hip_attn_decode_paged(qp, Kp[l], Vp[l], op, btp, slp, None, B, max_blocks,
+                                             max_len, nq, nkv, d, page, scale, window, kvd,
+                                             stream)
+        if rc:
+            raise L.MolotHipError(rc, "attn_decode_paged")
+
+    def cpu(args_):
+        return cpu_baseline_paged(args_, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page,
+                                  theta, scale, kv_bytes)
+
+    return SimpleNamespace(
+        step=step, attention=attention, kv_bytes=kv_bytes, step_bytes=step_bytes, layers=layers,
+        cache_desc=(f"{B} seqs, ctx {int(Lc.min())}..{int(Lc.max())} (sum {int(n.sum())}), "
+                    f"{nblk} pages, cache={cache_bytes / 2**20:.0f} MiB/layer bf16"),
+        paged=True, head_traffic=2 * nq * int(n.sum()) * d * s_kv, cpu=cpu,
+        config={"nq": nq, "nkv": nkv, "head_dim": d, "batch": B, "page": page,
+                "ctx_min": int(Lc.min()), "ctx_max": int(Lc.max()), "tokens": int(n.sum()),
+                "window": window, "rope_theta": theta},
+        keep=(Ks, Vs, q, k_new, v_new, bt_d, sl_d, inv, O))
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the path shards by KV head across GPUs with no exchange (see DESIGN.md), "
+              "but nothing here launches on more than one device.", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from molot_amd import attn
+    from molot_amd import lib as L
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 1
+    lib = L.load()
+    torch.cuda.set_device(0)
+    if args.split_chunk:
+        attn.set_split_chunk(args.split_chunk)
+    if args.wgs_per_cu or args.variant:
+        lib.molot_hip_set_tuning(args.wgs_per_cu, args.variant)
+    lib.molot_hip_set_block_order(args.block_order)
+
+    cfg = CONFIGS[args.config]
+    t_setup = time.time()
+    make = paged_workload if "batch" in cfg else contiguous_workload
+    wl = make(args, cfg, lib, L, torch, np)
+    kvd = cfg["kvd"]
+    log(args, f"setup {time.time() - t_setup:.1f}s: {args.config} layers={wl.layers} "
+        f"{wl.cache_desc}")
+
+    P = ctypes.c_void_p
+
+    def cur_stream():
+        return P(torch.cuda.current_stream().cuda_stream)
+
+    step, attention = wl.step, wl.attention
+    kv_bytes, step_bytes = wl.kv_bytes, wl.step_bytes
 
     if args.pmc_run:
         # eager launches only (one counter record per dispatch), then a copy of
@@ -219,6 +363,7 @@ def main() -> int:
         for i in range(args.warmup):
             step(i, sp)
     torch.cuda.synchronize()
+    nch, chk = attn.last_plan()
 
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
@@ -275,7 +420,7 @@ def main() -> int:
     a1_us, a2_us = kernel_times(attention, J)
     achieved = step_bytes / (k1_us * 1e-6) / 1e9
     log(args, f"attn_kernel {k1_us:.2f} us/launch -> {achieved:.0f} GB/s "
-        f"(chunks {nch.value} x {chk.value} tokens); combine_kernel {k2_us:.2f} us; "
+        f"(chunks {nch} x {chk} rows); combine_kernel {k2_us:.2f} us; "
         f"attention-only entry: {a1_us:.2f} + {a2_us:.2f} us")
 
     # ---- achievable streaming-read peak on this box (probe kernel, 4 GiB) ----
@@ -303,11 +448,14 @@ def main() -> int:
     try:
         with open(args.traffic) as f:
             tr = json.load(f)
-        if tr.get("config") == args.config:
-            traffic = tr.get("traffic_bytes_per_launch")
-    except (OSError, ValueError):
+        traffic = tr.get(args.config, {}).get("traffic_bytes_per_launch")
+    except (OSError, ValueError, AttributeError):
         pass
 
+    config = {"workload": DESCR[args.config], "config": args.config}
+    config.update(wl.config)
+    config.update({"kv_layers_cycled": wl.layers, "timing": mode, "split_chunks": nch,
+                   "chunk_rows": chk})
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -320,11 +468,9 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32" if kvd == 0 else "bf16-kv/f32-acc",
-        "data": "synthetic (seeded N(0,1) q/K/V, splitmix64+Box-Muller, seed 1234)",
-        "config": {"workload": DESCR[args.config], "config": args.config, "nq": nq, "nkv": nkv,
-                   "head_dim": d, "pos": pos, "n": n, "window": window, "rope_theta": theta,
-                   "batch": 1, "kv_layers_cycled": layers, "timing": mode,
-                   "split_chunks": nch.value, "chunk_tokens": chk.value},
+        "data": (f"synthetic (seeded N(0,{cfg['sigma']:g}) K/V, N(0,1) q/k/v, "
+                 "splitmix64+Box-Muller, seed 1234)"),
+        "config": config,
         "us_per_layer_step": round(us_step, 3),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
         "pct_of_measured_read_peak": round(100 * value / read_peak, 2),
@@ -332,11 +478,10 @@ def main() -> int:
         "kv_bytes_per_step": kv_bytes,
         "algorithmic_bytes_per_step": step_bytes,
         "total_gbps": round(step_bytes / (ms_per_step * 1e-3) / 1e9, 2),
-        "head_traffic_gbps": round(2 * nq * n_att * d * s_kv / (ms_per_step * 1e-3) / 1e9, 2),
+        "head_traffic_gbps": round(wl.head_traffic / (ms_per_step * 1e-3) / 1e9, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": f"attn_kernel<{d},{min(8, nq // nkv)},{'float' if kvd == 0 else 'bf16'},"
-                      "paged=false,rope=true> (then combine_kernel: split-K merge)",
+            "kernel": kernel_label(cfg["d"], cfg["nq"], cfg["nkv"], kvd, wl.paged, nch),
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
@@ -350,14 +495,26 @@ def main() -> int:
     }
 
     if args.cpu_seconds > 0:
-        out["cpu_baseline"] = cpu_baseline(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window,
-                                           kvd, sigma, scale, kv_bytes)
+        out["cpu_baseline"] = wl.cpu(args)
     print(json.dumps(out), flush=True)
     return 0
 
 
-def cpu_baseline(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window, kvd, sigma, scale,
-                 kv_bytes):
+def _cpu_loop(args, one):
+    for i in range(2):  # warmup 2 (bench/bench.cc:45-52)
+        one(i)
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        one(steps)
+        steps += 1
+        el = time.perf_counter() - t0
+        if (el >= args.cpu_seconds and steps >= 3) or steps >= 100000:
+            return steps, el
+
+
+def cpu_baseline_contiguous(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window, kvd, sigma,
+                            scale, kv_bytes):
     """The reference's decode step on the host cores (bounded sample).
 
     kind "reference": include/molot/attn.h + forward.h's rope/append sequence,
@@ -372,22 +529,27 @@ def cpu_baseline(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window, kvd, sigma
 
     cores = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
     n = pos + 1
+    t0 = max(0, pos - window + 1) if window > 0 else 0
     st = Stream(4321)
     S = nkv * d
-    # rotate copies so the KV stream is DRAM-cold w.r.t. the host LLC
-    per_copy = 2 * n * S * 4
-    copies = max(2, math.ceil(256 * 2**20 / per_copy))
+    # rotate copies so the attended KV exceeds the host LLC (DRAM-cold); rows
+    # before a window are never touched, so np.zeros leaves them unbacked
+    per_copy = 2 * (n - t0) * S * 4
+    copies = max(2, math.ceil(512 * 2**20 / per_copy))
+    rows = st.normal((pos - t0, S), sigma)
+    rows_v = st.normal((pos - t0, S), sigma)
+    if kvd:
+        rows = bf16_to_f32(f32_to_bf16(rows))
+        rows_v = bf16_to_f32(f32_to_bf16(rows_v))
     Ks, Vs = [], []
     for _ in range(copies):
         K = np.zeros((n, S), np.float32)
         V = np.zeros_like(K)
-        K[:pos] = st.normal((pos, S), sigma)
-        V[:pos] = st.normal((pos, S), sigma)
-        if kvd:
-            K[:pos] = bf16_to_f32(f32_to_bf16(K[:pos]))
-            V[:pos] = bf16_to_f32(f32_to_bf16(V[:pos]))
+        K[t0:pos] = rows
+        V[t0:pos] = rows_v
         Ks.append(K)
         Vs.append(V)
+    del rows, rows_v
     inv = oracle.rope_inv_freq(theta, d)
     O = np.empty((nq, d), np.float32)
     P = oracle._p
@@ -406,16 +568,7 @@ def cpu_baseline(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window, kvd, sigma
             oracle.lib().orc_decode_step(P(q), P(k), P(v_h), P(Ks[c]), P(Vs[c]), P(O), nq, nkv,
                                          d, pos, pos, P(inv), scale, window, 0, cores)
 
-    for i in range(2):  # warmup 2 (bench/bench.cc:45-52)
-        one(i)
-    t0 = time.perf_counter()
-    steps = 0
-    while True:
-        one(steps)
-        steps += 1
-        el = time.perf_counter() - t0
-        if (el >= args.cpu_seconds and steps >= 3) or steps >= 100000:
-            break
+    steps, el = _cpu_loop(args, one)
     if pool:
         pool.close()
     ms = el / steps * 1e3
@@ -428,11 +581,79 @@ def cpu_baseline(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window, kvd, sigma
         "kind": kind,
         "ms_per_step": round(ms, 4),
         "sample": (f"{steps} layer-steps of {args.config} (rope q/k + append + "
-                   f"attn_decode_gqa_cache, n={n}) cycling {copies} KV copies of "
-                   f"{per_copy / 2**20:.0f} MiB, {el:.1f} s; "
+                   f"attn_decode_gqa_cache, n={n}, rows {t0}..{n - 1}) cycling {copies} KV "
+                   f"copies of {per_copy / 2**20:.0f} MiB attended, {el:.1f} s; "
                    + ("reference headers via oracle/_ref, ThreadPool" if kind == "reference"
                       else "oracle C restatement, OpenMP static over heads")
                    + ("; bf16 values widened to fp32 (no reference bf16 path)" if kvd else "")),
+    }
+
+
+def cpu_baseline_paged(args, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page, theta, scale,
+                       kv_bytes):
+    """c4 on the host cores: the reference's decode step (rope q/k, append,
+    attn_decode_gqa_cache) once per sequence, over per-sequence contiguous
+    fp32 caches gathered from the pages and widened from bf16.  The reference
+    has neither a paged nor a bf16 cache, so this is the reference algorithm
+    on the same values, not a reference run of the same format; the
+    contiguous fp32 copies are 2x the GPU's bytes, and the GB/s reported is
+    the GPU workload's KV bytes over the CPU time."""
+    import numpy as np
+
+    import oracle
+    from molot_amd.synth import bf16_to_f32
+
+    cores = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+    B = len(n)
+    S = nkv * d
+    Kc, Vc = [], []
+    for b in range(B):
+        nb = int(n[b])
+        blk = bt[b, :(nb + page - 1) // page]
+        for src, dst in ((Kp_h, Kc), (Vp_h, Vc)):
+            x = bf16_to_f32(src[blk]).transpose(0, 2, 1, 3).reshape(-1, S)[:nb]
+            dst.append(np.ascontiguousarray(x))
+    inv = oracle.rope_inv_freq(theta, d)
+    O = np.empty((nq, d), np.float32)
+    P = oracle._p
+    kind = "reference" if oracle.ref_available() else "port"
+    pool = oracle.RefPool(cores) if kind == "reference" else None
+
+    def one(i):
+        for b in range(B):
+            nb = int(n[b])
+            q = q_h[b].copy()
+            k = k_h[b].copy()
+            v = v_h[b].copy()
+            if kind == "reference":
+                rc = oracle.ref().ref_decode_step(P(q), P(k), P(v), P(Kc[b]), P(Vc[b]), P(O), nq,
+                                                  nkv, d, nb - 1, nb, nb - 1, P(inv), scale, 0,
+                                                  pool.h)
+                assert rc == 0
+            else:
+                oracle.lib().orc_decode_step(P(q), P(k), P(v), P(Kc[b]), P(Vc[b]), P(O), nq,
+                                             nkv, d, nb - 1, nb - 1, P(inv), scale, 0, 0, cores)
+
+    steps, el = _cpu_loop(args, one)
+    if pool:
+        pool.close()
+    ms = el / steps * 1e3
+    gbps = kv_bytes / (ms * 1e-3) / 1e9
+    log(args, f"cpu baseline ({kind}, {cores} threads): {ms:.3f} ms/step -> {gbps:.1f} GB/s")
+    fp32_mib = sum(x.nbytes for x in Kc + Vc) / 2**20
+    return {
+        "value": round(gbps, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": kind,
+        "ms_per_step": round(ms, 4),
+        "sample": (f"{steps} batch-steps of c4 ({B} sequences, each rope q/k + append + "
+                   f"attn_decode_gqa_cache over its contiguous fp32 cache, {fp32_mib:.0f} MiB in "
+                   f"all), {el:.1f} s; "
+                   + ("reference headers via oracle/_ref, ThreadPool" if kind == "reference"
+                      else "oracle C restatement, OpenMP static over heads")
+                   + "; bf16 pages gathered and widened to fp32 (the reference has no paged "
+                     "or bf16 cache)"),
     }
 
 

@@ -166,6 +166,14 @@ void molot_hip_set_tuning(int wgs_per_cu, int variant);
  * order, bit-identical from run to run.  Process-wide. */
 void molot_hip_set_block_order(int dynamic);
 
+/* Kernel for bf16 KV caches with head dim 64 or 128.  mfma = 1 (default):
+ * the matrix-core kernel (scores and PV on v_mfma_f32_16x16x32_bf16, q and
+ * the probabilities split into three bf16 pieces each, fp32 accumulation);
+ * mfma = 0: the vector-ALU kernel of the fp32 caches.  Both compute the
+ * same softmax(q.K^T*scale).V to fp32 rounding.  Process-wide; for
+ * comparisons and tests. */
+void molot_hip_set_bf16_path(int mfma);
+
 /* Launch profiling, the counterpart of the reference's MOLOT_PROFILE
  * attention timer (include/molot/forward.h:114-137, :588-591).
  * molot_hip_profile_begin(max_launches) starts recording: each attention
@@ -179,9 +187,10 @@ void molot_hip_set_block_order(int dynamic);
 int molot_hip_profile_begin(int max_launches);
 int molot_hip_profile_end(float* attn_ms, float* combine_ms, int* launches, int* combines);
 
-/* Launch geometry the attention entry points would use for a problem:
- * writes the number of context chunks per KV head and tokens per chunk. */
-int molot_hip_split_plan(int nkv, int n_att, int d, int kv_dtype, int* nchunks, int* chunk);
+/* Geometry of the calling thread's last attention launch: context chunks
+ * per (sequence, KV head) (grid x; 1 = no combine kernel) and rows per
+ * chunk.  Returns MOLOT_EINVAL before the thread's first launch. */
+int molot_hip_last_plan(int* nchunks, int* chunk);
 
 #ifdef __cplusplus
 } /* extern "C" */

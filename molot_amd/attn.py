@@ -24,7 +24,7 @@ __all__ = [
     "attn_decode_gqa", "attn_decode_gqa_win", "attn_decode_head", "attn_decode_head_win",
     "attn_decode_strided", "decode_step", "attn_decode_paged", "decode_step_paged",
     "rope_append_paged", "vexp",
-    "split_plan", "set_split_chunk", "KVCache", "kv_dtype_of",
+    "last_plan", "set_split_chunk", "KVCache", "kv_dtype_of",
 ]
 
 
@@ -239,10 +239,11 @@ def vexp(x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
     return y
 
 
-def split_plan(nkv: int, n_att: int, d: int = 128, kv_dtype: int = KV_F32):
+def last_plan():
+    """(chunks per (sequence, KV head), rows per chunk) of this thread's last
+    attention launch."""
     nch, ch = ctypes.c_int(), ctypes.c_int()
-    check(_lib.load().molot_hip_split_plan(nkv, n_att, d, kv_dtype, ctypes.byref(nch),
-                                           ctypes.byref(ch)), "split_plan")
+    check(_lib.load().molot_hip_last_plan(ctypes.byref(nch), ctypes.byref(ch)), "last_plan")
     return nch.value, ch.value
 
 

@@ -363,6 +363,82 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// The workgroup's chunk partial from its waves' partials in LDS: running
+// max wm[w*GH + g], sum wl[w*GH + g] and unnormalised o red[w*RS + g*D + d]
+// of wave w (waves without rows hold max -inf).  A single-chunk problem
+// writes O = o / l (and, with ROPE, the rotated q from qs) directly;
+// otherwise (o, max, sum) goes to the workspace for combine_kernel.
+template <int D, int GH, int NW, int NT, bool ROPE>
+__device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm, const float* wl,
+                                             const float* red, int RS, const float* qs, int tid,
+                                             int lane, bool split, int64_t slot, int c,
+                                             int64_t qrow0) {
+  constexpr int P = GH * D;
+  // Every thread derives the chunk partial of its own output pairs from the
+  // wave partials (wave weights e^(m_w - M); waves without rows weigh
+  // e^-inf = 0).  Pairs: tid % Q + i*Q, i < PP; phase ph = tid / P.
+  constexpr int PP = (P + NT - 1) / NT, Q = P < NT ? P : NT;
+  const int ph = PP == 1 ? tid / P : 0;
+  int pr_[PP], g_[PP];
+  bool pv_[PP];
+  float po[PP], pm[PP], pl[PP];
+  // The 64 pairs of a wave lie in one head (D is a multiple of 64), so the
+  // wave weights are wave-uniform: lane ww < NW computes wave ww's weight,
+  // DPP/shuffle reductions give the chunk max and sum, and the weights reach
+  // every lane through readlane.
+  static_assert(D % 64 == 0 && NW <= 64, "wave-uniform head per 64 pairs");
+#pragma unroll
+  for (int i = 0; i < PP; ++i) {
+    pr_[i] = tid % Q + i * Q;
+    pv_[i] = pr_[i] < P;
+    g_[i] = pv_[i] ? pr_[i] / D : 0;
+    const int g = __builtin_amdgcn_readfirstlane(g_[i]);
+    const float mw_l = lane < NW ? wm[lane * GH + g] : -INFINITY;
+    const float m = group_max<NW <= 16 ? 16 : 64>(mw_l);  // lanes >= NW hold -inf
+    const float e_l = lane < NW ? softmax_exp(mw_l - m) : 0.f;  // waves without rows: 0
+    const float l = group_sum<NW <= 16 ? 16 : 64>(lane < NW ? e_l * wl[lane * GH + g] : 0.f);
+    float o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww)
+      o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e_l), ww)),
+               red[ww * RS + (pv_[i] ? pr_[i] : 0)], o);
+    po[i] = o;
+    pm[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
+    pl[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(l)));
+  }
+  const bool lead = ph == 0;  // phase 0 threads own the chunk partial's outputs
+  if (!split) {
+#pragma unroll
+    for (int i = 0; i < PP; ++i)
+      if (lead && pv_[i]) a.o[qrow0 * D + pr_[i]] = po[i] / pl[i];
+    if constexpr (ROPE) {
+      if (a.q_out)
+        for (int i = tid; i < P; i += NT) a.q_out[qrow0 * D + i] = qs[i];
+    }
+    return;
+  }
+
+  // ---- 5. the chunk partial for the combine kernel ----
+  // Plain stores: the combine kernel runs after this one on the same stream,
+  // so the kernel boundary orders them; no flag, counter or cleared memory
+  // is needed between the two launches.
+  float* po_s = a.part_o + (slot * a.nchunks + c) * P;
+  float* pml_s = a.part_ml + (slot * a.nchunks + c) * (GH * 2);
+#pragma unroll
+  for (int i = 0; i < PP; ++i) {
+    if (!(lead && pv_[i])) continue;
+    po_s[pr_[i]] = po[i];
+    if (pr_[i] - g_[i] * D == 0) {
+      pml_s[2 * g_[i]] = pm[i];
+      pml_s[2 * g_[i] + 1] = pl[i];
+    }
+  }
+  if constexpr (ROPE) {  // the rotated q leaves through the combine kernel
+    if (c == 0 && a.q_out)
+      for (int i = tid; i < P; i += NT) a.qrot[slot * P + i] = qs[i];
+  }
+}
+
 template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
 __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   using V16 = typename KVT<T>::vec;
@@ -748,69 +824,399 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       for (int e = 0; e < VW; ++e) red[(w * GH + g) * D + cs * VW + e] = acc[g][e];
   }
   lds_barrier();
-  // Every thread derives the chunk partial of its own output pairs from the
-  // wave partials (wave weights e^(m_w - M); waves without rows weigh
-  // e^-inf = 0).  Pairs: tid % Q + i*Q, i < PP; phase ph = tid / P.
-  constexpr int PP = C::PP, Q = C::Q;
-  const int ph = PP == 1 ? tid / P : 0;
-  int pr_[PP], g_[PP];
-  bool pv_[PP];
-  float po[PP], pm[PP], pl[PP];
-  // The 64 pairs of a wave lie in one head (D is a multiple of 64), so the
-  // wave weights are wave-uniform: lane ww < NW computes wave ww's weight,
-  // DPP/shuffle reductions give the chunk max and sum, and the weights reach
-  // every lane through readlane.
-  static_assert(D % 64 == 0 && NW <= 64, "wave-uniform head per 64 pairs");
-#pragma unroll
-  for (int i = 0; i < PP; ++i) {
-    pr_[i] = tid % Q + i * Q;
-    pv_[i] = pr_[i] < P;
-    g_[i] = pv_[i] ? pr_[i] / D : 0;
-    const int g = __builtin_amdgcn_readfirstlane(g_[i]);
-    const float mw_l = lane < NW ? wm[lane * GH + g] : -INFINITY;
-    const float m = group_max<NW <= 16 ? 16 : 64>(mw_l);  // lanes >= NW hold -inf
-    const float e_l = lane < NW ? softmax_exp(mw_l - m) : 0.f;  // waves without rows: 0
-    const float l = group_sum<NW <= 16 ? 16 : 64>(lane < NW ? e_l * wl[lane * GH + g] : 0.f);
-    float o = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww)
-      o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e_l), ww)),
-               red[ww * P + (pv_[i] ? pr_[i] : 0)], o);
-    po[i] = o;
-    pm[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
-    pl[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(l)));
+  finish_chunk<D, GH, NW, NT, ROPE>(a, wm, wl, red, P, qs, tid, lane, split, slot, c, qrow0);
+}
+
+// ---------------------------------------------------------------------------
+// bf16 KV on the matrix cores.
+//
+// A wave takes tiles of 32 cache rows of the workgroup's KV head (claimed
+// like the blocks of attn_kernel) and keeps the GH <= 16 query heads of the
+// group on the 16 columns of v_mfma_f32_16x16x32_bf16:
+//   scores  S^T (32 rows x 16 heads) = K (32 x D) . Q^T (D x 16), two 16-row
+//           halves, D/32 k-steps each.  K goes from HBM straight into the A
+//           operand: lane l holds row l%16 and elements 8*(l/16)..+7 of a
+//           32-wide k-step, one 16-byte load.  q (fp32) enters as three bf16
+//           pieces hi + mid + lo, which together hold its 24-bit significand,
+//           so the scores are the fp32 products of q with the bf16 K summed
+//           in fp32.
+//   softmax the accumulator of a half holds, in lane l, head l%16 and rows
+//           4*(l/16)+r: a lane owns one head and 8 rows of the tile, and the
+//           online max / rescale run in place (max across the 4 lanes of a
+//           head by two shuffles).
+//   PV      O^T (D x 16) += V^T (D x 32) . P^T (32 x 16) per 16-row block of
+//           O^T.  The k index of this product runs over the tile's rows in
+//           the order tau(g, e) = 16*(e/4) + 4g + e%4 (g = l/16): exactly the
+//           8 probabilities lane l already holds, so P is the B operand as it
+//           stands (again as bf16 hi + mid + lo).  V is staged in LDS
+//           (row-major, 32-byte segments XOR-swizzled by row so the
+//           transposed reads below hit distinct banks) and read back with
+//           ds_read_b64_tr_b16: lane l reads 8 bytes of row l/4 (+16) at
+//           column 16*dt + 4*(l%4), and the transpose hands lane i of each
+//           16-lane group element i%4 of lane 4e+i/4's read as slot e, i.e.
+//           V[tau(g, e)][16*dt + i]: the A operand.
+// Prologue, new token and chunk output are those of attn_kernel.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaWaves = 4;                  // waves per workgroup
+constexpr int kMfmaThreads = kMfmaWaves * 64;
+constexpr int kTile = 32;                      // cache rows per wave step
+
+// LDS of attn_mfma_kernel, in floats.  vt: per wave, 32 staged V rows of D
+// bf16 (16*D floats), which after the stream hold the wave's partial o.
+struct LdsM {
+  int qs, cs, sn, knew, vnew, wm, wl, vt, blk, misc, total;
+  __host__ __device__ LdsM(int D, int GH, int chunk, int page_shift, bool paged) {
+    int o = 0;
+    qs = o; o += GH * D;
+    cs = o; o += D / 2;
+    sn = o; o += D / 2;
+    knew = o; o += D;
+    vnew = o; o += D;
+    wm = o; o += kMfmaWaves * GH;
+    wl = o; o += kMfmaWaves * GH;
+    o = (o + 63) & ~63;  // 256-byte aligned: the swizzle's bank pattern
+    vt = o; o += kMfmaWaves * kTile * D / 2;
+    blk = o; o += paged ? ((chunk >> page_shift) + 2) : 0;
+    misc = o; o += 8;
+    total = o;
   }
-  const bool lead = ph == 0;  // phase 0 threads own the chunk partial's outputs
-  if (!split) {
-#pragma unroll
-    for (int i = 0; i < PP; ++i)
-      if (lead && pv_[i]) a.o[qrow0 * D + pr_[i]] = po[i] / pl[i];
-    if constexpr (ROPE) {
-      if (a.q_out)
-        for (int i = tid; i < P; i += NT) a.q_out[qrow0 * D + i] = qs[i];
-    }
+};
+
+// x = hi + mid + lo in bf16 (round to nearest even at each step); the three
+// pieces carry the full fp32 significand.
+__device__ __forceinline__ void split3(float x, __bf16& hi, __bf16& mid, __bf16& lo) {
+  hi = (__bf16)x;
+  float r = x - (float)hi;
+  mid = (__bf16)r;
+  r -= (float)mid;
+  lo = (__bf16)r;
+}
+
+__device__ __forceinline__ f32x4 mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int D, int GH, bool PAGED, bool ROPE>
+__global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) {
+  static_assert(D == 64 || D == 128, "MFMA tiles cover D = 64 or 128");
+  static_assert(GH >= 1 && GH <= 16, "the group's q heads on the 16 MFMA columns");
+  constexpr int NW = kMfmaWaves, NT = kMfmaThreads;
+  constexpr int KK = D / 32;  // k-steps of the score product
+  constexpr int DT = D / 16;  // 16-row blocks of O^T
+  constexpr int NSEG = D / 16;  // 32-byte segments of a staged V row
+  constexpr int RBY = 2 * D;  // bytes of a staged V row
+  constexpr int RS = kTile * D / 2;  // floats of a wave's LDS region
+
+  extern __shared__ float smem[];
+  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED);
+  float* qs = smem + L.qs;
+  float* knew = smem + L.knew;
+  float* vnew = smem + L.vnew;
+  int* misc = reinterpret_cast<int*>(smem + L.misc);
+
+  const int c = blockIdx.x;
+  const int G = a.nq / a.nkv;
+  const int nsub = G / GH;
+  const int sub = blockIdx.y % nsub;
+  const int h = blockIdx.y / nsub;
+  const int hq0 = h * G + sub * GH;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m16 = lane & 15, g4 = lane >> 4;
+
+  int n = a.n, t0 = a.t0, pos = a.pos;
+  if constexpr (PAGED) {
+    n = a.seq_lens[b];
+    pos = a.pos_arr ? a.pos_arr[b] : n - 1;
+    t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
+    if (t0 > n) t0 = n;
+  }
+  const int cend = ROPE ? n - 1 : n;
+  int nch = a.nchunks;
+  if constexpr (PAGED) {
+    const int span = cend - t0;
+    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (ROPE ? 1 : 0);
+    if (nch > a.nchunks) nch = a.nchunks;
+  }
+  if (c >= nch) {
+    if (c == 0)
+      for (int i = tid; i < GH * D; i += NT) a.o[((int64_t)b * a.nq + hq0) * D + i] = 0.f;
     return;
   }
+  const int tb = t0 + c * a.chunk;
+  const int cntg = max(0, min(a.chunk, cend - tb));
+  const bool is_new = ROPE && c == nch - 1;
+  const bool split = nch > 1;
+  const int64_t slot = (int64_t)b * gridDim.y + blockIdx.y;
 
-  // ---- 5. the chunk partial for the combine kernel ----
-  // Plain stores: the combine kernel runs after this one on the same stream,
-  // so the kernel boundary orders them; no flag, counter or cleared memory
-  // is needed between the two launches.
-  float* po_s = a.part_o + (slot * a.nchunks + c) * P;
-  float* pml_s = a.part_ml + (slot * a.nchunks + c) * (GH * 2);
+  const bf16_t* __restrict__ Kb = reinterpret_cast<const bf16_t*>(a.k);
+  const bf16_t* __restrict__ Vb = reinterpret_cast<const bf16_t*>(a.v);
+  const int64_t hoff = (int64_t)h * a.head_stride;
+  const int64_t qrow0 = (int64_t)b * a.nq + hq0;
+
+  // ---- prologue ----
+  if constexpr (PAGED) {
+    int32_t* sblk_w = reinterpret_cast<int32_t*>(smem + L.blk);
+    const int p0 = tb >> a.page_shift;
+    const int p1 = max(p0, (tb + cntg - 1) >> a.page_shift);
+    for (int i = tid; i <= p1 - p0; i += NT)
+      sblk_w[i] = a.block_table[(int64_t)b * a.max_blocks + p0 + i];
+    lds_barrier();
+  }
+  const int32_t* sblk = reinterpret_cast<const int32_t*>(smem + L.blk);
+  auto row_ptr = [&](const bf16_t* base, int t) -> const bf16_t* {
+    if constexpr (PAGED) {
+      const int pg = (t >> a.page_shift) - (tb >> a.page_shift);
+      return base + (int64_t)sblk[pg] * a.block_stride + hoff +
+             (int64_t)(t & ((1 << a.page_shift) - 1)) * a.tok_stride;
+    } else {
+      return base + (int64_t)t * a.tok_stride + hoff;
+    }
+  };
+  // Rows past the chunk end load the chunk's last row (row tb of an empty
+  // chunk): every wave issues the same loads on every path.
+  const int rmax = max(cntg - 1, 0);
+  const int ntiles = (cntg + kTile - 1) / kTile;
+  u32x4 kr[2][KK], vr[2][KK];
+  auto load_tile = [&](int tile) {
 #pragma unroll
-  for (int i = 0; i < PP; ++i) {
-    if (!(lead && pv_[i])) continue;
-    po_s[pr_[i]] = po[i];
-    if (pr_[i] - g_[i] * D == 0) {
-      pml_s[2 * g_[i]] = pm[i];
-      pml_s[2 * g_[i] + 1] = pl[i];
+    for (int u = 0; u < 2; ++u) {
+      const int t = tb + min(tile * kTile + 16 * u + m16, rmax);
+      const bf16_t* pk = row_ptr(Kb, t);
+      const bf16_t* pv = row_ptr(Vb, t);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) kr[u][kk] = load16(pk + 32 * kk + 8 * g4);
+#pragma unroll
+      for (int q = 0; q < KK; ++q) vr[u][q] = load16(pv + 8 * (g4 + 4 * q));
+    }
+  };
+  constexpr int QV = GH * D / 4;
+  constexpr int QPT = (QV + NT - 1) / NT;
+  static_assert(D <= NT, "one thread per head-dim element in the prologue");
+  f32x4 qv[QPT];
+#pragma unroll
+  for (int u = 0; u < QPT; ++u)
+    qv[u] = reinterpret_cast<const f32x4*>(a.q + qrow0 * D)[min(tid + u * NT, QV - 1)];
+  float invf = 0.f, knv = 0.f, vnv = 0.f;
+  if constexpr (ROPE) {
+    invf = a.inv_freq[min(tid, D / 2 - 1)];
+    knv = a.k_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    vnv = a.v_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+  }
+  int tile = w;  // each wave's first tile; the rest are claimed
+  load_tile(tile);
+  if (tid == 0) misc[0] = NW;
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    const int i = tid + u * NT;
+    if (i < QV) reinterpret_cast<f32x4*>(qs)[i] = qv[u];
+  }
+  if constexpr (ROPE) {
+    float* csn = smem + L.cs;
+    float* sn = smem + L.sn;
+    if (tid < D / 2) {
+      const float ang = (float)pos * invf;
+      double sd, cd;
+      sincos((double)ang, &sd, &cd);
+      csn[tid] = (float)cd;
+      sn[tid] = (float)sd;
+    }
+    if (is_new && tid < D) {
+      knew[tid] = knv;
+      vnew[tid] = vnv;
+    }
+    lds_barrier();
+    for (int i = tid; i < GH * (D / 2); i += NT) {
+      const int g = i / (D / 2), j = i - g * (D / 2);
+      const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
+      qs[g * D + j] = x0 * csn[j] - x1 * sn[j];
+      qs[g * D + j + D / 2] = x0 * sn[j] + x1 * csn[j];
+    }
+    if (is_new) {
+      for (int j = tid; j < D / 2; j += NT) {
+        const float k0 = knew[j], k1 = knew[j + D / 2];
+        const float r0 = k0 * csn[j] - k1 * sn[j];
+        const float r1 = k0 * sn[j] + k1 * csn[j];
+        knew[j] = __uint_as_float((uint32_t)f32_to_bf16(r0) << 16);
+        knew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(r1) << 16);
+        vnew[j] = __uint_as_float((uint32_t)f32_to_bf16(vnew[j]) << 16);
+        vnew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(vnew[j + D / 2]) << 16);
+      }
     }
   }
-  if constexpr (ROPE) {  // the rotated q leaves through the combine kernel
-    if (c == 0 && a.q_out)
-      for (int i = tid; i < P; i += NT) a.qrot[slot * P + i] = qs[i];
+  lds_barrier();
+
+  // q^T as the B operand: lane l holds head l%16 (zero past GH), elements
+  // 32*kk + 8*(l/16) + e, in three bf16 pieces
+  bf16x8_t qh[KK], qm[KK], ql[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = m16 < GH ? qs[m16 * D + 32 * kk + 8 * g4 + e] : 0.f;
+      __bf16 hi, mid, lo;
+      split3(x, hi, mid, lo);
+      qh[kk][e] = hi;
+      qm[kk][e] = mid;
+      ql[kk][e] = lo;
+    }
+
+  // ---- stream ----
+  char* vt = reinterpret_cast<char*>(smem + L.vt + w * RS);
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  int next_fixed = w + NW;
+  auto claim = [&]() -> int {
+    if (!a.dynamic) {
+      const int v = next_fixed;
+      next_fixed += NW;
+      return v;
+    }
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&misc[0], 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+  while (tile < ntiles) {
+    // V rows into this wave's LDS region (lane: row 16u + l%16, 16-byte
+    // chunks l/16 + 4q), 32-byte segment s of row r stored at s ^ (r % NSEG)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int q = 0; q < KK; ++q) {
+        const int r = 16 * u + m16, ch = g4 + 4 * q;
+        *reinterpret_cast<u32x4*>(vt + r * RBY + 32 * ((ch >> 1) ^ (r & (NSEG - 1))) +
+                                  16 * (ch & 1)) = vr[u][q];
+      }
+    // scores of the two 16-row halves
+    f32x4 sacc[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, kr[u][kk]);
+        sacc[u] = mfma_bf16(kv, ql[kk], sacc[u]);
+        sacc[u] = mfma_bf16(kv, qm[kk], sacc[u]);
+        sacc[u] = mfma_bf16(kv, qh[kk], sacc[u]);
+      }
+    }
+    // the next tile's loads go out while this one is finished
+    const int nx = claim();
+    if (nx < ntiles) load_tile(nx);
+    // online softmax on the accumulators: lane = head l%16, rows
+    // 16u + 4*(l/16) + r
+    float sv[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = tile * kTile + 16 * u + 4 * g4 + r;
+        sv[u][r] = row < cntg ? sacc[u][r] * a.scale : -INFINITY;
+        tmax = fmaxf(tmax, sv[u][r]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mn = fmaxf(m_run, tmax);  // finite: a claimed tile has a row
+    const float alpha = softmax_exp(m_run - mn);
+    m_run = mn;
+    bf16x8_t ph, pm, pl;
+    float ps = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = softmax_exp(sv[u][r] - mn);
+        ps += p;
+        __bf16 hi, mid, lo;
+        split3(p, hi, mid, lo);
+        ph[4 * u + r] = hi;
+        pm[4 * u + r] = mid;
+        pl[4 * u + r] = lo;
+      }
+    l_run = l_run * alpha + ps;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    __builtin_amdgcn_wave_barrier();
+    // PV: V^T of the 16-row block dt by two transposed reads
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      i16x4_t t2[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = (lane >> 2) + 16 * u;
+        t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(
+                vt + r * RBY + 32 * (dt ^ (r & (NSEG - 1))) + 8 * (lane & 3)));
+      }
+      const bf16x8_t av = __builtin_bit_cast(
+          bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
+      o[dt] = mfma_bf16(av, pl, o[dt]);
+      o[dt] = mfma_bf16(av, pm, o[dt]);
+      o[dt] = mfma_bf16(av, ph, o[dt]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    tile = nx;
   }
+
+  // ---- the new token: appended by subgroup 0, folded in by wave 0 ----
+  if (is_new && sub == 0 && tid < D) {
+    const int slot_row = n - 1;
+    int64_t off;
+    if constexpr (PAGED) {
+      const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
+      off = blk * a.block_stride + hoff +
+            (int64_t)(slot_row & ((1 << a.page_shift) - 1)) * a.tok_stride;
+    } else {
+      off = (int64_t)slot_row * a.tok_stride + hoff;
+    }
+    reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
+    reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
+  }
+  if (is_new && w == 0) {
+    float part = 0.f;
+    if (m16 < GH) {
+#pragma unroll 8
+      for (int d = g4 * (D / 4); d < (g4 + 1) * (D / 4); ++d)
+        part = fmaf(qs[m16 * D + d], knew[d], part);
+    }
+    part += __shfl_xor(part, 16);
+    part += __shfl_xor(part, 32);
+    const float snew = part * a.scale;
+    const float mn = fmaxf(m_run, snew);
+    const float alpha = softmax_exp(m_run - mn);
+    const float p = softmax_exp(snew - mn);
+    m_run = mn;
+    l_run = l_run * alpha + (g4 == 0 ? p : 0.f);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[dt][r] = o[dt][r] * alpha + p * vnew[16 * dt + 4 * g4 + r];
+  }
+
+  // ---- the wave's partial into its own LDS region, then the chunk ----
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  float* wm = smem + L.wm;
+  float* wl = smem + L.wl;
+  float* red = smem + L.vt;
+  if (m16 < GH) {
+    if (g4 == 0) {
+      wm[w * GH + m16] = m_run;
+      wl[w * GH + m16] = l_run;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4*>(red + w * RS + m16 * D + 16 * dt + 4 * g4) = o[dt];
+  }
+  lds_barrier();
+  finish_chunk<D, GH, NW, NT, ROPE>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c, qrow0);
 }
 
 // Log-sum-exp combine of the chunk partials of split-K launches.  Grid
@@ -959,6 +1365,7 @@ int g_split_chunk = 0;  // tokens per chunk, 0 = automatic
 int g_wgs_per_cu = 0;   // workgroups per CU, 0 = one
 int g_variant = 0;      // mapping variant of the 32q/8kv/d128 fp32 kernels (tuning sweeps)
 int g_dynamic = 1;      // block order: 1 = claimed by waves as they free up, 0 = fixed
+int g_bf16_mfma = 1;    // bf16 KV (D = 64, 128) on the matrix-core kernel
 
 // Launch profiling (off by default): while on, every attention launch
 // outside graph capture goes through hipExtLaunchKernelGGL with a start and
@@ -1076,11 +1483,10 @@ int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
 // Chunking + workspace of one launch.  `span` bounds every sequence's row
 // range tiled by chunks (cache rows only when the kernel folds in the new
 // token); B * nkv * subgroups slots share each chunk index.
-int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, bool paged, int align,
+int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int align, int wpc,
                 void* stream) {
-  (void)paged;
   const int rows = a.nkv * nsubs * B;
-  a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, 1);
+  a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, wpc);
   a.nchunks = span > 0 ? (span + a.chunk - 1) / a.chunk : 1;
   // bound the chunk count (grid x, and the combine's per-pair loop)
   while (a.nchunks > kMaxChunks && a.chunk < kMaxChunk) {
@@ -1106,13 +1512,20 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, bool pag
   return 0;
 }
 
-template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
-int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
-  int st = plan_launch(a, D, span, GH, nsubs, B, PAGED, C::RB, stream);
-  if (st) return st;
-  const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED);
-  const size_t lds = sizeof(float) * (size_t)L.total;
+using AttnFn = void (*)(AttnArgs);
+
+// geometry of this thread's last attention launch (molot_hip_last_plan)
+thread_local int t_last_nchunks = 0;
+thread_local int t_last_chunk = 0;
+
+// Launches an attention kernel of a planned problem and, for a split
+// context, combine_kernel after it on the same stream.
+int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d, int nsubs,
+                int B, bool paged, bool rope, void* stream) {
   if (lds > 65536) return (int)hipErrorInvalidConfiguration;
+  if ((gh * d) % kCombPairs || d % kCombPairs) return MOLOT_ENOTSUP;  // combine tiling
+  t_last_nchunks = a.nchunks;
+  t_last_chunk = a.chunk;
   a.dynamic = g_dynamic;
   std::lock_guard<std::mutex> plk(g_prof_mu);
   const bool prof = prof_active(stream);
@@ -1121,13 +1534,12 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
   if (prof) {
     pr.a0 = prof_event();
     pr.a1 = prof_event();
-    hipExtLaunchKernelGGL((attn_kernel<D, GH, T, PAGED, ROPE, C>), grid, dim3(C::NT), lds,
-                          (hipStream_t)stream, pr.a0, pr.a1, 0, a);
+    hipExtLaunchKernelGGL(kern, grid, dim3(threads), lds, (hipStream_t)stream, pr.a0, pr.a1, 0,
+                          a);
   } else {
-    hipLaunchKernelGGL((attn_kernel<D, GH, T, PAGED, ROPE, C>), grid, dim3(C::NT), lds,
-                       (hipStream_t)stream, a);
+    hipLaunchKernelGGL(kern, grid, dim3(threads), lds, (hipStream_t)stream, a);
   }
-  st = (int)hipGetLastError();
+  int st = (int)hipGetLastError();
   if (st || a.nchunks == 1) {
     if (prof) g_prof.push_back(pr);
     return st;
@@ -1142,16 +1554,15 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
   cb.pos_arr = a.pos_arr;
   cb.nq = a.nq;
   cb.nkv = a.nkv;
-  cb.gh = GH;
+  cb.gh = gh;
   cb.nsub = nsubs;
-  cb.d = D;
+  cb.d = d;
   cb.nchunks = a.nchunks;
   cb.chunk = a.chunk;
   cb.window = a.window;
-  cb.rope = ROPE ? 1 : 0;
-  cb.paged = PAGED ? 1 : 0;
-  static_assert((GH * D) % kCombPairs == 0 && D % kCombPairs == 0, "combine tiling");
-  dim3 cgrid(GH * D / kCombPairs, a.nkv * nsubs * B);
+  cb.rope = rope ? 1 : 0;
+  cb.paged = paged ? 1 : 0;
+  dim3 cgrid(gh * d / kCombPairs, a.nkv * nsubs * B);
   if (prof) {
     pr.c0 = prof_event();
     pr.c1 = prof_event();
@@ -1162,6 +1573,27 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
     hipLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), 0, (hipStream_t)stream, cb);
   }
   return (int)hipGetLastError();
+}
+
+template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
+int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
+  int st = plan_launch(a, D, span, GH, nsubs, B, C::RB, 1, stream);
+  if (st) return st;
+  const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED);
+  return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, C>, C::NT, sizeof(float) * (size_t)L.total,
+                     a, GH, D, nsubs, B, PAGED, ROPE, stream);
+}
+
+// bf16 KV, D = 64 or 128: the matrix-core kernel.  Two workgroups of four
+// waves per CU; paged batches are cut finer (their sequences differ in
+// length, and more, shorter chunks even out the CUs' shares).
+template <int D, int GH, bool PAGED, bool ROPE>
+int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
+  int st = plan_launch(a, D, span, GH, nsubs, B, kTile, PAGED ? 8 : 2, stream);
+  if (st) return st;
+  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED);
+  return launch_pair(attn_mfma_kernel<D, GH, PAGED, ROPE>, kMfmaThreads,
+                     sizeof(float) * (size_t)L.total, a, GH, D, nsubs, B, PAGED, ROPE, stream);
 }
 
 template <int D, int GH, typename T, bool PAGED, bool ROPE>
@@ -1228,9 +1660,28 @@ int zero_out(float* O, int64_t count, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
+template <int D, bool PAGED, bool ROPE>
+int dispatch_mfma(int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
+  switch (gh) {
+    case 1: return launch_mfma<D, 1, PAGED, ROPE>(a, span, nsubs, B, st);
+    case 2: return launch_mfma<D, 2, PAGED, ROPE>(a, span, nsubs, B, st);
+    case 4: return launch_mfma<D, 4, PAGED, ROPE>(a, span, nsubs, B, st);
+    case 8: return launch_mfma<D, 8, PAGED, ROPE>(a, span, nsubs, B, st);
+    case 16: return launch_mfma<D, 16, PAGED, ROPE>(a, span, nsubs, B, st);
+  }
+  return MOLOT_EINVAL;
+}
+
 template <bool PAGED, bool ROPE>
 int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
   const int G = a.nq / a.nkv;
+  if (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128)) {
+    // up to 16 q heads of a group share each K/V tile on the MFMA columns
+    const int gh = G % 16 == 0 ? 16 : pick_gh(G);
+    const int nsubs = G / gh;
+    return d == 64 ? dispatch_mfma<64, PAGED, ROPE>(gh, a, span, nsubs, B, stream)
+                   : dispatch_mfma<128, PAGED, ROPE>(gh, a, span, nsubs, B, stream);
+  }
   const int gh = pick_gh(G);
   const int nsubs = G / gh;
   return dispatch_attn<PAGED, ROPE>(d, kv_dtype, gh, a, span, nsubs, B, stream);
@@ -1264,22 +1715,16 @@ void molot_rope_inv_freq(float base, int d, float* out) {
 
 void molot_hip_set_split_chunk(int tokens) { g_split_chunk = tokens > 0 ? tokens : 0; }
 
-int molot_hip_split_plan(int nkv, int n_att, int d, int kv_dtype, int* nchunks, int* chunk) {
-  if (nkv <= 0 || n_att < 0 || !nchunks || !chunk || !supported_d(d)) return MOLOT_EINVAL;
-  // the plan of the default GQA-4 kernels (32q/8kv-style groups)
-  int align = 128, wpc = 1;
-  if (d == 128 && kv_dtype == MOLOT_KV_F32) {
-    using T = Tune<128, 4, float>;
-    align = T::NW * T::RB;
-    wpc = T::NW >= 16 ? 1 : 16 / T::NW;
-  }
-  const int ch = plan_chunk(n_att > 0 ? n_att : 1, nkv, align, wpc);
-  *chunk = ch;
-  *nchunks = n_att > 0 ? (n_att + ch - 1) / ch : 0;
+int molot_hip_last_plan(int* nchunks, int* chunk) {
+  if (!nchunks || !chunk || t_last_nchunks <= 0) return MOLOT_EINVAL;
+  *nchunks = t_last_nchunks;
+  *chunk = t_last_chunk;
   return 0;
 }
 
 void molot_hip_set_block_order(int dynamic) { g_dynamic = dynamic ? 1 : 0; }
+
+void molot_hip_set_bf16_path(int mfma) { g_bf16_mfma = mfma ? 1 : 0; }
 
 int molot_hip_profile_begin(int max_launches) {
   if (max_launches <= 0) return MOLOT_EINVAL;

@@ -48,7 +48,7 @@ _SIGS = {
     "molot_hip_rope_append_paged": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P,
                                     _I, _P],
     "molot_hip_vexp": [_P, _P, _I64, _P],
-    "molot_hip_split_plan": [_I, _I, _I, _I, ctypes.POINTER(_I), ctypes.POINTER(_I)],
+    "molot_hip_last_plan": [ctypes.POINTER(_I), ctypes.POINTER(_I)],
     "molot_hip_profile_begin": [_I],
     "molot_hip_profile_end": [ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_I),
                               ctypes.POINTER(_I)],
@@ -61,6 +61,7 @@ _VOID = {
     "molot_hip_set_split_chunk": [_I],
     "molot_hip_set_tuning": [_I, _I],
     "molot_hip_set_block_order": [_I],
+    "molot_hip_set_bf16_path": [_I],
 }
 _STR = {
     "molot_hip_strerror": [_I],

@@ -98,7 +98,7 @@ def test_validation_before_launch():
     assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 2, 4, 100, 8,
                                            4, 128, 16, 0.1, 0, 0, s) == L.EINVAL
     nch, ch = ctypes.c_int(), ctypes.c_int()
-    assert lib.molot_hip_split_plan(0, 10, 128, 0, ctypes.byref(nch), ctypes.byref(ch)) == L.EINVAL
+    assert lib.molot_hip_last_plan(None, ctypes.byref(ch)) == L.EINVAL
 
 
 def test_python_layer_checks_sizes_without_gpu():

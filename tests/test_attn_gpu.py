@@ -237,6 +237,76 @@ def test_bf16_cache_shapes(gpu, nq, nkv, d, pos):
     check_decode(make_decode(nq, nkv, d, pos, seed=pos, bf16=True), label="bf16")
 
 
+@pytest.mark.parametrize("nq,nkv,d", [(32, 8, 128), (64, 8, 128), (32, 2, 128), (16, 16, 64),
+                                      (32, 2, 64), (24, 8, 128), (12, 4, 64)])
+@pytest.mark.parametrize("pos", [0, 1, 31, 32, 33, 100, 2049])
+def test_bf16_mfma_shapes_and_ragged_lengths(gpu, nq, nkv, d, pos):
+    """bf16 KV on the matrix-core kernel: groups of 4, 8, 16, 1 and 3 q heads
+    per KV head (16 share one MFMA tile; 3 run as three 1-head groups), both
+    head dims it serves, and lengths on either side of its 32-row tiles."""
+    announce(f"bf16 mfma {nq}/{nkv}/{d} pos {pos}")
+    check_decode(make_decode(nq, nkv, d, pos, seed=pos + 3 * nq + d, bf16=True),
+                 label="bf16 mfma")
+
+
+@pytest.mark.parametrize("window", [1, 31, 33, 1000])
+def test_bf16_windows(gpu, window):
+    announce(f"bf16 window {window}")
+    check_decode(make_decode(32, 8, 128, 3000, window=window, seed=40 + window, bf16=True),
+                 label="bf16 window")
+
+
+def test_bf16_mfma_matches_valu_path(gpu):
+    """The matrix-core and the vector-ALU kernel agree on one bf16 cache (both
+    fp32-accurate on those values; they differ in summation order only)."""
+    from molot_amd import lib as L
+    announce("bf16 mfma vs valu 64q/8kv/d128 n=20000")
+    p = make_decode(64, 8, 128, 20000, seed=31, sigma_kv=0.5, bf16=True)
+    Q = dev(oracle.rope_apply(p.q, p.pos, p.inv_freq))
+    K, V = dev_bf16(p.K), dev_bf16(p.V)
+    outs = []
+    try:
+        for path in (1, 0):
+            L.load().molot_hip_set_bf16_path(path)
+            O = torch.empty((64, 128), device="cuda")
+            attn.attn_decode_gqa_cache(Q, K, V, O, 64, 8, p.pos, 128, p.scale, p.pos - 1, 0)
+            outs.append(host(O))
+    finally:
+        L.load().molot_hip_set_bf16_path(1)
+    assert normwise_err(outs[0], outs[1]) < 2e-6
+
+
+def test_bf16_properties(gpu):
+    """Exact-answer cases on the matrix-core kernel (values exact in bf16):
+    constant V gives that constant; V of KV head j equal to j+1 gives
+    O[h] = h // G + 1 (the GQA mapping); a dominant key returns its V row."""
+    announce("bf16 properties 64q/8kv/d128 n=9001")
+    st = Stream(41)
+    nq, nkv, d, n = 64, 8, 128, 9001
+    Q = st.normal((nq, d))
+    K = f32_to_bf16(st.normal((n, nkv * d), 0.5))
+    O = torch.empty((nq, d), device="cuda")
+    Vc = f32_to_bf16(np.full((n, nkv * d), -1.25, np.float32))
+    attn.attn_decode_gqa_cache(dev(Q), dev_bf16(K), dev_bf16(Vc), O, nq, nkv, n, d, 0.088, n - 1,
+                               0)
+    np.testing.assert_allclose(host(O), -1.25, rtol=1e-6)
+    Vj = f32_to_bf16(np.repeat(np.arange(1, nkv + 1, dtype=np.float32), d)[None, :].repeat(n, 0))
+    attn.attn_decode_gqa_cache(dev(Q), dev_bf16(K), dev_bf16(Vj), O, nq, nkv, n, d, 0.088, n - 1,
+                               0)
+    np.testing.assert_allclose(host(O), (np.arange(nq) // 8 + 1)[:, None].repeat(d, 1),
+                               rtol=1e-6)
+    # key 4321 of every head aligned with q (score ~ 60 above the rest)
+    Kd = bf16_to_f32(K).copy()
+    for h in range(nkv):
+        Kd[4321, h * d:(h + 1) * d] = 40.0 * np.sign(Q[h * 8])
+    V = st.normal((n, nkv * d))
+    Vb = f32_to_bf16(V)
+    attn.attn_decode_gqa_cache(dev(Q), dev_bf16(f32_to_bf16(Kd)), dev_bf16(Vb), O, nq, nkv, n, d,
+                               0.088, n - 1, 0)
+    np.testing.assert_allclose(host(O)[0::8], bf16_to_f32(Vb)[4321].reshape(nkv, d), rtol=1e-5,
+                               atol=1e-6)
+
+
 def test_empty_window_gives_zero(gpu):
     st = Stream(3)
     Q = dev(st.normal((4, 128)))
@@ -299,9 +369,9 @@ def test_properties_at_16k(gpu):
 
 
 def test_fresh_stream_workspace(gpu):
-    """First launches on a brand-new stream: its workspace is created (and
-    cleared on that stream) by the first launch, then grown by a larger one;
-    both must match the oracle (the split-K bookkeeping starts from zero)."""
+    """First launches on a brand-new stream: its workspace is created by the
+    first launch, then grown by a larger one (the old buffer is retired, not
+    freed); every launch must match the oracle."""
     s = torch.cuda.Stream()
     for pos, seed in ((3000, 21), (16384, 22), (16384, 23)):
         p = make_decode(32, 8, 128, pos, seed=seed)
@@ -501,18 +571,20 @@ def test_c4_fused_step(gpu):
     assert normwise_err(O, oO) < FP32_TOL
 
 
+@pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("dynamic", [0, 1])
-def test_graph_replays_match_eager(gpu, dynamic):
+def test_graph_replays_match_eager(gpu, dynamic, bf16):
     """The fused step captured in a HIP graph: every replay (with eager work and
     synchronisations between replays) equals the eager result -- bit for bit
-    with the fixed block order, to fp32 rounding with the dynamic one.
-    Exercises the per-slot arrival counters and epochs across launches."""
+    with the fixed block order, to fp32 rounding with the dynamic one.  fp32
+    KV runs the vector-ALU kernel, bf16 the matrix-core one; both reuse the
+    stream's split-K workspace across replays."""
     from molot_amd import lib as L
     L.load().molot_hip_set_block_order(dynamic)
     try:
-        p = make_decode(32, 8, 128, 6000, seed=12)
+        p = make_decode(32, 8, 128, 6000, seed=12, bf16=bf16)
         q0 = dev(p.q)
-        K, V = dev(p.K), dev(p.V)
+        K, V = (dev_bf16(p.K), dev_bf16(p.V)) if bf16 else (dev(p.K), dev(p.V))
         kn, vn, inv = dev(p.k_new), dev(p.v_new), dev(p.inv_freq)
         O = torch.empty((32, 128), device="cuda")
         q = q0.clone()
