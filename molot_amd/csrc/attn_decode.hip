@@ -197,7 +197,7 @@ __global__ void rope_append_kernel(RopeArgs a) {
 // ---------------------------------------------------------------------------
 // Fused decode attention.
 //
-// Grid (chunks, nkv * subgroups, sequences).  Workgroup (c, h/sub, b) owns the
+// Grid (nkv * subgroups, sequences, chunks).  Workgroup (h/sub, b, c) owns the
 // context rows [tb, tb + cnt) of KV head h and the GH query heads
 // hq0 .. hq0+GH-1 of that head's group; the workgroups sharing (b, h/sub)
 // form a "slot".
@@ -453,13 +453,13 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   float* vnew = smem + L.vnew;
   int* misc = reinterpret_cast<int*>(smem + L.misc);
 
-  const int c = blockIdx.x;
+  const int c = blockIdx.z;
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
-  const int sub = blockIdx.y % nsub;
-  const int h = blockIdx.y / nsub;
+  const int sub = blockIdx.x % nsub;
+  const int h = blockIdx.x / nsub;
   const int hq0 = h * G + sub * GH;
-  const int b = blockIdx.z;
+  const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const int cntg = max(0, min(a.chunk, cend - tb));  // rows read from the cache
   const bool is_new = ROPE && c == nch - 1;          // this chunk folds in the new token
   const bool split = nch > 1;
-  const int64_t slot = (int64_t)b * gridDim.y + blockIdx.y;
+  const int64_t slot = (int64_t)b * gridDim.x + blockIdx.x;
 
   const T* __restrict__ Kb = reinterpret_cast<const T*>(a.k);
   const T* __restrict__ Vb = reinterpret_cast<const T*>(a.v);
@@ -916,13 +916,13 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   float* vnew = smem + L.vnew;
   int* misc = reinterpret_cast<int*>(smem + L.misc);
 
-  const int c = blockIdx.x;
+  const int c = blockIdx.z;
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
-  const int sub = blockIdx.y % nsub;
-  const int h = blockIdx.y / nsub;
+  const int sub = blockIdx.x % nsub;
+  const int h = blockIdx.x / nsub;
   const int hq0 = h * G + sub * GH;
-  const int b = blockIdx.z;
+  const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -951,7 +951,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   const int cntg = max(0, min(a.chunk, cend - tb));
   const bool is_new = ROPE && c == nch - 1;
   const bool split = nch > 1;
-  const int64_t slot = (int64_t)b * gridDim.y + blockIdx.y;
+  const int64_t slot = (int64_t)b * gridDim.x + blockIdx.x;
 
   const bf16_t* __restrict__ Kb = reinterpret_cast<const bf16_t*>(a.k);
   const bf16_t* __restrict__ Vb = reinterpret_cast<const bf16_t*>(a.v);
@@ -1530,7 +1530,13 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   std::lock_guard<std::mutex> plk(g_prof_mu);
   const bool prof = prof_active(stream);
   ProfRec pr{nullptr, nullptr, nullptr, nullptr, a.nchunks > 1};
-  dim3 grid(a.nchunks, a.nkv * nsubs, B);
+  // Workgroup i runs on XCD i % 8 (its L2 and its share of the CUs), and
+  // workgroups are dispatched in linear order.  With the (KV head, subgroup)
+  // index fastest, every XCD gets the same heads' share of every chunk and
+  // sequence (equal work however the chunks of a batch differ in length),
+  // and the chunk index slowest makes the XCDs stream the same rows at the
+  // same time.
+  dim3 grid(a.nkv * nsubs, B, a.nchunks);
   if (prof) {
     pr.a0 = prof_event();
     pr.a1 = prof_event();
