@@ -139,6 +139,16 @@ inline void attn_decode_gqa(const float* Q, const float* K, const float* V, floa
   v.finish(s);
 }
 
+// The layer's norms of the fresh q, k, v (forward.h:554, 562-563): the
+// weights are device tables of hd floats (L.q_norm, L.k_norm); NULL skips
+// that norm; v_norm is hp.v_norm and eps hp.eps.
+struct LayerNorms {
+  const float* q_norm = nullptr;
+  const float* k_norm = nullptr;
+  bool v_norm = false;
+  float eps = 1e-6f;
+};
+
 // Device KV cache of one layer (Runner::KVC, forward.h:48-51) with the
 // decode-attention block of forward.h:556-591 in one fused launch.
 class DeviceKV {
@@ -170,6 +180,14 @@ class DeviceKV {
   // table of hd/2 floats (the layer's L.freq).
   void decode(float* q, const float* knew, const float* vnew, float* ao, int nq, int pos,
               const float* inv_freq, float scale, int window, hipStream_t s = nullptr) {
+    decode(q, knew, vnew, ao, nq, pos, inv_freq, scale, window, LayerNorms{}, s);
+  }
+
+  // forward.h:554-591: the same with the layer's norms of q, k and v fused
+  // into the launch (before RoPE and the append, as forward.h orders them).
+  void decode(float* q, const float* knew, const float* vnew, float* ao, int nq, int pos,
+              const float* inv_freq, float scale, int window, const LayerNorms& nm,
+              hipStream_t s = nullptr) {
     if (n >= cap) throw std::runtime_error("fwd: KV cache full");  // forward.h:570
     const size_t qf = (size_t)nq * hd, kf = (size_t)nkv * hd;
     QOView view(q, ao, qf, qf, s);
@@ -184,9 +202,15 @@ class DeviceKV {
       kd = kv_stage;
       vd = kv_stage + kf;
     }
-    check(molot_hip_decode_step(const_cast<float*>(view.q), kd, vd, k, v, view.o, nq, nkv, hd, n,
-                                pos, inv_freq, scale, window, kv_dtype, s),
-          "decode_step");
+    if (nm.q_norm || nm.k_norm || nm.v_norm)
+      check(molot_hip_decode_step_norm(const_cast<float*>(view.q), kd, vd, k, v, view.o, nq, nkv,
+                                       hd, n, pos, nm.q_norm, nm.k_norm, nm.v_norm ? 1 : 0,
+                                       nm.eps, inv_freq, scale, window, kv_dtype, s),
+            "decode_step_norm");
+    else
+      check(molot_hip_decode_step(const_cast<float*>(view.q), kd, vd, k, v, view.o, nq, nkv, hd,
+                                  n, pos, inv_freq, scale, window, kv_dtype, s),
+            "decode_step");
     ++n;
     view.finish(s);
   }

@@ -113,6 +113,20 @@ int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void
                           const float* inv_freq, float scale, int window, int kv_dtype,
                           void* stream);
 
+/* molot_hip_decode_step with the layer's norms fused in, in forward.h's
+ * order (include/molot/forward.h:554-568): each q head and each new k head
+ * RMS-normed with the weights q_norm[d] / k_norm[d]
+ * (Runner::rms_per_head, forward.h:138-140 -> rmsnorm, norm.h:9-28:
+ * y = (x * 1/sqrt(mean(x^2) + eps)) * w), v RMS-normed over all its nkv*d
+ * values without weights when v_norm != 0 (rmsnorm_plain, norm.h:82-96,
+ * forward.h:563), then RoPE, append and attention.  A NULL weight pointer
+ * skips that norm; eps >= 0 (the model's hp.eps). */
+int molot_hip_decode_step_norm(float* q, const float* k_new, const float* v_new, void* K,
+                               void* V, float* O, int nq, int nkv, int d, int slot, int pos,
+                               const float* q_norm, const float* k_norm, int v_norm, float eps,
+                               const float* inv_freq, float scale, int window, int kv_dtype,
+                               void* stream);
+
 /* Batched decode over a paged cache (continuous batching; no reference
  * counterpart).  Q/O [B][nq][d] fp32; K/V pages [num_blocks][nkv][page][d];
  * sequence b attends slots [t0_b, seq_lens[b]) through
@@ -135,6 +149,16 @@ int molot_hip_decode_step_paged(float* q, const float* k_new, const float* v_new
                                 int max_blocks, int max_seq_len, int nq, int nkv, int d, int page,
                                 const float* inv_freq, float scale, int window, int kv_dtype,
                                 void* stream);
+
+/* molot_hip_decode_step_paged with the layer's norms, per sequence, as
+ * molot_hip_decode_step_norm (include/molot/forward.h:554-568). */
+int molot_hip_decode_step_paged_norm(float* q, const float* k_new, const float* v_new, void* K,
+                                     void* V, float* O, const int32_t* block_table,
+                                     const int32_t* seq_lens, const int32_t* pos, int B,
+                                     int max_blocks, int max_seq_len, int nq, int nkv, int d,
+                                     int page, const float* q_norm, const float* k_norm,
+                                     int v_norm, float eps, const float* inv_freq, float scale,
+                                     int window, int kv_dtype, void* stream);
 
 /* RoPE + append for the paged cache: q[B][nq][d] rotated in place at pos[b];
  * k_new/v_new [B][nkv][d] (k rotated) written to slot seq_lens[b]-1 of

@@ -138,9 +138,14 @@ def attn_decode_head(Q, K, V, out, n, d, scale):
     return attn_decode_head_win(Q, K, V, out, n, d, scale, n if n > 0 else 0, 0)
 
 
-def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale, window):
+def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale, window,
+                q_norm=None, k_norm=None, v_norm=False, eps=1e-6):
     """forward.h:556-591 for one layer in one fused launch: RoPE of q (in place)
-    and k_new, append of k/v at `slot`, attention over slot+1 at pos_cur=pos."""
+    and k_new, append of k/v at `slot`, attention over slot+1 at pos_cur=pos.
+
+    With the layer's norms (forward.h:554, 562-563): q and k RMS-normed per
+    head with weights q_norm / k_norm ([d] device tensors), v over all its
+    nkv*d values when v_norm, before RoPE and the append."""
     kvd = kv_dtype_of(K)
     cap = K.numel() // (nkv * d)
     if slot < 0 or slot >= cap:
@@ -152,10 +157,24 @@ def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale
     _need(V, "V", K.dtype, (slot + 1) * nkv * d)
     _need(O, "O", torch.float32, nq * d)
     _need(inv_freq, "inv_freq", torch.float32, d // 2)
-    check(_lib.load().molot_hip_decode_step(
+    if q_norm is None and k_norm is None and not v_norm:
+        check(_lib.load().molot_hip_decode_step(
+            _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), nq, nkv, d, int(slot),
+            int(pos), _ptr(inv_freq), float(scale), int(window), kvd, _stream()), "decode_step")
+        return O
+    _need_norms(q_norm, k_norm, d)
+    check(_lib.load().molot_hip_decode_step_norm(
         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), nq, nkv, d, int(slot),
-        int(pos), _ptr(inv_freq), float(scale), int(window), kvd, _stream()), "decode_step")
+        int(pos), _ptr(q_norm), _ptr(k_norm), int(bool(v_norm)), float(eps), _ptr(inv_freq),
+        float(scale), int(window), kvd, _stream()), "decode_step_norm")
     return O
+
+
+def _need_norms(q_norm, k_norm, d):
+    if q_norm is not None:
+        _need(q_norm, "q_norm", torch.float32, d)
+    if k_norm is not None:
+        _need(k_norm, "k_norm", torch.float32, d)
 
 
 def _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V):
@@ -193,10 +212,12 @@ def attn_decode_paged(Q, K, V, O, block_table, seq_lens, pos, B, max_blocks, nq,
 
 
 def decode_step_paged(q, k_new, v_new, K, V, O, block_table, seq_lens, pos, B, max_blocks, nq,
-                      nkv, d, page, inv_freq, scale, window=0):
+                      nkv, d, page, inv_freq, scale, window=0, q_norm=None, k_norm=None,
+                      v_norm=False, eps=1e-6):
     """Fused RoPE + append + attention for B sequences over a paged cache.
 
-    seq_lens[b] counts the new token, which lands in slot seq_lens[b]-1."""
+    seq_lens[b] counts the new token, which lands in slot seq_lens[b]-1.
+    Norms as decode_step, per sequence."""
     kvd = kv_dtype_of(K)
     _need(q, "q", torch.float32, B * nq * d)
     _need(O, "O", torch.float32, B * nq * d)
@@ -206,10 +227,18 @@ def decode_step_paged(q, k_new, v_new, K, V, O, block_table, seq_lens, pos, B, m
     max_len = _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V)
     if B and int(seq_lens.min()) < 1:
         raise ValueError("decode_step_paged: every sequence needs seq_lens >= 1")
-    check(_lib.load().molot_hip_decode_step_paged(
+    if q_norm is None and k_norm is None and not v_norm:
+        check(_lib.load().molot_hip_decode_step_paged(
+            _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), _ptr(block_table),
+            _ptr(seq_lens), _ptr(pos), B, max_blocks, max_len, nq, nkv, d, page, _ptr(inv_freq),
+            float(scale), int(window), kvd, _stream()), "decode_step_paged")
+        return O
+    _need_norms(q_norm, k_norm, d)
+    check(_lib.load().molot_hip_decode_step_paged_norm(
         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), _ptr(block_table),
-        _ptr(seq_lens), _ptr(pos), B, max_blocks, max_len, nq, nkv, d, page, _ptr(inv_freq),
-        float(scale), int(window), kvd, _stream()), "decode_step_paged")
+        _ptr(seq_lens), _ptr(pos), B, max_blocks, max_len, nq, nkv, d, page, _ptr(q_norm),
+        _ptr(k_norm), int(bool(v_norm)), float(eps), _ptr(inv_freq), float(scale), int(window),
+        kvd, _stream()), "decode_step_paged_norm")
     return O
 
 

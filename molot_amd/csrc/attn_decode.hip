@@ -131,43 +131,86 @@ struct RopeArgs {
   const int32_t* block_table;
   const int32_t* seq_lens;
   const int32_t* pos_arr;
+  const float* q_norm;  // [d] q RMS-norm weights (NULL: no q norm)
+  const float* k_norm;  // [d] k RMS-norm weights (NULL: no k norm)
   int64_t tok_stride, head_stride, block_stride;
   int nq, nkv, d, slot, pos, max_blocks, page, kv_dtype, append;
+  int v_norm;           // RMS-norm v over all nkv*d values, no weights
+  float eps;
 };
+
+// Sum over the workgroup (at most 16 waves); every thread gets the total.
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+  v = group_sum<64>(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int k = 0; k < (int)((blockDim.x + 63) >> 6); ++k) t += sh[k];
+  __syncthreads();
+  return t;
+}
 
 // One workgroup per (head of q or k, sequence); one thread per rotation pair.
 // Angle is the fp32 product pos*inv_freq[i] (include/molot/attn.h:22); its
 // sine and cosine are evaluated in double and rounded, i.e. a full-range,
-// correctly rounded (barring double rounding) fp32 sin/cos.
+// correctly rounded (barring double rounding) fp32 sin/cos.  With the
+// layer's norms (forward.h:554, 562-563) a head is RMS-normed before its
+// rotation: (x * 1/sqrt(mean(x^2) + eps)) * w (include/molot/norm.h:9-28),
+// and v by the RMS of all nkv*d values of the sequence's v (norm.h:82-96).
 __global__ void rope_append_kernel(RopeArgs a) {
+  __shared__ float sh[16];
   const int hh = blockIdx.x;
   const int b = blockIdx.y;
   const int half = a.d >> 1;
   const int i = threadIdx.x;
-  if (i >= half) return;
+  const bool act = i < half;  // the reductions need every thread
+  const int ic = act ? i : 0;
   int pos = a.pos;
   int slot = a.slot;
   if (a.seq_lens) {
     slot = a.seq_lens[b] - 1;
     pos = a.pos_arr ? a.pos_arr[b] : slot;
   }
-  const float ang = (float)pos * a.inv_freq[i];
+  const float ang = (float)pos * a.inv_freq[ic];
   double sd, cd;
   sincos((double)ang, &sd, &cd);
   const float c = (float)cd, s = (float)sd;
+  auto rms_inv = [&](float ss, int n) { return 1.0f / sqrtf(ss / (float)n + a.eps); };
   if (hh < a.nq) {
     if (!a.q) return;
     float* x = a.q + ((int64_t)b * a.nq + hh) * a.d;
-    const float x0 = x[i], x1 = x[i + half];
-    x[i] = x0 * c - x1 * s;
-    x[i + half] = x0 * s + x1 * c;
+    float x0 = act ? x[i] : 0.f, x1 = act ? x[i + half] : 0.f;
+    if (a.q_norm) {
+      const float inv = rms_inv(block_sum(x0 * x0 + x1 * x1, sh), a.d);
+      x0 = x0 * inv * a.q_norm[ic];
+      x1 = x1 * inv * a.q_norm[ic + half];
+    }
+    if (act) {
+      x[i] = x0 * c - x1 * s;
+      x[i + half] = x0 * s + x1 * c;
+    }
     return;
   }
   if (!a.append) return;
   const int kh = hh - a.nq;
   const float* kx = a.k_new + ((int64_t)b * a.nkv + kh) * a.d;
   const float* vx = a.v_new + ((int64_t)b * a.nkv + kh) * a.d;
-  const float k0 = kx[i], k1 = kx[i + half];
+  float k0 = act ? kx[i] : 0.f, k1 = act ? kx[i + half] : 0.f;
+  float v0 = act ? vx[i] : 0.f, v1 = act ? vx[i + half] : 0.f;
+  if (a.k_norm) {
+    const float inv = rms_inv(block_sum(k0 * k0 + k1 * k1, sh), a.d);
+    k0 = k0 * inv * a.k_norm[ic];
+    k1 = k1 * inv * a.k_norm[ic + half];
+  }
+  if (a.v_norm) {
+    const float* vall = a.v_new + (int64_t)b * a.nkv * a.d;
+    float part = 0.f;
+    for (int j = i; j < a.nkv * a.d; j += blockDim.x) part = fmaf(vall[j], vall[j], part);
+    const float inv = rms_inv(block_sum(part, sh), a.nkv * a.d);
+    v0 *= inv;
+    v1 *= inv;
+  }
+  if (!act) return;
   const float r0 = k0 * c - k1 * s;
   const float r1 = k0 * s + k1 * c;
   int64_t off;
@@ -182,15 +225,15 @@ __global__ void rope_append_kernel(RopeArgs a) {
     float* vd = (float*)a.V + off;
     kd[i] = r0;
     kd[i + half] = r1;
-    vd[i] = vx[i];
-    vd[i + half] = vx[i + half];
+    vd[i] = v0;
+    vd[i + half] = v1;
   } else {
     uint16_t* kd = (uint16_t*)a.K + off;
     uint16_t* vd = (uint16_t*)a.V + off;
     kd[i] = f32_to_bf16(r0);
     kd[i + half] = f32_to_bf16(r1);
-    vd[i] = f32_to_bf16(vx[i]);
-    vd[i + half] = f32_to_bf16(vx[i + half]);
+    vd[i] = f32_to_bf16(v0);
+    vd[i + half] = f32_to_bf16(v1);
   }
 }
 
@@ -244,6 +287,11 @@ struct AttnArgs {
   int nq, nkv, n, t0, pos, chunk, nchunks, max_blocks, page_shift, window;
   int dynamic;           // 1: waves claim blocks from a workgroup counter; 0: fixed order
   float scale;
+  // the layer's norms of the fresh vectors (ROPE only; NULL / 0: none)
+  const float* q_norm;   // [D] weights of the per-head q RMS norm
+  const float* k_norm;   // [D] weights of the per-head k RMS norm
+  int v_norm;            // RMS-norm v over all nkv*D values, no weights
+  float eps;
 };
 
 // Work mapping of one kernel instance.
@@ -361,6 +409,41 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// RMS norms of the step's fresh vectors (forward.h:554, 562-563), in LDS
+// before RoPE: the GH q rows with weights q_norm and, in the workgroup that
+// appends the new token, its k with k_norm and its v scaled by the RMS of
+// all nkv*D values of v_new (rmsnorm / rmsnorm_plain, include/molot/
+// norm.h:9-28, :82-96: y = (x * 1/sqrt(mean(x^2) + eps)) * w).  One wave per
+// vector; the caller's barriers order the LDS accesses.
+template <int D, int GH, int NW>
+__device__ __forceinline__ void step_norms(const AttnArgs& a, float* qs, float* knew, float* vnew,
+                                           bool is_new, int b, int w, int lane) {
+  static_assert(NW >= 2, "k and v norms on two waves");
+  if (a.q_norm) {
+    for (int g = w; g < GH; g += NW) {
+      float ss = 0.f;
+      for (int j = lane; j < D; j += 64) ss = fmaf(qs[g * D + j], qs[g * D + j], ss);
+      const float inv = 1.0f / sqrtf(group_sum<64>(ss) / (float)D + a.eps);
+      for (int j = lane; j < D; j += 64) qs[g * D + j] = qs[g * D + j] * inv * a.q_norm[j];
+    }
+  }
+  if (!is_new) return;
+  if (a.k_norm && w == NW - 1) {
+    float ss = 0.f;
+    for (int j = lane; j < D; j += 64) ss = fmaf(knew[j], knew[j], ss);
+    const float inv = 1.0f / sqrtf(group_sum<64>(ss) / (float)D + a.eps);
+    for (int j = lane; j < D; j += 64) knew[j] = knew[j] * inv * a.k_norm[j];
+  }
+  if (a.v_norm && w == NW - 2) {
+    const float* vx = a.v_new + (int64_t)b * a.nkv * D;
+    const int nv = a.nkv * D;
+    float ss = 0.f;
+    for (int j = lane; j < nv; j += 64) ss = fmaf(vx[j], vx[j], ss);
+    const float inv = 1.0f / sqrtf(group_sum<64>(ss) / (float)nv + a.eps);
+    for (int j = lane; j < D; j += 64) vnew[j] *= inv;
+  }
 }
 
 // The workgroup's chunk partial from its waves' partials in LDS: running
@@ -584,6 +667,10 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       vnew[tid] = vnv;
     }
     lds_barrier();
+    if (a.q_norm || (is_new && (a.k_norm || a.v_norm))) {  // uniform over the workgroup
+      step_norms<D, GH, NW>(a, qs, knew, vnew, is_new, b, w, lane);
+      lds_barrier();
+    }
     for (int i = tid; i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
       const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
@@ -1030,6 +1117,10 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       vnew[tid] = vnv;
     }
     lds_barrier();
+    if (a.q_norm || (is_new && (a.k_norm || a.v_norm))) {  // uniform over the workgroup
+      step_norms<D, GH, NW>(a, qs, knew, vnew, is_new, b, w, lane);
+      lds_barrier();
+    }
     for (int i = tid; i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
       const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
@@ -1693,6 +1784,16 @@ int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
   return dispatch_attn<PAGED, ROPE>(d, kv_dtype, gh, a, span, nsubs, B, stream);
 }
 
+// The layer's norms of the fresh q, k and v (forward.h:554, 562-563).
+struct Norms {
+  const float* q = nullptr;  // per-head q weights [d], NULL: none
+  const float* k = nullptr;  // per-head k weights [d], NULL: none
+  int v = 0;                 // v over all nkv*d values, no weights
+  float eps = 0.f;
+};
+
+bool norms_ok(const Norms& nm) { return nm.eps >= 0.f && nm.eps < INFINITY; }
+
 }  // namespace
 
 // ===========================================================================
@@ -1802,10 +1903,11 @@ int molot_hip_rope_apply(float* x, int nheads, int d, int pos, const float* inv_
   return (int)hipGetLastError();
 }
 
-int molot_hip_rope_append(float* q, const float* k_new, const float* v_new, void* K, void* V,
-                          int nq, int nkv, int d, int slot, int pos, const float* inv_freq,
-                          int kv_dtype, void* stream) {
+static int rope_append_impl(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                            int nq, int nkv, int d, int slot, int pos, const float* inv_freq,
+                            int kv_dtype, const Norms& nm, void* stream) {
   if (nq < 0 || nkv <= 0 || d <= 0 || (d & 1) || d > 2048 || slot < 0) return MOLOT_EINVAL;
+  if (!norms_ok(nm)) return MOLOT_EINVAL;
   if ((nq > 0 && !q) || !k_new || !v_new || !K || !V || !inv_freq) return MOLOT_EINVAL;
   if (kv_dtype != MOLOT_KV_F32 && kv_dtype != MOLOT_KV_BF16) return MOLOT_EINVAL;
   RopeArgs a{};
@@ -1824,9 +1926,20 @@ int molot_hip_rope_append(float* q, const float* k_new, const float* v_new, void
   a.pos = pos;
   a.kv_dtype = kv_dtype;
   a.append = 1;
+  a.q_norm = nm.q;
+  a.k_norm = nm.k;
+  a.v_norm = nm.v;
+  a.eps = nm.eps;
   hipLaunchKernelGGL(rope_append_kernel, dim3(nq + nkv, 1), dim3(((d / 2) + 63) / 64 * 64), 0,
                      (hipStream_t)stream, a);
   return (int)hipGetLastError();
+}
+
+int molot_hip_rope_append(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                          int nq, int nkv, int d, int slot, int pos, const float* inv_freq,
+                          int kv_dtype, void* stream) {
+  return rope_append_impl(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq, kv_dtype,
+                          Norms{}, stream);
 }
 
 int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, float* O, int nq,
@@ -1889,12 +2002,13 @@ int molot_hip_attn_decode_head_win(const float* Q, const void* K, const void* V,
                                        pos_cur, window, kv_dtype, stream);
 }
 
-int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
-                          float* O, int nq, int nkv, int d, int slot, int pos,
-                          const float* inv_freq, float scale, int window, int kv_dtype,
-                          void* stream) {
+static int decode_step_impl(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                            float* O, int nq, int nkv, int d, int slot, int pos,
+                            const float* inv_freq, float scale, int window, int kv_dtype,
+                            const Norms& nm, void* stream) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
+  if (!norms_ok(nm)) return MOLOT_EINVAL;
   if (!q || !k_new || !v_new || !K || !V || !O || !inv_freq || slot < 0) return MOLOT_EINVAL;
   if (!aligned16(K) || !aligned16(V) || !aligned16(q) || !aligned16(O)) return MOLOT_EINVAL;
   const int n = slot + 1;
@@ -1902,12 +2016,16 @@ int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void
   if (t0 > n) t0 = n;
   if (t0 > n - 1) {
     // the new token itself is outside the window: append, rotate q, o = 0
-    st = molot_hip_rope_append(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq, kv_dtype,
-                               stream);
+    st = rope_append_impl(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq, kv_dtype, nm,
+                          stream);
     if (st) return st;
     return zero_out(O, (int64_t)nq * d, (hipStream_t)stream);
   }
   AttnArgs a{};
+  a.q_norm = nm.q;
+  a.k_norm = nm.k;
+  a.v_norm = nm.v;
+  a.eps = nm.eps;
   a.q = q;
   a.q_out = q;
   a.k_new = k_new;
@@ -1926,6 +2044,28 @@ int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void
   a.window = window;
   a.scale = scale;
   return run_attn<false, true>(a, d, kv_dtype, n - 1 - t0, 1, stream);  // cache rows
+}
+
+int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                          float* O, int nq, int nkv, int d, int slot, int pos,
+                          const float* inv_freq, float scale, int window, int kv_dtype,
+                          void* stream) {
+  return decode_step_impl(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale,
+                          window, kv_dtype, Norms{}, stream);
+}
+
+int molot_hip_decode_step_norm(float* q, const float* k_new, const float* v_new, void* K,
+                               void* V, float* O, int nq, int nkv, int d, int slot, int pos,
+                               const float* q_norm, const float* k_norm, int v_norm, float eps,
+                               const float* inv_freq, float scale, int window, int kv_dtype,
+                               void* stream) {
+  Norms nm;
+  nm.q = q_norm;
+  nm.k = k_norm;
+  nm.v = v_norm ? 1 : 0;
+  nm.eps = eps;
+  return decode_step_impl(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale,
+                          window, kv_dtype, nm, stream);
 }
 
 static int paged_args(AttnArgs& a, const float* Q, void* K, void* V, float* O,
@@ -1980,12 +2120,19 @@ int molot_hip_attn_decode_paged(const float* Q, const void* K, const void* V, fl
   return run_attn<true, false>(a, d, kv_dtype, span, B, stream);
 }
 
-int molot_hip_decode_step_paged(float* q, const float* k_new, const float* v_new, void* K,
-                                void* V, float* O, const int32_t* block_table,
-                                const int32_t* seq_lens, const int32_t* pos, int B,
-                                int max_blocks, int max_seq_len, int nq, int nkv, int d, int page,
-                                const float* inv_freq, float scale, int window, int kv_dtype,
-                                void* stream) {
+static int rope_append_paged_impl(float* q, const float* k_new, const float* v_new, void* K,
+                                  void* V, const int32_t* block_table, const int32_t* seq_lens,
+                                  const int32_t* pos, int B, int max_blocks, int nq, int nkv,
+                                  int d, int page, const float* inv_freq, int kv_dtype,
+                                  const Norms& nm, void* stream);
+
+static int decode_step_paged_impl(float* q, const float* k_new, const float* v_new, void* K,
+                                  void* V, float* O, const int32_t* block_table,
+                                  const int32_t* seq_lens, const int32_t* pos, int B,
+                                  int max_blocks, int max_seq_len, int nq, int nkv, int d,
+                                  int page, const float* inv_freq, float scale, int window,
+                                  int kv_dtype, const Norms& nm, void* stream) {
+  if (!norms_ok(nm)) return MOLOT_EINVAL;
   AttnArgs a{};
   int span = 0;
   int st = paged_args(a, q, K, V, O, block_table, seq_lens, pos, B, max_blocks, max_seq_len, nq,
@@ -1997,11 +2144,15 @@ int molot_hip_decode_step_paged(float* q, const float* k_new, const float* v_new
     // a position behind the cache end can leave the new slot outside the
     // window; the split path only folds in rows it attends, so take the
     // unfused kernels there (append, then attention over the cache)
-    st = molot_hip_rope_append_paged(q, k_new, v_new, K, V, block_table, seq_lens, pos, B,
-                                     max_blocks, nq, nkv, d, page, inv_freq, kv_dtype, stream);
+    st = rope_append_paged_impl(q, k_new, v_new, K, V, block_table, seq_lens, pos, B,
+                                max_blocks, nq, nkv, d, page, inv_freq, kv_dtype, nm, stream);
     if (st) return st;
     return run_attn<true, false>(a, d, kv_dtype, span, B, stream);
   }
+  a.q_norm = nm.q;
+  a.k_norm = nm.k;
+  a.v_norm = nm.v;
+  a.eps = nm.eps;
   a.q_out = q;
   a.k_new = k_new;
   a.v_new = v_new;
@@ -2009,10 +2160,48 @@ int molot_hip_decode_step_paged(float* q, const float* k_new, const float* v_new
   return run_attn<true, true>(a, d, kv_dtype, span, B, stream);  // span >= cache rows
 }
 
+int molot_hip_decode_step_paged(float* q, const float* k_new, const float* v_new, void* K,
+                                void* V, float* O, const int32_t* block_table,
+                                const int32_t* seq_lens, const int32_t* pos, int B,
+                                int max_blocks, int max_seq_len, int nq, int nkv, int d, int page,
+                                const float* inv_freq, float scale, int window, int kv_dtype,
+                                void* stream) {
+  return decode_step_paged_impl(q, k_new, v_new, K, V, O, block_table, seq_lens, pos, B,
+                                max_blocks, max_seq_len, nq, nkv, d, page, inv_freq, scale,
+                                window, kv_dtype, Norms{}, stream);
+}
+
+int molot_hip_decode_step_paged_norm(float* q, const float* k_new, const float* v_new, void* K,
+                                     void* V, float* O, const int32_t* block_table,
+                                     const int32_t* seq_lens, const int32_t* pos, int B,
+                                     int max_blocks, int max_seq_len, int nq, int nkv, int d,
+                                     int page, const float* q_norm, const float* k_norm,
+                                     int v_norm, float eps, const float* inv_freq, float scale,
+                                     int window, int kv_dtype, void* stream) {
+  Norms nm;
+  nm.q = q_norm;
+  nm.k = k_norm;
+  nm.v = v_norm ? 1 : 0;
+  nm.eps = eps;
+  return decode_step_paged_impl(q, k_new, v_new, K, V, O, block_table, seq_lens, pos, B,
+                                max_blocks, max_seq_len, nq, nkv, d, page, inv_freq, scale,
+                                window, kv_dtype, nm, stream);
+}
+
 int molot_hip_rope_append_paged(float* q, const float* k_new, const float* v_new, void* K,
                                 void* V, const int32_t* block_table, const int32_t* seq_lens,
                                 const int32_t* pos, int B, int max_blocks, int nq, int nkv, int d,
                                 int page, const float* inv_freq, int kv_dtype, void* stream) {
+  return rope_append_paged_impl(q, k_new, v_new, K, V, block_table, seq_lens, pos, B, max_blocks,
+                                nq, nkv, d, page, inv_freq, kv_dtype, Norms{}, stream);
+}
+
+static int rope_append_paged_impl(float* q, const float* k_new, const float* v_new, void* K,
+                                  void* V, const int32_t* block_table, const int32_t* seq_lens,
+                                  const int32_t* pos, int B, int max_blocks, int nq, int nkv,
+                                  int d, int page, const float* inv_freq, int kv_dtype,
+                                  const Norms& nm, void* stream) {
+  if (!norms_ok(nm)) return MOLOT_EINVAL;
   if (nq < 0 || nkv <= 0 || d <= 0 || (d & 1) || d > 2048 || B < 0 || max_blocks <= 0 ||
       page <= 0)
     return MOLOT_EINVAL;
@@ -2040,6 +2229,10 @@ int molot_hip_rope_append_paged(float* q, const float* k_new, const float* v_new
   a.page = page;
   a.kv_dtype = kv_dtype;
   a.append = 1;
+  a.q_norm = nm.q;
+  a.k_norm = nm.k;
+  a.v_norm = nm.v;
+  a.eps = nm.eps;
   hipLaunchKernelGGL(rope_append_kernel, dim3(nq + nkv, B), dim3(((d / 2) + 63) / 64 * 64), 0,
                      (hipStream_t)stream, a);
   return (int)hipGetLastError();

@@ -41,10 +41,14 @@ _SIGS = {
     "molot_hip_attn_decode_strided": [_P, _P, _P, _P, _I, _I, _I, _I, _I64, _I64, _F, _I, _I,
                                       _I, _P],
     "molot_hip_decode_step": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _I, _P],
+    "molot_hip_decode_step_norm": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P,
+                                   _F, _I, _I, _P],
     "molot_hip_attn_decode_paged": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,
                                     _I, _I, _P],
     "molot_hip_decode_step_paged": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                                     _I, _P, _F, _I, _I, _P],
+    "molot_hip_decode_step_paged_norm": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
+                                         _I, _I, _P, _P, _I, _F, _P, _F, _I, _I, _P],
     "molot_hip_rope_append_paged": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P,
                                     _I, _P],
     "molot_hip_vexp": [_P, _P, _I64, _P],

@@ -64,6 +64,9 @@ def lib() -> ctypes.CDLL:
                                        _I]),
             "orc_attn_decode_f64": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _D, _I, _I, _I, _I64,
                                            _I64, _I64, _P, _I, _I]),
+            "orc_rmsnorm": (None, [_P, _P, _P, _I, _F]),
+            "orc_decode_step_norm": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P,
+                                            _I, _F, _P, _F, _I, _I, _I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -110,6 +113,10 @@ def ref() -> ctypes.CDLL:
             "ref_attn_decode_gqa_win": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P]),
             "ref_decode_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _F, _I,
                                      _P]),
+            "ref_rmsnorm": (None, [_P, _P, _P, _I, _F]),
+            "ref_rmsnorm_plain": (None, [_P, _P, _I, _F]),
+            "ref_decode_step_norm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P,
+                                          _I, _F, _P, _F, _I, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(R, name)
@@ -247,4 +254,33 @@ def decode_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, slot, pos, inv_freq, scale,
     lib().orc_decode_step(_p(q), _p(k), _p(v), _p(Kc), _p(Vc), _p(O), nq, nkv, d, int(slot),
                           int(pos), _p(_f32(inv_freq)), float(scale), int(window), _kv_code(Kc),
                           int(nthreads))
+    return q, k, O
+
+
+def rmsnorm(x: np.ndarray, w=None, eps: float = 1e-6) -> np.ndarray:
+    """norm.h:9-28 over the last axis (w None: rmsnorm_plain, norm.h:82-96)."""
+    x = _f32(x)
+    n = x.shape[-1]
+    y = np.empty_like(x)
+    wp = None if w is None else _f32(w)
+    xs, ys = x.reshape(-1, n), y.reshape(-1, n)
+    for i in range(xs.shape[0]):
+        lib().orc_rmsnorm(_p(xs[i]), _p(wp), _p(ys[i]), n, float(eps))
+    return y
+
+
+def decode_step_norm(q, k_new, v_new, Kc, Vc, nq, nkv, d, slot, pos, q_norm, k_norm, v_norm,
+                     eps, inv_freq, scale, window, nthreads=0):
+    """forward.h:554-591 with the layer's norms: returns (q_rot, k_rot, O);
+    Kc/Vc are updated in place."""
+    q = _f32(q).copy()
+    k = _f32(k_new).copy()
+    v = _f32(v_new)
+    O = np.empty((nq, d), dtype=np.float32)
+    qn = None if q_norm is None else _f32(q_norm)
+    kn = None if k_norm is None else _f32(k_norm)
+    lib().orc_decode_step_norm(_p(q), _p(k), _p(v), _p(Kc), _p(Vc), _p(O), nq, nkv, d, int(slot),
+                               int(pos), _p(qn), _p(kn), int(v_norm), float(eps),
+                               _p(_f32(inv_freq)), float(scale), int(window), _kv_code(Kc),
+                               int(nthreads))
     return q, k, O

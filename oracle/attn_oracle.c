@@ -20,6 +20,12 @@
  *                              algorithm covers attn.h:57-120 and :178-187.
  *       orc_decode_step     <- include/molot/forward.h:556-591 (rope q, rope k,
  *                              append, attention)
+ *       orc_rmsnorm         <- include/molot/norm.h:9-28 (weights) and
+ *                              :82-96 (w == NULL: rmsnorm_plain)
+ *       orc_decode_step_norm <- include/molot/forward.h:554-591 with the
+ *                              layer's norms: q and k per head
+ *                              (rms_per_head, :138-140), v over all its
+ *                              nkv*d values (:563), before RoPE
  *     Threading follows ThreadPool::parallel_for (thread_pool.h:54-89): a
  *     static contiguous split of the query heads, via OpenMP schedule(static).
  *
@@ -135,6 +141,15 @@ float orc_dot(const float* a, const float* b, int n) {
   float tail = 0;
   for (; i < n; ++i) tail += a[i] * b[i];
   return orc_hsum16(acc) + tail;
+}
+
+/* rmsnorm (norm.h:9-28): the sum of squares with the 16-lane FMA
+ * accumulation of the reference's AVX512 loop (as orc_dot), mean = sum/n,
+ * inv = 1/sqrt(mean + eps) in fp32, y = (x*inv)*w.  w == NULL is
+ * rmsnorm_plain (norm.h:82-96): y = x*inv.  y may alias x. */
+void orc_rmsnorm(const float* x, const float* w, float* y, int n, float eps) {
+  const float inv = 1.0f / sqrtf(orc_dot(x, x, n) / (float)n + eps);
+  for (int i = 0; i < n; ++i) y[i] = w ? (x[i] * inv) * w[i] : x[i] * inv;
 }
 
 /* ------------------------------------------------------------------ */
@@ -287,6 +302,29 @@ void orc_decode_step(float* q, float* k_new, const float* v_new, void* Kc, void*
   }
   orc_attn_decode(q, Kc, Vc, O, nq, nkv, slot + 1, d, scale, pos, window, kv_dtype, (int64_t)S,
                   d, 0, NULL, 0, nthreads);
+}
+
+/* forward.h:554-591 with the layer's norms: q heads RMS-normed with q_norm
+ * (forward.h:554), k heads with k_norm (:562), v by the RMS of all its
+ * nkv*d values when v_norm (:563), then orc_decode_step.  NULL weights skip
+ * that norm.  v_new is left unchanged (the normed copy is appended). */
+void orc_decode_step_norm(float* q, float* k_new, const float* v_new, void* Kc, void* Vc,
+                          float* O, int nq, int nkv, int d, int slot, int pos,
+                          const float* q_norm, const float* k_norm, int v_norm, float eps,
+                          const float* inv_freq, float scale, int window, int kv_dtype,
+                          int nthreads) {
+  const size_t S = (size_t)nkv * d;
+  float* v = (float*)malloc(S * sizeof(float));
+  memcpy(v, v_new, S * sizeof(float));
+  if (q_norm)
+    for (int h = 0; h < nq; ++h) orc_rmsnorm(q + (size_t)h * d, q_norm, q + (size_t)h * d, d, eps);
+  if (k_norm)
+    for (int h = 0; h < nkv; ++h)
+      orc_rmsnorm(k_new + (size_t)h * d, k_norm, k_new + (size_t)h * d, d, eps);
+  if (v_norm) orc_rmsnorm(v, NULL, v, (int)S, eps);
+  orc_decode_step(q, k_new, v, Kc, Vc, O, nq, nkv, d, slot, pos, inv_freq, scale, window,
+                  kv_dtype, nthreads);
+  free(v);
 }
 
 /* ------------------------------------------------------------------ */

@@ -18,6 +18,7 @@ void orc_rope_apply(float* x, int d, int pos, const float* inv_freq);
 void orc_rope_apply_heads(float* x, int nheads, int d, int pos, const float* inv_freq);
 void orc_vexp16(const float* in, float* out);
 float orc_dot(const float* a, const float* b, int n);
+void orc_rmsnorm(const float* x, const float* w, float* y, int n, float eps);
 void orc_attn_decode(const float* Q, const void* K, const void* V, float* O, int nq, int nkv,
                      int n, int d, float scale, int pos_cur, int window, int kv_dtype,
                      int64_t tok_stride, int64_t head_stride, int64_t block_stride,
@@ -28,6 +29,11 @@ void orc_attn_decode_gqa_cache(const float* Q, const float* K, const float* V, f
 void orc_decode_step(float* q, float* k_new, const float* v_new, void* Kc, void* Vc, float* O,
                      int nq, int nkv, int d, int slot, int pos, const float* inv_freq,
                      float scale, int window, int kv_dtype, int nthreads);
+void orc_decode_step_norm(float* q, float* k_new, const float* v_new, void* Kc, void* Vc,
+                          float* O, int nq, int nkv, int d, int slot, int pos,
+                          const float* q_norm, const float* k_norm, int v_norm, float eps,
+                          const float* inv_freq, float scale, int window, int kv_dtype,
+                          int nthreads);
 void orc_attn_decode_f64(const float* Q, const void* K, const void* V, double* O, int nq,
                          int nkv, int n, int d, double scale, int pos_cur, int window,
                          int kv_dtype, int64_t tok_stride, int64_t head_stride,

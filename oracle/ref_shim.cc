@@ -89,4 +89,35 @@ int ref_decode_step(float* q, float* k, const float* v, float* Kc, float* Vc, fl
   return 0;
 }
 
+void ref_rmsnorm(const float* x, const float* w, float* y, int n, float eps) {
+  molot::rmsnorm(x, w, y, n, eps);
+}
+
+void ref_rmsnorm_plain(const float* x, float* y, int n, float eps) {
+  molot::rmsnorm_plain(x, y, n, eps);
+}
+
+// forward.h:554-591 with the layer's norms, in forward.h's order: q heads
+// RMS-normed with q_norm (Runner::rms_per_head, forward.h:138-140) and
+// rotated; k heads normed with k_norm, v normed over all its nkv*d values
+// when v_norm (forward.h:562-563), k rotated; append; attention.
+int ref_decode_step_norm(float* q, float* k, float* v, float* Kc, float* Vc, float* O, int nq,
+                         int nkv, int d, int slot, int cap, int pos, const float* q_norm,
+                         const float* k_norm, int v_norm, float eps, const float* inv_freq,
+                         float scale, int window, void* pool) {
+  for (int hh = 0; hh < nq; ++hh)
+    molot::rmsnorm(q + (size_t)hh * d, q_norm, q + (size_t)hh * d, d, eps);
+  for (int hh = 0; hh < nq; ++hh) molot::rope_apply(q + (size_t)hh * d, d, pos, inv_freq);
+  for (int hh = 0; hh < nkv; ++hh)
+    molot::rmsnorm(k + (size_t)hh * d, k_norm, k + (size_t)hh * d, d, eps);
+  if (v_norm) molot::rmsnorm_plain(v, v, nkv * d, eps);
+  for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(k + (size_t)hh * d, d, pos, inv_freq);
+  if (slot >= cap) return -1;
+  std::memcpy(Kc + (size_t)slot * nkv * d, k, (size_t)nkv * d * 4);
+  std::memcpy(Vc + (size_t)slot * nkv * d, v, (size_t)nkv * d * 4);
+  molot::attn_decode_gqa_cache(q, Kc, Vc, O, nq, nkv, slot + 1, d, scale, pos, window,
+                               *static_cast<molot::ThreadPool*>(pool));
+  return 0;
+}
+
 }  // extern "C"

@@ -97,6 +97,46 @@ int main() {
     for (size_t i = 0; i < Kd.size(); ++i) kerr = std::fmax(kerr, std::fabs(Kd[i] - Kref[i]));
     CHECK(kerr < 1e-5, "appended K differs by %g", kerr);
 
+    // ---- 1b. with the layer's norms (forward.h:554-568), gemma-style scale 1 ----
+    {
+      molot::amd::DeviceKV kvn(cap, nkv, d);
+      std::vector<float> Kn((size_t)cap * nkv * d, 0.f), Vn((size_t)cap * nkv * d, 0.f);
+      std::vector<float> qw(d), kw(d);
+      rng.normal(qw);
+      rng.normal(kw);
+      for (int i = 0; i < d; ++i) {
+        qw[i] = 1.0f + 0.2f * qw[i];
+        kw[i] = 1.0f + 0.2f * kw[i];
+      }
+      float* w_d = nullptr;
+      molot::amd::check_hip(hipMalloc(&w_d, 2 * d * 4), "hipMalloc");
+      molot::amd::check_hip(hipMemcpy(w_d, qw.data(), d * 4, hipMemcpyHostToDevice), "");
+      molot::amd::check_hip(hipMemcpy(w_d + d, kw.data(), d * 4, hipMemcpyHostToDevice), "");
+      molot::amd::LayerNorms nm;
+      nm.q_norm = w_d;
+      nm.k_norm = w_d + d;
+      nm.v_norm = true;
+      nm.eps = 1e-6f;
+      double wn = 0;
+      for (int pos = 0; pos < 40; ++pos) {
+        std::vector<float> q(nq * d), k(nkv * d), v(nkv * d), ao(nq * d), ao_ref(nq * d);
+        rng.normal(q);
+        rng.normal(k);
+        rng.normal(v);
+        std::vector<float> q_ref = q, k_ref = k;
+        kvn.decode(q.data(), k.data(), v.data(), ao.data(), nq, pos, inv_d, 1.0f, 0, nm);
+        orc_decode_step_norm(q_ref.data(), k_ref.data(), v.data(), Kn.data(), Vn.data(),
+                             ao_ref.data(), nq, nkv, d, pos, pos, qw.data(), kw.data(), 1, 1e-6f,
+                             inv.data(), 1.0f, 0, ORC_KV_F32, 1);
+        wn = std::fmax(wn, normwise(ao, ao_ref));
+        CHECK(normwise(q, q_ref) < 2e-6, "normed rotated q differs at pos %d", pos);
+      }
+      CHECK(wn < 1e-5, "DeviceKV decode with norms normwise err %g", wn);
+      std::printf("[%s] DeviceKV 40 decode steps with q/k/v norms: max normwise err %.2e\n",
+                  wn < 1e-5 ? "ok" : "FAIL", wn);
+      (void)hipFree(w_d);
+    }
+
     // ---- 2. attn.h drop-in on the same cache, host q/o, sliding window ----
     std::vector<float> q(nq * d), o(nq * d), o_ref(nq * d);
     rng.normal(q);

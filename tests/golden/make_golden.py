@@ -7,7 +7,8 @@ through oracle.ref().  Each fixture stores its inputs and the reference's
 outputs as plain arrays (np.savez, no pickles), so tests need neither the
 reference nor the generator to reproduce them.
 
-Usage:  make -C oracle && python tests/golden/make_golden.py
+Usage:  make -C oracle && python tests/golden/make_golden.py [fixture ...]
+        (no names: write every fixture)
 """
 from __future__ import annotations
 
@@ -61,6 +62,54 @@ def gen_decode_step(name, nq, nkv, d, n0, base, window, scale, seed, pool):
     _save(name, q=q, k_new=k, v_new=v, K=Kc[:n0], V=Vc[:n0], inv_freq=inv, q_rot=q_rot,
           k_rot=k_rot, O=O, nq=nq, nkv=nkv, d=d, pos=n0, base=base, window=window, scale=scale,
           seed=seed)
+
+
+def gen_decode_step_norm(name, nq, nkv, d, n0, base, window, scale, eps, v_norm, seed, pool):
+    """forward.h:554-591 with the layer's norms, through the reference:
+    rmsnorm of q and k heads (weights), rmsnorm_plain of v, rope, append,
+    attention.  Weights are drawn around 1 like trained norm gains."""
+    R = oracle.ref()
+    st = Stream(seed)
+    q = st.normal((nq, d), 3.0)
+    k = st.normal((nkv, d), 3.0)
+    v = st.normal((nkv, d), 3.0)
+    q_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    k_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    cap = n0 + 1
+    Kc = np.zeros((cap, nkv * d), np.float32)
+    Vc = np.zeros((cap, nkv * d), np.float32)
+    Kc[:n0] = st.normal((n0, nkv * d))
+    Vc[:n0] = st.normal((n0, nkv * d))
+    inv = ref_inv_freq(base, d)
+    q_rot, k_rot, v_out = q.copy(), k.copy(), v.copy()
+    Kout, Vout = Kc.copy(), Vc.copy()
+    O = np.empty((nq, d), np.float32)
+    rc = R.ref_decode_step_norm(P(q_rot), P(k_rot), P(v_out), P(Kout), P(Vout), P(O), nq, nkv, d,
+                                n0, cap, n0, P(q_norm), P(k_norm), int(v_norm), float(eps), P(inv),
+                                float(scale), int(window), pool.h)
+    assert rc == 0
+    _save(name, q=q, k_new=k, v_new=v, K=Kc[:n0], V=Vc[:n0], inv_freq=inv, q_norm=q_norm,
+          k_norm=k_norm, q_rot=q_rot, k_rot=k_rot, v_normed=v_out, O=O, nq=nq, nkv=nkv, d=d,
+          pos=n0, base=base, window=window, scale=scale, eps=eps, v_norm=v_norm, seed=seed)
+
+
+def gen_rmsnorm(name, sizes, seed):
+    """rmsnorm / rmsnorm_plain (norm.h:9-28, :82-96) on rows of several
+    lengths (vector body and scalar tail) and magnitudes where eps matters."""
+    R = oracle.ref()
+    st = Stream(seed)
+    out = {}
+    for n in sizes:
+        for tag, sig in (("unit", 1.0), ("tiny", 1e-3)):
+            x = st.normal((n,), sig)
+            w = (1.0 + st.normal((n,), 0.3)).astype(np.float32)
+            y = np.empty(n, np.float32)
+            yp = np.empty(n, np.float32)
+            R.ref_rmsnorm(P(x), P(w), P(y), n, 1e-6)
+            R.ref_rmsnorm_plain(P(x), P(yp), n, 1e-6)
+            out[f"x_{tag}_{n}"], out[f"w_{tag}_{n}"] = x, w
+            out[f"y_{tag}_{n}"], out[f"yplain_{tag}_{n}"] = y, yp
+    _save(name, sizes=np.array(sizes), eps=1e-6, seed=seed, **out)
 
 
 def gen_head(name, n, d, sigma, seed):
@@ -149,23 +198,48 @@ def gen_vexp(name, seed):
 def main() -> None:
     if not oracle.ref_available():
         sys.exit("reference library not available: build it with `make -C oracle` here")
+    only = set(sys.argv[1:])  # fixture names to (re)write; all when empty
+
+    def want(name):
+        return not only or name in only
+
     with oracle.RefPool(4) as pool:
-        gen_decode_step("decode_step_g4_d128", nq=8, nkv=2, d=128, n0=100, base=500000.0,
-                        window=0, scale=1.0 / math.sqrt(128), seed=11, pool=pool)
-        gen_decode_step("decode_step_win_d256", nq=4, nkv=2, d=256, n0=60, base=10000.0,
-                        window=16, scale=1.0 / math.sqrt(256), seed=12, pool=pool)
-        gen_decode_step("decode_step_g8_d64_scale1", nq=8, nkv=1, d=64, n0=150, base=500000.0,
-                        window=0, scale=1.0, seed=13, pool=pool)
-        gen_head("head_bench_check", n=160, d=128, sigma=0.2, seed=1234)
-        gen_gqa_headmajor("gqa_headmajor_d64", nq=4, nkv=1, n=97, d=64, pos_cur=97, window=0,
-                          seed=14, pool=pool)
-        gen_gqa_headmajor("gqa_win_headmajor_d64", nq=4, nkv=2, n=90, d=64, pos_cur=89,
-                          window=20, seed=15, pool=pool)
-        gen_bf16_cache("bf16_cache_g8_d128", nq=8, nkv=1, n=70, d=128, sigma=1.0, seed=16,
-                       pool=pool)
-    gen_rope("rope_d128_theta5e5", 128, 500000.0, [0, 1, 7, 4096, 16384, 131072], seed=17)
-    gen_rope("rope_d256_theta1e4", 256, 10000.0, [0, 3, 1023, 32768], seed=18)
-    gen_vexp("vexp_points", seed=19)
+        if want("decode_step_g4_d128"):
+            gen_decode_step("decode_step_g4_d128", nq=8, nkv=2, d=128, n0=100, base=500000.0,
+                            window=0, scale=1.0 / math.sqrt(128), seed=11, pool=pool)
+        if want("decode_step_win_d256"):
+            gen_decode_step("decode_step_win_d256", nq=4, nkv=2, d=256, n0=60, base=10000.0,
+                            window=16, scale=1.0 / math.sqrt(256), seed=12, pool=pool)
+        if want("decode_step_g8_d64_scale1"):
+            gen_decode_step("decode_step_g8_d64_scale1", nq=8, nkv=1, d=64, n0=150,
+                            base=500000.0, window=0, scale=1.0, seed=13, pool=pool)
+        if want("decode_step_norm_g4_d128"):
+            gen_decode_step_norm("decode_step_norm_g4_d128", nq=8, nkv=2, d=128, n0=90,
+                                 base=500000.0, window=0, scale=1.0, eps=1e-6, v_norm=1,
+                                 seed=20, pool=pool)
+        if want("decode_step_norm_win_d256"):
+            gen_decode_step_norm("decode_step_norm_win_d256", nq=4, nkv=2, d=256, n0=60,
+                                 base=10000.0, window=16, scale=1.0, eps=1e-6, v_norm=0,
+                                 seed=21, pool=pool)
+        if want("head_bench_check"):
+            gen_head("head_bench_check", n=160, d=128, sigma=0.2, seed=1234)
+        if want("gqa_headmajor_d64"):
+            gen_gqa_headmajor("gqa_headmajor_d64", nq=4, nkv=1, n=97, d=64, pos_cur=97,
+                              window=0, seed=14, pool=pool)
+        if want("gqa_win_headmajor_d64"):
+            gen_gqa_headmajor("gqa_win_headmajor_d64", nq=4, nkv=2, n=90, d=64, pos_cur=89,
+                              window=20, seed=15, pool=pool)
+        if want("bf16_cache_g8_d128"):
+            gen_bf16_cache("bf16_cache_g8_d128", nq=8, nkv=1, n=70, d=128, sigma=1.0, seed=16,
+                           pool=pool)
+    if want("rope_d128_theta5e5"):
+        gen_rope("rope_d128_theta5e5", 128, 500000.0, [0, 1, 7, 4096, 16384, 131072], seed=17)
+    if want("rope_d256_theta1e4"):
+        gen_rope("rope_d256_theta1e4", 256, 10000.0, [0, 3, 1023, 32768], seed=18)
+    if want("vexp_points"):
+        gen_vexp("vexp_points", seed=19)
+    if want("rmsnorm_cases"):
+        gen_rmsnorm("rmsnorm_cases", [7, 16, 100, 128, 256, 1024], seed=22)
 
 
 if __name__ == "__main__":

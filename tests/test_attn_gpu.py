@@ -307,6 +307,108 @@ def test_bf16_properties(gpu):
                                atol=1e-6)
 
 
+# ---------------------------------------------------------------------------
+# the layer's norms fused into the step (forward.h:554, 562-563)
+
+def _norm_weights(d, seed):
+    st = Stream(seed)
+    return ((1 + st.normal((d,), 0.2)).astype(np.float32),
+            (1 + st.normal((d,), 0.2)).astype(np.float32))
+
+
+@pytest.mark.parametrize("name", ["decode_step_norm_g4_d128", "decode_step_norm_win_d256"])
+def test_golden_decode_step_norm(gpu, name):
+    """Against the compiled reference's forward.h sequence with norms."""
+    g = golden(name)
+    nq, nkv, d, pos = int(g["nq"]), int(g["nkv"]), int(g["d"]), int(g["pos"])
+    K = np.zeros((pos + 1, nkv * d), np.float32)
+    V = np.zeros_like(K)
+    K[:pos], V[:pos] = g["K"], g["V"]
+    q, Kd, Vd = dev(g["q"]), dev(K), dev(V)
+    O = torch.empty((nq, d), device="cuda")
+    attn.decode_step(q, dev(g["k_new"]), dev(g["v_new"]), Kd, Vd, O, nq, nkv, d, pos, pos,
+                     dev(g["inv_freq"]), float(g["scale"]), int(g["window"]),
+                     q_norm=dev(g["q_norm"]), k_norm=dev(g["k_norm"]), v_norm=bool(g["v_norm"]),
+                     eps=float(g["eps"]))
+    np.testing.assert_allclose(host(q), g["q_rot"], rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(host(Kd)[pos], g["k_rot"].reshape(-1), rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(host(Vd)[pos], g["v_normed"].reshape(-1), rtol=1e-6, atol=1e-7)
+    assert normwise_err(host(O), g["O"]) < FP32_TOL
+
+
+def _check_step_norm(p, qn, kn, v_norm, label):
+    q = dev(p.q)
+    K = dev_bf16(p.K) if p.kv_dtype else dev(p.K)
+    V = dev_bf16(p.V) if p.kv_dtype else dev(p.V)
+    O = torch.empty((p.nq, p.d), device="cuda")
+    attn.decode_step(q, dev(p.k_new), dev(p.v_new), K, V, O, p.nq, p.nkv, p.d, p.pos, p.pos,
+                     dev(p.inv_freq), p.scale, p.window, q_norm=None if qn is None else dev(qn),
+                     k_norm=None if kn is None else dev(kn), v_norm=v_norm, eps=1e-6)
+    Kc, Vc = p.K.copy(), p.V.copy()
+    oq, ok, oO = oracle.decode_step_norm(p.q, p.k_new, p.v_new, Kc, Vc, p.nq, p.nkv, p.d, p.pos,
+                                         p.pos, qn, kn, v_norm, 1e-6, p.inv_freq, p.scale,
+                                         p.window)
+    np.testing.assert_allclose(host(q), oq, rtol=2e-6, atol=4e-6)
+    if p.kv_dtype:
+        Vh = host(V.view(torch.int16)).view(np.uint16)
+        kd = np.abs(bf16_to_f32(host(K.view(torch.int16)).view(np.uint16)[p.pos]) -
+                    bf16_to_f32(Kc[p.pos]))
+        assert np.max(kd) <= 8e-3 * max(1.0, float(np.max(np.abs(bf16_to_f32(Kc[p.pos])))))
+        vd = np.abs(bf16_to_f32(Vh[p.pos]) - bf16_to_f32(Vc[p.pos]))
+        assert np.max(vd) <= 8e-3 * max(1.0, float(np.max(np.abs(bf16_to_f32(Vc[p.pos])))))
+        tol = BF16_TOL
+    else:
+        np.testing.assert_allclose(host(K)[p.pos], Kc[p.pos], rtol=2e-6, atol=4e-6)
+        np.testing.assert_allclose(host(V)[p.pos], Vc[p.pos], rtol=1e-6, atol=1e-7)
+        tol = FP32_TOL
+    err = normwise_err(host(O), oO)
+    print(f"{label} normwise err vs oracle {err:.3e}", flush=True)
+    assert err < tol
+
+
+def test_step_norms_c3_gemma_shape(gpu):
+    """Gemma-style layer at the c3 shape: q/k norm weights, v norm, scale 1."""
+    announce("norms c3 8q/4kv/d256 pos 32768 window 1024 scale 1")
+    p = make_decode(8, 4, 256, 32768, base=10000.0, window=1024, scale=1.0, seed=51)
+    qn, kn = _norm_weights(256, 52)
+    _check_step_norm(p, qn, kn, True, "norms c3")
+
+
+@pytest.mark.parametrize("which", ["q", "k", "v", "qkv"])
+def test_step_norms_each_alone(gpu, which):
+    announce(f"norms {which} 32q/8kv/d128 pos 3000")
+    p = make_decode(32, 8, 128, 3000, seed=53)
+    qn, kn = _norm_weights(128, 54)
+    _check_step_norm(p, qn if "q" in which else None, kn if "k" in which else None,
+                     "v" in which, f"norms {which}")
+
+
+def test_step_norms_bf16_matrix_core(gpu):
+    announce("norms bf16 64q/8kv/d128 pos 20000")
+    p = make_decode(64, 8, 128, 20000, seed=55, sigma_kv=0.5, bf16=True)
+    qn, kn = _norm_weights(128, 56)
+    _check_step_norm(p, qn, kn, True, "norms bf16")
+
+
+def test_step_norms_new_token_outside_window(gpu):
+    """slot 10 at pos 100 with window 5: nothing attended (O = 0), the normed
+    rotated k and the normed v still land in the slot (unfused kernel)."""
+    p = make_decode(8, 2, 64, 10, seed=57)
+    qn, kn = _norm_weights(64, 58)
+    q = dev(p.q)
+    K, V = dev(p.K), dev(p.V)
+    O = torch.full((8, 64), 3.0, device="cuda")
+    attn.decode_step(q, dev(p.k_new), dev(p.v_new), K, V, O, 8, 2, 64, 10, 100, dev(p.inv_freq),
+                     p.scale, 5, q_norm=dev(qn), k_norm=dev(kn), v_norm=True, eps=1e-6)
+    Kc, Vc = p.K.copy(), p.V.copy()
+    oq, ok, _ = oracle.decode_step_norm(p.q, p.k_new, p.v_new, Kc, Vc, 8, 2, 64, 10, 100, qn, kn,
+                                        1, 1e-6, p.inv_freq, p.scale, 5)
+    assert np.all(host(O) == 0)
+    np.testing.assert_allclose(host(q), oq, rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(host(K)[10], Kc[10], rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(host(V)[10], Vc[10], rtol=1e-6, atol=1e-7)
+
+
 def test_empty_window_gives_zero(gpu):
     st = Stream(3)
     Q = dev(st.normal((4, 128)))
@@ -569,6 +671,49 @@ def test_c4_fused_step(gpu):
     oq, oK, oV, oO = oracle_paged(P, inv, s)
     np.testing.assert_array_equal(Vh, oV)
     assert normwise_err(O, oO) < FP32_TOL
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("explicit_pos", [False, True])
+def test_paged_step_norms(gpu, bf16, explicit_pos):
+    """Paged batch with the layer's norms, per sequence; explicit positions
+    take the unfused RoPE/append kernel, which applies the same norms."""
+    announce(f"paged norms bf16={bf16} explicit_pos={explicit_pos}")
+    P = make_paged(13, 32, 8, 128, 0, 1500, seed=61 + bf16, bf16=bf16)
+    inv = oracle.rope_inv_freq(500000.0, 128)
+    qn, kn = _norm_weights(128, 62)
+    pos = (P["n"] - 1 + 7).astype(np.int32) if explicit_pos else None
+    bf = P["Kp"].dtype == np.uint16
+    K = dev_bf16(P["Kp"]) if bf else dev(P["Kp"])
+    V = dev_bf16(P["Vp"]) if bf else dev(P["Vp"])
+    q = dev(P["q"])
+    O = torch.empty((P["B"], 32, 128), device="cuda")
+    attn.decode_step_paged(q, dev(P["k_new"]), dev(P["v_new"]), K, V, O,
+                           dev(P["bt"].reshape(-1)), dev(P["n"]),
+                           None if pos is None else dev(pos), P["B"], P["max_blocks"], 32, 8, 128,
+                           16, dev(inv), 0.088, 0, q_norm=dev(qn), k_norm=dev(kn), v_norm=True,
+                           eps=1e-6)
+    Pn = dict(P)
+    Pn["q"] = oracle.rmsnorm(P["q"], qn, 1e-6)
+    Pn["k_new"] = oracle.rmsnorm(P["k_new"], kn, 1e-6)
+    Pn["v_new"] = oracle.rmsnorm(P["v_new"].reshape(P["B"], -1), None, 1e-6).reshape(
+        P["v_new"].shape)
+    oq, oK, oV, oO = oracle_paged(Pn, inv, 0.088, 0, pos)
+    np.testing.assert_allclose(host(q), oq, rtol=2e-6, atol=4e-6)
+    err = normwise_err(host(O), oO)
+    print(f"paged norms normwise err {err:.3e}", flush=True)
+    if bf:  # the normed v may differ by an fp32 ulp before its bf16 rounding
+        Vh = host(V.view(torch.int16)).view(np.uint16)
+        for b in range(P["B"]):
+            slot = int(P["n"][b]) - 1
+            blk = P["bt"][b, slot // 16]
+            ref = bf16_to_f32(oV[blk, :, slot % 16])
+            assert np.max(np.abs(bf16_to_f32(Vh[blk, :, slot % 16]) - ref)) <= \
+                8e-3 * max(1.0, float(np.max(np.abs(ref))))
+        assert err < BF16_TOL
+    else:
+        np.testing.assert_allclose(host(V), oV, rtol=1e-6, atol=1e-7)
+        assert err < FP32_TOL
 
 
 @pytest.mark.parametrize("bf16", [False, True])

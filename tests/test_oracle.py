@@ -214,6 +214,81 @@ def test_decode_step_golden(name):
     assert normwise_err(O, g["O"]) < 2e-6
 
 
+# ---------------------------------------------------------------------------
+# rmsnorm (norm.h:9-28), rmsnorm_plain (norm.h:82-96) and the step with the
+# layer's norms (forward.h:554-563)
+
+def _rms_f64(x, w, eps):
+    x64 = x.astype(np.float64)
+    y = x64 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + eps)
+    return y if w is None else y * w.astype(np.float64)
+
+
+def test_rmsnorm_golden_and_closed_form():
+    """Against the compiled reference's outputs and the float64 formula, on
+    row lengths with and without a scalar tail; the "tiny" rows have
+    mean(x^2) ~ eps, so a dropped or misplaced eps fails."""
+    g = golden("rmsnorm_cases")
+    eps = float(g["eps"])
+    for n in g["sizes"]:
+        for tag in ("unit", "tiny"):
+            x, w = g[f"x_{tag}_{n}"], g[f"w_{tag}_{n}"]
+            y, yp = oracle.rmsnorm(x, w, eps), oracle.rmsnorm(x, None, eps)
+            np.testing.assert_allclose(y, g[f"y_{tag}_{n}"], rtol=5e-7, atol=0)
+            np.testing.assert_allclose(yp, g[f"yplain_{tag}_{n}"], rtol=5e-7, atol=0)
+            np.testing.assert_allclose(y, _rms_f64(x, w, eps), rtol=1e-6)
+            np.testing.assert_allclose(yp, _rms_f64(x, None, eps), rtol=1e-6)
+
+
+def test_rmsnorm_invariants():
+    st = Stream(32)
+    x = st.normal((6, 128))
+    w = (1 + st.normal((128,), 0.3)).astype(np.float32)
+    # with eps = 0, scaling by 4 is exact through every step: same bits
+    np.testing.assert_array_equal(oracle.rmsnorm(4 * x, w, 0.0), oracle.rmsnorm(x, w, 0.0))
+    # plain: unit RMS; weighted: the plain result times w, elementwise
+    yp = oracle.rmsnorm(x, None, 0.0)
+    np.testing.assert_allclose(np.sqrt(np.mean(yp.astype(np.float64) ** 2, axis=1)), 1.0,
+                               rtol=1e-6)
+    np.testing.assert_array_equal(oracle.rmsnorm(x, w, 1e-6), oracle.rmsnorm(x, None, 1e-6) * w)
+
+
+def _step_norm_from_golden(g):
+    nq, nkv, d, pos = int(g["nq"]), int(g["nkv"]), int(g["d"]), int(g["pos"])
+    Kc = np.zeros((pos + 1, nkv * d), np.float32)
+    Vc = np.zeros_like(Kc)
+    Kc[:pos] = g["K"]
+    Vc[:pos] = g["V"]
+    q_rot, k_rot, O = oracle.decode_step_norm(g["q"], g["k_new"], g["v_new"], Kc, Vc, nq, nkv, d,
+                                              pos, pos, g["q_norm"], g["k_norm"],
+                                              int(g["v_norm"]), float(g["eps"]), g["inv_freq"],
+                                              float(g["scale"]), int(g["window"]))
+    return q_rot, k_rot, O, Kc, Vc
+
+
+@pytest.mark.parametrize("name", ["decode_step_norm_g4_d128", "decode_step_norm_win_d256"])
+def test_decode_step_norm_golden(name):
+    g = golden(name)
+    pos = int(g["pos"])
+    q_rot, k_rot, O, Kc, Vc = _step_norm_from_golden(g)
+    np.testing.assert_allclose(q_rot, g["q_rot"], rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(k_rot, g["k_rot"], rtol=2e-6, atol=2e-6)
+    np.testing.assert_array_equal(Kc[pos], k_rot.reshape(-1))
+    np.testing.assert_allclose(Vc[pos], g["v_normed"].reshape(-1), rtol=5e-7, atol=0)
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+def test_v_norm_is_over_all_kv_heads():
+    """forward.h:563 normalises v over all nkv*d values at once; a per-head
+    normalisation (a plausible misreading) misses the reference's cache row."""
+    g = golden("decode_step_norm_g4_d128")
+    nkv, d, eps = int(g["nkv"]), int(g["d"]), float(g["eps"])
+    joint = oracle.rmsnorm(g["v_new"].reshape(-1), None, eps)
+    per_head = oracle.rmsnorm(g["v_new"].reshape(nkv, d), None, eps).reshape(-1)
+    np.testing.assert_allclose(joint, g["v_normed"].reshape(-1), rtol=5e-7, atol=0)
+    assert np.max(np.abs(per_head - g["v_normed"].reshape(-1))) > 1e-3
+
+
 def test_head_golden():
     g = golden("head_bench_check")
     n, d = int(g["n"]), int(g["d"])
@@ -416,6 +491,36 @@ def test_restatement_vs_reference(nq, nkv, d, n, window, pos_cur):
         oracle.ref().ref_attn_decode_gqa_cache(oracle._p(Q), oracle._p(K), oracle._p(V),
                                                oracle._p(R), nq, nkv, n, d, s, pos_cur, window,
                                                pool.h)
+    assert normwise_err(O, R) < 2e-6
+
+
+@needs_ref
+def test_decode_step_norm_vs_reference():
+    """The restated step with norms against the compiled forward.h sequence
+    at the headline head shape (q/k norm weights, joint v norm, window)."""
+    st = Stream(33)
+    nq, nkv, d, pos, window = 32, 8, 128, 1500, 700
+    q, k, v = st.normal((nq, d), 2.0), st.normal((nkv, d), 2.0), st.normal((nkv, d), 2.0)
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    kn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    K = np.zeros((pos + 1, nkv * d), np.float32)
+    V = np.zeros_like(K)
+    K[:pos], V[:pos] = kv_token_major(st, pos, nkv, d)
+    inv = oracle.rope_inv_freq(500000.0, d)
+    Ko, Vo = K.copy(), V.copy()
+    q_rot, k_rot, O = oracle.decode_step_norm(q, k, v, Ko, Vo, nq, nkv, d, pos, pos, qn, kn, 1,
+                                              1e-6, inv, 1.0, window)
+    qr, kr, vr = q.copy(), k.copy(), v.copy()
+    Kr, Vr = K.copy(), V.copy()
+    R = np.empty((nq, d), np.float32)
+    P = oracle._p
+    with oracle.RefPool(4) as pool:
+        rc = oracle.ref().ref_decode_step_norm(P(qr), P(kr), P(vr), P(Kr), P(Vr), P(R), nq, nkv, d,
+                                               pos, pos + 1, pos, P(qn), P(kn), 1, 1e-6, P(inv),
+                                               1.0, window, pool.h)
+    assert rc == 0
+    np.testing.assert_allclose(q_rot, qr, rtol=2e-6, atol=2e-6)
+    np.testing.assert_allclose(Vo[pos], Vr[pos], rtol=5e-7, atol=0)
     assert normwise_err(O, R) < 2e-6
 
 
