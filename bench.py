@@ -85,6 +85,8 @@ def parse():
     ap.add_argument("--split-chunk", type=int, default=0, help="tokens per chunk (0 = auto)")
     ap.add_argument("--wgs-per-cu", type=int, default=0, help="workgroups per CU (0 = auto)")
     ap.add_argument("--variant", type=int, default=0, help="kernel mapping variant (0 = default)")
+    ap.add_argument("--norms", action="store_true",
+                    help="the step with the layer's q/k/v RMS norms fused in (forward.h:554-563)")
     ap.add_argument("--block-order", type=int, default=1,
                     help="1 = waves claim K/V blocks dynamically (default), 0 = fixed order")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
@@ -165,18 +167,24 @@ def contiguous_workload(args, cfg, lib, L, torch, np):
     v_new = torch.from_numpy(v_h).cuda()
     inv = attn.rope_inv_freq(theta, d).cuda()
     O = torch.empty((nq, d), dtype=torch.float32, device="cuda")
+    wts = torch.from_numpy((1 + st.normal((2, d), 0.2)).astype(np.float32)).cuda()
     torch.cuda.synchronize()
     del K_h, V_h
 
     P = ctypes.c_void_p
     qp, kp, vp, ip, op = (P(t.data_ptr()) for t in (q, k_new, v_new, inv, O))
+    qnp, knp = P(wts[0].data_ptr()), P(wts[1].data_ptr())
     Kp = [P(t.data_ptr()) for t in Ks]
     Vp = [P(t.data_ptr()) for t in Vs]
 
     def step(i, stream):
         l = i % layers
-        rc = lib.molot_hip_decode_step(qp, kp, vp, Kp[l], Vp[l], op, nq, nkv, d, pos, pos, ip,
-                                       scale, window, kvd, stream)
+        if args.norms:
+            rc = lib.molot_hip_decode_step_norm(qp, kp, vp, Kp[l], Vp[l], op, nq, nkv, d, pos, pos,
+                                                qnp, knp, 1, 1e-6, ip, scale, window, kvd, stream)
+        else:
+            rc = lib.molot_hip_decode_step(qp, kp, vp, Kp[l], Vp[l], op, nq, nkv, d, pos, pos, ip,
+                                           scale, window, kvd, stream)
         if rc:
             raise L.MolotHipError(rc, "decode_step")
 
@@ -196,7 +204,7 @@ def contiguous_workload(args, cfg, lib, L, torch, np):
         cache_desc=f"cache={cache_bytes / 2**20:.0f} MiB/layer dtype={dt}", paged=False,
         head_traffic=2 * nq * n_att * d * s_kv, cpu=cpu,
         config={"nq": nq, "nkv": nkv, "head_dim": d, "pos": pos, "n": n, "window": window,
-                "rope_theta": theta, "batch": 1},
+                "rope_theta": theta, "batch": 1, "qkv_norms": bool(args.norms)},
         keep=(Ks, Vs, q, k_new, v_new, inv, O))
 
 
@@ -255,20 +263,28 @@ def paged_workload(args, cfg, lib, L, torch, np):
     sl_d = torch.from_numpy(n.astype(np.int32)).cuda()
     inv = attn.rope_inv_freq(theta, d).cuda()
     O = torch.empty((B, nq, d), dtype=torch.float32, device="cuda")
+    wts = torch.from_numpy((1 + st.normal((2, d), 0.2)).astype(np.float32)).cuda()
     torch.cuda.synchronize()
     max_len = int(n.max())
 
     P = ctypes.c_void_p
     qp, kp, vp, ip, op, btp, slp = (P(t.data_ptr())
                                     for t in (q, k_new, v_new, inv, O, bt_d, sl_d))
+    qnp, knp = P(wts[0].data_ptr()), P(wts[1].data_ptr())
     Kp = [P(t.data_ptr()) for t in Ks]
     Vp = [P(t.data_ptr()) for t in Vs]
 
     def step(i, stream):
         l = i % layers
-        rc = lib.molot_hip_decode_step_paged(qp, kp, vp, Kp[l], Vp[l], op, btp, slp, None, B,
-                                             max_blocks, max_len, nq, nkv, d, page, ip, scale,
-                                             window, kvd, stream)
+        if args.norms:
+            rc = lib.molot_hip_decode_step_paged_norm(qp, kp, vp, Kp[l], Vp[l], op, btp, slp, None,
+                                                      B, max_blocks, max_len, nq, nkv, d, page,
+                                                      qnp, knp, 1, 1e-6, ip, scale, window, kvd,
+                                                      stream)
+        else:
+            rc = lib.molot_hip_decode_step_paged(qp, kp, vp, Kp[l], Vp[l], op, btp, slp, None, B,
+                                                 max_blocks, max_len, nq, nkv, d, page, ip, scale,
+                                                 window, kvd, stream)
         if rc:
             raise L.MolotHipError(rc, "decode_step_paged")
 
@@ -291,7 +307,7 @@ def paged_workload(args, cfg, lib, L, torch, np):
         paged=True, head_traffic=2 * nq * int(n.sum()) * d * s_kv, cpu=cpu,
         config={"nq": nq, "nkv": nkv, "head_dim": d, "batch": B, "page": page,
                 "ctx_min": int(Lc.min()), "ctx_max": int(Lc.max()), "tokens": int(n.sum()),
-                "window": window, "rope_theta": theta},
+                "window": window, "rope_theta": theta, "qkv_norms": bool(args.norms)},
         keep=(Ks, Vs, q, k_new, v_new, bt_d, sl_d, inv, O))
 
 

@@ -168,6 +168,27 @@ int molot_hip_rope_append_paged(float* q, const float* k_new, const float* v_new
                                 const int32_t* pos, int B, int max_blocks, int nq, int nkv, int d,
                                 int page, const float* inv_freq, int kv_dtype, void* stream);
 
+/* Causal prefill attention, counterpart of attn_prefill_gqa
+ * (include/molot/gemm.h:409-446, called at forward.h:394-399): Qm and Om
+ * [M][nq][d] fp32; K/V the token-major cache [N][nkv*d] holding the M new
+ * tokens; query m sits at position pos0 + m and attends slots
+ * [t0, min(pos0 + m + 1, N)), t0 = max(0, pos - window + 1) for window > 0.
+ * A query with no slot gets O = 0.  scale as given. */
+int molot_hip_attn_prefill_gqa(const float* Qm, const void* K, const void* V, float* Om, int nq,
+                               int nkv, int M, int N, int d, float scale, int pos0, int window,
+                               int kv_dtype, void* stream);
+
+/* One layer's prefill of M prompt tokens, forward.h:367-399: per token the
+ * layer's norms (as molot_hip_decode_step_norm; NULL weights / v_norm = 0
+ * skip them) and RoPE of q (in place, [M][nq][d]) and k_new ([M][nkv][d]),
+ * append of k/v at slots slot0 .. slot0+M-1 (positions pos0 ..), then
+ * causal prefill attention over N = slot0 + M into O [M][nq][d]. */
+int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                           float* O, int nq, int nkv, int d, int M, int slot0, int pos0,
+                           const float* q_norm, const float* k_norm, int v_norm, float eps,
+                           const float* inv_freq, float scale, int window, int kv_dtype,
+                           void* stream);
+
 /* Softmax exponential used by the attention kernels, applied elementwise
  * (x, y device [n]).  Counterpart of exp_avx512_ps, include/molot/norm.h:35-47,
  * exposed so its accuracy can be checked against the reference's

@@ -24,7 +24,7 @@ __all__ = [
     "attn_decode_gqa", "attn_decode_gqa_win", "attn_decode_head", "attn_decode_head_win",
     "attn_decode_strided", "decode_step", "attn_decode_paged", "decode_step_paged",
     "rope_append_paged", "vexp",
-    "last_plan", "set_split_chunk", "KVCache", "kv_dtype_of",
+    "last_plan", "set_split_chunk", "attn_prefill_gqa", "prefill_step", "KVCache", "kv_dtype_of",
 ]
 
 
@@ -239,6 +239,43 @@ def decode_step_paged(q, k_new, v_new, K, V, O, block_table, seq_lens, pos, B, m
         _ptr(seq_lens), _ptr(pos), B, max_blocks, max_len, nq, nkv, d, page, _ptr(q_norm),
         _ptr(k_norm), int(bool(v_norm)), float(eps), _ptr(inv_freq), float(scale), int(window),
         kvd, _stream()), "decode_step_paged_norm")
+    return O
+
+
+def attn_prefill_gqa(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window=0):
+    """gemm.h:409-446: causal prefill attention of M queries [M][nq][d]
+    (positions pos0..) over the token-major cache [N][nkv*d]."""
+    kvd = kv_dtype_of(K)
+    _need(Qm, "Qm", torch.float32, M * nq * d)
+    _need(Om, "Om", torch.float32, M * nq * d)
+    _need(K, "K", _KV_DTYPES, N * nkv * d)
+    _need(V, "V", K.dtype, N * nkv * d)
+    check(_lib.load().molot_hip_attn_prefill_gqa(
+        _ptr(Qm), _ptr(K), _ptr(V), _ptr(Om), nq, nkv, int(M), int(N), d, float(scale),
+        int(pos0), int(window), kvd, _stream()), "attn_prefill_gqa")
+    return Om
+
+
+def prefill_step(q, k_new, v_new, K, V, O, nq, nkv, d, M, slot0, pos0, inv_freq, scale,
+                 window=0, q_norm=None, k_norm=None, v_norm=False, eps=1e-6):
+    """forward.h:367-399 for one layer: norms (optional) and RoPE of the M
+    prompt tokens' q (in place) and k, append at slots slot0.., then causal
+    prefill attention over slot0 + M."""
+    kvd = kv_dtype_of(K)
+    cap = K.numel() // (nkv * d)
+    if slot0 + M > cap:
+        raise RuntimeError("fwd: KV cache full")  # forward.h:380
+    _need(q, "q", torch.float32, M * nq * d)
+    _need(k_new, "k_new", torch.float32, M * nkv * d)
+    _need(v_new, "v_new", torch.float32, M * nkv * d)
+    _need(O, "O", torch.float32, M * nq * d)
+    _need(V, "V", K.dtype, cap * nkv * d)
+    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need_norms(q_norm, k_norm, d)
+    check(_lib.load().molot_hip_prefill_step(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), nq, nkv, d, int(M),
+        int(slot0), int(pos0), _ptr(q_norm), _ptr(k_norm), int(bool(v_norm)), float(eps),
+        _ptr(inv_freq), float(scale), int(window), kvd, _stream()), "prefill_step")
     return O
 
 

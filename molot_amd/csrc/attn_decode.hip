@@ -137,6 +137,7 @@ struct RopeArgs {
   int nq, nkv, d, slot, pos, max_blocks, page, kv_dtype, append;
   int v_norm;           // RMS-norm v over all nkv*d values, no weights
   float eps;
+  int tokens;           // grid row b = token b of a prefill: slot + b at pos + b
 };
 
 // Sum over the workgroup (at most 16 waves); every thread gets the total.
@@ -170,6 +171,9 @@ __global__ void rope_append_kernel(RopeArgs a) {
   if (a.seq_lens) {
     slot = a.seq_lens[b] - 1;
     pos = a.pos_arr ? a.pos_arr[b] : slot;
+  } else if (a.tokens) {
+    slot += b;
+    pos += b;
   }
   const float ang = (float)pos * a.inv_freq[ic];
   double sd, cd;
@@ -1310,6 +1314,201 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   finish_chunk<D, GH, NW, NT, ROPE>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c, qrow0);
 }
 
+// ---------------------------------------------------------------------------
+// Causal prefill attention (include/molot/gemm.h:409-446) on the matrix cores.
+//
+// The query rows of one KV head are r = m*G + g: token m (position pos0 + m)
+// and q head h*G + g of the group.  A workgroup of 4 waves owns 64
+// consecutive rows, wave w the 16 rows w*16.. on the 16 columns of
+// v_mfma_f32_16x16x4f32 (fp32 operands: exact products).  It streams the keys
+// its rows attend, KT per tile, through LDS -- K row-major [KT][D+4], V
+// transposed [D][KT+4] (the padding spreads rows over the banks) -- with the
+// next tile's global loads in flight while the current one is used:
+//   S^T (KT keys x 16 rows) = K . Q^T per 16-key half: A = K from LDS (lane:
+//   key l%16; one ds_read_b128 of d = 16J + 4*(l/16) .. +3 feeds four
+//   k-steps), B = Q^T held in registers in that same d order.
+//   Online softmax per row (accumulator column l%16), each row masked to its
+//   own causal end min(pos+1, N) and window start.
+//   O^T (D x 16) += V^T . P^T per 16-row block of D: k-step j of half u pairs
+//   lane group g with key 16u + 4g + j, where the score accumulator left
+//   that key's probability (its rows 4g + r, r = j): P is the B operand in
+//   place, and V^T comes four keys per ds_read_b128.
+// The reference's exps are libm expf summed in double with the weights
+// normalised before PV; here device expf, fp32 running sums with the usual
+// max rescaling, and one division at the end (fp32 rounding differences).
+struct PfArgs {
+  const float* q;  // [M][nq][D]
+  const void* k;   // [N][nkv*D] token-major cache
+  const void* v;
+  float* o;        // [M][nq][D]
+  int nq, nkv, M, N, pos0, window, nqb;  // nqb: 64-row blocks per KV head
+  float scale;
+};
+
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = kPfWaves * 64;
+
+template <int D, typename T>
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
+  constexpr int NT = kPfThreads, QB = 16 * kPfWaves;
+  constexpr int KT = D == 256 ? 16 : 32;  // keys per tile (LDS under 64 KiB)
+  constexpr int KH = KT / 16;             // 16-key halves per tile
+  constexpr int KSR = D + 4, VSR = KT + 4;
+  constexpr int JS = D / 4, DT = D / 16;
+  constexpr int VW = KVT<T>::VW;          // elements per 16-byte load
+  constexpr int CH = KT * D / VW;         // 16-byte chunks per tile (K or V)
+  constexpr int CPT = (CH + NT - 1) / NT;
+  static_assert(CH % NT == 0, "whole chunks per thread");
+  __shared__ __attribute__((aligned(16))) float ks[KT * KSR];
+  __shared__ __attribute__((aligned(16))) float vs[D * VSR];
+
+  const int G = a.nq / a.nkv;
+  const int h = blockIdx.x % a.nkv;  // heads fastest: every XCD gets every head's share
+  const int qb = a.nqb - 1 - (int)(blockIdx.x / a.nkv);  // latest rows (most keys) first
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int rows = a.M * G;
+  const int r0 = qb * QB;  // first row of the workgroup (< rows)
+  const int rl = min(r0 + QB, rows) - 1;
+
+  auto t0_of = [&](int m) {
+    const int pos = a.pos0 + m;
+    int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
+    return t0 > a.N ? a.N : t0;
+  };
+  auto nn_of = [&](int m) { return a.pos0 + m + 1 < a.N ? a.pos0 + m + 1 : a.N; };
+  // the workgroup's key range: t0 and the causal end grow with the token
+  const int kt_lo = t0_of(r0 / G);
+  const int kt_hi = nn_of(rl / G);
+  const int ntile = kt_hi > kt_lo ? (kt_hi - kt_lo + KT - 1) / KT : 0;
+
+  // this lane's query row (column c16 of wave w)
+  const int row = r0 + 16 * w + c16;
+  const bool rv = row < rows;
+  const int m = rv ? row / G : 0;
+  const int g = rv ? row - m * G : 0;
+  const int rt0 = rv ? t0_of(m) : 0, rnn = rv ? nn_of(m) : 0;
+  const int64_t qoff = ((int64_t)m * a.nq + h * G + g) * D;
+
+  // Q^T in the k order of the score product
+  float qv[JS];
+#pragma unroll
+  for (int J = 0; J < D / 16; ++J) {
+    f32x4 x = rv ? *reinterpret_cast<const f32x4*>(a.q + qoff + 16 * J + 4 * g4)
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qv[4 * J + i] = x[i];
+  }
+
+  // tile loads: chunk c = tid + NT*i is key c / (D/VW), elements VW*(c % (D/VW))
+  const T* Kb = reinterpret_cast<const T*>(a.k);
+  const T* Vb = reinterpret_cast<const T*>(a.v);
+  const int64_t ts = (int64_t)a.nkv * D;
+  typename KVT<T>::vec kreg[CPT], vreg[CPT];
+  auto load_tile = [&](int tk) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + NT * i;
+      const int key = c / (D / VW), e = VW * (c % (D / VW));
+      const int t = min(tk + key, kt_hi - 1);  // rows past the range: the last one (masked)
+      kreg[i] = load16(Kb + (int64_t)t * ts + (int64_t)h * D + e);
+      vreg[i] = load16(Vb + (int64_t)t * ts + (int64_t)h * D + e);
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + NT * i;
+      const int key = c / (D / VW), e = VW * (c % (D / VW));
+      float kx[VW], vx[VW];
+      KVT<T>::unpack(kreg[i], kx);
+      KVT<T>::unpack(vreg[i], vx);
+#pragma unroll
+      for (int e4 = 0; e4 < VW; e4 += 4)
+        *reinterpret_cast<f32x4*>(ks + key * KSR + e + e4) =
+            f32x4{kx[e4], kx[e4 + 1], kx[e4 + 2], kx[e4 + 3]};
+#pragma unroll
+      for (int j = 0; j < VW; ++j) vs[(e + j) * VSR + key] = vx[j];
+    }
+  };
+
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  if (ntile > 0) load_tile(kt_lo);
+  for (int it = 0; it < ntile; ++it) {
+    const int tk = kt_lo + it * KT;
+    store_tile();
+    __syncthreads();
+    if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
+    // scores of the KH 16-key halves
+    f32x4 sacc[KH];
+#pragma unroll
+    for (int u = 0; u < KH; ++u) {
+      sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int J = 0; J < D / 16; ++J) {
+        const f32x4 kx = *reinterpret_cast<const f32x4*>(ks + (16 * u + c16) * KSR + 16 * J +
+                                                         4 * g4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[i], qv[4 * J + i], sacc[u], 0, 0, 0);
+      }
+    }
+    // online softmax of this lane's row over its 4*KH keys of the tile
+    float sv[KH][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < KH; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = tk + 16 * u + 4 * g4 + r;
+        sv[u][r] = (t >= rt0 && t < rnn) ? sacc[u][r] * a.scale : -INFINITY;
+        tmax = fmaxf(tmax, sv[u][r]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float mn = fmaxf(m_run, tmax);
+    // a row with no key yet keeps max -inf: nothing to rescale, p = 0
+    const float alpha = mn == -INFINITY ? 1.f : softmax_exp(m_run - mn);
+    m_run = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int u = 0; u < KH; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[u][r] = sv[u][r] == -INFINITY ? 0.f : softmax_exp(sv[u][r] - mn);
+        ps += sv[u][r];
+      }
+    l_run = l_run * alpha + ps;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    // PV
+#pragma unroll
+    for (int u = 0; u < KH; ++u)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const f32x4 vx = *reinterpret_cast<const f32x4*>(vs + (16 * dt + c16) * VSR + 16 * u +
+                                                         4 * g4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vx[j], sv[u][j], o[dt], 0, 0, 0);
+      }
+    __syncthreads();  // the tile's LDS is rewritten next
+  }
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  if (rv) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;  // no key: O = 0 (gemm.h:438)
+    float* orow = a.o + qoff;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4*>(orow + 16 * dt + 4 * g4) = o[dt] * inv;
+  }
+}
+
 // Log-sum-exp combine of the chunk partials of split-K launches.  Grid
 // (P/64, slots): a workgroup takes 64 output pairs of one head of a slot
 // (64 divides D) with 4 threads per pair, thread phase ph folding chunks
@@ -2236,6 +2435,102 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
   hipLaunchKernelGGL(rope_append_kernel, dim3(nq + nkv, B), dim3(((d / 2) + 63) / 64 * 64), 0,
                      (hipStream_t)stream, a);
   return (int)hipGetLastError();
+}
+
+static int attn_prefill_impl(const float* Qm, const void* K, const void* V, float* Om, int nq,
+                             int nkv, int M, int N, int d, float scale, int pos0, int window,
+                             int kv_dtype, void* stream) {
+  int st = check_common(nq, nkv, d, kv_dtype);
+  if (st) return st;
+  if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
+  if (M == 0) return 0;
+  if (N == 0) return zero_out(Om, (int64_t)M * nq * d, (hipStream_t)stream);
+  if (!K || !V || !aligned16(K) || !aligned16(V) || !aligned16(Qm) || !aligned16(Om))
+    return MOLOT_EINVAL;
+  const int64_t rows = (int64_t)M * (nq / nkv);
+  const int64_t nqb = (rows + 16 * kPfWaves - 1) / (16 * kPfWaves);
+  if (nqb * nkv > (int64_t)0x7FFFFFFF) return MOLOT_ENOTSUP;
+  PfArgs a{};
+  a.q = Qm;
+  a.k = K;
+  a.v = V;
+  a.o = Om;
+  a.nq = nq;
+  a.nkv = nkv;
+  a.M = M;
+  a.N = N;
+  a.pos0 = pos0;
+  a.window = window;
+  a.nqb = (int)nqb;
+  a.scale = scale;
+  using PfFn = void (*)(PfArgs);
+  PfFn pk = kv_dtype == MOLOT_KV_F32
+                ? (d == 64 ? prefill_kernel<64, float>
+                           : d == 128 ? prefill_kernel<128, float> : prefill_kernel<256, float>)
+                : (d == 64 ? prefill_kernel<64, bf16_t>
+                           : d == 128 ? prefill_kernel<128, bf16_t> : prefill_kernel<256, bf16_t>);
+  const dim3 grid((unsigned)(nqb * nkv));
+  std::lock_guard<std::mutex> plk(g_prof_mu);
+  if (prof_active(stream)) {
+    ProfRec pr{prof_event(), prof_event(), nullptr, nullptr, false};
+    hipExtLaunchKernelGGL(pk, grid, dim3(kPfThreads), 0, (hipStream_t)stream, pr.a0, pr.a1, 0, a);
+    g_prof.push_back(pr);
+  } else {
+    hipLaunchKernelGGL(pk, grid, dim3(kPfThreads), 0, (hipStream_t)stream, a);
+  }
+  return (int)hipGetLastError();
+}
+
+int molot_hip_attn_prefill_gqa(const float* Qm, const void* K, const void* V, float* Om, int nq,
+                               int nkv, int M, int N, int d, float scale, int pos0, int window,
+                               int kv_dtype, void* stream) {
+  return attn_prefill_impl(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window, kv_dtype,
+                           stream);
+}
+
+int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                           float* O, int nq, int nkv, int d, int M, int slot0, int pos0,
+                           const float* q_norm, const float* k_norm, int v_norm, float eps,
+                           const float* inv_freq, float scale, int window, int kv_dtype,
+                           void* stream) {
+  int st = check_common(nq, nkv, d, kv_dtype);
+  if (st) return st;
+  Norms nm;
+  nm.q = q_norm;
+  nm.k = k_norm;
+  nm.v = v_norm ? 1 : 0;
+  nm.eps = eps;
+  if (!norms_ok(nm) || M < 0 || slot0 < 0 || pos0 < 0) return MOLOT_EINVAL;
+  if (M == 0) return 0;
+  if (!q || !k_new || !v_new || !K || !V || !O || !inv_freq) return MOLOT_EINVAL;
+  if ((int64_t)M > 65535) return MOLOT_ENOTSUP;  // one grid row per token
+  RopeArgs r{};
+  r.q = q;
+  r.k_new = k_new;
+  r.v_new = v_new;
+  r.K = K;
+  r.V = V;
+  r.inv_freq = inv_freq;
+  r.tok_stride = (int64_t)nkv * d;
+  r.head_stride = d;
+  r.nq = nq;
+  r.nkv = nkv;
+  r.d = d;
+  r.slot = slot0;
+  r.pos = pos0;
+  r.kv_dtype = kv_dtype;
+  r.append = 1;
+  r.tokens = 1;
+  r.q_norm = nm.q;
+  r.k_norm = nm.k;
+  r.v_norm = nm.v;
+  r.eps = nm.eps;
+  hipLaunchKernelGGL(rope_append_kernel, dim3(nq + nkv, M), dim3(((d / 2) + 63) / 64 * 64), 0,
+                     (hipStream_t)stream, r);
+  st = (int)hipGetLastError();
+  if (st) return st;
+  return attn_prefill_impl(q, K, V, O, nq, nkv, M, slot0 + M, d, scale, pos0, window, kv_dtype,
+                           stream);
 }
 
 int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream) {

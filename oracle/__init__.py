@@ -65,6 +65,7 @@ def lib() -> ctypes.CDLL:
             "orc_attn_decode_f64": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _D, _I, _I, _I, _I64,
                                            _I64, _I64, _P, _I, _I]),
             "orc_rmsnorm": (None, [_P, _P, _P, _I, _F]),
+            "orc_attn_prefill": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _I]),
             "orc_decode_step_norm": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P,
                                             _I, _F, _P, _F, _I, _I, _I]),
         }
@@ -113,6 +114,10 @@ def ref() -> ctypes.CDLL:
             "ref_attn_decode_gqa_win": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _F, _I, _I, _P]),
             "ref_decode_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _F, _I,
                                      _P]),
+            "ref_attn_prefill_gqa": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I,
+                                            _P]),
+            "ref_prefill_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P,
+                                      _I, _F, _P, _F, _I, _P]),
             "ref_rmsnorm": (None, [_P, _P, _P, _I, _F]),
             "ref_rmsnorm_plain": (None, [_P, _P, _I, _F]),
             "ref_decode_step_norm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P,
@@ -284,3 +289,45 @@ def decode_step_norm(q, k_new, v_new, Kc, Vc, nq, nkv, d, slot, pos, q_norm, k_n
                                _p(_f32(inv_freq)), float(scale), int(window), _kv_code(Kc),
                                int(nthreads))
     return q, k, O
+
+
+def attn_prefill(Qm, K, V, nq, nkv, M, N, d, scale, pos0, window, nthreads=0) -> np.ndarray:
+    """gemm.h:409-446: causal prefill of M queries [M][nq][d] over the
+    token-major cache [N][nkv*d] (float32 or bf16 bits)."""
+    Qm = _f32(Qm)
+    K = np.ascontiguousarray(K)
+    V = np.ascontiguousarray(V)
+    O = np.empty((M, nq, d), dtype=np.float32)
+    lib().orc_attn_prefill(_p(Qm), _p(K), _p(V), _p(O), nq, nkv, int(M), int(N), d, float(scale),
+                           int(pos0), int(window), _kv_code(K), int(nthreads))
+    return O
+
+
+def prefill_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, M, slot0, pos0, q_norm, k_norm, v_norm,
+                 eps, inv_freq, scale, window, nthreads=0):
+    """forward.h:367-399 for one layer from the restated parts: per token m
+    the norms (NULL weights / v_norm 0 skip them) and RoPE at pos0 + m of q
+    [M][nq][d] and k_new [M][nkv][d], append at slot slot0 + m (bf16 caches
+    rounded), then attn_prefill over N = slot0 + M.  Returns (q_rot, O);
+    Kc/Vc are updated in place."""
+    q = _f32(q).copy().reshape(M, nq, d)
+    k = _f32(k_new).copy().reshape(M, nkv, d)
+    v = _f32(v_new).copy().reshape(M, nkv, d)
+    inv = _f32(inv_freq)
+    for m in range(M):
+        if q_norm is not None:
+            q[m] = rmsnorm(q[m], q_norm, eps)
+        q[m] = rope_apply(q[m], pos0 + m, inv)
+        if k_norm is not None:
+            k[m] = rmsnorm(k[m], k_norm, eps)
+        if v_norm:
+            v[m] = rmsnorm(v[m].reshape(-1), None, eps).reshape(nkv, d)
+        k[m] = rope_apply(k[m], pos0 + m, inv)
+        if Kc.dtype == np.uint16:
+            Kc[slot0 + m] = f32_to_bf16(k[m].reshape(-1))
+            Vc[slot0 + m] = f32_to_bf16(v[m].reshape(-1))
+        else:
+            Kc[slot0 + m] = k[m].reshape(-1)
+            Vc[slot0 + m] = v[m].reshape(-1)
+    O = attn_prefill(q, Kc, Vc, nq, nkv, M, slot0 + M, d, scale, pos0, window, nthreads)
+    return q, O

@@ -20,6 +20,8 @@
  *                              algorithm covers attn.h:57-120 and :178-187.
  *       orc_decode_step     <- include/molot/forward.h:556-591 (rope q, rope k,
  *                              append, attention)
+ *       orc_attn_prefill    <- include/molot/gemm.h:409-446 (causal prefill:
+ *                              scalar expf, double denominator)
  *       orc_rmsnorm         <- include/molot/norm.h:9-28 (weights) and
  *                              :82-96 (w == NULL: rmsnorm_plain)
  *       orc_decode_step_norm <- include/molot/forward.h:554-591 with the
@@ -325,6 +327,64 @@ void orc_decode_step_norm(float* q, float* k_new, const float* v_new, void* Kc, 
   orc_decode_step(q, k_new, v, Kc, Vc, O, nq, nkv, d, slot, pos, inv_freq, scale, window,
                   kv_dtype, nthreads);
   free(v);
+}
+
+/* Causal prefill attention (gemm.h:409-446) over the token-major cache
+ * [N][nkv*d] that already holds the M new tokens.  Query m of head h sits at
+ * position pos0 + m and attends slots [t0, nn): t0 from the window at that
+ * position (clamped to N), nn = min(pos0 + m + 1, N).  Per (h, m):
+ * s_t = dot(q, K_t) * scale with a running max (init -1e30); e_t =
+ * expf(s_t - max) -- the scalar libm exp, not the vector exp of the decode
+ * path -- summed in double; inv = (float)(1/den); out = sum_t V_t*(e_t*inv)
+ * in fp32 over t in order.  Parallel over (head, query) like the
+ * reference's parallel_for over nq*M.  bf16 caches (no reference
+ * counterpart) are widened. */
+void orc_attn_prefill(const float* Qm, const void* K, const void* V, float* Om, int nq, int nkv,
+                      int M, int N, int d, float scale, int pos0, int window, int kv_dtype,
+                      int nthreads) {
+  const orc_kv_t kv = {K, V, kv_dtype, (int64_t)nkv * d, d, 0, NULL, 0};
+  const int G = nq / nkv;
+#ifdef _OPENMP
+  if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+  (void)nthreads;
+#endif
+#pragma omp parallel
+  {
+    float* scores = (float*)malloc((size_t)(N > 0 ? N : 1) * sizeof(float));
+    float* rowbuf = (float*)malloc((size_t)d * sizeof(float));
+#pragma omp for schedule(static)
+    for (int64_t hm = 0; hm < (int64_t)nq * M; ++hm) {
+      const int h = (int)(hm / M), m = (int)(hm % M);
+      const int kvh = h / G;
+      const int pos = pos0 + m;
+      int t0 = orc_t0(pos, window);
+      if (t0 > N) t0 = N;
+      const int nn = pos + 1 < N ? pos + 1 : N;
+      const float* qh = Qm + ((size_t)m * nq + h) * d;
+      float* oh = Om + ((size_t)m * nq + h) * d;
+      float mx = -1e30f;
+      for (int t = t0; t < nn; ++t) {
+        const float s = orc_dot(qh, orc_row(&kv, 0, kvh, t, d, rowbuf), d) * scale;
+        scores[t] = s;
+        if (s > mx) mx = s;
+      }
+      double den = 0;
+      for (int t = t0; t < nn; ++t) {
+        scores[t] = expf(scores[t] - mx);
+        den += scores[t];
+      }
+      const float inv = (float)(1.0 / den);
+      for (int j = 0; j < d; ++j) oh[j] = 0;
+      for (int t = t0; t < nn; ++t) {
+        const float w = scores[t] * inv;
+        const float* vr = orc_row(&kv, 1, kvh, t, d, rowbuf);
+        for (int j = 0; j < d; ++j) oh[j] += vr[j] * w;
+      }
+    }
+    free(scores);
+    free(rowbuf);
+  }
 }
 
 /* ------------------------------------------------------------------ */

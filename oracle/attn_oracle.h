@@ -34,6 +34,9 @@ void orc_decode_step_norm(float* q, float* k_new, const float* v_new, void* Kc, 
                           const float* q_norm, const float* k_norm, int v_norm, float eps,
                           const float* inv_freq, float scale, int window, int kv_dtype,
                           int nthreads);
+void orc_attn_prefill(const float* Qm, const void* K, const void* V, float* Om, int nq, int nkv,
+                      int M, int N, int d, float scale, int pos0, int window, int kv_dtype,
+                      int nthreads);
 void orc_attn_decode_f64(const float* Q, const void* K, const void* V, double* O, int nq,
                          int nkv, int n, int d, double scale, int pos_cur, int window,
                          int kv_dtype, int64_t tok_stride, int64_t head_stride,

@@ -89,6 +89,45 @@ int ref_decode_step(float* q, float* k, const float* v, float* Kc, float* Vc, fl
   return 0;
 }
 
+void ref_attn_prefill_gqa(const float* Qm, const float* K, const float* V, float* Om, int nq,
+                          int nkv, int M, int N, int d, float scale, int pos0, int window,
+                          void* pool) {
+  molot::attn_prefill_gqa(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window,
+                          *static_cast<molot::ThreadPool*>(pool));
+}
+
+// One layer's prefill in forward.h's order (forward.h:367-399): per token
+// q heads RMS-normed with q_norm and rotated at pos0 + m, k heads normed
+// with k_norm, v normed over its nkv*d values when v_norm, k rotated, k/v
+// appended at slot slot0 + m; then attn_prefill_gqa over N = slot0 + M.
+// NULL weights skip a norm (forward.h always has them; the shim lets tests
+// isolate RoPE + append).  Returns -1 where forward.h:380 would throw.
+int ref_prefill_step(float* Q, float* Kn, float* Vn, float* Kc, float* Vc, float* O, int nq,
+                     int nkv, int d, int M, int slot0, int cap, int pos0, const float* q_norm,
+                     const float* k_norm, int v_norm, float eps, const float* inv_freq,
+                     float scale, int window, void* pool) {
+  if (slot0 + M > cap) return -1;
+  for (int mm = 0; mm < M; ++mm) {
+    float* qq = Q + (size_t)mm * nq * d;
+    float* kk = Kn + (size_t)mm * nkv * d;
+    float* vv = Vn + (size_t)mm * nkv * d;
+    for (int hh = 0; hh < nq; ++hh) {
+      if (q_norm) molot::rmsnorm(qq + (size_t)hh * d, q_norm, qq + (size_t)hh * d, d, eps);
+      molot::rope_apply(qq + (size_t)hh * d, d, pos0 + mm, inv_freq);
+    }
+    if (k_norm)
+      for (int hh = 0; hh < nkv; ++hh)
+        molot::rmsnorm(kk + (size_t)hh * d, k_norm, kk + (size_t)hh * d, d, eps);
+    if (v_norm) molot::rmsnorm_plain(vv, vv, nkv * d, eps);
+    for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(kk + (size_t)hh * d, d, pos0 + mm, inv_freq);
+    std::memcpy(Kc + (size_t)(slot0 + mm) * nkv * d, kk, (size_t)nkv * d * 4);
+    std::memcpy(Vc + (size_t)(slot0 + mm) * nkv * d, vv, (size_t)nkv * d * 4);
+  }
+  molot::attn_prefill_gqa(Q, Kc, Vc, O, nq, nkv, M, slot0 + M, d, scale, pos0, window,
+                          *static_cast<molot::ThreadPool*>(pool));
+  return 0;
+}
+
 void ref_rmsnorm(const float* x, const float* w, float* y, int n, float eps) {
   molot::rmsnorm(x, w, y, n, eps);
 }

@@ -112,6 +112,37 @@ def gen_rmsnorm(name, sizes, seed):
     _save(name, sizes=np.array(sizes), eps=1e-6, seed=seed, **out)
 
 
+def gen_prefill(name, nq, nkv, d, M, n0, base, window, scale, eps, norms, seed, pool):
+    """forward.h:367-399 for one layer through the reference: per-token norms
+    (when `norms`) and RoPE, append of M rows after n0 cached ones, then
+    attn_prefill_gqa (gemm.h:409-446) over N = n0 + M at pos0 = n0."""
+    R = oracle.ref()
+    st = Stream(seed)
+    q = st.normal((M, nq, d), 2.0)
+    k = st.normal((M, nkv, d), 2.0)
+    v = st.normal((M, nkv, d), 2.0)
+    q_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    k_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    cap = n0 + M
+    Kc = np.zeros((cap, nkv * d), np.float32)
+    Vc = np.zeros((cap, nkv * d), np.float32)
+    Kc[:n0] = st.normal((n0, nkv * d))
+    Vc[:n0] = st.normal((n0, nkv * d))
+    inv = ref_inv_freq(base, d)
+    q_rot, k_rot, v_out = q.copy(), k.copy(), v.copy()
+    Kout, Vout = Kc.copy(), Vc.copy()
+    O = np.empty((M, nq, d), np.float32)
+    rc = R.ref_prefill_step(P(q_rot), P(k_rot), P(v_out), P(Kout), P(Vout), P(O), nq, nkv, d, M,
+                            n0, cap, n0, P(q_norm) if norms else None,
+                            P(k_norm) if norms else None, int(norms), float(eps), P(inv),
+                            float(scale), int(window), pool.h)
+    assert rc == 0
+    _save(name, q=q, k_new=k, v_new=v, K=Kc[:n0], V=Vc[:n0], inv_freq=inv, q_norm=q_norm,
+          k_norm=k_norm, norms=int(norms), q_rot=q_rot, K_after=Kout[n0:], V_after=Vout[n0:],
+          O=O, nq=nq, nkv=nkv, d=d, M=M, pos0=n0, base=base, window=window, scale=scale, eps=eps,
+          seed=seed)
+
+
 def gen_head(name, n, d, sigma, seed):
     """attn_decode_head (attn.h:104-107), the bench/bench.cc:186-218 check shape."""
     R = oracle.ref()
@@ -221,6 +252,13 @@ def main() -> None:
             gen_decode_step_norm("decode_step_norm_win_d256", nq=4, nkv=2, d=256, n0=60,
                                  base=10000.0, window=16, scale=1.0, eps=1e-6, v_norm=0,
                                  seed=21, pool=pool)
+        if want("prefill_g4_d64"):
+            gen_prefill("prefill_g4_d64", nq=4, nkv=1, d=64, M=21, n0=30, base=500000.0,
+                        window=0, scale=1.0 / math.sqrt(64), eps=1e-6, norms=False, seed=23,
+                        pool=pool)
+        if want("prefill_norm_win_d128"):
+            gen_prefill("prefill_norm_win_d128", nq=4, nkv=2, d=128, M=12, n0=20, base=10000.0,
+                        window=8, scale=1.0, eps=1e-6, norms=True, seed=24, pool=pool)
         if want("head_bench_check"):
             gen_head("head_bench_check", n=160, d=128, sigma=0.2, seed=1234)
         if want("gqa_headmajor_d64"):

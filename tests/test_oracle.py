@@ -289,6 +289,97 @@ def test_v_norm_is_over_all_kv_heads():
     assert np.max(np.abs(per_head - g["v_normed"].reshape(-1))) > 1e-3
 
 
+# ---------------------------------------------------------------------------
+# prefill attention (gemm.h:409-446) and the layer's prefill (forward.h:367-399)
+
+def _prefill_f64(Q, K, V, nq, nkv, M, N, d, scale, pos0, window):
+    G = nq // nkv
+    O = np.zeros((M, nq, d))
+    for m in range(M):
+        pos = pos0 + m
+        t0 = min(max(0, pos - window + 1) if window > 0 else 0, N)
+        nn = min(pos + 1, N)
+        if nn <= t0:
+            continue
+        for h in range(nq):
+            kv = h // G
+            Kh = K[t0:nn, kv * d:(kv + 1) * d].astype(np.float64)
+            Vh = V[t0:nn, kv * d:(kv + 1) * d].astype(np.float64)
+            s = Kh @ Q[m, h].astype(np.float64) * scale
+            e = np.exp(s - s.max())
+            O[m, h] = (e / e.sum()) @ Vh
+    return O
+
+
+@pytest.mark.parametrize("name", ["prefill_g4_d64", "prefill_norm_win_d128"])
+def test_prefill_golden(name):
+    g = golden(name)
+    nq, nkv, d, M, pos0 = (int(g[k]) for k in ("nq", "nkv", "d", "M", "pos0"))
+    Kc = np.zeros((pos0 + M, nkv * d), np.float32)
+    Vc = np.zeros_like(Kc)
+    Kc[:pos0], Vc[:pos0] = g["K"], g["V"]
+    norms = int(g["norms"])
+    q_rot, O = oracle.prefill_step(g["q"], g["k_new"], g["v_new"], Kc, Vc, nq, nkv, d, M, pos0,
+                                   pos0, g["q_norm"] if norms else None,
+                                   g["k_norm"] if norms else None, norms, float(g["eps"]),
+                                   g["inv_freq"], float(g["scale"]), int(g["window"]))
+    np.testing.assert_allclose(q_rot, g["q_rot"], rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(Kc[pos0:], g["K_after"], rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(Vc[pos0:], g["V_after"], rtol=1e-6, atol=1e-7)
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+@pytest.mark.parametrize("nq,nkv,d,M,N,pos0,window", [(8, 2, 64, 40, 90, 50, 0),
+                                                      (4, 4, 128, 33, 33, 0, 0),
+                                                      (16, 1, 64, 20, 70, 50, 16),
+                                                      (6, 2, 256, 9, 200, 191, 0),
+                                                      (8, 2, 64, 12, 30, 25, 0)])
+def test_prefill_vs_f64(nq, nkv, d, M, N, pos0, window):
+    """Causal masking, windows, a cache longer than the prompt's positions
+    (pos0 + M > N clips at N) and every GQA grouping, against float64."""
+    st = Stream(M + N + d)
+    Q = st.normal((M, nq, d))
+    K, V = kv_token_major(st, N, nkv, d)
+    O = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, 1 / math.sqrt(d), pos0, window)
+    R = _prefill_f64(Q, K, V, nq, nkv, M, N, d, 1 / math.sqrt(d), pos0, window)
+    assert normwise_err(O, R) < 1e-6
+
+
+def test_prefill_single_query_is_decode_attention():
+    """M = 1 at pos0 = N - 1 is the decode attention of attn.h:125-177 (which
+    uses the vector exp: the two differ by its 1.5e-6 relative error)."""
+    st = Stream(34)
+    nq, nkv, d, N = 32, 8, 128, 777
+    Q = st.normal((1, nq, d))
+    K, V = kv_token_major(st, N, nkv, d)
+    for window in (0, 100):
+        O = oracle.attn_prefill(Q, K, V, nq, nkv, 1, N, d, 0.088, N - 1, window)
+        R = oracle.attn_decode_gqa_cache(Q[0], K, V, nq, nkv, N, d, 0.088, N - 1, window)
+        assert normwise_err(O[0], R) < 5e-6
+
+
+def test_prefill_first_token_sees_only_itself():
+    st = Stream(35)
+    nq, nkv, d, M = 8, 2, 64, 5
+    Q = st.normal((M, nq, d))
+    K, V = kv_token_major(st, M, nkv, d)
+    O = oracle.attn_prefill(Q, K, V, nq, nkv, M, M, d, 0.125, 0, 0)
+    for h in range(nq):
+        np.testing.assert_array_equal(O[0, h], V[0, (h // 4) * d:(h // 4 + 1) * d])
+
+
+def test_planted_non_causal_prefill_is_caught():
+    """Attending the whole cache instead of the causal prefix fails float64."""
+    st = Stream(36)
+    nq, nkv, d, M, N = 4, 1, 64, 16, 16
+    Q = st.normal((M, nq, d))
+    K, V = kv_token_major(st, N, nkv, d)
+    R = _prefill_f64(Q, K, V, nq, nkv, M, N, d, 0.125, 0, 0)
+    full = np.stack([oracle.attn_decode_gqa_cache(Q[m], K, V, nq, nkv, N, d, 0.125, N - 1, 0)
+                     for m in range(M)])
+    assert normwise_err(full, R) > 1e-2
+
+
 def test_head_golden():
     g = golden("head_bench_check")
     n, d = int(g["n"]), int(g["d"])
@@ -522,6 +613,22 @@ def test_decode_step_norm_vs_reference():
     np.testing.assert_allclose(q_rot, qr, rtol=2e-6, atol=2e-6)
     np.testing.assert_allclose(Vo[pos], Vr[pos], rtol=5e-7, atol=0)
     assert normwise_err(O, R) < 2e-6
+
+
+@needs_ref
+def test_prefill_vs_reference():
+    st = Stream(37)
+    nq, nkv, d, M, N, pos0 = 32, 8, 128, 70, 300, 230
+    Q = st.normal((M, nq, d))
+    K, V = kv_token_major(st, N, nkv, d)
+    for window in (0, 64):
+        O = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, 0.088, pos0, window)
+        R = np.empty_like(O)
+        with oracle.RefPool(4) as pool:
+            oracle.ref().ref_attn_prefill_gqa(oracle._p(Q), oracle._p(K), oracle._p(V),
+                                              oracle._p(R), nq, nkv, M, N, d, 0.088, pos0, window,
+                                              pool.h)
+        assert normwise_err(O, R) < 1e-6
 
 
 @needs_ref

@@ -1,0 +1,177 @@
+"""Parity of the HIP prefill attention (include/molot/gemm.h:409-446) and of
+one layer's fused prefill (forward.h:367-399) with the oracle (MI355X only).
+
+Every call goes through the C ABI.  Bar: normwise max|gpu-ref|/max|ref|
+<= 1e-5 against the oracle on the same values (fp32 caches, and bf16 caches
+widened: the kernel itself is fp32-accurate on those values); RoPE outputs
+and the appended rows within fp32 rounding of the oracle's.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import normwise_err
+from gpu_util import dev, dev_bf16, host
+from molot_amd import attn
+from molot_amd.synth import Stream, bf16_to_f32, f32_to_bf16
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def golden(name):
+    with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def cache(st, N, nkv, d, bf16):
+    K = st.normal((N, nkv * d))
+    V = st.normal((N, nkv * d))
+    if bf16:
+        return f32_to_bf16(K), f32_to_bf16(V)
+    return K, V
+
+
+def on_dev(x):
+    return dev_bf16(x) if x.dtype == np.uint16 else dev(x)
+
+
+@pytest.mark.parametrize("name", ["prefill_g4_d64", "prefill_norm_win_d128"])
+def test_golden_prefill_step(gpu, name):
+    """Against the compiled reference's forward.h prefill sequence."""
+    g = golden(name)
+    nq, nkv, d, M, pos0 = (int(g[k]) for k in ("nq", "nkv", "d", "M", "pos0"))
+    norms = int(g["norms"])
+    K = np.zeros((pos0 + M, nkv * d), np.float32)
+    V = np.zeros_like(K)
+    K[:pos0], V[:pos0] = g["K"], g["V"]
+    q, Kd, Vd = dev(g["q"]), dev(K), dev(V)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.prefill_step(q, dev(g["k_new"]), dev(g["v_new"]), Kd, Vd, O, nq, nkv, d, M, pos0, pos0,
+                      dev(g["inv_freq"]), float(g["scale"]), int(g["window"]),
+                      q_norm=dev(g["q_norm"]) if norms else None,
+                      k_norm=dev(g["k_norm"]) if norms else None, v_norm=bool(norms),
+                      eps=float(g["eps"]))
+    np.testing.assert_allclose(host(q), g["q_rot"], rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(host(Kd)[pos0:], g["K_after"], rtol=2e-6, atol=4e-6)
+    np.testing.assert_allclose(host(Vd)[pos0:], g["V_after"], rtol=1e-6, atol=1e-7)
+    assert normwise_err(host(O), g["O"]) < TOL
+
+
+@pytest.mark.parametrize("nq,nkv,d,M,N,pos0,window,bf16", [
+    (32, 8, 128, 100, 100, 0, 0, False),     # fresh prompt
+    (32, 8, 128, 77, 1077, 1000, 0, False),  # appended to a context
+    (8, 4, 256, 50, 3050, 3000, 1024, False),  # gemma-style window, d256
+    (8, 4, 256, 70, 170, 100, 33, True),
+    (64, 8, 128, 33, 533, 500, 0, True),     # G = 8
+    (32, 2, 64, 21, 71, 50, 0, False),       # G = 16
+    (16, 16, 64, 65, 65, 0, 0, True),        # G = 1
+    (12, 4, 128, 30, 60, 30, 7, False),      # G = 3
+    (8, 2, 64, 12, 30, 25, 0, False),        # pos0 + M > N: causal end clipped at N
+    (8, 2, 128, 1, 500, 499, 0, False),      # a single query
+])
+def test_prefill_vs_oracle(gpu, nq, nkv, d, M, N, pos0, window, bf16):
+    announce(f"prefill {nq}/{nkv}/{d} M={M} N={N} pos0={pos0} win={window} bf16={bf16}")
+    st = Stream(M + N + d + nq)
+    Q = st.normal((M, nq, d))
+    K, V = cache(st, N, nkv, d, bf16)
+    O = torch.empty((M, nq, d), device="cuda")
+    scale = 1 / math.sqrt(d)
+    attn.attn_prefill_gqa(dev(Q), on_dev(K), on_dev(V), O, nq, nkv, M, N, d, scale, pos0, window)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, scale, pos0, window)
+    err = normwise_err(host(O), R)
+    print(f"prefill normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
+def test_prefill_empty_cases(gpu):
+    """Queries whose window holds no slot get O = 0; an empty cache gives 0."""
+    st = Stream(70)
+    nq, nkv, d = 8, 2, 64
+    Q = st.normal((4, nq, d))
+    K, V = cache(st, 10, nkv, d, False)
+    O = torch.full((4, nq, d), 5.0, device="cuda")
+    # positions 40..43 with window 5 over a 10-slot cache: nothing attended
+    attn.attn_prefill_gqa(dev(Q), dev(K), dev(V), O, nq, nkv, 4, 10, d, 0.125, 40, 5)
+    assert np.all(host(O) == 0)
+    O.fill_(5.0)
+    attn.attn_prefill_gqa(dev(Q), dev(K), dev(V), O, nq, nkv, 4, 0, d, 0.125, 0, 0)
+    assert np.all(host(O) == 0)
+
+
+def test_prefill_single_query_matches_decode_kernel(gpu):
+    """M = 1 through the prefill kernel equals the decode kernel's attention."""
+    st = Stream(71)
+    nq, nkv, d, N = 32, 8, 128, 4097
+    Q = st.normal((1, nq, d))
+    K, V = cache(st, N, nkv, d, False)
+    Op = torch.empty((1, nq, d), device="cuda")
+    Od = torch.empty((nq, d), device="cuda")
+    attn.attn_prefill_gqa(dev(Q), dev(K), dev(V), Op, nq, nkv, 1, N, d, 0.088, N - 1, 0)
+    attn.attn_decode_gqa_cache(dev(Q[0]), dev(K), dev(V), Od, nq, nkv, N, d, 0.088, N - 1, 0)
+    assert normwise_err(host(Op)[0], host(Od)) < 2e-6
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_prefill_step_vs_oracle(gpu, bf16):
+    """One layer's prefill with norms: 200 prompt tokens after 300 cached."""
+    announce(f"prefill step 32q/8kv/d128 M=200 after 300 bf16={bf16}")
+    st = Stream(72 + bf16)
+    nq, nkv, d, M, n0 = 32, 8, 128, 200, 300
+    q = st.normal((M, nq, d), 2.0)
+    k = st.normal((M, nkv, d), 2.0)
+    v = st.normal((M, nkv, d), 2.0)
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    kn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    K, V = cache(st, n0 + M, nkv, d, bf16)
+    K[n0:] = 0
+    V[n0:] = 0
+    inv = oracle.rope_inv_freq(500000.0, d)
+    qd, Kd, Vd = dev(q), on_dev(K), on_dev(V)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.prefill_step(qd, dev(k), dev(v), Kd, Vd, O, nq, nkv, d, M, n0, n0, dev(inv), 0.088, 0,
+                      q_norm=dev(qn), k_norm=dev(kn), v_norm=True, eps=1e-6)
+    Kc, Vc = K.copy(), V.copy()
+    oq, oO = oracle.prefill_step(q, k, v, Kc, Vc, nq, nkv, d, M, n0, n0, qn, kn, 1, 1e-6, inv,
+                                 0.088, 0)
+    np.testing.assert_allclose(host(qd), oq, rtol=2e-6, atol=4e-6)
+    if bf16:  # the normed rows may differ by an fp32 ulp before their bf16 rounding
+        Kh = bf16_to_f32(host(Kd.view(torch.int16)).view(np.uint16))
+        Vh = bf16_to_f32(host(Vd.view(torch.int16)).view(np.uint16))
+        assert np.max(np.abs(Kh - bf16_to_f32(Kc))) <= 8e-3 * np.max(np.abs(bf16_to_f32(Kc)))
+        assert np.max(np.abs(Vh - bf16_to_f32(Vc))) <= 8e-3 * np.max(np.abs(bf16_to_f32(Vc)))
+        # the attention itself against the oracle on the GPU's own cache rows
+        R = oracle.attn_prefill(host(qd), host(Kd.view(torch.int16)).view(np.uint16),
+                                host(Vd.view(torch.int16)).view(np.uint16), nq, nkv, M, n0 + M,
+                                d, 0.088, n0, 0)
+        assert normwise_err(host(O), R) < TOL
+        assert normwise_err(host(O), oO) < 2e-2
+    else:
+        np.testing.assert_allclose(host(Kd), Kc, rtol=2e-6, atol=4e-6)
+        np.testing.assert_allclose(host(Vd), Vc, rtol=1e-6, atol=1e-7)
+        assert normwise_err(host(O), oO) < TOL
+
+
+def test_prefill_2k_prompt(gpu):
+    """A 2048-token prompt at the headline head shape (the bench workload)."""
+    announce("prefill 32q/8kv/d128 M=2048 fresh")
+    st = Stream(74)
+    nq, nkv, d, M = 32, 8, 128, 2048
+    Q = st.normal((M, nq, d))
+    K, V = cache(st, M, nkv, d, False)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.attn_prefill_gqa(dev(Q), dev(K), dev(V), O, nq, nkv, M, M, d, 0.088, 0, 0)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, M, d, 0.088, 0, 0)
+    err = normwise_err(host(O), R)
+    print(f"prefill 2k normwise err {err:.3e}", flush=True)
+    assert err < TOL
