@@ -57,7 +57,13 @@ CONFIGS = {
     # paged bf16 cache, 64 sequences of context U[512, 8192], shuffled 16-row pages
     "c4": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=1, sigma=1.0, batch=64,
                lmin=512, lmax=8192, page=16),
+    # prefill (gemm.h:409-446, forward.h:367-399): M prompt tokens after n0 cached
+    "p1": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=0, sigma=1.0, prompt=2048,
+               n0=0),
+    "p2": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=0, sigma=1.0, prompt=512,
+               n0=16384),
 }
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 DESCR = {
     "c1": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 fp32 KV, pos 4096 (n=4097), batch 1",
     "c2": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 fp32 KV, ctx 16384 (n=16385), batch 1",
@@ -65,6 +71,9 @@ DESCR = {
     "c4": "continuous-batching decode step, 64 sequences of ctx U[512,8192], 32q/8kv/d128, "
           "bf16 KV in shuffled 16-token pages",
     "c5": "long-context GQA decode layer-step, 64q/8kv/d128 bf16 KV, pos 131072 (n=131073)",
+    "p1": "layer prefill (RoPE + append + causal attention), 2048-token prompt, 32q/8kv/d128 "
+          "fp32 KV",
+    "p2": "layer prefill, 512-token prompt after 16384 cached tokens, 32q/8kv/d128 fp32 KV",
 }
 
 
@@ -337,6 +346,8 @@ def main() -> int:
     lib.molot_hip_set_block_order(args.block_order)
 
     cfg = CONFIGS[args.config]
+    if "prompt" in cfg:
+        return run_prefill(args, cfg, lib, L, torch, np)
     t_setup = time.time()
     make = paged_workload if "batch" in cfg else contiguous_workload
     wl = make(args, cfg, lib, L, torch, np)
@@ -514,6 +525,141 @@ def main() -> int:
         out["cpu_baseline"] = wl.cpu(args)
     print(json.dumps(out), flush=True)
     return 0
+
+
+def run_prefill(args, cfg, lib, L, torch, np):
+    """Prefill configs: one step = molot_hip_prefill_step for one layer (RoPE
+    of the prompt's q and k, append of its M rows, causal attention); value =
+    attention TFLOP/s, 4*d flops per (q head, query, attended key)."""
+    from molot_amd import attn
+    from molot_amd.synth import Stream
+
+    nq, nkv, d, M, n0 = cfg["nq"], cfg["nkv"], cfg["d"], cfg["prompt"], cfg["n0"]
+    theta, window = cfg["theta"], cfg["window"]
+    N = n0 + M
+    scale = 1.0 / math.sqrt(d)
+    t0s = [max(0, n0 + m - window + 1) if window > 0 else 0 for m in range(M)]
+    keys = sum(min(n0 + m + 1, N) - t0s[m] for m in range(M))
+    flops = 4 * d * nq * keys
+    t_setup = time.time()
+    st = Stream(1234)
+    q_h = st.normal((M, nq, d))
+    k_h = st.normal((M, nkv, d))
+    v_h = st.normal((M, nkv, d))
+    K_h = np.zeros((N, nkv * d), np.float32)
+    V_h = np.zeros_like(K_h)
+    K_h[:n0] = st.normal((n0, nkv * d))
+    V_h[:n0] = st.normal((n0, nkv * d))
+    q, kn, vn = (torch.from_numpy(x).cuda() for x in (q_h, k_h, v_h))
+    K, V = torch.from_numpy(K_h).cuda(), torch.from_numpy(V_h).cuda()
+    inv = attn.rope_inv_freq(theta, d).cuda()
+    O = torch.empty((M, nq, d), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    log(args, f"setup {time.time() - t_setup:.1f}s: {args.config} M={M} after {n0}, "
+        f"{keys} (query, key) pairs per head, {flops / 1e9:.1f} GFLOP/step")
+    P = ctypes.c_void_p
+    qp, kp, vp, Kp, Vp, ip, op = (P(t.data_ptr()) for t in (q, kn, vn, K, V, inv, O))
+
+    def step(i, stream):
+        rc = lib.molot_hip_prefill_step(qp, kp, vp, Kp, Vp, op, nq, nkv, d, M, n0, n0, None, None,
+                                        0, 1e-6, ip, scale, window, 0, stream)
+        if rc:
+            raise L.MolotHipError(rc, "prefill_step")
+
+    def cur_stream():
+        return P(torch.cuda.current_stream().cuda_stream)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    steps = max(1, args.steps // 25)  # each step is ~100x a decode step
+    with torch.cuda.stream(s):
+        sp = cur_stream()
+        for i in range(max(2, args.warmup // 10)):
+            step(i, sp)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(s)
+        for i in range(steps):
+            step(i, sp)
+        end.record(s)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    value = flops / (ms * 1e-3) / 1e12
+    log(args, f"eager: {steps} steps, {ms * 1e3:.1f} us/step -> {value:.1f} TFLOP/s "
+        f"({100 * value / FP32_MFMA_PEAK_TFLOPS:.1f}% of fp32 MFMA peak)")
+    with torch.cuda.stream(s):
+        L.check(lib.molot_hip_profile_begin(steps), "profile_begin")
+        for i in range(steps):
+            step(i, sp)
+    am, cm = ctypes.c_float(), ctypes.c_float()
+    na, nc = ctypes.c_int(), ctypes.c_int()
+    L.check(lib.molot_hip_profile_end(ctypes.byref(am), ctypes.byref(cm), ctypes.byref(na),
+                                      ctypes.byref(nc)), "profile_end")
+    k_us = am.value / max(1, na.value) * 1e3
+    achieved = flops / (k_us * 1e-6) / 1e12
+    log(args, f"prefill_kernel {k_us:.1f} us/launch -> {achieved:.1f} TFLOP/s")
+    out = {
+        "metric": "prefill attention TFLOP/s (causal, 4*d flops per head x query x key)",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": max(2, args.warmup // 10),
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) q/k/v and cache, splitmix64+Box-Muller, seed 1234)",
+        "config": {"workload": DESCR[args.config], "config": args.config, "nq": nq, "nkv": nkv,
+                   "head_dim": d, "prompt": M, "cached": n0, "window": window,
+                   "rope_theta": theta, "timing": "eager"},
+        "flops_per_step": flops,
+        "roofline": {"bound": "mfma", "kernel": "prefill_kernel<%d,float>" % d,
+                     "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                     "traffic": None, "launch_us": round(k_us, 2)},
+    }
+    if args.cpu_seconds > 0:
+        out["cpu_baseline"] = cpu_baseline_prefill(args, q_h, K_h, V_h, nq, nkv, d, M, N, n0,
+                                                   scale, window, flops)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cpu_baseline_prefill(args, q_h, K_h, V_h, nq, nkv, d, M, N, n0, scale, window, flops):
+    """The reference's attn_prefill_gqa (gemm.h:409-446, oracle/_ref) on the
+    host cores over the same cache (the new rows left as drawn: timing
+    only), whole calls within the time budget."""
+    import numpy as np
+
+    import oracle
+    cores = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+    O = np.empty_like(q_h)
+    P = oracle._p
+    kind = "reference" if oracle.ref_available() else "port"
+    pool = oracle.RefPool(cores) if kind == "reference" else None
+
+    def one(i):
+        if kind == "reference":
+            oracle.ref().ref_attn_prefill_gqa(P(q_h), P(K_h), P(V_h), P(O), nq, nkv, M, N, d,
+                                              scale, n0, window, pool.h)
+        else:
+            oracle.lib().orc_attn_prefill(P(q_h), P(K_h), P(V_h), P(O), nq, nkv, M, N, d, scale,
+                                          n0, window, 0, cores)
+
+    steps, el = _cpu_loop(args, one)
+    if pool:
+        pool.close()
+    ms = el / steps * 1e3
+    tf = flops / (ms * 1e-3) / 1e12
+    log(args, f"cpu baseline ({kind}, {cores} threads): {ms:.1f} ms/step -> {tf * 1e3:.1f} GFLOP/s")
+    return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": cores, "kind": kind,
+            "ms_per_step": round(ms, 3),
+            "sample": f"{steps} calls of attn_prefill_gqa on the {args.config} workload, "
+                      f"{el:.1f} s, ThreadPool" if kind == "reference" else
+                      f"{steps} calls of the oracle's prefill, {el:.1f} s, OpenMP"}
 
 
 def _cpu_loop(args, one):

@@ -377,7 +377,7 @@ struct Tune {
 
 // Dynamic LDS layout shared by host (size) and device (offsets), in floats.
 struct Lds {
-  int qs, cs, sn, knew, vnew, pw, wm, wl, red, blk, misc, total;
+  int qs, cs, sn, knew, vnew, nw, pw, wm, wl, red, blk, misc, total;
   __host__ __device__ Lds(int D, int GH, int NW, int RB, int chunk, int page_shift, bool paged) {
     int o = 0;
     qs = o; o += GH * D;
@@ -385,6 +385,7 @@ struct Lds {
     sn = o; o += D / 2;
     knew = o; o += D;
     vnew = o; o += D;
+    nw = o; o += D;                  // k norm weights
     pw = o; o += NW * RB * GH;
     wm = o; o += NW * GH;
     wl = o; o += NW * GH;
@@ -415,39 +416,99 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// RMS norms of the step's fresh vectors (forward.h:554, 562-563), in LDS
-// before RoPE: the GH q rows with weights q_norm and, in the workgroup that
-// appends the new token, its k with k_norm and its v scaled by the RMS of
-// all nkv*D values of v_new (rmsnorm / rmsnorm_plain, include/molot/
-// norm.h:9-28, :82-96: y = (x * 1/sqrt(mean(x^2) + eps)) * w).  One wave per
-// vector; the caller's barriers order the LDS accesses.
-template <int D, int GH, int NW>
-__device__ __forceinline__ void step_norms(const AttnArgs& a, float* qs, float* knew, float* vnew,
-                                           bool is_new, int b, int w, int lane) {
-  static_assert(NW >= 2, "k and v norms on two waves");
-  if (a.q_norm) {
-    for (int g = w; g < GH; g += NW) {
-      float ss = 0.f;
-      for (int j = lane; j < D; j += 64) ss = fmaf(qs[g * D + j], qs[g * D + j], ss);
-      const float inv = 1.0f / sqrtf(group_sum<64>(ss) / (float)D + a.eps);
-      for (int j = lane; j < D; j += 64) qs[g * D + j] = qs[g * D + j] * inv * a.q_norm[j];
+// RMS norms of the step's fresh vectors (forward.h:554, 562-563):
+// y = (x * 1/sqrt(mean(x^2) + eps)) * w (rmsnorm, include/molot/norm.h:9-28).
+//
+// q, in registers before it is staged: thread i of the prologue holds the
+// float4 i of the GH q rows, so each row is D/4 aligned lanes of a wave and
+// its sum of squares a group sum, with no LDS round trip and no barrier.
+template <int D, int QPT>
+__device__ __forceinline__ void q_norm_regs(const AttnArgs& a, f32x4 (&qv)[QPT],
+                                            const f32x4 (&qw)[QPT]) {
+  static_assert(D / 4 <= 64 && 64 % (D / 4) == 0, "a q row within one wave");
+#pragma unroll
+  for (int u = 0; u < QPT; ++u) {
+    float ss = qv[u][0] * qv[u][0];
+    ss = fmaf(qv[u][1], qv[u][1], ss);
+    ss = fmaf(qv[u][2], qv[u][2], ss);
+    ss = fmaf(qv[u][3], qv[u][3], ss);
+    const float inv = 1.0f / sqrtf(group_sum<D / 4>(ss) / (float)D + a.eps);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qv[u][e] = qv[u][e] * inv * qw[u][e];
+  }
+}
+
+// k and v of the new token, in the workgroup that appends it: the waves'
+// partial sums of squares go to LDS before the prologue's barrier (k: one
+// element per thread; v: all nkv*D values of v_new, see v_norm_load), and
+// the threads that rotate k and round v after that barrier scale them:
+// k by 1/sqrt(mean(k^2) + eps) and its weights (staged in LDS), v by the RMS
+// of all of v_new without weights (rmsnorm_plain, norm.h:82-96).
+template <int D>
+__device__ __forceinline__ void k_norm_share(int tid, int w, int lane, float knv, float* ksum) {
+  const float ss = group_sum<64>(tid < D ? knv * knv : 0.f);
+  if (lane == 0) ksum[w] = ss;
+}
+
+struct NewNorms {
+  float kinv, vinv;
+  __device__ __forceinline__ void apply(const AttnArgs& a, const float* kw, int j, int half,
+                                        float& k0, float& k1, float& v0, float& v1) const {
+    if (a.k_norm) {
+      k0 = k0 * kinv * kw[j];
+      k1 = k1 * kinv * kw[j + half];
+    }
+    if (a.v_norm) {
+      v0 *= vinv;
+      v1 *= vinv;
     }
   }
-  if (!is_new) return;
-  if (a.k_norm && w == NW - 1) {
+};
+
+template <int D, int NW>
+__device__ __forceinline__ NewNorms new_norms(const AttnArgs& a, const float* ksum,
+                                              const float* vsum) {
+  NewNorms r{1.f, 1.f};
+  if (a.k_norm) {
     float ss = 0.f;
-    for (int j = lane; j < D; j += 64) ss = fmaf(knew[j], knew[j], ss);
-    const float inv = 1.0f / sqrtf(group_sum<64>(ss) / (float)D + a.eps);
-    for (int j = lane; j < D; j += 64) knew[j] = knew[j] * inv * a.k_norm[j];
+#pragma unroll
+    for (int k = 0; k < NW; ++k) ss += ksum[k];
+    r.kinv = 1.0f / sqrtf(ss / (float)D + a.eps);
   }
-  if (a.v_norm && w == NW - 2) {
-    const float* vx = a.v_new + (int64_t)b * a.nkv * D;
-    const int nv = a.nkv * D;
+  if (a.v_norm) {
     float ss = 0.f;
-    for (int j = lane; j < nv; j += 64) ss = fmaf(vx[j], vx[j], ss);
-    const float inv = 1.0f / sqrtf(group_sum<64>(ss) / (float)nv + a.eps);
-    for (int j = lane; j < D; j += 64) vnew[j] *= inv;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) ss += vsum[k];
+    r.vinv = 1.0f / sqrtf(ss / (float)(a.nkv * D) + a.eps);
   }
+  return r;
+}
+
+// The joint v norm needs all nkv*D values of the sequence's v_new.  Their
+// loads are issued in the prologue before any K/V row (loads retire in
+// order, so the sum below does not wait for the stream's first block), up
+// to kVnPT per thread; the rest, if any, are summed by a plain loop.
+constexpr int kVnPT = 8;
+
+template <int D, int NT>
+__device__ __forceinline__ void v_norm_load(const AttnArgs& a, int b, int tid, float (&vq)[kVnPT]) {
+  const float* vx = a.v_new + (int64_t)b * a.nkv * D;
+  const int nv = a.nkv * D;
+#pragma unroll
+  for (int u = 0; u < kVnPT; ++u) vq[u] = tid + u * NT < nv ? vx[tid + u * NT] : 0.f;
+}
+
+// The wave's sum of squares of its threads' shares into vsum[w].
+template <int D, int NT>
+__device__ __forceinline__ void v_norm_share(const AttnArgs& a, int b, int tid, int w, int lane,
+                                             const float (&vq)[kVnPT], float* vsum) {
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < kVnPT; ++u) ss = fmaf(vq[u], vq[u], ss);
+  const float* vx = a.v_new + (int64_t)b * a.nkv * D;
+  for (int j = tid + kVnPT * NT; j < a.nkv * D; j += NT) ss = fmaf(vx[j], vx[j], ss);
+  ss = group_sum<64>(ss);
+  if (lane == 0) vsum[w] = ss;
 }
 
 // The workgroup's chunk partial from its waves' partials in LDS: running
@@ -540,7 +601,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   float* vnew = smem + L.vnew;
   int* misc = reinterpret_cast<int*>(smem + L.misc);
 
-  const int c = blockIdx.z;
+  const int z = blockIdx.z;  // chunk slot; chunk c = nch - 1 - z (below)
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
   const int sub = blockIdx.x % nsub;
@@ -567,11 +628,14 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (ROPE ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
-  if (c >= nch) {  // whole workgroup: chunk past this sequence's end (never arrives)
-    if (c == 0)    // empty attended range: o = 0 (include/molot/attn.h:162 with no rows)
+  if (z >= nch) {  // whole workgroup: chunk past this sequence's end (never arrives)
+    if (z == 0)    // empty attended range: o = 0 (include/molot/attn.h:162 with no rows)
       for (int i = tid; i < GH * D; i += NT) a.o[((int64_t)b * a.nq + hq0) * D + i] = 0.f;
     return;
   }
+  // Chunks in reverse: the last one, which holds the new token (and with it
+  // the append, the fold and any norms of k and v), is dispatched first.
+  const int c = nch - 1 - z;
   const int tb = t0 + c * a.chunk;
   const int cntg = max(0, min(a.chunk, cend - tb));  // rows read from the cache
   const bool is_new = ROPE && c == nch - 1;          // this chunk folds in the new token
@@ -638,18 +702,31 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int u = 0; u < QPT; ++u)
     qv[u] = reinterpret_cast<const f32x4*>(a.q + qrow0 * D)[min(tid + u * NT, QV - 1)];
-  float invf = 0.f, knv = 0.f, vnv = 0.f;
+  float invf = 0.f, knv = 0.f, vnv = 0.f, kwv = 0.f;
+  f32x4 qwt[QPT];  // q norm weights of this thread's q elements
   if constexpr (ROPE) {
     invf = a.inv_freq[min(tid, D / 2 - 1)];
     knv = a.k_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
     vnv = a.v_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    if (a.q_norm) {
+#pragma unroll
+      for (int u = 0; u < QPT; ++u)
+        qwt[u] = reinterpret_cast<const f32x4*>(a.q_norm)[min(tid + u * NT, QV - 1) % (D / 4)];
+    }
+    if (is_new && a.k_norm) kwv = a.k_norm[min(tid, D - 1)];
   }
+  float vq[kVnPT];
+  const bool vn = ROPE && is_new && a.v_norm;  // uniform over the workgroup
+  if (vn) v_norm_load<D, NT>(a, b, tid, vq);
   // each wave's first NBUF blocks: w (and w + NW); the rest are claimed
   int bA = w, bB = w + NW;
   load_block(kA, vA, bA * RB);
   if constexpr (C::NBUF == 2) load_block(kB, vB, bB * RB);
   if (tid == 0) {
     misc[0] = C::NBUF * NW;  // next block to claim
+  }
+  if constexpr (ROPE) {
+    if (a.q_norm) q_norm_regs<D, QPT>(a, qv, qwt);
   }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
@@ -670,11 +747,10 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       knew[tid] = knv;
       vnew[tid] = vnv;
     }
+    if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl);
+    if (tid < D) smem[L.nw + tid] = kwv;
+    if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
     lds_barrier();
-    if (a.q_norm || (is_new && (a.k_norm || a.v_norm))) {  // uniform over the workgroup
-      step_norms<D, GH, NW>(a, qs, knew, vnew, is_new, b, w, lane);
-      lds_barrier();
-    }
     for (int i = tid; i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
       const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
@@ -682,13 +758,16 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       qs[g * D + j + D / 2] = x0 * sn[j] + x1 * csn[j];
     }
     if (is_new) {
-      // the appended row as the cache will hold it: rotated k, k and v
-      // rounded to the cache type (stored into the cache after the stream)
+      // the appended row as the cache will hold it: normed (as configured),
+      // rotated k, k and v rounded to the cache type (stored into the cache
+      // after the stream)
+      const NewNorms nn = new_norms<D, NW>(a, smem + L.wm, smem + L.wl);
       for (int j = tid; j < D / 2; j += NT) {
-        const float k0 = knew[j], k1 = knew[j + D / 2];
+        float k0 = knew[j], k1 = knew[j + D / 2];
+        float v0 = vnew[j], v1 = vnew[j + D / 2];
+        nn.apply(a, smem + L.nw, j, D / 2, k0, k1, v0, v1);
         float r0 = k0 * csn[j] - k1 * sn[j];
         float r1 = k0 * sn[j] + k1 * csn[j];
-        float v0 = vnew[j], v1 = vnew[j + D / 2];
         if constexpr (sizeof(T) == 2) {
           r0 = __uint_as_float((uint32_t)f32_to_bf16(r0) << 16);
           r1 = __uint_as_float((uint32_t)f32_to_bf16(r1) << 16);
@@ -957,7 +1036,7 @@ constexpr int kTile = 32;                      // cache rows per wave step
 // LDS of attn_mfma_kernel, in floats.  vt: per wave, 32 staged V rows of D
 // bf16 (16*D floats), which after the stream hold the wave's partial o.
 struct LdsM {
-  int qs, cs, sn, knew, vnew, wm, wl, vt, blk, misc, total;
+  int qs, cs, sn, knew, vnew, nw, wm, wl, vt, blk, misc, total;
   __host__ __device__ LdsM(int D, int GH, int chunk, int page_shift, bool paged) {
     int o = 0;
     qs = o; o += GH * D;
@@ -965,6 +1044,7 @@ struct LdsM {
     sn = o; o += D / 2;
     knew = o; o += D;
     vnew = o; o += D;
+    nw = o; o += D;  // k norm weights
     wm = o; o += kMfmaWaves * GH;
     wl = o; o += kMfmaWaves * GH;
     o = (o + 63) & ~63;  // 256-byte aligned: the swizzle's bank pattern
@@ -1007,7 +1087,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   float* vnew = smem + L.vnew;
   int* misc = reinterpret_cast<int*>(smem + L.misc);
 
-  const int c = blockIdx.z;
+  const int z = blockIdx.z;  // chunk slot; chunk c = nch - 1 - z (below)
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
   const int sub = blockIdx.x % nsub;
@@ -1033,11 +1113,12 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (ROPE ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
-  if (c >= nch) {
-    if (c == 0)
+  if (z >= nch) {
+    if (z == 0)
       for (int i = tid; i < GH * D; i += NT) a.o[((int64_t)b * a.nq + hq0) * D + i] = 0.f;
     return;
   }
+  const int c = nch - 1 - z;  // the new token's chunk first, as in attn_kernel
   const int tb = t0 + c * a.chunk;
   const int cntg = max(0, min(a.chunk, cend - tb));
   const bool is_new = ROPE && c == nch - 1;
@@ -1092,15 +1173,28 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 #pragma unroll
   for (int u = 0; u < QPT; ++u)
     qv[u] = reinterpret_cast<const f32x4*>(a.q + qrow0 * D)[min(tid + u * NT, QV - 1)];
-  float invf = 0.f, knv = 0.f, vnv = 0.f;
+  float invf = 0.f, knv = 0.f, vnv = 0.f, kwv = 0.f;
+  f32x4 qwt[QPT];  // q norm weights of this thread's q elements
   if constexpr (ROPE) {
     invf = a.inv_freq[min(tid, D / 2 - 1)];
     knv = a.k_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
     vnv = a.v_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    if (a.q_norm) {
+#pragma unroll
+      for (int u = 0; u < QPT; ++u)
+        qwt[u] = reinterpret_cast<const f32x4*>(a.q_norm)[min(tid + u * NT, QV - 1) % (D / 4)];
+    }
+    if (is_new && a.k_norm) kwv = a.k_norm[min(tid, D - 1)];
   }
+  float vq[kVnPT];
+  const bool vn = ROPE && is_new && a.v_norm;  // uniform over the workgroup
+  if (vn) v_norm_load<D, NT>(a, b, tid, vq);
   int tile = w;  // each wave's first tile; the rest are claimed
   load_tile(tile);
   if (tid == 0) misc[0] = NW;
+  if constexpr (ROPE) {
+    if (a.q_norm) q_norm_regs<D, QPT>(a, qv, qwt);
+  }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
     const int i = tid + u * NT;
@@ -1120,11 +1214,10 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       knew[tid] = knv;
       vnew[tid] = vnv;
     }
+    if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl);
+    if (tid < D) smem[L.nw + tid] = kwv;
+    if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
     lds_barrier();
-    if (a.q_norm || (is_new && (a.k_norm || a.v_norm))) {  // uniform over the workgroup
-      step_norms<D, GH, NW>(a, qs, knew, vnew, is_new, b, w, lane);
-      lds_barrier();
-    }
     for (int i = tid; i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
       const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
@@ -1132,14 +1225,17 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       qs[g * D + j + D / 2] = x0 * sn[j] + x1 * csn[j];
     }
     if (is_new) {
+      const NewNorms nn = new_norms<D, NW>(a, smem + L.wm, smem + L.wl);
       for (int j = tid; j < D / 2; j += NT) {
-        const float k0 = knew[j], k1 = knew[j + D / 2];
+        float k0 = knew[j], k1 = knew[j + D / 2];
+        float v0 = vnew[j], v1 = vnew[j + D / 2];
+        nn.apply(a, smem + L.nw, j, D / 2, k0, k1, v0, v1);
         const float r0 = k0 * csn[j] - k1 * sn[j];
         const float r1 = k0 * sn[j] + k1 * csn[j];
         knew[j] = __uint_as_float((uint32_t)f32_to_bf16(r0) << 16);
         knew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(r1) << 16);
-        vnew[j] = __uint_as_float((uint32_t)f32_to_bf16(vnew[j]) << 16);
-        vnew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(vnew[j + D / 2]) << 16);
+        vnew[j] = __uint_as_float((uint32_t)f32_to_bf16(v0) << 16);
+        vnew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(v1) << 16);
       }
     }
   }
