@@ -189,6 +189,17 @@ int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, voi
                            const float* inv_freq, float scale, int window, int kv_dtype,
                            void* stream);
 
+/* molot_hip_prefill_step for one sequence of a paged cache (no reference
+ * counterpart): its M prompt rows go to slots slot0 .. slot0+M-1 through its
+ * block-table row block_row[max_blocks] (device int32) into pages
+ * [num_blocks][nkv][page][d]; the attention reads the same pages. */
+int molot_hip_prefill_step_paged(float* q, const float* k_new, const float* v_new, void* K,
+                                 void* V, float* O, const int32_t* block_row, int max_blocks,
+                                 int page, int nq, int nkv, int d, int M, int slot0, int pos0,
+                                 const float* q_norm, const float* k_norm, int v_norm, float eps,
+                                 const float* inv_freq, float scale, int window, int kv_dtype,
+                                 void* stream);
+
 /* Softmax exponential used by the attention kernels, applied elementwise
  * (x, y device [n]).  Counterpart of exp_avx512_ps, include/molot/norm.h:35-47,
  * exposed so its accuracy can be checked against the reference's

@@ -3,6 +3,7 @@
 ``build_all()`` compiles, in-tree:
   molot_amd/libmolot_amd.so   HIP kernels + C ABI (hipcc, gfx950)
   tests/cpp/test_attn_cpp      C++ self-check of the header-only C++ layer
+  tests/cpp/test_paged_kv      C++ self-check of the paged-KV manager
                               (include/molot_amd/attn.hpp), linked to the above
                               and to the oracle (its checker)
 The oracle (oracle/Makefile) is test infrastructure and is built by
@@ -57,22 +58,27 @@ def build_library() -> str:
     return LIB
 
 
-def build_cpp_test() -> str:
-    src = os.path.join(ROOT, "tests", "cpp", "test_attn_cpp.cpp")
+def build_cpp_test(name: str = "test_attn_cpp") -> str:
+    src = os.path.join(ROOT, "tests", "cpp", name + ".cpp")
+    out = os.path.join(ROOT, "tests", "cpp", name)
     oracle_inc = os.path.join(ROOT, "oracle")
-    tmp = CPP_TEST + ".tmp"
+    tmp = out + ".tmp"
     # rpaths relative to the binary, so the tree can move (the GPU box copies it)
     _run([_hipcc(), *HIP_FLAGS, f"-I{INCLUDE}", f"-I{oracle_inc}", src, "-o", tmp,
           f"-L{PKG}", "-lmolot_amd", f"-L{os.path.join(ROOT, 'oracle')}", "-loracle",
           "-Wl,-rpath,$ORIGIN/../../molot_amd", "-Wl,-rpath,$ORIGIN/../../oracle"])
-    os.replace(tmp, CPP_TEST)
-    return CPP_TEST
+    os.replace(tmp, out)
+    return out
+
+
+CPP_TESTS = ("test_attn_cpp", "test_paged_kv")
 
 
 def build_all() -> None:
     build_library()
-    if os.path.exists(os.path.join(ROOT, "tests", "cpp", "test_attn_cpp.cpp")):
-        build_cpp_test()
+    for name in CPP_TESTS:
+        if os.path.exists(os.path.join(ROOT, "tests", "cpp", name + ".cpp")):
+            build_cpp_test(name)
 
 
 if __name__ == "__main__":

@@ -1434,17 +1434,19 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 // max rescaling, and one division at the end (fp32 rounding differences).
 struct PfArgs {
   const float* q;  // [M][nq][D]
-  const void* k;   // [N][nkv*D] token-major cache
+  const void* k;   // token-major cache [N][nkv*D], or pages [block][nkv][page][D]
   const void* v;
   float* o;        // [M][nq][D]
+  const int32_t* block_table;  // paged: the sequence's row of block ids
   int nq, nkv, M, N, pos0, window, nqb;  // nqb: 64-row blocks per KV head
+  int page_shift;
   float scale;
 };
 
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * 64;
 
-template <int D, typename T>
+template <int D, typename T, bool PAGED>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
   constexpr int NT = kPfThreads, QB = 16 * kPfWaves;
   constexpr int KT = D == 256 ? 16 : 32;  // keys per tile (LDS under 64 KiB)
@@ -1500,7 +1502,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
   // tile loads: chunk c = tid + NT*i is key c / (D/VW), elements VW*(c % (D/VW))
   const T* Kb = reinterpret_cast<const T*>(a.k);
   const T* Vb = reinterpret_cast<const T*>(a.v);
-  const int64_t ts = (int64_t)a.nkv * D;
+  auto row_off = [&](int t) -> int64_t {  // element offset of row t of head h
+    if constexpr (PAGED) {
+      const int64_t blk = a.block_table[t >> a.page_shift];
+      const int pg = 1 << a.page_shift;
+      return (blk * a.nkv + h) * pg * D + (int64_t)(t & (pg - 1)) * D;
+    } else {
+      return (int64_t)t * a.nkv * D + (int64_t)h * D;
+    }
+  };
   typename KVT<T>::vec kreg[CPT], vreg[CPT];
   auto load_tile = [&](int tk) {
 #pragma unroll
@@ -1508,8 +1518,9 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
       const int c = tid + NT * i;
       const int key = c / (D / VW), e = VW * (c % (D / VW));
       const int t = min(tk + key, kt_hi - 1);  // rows past the range: the last one (masked)
-      kreg[i] = load16(Kb + (int64_t)t * ts + (int64_t)h * D + e);
-      vreg[i] = load16(Vb + (int64_t)t * ts + (int64_t)h * D + e);
+      const int64_t off = row_off(t) + e;
+      kreg[i] = load16(Kb + off);
+      vreg[i] = load16(Vb + off);
     }
   };
   auto store_tile = [&]() {
@@ -2535,7 +2546,7 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
 
 static int attn_prefill_impl(const float* Qm, const void* K, const void* V, float* Om, int nq,
                              int nkv, int M, int N, int d, float scale, int pos0, int window,
-                             int kv_dtype, void* stream) {
+                             int kv_dtype, const int32_t* block_row, int page, void* stream) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
@@ -2559,12 +2570,29 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   a.window = window;
   a.nqb = (int)nqb;
   a.scale = scale;
+  a.block_table = block_row;
+  if (block_row) {
+    if (page <= 0 || (page & (page - 1))) return MOLOT_EINVAL;
+    while ((1 << a.page_shift) < page) ++a.page_shift;
+  }
   using PfFn = void (*)(PfArgs);
-  PfFn pk = kv_dtype == MOLOT_KV_F32
-                ? (d == 64 ? prefill_kernel<64, float>
-                           : d == 128 ? prefill_kernel<128, float> : prefill_kernel<256, float>)
-                : (d == 64 ? prefill_kernel<64, bf16_t>
-                           : d == 128 ? prefill_kernel<128, bf16_t> : prefill_kernel<256, bf16_t>);
+  PfFn pk;
+  if (!block_row)
+    pk = kv_dtype == MOLOT_KV_F32
+             ? (d == 64 ? prefill_kernel<64, float, false>
+                        : d == 128 ? prefill_kernel<128, float, false>
+                                   : prefill_kernel<256, float, false>)
+             : (d == 64 ? prefill_kernel<64, bf16_t, false>
+                        : d == 128 ? prefill_kernel<128, bf16_t, false>
+                                   : prefill_kernel<256, bf16_t, false>);
+  else
+    pk = kv_dtype == MOLOT_KV_F32
+             ? (d == 64 ? prefill_kernel<64, float, true>
+                        : d == 128 ? prefill_kernel<128, float, true>
+                                   : prefill_kernel<256, float, true>)
+             : (d == 64 ? prefill_kernel<64, bf16_t, true>
+                        : d == 128 ? prefill_kernel<128, bf16_t, true>
+                                   : prefill_kernel<256, bf16_t, true>);
   const dim3 grid((unsigned)(nqb * nkv));
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {
@@ -2581,14 +2609,14 @@ int molot_hip_attn_prefill_gqa(const float* Qm, const void* K, const void* V, fl
                                int nkv, int M, int N, int d, float scale, int pos0, int window,
                                int kv_dtype, void* stream) {
   return attn_prefill_impl(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window, kv_dtype,
-                           stream);
+                           nullptr, 0, stream);
 }
 
-int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
-                           float* O, int nq, int nkv, int d, int M, int slot0, int pos0,
-                           const float* q_norm, const float* k_norm, int v_norm, float eps,
-                           const float* inv_freq, float scale, int window, int kv_dtype,
-                           void* stream) {
+static int prefill_step_impl(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                             float* O, int nq, int nkv, int d, int M, int slot0, int pos0,
+                             const float* q_norm, const float* k_norm, int v_norm, float eps,
+                             const float* inv_freq, float scale, int window, int kv_dtype,
+                             const int32_t* block_row, int page, int max_blocks, void* stream) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   Norms nm;
@@ -2600,6 +2628,9 @@ int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, voi
   if (M == 0) return 0;
   if (!q || !k_new || !v_new || !K || !V || !O || !inv_freq) return MOLOT_EINVAL;
   if ((int64_t)M > 65535) return MOLOT_ENOTSUP;  // one grid row per token
+  if (block_row && ((int64_t)slot0 + M > (int64_t)max_blocks * page || page <= 0 ||
+                    (page & (page - 1))))
+    return MOLOT_EINVAL;
   RopeArgs r{};
   r.q = q;
   r.k_new = k_new;
@@ -2607,8 +2638,17 @@ int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, voi
   r.K = K;
   r.V = V;
   r.inv_freq = inv_freq;
-  r.tok_stride = (int64_t)nkv * d;
-  r.head_stride = d;
+  if (block_row) {  // every token of the one sequence through its block-table row
+    r.block_table = block_row;
+    r.max_blocks = 0;
+    r.page = page;
+    r.tok_stride = d;
+    r.head_stride = (int64_t)page * d;
+    r.block_stride = (int64_t)nkv * page * d;
+  } else {
+    r.tok_stride = (int64_t)nkv * d;
+    r.head_stride = d;
+  }
   r.nq = nq;
   r.nkv = nkv;
   r.d = d;
@@ -2626,7 +2666,28 @@ int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, voi
   st = (int)hipGetLastError();
   if (st) return st;
   return attn_prefill_impl(q, K, V, O, nq, nkv, M, slot0 + M, d, scale, pos0, window, kv_dtype,
-                           stream);
+                           block_row, page, stream);
+}
+
+int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
+                           float* O, int nq, int nkv, int d, int M, int slot0, int pos0,
+                           const float* q_norm, const float* k_norm, int v_norm, float eps,
+                           const float* inv_freq, float scale, int window, int kv_dtype,
+                           void* stream) {
+  return prefill_step_impl(q, k_new, v_new, K, V, O, nq, nkv, d, M, slot0, pos0, q_norm, k_norm,
+                           v_norm, eps, inv_freq, scale, window, kv_dtype, nullptr, 0, 0, stream);
+}
+
+int molot_hip_prefill_step_paged(float* q, const float* k_new, const float* v_new, void* K,
+                                 void* V, float* O, const int32_t* block_row, int max_blocks,
+                                 int page, int nq, int nkv, int d, int M, int slot0, int pos0,
+                                 const float* q_norm, const float* k_norm, int v_norm, float eps,
+                                 const float* inv_freq, float scale, int window, int kv_dtype,
+                                 void* stream) {
+  if (!block_row || max_blocks <= 0) return MOLOT_EINVAL;
+  return prefill_step_impl(q, k_new, v_new, K, V, O, nq, nkv, d, M, slot0, pos0, q_norm, k_norm,
+                           v_norm, eps, inv_freq, scale, window, kv_dtype, block_row, page,
+                           max_blocks, stream);
 }
 
 int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream) {

@@ -55,6 +55,8 @@ _SIGS = {
     "molot_hip_attn_prefill_gqa": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P],
     "molot_hip_prefill_step": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P,
                                _F, _I, _I, _P],
+    "molot_hip_prefill_step_paged": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                                     _P, _P, _I, _F, _P, _F, _I, _I, _P],
     "molot_hip_last_plan": [ctypes.POINTER(_I), ctypes.POINTER(_I)],
     "molot_hip_profile_begin": [_I],
     "molot_hip_profile_end": [ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_I),

@@ -13,6 +13,7 @@ extern "C" {
 #define ORC_KV_BF16 1
 
 uint16_t orc_f32_to_bf16(float f);
+void orc_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n);
 void orc_rope_inv_freq(float base, int d, float* out);
 void orc_rope_apply(float* x, int d, int pos, const float* inv_freq);
 void orc_rope_apply_heads(float* x, int nheads, int d, int pos, const float* inv_freq);

@@ -1,11 +1,14 @@
-"""The header-only C++ layer (include/molot_amd/attn.hpp) on the GPU: runs the
-self-checking binary tests/cpp/test_attn_cpp (built by __graft_entry__.build())."""
+"""The header-only C++ layer (include/molot_amd/attn.hpp, paged_kv.hpp) on the
+GPU: runs the self-checking binaries tests/cpp/test_attn_cpp and
+tests/cpp/test_paged_kv (built by __graft_entry__.build())."""
 import os
 import subprocess
 
 import pytest
 
-BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "test_attn_cpp")
+HERE = os.path.dirname(os.path.abspath(__file__))
+BIN = os.path.join(HERE, "cpp", "test_attn_cpp")
+BIN_PAGED = os.path.join(HERE, "cpp", "test_paged_kv")
 
 
 @pytest.mark.gpu
@@ -23,5 +26,25 @@ def test_cpp_layer_binary_links():
     if not os.path.exists(BIN):
         pytest.skip("C++ self-check not built in this tree")
     out = subprocess.run(["ldd", BIN], capture_output=True, text=True).stdout
+    assert "not found" not in out, out
+    assert "libmolot_amd.so" in out and "liboracle.so" in out
+
+
+@pytest.mark.gpu
+def test_paged_kv_manager_selfcheck(gpu):
+    """Continuous batching through PagedKVCache: prefill, batched decode over
+    two layers, a freed sequence's blocks reused, a full pool's error."""
+    if not os.path.exists(BIN_PAGED):
+        pytest.fail(f"{BIN_PAGED} not built (run __graft_entry__.build())")
+    r = subprocess.run([BIN_PAGED], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "PASSED" in r.stdout
+
+
+def test_paged_kv_binary_links():
+    if not os.path.exists(BIN_PAGED):
+        pytest.skip("paged-KV self-check not built in this tree")
+    out = subprocess.run(["ldd", BIN_PAGED], capture_output=True, text=True).stdout
     assert "not found" not in out, out
     assert "libmolot_amd.so" in out and "liboracle.so" in out
