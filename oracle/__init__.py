@@ -26,6 +26,7 @@ REF_SO = os.path.join(_HERE, "_ref", "libmolot_ref.so")
 
 KV_F32 = 0
 KV_BF16 = 1
+KV_Q8 = 2
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -65,6 +66,10 @@ def lib() -> ctypes.CDLL:
             "orc_attn_decode_f64": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _D, _I, _I, _I, _I64,
                                            _I64, _I64, _P, _I, _I]),
             "orc_rmsnorm": (None, [_P, _P, _P, _I, _F]),
+            "orc_q8_row_bytes": (_I, [_I, _I]),
+            "orc_q8_block_bytes": (_I64, [_I, _I, _I]),
+            "orc_quantize_q8_row": (None, [_P, _I, _P, _P]),
+            "orc_q8_store_token": (None, [_P, _I64, _P, _I, _I]),
             "orc_attn_prefill": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _I]),
             "orc_decode_step_norm": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P,
                                             _I, _F, _P, _F, _I, _I, _I]),
@@ -118,6 +123,7 @@ def ref() -> ctypes.CDLL:
                                             _P]),
             "ref_prefill_step": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P,
                                       _I, _F, _P, _F, _I, _P]),
+            "ref_quantize_q8_row": (None, [_P, _I, _P, _P]),
             "ref_rmsnorm": (None, [_P, _P, _P, _I, _F]),
             "ref_rmsnorm_plain": (None, [_P, _P, _I, _F]),
             "ref_decode_step_norm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P,
@@ -197,7 +203,9 @@ def _kv_code(K: np.ndarray) -> int:
         return KV_F32
     if K.dtype == np.uint16:
         return KV_BF16
-    raise TypeError(f"KV dtype {K.dtype}: float32 or uint16 (bf16 bits)")
+    if K.dtype == np.uint8:
+        return KV_Q8
+    raise TypeError(f"KV dtype {K.dtype}: float32, uint16 (bf16 bits) or uint8 (Q8 bytes)")
 
 
 def attn_decode(Q, K, V, nq, nkv, n, d, scale, pos_cur, window, tok_stride, head_stride,
@@ -331,3 +339,37 @@ def prefill_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, M, slot0, pos0, q_norm, k_
             Vc[slot0 + m] = v[m].reshape(-1)
     O = attn_prefill(q, Kc, Vc, nq, nkv, M, slot0 + M, d, scale, pos0, window, nthreads)
     return q, O
+
+
+# ---------------------------------------------------------------------------
+# Q8 KV cache (this build's format; see attn_oracle.c): token-major rows of
+# [nkv][d] int8 then nkv fp32 scales padded to 16 bytes, as uint8 arrays.
+
+def q8_row_bytes(nkv: int, d: int) -> int:
+    return int(lib().orc_q8_row_bytes(nkv, d))
+
+
+def quantize_q8_row(x: np.ndarray):
+    """quantize_q8_row (quant.h:34-50) of one row: (scale, int8 values)."""
+    x = _f32(x)
+    q = np.empty(x.size, np.int8)
+    s = np.empty(1, np.float32)
+    lib().orc_quantize_q8_row(_p(x), x.size, _p(q), _p(s))
+    return float(s[0]), q
+
+
+def q8_cache(X: np.ndarray, nkv: int, d: int) -> np.ndarray:
+    """A token-major Q8 cache [N][row bytes] from fp32 rows X [N][nkv*d]."""
+    X = _f32(X)
+    N = X.shape[0]
+    out = np.zeros((N, q8_row_bytes(nkv, d)), np.uint8)
+    for t in range(N):
+        lib().orc_q8_store_token(_p(out), t, _p(X[t]), nkv, d)
+    return out
+
+
+def q8_dequant(C: np.ndarray, nkv: int, d: int) -> np.ndarray:
+    """fp32 [N][nkv*d] of a token-major Q8 cache."""
+    q = C[:, :nkv * d].view(np.int8).astype(np.float32).reshape(C.shape[0], nkv, d)
+    s = C[:, nkv * d:nkv * d + 4 * nkv].copy().view(np.float32).reshape(C.shape[0], nkv, 1)
+    return (q * s).reshape(C.shape[0], nkv * d)

@@ -22,6 +22,9 @@
  *                              append, attention)
  *       orc_attn_prefill    <- include/molot/gemm.h:409-446 (causal prefill:
  *                              scalar expf, double denominator)
+ *       orc_quantize_q8_row <- include/molot/quant.h:34-50 (quantize_q8_row), the
+ *                              row quantizer of this build's Q8 KV cache
+ *                              (kv_dtype ORC_KV_Q8, see below)
  *       orc_rmsnorm         <- include/molot/norm.h:9-28 (weights) and
  *                              :82-96 (w == NULL: rmsnorm_plain)
  *       orc_decode_step_norm <- include/molot/forward.h:554-591 with the
@@ -169,7 +172,64 @@ typedef struct {
   int64_t tok_stride, head_stride, block_stride;
   const int32_t* block_table; /* NULL => contiguous */
   int page;
+  int nkv, d; /* Q8: scale addressing */
 } orc_kv_t;
+
+/* ------------------------------------------------------------------ */
+/* Q8 KV cache (ORC_KV_Q8).  The reference planned an int8 KV cache
+ * (its DESIGN.md:48, exp/README.md:36-39 "kv_q8, deferred") but never fixed
+ * a format; this build's is its own Q8_0 row quantizer applied per KV head
+ * row: orc_quantize_q8_row.  Byte layouts:
+ *   token-major: row t = [nkv][d] int8, then nkv fp32 scales, padded to 16
+ *                bytes: orc_q8_row_bytes(nkv, d) bytes per token;
+ *   paged:       block = [nkv][page][d] int8, then [nkv][page] fp32 scales:
+ *                orc_q8_block_bytes(nkv, d, page) bytes per block.
+ * A row dequantizes as q_i * s. */
+int orc_q8_row_bytes(int nkv, int d) { return nkv * d + ((4 * nkv + 15) & ~15); }
+int64_t orc_q8_block_bytes(int nkv, int d, int page) {
+  return (int64_t)nkv * page * d + (int64_t)4 * nkv * page;
+}
+
+/* quantize_q8_row (quant.h:34-50) on one row of d values: s = absmax/127
+ * (1 when that is not > 0), q_i = clamp(nearbyint(x_i / s), -127, 127). */
+void orc_quantize_q8_row(const float* x, int d, int8_t* q, float* s) {
+  float amax = 0;
+  for (int i = 0; i < d; ++i) amax = amax > fabsf(x[i]) ? amax : fabsf(x[i]);
+  float sc = amax / 127.0f;
+  if (!(sc > 0)) sc = 1.0f;
+  *s = sc;
+  for (int i = 0; i < d; ++i) {
+    int v = (int)nearbyintf(x[i] / sc);
+    q[i] = (int8_t)(v > 127 ? 127 : (v < -127 ? -127 : v));
+  }
+}
+
+/* Token t of a token-major Q8 cache from its nkv rows x [nkv][d]. */
+void orc_q8_store_token(void* base, int64_t t, const float* x, int nkv, int d) {
+  uint8_t* row = (uint8_t*)base + t * orc_q8_row_bytes(nkv, d);
+  for (int h = 0; h < nkv; ++h)
+    orc_quantize_q8_row(x + (size_t)h * d, d, (int8_t*)row + (size_t)h * d,
+                        (float*)(row + (size_t)nkv * d) + h);
+}
+
+/* The strides of a Q8 cache are its byte layout's (the callers' element
+ * strides describe fp32/bf16 layouts); head-major Q8 is not a layout here. */
+static orc_kv_t orc_kv_make(const void* K, const void* V, int kv_dtype, int64_t tok,
+                            int64_t head, int64_t block, const int32_t* bt, int page, int nkv,
+                            int d) {
+  orc_kv_t kv = {K, V, kv_dtype, tok, head, block, bt, page, nkv, d};
+  if (kv_dtype == ORC_KV_Q8) {
+    if (bt) {
+      kv.tok_stride = d;
+      kv.head_stride = (int64_t)page * d;
+      kv.block_stride = orc_q8_block_bytes(nkv, d, page);
+    } else {
+      kv.tok_stride = orc_q8_row_bytes(nkv, d);
+      kv.head_stride = d;
+    }
+  }
+  return kv;
+}
 
 static inline int64_t orc_row_off(const orc_kv_t* kv, int h, int t) {
   if (!kv->block_table) return (int64_t)t * kv->tok_stride + (int64_t)h * kv->head_stride;
@@ -184,6 +244,21 @@ static inline const float* orc_row(const orc_kv_t* kv, int which, int h, int t, 
   const void* base = which ? kv->v : kv->k;
   int64_t off = orc_row_off(kv, h, t);
   if (kv->kv_dtype == ORC_KV_F32) return (const float*)base + off;
+  if (kv->kv_dtype == ORC_KV_Q8) {
+    const int8_t* p = (const int8_t*)base + off;
+    int64_t soff;
+    if (kv->block_table) {
+      const int64_t b = kv->block_table[t / kv->page];
+      soff = b * kv->block_stride + (int64_t)kv->nkv * kv->page * kv->d +
+             4 * ((int64_t)h * kv->page + t % kv->page);
+    } else {
+      soff = (int64_t)t * kv->tok_stride + (int64_t)kv->nkv * kv->d + 4 * (int64_t)h;
+    }
+    float sc;
+    memcpy(&sc, (const uint8_t*)base + soff, 4);
+    for (int j = 0; j < d; ++j) dst[j] = (float)p[j] * sc;
+    return dst;
+  }
   const uint16_t* p = (const uint16_t*)base + off;
   for (int j = 0; j < d; ++j) dst[j] = orc_bf16_to_f32(p[j]);
   return dst;
@@ -243,7 +318,8 @@ void orc_attn_decode(const float* Q, const void* K, const void* V, float* O, int
                      int n, int d, float scale, int pos_cur, int window, int kv_dtype,
                      int64_t tok_stride, int64_t head_stride, int64_t block_stride,
                      const int32_t* block_table, int page, int nthreads) {
-  orc_kv_t kv = {K, V, kv_dtype, tok_stride, head_stride, block_stride, block_table, page};
+  const orc_kv_t kv = orc_kv_make(K, V, kv_dtype, tok_stride, head_stride, block_stride,
+                                  block_table, page, nkv, d);
   int groups = nq / nkv;
   int t0 = orc_t0(pos_cur, window);
   int nt = orc_threads(nthreads);
@@ -298,6 +374,9 @@ void orc_decode_step(float* q, float* k_new, const float* v_new, void* Kc, void*
   if (kv_dtype == ORC_KV_F32) {
     memcpy((float*)Kc + (size_t)slot * S, k_new, S * 4);
     memcpy((float*)Vc + (size_t)slot * S, v_new, S * 4);
+  } else if (kv_dtype == ORC_KV_Q8) {
+    orc_q8_store_token(Kc, slot, k_new, nkv, d);
+    orc_q8_store_token(Vc, slot, v_new, nkv, d);
   } else {
     orc_f32_to_bf16_array(k_new, (uint16_t*)Kc + (size_t)slot * S, (int64_t)S);
     orc_f32_to_bf16_array(v_new, (uint16_t*)Vc + (size_t)slot * S, (int64_t)S);
@@ -342,7 +421,7 @@ void orc_decode_step_norm(float* q, float* k_new, const float* v_new, void* Kc, 
 void orc_attn_prefill(const float* Qm, const void* K, const void* V, float* Om, int nq, int nkv,
                       int M, int N, int d, float scale, int pos0, int window, int kv_dtype,
                       int nthreads) {
-  const orc_kv_t kv = {K, V, kv_dtype, (int64_t)nkv * d, d, 0, NULL, 0};
+  const orc_kv_t kv = orc_kv_make(K, V, kv_dtype, (int64_t)nkv * d, d, 0, NULL, 0, nkv, d);
   const int G = nq / nkv;
 #ifdef _OPENMP
   if (nthreads > 0) omp_set_num_threads(nthreads);
@@ -395,7 +474,8 @@ void orc_attn_decode_f64(const float* Q, const void* K, const void* V, double* O
                          int kv_dtype, int64_t tok_stride, int64_t head_stride,
                          int64_t block_stride, const int32_t* block_table, int page,
                          int nthreads) {
-  orc_kv_t kv = {K, V, kv_dtype, tok_stride, head_stride, block_stride, block_table, page};
+  const orc_kv_t kv = orc_kv_make(K, V, kv_dtype, tok_stride, head_stride, block_stride,
+                                  block_table, page, nkv, d);
   int groups = nq / nkv;
   int t0 = orc_t0(pos_cur, window);
   int nt = orc_threads(nthreads);

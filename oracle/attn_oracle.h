@@ -11,6 +11,7 @@ extern "C" {
 
 #define ORC_KV_F32 0
 #define ORC_KV_BF16 1
+#define ORC_KV_Q8 2
 
 uint16_t orc_f32_to_bf16(float f);
 void orc_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n);
@@ -20,6 +21,10 @@ void orc_rope_apply_heads(float* x, int nheads, int d, int pos, const float* inv
 void orc_vexp16(const float* in, float* out);
 float orc_dot(const float* a, const float* b, int n);
 void orc_rmsnorm(const float* x, const float* w, float* y, int n, float eps);
+int orc_q8_row_bytes(int nkv, int d);
+int64_t orc_q8_block_bytes(int nkv, int d, int page);
+void orc_quantize_q8_row(const float* x, int d, int8_t* q, float* s);
+void orc_q8_store_token(void* base, int64_t t, const float* x, int nkv, int d);
 void orc_attn_decode(const float* Q, const void* K, const void* V, float* O, int nq, int nkv,
                      int n, int d, float scale, int pos_cur, int window, int kv_dtype,
                      int64_t tok_stride, int64_t head_stride, int64_t block_stride,

@@ -128,6 +128,15 @@ int ref_prefill_step(float* Q, float* Kn, float* Vn, float* Kc, float* Vc, float
   return 0;
 }
 
+// quantize_q8_row (quant.h:34-50) on one row: scale, int8 values, and the
+// per-32 block sums it also writes (ignored by the KV format).
+void ref_quantize_q8_row(const float* x, int cols, float* scale, int8_t* q) {
+  const int nblocks = (cols + 31) / 32;
+  int32_t bsums[64];
+  if (nblocks > 64) return;
+  molot::quantize_q8_row(x, cols, nblocks, scale, q, bsums);
+}
+
 void ref_rmsnorm(const float* x, const float* w, float* y, int n, float eps) {
   molot::rmsnorm(x, w, y, n, eps);
 }

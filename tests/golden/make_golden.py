@@ -143,6 +143,26 @@ def gen_prefill(name, nq, nkv, d, M, n0, base, window, scale, eps, norms, seed, 
           seed=seed)
 
 
+def gen_q8_rows(name, d, seed):
+    """quantize_q8_row (quant.h:34-50) through the reference on rows that
+    probe its edges: Gaussian rows of two scales, an all-zero row (scale 1),
+    rows of exact half-steps (ties of nearbyint), tiny values, and a row
+    whose absmax element sits at +-127 exactly."""
+    R = oracle.ref()
+    st = Stream(seed)
+    rows = [st.normal((d,), 1.0), st.normal((d,), 3.0), np.zeros(d, np.float32)]
+    s = np.float32(0.5)
+    ties = (np.arange(d, dtype=np.float32) - d / 2 + np.float32(0.5)) * s
+    ties[0] = np.float32(127.0) * s  # fixes the scale at 0.5: every x/s is k + 0.5
+    rows += [ties, -ties, st.normal((d,), 1e-30), st.normal((d,), 1e-3)]
+    X = np.stack([r.astype(np.float32) for r in rows])
+    S = np.empty(len(rows), np.float32)
+    Q = np.empty((len(rows), d), np.int8)
+    for i in range(len(rows)):
+        R.ref_quantize_q8_row(P(X[i]), d, P(S[i:i + 1]), P(Q[i]))
+    _save(name, X=X, S=S, Q=Q, d=d, seed=seed)
+
+
 def gen_head(name, n, d, sigma, seed):
     """attn_decode_head (attn.h:104-107), the bench/bench.cc:186-218 check shape."""
     R = oracle.ref()
@@ -276,6 +296,8 @@ def main() -> None:
         gen_rope("rope_d256_theta1e4", 256, 10000.0, [0, 3, 1023, 32768], seed=18)
     if want("vexp_points"):
         gen_vexp("vexp_points", seed=19)
+    if want("q8_rows_d128"):
+        gen_q8_rows("q8_rows_d128", 128, seed=25)
     if want("rmsnorm_cases"):
         gen_rmsnorm("rmsnorm_cases", [7, 16, 100, 128, 256, 1024], seed=22)
 

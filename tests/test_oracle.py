@@ -380,6 +380,66 @@ def test_planted_non_causal_prefill_is_caught():
     assert normwise_err(full, R) > 1e-2
 
 
+# ---------------------------------------------------------------------------
+# Q8 KV cache: quantize_q8_row (quant.h:34-50) per KV head row
+
+def test_q8_quantizer_golden():
+    """Bit-exact against the compiled reference on its edge cases (zero row,
+    exact half-step ties, tiny values, the absmax element at +-127)."""
+    g = golden("q8_rows_d128")
+    for i in range(g["X"].shape[0]):
+        s, q = oracle.quantize_q8_row(g["X"][i])
+        assert s == g["S"][i], i
+        np.testing.assert_array_equal(q, g["Q"][i])
+
+
+def test_q8_quantizer_bounds():
+    st = Stream(38)
+    for sigma in (1.0, 5.0, 1e-4):
+        x = st.normal((128,), sigma)
+        s, q = oracle.quantize_q8_row(x)
+        assert s == np.float32(np.abs(x).max()) / np.float32(127.0)
+        assert np.abs(q.astype(np.int32)).max() == 127
+        # round-off at most half a step (division and product rounding aside)
+        assert np.max(np.abs(x - q.astype(np.float32) * np.float32(s))) <= 0.5 * s * (1 + 1e-5)
+    # values already on the grid come back exactly
+    k = np.arange(-127, 129, 2, dtype=np.float32)[:128]
+    s, q = oracle.quantize_q8_row(k * np.float32(0.25))
+    assert s == 0.25
+    np.testing.assert_array_equal(q, k.astype(np.int8))
+
+
+def test_q8_attention_is_attention_on_dequantized_rows():
+    """The Q8 cache read through its byte layout (rows, then per-head scales)
+    gives bit for bit the attention over its dequantized fp32 rows: pins the
+    scale addressing, which a wrong offset would break."""
+    st = Stream(39)
+    nq, nkv, d, n = 16, 4, 128, 301
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d, 2.0)
+    Kq, Vq = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
+    assert Kq.shape == (n, nkv * d + 16)
+    Kd, Vd = oracle.q8_dequant(Kq, nkv, d), oracle.q8_dequant(Vq, nkv, d)
+    for window in (0, 77):
+        a = oracle.attn_decode_gqa_cache(Q, Kq, Vq, nq, nkv, n, d, 0.088, n - 1, window)
+        b = oracle.attn_decode_gqa_cache(Q, Kd, Vd, nq, nkv, n, d, 0.088, n - 1, window)
+        np.testing.assert_array_equal(a, b)
+    # and the quantization error of the cache is the 8-bit one
+    assert np.max(np.abs(Kd - K)) <= np.abs(K).max() / 127 * 0.51
+
+
+def test_q8_decode_step_appends_quantized_row():
+    st = Stream(40)
+    nq, nkv, d, pos = 8, 2, 64, 90
+    q, k, v = st.normal((nq, d)), st.normal((nkv, d)), st.normal((nkv, d))
+    K, V = kv_token_major(st, pos + 1, nkv, d)
+    Kq, Vq = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
+    inv = oracle.rope_inv_freq(10000.0, d)
+    _, k_rot, O = oracle.decode_step(q, k, v, Kq, Vq, nq, nkv, d, pos, pos, inv, 0.125, 0)
+    np.testing.assert_array_equal(Kq[pos], oracle.q8_cache(k_rot.reshape(1, -1), nkv, d)[0])
+    np.testing.assert_array_equal(Vq[pos], oracle.q8_cache(v.reshape(1, -1), nkv, d)[0])
+
+
 def test_head_golden():
     g = golden("head_bench_check")
     n, d = int(g["n"]), int(g["d"])
