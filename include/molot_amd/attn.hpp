@@ -159,7 +159,10 @@ class DeviceKV {
 
   DeviceKV(int cap_, int nkv_, int hd_, int kv_dtype_ = MOLOT_KV_F32)
       : cap(cap_), nkv(nkv_), hd(hd_), kv_dtype(kv_dtype_) {
-    const size_t bytes = (size_t)cap * nkv * hd * (kv_dtype == MOLOT_KV_F32 ? 4 : 2);
+    const size_t bytes =
+        kv_dtype == MOLOT_KV_Q8
+            ? (size_t)cap * (size_t)molot_hip_q8_row_bytes(nkv, hd)
+            : (size_t)cap * nkv * hd * (kv_dtype == MOLOT_KV_F32 ? 4 : 2);
     check_hip(hipMalloc(&k, bytes), "hipMalloc K");
     check_hip(hipMalloc(&v, bytes), "hipMalloc V");
     check_hip(hipMemset(k, 0, bytes), "hipMemset K");

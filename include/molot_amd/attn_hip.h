@@ -34,6 +34,22 @@ extern "C" {
 /* KV element types. */
 #define MOLOT_KV_F32 0
 #define MOLOT_KV_BF16 1 /* RNE-rounded as include/molot/quant.h:192-198 */
+/* Q8: each KV head row of d values is quantized as quantize_q8_row
+ * (include/molot/quant.h:34-50): fp32 scale s = absmax/127 (1 when not > 0),
+ * int8 codes clamp(nearbyint(x/s), -127, 127); it dequantizes as code * s.
+ * The reference plans an int8 KV cache (DESIGN.md:48, exp/README.md:36-39)
+ * without fixing a layout; this library's layouts, in bytes:
+ *   token-major  row t = [nkv][d] codes, then nkv fp32 scales, padded to 16
+ *                bytes: molot_hip_q8_row_bytes(nkv, d) bytes per token;
+ *   paged        block = [nkv][page][d] codes, then [nkv][page] fp32 scales:
+ *                molot_hip_q8_block_bytes(nkv, d, page) bytes per block.
+ * Q8 runs on head dims 64 and 128 (MOLOT_ENOTSUP otherwise); the head-major
+ * entry points take no Q8 cache (MOLOT_EINVAL). */
+#define MOLOT_KV_Q8 2
+
+/* Bytes of one token of a token-major Q8 cache, and of one paged Q8 block. */
+int molot_hip_q8_row_bytes(int nkv, int d);
+int64_t molot_hip_q8_block_bytes(int nkv, int d, int page);
 
 /* Status codes besides hipError_t values (which are positive). */
 #define MOLOT_OK 0
@@ -98,7 +114,9 @@ int molot_hip_attn_decode_head_win(const float* Q, const void* K, const void* V,
                                    int kv_dtype, void* stream);
 
 /* General strided form behind all of the above: row t of KV head h at
- * element offset t*tok_stride + h*head_stride. */
+ * element offset t*tok_stride + h*head_stride.  Q8: the token-major Q8
+ * layout only, tok_stride = molot_hip_q8_row_bytes(nkv, d) and
+ * head_stride = d (bytes). */
 int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, float* O, int nq,
                                   int nkv, int n, int d, int64_t tok_stride, int64_t head_stride,
                                   float scale, int pos_cur, int window, int kv_dtype,

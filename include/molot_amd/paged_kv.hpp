@@ -7,7 +7,8 @@
 // Runner per chat); its design notes plan vLLM-style 16-token pages
 // (DESIGN.md:47-48) and its README lists them as not implemented
 // (README.md:112-114).  This class is that caller side:
-//   * one pool of pages per layer, [num_blocks][nkv][page][hd], all layers
+//   * one pool of pages per layer, [num_blocks][nkv][page][hd] (a Q8 pool:
+//     MOLOT_KV_Q8 blocks of molot_hip_q8_block_bytes each), all layers
 //     sharing one block allocator, so a sequence's block ids are the same in
 //     every layer;
 //   * sequences are added and freed at any time (continuous batching); a
@@ -43,7 +44,9 @@ class PagedKVCache {
         (page & (page - 1)))
       throw std::runtime_error("PagedKVCache: bad geometry");
     const size_t esz = kv_dtype == MOLOT_KV_F32 ? 4 : 2;
-    pool_bytes_ = (size_t)num_blocks * nkv * page * hd * esz;
+    pool_bytes_ = kv_dtype == MOLOT_KV_Q8
+                      ? (size_t)num_blocks * (size_t)molot_hip_q8_block_bytes(nkv, hd, page)
+                      : (size_t)num_blocks * nkv * page * hd * esz;
     k_.assign(layers, nullptr);
     v_.assign(layers, nullptr);
     for (int l = 0; l < layers; ++l) {

@@ -17,10 +17,10 @@ import math
 import torch
 
 from . import lib as _lib
-from .lib import KV_BF16, KV_F32, check
+from .lib import KV_BF16, KV_F32, KV_Q8, check
 
 __all__ = [
-    "KV_F32", "KV_BF16", "rope_inv_freq", "rope_apply", "rope_append", "attn_decode_gqa_cache",
+    "KV_F32", "KV_BF16", "KV_Q8", "q8_row_bytes", "q8_block_bytes", "rope_inv_freq", "rope_apply", "rope_append", "attn_decode_gqa_cache",
     "attn_decode_gqa", "attn_decode_gqa_win", "attn_decode_head", "attn_decode_head_win",
     "attn_decode_strided", "decode_step", "attn_decode_paged", "decode_step_paged",
     "rope_append_paged", "vexp",
@@ -50,15 +50,38 @@ def _need(t: torch.Tensor, name: str, dtype=None, min_numel: int = 0) -> None:
 
 
 def kv_dtype_of(t: torch.Tensor) -> int:
-    """KV element code of a cache tensor (fp32, or bf16 stored as bf16/int16 bits)."""
+    """KV element code of a cache tensor: fp32, bf16 (as bf16/int16 bits), or
+    Q8 (uint8/int8 bytes of the Q8 layouts, include/molot_amd/attn_hip.h)."""
     if t.dtype == torch.float32:
         return KV_F32
     if t.dtype in (torch.bfloat16, torch.int16, torch.uint16):
         return KV_BF16
-    raise TypeError(f"KV cache dtype {t.dtype} not supported (float32 or bfloat16)")
+    if t.dtype in (torch.uint8, torch.int8):
+        return KV_Q8
+    raise TypeError(f"KV cache dtype {t.dtype} not supported (float32, bfloat16 or Q8 bytes)")
 
 
-_KV_DTYPES = (torch.float32, torch.bfloat16, torch.int16, torch.uint16)
+_KV_DTYPES = (torch.float32, torch.bfloat16, torch.int16, torch.uint16, torch.uint8, torch.int8)
+
+
+def q8_row_bytes(nkv: int, d: int) -> int:
+    """Bytes per token of a token-major Q8 cache (codes, then padded scales)."""
+    return int(_lib.load().molot_hip_q8_row_bytes(int(nkv), int(d)))
+
+
+def q8_block_bytes(nkv: int, d: int, page: int) -> int:
+    """Bytes per block of a paged Q8 cache."""
+    return int(_lib.load().molot_hip_q8_block_bytes(int(nkv), int(d), int(page)))
+
+
+def _row_units(kvd: int, nkv: int, d: int) -> int:
+    """Tensor elements per token of a token-major cache."""
+    return q8_row_bytes(nkv, d) if kvd == KV_Q8 else nkv * d
+
+
+def _block_units(kvd: int, nkv: int, d: int, page: int) -> int:
+    """Tensor elements per block of a paged cache."""
+    return q8_block_bytes(nkv, d, page) if kvd == KV_Q8 else nkv * page * d
 
 
 def rope_inv_freq(base: float, d: int) -> torch.Tensor:
@@ -82,14 +105,15 @@ def rope_apply(x: torch.Tensor, pos: int, inv_freq: torch.Tensor) -> torch.Tenso
 def rope_append(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq, cap=None):
     """RoPE q (in place) and k_new, append k/v at `slot` (forward.h:556-575)."""
     kvd = kv_dtype_of(K)
-    cap = K.numel() // (nkv * d) if cap is None else cap
+    row = _row_units(kvd, nkv, d)
+    cap = K.numel() // row if cap is None else cap
     if slot < 0 or slot >= cap:
         raise RuntimeError("fwd: KV cache full")  # forward.h:570
     _need(q, "q", torch.float32, nq * d)
     _need(k_new, "k_new", torch.float32, nkv * d)
     _need(v_new, "v_new", torch.float32, nkv * d)
-    _need(K, "K", _KV_DTYPES, (slot + 1) * nkv * d)
-    _need(V, "V", K.dtype, (slot + 1) * nkv * d)
+    _need(K, "K", _KV_DTYPES, (slot + 1) * row)
+    _need(V, "V", K.dtype, (slot + 1) * row)
     _need(inv_freq, "inv_freq", torch.float32, d // 2)
     check(_lib.load().molot_hip_rope_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V),
                                             nq, nkv, d, int(slot), int(pos), _ptr(inv_freq), kvd,
@@ -98,12 +122,15 @@ def rope_append(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq, cap=None
 
 def attn_decode_strided(Q, K, V, O, nq, nkv, n, d, tok_stride, head_stride, scale, pos_cur,
                         window):
-    """Attention with row t of KV head h at t*tok_stride + h*head_stride."""
+    """Attention with row t of KV head h at t*tok_stride + h*head_stride
+    (Q8: the token-major byte layout, tok_stride = q8_row_bytes(nkv, d))."""
     kvd = kv_dtype_of(K)
     _need(Q, "Q", torch.float32, nq * d)
     _need(O, "O", torch.float32, nq * d)
     if n > 0:
         span = (n - 1) * tok_stride + (nkv - 1) * head_stride + d
+        if kvd == KV_Q8:
+            span = n * tok_stride  # the row's scales end it
         _need(K, "K", _KV_DTYPES, span)
         _need(V, "V", K.dtype, span)
     check(_lib.load().molot_hip_attn_decode_strided(
@@ -114,8 +141,8 @@ def attn_decode_strided(Q, K, V, O, nq, nkv, n, d, tok_stride, head_stride, scal
 
 def attn_decode_gqa_cache(Q, K, V, O, nq, nkv, n, qhd, scale, pos_cur, window):
     """GQA decode over the token-major cache [n][nkv*qhd] (attn.h:125-177)."""
-    return attn_decode_strided(Q, K, V, O, nq, nkv, n, qhd, nkv * qhd, qhd, scale, pos_cur,
-                               window)
+    row = _row_units(kv_dtype_of(K), nkv, qhd)
+    return attn_decode_strided(Q, K, V, O, nq, nkv, n, qhd, row, qhd, scale, pos_cur, window)
 
 
 def attn_decode_gqa(Q, K, V, O, nq, nkv, n, d, scale):
@@ -147,14 +174,15 @@ def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale
     head with weights q_norm / k_norm ([d] device tensors), v over all its
     nkv*d values when v_norm, before RoPE and the append."""
     kvd = kv_dtype_of(K)
-    cap = K.numel() // (nkv * d)
+    row = _row_units(kvd, nkv, d)
+    cap = K.numel() // row
     if slot < 0 or slot >= cap:
         raise RuntimeError("fwd: KV cache full")  # forward.h:570
     _need(q, "q", torch.float32, nq * d)
     _need(k_new, "k_new", torch.float32, nkv * d)
     _need(v_new, "v_new", torch.float32, nkv * d)
-    _need(K, "K", _KV_DTYPES, (slot + 1) * nkv * d)
-    _need(V, "V", K.dtype, (slot + 1) * nkv * d)
+    _need(K, "K", _KV_DTYPES, (slot + 1) * row)
+    _need(V, "V", K.dtype, (slot + 1) * row)
     _need(O, "O", torch.float32, nq * d)
     _need(inv_freq, "inv_freq", torch.float32, d // 2)
     if q_norm is None and k_norm is None and not v_norm:
@@ -182,9 +210,10 @@ def _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V):
     _need(seq_lens, "seq_lens", torch.int32, B)
     if pos is not None:
         _need(pos, "pos", torch.int32, B)
-    nblocks = K.numel() // (nkv * page * d)
-    _need(K, "K", _KV_DTYPES, nblocks * nkv * page * d)
-    _need(V, "V", K.dtype, nblocks * nkv * page * d)
+    bu = _block_units(kv_dtype_of(K), nkv, d, page)
+    nblocks = K.numel() // bu
+    _need(K, "K", _KV_DTYPES, nblocks * bu)
+    _need(V, "V", K.dtype, nblocks * bu)
     # host-side bounds check of every block id a kernel can reach
     lens = seq_lens.cpu()
     if int(lens.min()) < 0 or int(lens.max()) > max_blocks * page:
@@ -246,10 +275,11 @@ def attn_prefill_gqa(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window=0):
     """gemm.h:409-446: causal prefill attention of M queries [M][nq][d]
     (positions pos0..) over the token-major cache [N][nkv*d]."""
     kvd = kv_dtype_of(K)
+    row = _row_units(kvd, nkv, d)
     _need(Qm, "Qm", torch.float32, M * nq * d)
     _need(Om, "Om", torch.float32, M * nq * d)
-    _need(K, "K", _KV_DTYPES, N * nkv * d)
-    _need(V, "V", K.dtype, N * nkv * d)
+    _need(K, "K", _KV_DTYPES, N * row)
+    _need(V, "V", K.dtype, N * row)
     check(_lib.load().molot_hip_attn_prefill_gqa(
         _ptr(Qm), _ptr(K), _ptr(V), _ptr(Om), nq, nkv, int(M), int(N), d, float(scale),
         int(pos0), int(window), kvd, _stream()), "attn_prefill_gqa")
@@ -262,14 +292,16 @@ def prefill_step(q, k_new, v_new, K, V, O, nq, nkv, d, M, slot0, pos0, inv_freq,
     prompt tokens' q (in place) and k, append at slots slot0.., then causal
     prefill attention over slot0 + M."""
     kvd = kv_dtype_of(K)
-    cap = K.numel() // (nkv * d)
+    row = _row_units(kvd, nkv, d)
+    cap = K.numel() // row
     if slot0 + M > cap:
         raise RuntimeError("fwd: KV cache full")  # forward.h:380
     _need(q, "q", torch.float32, M * nq * d)
     _need(k_new, "k_new", torch.float32, M * nkv * d)
     _need(v_new, "v_new", torch.float32, M * nkv * d)
     _need(O, "O", torch.float32, M * nq * d)
-    _need(V, "V", K.dtype, cap * nkv * d)
+    _need(K, "K", _KV_DTYPES, cap * row)
+    _need(V, "V", K.dtype, cap * row)
     _need(inv_freq, "inv_freq", torch.float32, d // 2)
     _need_norms(q_norm, k_norm, d)
     check(_lib.load().molot_hip_prefill_step(
@@ -325,10 +357,11 @@ class KVCache:
     """
 
     def __init__(self, cap: int, nkv: int, hd: int, kv_dtype: int = KV_F32, device="cuda"):
-        dt = torch.float32 if kv_dtype == KV_F32 else torch.bfloat16
+        dt = {KV_F32: torch.float32, KV_BF16: torch.bfloat16, KV_Q8: torch.uint8}[kv_dtype]
         self.cap, self.nkv, self.hd, self.n = cap, nkv, hd, 0
-        self.k = torch.zeros(cap * nkv * hd, dtype=dt, device=device)
-        self.v = torch.zeros(cap * nkv * hd, dtype=dt, device=device)
+        size = cap * _row_units(kv_dtype, nkv, hd)
+        self.k = torch.zeros(size, dtype=dt, device=device)
+        self.v = torch.zeros(size, dtype=dt, device=device)
 
     def reset(self) -> None:
         self.n = 0  # molot_chat.cc /reset: n = 0

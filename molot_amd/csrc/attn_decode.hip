@@ -25,6 +25,7 @@
 #include <cstdlib>
 #include <map>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -69,6 +70,26 @@ struct KVT<bf16_t> {
   }
 };
 
+// Q8 codes (the row scale is applied by the kernel that reads them).
+struct q8_t {
+  int8_t code;
+};
+
+template <>
+struct KVT<q8_t> {
+  static constexpr int VW = 16;
+  using vec = u32x4;
+  __device__ static __forceinline__ void unpack(const vec& v, float* x) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[4 * i] = (float)(int8_t)(v[i] & 0xFF);
+      x[4 * i + 1] = (float)(int8_t)((v[i] >> 8) & 0xFF);
+      x[4 * i + 2] = (float)(int8_t)((v[i] >> 16) & 0xFF);
+      x[4 * i + 3] = (float)((int32_t)v[i] >> 24);
+    }
+  }
+};
+
 // K/V rows are read exactly once per step: non-temporal 16-byte loads (the
 // streaming hint measurably raises the sustained HBM read rate on gfx950).
 template <typename T>
@@ -81,6 +102,21 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   uint32_t u = __float_as_uint(f);
   u += 0x7FFFu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// Q8 rows (the Q8_0 row quantizer of include/molot/quant.h:34-50, applied
+// per KV head row): s = absmax/127 (1 when that is not > 0), codes
+// clamp(nearbyint(x/s), -127, 127); a row dequantizes as code * s.  The
+// divisions are IEEE-correct (hipcc's default for fp32 / ), so the codes and
+// scales are the reference quantizer's bit for bit on the same fp32 input.
+__device__ __forceinline__ float q8_scale(float amax) {
+  const float s = amax / 127.0f;
+  return s > 0.f ? s : 1.0f;
+}
+__device__ __forceinline__ int q8_code(float x, float s) {
+  const int v = (int)__builtin_rintf(x / s);
+  return v > 127 ? 127 : (v < -127 ? -127 : v);
 }
 
 // ---------------------------------------------------------------------------
@@ -138,6 +174,7 @@ struct RopeArgs {
   int v_norm;           // RMS-norm v over all nkv*d values, no weights
   float eps;
   int tokens;           // grid row b = token b of a prefill: slot + b at pos + b
+  int64_t sc_off, sc_head;  // Q8 scales, as AttnArgs::sc_off / sc_head
 };
 
 // Sum over the workgroup (at most 16 waves); every thread gets the total.
@@ -147,6 +184,17 @@ __device__ __forceinline__ float block_sum(float v, float* sh) {
   __syncthreads();
   float t = 0.f;
   for (int k = 0; k < (int)((blockDim.x + 63) >> 6); ++k) t += sh[k];
+  __syncthreads();
+  return t;
+}
+
+// Maximum over the workgroup (at most 16 waves); every thread gets it.
+__device__ __forceinline__ float block_max(float v, float* sh) {
+  v = group_max<64>(v);
+  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float t = sh[0];
+  for (int k = 1; k < (int)((blockDim.x + 63) >> 6); ++k) t = fmaxf(t, sh[k]);
   __syncthreads();
   return t;
 }
@@ -214,17 +262,36 @@ __global__ void rope_append_kernel(RopeArgs a) {
     v0 *= inv;
     v1 *= inv;
   }
-  if (!act) return;
-  const float r0 = k0 * c - k1 * s;
+  const float r0 = k0 * c - k1 * s;  // 0 on the threads past the pairs
   const float r1 = k0 * s + k1 * c;
-  int64_t off;
+  float ks = 0.f, vs = 0.f;
+  if (a.kv_dtype == MOLOT_KV_Q8) {  // uniform: every thread takes the maxima
+    ks = q8_scale(block_max(fmaxf(fabsf(r0), fabsf(r1)), sh));
+    vs = q8_scale(block_max(fmaxf(fabsf(v0), fabsf(v1)), sh));
+  }
+  if (!act) return;
+  // element (Q8: byte) offset of the row, and (Q8) of its scale
+  int64_t off, soff;
   if (a.block_table) {
     const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + slot / a.page];
     off = blk * a.block_stride + (int64_t)kh * a.head_stride + (int64_t)(slot % a.page) * a.tok_stride;
+    soff = blk * a.block_stride + a.sc_off + kh * a.sc_head + 4 * (int64_t)(slot % a.page);
   } else {
     off = (int64_t)slot * a.tok_stride + (int64_t)kh * a.head_stride;
+    soff = (int64_t)slot * a.tok_stride + a.sc_off + kh * a.sc_head;
   }
-  if (a.kv_dtype == MOLOT_KV_F32) {
+  if (a.kv_dtype == MOLOT_KV_Q8) {
+    int8_t* kd = (int8_t*)a.K + off;
+    int8_t* vd = (int8_t*)a.V + off;
+    kd[i] = (int8_t)q8_code(r0, ks);
+    kd[i + half] = (int8_t)q8_code(r1, ks);
+    vd[i] = (int8_t)q8_code(v0, vs);
+    vd[i + half] = (int8_t)q8_code(v1, vs);
+    if (i == 0) {
+      *(float*)((char*)a.K + soff) = ks;
+      *(float*)((char*)a.V + soff) = vs;
+    }
+  } else if (a.kv_dtype == MOLOT_KV_F32) {
     float* kd = (float*)a.K + off;
     float* vd = (float*)a.V + off;
     kd[i] = r0;
@@ -296,6 +363,10 @@ struct AttnArgs {
   const float* k_norm;   // [D] weights of the per-head k RMS norm
   int v_norm;            // RMS-norm v over all nkv*D values, no weights
   float eps;
+  // Q8 caches: byte offset of head 0's fp32 row scales from the token's row
+  // (token-major) or the block (paged), and the byte stride between heads'
+  // scales; a paged block's scales step 4 bytes per slot
+  int64_t sc_off, sc_head;
 };
 
 // Work mapping of one kernel instance.
@@ -1034,10 +1105,11 @@ constexpr int kMfmaThreads = kMfmaWaves * 64;
 constexpr int kTile = 32;                      // cache rows per wave step
 
 // LDS of attn_mfma_kernel, in floats.  vt: per wave, 32 staged V rows of D
-// bf16 (16*D floats), which after the stream hold the wave's partial o.
+// bf16 (16*D floats), which after the stream hold the wave's partial o;
+// sc (Q8): per wave, the K then the V row scales of its current tile.
 struct LdsM {
-  int qs, cs, sn, knew, vnew, nw, wm, wl, vt, blk, misc, total;
-  __host__ __device__ LdsM(int D, int GH, int chunk, int page_shift, bool paged) {
+  int qs, cs, sn, knew, vnew, nw, wm, wl, sc, vt, blk, misc, total;
+  __host__ __device__ LdsM(int D, int GH, int chunk, int page_shift, bool paged, bool q8) {
     int o = 0;
     qs = o; o += GH * D;
     cs = o; o += D / 2;
@@ -1047,6 +1119,8 @@ struct LdsM {
     nw = o; o += D;  // k norm weights
     wm = o; o += kMfmaWaves * GH;
     wl = o; o += kMfmaWaves * GH;
+    o = (o + 3) & ~3;
+    sc = o; o += q8 ? kMfmaWaves * 2 * kTile : 0;
     o = (o + 63) & ~63;  // 256-byte aligned: the swizzle's bank pattern
     vt = o; o += kMfmaWaves * kTile * D / 2;
     blk = o; o += paged ? ((chunk >> page_shift) + 2) : 0;
@@ -1069,7 +1143,35 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int D, int GH, bool PAGED, bool ROPE>
+// 16 int8 codes -> 16 bf16 (exact: |code| <= 127), bytes 0-7 into lo, 8-15
+// into hi, each in memory order.
+__device__ __forceinline__ uint32_t bf16_pair_exact(float a, float b) {
+  return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xFFFF0000u);
+}
+__device__ __forceinline__ void i8x16_to_bf16(const u32x4& x, u32x4& lo, u32x4& hi) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t w = x[i];
+    const float f0 = (float)(int8_t)(w & 0xFF), f1 = (float)(int8_t)((w >> 8) & 0xFF);
+    const float f2 = (float)(int8_t)((w >> 16) & 0xFF), f3 = (float)((int32_t)w >> 24);
+    u32x4& dst = i < 2 ? lo : hi;
+    dst[2 * (i & 1)] = bf16_pair_exact(f0, f1);
+    dst[2 * (i & 1) + 1] = bf16_pair_exact(f2, f3);
+  }
+}
+
+// Matrix-core decode over a bf16 (Q8 = false) or Q8 (Q8 = true) cache.
+//
+// Q8: each lane reads 16 codes per 16-byte load, covering two k-steps: load
+// j of lane group g holds row bytes 64j + 16g .. +15, so k-step kk, element
+// e is head-dim index 64*(kk/2) + 16g + 8*(kk%2) + e, and q^T takes the same
+// order.  Codes widen to bf16 exactly; a score is (codes . q) * s_k * scale,
+// and the PV operand is p * s_v in the same three bf16 pieces as bf16's p
+// (the row sum l takes p itself).  Lane (row l%16) loads its A-row's two
+// scales; they pass through a per-wave LDS slot to the accumulator lanes of
+// rows 16u + 4*(l/16) + r.  The new token's k (rotated) and v rows are
+// quantized in the workgroup like the cache rows and folded in as code * s.
+template <int D, int GH, bool PAGED, bool ROPE, bool Q8>
 __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) {
   static_assert(D == 64 || D == 128, "MFMA tiles cover D = 64 or 128");
   static_assert(GH >= 1 && GH <= 16, "the group's q heads on the 16 MFMA columns");
@@ -1079,9 +1181,11 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   constexpr int NSEG = D / 16;  // 32-byte segments of a staged V row
   constexpr int RBY = 2 * D;  // bytes of a staged V row
   constexpr int RS = kTile * D / 2;  // floats of a wave's LDS region
+  constexpr int KL = Q8 ? D / 64 : KK;  // 16-byte loads per row and lane (K or V)
+  using E = typename std::conditional<Q8, int8_t, bf16_t>::type;
 
   extern __shared__ float smem[];
-  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED);
+  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8);
   float* qs = smem + L.qs;
   float* knew = smem + L.knew;
   float* vnew = smem + L.vnew;
@@ -1125,8 +1229,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   const bool split = nch > 1;
   const int64_t slot = (int64_t)b * gridDim.x + blockIdx.x;
 
-  const bf16_t* __restrict__ Kb = reinterpret_cast<const bf16_t*>(a.k);
-  const bf16_t* __restrict__ Vb = reinterpret_cast<const bf16_t*>(a.v);
+  const E* __restrict__ Kb = reinterpret_cast<const E*>(a.k);
+  const E* __restrict__ Vb = reinterpret_cast<const E*>(a.v);
   const int64_t hoff = (int64_t)h * a.head_stride;
   const int64_t qrow0 = (int64_t)b * a.nq + hq0;
 
@@ -1140,7 +1244,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     lds_barrier();
   }
   const int32_t* sblk = reinterpret_cast<const int32_t*>(smem + L.blk);
-  auto row_ptr = [&](const bf16_t* base, int t) -> const bf16_t* {
+  auto row_ptr = [&](const E* base, int t) -> const E* {
     if constexpr (PAGED) {
       const int pg = (t >> a.page_shift) - (tb >> a.page_shift);
       return base + (int64_t)sblk[pg] * a.block_stride + hoff +
@@ -1149,21 +1253,52 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       return base + (int64_t)t * a.tok_stride + hoff;
     }
   };
+  // Q8: the fp32 scale of row t of head h
+  auto sc_ptr = [&](const E* base, int t) -> const float* {
+    const char* p = reinterpret_cast<const char*>(base) + a.sc_off + h * a.sc_head;
+    if constexpr (PAGED) {
+      const int pg = (t >> a.page_shift) - (tb >> a.page_shift);
+      return reinterpret_cast<const float*>(p + (int64_t)sblk[pg] * a.block_stride) +
+             (t & ((1 << a.page_shift) - 1));
+    } else {
+      return reinterpret_cast<const float*>(p + (int64_t)t * a.tok_stride);
+    }
+  };
   // Rows past the chunk end load the chunk's last row (row tb of an empty
   // chunk): every wave issues the same loads on every path.
   const int rmax = max(cntg - 1, 0);
   const int ntiles = (cntg + kTile - 1) / kTile;
-  u32x4 kr[2][KK], vr[2][KK];
+  u32x4 kr[2][KL], vr[2][KL];
+  float skr[2] = {0.f, 0.f}, svr[2] = {0.f, 0.f};  // Q8: scales of this lane's A-rows
   auto load_tile = [&](int tile) {
+    if constexpr (Q8) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = tb + min(tile * kTile + 16 * u + m16, rmax);
+        skr[u] = __builtin_nontemporal_load(sc_ptr(Kb, t));
+        svr[u] = __builtin_nontemporal_load(sc_ptr(Vb, t));
+      }
+    }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int t = tb + min(tile * kTile + 16 * u + m16, rmax);
-      const bf16_t* pk = row_ptr(Kb, t);
-      const bf16_t* pv = row_ptr(Vb, t);
+      const E* pk = row_ptr(Kb, t);
+      const E* pv = row_ptr(Vb, t);
+      if constexpr (Q8) {
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kr[u][kk] = load16(pk + 32 * kk + 8 * g4);
+        for (int j = 0; j < KL; ++j)
+          kr[u][j] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(pk + 64 * j + 16 * g4));
 #pragma unroll
-      for (int q = 0; q < KK; ++q) vr[u][q] = load16(pv + 8 * (g4 + 4 * q));
+        for (int j = 0; j < KL; ++j)
+          vr[u][j] = __builtin_nontemporal_load(
+              reinterpret_cast<const u32x4*>(pv + 16 * (g4 + 4 * j)));
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) kr[u][kk] = load16(pk + 32 * kk + 8 * g4);
+#pragma unroll
+        for (int q = 0; q < KK; ++q) vr[u][q] = load16(pv + 8 * (g4 + 4 * q));
+      }
     }
   };
   constexpr int QV = GH * D / 4;
@@ -1232,23 +1367,32 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
         nn.apply(a, smem + L.nw, j, D / 2, k0, k1, v0, v1);
         const float r0 = k0 * csn[j] - k1 * sn[j];
         const float r1 = k0 * sn[j] + k1 * csn[j];
-        knew[j] = __uint_as_float((uint32_t)f32_to_bf16(r0) << 16);
-        knew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(r1) << 16);
-        vnew[j] = __uint_as_float((uint32_t)f32_to_bf16(v0) << 16);
-        vnew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(v1) << 16);
+        if constexpr (Q8) {  // quantized after the stream (whole rows)
+          knew[j] = r0;
+          knew[j + D / 2] = r1;
+          vnew[j] = v0;
+          vnew[j + D / 2] = v1;
+        } else {
+          knew[j] = __uint_as_float((uint32_t)f32_to_bf16(r0) << 16);
+          knew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(r1) << 16);
+          vnew[j] = __uint_as_float((uint32_t)f32_to_bf16(v0) << 16);
+          vnew[j + D / 2] = __uint_as_float((uint32_t)f32_to_bf16(v1) << 16);
+        }
       }
     }
   }
   lds_barrier();
 
   // q^T as the B operand: lane l holds head l%16 (zero past GH), elements
-  // 32*kk + 8*(l/16) + e, in three bf16 pieces
+  // 32*kk + 8*(l/16) + e (Q8: 64*(kk/2) + 16*(l/16) + 8*(kk%2) + e), in
+  // three bf16 pieces
   bf16x8_t qh[KK], qm[KK], ql[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float x = m16 < GH ? qs[m16 * D + 32 * kk + 8 * g4 + e] : 0.f;
+      const int di = Q8 ? 64 * (kk >> 1) + 16 * g4 + 8 * (kk & 1) + e : 32 * kk + 8 * g4 + e;
+      const float x = m16 < GH ? qs[m16 * D + di] : 0.f;
       __bf16 hi, mid, lo;
       split3(x, hi, mid, lo);
       qh[kk][e] = hi;
@@ -1273,28 +1417,76 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     if (lane == 0) v = atomicAdd(&misc[0], 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
+  float* scw = smem + L.sc + w * (2 * kTile);  // Q8: this wave's scale slots
   while (tile < ntiles) {
     // V rows into this wave's LDS region (lane: row 16u + l%16, 16-byte
     // chunks l/16 + 4q), 32-byte segment s of row r stored at s ^ (r % NSEG)
+    f32x4 sk4[2], sv4[2];  // Q8: scales of accumulator rows 16u + 4*(l/16) + r
+    if constexpr (Q8) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int q = 0; q < KK; ++q) {
-        const int r = 16 * u + m16, ch = g4 + 4 * q;
-        *reinterpret_cast<u32x4*>(vt + r * RBY + 32 * ((ch >> 1) ^ (r & (NSEG - 1))) +
-                                  16 * (ch & 1)) = vr[u][q];
+        for (int j = 0; j < KL; ++j) {
+          // load j holds row bytes 16*(l/16 + 4j): 32-byte bf16 segment l/16 + 4j
+          const int r = 16 * u + m16, s = g4 + 4 * j;
+          u32x4 lo, hi;
+          i8x16_to_bf16(vr[u][j], lo, hi);
+          char* dst = vt + r * RBY + 32 * (s ^ (r & (NSEG - 1)));
+          *reinterpret_cast<u32x4*>(dst) = lo;
+          *reinterpret_cast<u32x4*>(dst + 16) = hi;
+        }
+      if (g4 == 0) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          scw[16 * u + m16] = skr[u];
+          scw[kTile + 16 * u + m16] = svr[u];
+        }
       }
+      // the slots are this wave's own: LDS keeps its order, and the fence
+      // keeps the compiler from moving the reads above the writes
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        sk4[u] = *reinterpret_cast<const f32x4*>(scw + 16 * u + 4 * g4);
+        sv4[u] = *reinterpret_cast<const f32x4*>(scw + kTile + 16 * u + 4 * g4);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int q = 0; q < KK; ++q) {
+          const int r = 16 * u + m16, ch = g4 + 4 * q;
+          *reinterpret_cast<u32x4*>(vt + r * RBY + 32 * ((ch >> 1) ^ (r & (NSEG - 1))) +
+                                    16 * (ch & 1)) = vr[u][q];
+        }
+    }
     // scores of the two 16-row halves
     f32x4 sacc[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (Q8) {
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, kr[u][kk]);
-        sacc[u] = mfma_bf16(kv, ql[kk], sacc[u]);
-        sacc[u] = mfma_bf16(kv, qm[kk], sacc[u]);
-        sacc[u] = mfma_bf16(kv, qh[kk], sacc[u]);
+        for (int j = 0; j < KL; ++j) {
+          u32x4 lo, hi;
+          i8x16_to_bf16(kr[u][j], lo, hi);
+          const bf16x8_t k0 = __builtin_bit_cast(bf16x8_t, lo);
+          const bf16x8_t k1 = __builtin_bit_cast(bf16x8_t, hi);
+          sacc[u] = mfma_bf16(k0, ql[2 * j], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qm[2 * j], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qh[2 * j], sacc[u]);
+          sacc[u] = mfma_bf16(k1, ql[2 * j + 1], sacc[u]);
+          sacc[u] = mfma_bf16(k1, qm[2 * j + 1], sacc[u]);
+          sacc[u] = mfma_bf16(k1, qh[2 * j + 1], sacc[u]);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, kr[u][kk]);
+          sacc[u] = mfma_bf16(kv, ql[kk], sacc[u]);
+          sacc[u] = mfma_bf16(kv, qm[kk], sacc[u]);
+          sacc[u] = mfma_bf16(kv, qh[kk], sacc[u]);
+        }
       }
     }
     // the next tile's loads go out while this one is finished
@@ -1309,7 +1501,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = tile * kTile + 16 * u + 4 * g4 + r;
-        sv[u][r] = row < cntg ? sacc[u][r] * a.scale : -INFINITY;
+        const float sc = Q8 ? a.scale * sk4[u][r] : a.scale;
+        sv[u][r] = row < cntg ? sacc[u][r] * sc : -INFINITY;
         tmax = fmaxf(tmax, sv[u][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
@@ -1326,7 +1519,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
         const float p = softmax_exp(sv[u][r] - mn);
         ps += p;
         __bf16 hi, mid, lo;
-        split3(p, hi, mid, lo);
+        split3(Q8 ? p * sv4[u][r] : p, hi, mid, lo);
         ph[4 * u + r] = hi;
         pm[4 * u + r] = mid;
         pl[4 * u + r] = lo;
@@ -1357,18 +1550,54 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   }
 
   // ---- the new token: appended by subgroup 0, folded in by wave 0 ----
-  if (is_new && sub == 0 && tid < D) {
+  const bool store_new = is_new && sub == 0 && (Q8 ? w == 0 : tid < D);
+  int64_t off = 0;                    // element (Q8: byte) offset of the new row
+  [[maybe_unused]] int64_t soff = 0;  // Q8: byte offset of its scale
+  if (store_new) {
     const int slot_row = n - 1;
-    int64_t off;
     if constexpr (PAGED) {
       const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
-      off = blk * a.block_stride + hoff +
-            (int64_t)(slot_row & ((1 << a.page_shift) - 1)) * a.tok_stride;
+      const int sl = slot_row & ((1 << a.page_shift) - 1);
+      off = blk * a.block_stride + hoff + (int64_t)sl * a.tok_stride;
+      soff = blk * a.block_stride + a.sc_off + h * a.sc_head + 4 * sl;
     } else {
       off = (int64_t)slot_row * a.tok_stride + hoff;
+      soff = (int64_t)slot_row * a.tok_stride + a.sc_off + h * a.sc_head;
     }
-    reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
-    reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
+  }
+  if constexpr (!Q8) {
+    if (store_new) {
+      reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
+      reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
+    }
+  } else if (is_new && w == 0) {
+    // quantize the k and v rows as the cache holds them; LDS gets code * s
+    constexpr int EPL = D / 64;
+    float kx[EPL], vx[EPL];
+    float ka = 0.f, va = 0.f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      kx[e] = knew[lane + 64 * e];
+      vx[e] = vnew[lane + 64 * e];
+      ka = fmaxf(ka, fabsf(kx[e]));
+      va = fmaxf(va, fabsf(vx[e]));
+    }
+    const float ks = q8_scale(group_max<64>(ka)), vs = q8_scale(group_max<64>(va));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      const int kc = q8_code(kx[e], ks), vc = q8_code(vx[e], vs);
+      knew[lane + 64 * e] = (float)kc * ks;
+      vnew[lane + 64 * e] = (float)vc * vs;
+      if (store_new) {
+        reinterpret_cast<int8_t*>(a.k)[off + lane + 64 * e] = (int8_t)kc;
+        reinterpret_cast<int8_t*>(a.v)[off + lane + 64 * e] = (int8_t)vc;
+      }
+    }
+    if (store_new && lane == 0) {
+      *reinterpret_cast<float*>(reinterpret_cast<char*>(a.k) + soff) = ks;
+      *reinterpret_cast<float*>(reinterpret_cast<char*>(a.v) + soff) = vs;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the fold reads other lanes' rows
   }
   if (is_new && w == 0) {
     float part = 0.f;
@@ -1456,7 +1685,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
   constexpr int VW = KVT<T>::VW;          // elements per 16-byte load
   constexpr int CH = KT * D / VW;         // 16-byte chunks per tile (K or V)
   constexpr int CPT = (CH + NT - 1) / NT;
-  static_assert(CH % NT == 0, "whole chunks per thread");
+  constexpr bool Q8 = std::is_same<T, q8_t>::value;
+  static_assert(CH % NT == 0 || CH < NT, "whole chunks per thread");
   __shared__ __attribute__((aligned(16))) float ks[KT * KSR];
   __shared__ __attribute__((aligned(16))) float vs[D * VSR];
 
@@ -1502,23 +1732,43 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
   // tile loads: chunk c = tid + NT*i is key c / (D/VW), elements VW*(c % (D/VW))
   const T* Kb = reinterpret_cast<const T*>(a.k);
   const T* Vb = reinterpret_cast<const T*>(a.v);
-  auto row_off = [&](int t) -> int64_t {  // element offset of row t of head h
+  // Q8 byte layouts: token-major rows of R bytes, paged blocks of BB bytes
+  const int pg = 1 << a.page_shift;
+  const int64_t R = (int64_t)a.nkv * D + ((4 * a.nkv + 15) & ~15);
+  const int64_t BB = (int64_t)a.nkv * pg * (D + 4);
+  // element (Q8: byte) offset of row t of head h, and (Q8) of its scale
+  auto row_off = [&](int t, int64_t& soff) -> int64_t {
     if constexpr (PAGED) {
       const int64_t blk = a.block_table[t >> a.page_shift];
-      const int pg = 1 << a.page_shift;
-      return (blk * a.nkv + h) * pg * D + (int64_t)(t & (pg - 1)) * D;
+      const int sl = t & (pg - 1);
+      if constexpr (Q8) {
+        soff = blk * BB + (int64_t)a.nkv * pg * D + 4 * ((int64_t)h * pg + sl);
+        return blk * BB + ((int64_t)h * pg + sl) * D;
+      }
+      return (blk * a.nkv + h) * pg * D + (int64_t)sl * D;
     } else {
+      if constexpr (Q8) {
+        soff = (int64_t)t * R + (int64_t)a.nkv * D + 4 * h;
+        return (int64_t)t * R + (int64_t)h * D;
+      }
       return (int64_t)t * a.nkv * D + (int64_t)h * D;
     }
   };
   typename KVT<T>::vec kreg[CPT], vreg[CPT];
+  [[maybe_unused]] float ksc[CPT], vsc[CPT];  // Q8: the chunks' row scales
   auto load_tile = [&](int tk) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + NT * i;
+      if (CH < NT && c >= CH) break;
       const int key = c / (D / VW), e = VW * (c % (D / VW));
       const int t = min(tk + key, kt_hi - 1);  // rows past the range: the last one (masked)
-      const int64_t off = row_off(t) + e;
+      int64_t soff = 0;
+      const int64_t off = row_off(t, soff) + e;
+      if constexpr (Q8) {
+        ksc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.k) + soff);
+        vsc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v) + soff);
+      }
       kreg[i] = load16(Kb + off);
       vreg[i] = load16(Vb + off);
     }
@@ -1527,10 +1777,18 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + NT * i;
+      if (CH < NT && c >= CH) break;
       const int key = c / (D / VW), e = VW * (c % (D / VW));
       float kx[VW], vx[VW];
       KVT<T>::unpack(kreg[i], kx);
       KVT<T>::unpack(vreg[i], vx);
+      if constexpr (Q8) {  // code * s, the dequantized value
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          kx[j] *= ksc[i];
+          vx[j] *= vsc[i];
+        }
+      }
 #pragma unroll
       for (int e4 = 0; e4 < VW; e4 += 4)
         *reinterpret_cast<f32x4*>(ks + key * KSR + e + e4) =
@@ -1990,12 +2248,12 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
 // bf16 KV, D = 64 or 128: the matrix-core kernel.  Two workgroups of four
 // waves per CU; paged batches are cut finer (their sequences differ in
 // length, and more, shorter chunks even out the CUs' shares).
-template <int D, int GH, bool PAGED, bool ROPE>
+template <int D, int GH, bool PAGED, bool ROPE, bool Q8>
 int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
   int st = plan_launch(a, D, span, GH, nsubs, B, kTile, PAGED ? 8 : 2, stream);
   if (st) return st;
-  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED);
-  return launch_pair(attn_mfma_kernel<D, GH, PAGED, ROPE>, kMfmaThreads,
+  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8);
+  return launch_pair(attn_mfma_kernel<D, GH, PAGED, ROPE, Q8>, kMfmaThreads,
                      sizeof(float) * (size_t)L.total, a, GH, D, nsubs, B, PAGED, ROPE, stream);
 }
 
@@ -2047,11 +2305,51 @@ int dispatch_attn(int d, int kv_dtype, int gh, const AttnArgs& a, int span, int 
 
 bool supported_d(int d) { return d == 64 || d == 128 || d == 256; }
 
+bool valid_kv(int kv_dtype) {
+  return kv_dtype == MOLOT_KV_F32 || kv_dtype == MOLOT_KV_BF16 || kv_dtype == MOLOT_KV_Q8;
+}
+
+// bytes of one K/V element (Q8: one code)
+int kv_esz(int kv_dtype) { return kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1; }
+
+// Q8 byte layouts: a token-major row (codes, then the nkv scales padded to
+// 16 bytes) and a paged block (codes [nkv][page][d], then scales [nkv][page])
+int64_t q8_row_bytes(int nkv, int d) { return (int64_t)nkv * d + ((4 * (int64_t)nkv + 15) & ~15); }
+int64_t q8_block_bytes(int nkv, int d, int page) { return (int64_t)nkv * page * (d + 4); }
+
 int check_common(int nq, int nkv, int d, int kv_dtype) {
   if (nq <= 0 || nkv <= 0 || nq % nkv != 0) return MOLOT_EINVAL;
-  if (kv_dtype != MOLOT_KV_F32 && kv_dtype != MOLOT_KV_BF16) return MOLOT_EINVAL;
+  if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
   if (!supported_d(d)) return MOLOT_ENOTSUP;
+  if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // matrix-core kernels only
   return 0;
+}
+
+// The strides and scale offsets of the token-major cache [cap][nkv*d]
+// (Q8: its byte layout) in a or r.
+template <typename A>
+void token_major(A& a, int nkv, int d, int kv_dtype) {
+  const bool q8 = kv_dtype == MOLOT_KV_Q8;
+  a.tok_stride = q8 ? q8_row_bytes(nkv, d) : (int64_t)nkv * d;
+  a.head_stride = d;
+  a.sc_off = (int64_t)nkv * d;
+  a.sc_head = 4;
+}
+
+// The same for pages [block][nkv][page][d].
+template <typename A>
+void paged_layout(A& a, int nkv, int d, int page, int kv_dtype) {
+  a.tok_stride = d;
+  a.head_stride = (int64_t)page * d;
+  a.block_stride =
+      kv_dtype == MOLOT_KV_Q8 ? q8_block_bytes(nkv, d, page) : (int64_t)nkv * page * d;
+  a.sc_off = (int64_t)nkv * page * d;
+  a.sc_head = 4LL * page;
+}
+
+// Q8 pages: 16-byte aligned blocks need nkv*page scales to fill 16 bytes
+bool q8_pages_ok(int nkv, int page, int kv_dtype) {
+  return kv_dtype != MOLOT_KV_Q8 || ((int64_t)nkv * page) % 4 == 0;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -2063,14 +2361,14 @@ int zero_out(float* O, int64_t count, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
-template <int D, bool PAGED, bool ROPE>
+template <int D, bool PAGED, bool ROPE, bool Q8>
 int dispatch_mfma(int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
   switch (gh) {
-    case 1: return launch_mfma<D, 1, PAGED, ROPE>(a, span, nsubs, B, st);
-    case 2: return launch_mfma<D, 2, PAGED, ROPE>(a, span, nsubs, B, st);
-    case 4: return launch_mfma<D, 4, PAGED, ROPE>(a, span, nsubs, B, st);
-    case 8: return launch_mfma<D, 8, PAGED, ROPE>(a, span, nsubs, B, st);
-    case 16: return launch_mfma<D, 16, PAGED, ROPE>(a, span, nsubs, B, st);
+    case 1: return launch_mfma<D, 1, PAGED, ROPE, Q8>(a, span, nsubs, B, st);
+    case 2: return launch_mfma<D, 2, PAGED, ROPE, Q8>(a, span, nsubs, B, st);
+    case 4: return launch_mfma<D, 4, PAGED, ROPE, Q8>(a, span, nsubs, B, st);
+    case 8: return launch_mfma<D, 8, PAGED, ROPE, Q8>(a, span, nsubs, B, st);
+    case 16: return launch_mfma<D, 16, PAGED, ROPE, Q8>(a, span, nsubs, B, st);
   }
   return MOLOT_EINVAL;
 }
@@ -2078,12 +2376,17 @@ int dispatch_mfma(int gh, const AttnArgs& a, int span, int nsubs, int B, void* s
 template <bool PAGED, bool ROPE>
 int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
   const int G = a.nq / a.nkv;
-  if (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128)) {
-    // up to 16 q heads of a group share each K/V tile on the MFMA columns
+  const bool q8 = kv_dtype == MOLOT_KV_Q8;
+  if (q8 || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128))) {
+    // up to 16 q heads of a group share each K/V tile on the MFMA columns;
+    // Q8 caches (D = 64, 128: checked by the entry points) only run here
     const int gh = G % 16 == 0 ? 16 : pick_gh(G);
     const int nsubs = G / gh;
-    return d == 64 ? dispatch_mfma<64, PAGED, ROPE>(gh, a, span, nsubs, B, stream)
-                   : dispatch_mfma<128, PAGED, ROPE>(gh, a, span, nsubs, B, stream);
+    if (q8)
+      return d == 64 ? dispatch_mfma<64, PAGED, ROPE, true>(gh, a, span, nsubs, B, stream)
+                     : dispatch_mfma<128, PAGED, ROPE, true>(gh, a, span, nsubs, B, stream);
+    return d == 64 ? dispatch_mfma<64, PAGED, ROPE, false>(gh, a, span, nsubs, B, stream)
+                   : dispatch_mfma<128, PAGED, ROPE, false>(gh, a, span, nsubs, B, stream);
   }
   const int gh = pick_gh(G);
   const int nsubs = G / gh;
@@ -2121,6 +2424,14 @@ const char* molot_hip_strerror(int status) {
 }
 
 const char* molot_hip_version(void) { return "molot_amd 0.2"; }
+
+int molot_hip_q8_row_bytes(int nkv, int d) {
+  return nkv > 0 && d > 0 ? (int)q8_row_bytes(nkv, d) : 0;
+}
+
+int64_t molot_hip_q8_block_bytes(int nkv, int d, int page) {
+  return nkv > 0 && d > 0 && page > 0 ? q8_block_bytes(nkv, d, page) : 0;
+}
 
 void molot_rope_inv_freq(float base, int d, float* out) {
   for (int i = 0; i < d / 2; ++i) out[i] = 1.0f / powf(base, (2.0f * (float)i) / (float)d);
@@ -2215,7 +2526,7 @@ static int rope_append_impl(float* q, const float* k_new, const float* v_new, vo
   if (nq < 0 || nkv <= 0 || d <= 0 || (d & 1) || d > 2048 || slot < 0) return MOLOT_EINVAL;
   if (!norms_ok(nm)) return MOLOT_EINVAL;
   if ((nq > 0 && !q) || !k_new || !v_new || !K || !V || !inv_freq) return MOLOT_EINVAL;
-  if (kv_dtype != MOLOT_KV_F32 && kv_dtype != MOLOT_KV_BF16) return MOLOT_EINVAL;
+  if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
   RopeArgs a{};
   a.q = q;
   a.k_new = k_new;
@@ -2223,8 +2534,7 @@ static int rope_append_impl(float* q, const float* k_new, const float* v_new, vo
   a.K = K;
   a.V = V;
   a.inv_freq = inv_freq;
-  a.tok_stride = (int64_t)nkv * d;
-  a.head_stride = d;
+  token_major(a, nkv, d, kv_dtype);
   a.nq = nq;
   a.nkv = nkv;
   a.d = d;
@@ -2255,12 +2565,14 @@ int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, 
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   if (!Q || !O || n < 0) return MOLOT_EINVAL;
+  if (kv_dtype == MOLOT_KV_Q8 && (tok_stride != q8_row_bytes(nkv, d) || head_stride != d))
+    return MOLOT_EINVAL;  // Q8: the token-major byte layout only
   int t0 = (window > 0 && pos_cur - window + 1 > 0) ? pos_cur - window + 1 : 0;
   if (t0 > n) t0 = n;
   const int n_att = n - t0;
   if (n_att <= 0) return zero_out(O, (int64_t)nq * d, (hipStream_t)stream);  // o = 0
   if (!K || !V) return MOLOT_EINVAL;
-  const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : 2;
+  const int esz = kv_esz(kv_dtype);
   if (!aligned16(K) || !aligned16(V) || !aligned16(Q) || !aligned16(O) ||
       (tok_stride * esz) % 16 || (head_stride * esz) % 16)
     return MOLOT_EINVAL;  // 16-byte vector loads of every row
@@ -2271,6 +2583,8 @@ int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, 
   a.o = O;
   a.tok_stride = tok_stride;
   a.head_stride = head_stride;
+  a.sc_off = (int64_t)nkv * d;  // Q8 scales after the row's codes
+  a.sc_head = 4;
   a.nq = nq;
   a.nkv = nkv;
   a.n = n;
@@ -2284,8 +2598,9 @@ int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, 
 int molot_hip_attn_decode_gqa_cache(const float* Q, const void* K, const void* V, float* O,
                                     int nq, int nkv, int n, int qhd, float scale, int pos_cur,
                                     int window, int kv_dtype, void* stream) {
-  return molot_hip_attn_decode_strided(Q, K, V, O, nq, nkv, n, qhd, (int64_t)nkv * qhd, qhd,
-                                       scale, pos_cur, window, kv_dtype, stream);
+  const int64_t row = kv_dtype == MOLOT_KV_Q8 ? q8_row_bytes(nkv, qhd) : (int64_t)nkv * qhd;
+  return molot_hip_attn_decode_strided(Q, K, V, O, nq, nkv, n, qhd, row, qhd, scale, pos_cur,
+                                       window, kv_dtype, stream);
 }
 
 int molot_hip_attn_decode_gqa(const float* Q, const void* K, const void* V, float* O, int nq,
@@ -2340,8 +2655,7 @@ static int decode_step_impl(float* q, const float* k_new, const float* v_new, vo
   a.v = V;
   a.inv_freq = inv_freq;
   a.o = O;
-  a.tok_stride = (int64_t)nkv * d;
-  a.head_stride = d;
+  token_major(a, nkv, d, kv_dtype);
   a.nq = nq;
   a.nkv = nkv;
   a.n = n;
@@ -2385,8 +2699,8 @@ static int paged_args(AttnArgs& a, const float* Q, void* K, void* V, float* O,
     return MOLOT_EINVAL;
   if ((int64_t)max_seq_len > (int64_t)max_blocks * page) return MOLOT_EINVAL;
   if (!aligned16(K) || !aligned16(V) || !aligned16(Q) || !aligned16(O)) return MOLOT_EINVAL;
-  const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : 2;
-  if (((int64_t)d * esz) % 16) return MOLOT_EINVAL;
+  const int esz = kv_esz(kv_dtype);
+  if (((int64_t)d * esz) % 16 || !q8_pages_ok(nkv, page, kv_dtype)) return MOLOT_EINVAL;
   int shift = 0;
   while ((1 << shift) < page) ++shift;
   a.q = Q;
@@ -2396,9 +2710,7 @@ static int paged_args(AttnArgs& a, const float* Q, void* K, void* V, float* O,
   a.block_table = block_table;
   a.seq_lens = seq_lens;
   a.pos_arr = pos;
-  a.tok_stride = d;
-  a.head_stride = (int64_t)page * d;
-  a.block_stride = (int64_t)nkv * page * d;
+  paged_layout(a, nkv, d, page, kv_dtype);
   a.nq = nq;
   a.nkv = nkv;
   a.max_blocks = max_blocks;
@@ -2513,7 +2825,7 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
     return MOLOT_EINVAL;
   if ((nq > 0 && !q) || !k_new || !v_new || !K || !V || !inv_freq || !block_table || !seq_lens)
     return MOLOT_EINVAL;
-  if (kv_dtype != MOLOT_KV_F32 && kv_dtype != MOLOT_KV_BF16) return MOLOT_EINVAL;
+  if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
   if (B == 0) return 0;
   RopeArgs a{};
   a.q = q;
@@ -2525,9 +2837,7 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
   a.block_table = block_table;
   a.seq_lens = seq_lens;
   a.pos_arr = pos;
-  a.tok_stride = d;
-  a.head_stride = (int64_t)page * d;
-  a.block_stride = (int64_t)nkv * page * d;
+  paged_layout(a, nkv, d, page, kv_dtype);
   a.nq = nq;
   a.nkv = nkv;
   a.d = d;
@@ -2572,12 +2882,16 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   a.scale = scale;
   a.block_table = block_row;
   if (block_row) {
-    if (page <= 0 || (page & (page - 1))) return MOLOT_EINVAL;
+    if (page <= 0 || (page & (page - 1)) || !q8_pages_ok(nkv, page, kv_dtype))
+      return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
   using PfFn = void (*)(PfArgs);
   PfFn pk;
-  if (!block_row)
+  if (kv_dtype == MOLOT_KV_Q8)  // D = 64, 128 (check_common)
+    pk = block_row ? (d == 64 ? prefill_kernel<64, q8_t, true> : prefill_kernel<128, q8_t, true>)
+                   : (d == 64 ? prefill_kernel<64, q8_t, false> : prefill_kernel<128, q8_t, false>);
+  else if (!block_row)
     pk = kv_dtype == MOLOT_KV_F32
              ? (d == 64 ? prefill_kernel<64, float, false>
                         : d == 128 ? prefill_kernel<128, float, false>
@@ -2629,7 +2943,7 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   if (!q || !k_new || !v_new || !K || !V || !O || !inv_freq) return MOLOT_EINVAL;
   if ((int64_t)M > 65535) return MOLOT_ENOTSUP;  // one grid row per token
   if (block_row && ((int64_t)slot0 + M > (int64_t)max_blocks * page || page <= 0 ||
-                    (page & (page - 1))))
+                    (page & (page - 1)) || !q8_pages_ok(nkv, page, kv_dtype)))
     return MOLOT_EINVAL;
   RopeArgs r{};
   r.q = q;
@@ -2642,12 +2956,9 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
     r.block_table = block_row;
     r.max_blocks = 0;
     r.page = page;
-    r.tok_stride = d;
-    r.head_stride = (int64_t)page * d;
-    r.block_stride = (int64_t)nkv * page * d;
+    paged_layout(r, nkv, d, page, kv_dtype);
   } else {
-    r.tok_stride = (int64_t)nkv * d;
-    r.head_stride = d;
+    token_major(r, nkv, d, kv_dtype);
   }
   r.nq = nq;
   r.nkv = nkv;

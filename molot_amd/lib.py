@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libmolot_amd.so")
 
 KV_F32 = 0
 KV_BF16 = 1
+KV_Q8 = 2
 
 OK = 0
 EINVAL = -22
@@ -58,6 +59,7 @@ _SIGS = {
     "molot_hip_prefill_step_paged": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                      _P, _P, _I, _F, _P, _F, _I, _I, _P],
     "molot_hip_last_plan": [ctypes.POINTER(_I), ctypes.POINTER(_I)],
+    "molot_hip_q8_row_bytes": [_I, _I],
     "molot_hip_profile_begin": [_I],
     "molot_hip_profile_end": [ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_I),
                               ctypes.POINTER(_I)],
@@ -76,9 +78,12 @@ _STR = {
     "molot_hip_strerror": [_I],
     "molot_hip_version": [],
 }
+_I64RET = {
+    "molot_hip_q8_block_bytes": [_I, _I, _I],
+}
 
 # Every function include/molot_amd/*.h declares.
-EXPORTS = sorted(list(_SIGS) + list(_VOID) + list(_STR))
+EXPORTS = sorted(list(_SIGS) + list(_VOID) + list(_STR) + list(_I64RET))
 
 
 def load() -> ctypes.CDLL:
@@ -104,6 +109,10 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = args
             fn.restype = ctypes.c_char_p
+        for name, args in _I64RET.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int64
         _lib = lib
         return lib
 

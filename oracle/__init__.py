@@ -70,6 +70,7 @@ def lib() -> ctypes.CDLL:
             "orc_q8_block_bytes": (_I64, [_I, _I, _I]),
             "orc_quantize_q8_row": (None, [_P, _I, _P, _P]),
             "orc_q8_store_token": (None, [_P, _I64, _P, _I, _I]),
+            "orc_q8_store_tokens": (None, [_P, _I64, _P, _I, _I]),
             "orc_attn_prefill": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _I]),
             "orc_decode_step_norm": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P,
                                             _I, _F, _P, _F, _I, _I, _I]),
@@ -334,6 +335,9 @@ def prefill_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, M, slot0, pos0, q_norm, k_
         if Kc.dtype == np.uint16:
             Kc[slot0 + m] = f32_to_bf16(k[m].reshape(-1))
             Vc[slot0 + m] = f32_to_bf16(v[m].reshape(-1))
+        elif Kc.dtype == np.uint8:
+            q8_store_token(Kc, slot0 + m, k[m], nkv, d)
+            q8_store_token(Vc, slot0 + m, v[m], nkv, d)
         else:
             Kc[slot0 + m] = k[m].reshape(-1)
             Vc[slot0 + m] = v[m].reshape(-1)
@@ -360,12 +364,56 @@ def quantize_q8_row(x: np.ndarray):
 
 def q8_cache(X: np.ndarray, nkv: int, d: int) -> np.ndarray:
     """A token-major Q8 cache [N][row bytes] from fp32 rows X [N][nkv*d]."""
-    X = _f32(X)
+    X = np.ascontiguousarray(_f32(X).reshape(-1, nkv * d))
     N = X.shape[0]
     out = np.zeros((N, q8_row_bytes(nkv, d)), np.uint8)
-    for t in range(N):
-        lib().orc_q8_store_token(_p(out), t, _p(X[t]), nkv, d)
+    lib().orc_q8_store_tokens(_p(out), N, _p(X), nkv, d)
     return out
+
+
+def q8_store_token(C: np.ndarray, t: int, x: np.ndarray, nkv: int, d: int) -> None:
+    """Quantize rows x [nkv][d] into token t of the token-major Q8 cache C."""
+    assert C.dtype == np.uint8 and C.flags.c_contiguous and C.shape[1] == q8_row_bytes(nkv, d)
+    lib().orc_q8_store_token(_p(C), int(t), _p(_f32(x).reshape(-1)), nkv, d)
+
+
+# Paged Q8: block = [nkv][page][d] int8 codes, then [nkv][page] fp32 scales
+# (q8_block_bytes(nkv, d, page) bytes), as uint8 arrays [nblk][block bytes].
+
+def q8_block_bytes(nkv: int, d: int, page: int) -> int:
+    return int(lib().orc_q8_block_bytes(nkv, d, page))
+
+
+def q8_pages(Xp: np.ndarray) -> np.ndarray:
+    """Quantize fp32 pages Xp [nblk][nkv][page][d] row by row into Q8 blocks."""
+    nblk, nkv, page, d = Xp.shape
+    tok = np.ascontiguousarray(_f32(Xp).transpose(0, 2, 1, 3)).reshape(nblk * page, nkv * d)
+    C = q8_cache(tok, nkv, d)
+    codes = C[:, :nkv * d].reshape(nblk, page, nkv, d).transpose(0, 2, 1, 3)
+    scales = C[:, nkv * d:nkv * d + 4 * nkv].reshape(nblk, page, nkv, 4).transpose(0, 2, 1, 3)
+    out = np.concatenate([codes.reshape(nblk, -1), scales.reshape(nblk, -1)], axis=1)
+    assert out.shape[1] == q8_block_bytes(nkv, d, page)
+    return np.ascontiguousarray(out)
+
+
+def q8_pages_dequant(P: np.ndarray, nkv: int, d: int, page: int) -> np.ndarray:
+    """fp32 [nblk][nkv][page][d] of Q8 blocks."""
+    nblk = P.shape[0]
+    q = P[:, :nkv * page * d].view(np.int8).astype(np.float32).reshape(nblk, nkv, page, d)
+    s = np.ascontiguousarray(P[:, nkv * page * d:]).view(np.float32).reshape(nblk, nkv, page, 1)
+    return q * s
+
+
+def q8_page_store(P: np.ndarray, blk: int, sl: int, x: np.ndarray, nkv: int, d: int,
+                  page: int) -> None:
+    """Quantize rows x [nkv][d] into slot sl of Q8 block blk."""
+    x = _f32(x).reshape(nkv, d)
+    for h in range(nkv):
+        s, q = quantize_q8_row(x[h])
+        o = (h * page + sl) * d
+        P[blk, o:o + d] = q.view(np.uint8)
+        so = nkv * page * d + 4 * (h * page + sl)
+        P[blk, so:so + 4] = np.array([s], np.float32).view(np.uint8)
 
 
 def q8_dequant(C: np.ndarray, nkv: int, d: int) -> np.ndarray:

@@ -212,6 +212,11 @@ void orc_q8_store_token(void* base, int64_t t, const float* x, int nkv, int d) {
                         (float*)(row + (size_t)nkv * d) + h);
 }
 
+/* Tokens 0..n-1 of a token-major Q8 cache from rows x [n][nkv*d]. */
+void orc_q8_store_tokens(void* base, int64_t n, const float* x, int nkv, int d) {
+  for (int64_t t = 0; t < n; ++t) orc_q8_store_token(base, t, x + t * (size_t)nkv * d, nkv, d);
+}
+
 /* The strides of a Q8 cache are its byte layout's (the callers' element
  * strides describe fp32/bf16 layouts); head-major Q8 is not a layout here. */
 static orc_kv_t orc_kv_make(const void* K, const void* V, int kv_dtype, int64_t tok,

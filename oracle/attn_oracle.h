@@ -25,6 +25,7 @@ int orc_q8_row_bytes(int nkv, int d);
 int64_t orc_q8_block_bytes(int nkv, int d, int page);
 void orc_quantize_q8_row(const float* x, int d, int8_t* q, float* s);
 void orc_q8_store_token(void* base, int64_t t, const float* x, int nkv, int d);
+void orc_q8_store_tokens(void* base, int64_t n, const float* x, int nkv, int d);
 void orc_attn_decode(const float* Q, const void* K, const void* V, float* O, int nq, int nkv,
                      int n, int d, float scale, int pos_cur, int window, int kv_dtype,
                      int64_t tok_stride, int64_t head_stride, int64_t block_stride,

@@ -71,3 +71,29 @@ def oracle_decode(p: Decode, nthreads=0):
 
 def widen(K: np.ndarray) -> np.ndarray:
     return bf16_to_f32(K) if K.dtype == np.uint16 else K
+
+
+def make_paged(B, nq, nkv, d, lmin, lmax, page=16, seed=1234, bf16=True, spare_blocks=7):
+    """B sequences of U[lmin, lmax) cached tokens plus a new one, in shuffled
+    pages of a pool with spare blocks (fp32, or bf16 bits)."""
+    st = Stream(seed)
+    q = st.normal((B, nq, d))
+    k_new = st.normal((B, nkv, d))
+    v_new = st.normal((B, nkv, d))
+    L = st.uniform_int(lmin, lmax, B).astype(np.int32)  # context before the new token
+    n = L + 1
+    blocks = (n + page - 1) // page
+    nblk = int(blocks.sum()) + spare_blocks
+    perm = st.permutation(nblk)
+    max_blocks = int(blocks.max())
+    bt = np.zeros((B, max_blocks), np.int32)
+    o = 0
+    for b in range(B):
+        bt[b, :blocks[b]] = perm[o:o + blocks[b]]
+        o += blocks[b]
+    Kp = st.normal((nblk, nkv, page, d))
+    Vp = st.normal((nblk, nkv, page, d))
+    if bf16:
+        Kp, Vp = f32_to_bf16(Kp), f32_to_bf16(Vp)
+    return dict(q=q, k_new=k_new, v_new=v_new, n=n, bt=bt, Kp=Kp, Vp=Vp, page=page,
+                max_blocks=max_blocks, B=B, nq=nq, nkv=nkv, d=d)

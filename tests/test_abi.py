@@ -109,3 +109,46 @@ def test_python_layer_checks_sizes_without_gpu():
     cpu = torch.zeros(10)
     with pytest.raises(ValueError, match="device tensor"):
         attn.attn_decode_gqa_cache(cpu, cpu, cpu, cpu, 1, 1, 10, 128, 0.1, 9, 0)
+
+
+def test_q8_layout_sizes_match_oracle():
+    lib = L.load()
+    for nkv, d, page in [(8, 128, 16), (2, 64, 16), (1, 64, 4), (3, 128, 8), (16, 64, 32)]:
+        assert lib.molot_hip_q8_row_bytes(nkv, d) == oracle.q8_row_bytes(nkv, d)
+        assert lib.molot_hip_q8_block_bytes(nkv, d, page) == oracle.q8_block_bytes(nkv, d, page)
+    # 1024 codes + 8 scales (32 bytes, already 16-byte aligned); 3 heads: 12 -> 16 bytes
+    assert lib.molot_hip_q8_row_bytes(8, 128) == 1056
+    assert lib.molot_hip_q8_row_bytes(3, 128) == 3 * 128 + 16
+    assert lib.molot_hip_q8_block_bytes(8, 128, 16) == 8 * 16 * 128 + 4 * 8 * 16
+    assert lib.molot_hip_q8_row_bytes(0, 128) == 0
+
+
+def test_q8_validation_before_launch():
+    lib = L.load()
+    s = ctypes.c_void_p(0)
+    Q8 = L.KV_Q8
+    # d = 256: no Q8 kernels
+    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 256, 0.1, 9, 0,
+                                               Q8, s) == L.ENOTSUP
+    # element strides instead of the token-major Q8 byte layout
+    assert lib.molot_hip_attn_decode_strided(_p(), _p(), _p(), _p(), 8, 2, 10, 128, 256, 128,
+                                             0.1, 9, 0, Q8, s) == L.EINVAL
+    # the head-major entry points take no Q8 cache
+    assert lib.molot_hip_attn_decode_gqa(_p(), _p(), _p(), _p(), 8, 2, 10, 64, 0.1, Q8,
+                                         s) == L.EINVAL
+    # paged Q8 blocks stay 16-byte aligned only when nkv * page is a multiple of 4
+    assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4, 4, 8,
+                                           1, 64, 2, 0.1, 0, Q8, s) == L.EINVAL
+    assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 256, 0.1, 6, 0,
+                                          Q8, s) == L.ENOTSUP
+
+
+def test_python_kv_dtype_codes():
+    import torch
+    from molot_amd import attn
+
+    assert attn.kv_dtype_of(torch.zeros(1, dtype=torch.uint8)) == L.KV_Q8
+    assert attn.kv_dtype_of(torch.zeros(1, dtype=torch.bfloat16)) == L.KV_BF16
+    assert attn.kv_dtype_of(torch.zeros(1)) == L.KV_F32
+    with pytest.raises(TypeError):
+        attn.kv_dtype_of(torch.zeros(1, dtype=torch.float16))

@@ -15,7 +15,7 @@ import torch
 
 import oracle
 from conftest import normwise_err
-from gpu_util import dev, dev_bf16, host, make_decode, oracle_decode, widen
+from gpu_util import dev, dev_bf16, host, make_decode, make_paged, oracle_decode, widen
 from molot_amd import attn
 from molot_amd.synth import Stream, bf16_to_f32, f32_to_bf16
 
@@ -539,30 +539,6 @@ def test_repeated_calls_are_deterministic(gpu):
 
 # ---------------------------------------------------------------------------
 # paged, batched (config 4 and smaller)
-
-def make_paged(B, nq, nkv, d, lmin, lmax, page=16, seed=1234, bf16=True, spare_blocks=7):
-    st = Stream(seed)
-    q = st.normal((B, nq, d))
-    k_new = st.normal((B, nkv, d))
-    v_new = st.normal((B, nkv, d))
-    L = st.uniform_int(lmin, lmax, B).astype(np.int32)  # context before the new token
-    n = L + 1
-    blocks = (n + page - 1) // page
-    nblk = int(blocks.sum()) + spare_blocks
-    perm = st.permutation(nblk)
-    max_blocks = int(blocks.max())
-    bt = np.zeros((B, max_blocks), np.int32)
-    o = 0
-    for b in range(B):
-        bt[b, :blocks[b]] = perm[o:o + blocks[b]]
-        o += blocks[b]
-    Kp = st.normal((nblk, nkv, page, d))
-    Vp = st.normal((nblk, nkv, page, d))
-    if bf16:
-        Kp, Vp = f32_to_bf16(Kp), f32_to_bf16(Vp)
-    return dict(q=q, k_new=k_new, v_new=v_new, n=n, bt=bt, Kp=Kp, Vp=Vp, page=page,
-                max_blocks=max_blocks, B=B, nq=nq, nkv=nkv, d=d)
-
 
 def run_paged(P, inv, scale, window=0, pos=None):
     bf = P["Kp"].dtype == np.uint16

@@ -440,6 +440,46 @@ def test_q8_decode_step_appends_quantized_row():
     np.testing.assert_array_equal(Vq[pos], oracle.q8_cache(v.reshape(1, -1), nkv, d)[0])
 
 
+def test_q8_paged_is_token_major_through_a_block_table():
+    """Paged Q8 blocks ([nkv][page][d] codes, then [nkv][page] scales) read
+    through a shuffled block table give bit for bit the token-major Q8
+    attention on the same rows: pins the paged scale addressing."""
+    st = Stream(41)
+    nq, nkv, d, n, page = 16, 4, 64, 203, 16
+    Q = st.normal((nq, d))
+    K, V = kv_token_major(st, n, nkv, d, 2.0)
+    nblk = (n + page - 1) // page
+    perm = st.permutation(nblk + 3)[:nblk].astype(np.int32)
+    Kp = np.zeros((nblk + 3, nkv, page, d), np.float32)
+    Vp = np.zeros_like(Kp)
+    for i in range(nblk):
+        rows = slice(i * page, min(n, (i + 1) * page))
+        m = rows.stop - rows.start
+        Kp[perm[i], :, :m] = K[rows].reshape(m, nkv, d).transpose(1, 0, 2)
+        Vp[perm[i], :, :m] = V[rows].reshape(m, nkv, d).transpose(1, 0, 2)
+    Pk, Pv = oracle.q8_pages(Kp), oracle.q8_pages(Vp)
+    assert Pk.shape == (nblk + 3, nkv * page * (d + 4))
+    # the pages dequantize to the token-major cache's rows
+    Kd = oracle.q8_dequant(oracle.q8_cache(K, nkv, d), nkv, d)
+    Pd = oracle.q8_pages_dequant(Pk, nkv, d, page)
+    for i in range(nblk):
+        m = min(n, (i + 1) * page) - i * page
+        np.testing.assert_array_equal(Pd[perm[i], :, :m],
+                                      Kd[i * page:i * page + m].reshape(m, nkv, d).transpose(1, 0, 2))
+    for window in (0, 50):
+        a = oracle.attn_decode_paged(Q[None], Pk, Pv, perm[None], np.array([n], np.int32), None, 1,
+                                     nblk, nq, nkv, d, page, 0.1, window)[0]
+        b = oracle.attn_decode_gqa_cache(Q, oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d),
+                                         nq, nkv, n, d, 0.1, n - 1, window)
+        np.testing.assert_array_equal(a, b)
+    # one slot rewritten in place equals re-quantizing the pages with it
+    x = st.normal((nkv, d))
+    P2 = Pk.copy()
+    oracle.q8_page_store(P2, int(perm[3]), 5, x, nkv, d, page)
+    Kp[perm[3], :, 5] = x
+    np.testing.assert_array_equal(P2, oracle.q8_pages(Kp))
+
+
 def test_head_golden():
     g = golden("head_bench_check")
     n, d = int(g["n"]), int(g["d"])
