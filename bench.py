@@ -6,7 +6,9 @@ heads, head dim 128, fp32 token-major KV cache holding 16384 positions, one
 new token at pos 16384 (n = 16385 after the append), RoPE theta 500000,
 scale 1/sqrt(128), batch 1, q/K/V ~ N(0,1) from the repo's seeded generator.
 `--config c1|c3|c4|c5` measures the other BASELINE configs the same way
-(c4: 64 sequences over a paged bf16 cache, molot_hip_decode_step_paged).
+(c4: 64 sequences over a paged bf16 cache, molot_hip_decode_step_paged);
+c2q8|c4q8|c5q8 run c2, c4 and c5 over Q8 caches (int8 codes + an fp32 scale
+per KV head row); p1|p2 time the layer prefill.
 
 One step = one layer-step of the hot path through the C ABI
 (molot_hip_decode_step): RoPE of q and k, append of k/v into the cache,
@@ -57,6 +59,11 @@ CONFIGS = {
     # paged bf16 cache, 64 sequences of context U[512, 8192], shuffled 16-row pages
     "c4": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=1, sigma=1.0, batch=64,
                lmin=512, lmax=8192, page=16),
+    # the same workloads over Q8 caches (int8 codes + an fp32 scale per KV head row)
+    "c2q8": dict(nq=32, nkv=8, d=128, pos=16384, theta=500000.0, window=0, kvd=2, sigma=1.0),
+    "c5q8": dict(nq=64, nkv=8, d=128, pos=131072, theta=500000.0, window=0, kvd=2, sigma=0.5),
+    "c4q8": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=2, sigma=1.0, batch=64,
+                 lmin=512, lmax=8192, page=16),
     # prefill (gemm.h:409-446, forward.h:367-399): M prompt tokens after n0 cached
     "p1": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=0, sigma=1.0, prompt=2048,
                n0=0),
@@ -71,6 +78,10 @@ DESCR = {
     "c4": "continuous-batching decode step, 64 sequences of ctx U[512,8192], 32q/8kv/d128, "
           "bf16 KV in shuffled 16-token pages",
     "c5": "long-context GQA decode layer-step, 64q/8kv/d128 bf16 KV, pos 131072 (n=131073)",
+    "c2q8": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 Q8 KV, ctx 16384 (n=16385), batch 1",
+    "c5q8": "long-context GQA decode layer-step, 64q/8kv/d128 Q8 KV, pos 131072 (n=131073)",
+    "c4q8": "continuous-batching decode step, 64 sequences of ctx U[512,8192], 32q/8kv/d128, "
+            "Q8 KV in shuffled 16-token pages",
     "p1": "layer prefill (RoPE + append + causal attention), 2048-token prompt, 32q/8kv/d128 "
           "fp32 KV",
     "p2": "layer prefill, 512-token prompt after 16384 cached tokens, 32q/8kv/d128 fp32 KV",
@@ -112,21 +123,41 @@ def log(args, *a):
         print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def algorithmic_bytes(nq, nkv, d, n_att, s_kv):
+def row_bytes(kvd, d):
+    """Bytes of one cached KV head row: fp32, bf16, or Q8 (d codes + an fp32 scale)."""
+    return 4 * d if kvd == 0 else 2 * d if kvd == 1 else d + 4
+
+
+def algorithmic_bytes(nq, nkv, d, n_att, rb):
     """Bytes one sequence's layer-step must move (decode-attention roofline):
-    KV stream 2*nkv*n_att*d*s_kv, q read + O write 2*nq*d*4, new k/v read as
-    fp32 and written at s_kv.  The RoPE table (d/2*4) is added once per step."""
-    kv = 2 * nkv * n_att * d * s_kv
-    other = 2 * nq * d * 4 + 2 * nkv * d * (4 + s_kv)
+    KV stream 2*nkv*n_att*rb (rb = bytes per cached head row), q read + O
+    write 2*nq*d*4, new k/v read as fp32 and written as rows.  The RoPE table
+    (d/2*4) is added once per step."""
+    kv = 2 * nkv * n_att * rb
+    other = 2 * nq * d * 4 + 2 * nkv * (4 * d + rb)
     return kv, kv + other
 
 
 def kernel_label(d, nq, nkv, kvd, paged, nchunks):
     G = nq // nkv
-    gh = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
-    t = "float" if kvd == 0 else "bf16"
-    s = f"attn_kernel<{d},{gh},{t},paged={'true' if paged else 'false'},rope=true>"
+    pg = "true" if paged else "false"
+    if kvd and d in (64, 128):  # the matrix-core kernel (bf16 and Q8 caches)
+        gh = 16 if G % 16 == 0 else 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
+        s = (f"attn_mfma_kernel<{d},{gh},paged={pg},rope=true,"
+             f"q8={'true' if kvd == 2 else 'false'}>")
+    else:
+        gh = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
+        t = "float" if kvd == 0 else "bf16"
+        s = f"attn_kernel<{d},{gh},{t},paged={pg},rope=true>"
     return s + (" (then combine_kernel: split-K merge)" if nchunks > 1 else " (single chunk)")
+
+
+def synthetic_q8(st, rows, nkv, d, sigma, np):
+    """Q8 rows of the format (codes, then per-head fp32 scales): codes
+    rint(32 N(0,1)) clipped to +-127, scale sigma/32 (values ~ N(0, sigma^2))."""
+    codes = np.clip(np.rint(st.normal((rows, nkv * d)) * 32.0), -127, 127).astype(np.int8)
+    scales = np.full((rows, nkv), sigma / 32.0, np.float32)
+    return codes, scales
 
 
 # ---------------------------------------------------------------------------
@@ -139,13 +170,14 @@ def contiguous_workload(args, cfg, lib, L, torch, np):
 
     nq, nkv, d, pos = cfg["nq"], cfg["nkv"], cfg["d"], cfg["pos"]
     theta, window, kvd, sigma = cfg["theta"], cfg["window"], cfg["kvd"], cfg["sigma"]
-    s_kv = 4 if kvd == 0 else 2
+    rb = row_bytes(kvd, d)
     n = pos + 1
     t0 = max(0, pos - window + 1) if window > 0 else 0
     n_att = n - t0
-    kv_bytes, step_bytes = algorithmic_bytes(nq, nkv, d, n_att, s_kv)
+    kv_bytes, step_bytes = algorithmic_bytes(nq, nkv, d, n_att, rb)
     step_bytes += (d // 2) * 4
-    cache_bytes = 2 * n * nkv * d * s_kv
+    R = lib.molot_hip_q8_row_bytes(nkv, d) if kvd == 2 else nkv * rb  # bytes per token
+    cache_bytes = 2 * n * R
     layers = args.layers or max(2, math.ceil(COLD_BYTES / kv_bytes))
     scale = 1.0 / math.sqrt(d)
 
@@ -153,15 +185,24 @@ def contiguous_workload(args, cfg, lib, L, torch, np):
     q_h = st.normal((nq, d))
     k_h = st.normal((nkv, d))
     v_h = st.normal((nkv, d))
-    K_h = np.zeros((n, nkv * d), np.float32)
-    V_h = np.zeros_like(K_h)
-    # only the attended rows are drawn (a window's earlier rows are never read)
-    K_h[t0:pos] = st.normal((pos - t0, nkv * d), sigma)
-    V_h[t0:pos] = st.normal((pos - t0, nkv * d), sigma)
-    dt = torch.float32 if kvd == 0 else torch.bfloat16
+    if kvd == 2:
+        # token-major Q8 rows [n][R]: codes [nkv][d], then the nkv scales
+        K_h = np.zeros((n, R), np.uint8)
+        V_h = np.zeros_like(K_h)
+        for X in (K_h, V_h):
+            codes, scales = synthetic_q8(st, pos - t0, nkv, d, sigma, np)
+            X[t0:pos, :nkv * d] = codes.view(np.uint8)
+            X[t0:pos, nkv * d:nkv * d + 4 * nkv] = scales.view(np.uint8)
+    else:
+        K_h = np.zeros((n, nkv * d), np.float32)
+        V_h = np.zeros_like(K_h)
+        # only the attended rows are drawn (a window's earlier rows are never read)
+        K_h[t0:pos] = st.normal((pos - t0, nkv * d), sigma)
+        V_h[t0:pos] = st.normal((pos - t0, nkv * d), sigma)
+    dt = {0: torch.float32, 1: torch.bfloat16, 2: torch.uint8}[kvd]
 
     def to_dev(a):
-        if kvd == 0:
+        if kvd != 1:
             return torch.from_numpy(a).cuda()
         return torch.from_numpy(f32_to_bf16(a).view(np.int16)).cuda().view(torch.bfloat16)
 
@@ -211,7 +252,7 @@ def contiguous_workload(args, cfg, lib, L, torch, np):
     return SimpleNamespace(
         step=step, attention=attention, kv_bytes=kv_bytes, step_bytes=step_bytes, layers=layers,
         cache_desc=f"cache={cache_bytes / 2**20:.0f} MiB/layer dtype={dt}", paged=False,
-        head_traffic=2 * nq * n_att * d * s_kv, cpu=cpu,
+        head_traffic=2 * nq * n_att * rb, cpu=cpu,
         config={"nq": nq, "nkv": nkv, "head_dim": d, "pos": pos, "n": n, "window": window,
                 "rope_theta": theta, "batch": 1, "qkv_norms": bool(args.norms)},
         keep=(Ks, Vs, q, k_new, v_new, inv, O))
@@ -226,8 +267,8 @@ def paged_workload(args, cfg, lib, L, torch, np):
 
     nq, nkv, d, B, page = cfg["nq"], cfg["nkv"], cfg["d"], cfg["batch"], cfg["page"]
     theta, window, kvd, sigma = cfg["theta"], cfg["window"], cfg["kvd"], cfg["sigma"]
-    assert kvd == 1 and window == 0
-    s_kv = 2
+    assert kvd in (1, 2) and window == 0
+    rb = row_bytes(kvd, d)
     st = Stream(1234)
     q_h = st.normal((B, nq, d))
     k_h = st.normal((B, nkv, d))
@@ -243,20 +284,33 @@ def paged_workload(args, cfg, lib, L, torch, np):
     for b in range(B):
         bt[b, :blocks[b]] = perm[o:o + blocks[b]]
         o += blocks[b]
-    Kp_h = f32_to_bf16(st.normal((nblk, nkv, page, d), sigma))
-    Vp_h = f32_to_bf16(st.normal((nblk, nkv, page, d), sigma))
+    if kvd == 2:
+        # Q8 blocks: codes [nkv][page][d], then scales [nkv][page]
+        pools = []
+        for _ in range(2):
+            codes, scales = synthetic_q8(st, nblk * page, nkv, d, sigma, np)
+            codes = codes.reshape(nblk, page, nkv, d).transpose(0, 2, 1, 3).reshape(nblk, -1)
+            scales = scales.reshape(nblk, page, nkv).transpose(0, 2, 1).reshape(nblk, -1)
+            pools.append(np.ascontiguousarray(np.concatenate(
+                [codes.view(np.uint8), scales.view(np.uint8)], axis=1)))
+        Kp_h, Vp_h = pools
+    else:
+        Kp_h = f32_to_bf16(st.normal((nblk, nkv, page, d), sigma))
+        Vp_h = f32_to_bf16(st.normal((nblk, nkv, page, d), sigma))
 
     kv_bytes = 0
     step_bytes = (d // 2) * 4 + int(blocks.sum()) * 4  # RoPE table + block-table entries
     for b in range(B):
-        kv, tot = algorithmic_bytes(nq, nkv, d, int(n[b]), s_kv)
+        kv, tot = algorithmic_bytes(nq, nkv, d, int(n[b]), rb)
         kv_bytes += kv
         step_bytes += tot + 4  # + its seq_lens entry
-    cache_bytes = 2 * nblk * nkv * page * d * s_kv
+    cache_bytes = 2 * nblk * nkv * page * rb
     layers = args.layers or max(2, math.ceil(COLD_BYTES / kv_bytes))
     scale = 1.0 / math.sqrt(d)
 
     def to_dev_bf16(a):
+        if kvd == 2:
+            return torch.from_numpy(a).cuda()
         return torch.from_numpy(a.view(np.int16)).cuda().view(torch.bfloat16)
 
     K0, V0 = to_dev_bf16(Kp_h), to_dev_bf16(Vp_h)
@@ -307,13 +361,14 @@ def paged_workload(args, cfg, lib, L, torch, np):
 
     def cpu(args_):
         return cpu_baseline_paged(args_, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page,
-                                  theta, scale, kv_bytes)
+                                  theta, scale, kv_bytes, kvd)
 
     return SimpleNamespace(
         step=step, attention=attention, kv_bytes=kv_bytes, step_bytes=step_bytes, layers=layers,
         cache_desc=(f"{B} seqs, ctx {int(Lc.min())}..{int(Lc.max())} (sum {int(n.sum())}), "
-                    f"{nblk} pages, cache={cache_bytes / 2**20:.0f} MiB/layer bf16"),
-        paged=True, head_traffic=2 * nq * int(n.sum()) * d * s_kv, cpu=cpu,
+                    f"{nblk} pages, cache={cache_bytes / 2**20:.0f} MiB/layer "
+                    f"{'Q8' if kvd == 2 else 'bf16'}"),
+        paged=True, head_traffic=2 * nq * int(n.sum()) * rb, cpu=cpu,
         config={"nq": nq, "nkv": nkv, "head_dim": d, "batch": B, "page": page,
                 "ctx_min": int(Lc.min()), "ctx_max": int(Lc.max()), "tokens": int(n.sum()),
                 "window": window, "rope_theta": theta, "qkv_norms": bool(args.norms)},
@@ -494,9 +549,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if kvd == 0 else "bf16-kv/f32-acc",
-        "data": (f"synthetic (seeded N(0,{cfg['sigma']:g}) K/V, N(0,1) q/k/v, "
-                 "splitmix64+Box-Muller, seed 1234)"),
+        "dtype": {0: "f32", 1: "bf16-kv/f32-acc", 2: "q8-kv/f32-acc"}[kvd],
+        "data": (f"synthetic (seeded N(0,{cfg['sigma']:g}) K/V"
+                 + (" as Q8 codes rint(32 N(0,1)) with scale sigma/32" if kvd == 2 else "")
+                 + ", N(0,1) q/k/v, splitmix64+Box-Muller, seed 1234)"),
         "config": config,
         "us_per_layer_step": round(us_step, 3),
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
@@ -700,7 +756,7 @@ def cpu_baseline_contiguous(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window,
     copies = max(2, math.ceil(512 * 2**20 / per_copy))
     rows = st.normal((pos - t0, S), sigma)
     rows_v = st.normal((pos - t0, S), sigma)
-    if kvd:
+    if kvd == 1:
         rows = bf16_to_f32(f32_to_bf16(rows))
         rows_v = bf16_to_f32(f32_to_bf16(rows_v))
     Ks, Vs = [], []
@@ -747,19 +803,22 @@ def cpu_baseline_contiguous(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window,
                    f"copies of {per_copy / 2**20:.0f} MiB attended, {el:.1f} s; "
                    + ("reference headers via oracle/_ref, ThreadPool" if kind == "reference"
                       else "oracle C restatement, OpenMP static over heads")
-                   + ("; bf16 values widened to fp32 (no reference bf16 path)" if kvd else "")),
+                   + ("; bf16 values widened to fp32 (no reference bf16 path)" if kvd == 1
+                      else "; fp32 rows of the same shape (no reference Q8 cache)" if kvd == 2
+                      else "")),
     }
 
 
 def cpu_baseline_paged(args, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page, theta, scale,
-                       kv_bytes):
+                       kv_bytes, kvd=1):
     """c4 on the host cores: the reference's decode step (rope q/k, append,
     attn_decode_gqa_cache) once per sequence, over per-sequence contiguous
-    fp32 caches gathered from the pages and widened from bf16.  The reference
-    has neither a paged nor a bf16 cache, so this is the reference algorithm
-    on the same values, not a reference run of the same format; the
-    contiguous fp32 copies are 2x the GPU's bytes, and the GB/s reported is
-    the GPU workload's KV bytes over the CPU time."""
+    fp32 caches gathered from the pages and widened from bf16 (or
+    dequantized from Q8).  The reference has neither a paged nor a bf16 or
+    Q8 cache, so this is the reference algorithm on the same values, not a
+    reference run of the same format; the contiguous fp32 copies are 2x
+    (bf16) or ~4x (Q8) the GPU's bytes, and the GB/s reported is the GPU
+    workload's KV bytes over the CPU time."""
     import numpy as np
 
     import oracle
@@ -769,11 +828,19 @@ def cpu_baseline_paged(args, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page,
     B = len(n)
     S = nkv * d
     Kc, Vc = [], []
+    def widen(pages):  # [blocks][nkv][page][d] fp32 values of bf16 or Q8 pages
+        if kvd == 1:
+            return bf16_to_f32(pages)
+        m = pages.shape[0]
+        codes = pages[:, :nkv * page * d].view(np.int8).astype(np.float32)
+        sc = np.ascontiguousarray(pages[:, nkv * page * d:]).view(np.float32)
+        return codes.reshape(m, nkv, page, d) * sc.reshape(m, nkv, page, 1)
+
     for b in range(B):
         nb = int(n[b])
         blk = bt[b, :(nb + page - 1) // page]
         for src, dst in ((Kp_h, Kc), (Vp_h, Vc)):
-            x = bf16_to_f32(src[blk]).transpose(0, 2, 1, 3).reshape(-1, S)[:nb]
+            x = widen(src[blk]).transpose(0, 2, 1, 3).reshape(-1, S)[:nb]
             dst.append(np.ascontiguousarray(x))
     inv = oracle.rope_inv_freq(theta, d)
     O = np.empty((nq, d), np.float32)
@@ -809,13 +876,15 @@ def cpu_baseline_paged(args, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page,
         "cores": cores,
         "kind": kind,
         "ms_per_step": round(ms, 4),
-        "sample": (f"{steps} batch-steps of c4 ({B} sequences, each rope q/k + append + "
+        "sample": (f"{steps} batch-steps of {args.config} ({B} sequences, each rope q/k + append + "
                    f"attn_decode_gqa_cache over its contiguous fp32 cache, {fp32_mib:.0f} MiB in "
                    f"all), {el:.1f} s; "
                    + ("reference headers via oracle/_ref, ThreadPool" if kind == "reference"
                       else "oracle C restatement, OpenMP static over heads")
-                   + "; bf16 pages gathered and widened to fp32 (the reference has no paged "
-                     "or bf16 cache)"),
+                   + ("; Q8 pages gathered and dequantized to fp32 (the reference has no "
+                      "paged or Q8 cache)" if kvd == 2 else
+                      "; bf16 pages gathered and widened to fp32 (the reference has no paged "
+                      "or bf16 cache)")),
     }
 
 

@@ -357,6 +357,7 @@ struct AttnArgs {
   int64_t tok_stride, head_stride, block_stride;
   int nq, nkv, n, t0, pos, chunk, nchunks, max_blocks, page_shift, window;
   int dynamic;           // 1: waves claim blocks from a workgroup counter; 0: fixed order
+  int chunk_fast;        // 1-D grid, the KV heads of a chunk on one XCD (B = 1; see launch_pair)
   float scale;
   // the layer's norms of the fresh vectors (ROPE only; NULL / 0: none)
   const float* q_norm;   // [D] weights of the per-head q RMS norm
@@ -1191,13 +1192,25 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   float* vnew = smem + L.vnew;
   int* misc = reinterpret_cast<int*>(smem + L.misc);
 
-  const int z = blockIdx.z;  // chunk slot; chunk c = nch - 1 - z (below)
+  // chunk slot z (chunk c = nch - 1 - z, below), (KV head, subgroup) index
+  // hs and sequence b of this workgroup
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
-  const int sub = blockIdx.x % nsub;
-  const int h = blockIdx.x / nsub;
+  int z, hs, b;
+  if (a.chunk_fast) {  // workgroup id runs on XCD id % 8 (launch_pair)
+    const int HS = a.nkv * nsub;
+    const int k = (int)(blockIdx.x >> 3);
+    z = (k / HS) * 8 + (int)(blockIdx.x & 7);  // padded ids (z >= nchunks) exit below
+    hs = k % HS;
+    b = 0;
+  } else {
+    z = blockIdx.z;
+    hs = blockIdx.x;
+    b = blockIdx.y;
+  }
+  const int sub = hs % nsub;
+  const int h = hs / nsub;
   const int hq0 = h * G + sub * GH;
-  const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1227,7 +1240,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   const int cntg = max(0, min(a.chunk, cend - tb));
   const bool is_new = ROPE && c == nch - 1;
   const bool split = nch > 1;
-  const int64_t slot = (int64_t)b * gridDim.x + blockIdx.x;
+  const int64_t slot = (int64_t)b * a.nkv * nsub + hs;
 
   const E* __restrict__ Kb = reinterpret_cast<const E*>(a.k);
   const E* __restrict__ Vb = reinterpret_cast<const E*>(a.v);
@@ -1383,6 +1396,18 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   }
   lds_barrier();
 
+  int next_fixed = w + NW;
+  auto claim = [&]() -> int {
+    if (!a.dynamic) {
+      const int v = next_fixed;
+      next_fixed += NW;
+      return v;
+    }
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&misc[0], 1);
+    return __builtin_amdgcn_readfirstlane(v);
+  };
+
   // q^T as the B operand: lane l holds head l%16 (zero past GH), elements
   // 32*kk + 8*(l/16) + e (Q8: 64*(kk/2) + 16*(l/16) + 8*(kk%2) + e), in
   // three bf16 pieces
@@ -1406,17 +1431,6 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-  int next_fixed = w + NW;
-  auto claim = [&]() -> int {
-    if (!a.dynamic) {
-      const int v = next_fixed;
-      next_fixed += NW;
-      return v;
-    }
-    int v = 0;
-    if (lane == 0) v = atomicAdd(&misc[0], 1);
-    return __builtin_amdgcn_readfirstlane(v);
-  };
   float* scw = smem + L.sc + w * (2 * kTile);  // Q8: this wave's scale slots
   while (tile < ntiles) {
     // V rows into this wave's LDS region (lane: row 16u + l%16, 16-byte
@@ -2190,8 +2204,17 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   // index fastest, every XCD gets the same heads' share of every chunk and
   // sequence (equal work however the chunks of a batch differ in length),
   // and the chunk index slowest makes the XCDs stream the same rows at the
-  // same time.
-  dim3 grid(a.nkv * nsubs, B, a.nchunks);
+  // same time.  chunk_fast (token-major Q8, one sequence) groups by chunk
+  // instead: the KV heads of one token share 128-byte lines (head rows of d
+  // bytes at t*R + h*d, the token's scales after them), so all heads of a
+  // chunk go to one XCD, whose L2 then fetches each shared line once.  A 1-D
+  // grid of 8 * ceil(nchunks / 8) * heads workgroups: id runs chunk slot
+  // (id / 8 / heads) * 8 + id % 8 and head (id / 8) % heads, so chunk slot z
+  // is on XCD z % 8 whatever the chunk count, each XCD's heads of a chunk are
+  // dispatched together, and the padding ids exit at once.
+  const dim3 grid = a.chunk_fast
+                        ? dim3((unsigned)((a.nchunks + 7) / 8 * 8 * a.nkv * nsubs), 1, 1)
+                        : dim3(a.nkv * nsubs, B, a.nchunks);
   if (prof) {
     pr.a0 = prof_event();
     pr.a1 = prof_event();
@@ -2252,6 +2275,7 @@ template <int D, int GH, bool PAGED, bool ROPE, bool Q8>
 int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
   int st = plan_launch(a, D, span, GH, nsubs, B, kTile, PAGED ? 8 : 2, stream);
   if (st) return st;
+  a.chunk_fast = Q8 && !PAGED && B == 1;
   const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8);
   return launch_pair(attn_mfma_kernel<D, GH, PAGED, ROPE, Q8>, kMfmaThreads,
                      sizeof(float) * (size_t)L.total, a, GH, D, nsubs, B, PAGED, ROPE, stream);
