@@ -1104,6 +1104,18 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 constexpr int kMfmaWaves = 4;                  // waves per workgroup
 constexpr int kMfmaThreads = kMfmaWaves * 64;
 constexpr int kTile = 32;                      // cache rows per wave step
+// The matrix-core kernel's softmax runs in base 2: q is pre-scaled by
+// scale*log2(e), so a score is already x*log2(e) and p = 2^(s - m) is one
+// v_exp_f32 (relative error ~|s - m| * 2^-24, within the reference's own
+// exp, exp_avx512_ps at 1.5e-6).  Its running max moves only when a score
+// exceeds it by more than kLazyMax (p <= 2^8 otherwise): o and l always
+// share the max they were formed with, so the result is exact either way,
+// and most tiles skip the rescale.  The maxima leave the kernel in natural
+// units (m * ln 2) for the split-K merge.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kLazyMax = 8.f;
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // LDS of attn_mfma_kernel, in floats.  vt: per wave, 32 staged V rows of D
 // bf16 (16*D floats), which after the stream hold the wave's partial o;
@@ -1145,9 +1157,12 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4 c) {
 }
 
 // 16 int8 codes -> 16 bf16 (exact: |code| <= 127), bytes 0-7 into lo, 8-15
-// into hi, each in memory order.
+// into hi, each in memory order.  One v_cvt_pk_bf16_f32 per pair (its
+// rounding is the identity on these values).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t bf16_pair_exact(float a, float b) {
-  return (__float_as_uint(a) >> 16) | (__float_as_uint(b) & 0xFFFF0000u);
+  const bf16x2_t p = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, p);
 }
 __device__ __forceinline__ void i8x16_to_bf16(const u32x4& x, u32x4& lo, u32x4& hi) {
 #pragma unroll
@@ -1413,15 +1428,16 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   };
 
   // q^T as the B operand: lane l holds head l%16 (zero past GH), elements
-  // 32*kk + 8*(l/16) + e (Q8: 64*(kk/2) + 16*(l/16) + 8*(kk%2) + e), in
-  // three bf16 pieces
+  // 32*kk + 8*(l/16) + e (Q8: 64*(kk/2) + 16*(l/16) + 8*(kk%2) + e), scaled
+  // by scale*log2(e), in three bf16 pieces
+  const float qsc = a.scale * kLog2e;
   bf16x8_t qh[KK], qm[KK], ql[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int di = Q8 ? 64 * (kk >> 1) + 16 * g4 + 8 * (kk & 1) + e : 32 * kk + 8 * g4 + e;
-      const float x = m16 < GH ? qs[m16 * D + di] : 0.f;
+      const float x = m16 < GH ? qs[m16 * D + di] * qsc : 0.f;
       __bf16 hi, mid, lo;
       split3(x, hi, mid, lo);
       qh[kk][e] = hi;
@@ -1510,7 +1526,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     // the next tile's loads go out while this one is finished
     const int nx = claim();
     if (nx < ntiles) load_tile(nx);
-    // online softmax on the accumulators: lane = head l%16, rows
+    // online softmax (base 2) on the accumulators: lane = head l%16, rows
     // 16u + 4*(l/16) + r
     float sv[2][4];
     float tmax = -INFINITY;
@@ -1519,22 +1535,27 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = tile * kTile + 16 * u + 4 * g4 + r;
-        const float sc = Q8 ? a.scale * sk4[u][r] : a.scale;
-        sv[u][r] = row < cntg ? sacc[u][r] * sc : -INFINITY;
+        sv[u][r] = row < cntg ? (Q8 ? sacc[u][r] * sk4[u][r] : sacc[u][r]) : -INFINITY;
         tmax = fmaxf(tmax, sv[u][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mn = fmaxf(m_run, tmax);  // finite: a claimed tile has a row
-    const float alpha = softmax_exp(m_run - mn);
-    m_run = mn;
+    // finite: a claimed tile has a row; the first tile always moves the max
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kLazyMax) != 0) {
+      const float mn = fmaxf(m_run, tmax);
+      const float alpha = exp2_hw(m_run - mn);
+      m_run = mn;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
     bf16x8_t ph, pm, pl;
     float ps = 0.f;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = softmax_exp(sv[u][r] - mn);
+        const float p = exp2_hw(sv[u][r] - m_run);
         ps += p;
         __bf16 hi, mid, lo;
         split3(Q8 ? p * sv4[u][r] : p, hi, mid, lo);
@@ -1542,9 +1563,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
         pm[4 * u + r] = mid;
         pl[4 * u + r] = lo;
       }
-    l_run = l_run * alpha + ps;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    l_run += ps;
     __builtin_amdgcn_wave_barrier();
     // PV: V^T of the 16-row block dt by two transposed reads
 #pragma unroll
@@ -1626,10 +1645,10 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     }
     part += __shfl_xor(part, 16);
     part += __shfl_xor(part, 32);
-    const float snew = part * a.scale;
+    const float snew = part * qsc;  // base 2, as the streamed scores
     const float mn = fmaxf(m_run, snew);
-    const float alpha = softmax_exp(m_run - mn);
-    const float p = softmax_exp(snew - mn);
+    const float alpha = exp2_hw(m_run - mn);
+    const float p = exp2_hw(snew - mn);
     m_run = mn;
     l_run = l_run * alpha + (g4 == 0 ? p : 0.f);
 #pragma unroll
@@ -1646,7 +1665,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   float* red = smem + L.vt;
   if (m16 < GH) {
     if (g4 == 0) {
-      wm[w * GH + m16] = m_run;
+      wm[w * GH + m16] = m_run * kLn2;  // natural units for the merge
       wl[w * GH + m16] = l_run;
     }
 #pragma unroll
