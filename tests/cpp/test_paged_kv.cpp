@@ -1,7 +1,8 @@
 // Self-check of the paged-KV manager (include/molot_amd/paged_kv.hpp) on
 // the GPU: sequences prefilled and decoded as a continuous batch across two
 // layers, one freed and its blocks reused by a new one, against the CPU
-// oracle (oracle/attn_oracle.c) on per-sequence contiguous caches.  The
+// oracle (oracle/attn_oracle.c) on per-sequence contiguous caches of the
+// same element type -- once over bf16 pages and once over Q8 pages.  The
 // oracle's attention runs on the rows the GPU appended (read back from the
 // pages) after those rows are checked against the oracle's own append, so
 // the output comparison isolates the attention.  Run by
@@ -31,12 +32,74 @@ float bf2f(uint16_t b) {
   return f;
 }
 
-// one sequence's oracle state: a contiguous bf16 cache per layer
+// The byte formats of one token's KV row: bf16 [nkv][d], or a token-major
+// Q8 row ([nkv][d] codes, then the nkv fp32 scales, padded to 16 bytes).
+struct Fmt {
+  int kv_dtype;
+  size_t row_bytes() const {
+    return kv_dtype == MOLOT_KV_Q8 ? (size_t)orc_q8_row_bytes(kNkv, kD) : (size_t)kNkv * kD * 2;
+  }
+  // oracle append of fp32 rows x [nkv][d] into token t of cache C
+  void store(std::vector<uint8_t>& C, int t, const float* x) const {
+    if (kv_dtype == MOLOT_KV_Q8)
+      orc_q8_store_token(C.data(), t, x, kNkv, kD);
+    else
+      orc_f32_to_bf16_array(x, (uint16_t*)(C.data() + (size_t)t * row_bytes()), kNkv * kD);
+  }
+  // fp32 value of element (h, i) of a row
+  float value(const uint8_t* row, int h, int i) const {
+    if (kv_dtype == MOLOT_KV_Q8) {
+      float s;
+      std::memcpy(&s, row + (size_t)kNkv * kD + 4 * h, 4);
+      return (float)(int8_t)row[(size_t)h * kD + i] * s;
+    }
+    uint16_t b;
+    std::memcpy(&b, row + ((size_t)h * kD + i) * 2, 2);
+    return bf2f(b);
+  }
+  // the step between neighbouring values of head h's row (bf16: relative)
+  float step(const uint8_t* row, int h) const {
+    if (kv_dtype == MOLOT_KV_Q8) {
+      float s;
+      std::memcpy(&s, row + (size_t)kNkv * kD + 4 * h, 4);
+      return s;
+    }
+    return 0.f;
+  }
+  // token t of a sequence from its pages (blocks) into a token-major row
+  void read_row(const void* pages, const std::vector<int>& blocks, int t, uint8_t* out) const {
+    const size_t blk = (size_t)blocks[t / kPage];
+    const int sl = t % kPage;
+    for (int h = 0; h < kNkv; ++h) {
+      if (kv_dtype == MOLOT_KV_Q8) {
+        const size_t bb = (size_t)molot_hip_q8_block_bytes(kNkv, kD, kPage);
+        const char* base = (const char*)pages + blk * bb;
+        molot::amd::check_hip(hipMemcpy(out + (size_t)h * kD,
+                                        base + ((size_t)h * kPage + sl) * kD, kD,
+                                        hipMemcpyDeviceToHost),
+                              "D2H codes");
+        molot::amd::check_hip(
+            hipMemcpy(out + (size_t)kNkv * kD + 4 * h,
+                      base + (size_t)kNkv * kPage * kD + 4 * ((size_t)h * kPage + sl), 4,
+                      hipMemcpyDeviceToHost),
+            "D2H scale");
+      } else {
+        const size_t off = ((blk * kNkv + h) * kPage + sl) * kD * 2;
+        molot::amd::check_hip(hipMemcpy(out + (size_t)h * kD * 2, (const char*)pages + off,
+                                        kD * 2, hipMemcpyDeviceToHost),
+                              "D2H row");
+      }
+    }
+  }
+};
+
+// one sequence's oracle state: a contiguous cache per layer
 struct RefSeq {
   int len = 0;
-  std::vector<std::vector<uint16_t>> K, V;
-  RefSeq() : K(kLayers, std::vector<uint16_t>((size_t)kCap * kNkv * kD)),
-             V(kLayers, std::vector<uint16_t>((size_t)kCap * kNkv * kD)) {}
+  std::vector<std::vector<uint8_t>> K, V;
+  explicit RefSeq(const Fmt& f = Fmt{MOLOT_KV_BF16})
+      : K(kLayers, std::vector<uint8_t>((size_t)kCap * f.row_bytes())),
+        V(kLayers, std::vector<uint8_t>((size_t)kCap * f.row_bytes())) {}
 };
 
 struct Dev {
@@ -69,48 +132,44 @@ void ref_token(float* q, float* k, float* v, int pos, const float* inv, const fl
   orc_rope_apply_heads(k, kNkv, kD, pos, inv);
 }
 
-// Reads rows [r0, r1) of sequence `blocks` from a layer's bf16 pages.
-std::vector<uint16_t> read_rows(const molot::amd::PagedKVCache& kv, void* pages,
-                                const std::vector<int>& blocks, int r0, int r1) {
-  std::vector<uint16_t> out((size_t)(r1 - r0) * kNkv * kD);
-  for (int t = r0; t < r1; ++t)
-    for (int h = 0; h < kNkv; ++h) {
-      const size_t off = (((size_t)blocks[t / kPage] * kNkv + h) * kPage + t % kPage) * kD;
-      molot::amd::check_hip(hipMemcpy(out.data() + ((size_t)(t - r0) * kNkv + h) * kD,
-                                      (const uint16_t*)pages + off, kD * 2,
-                                      hipMemcpyDeviceToHost),
-                            "D2H row");
-    }
-  return out;
-}
-
-// The GPU's appended rows match the oracle's own append to a bf16 ulp (the
-// normed, rotated fp32 values may differ by an fp32 ulp before rounding),
-// then replace them so the attention is compared on identical caches.
-double adopt_rows(RefSeq& r, int layer, const std::vector<uint16_t>& gk,
-                  const std::vector<uint16_t>& gv, int r0, int r1) {
+// The GPU's appended rows [r0, r1) of one layer against the oracle's own
+// append, then copied over it so the attention is compared on identical
+// caches.  The normed, rotated fp32 values may differ by an fp32 ulp before
+// rounding: bf16 rows agree to a bf16 ulp (relative), Q8 rows to one code
+// (a scale may differ by an ulp, and a value on a rounding midpoint round
+// the other way).  Returns the worst deviation in those units.
+double adopt_rows(const Fmt& f, RefSeq& r, int layer, const molot::amd::PagedKVCache& kv,
+                  const std::vector<int>& blocks, int r0, int r1) {
+  const size_t R = f.row_bytes();
+  std::vector<uint8_t> g(R);
   double worst = 0;
   for (int side = 0; side < 2; ++side) {
-    std::vector<uint16_t>& C = side ? r.V[layer] : r.K[layer];
-    const std::vector<uint16_t>& G = side ? gv : gk;
-    for (size_t i = 0; i < G.size(); ++i) {
-      const float a = bf2f(C[(size_t)r0 * kNkv * kD + i]), b = bf2f(G[i]);
-      worst = std::fmax(worst, std::fabs(a - b) / std::fmax(1.0f, std::fabs(a)));
-      C[(size_t)r0 * kNkv * kD + i] = G[i];
+    std::vector<uint8_t>& C = side ? r.V[layer] : r.K[layer];
+    const void* pages = side ? kv.v_pages(layer) : kv.k_pages(layer);
+    for (int t = r0; t < r1; ++t) {
+      f.read_row(pages, blocks, t, g.data());
+      uint8_t* c = C.data() + (size_t)t * R;
+      for (int h = 0; h < kNkv; ++h) {
+        const float unit = f.kv_dtype == MOLOT_KV_Q8 ? std::fmax(f.step(c, h), f.step(g.data(), h))
+                                                     : 0.f;
+        for (int i = 0; i < kD; ++i) {
+          const float a = f.value(c, h, i), b = f.value(g.data(), h, i);
+          const double d = f.kv_dtype == MOLOT_KV_Q8
+                               ? std::fabs(a - b) / (1.0001 * unit)
+                               : std::fabs(a - b) / std::fmax(1.0f, std::fabs(a)) / 8e-3;
+          worst = std::fmax(worst, d);
+        }
+      }
+      std::memcpy(c, g.data(), R);
     }
   }
-  (void)r1;
   return worst;
 }
 
-}  // namespace
-
-int main() {
-  int ndev = 0;
-  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
-    std::printf("no GPU\n");
-    return 2;
-  }
+int run_scenario(int kv_dtype, const char* name) {
+  const int failures0 = failures;
+  const Fmt f{kv_dtype};
+  const int odt = kv_dtype == MOLOT_KV_Q8 ? ORC_KV_Q8 : ORC_KV_BF16;
   Rng rng(2024);
   std::vector<float> inv(kD / 2), qn(kD), kn(kD);
   orc_rope_inv_freq(500000.0f, kD, inv.data());
@@ -132,8 +191,8 @@ int main() {
   norms[0].v_norm = true;
   norms[0].eps = kEps;
 
-  molot::amd::PagedKVCache kv(kLayers, kBlocks, kNkv, kD, kPage, MOLOT_KV_BF16);
-  std::vector<RefSeq> ref(8);
+  molot::amd::PagedKVCache kv(kLayers, kBlocks, kNkv, kD, kPage, kv_dtype);
+  std::vector<RefSeq> ref(8, RefSeq(f));
   double worst_o = 0, worst_row = 0;
 
   auto prefill = [&](int id, int M) {
@@ -159,20 +218,15 @@ int main() {
         float* vm = v.data() + (size_t)m * kNkv * kD;
         ref_token(qm, km, vm, pos0 + m, inv.data(), n ? qn.data() : nullptr,
                   n ? kn.data() : nullptr, n);
-        orc_f32_to_bf16_array(km, r.K[l].data() + (size_t)(pos0 + m) * kNkv * kD, kNkv * kD);
-        orc_f32_to_bf16_array(vm, r.V[l].data() + (size_t)(pos0 + m) * kNkv * kD, kNkv * kD);
+        f.store(r.K[l], pos0 + m, km);
+        f.store(r.V[l], pos0 + m, vm);
       }
-      worst_row = std::fmax(worst_row,
-                            adopt_rows(r, l, read_rows(kv, kv.k_pages(l), kv.blocks(id), pos0,
-                                                       pos0 + M),
-                                       read_rows(kv, kv.v_pages(l), kv.blocks(id), pos0,
-                                                 pos0 + M),
-                                       pos0, pos0 + M));
+      worst_row = std::fmax(worst_row, adopt_rows(f, r, l, kv, kv.blocks(id), pos0, pos0 + M));
       std::vector<float> O((size_t)M * kNq * kD);
       orc_attn_prefill(q.data(), r.K[l].data(), r.V[l].data(), O.data(), kNq, kNkv, M, pos0 + M,
-                       kD, kScale, pos0, 0, ORC_KV_BF16, 0);
+                       kD, kScale, pos0, 0, odt, 0);
       worst_o = std::fmax(worst_o, normwise(dO.get(O.size()), O));
-      CHECK(normwise(dq.get(q.size()), q) < 2e-6, "prefill q seq %d layer %d", id, l);
+      CHECK(normwise(dq.get(q.size()), q) < 2e-6, "%s prefill q seq %d layer %d", name, id, l);
     }
     kv.end_prefill();
     r.len += M;
@@ -202,17 +256,13 @@ int main() {
         float* vb = v.data() + (size_t)b * kNkv * kD;
         ref_token(qb, kb, vb, r.len, inv.data(), n ? qn.data() : nullptr,
                   n ? kn.data() : nullptr, n);
-        orc_f32_to_bf16_array(kb, r.K[l].data() + (size_t)r.len * kNkv * kD, kNkv * kD);
-        orc_f32_to_bf16_array(vb, r.V[l].data() + (size_t)r.len * kNkv * kD, kNkv * kD);
-        worst_row = std::fmax(worst_row,
-                              adopt_rows(r, l, read_rows(kv, kv.k_pages(l), kv.blocks(ids[b]),
-                                                         r.len, r.len + 1),
-                                         read_rows(kv, kv.v_pages(l), kv.blocks(ids[b]), r.len,
-                                                   r.len + 1),
-                                         r.len, r.len + 1));
+        f.store(r.K[l], r.len, kb);
+        f.store(r.V[l], r.len, vb);
+        worst_row =
+            std::fmax(worst_row, adopt_rows(f, r, l, kv, kv.blocks(ids[b]), r.len, r.len + 1));
         std::vector<float> O((size_t)kNq * kD);
         orc_attn_decode(qb, r.K[l].data(), r.V[l].data(), O.data(), kNq, kNkv, r.len + 1, kD,
-                        kScale, r.len, 0, ORC_KV_BF16, (int64_t)kNkv * kD, kD, 0, nullptr, 0, 0);
+                        kScale, r.len, 0, odt, (int64_t)kNkv * kD, kD, 0, nullptr, 0, 0);
         std::vector<float> g(got.begin() + (size_t)b * kNq * kD,
                              got.begin() + (size_t)(b + 1) * kNq * kD);
         worst_o = std::fmax(worst_o, normwise(g, O));
@@ -230,24 +280,25 @@ int main() {
   const int freed = kv.free_blocks();
   const int b_blocks = (int)kv.blocks(Bq).size();
   kv.free_sequence(Bq);
-  CHECK(kv.free_blocks() == freed + b_blocks, "freed blocks %d", kv.free_blocks());
+  CHECK(kv.free_blocks() == freed + b_blocks, "%s freed blocks %d", name, kv.free_blocks());
   const int Dq = kv.add_sequence();
-  CHECK(Dq == Bq, "sequence id reused (%d)", Dq);
-  ref[Dq] = RefSeq{};
+  CHECK(Dq == Bq, "%s sequence id reused (%d)", name, Dq);
+  ref[Dq] = RefSeq(f);
   prefill(Dq, 50);  // lands in B's freed blocks
   for (int s = 0; s < 4; ++s) decode({A, C, Dq});
   decode({C});
-  CHECK(kv.length(A) == 30 && kv.length(C) == 16 && kv.length(Dq) == 54, "lengths %d %d %d",
-        kv.length(A), kv.length(C), kv.length(Dq));
-  CHECK(worst_o < 1e-5, "paged outputs vs oracle: normwise %g", worst_o);
-  CHECK(worst_row <= 8e-3, "appended rows vs oracle: %g", worst_row);
-  std::printf("[%s] PagedKVCache: 4 sequences, 2 layers, prefill + 11 decode steps, block "
-              "reuse: max normwise err %.2e, rows within %.1e\n",
-              failures ? "FAIL" : "ok", worst_o, worst_row);
+  CHECK(kv.length(A) == 30 && kv.length(C) == 16 && kv.length(Dq) == 54, "%s lengths %d %d %d",
+        name, kv.length(A), kv.length(C), kv.length(Dq));
+  CHECK(worst_o < 1e-5, "%s paged outputs vs oracle: normwise %g", name, worst_o);
+  CHECK(worst_row <= 1.0, "%s appended rows vs oracle: %g of the allowed deviation", name,
+        worst_row);
+  std::printf("[%s] PagedKVCache %s: 4 sequences, 2 layers, prefill + 11 decode steps, block "
+              "reuse: max normwise err %.2e, rows within %.2f of the allowed deviation\n",
+              failures > failures0 ? "FAIL" : "ok", name, worst_o, worst_row);
 
   // a full pool reports what a full contiguous cache does (forward.h:570)
   {
-    molot::amd::PagedKVCache small(1, 2, kNkv, kD, kPage, MOLOT_KV_BF16);
+    molot::amd::PagedKVCache small(1, 2, kNkv, kD, kPage, kv_dtype);
     const int s = small.add_sequence();
     bool threw = false;
     try {
@@ -255,8 +306,21 @@ int main() {
     } catch (const std::runtime_error& e) {
       threw = std::strcmp(e.what(), "fwd: KV cache full") == 0;
     }
-    CHECK(threw, "full pool did not throw 'fwd: KV cache full'");
+    CHECK(threw, "%s full pool did not throw 'fwd: KV cache full'", name);
   }
+  return failures - failures0;
+}
+
+}  // namespace
+
+int main() {
+  int ndev = 0;
+  if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+    std::printf("no GPU\n");
+    return 2;
+  }
+  run_scenario(MOLOT_KV_BF16, "bf16");
+  run_scenario(MOLOT_KV_Q8, "Q8");
   std::printf(failures ? "FAILED (%d)\n" : "PASSED\n", failures);
   return failures ? 1 : 0;
 }
