@@ -1724,6 +1724,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
   constexpr int CPT = (CH + NT - 1) / NT;
   constexpr bool Q8 = std::is_same<T, q8_t>::value;
   static_assert(CH % NT == 0 || CH < NT, "whole chunks per thread");
+  static_assert(KT % 16 == 0 && (D / VW) % 4 == 0 && CH % 64 == 0, "chunk mapping");
   __shared__ __attribute__((aligned(16))) float ks[KT * KSR];
   __shared__ __attribute__((aligned(16))) float vs[D * VSR];
 
@@ -1766,7 +1767,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
     for (int i = 0; i < 4; ++i) qv[4 * J + i] = x[i];
   }
 
-  // tile loads: chunk c = tid + NT*i is key c / (D/VW), elements VW*(c % (D/VW))
+  // tile loads: chunk c = tid + NT*i.  Within a wave, lanes l and l + 16*x
+  // hold keys l%16 (+16 per 64 chunks, up to KT) and element groups l/16 + 4
+  // per KT/16 such blocks: each load instruction reads 64 contiguous bytes
+  // of 16 rows, and the transposed V stores of 16 lanes hit 16 banks (one
+  // key per lane; a key-major mapping put 16 lanes of one key on one bank).
+  auto chunk_of = [&](int c, int& key, int& e) {
+    constexpr int KT16 = KT / 16;
+    key = (c & 15) + 16 * ((c >> 6) % KT16);
+    e = VW * (((c >> 4) & 3) + 4 * ((c >> 6) / KT16));
+  };
   const T* Kb = reinterpret_cast<const T*>(a.k);
   const T* Vb = reinterpret_cast<const T*>(a.v);
   // Q8 byte layouts: token-major rows of R bytes, paged blocks of BB bytes
@@ -1798,7 +1808,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + NT * i;
       if (CH < NT && c >= CH) break;
-      const int key = c / (D / VW), e = VW * (c % (D / VW));
+      int key, e;
+      chunk_of(c, key, e);
       const int t = min(tk + key, kt_hi - 1);  // rows past the range: the last one (masked)
       int64_t soff = 0;
       const int64_t off = row_off(t, soff) + e;
@@ -1815,7 +1826,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + NT * i;
       if (CH < NT && c >= CH) break;
-      const int key = c / (D / VW), e = VW * (c % (D / VW));
+      int key, e;
+      chunk_of(c, key, e);
       float kx[VW], vx[VW];
       KVT<T>::unpack(kreg[i], kx);
       KVT<T>::unpack(vreg[i], vx);
