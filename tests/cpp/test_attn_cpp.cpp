@@ -3,9 +3,12 @@
 // (bench/bench.cc:35-43: CHECK counts failures, exit status 1 on any).
 // The checker is the CPU oracle (oracle/attn_oracle.c), linked as a test
 // dependency.  Run by tests/test_cpp_layer.py.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 #include <vector>
 
@@ -96,6 +99,55 @@ int main() {
       std::printf("[%s] DeviceKV 40 decode steps with q/k/v norms: max normwise err %.2e\n",
                   wn < 1e-5 ? "ok" : "FAIL", wn);
       (void)hipFree(w_d);
+    }
+
+    // ---- 1c. a Q8 cache (rows quantized as quant.h:34-50) ----
+    // Each step's appended k and v rows against the oracle's quantizer (the
+    // rotated k may differ by an fp32 ulp before quantization: codes within
+    // one, scales within an ulp), then the GPU's bytes replace the oracle's
+    // so the attention is compared on identical caches.
+    {
+      const int R = orc_q8_row_bytes(nkv, d);
+      molot::amd::DeviceKV kvq(cap, nkv, d, MOLOT_KV_Q8);
+      std::vector<uint8_t> Kq((size_t)cap * R, 0), Vq((size_t)cap * R, 0), row(R);
+      double wq = 0, sdiff = 0;
+      int cdiff = 0;
+      for (int pos = 0; pos < 48; ++pos) {
+        std::vector<float> q(nq * d), k(nkv * d), v(nkv * d), ao(nq * d), ao_ref(nq * d);
+        rng.normal(q);
+        rng.normal(k);
+        rng.normal(v);
+        std::vector<float> q_ref = q, k_ref = k;
+        kvq.decode(q.data(), k.data(), v.data(), ao.data(), nq, pos, inv_d, scale, 0);
+        orc_decode_step(q_ref.data(), k_ref.data(), v.data(), Kq.data(), Vq.data(),
+                        ao_ref.data(), nq, nkv, d, pos, pos, inv.data(), scale, 0, ORC_KV_Q8, 1);
+        for (int side = 0; side < 2; ++side) {
+          std::vector<uint8_t>& C = side ? Vq : Kq;
+          const char* src = (const char*)(side ? kvq.v : kvq.k) + (size_t)pos * R;
+          molot::amd::check_hip(hipMemcpy(row.data(), src, R, hipMemcpyDeviceToHost), "D2H row");
+          uint8_t* ref_row = C.data() + (size_t)pos * R;
+          for (int i = 0; i < nkv * d; ++i)
+            cdiff = std::max(cdiff, std::abs((int)(int8_t)row[i] - (int)(int8_t)ref_row[i]));
+          for (int h = 0; h < nkv; ++h) {
+            float a, b;
+            std::memcpy(&a, row.data() + nkv * d + 4 * h, 4);
+            std::memcpy(&b, ref_row + nkv * d + 4 * h, 4);
+            sdiff = std::fmax(sdiff, std::fabs(a - b) / b);
+          }
+          std::memcpy(ref_row, row.data(), R);
+        }
+        std::vector<float> o2(nq * d);
+        orc_attn_decode(q_ref.data(), Kq.data(), Vq.data(), o2.data(), nq, nkv, pos + 1, d, scale,
+                        pos, 0, ORC_KV_Q8, 0, 0, 0, nullptr, 0, 1);
+        wq = std::fmax(wq, normwise(ao, o2));
+        CHECK(normwise(q, q_ref) < 1e-6, "Q8: rotated q differs at pos %d", pos);
+      }
+      CHECK(cdiff <= 1 && sdiff <= 1e-6, "Q8 appended rows: codes off by %d, scales by %g", cdiff,
+            sdiff);
+      CHECK(wq < 1e-5, "DeviceKV Q8 decode normwise err %g", wq);
+      std::printf("[%s] DeviceKV Q8 48 decode steps: max normwise err %.2e, appended codes "
+                  "within %d\n",
+                  (wq < 1e-5 && cdiff <= 1 && sdiff <= 1e-6) ? "ok" : "FAIL", wq, cdiff);
     }
 
     // ---- 2. attn.h drop-in on the same cache, host q/o, sliding window ----
