@@ -19,6 +19,7 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -615,7 +616,8 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
     const int g = __builtin_amdgcn_readfirstlane(g_[i]);
     const float mw_l = lane < NW ? wm[lane * GH + g] : -INFINITY;
     const float m = group_max<NW <= 16 ? 16 : 64>(mw_l);  // lanes >= NW hold -inf
-    const float e_l = lane < NW ? softmax_exp(mw_l - m) : 0.f;  // waves without rows: 0
+    // waves without rows weigh 0 (also when no wave of the chunk has one)
+    const float e_l = lane < NW && mw_l != -INFINITY ? softmax_exp(mw_l - m) : 0.f;
     const float l = group_sum<NW <= 16 ? 16 : 64>(lane < NW ? e_l * wl[lane * GH + g] : 0.f);
     float o = 0.f;
 #pragma unroll
@@ -1292,10 +1294,26 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       return reinterpret_cast<const float*>(p + (int64_t)t * a.tok_stride);
     }
   };
-  // Rows past the chunk end load the chunk's last row (row tb of an empty
-  // chunk): every wave issues the same loads on every path.
-  const int rmax = max(cntg - 1, 0);
-  const int ntiles = (cntg + kTile - 1) / kTile;
+  // Row mapping.  Paged: the chunk's rows [tb, tb + cntg), in order.  A
+  // contiguous cache: tile k of chunk c is the range's 32-row tile
+  // c + k*nch (cyclic), so at any moment the launch's workgroups read
+  // neighbouring tiles (a streaming probe of c5's layout: 5.17 TB/s with
+  // each chunk one block of rows, 5.78 TB/s cyclic).  Rows past the end load
+  // the last row of the range (the first of an empty one): every wave issues
+  // the same loads on every path.
+  const int rlim = PAGED ? cntg : cend - t0;  // rows of the chunk / of the whole range
+  const int rfirst = PAGED ? tb : t0;
+  const int rmax = max(rlim - 1, 0);
+  int ntiles;
+  if constexpr (PAGED) {
+    ntiles = (cntg + kTile - 1) / kTile;
+  } else {
+    const int gt = (rlim + kTile - 1) / kTile;  // tiles of the range
+    ntiles = c < gt ? (gt - 1 - c) / nch + 1 : 0;
+  }
+  auto tile_row = [&](int tile) -> int {  // first row of a tile, from rfirst
+    return PAGED ? tile * kTile : (c + tile * nch) * kTile;
+  };
   u32x4 kr[2][KL], vr[2][KL];
   float skr[2] = {0.f, 0.f}, svr[2] = {0.f, 0.f};  // Q8: scales of this lane's A-rows
   // Rows load without the streaming hint here (measured: c4 bf16 -8%, c5q8
@@ -1306,14 +1324,14 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     if constexpr (Q8) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int t = tb + min(tile * kTile + 16 * u + m16, rmax);
+        const int t = rfirst + min(tile_row(tile) + 16 * u + m16, rmax);
         skr[u] = *sc_ptr(Kb, t);
         svr[u] = *sc_ptr(Vb, t);
       }
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int t = tb + min(tile * kTile + 16 * u + m16, rmax);
+      const int t = rfirst + min(tile_row(tile) + 16 * u + m16, rmax);
       const E* pk = row_ptr(Kb, t);
       const E* pv = row_ptr(Vb, t);
       if constexpr (Q8) {
@@ -1534,8 +1552,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = tile * kTile + 16 * u + 4 * g4 + r;
-        sv[u][r] = row < cntg ? (Q8 ? sacc[u][r] * sk4[u][r] : sacc[u][r]) : -INFINITY;
+        const int row = tile_row(tile) + 16 * u + 4 * g4 + r;
+        sv[u][r] = row < rlim ? (Q8 ? sacc[u][r] * sk4[u][r] : sacc[u][r]) : -INFINITY;
         tmax = fmaxf(tmax, sv[u][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
@@ -2169,7 +2187,8 @@ int pick_gh(int G) {
 
 // Tokens per chunk: enough chunks that the launch holds `wpc` workgroups
 // per CU (one by default: a workgroup fills its CU), rounded up to a
-// multiple of `align` rows.
+// multiple of `align` rows (a forced size too: the matrix-core kernel deals
+// 32-row tiles to the chunks, and every chunk must get one).
 int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
   int chunk = g_split_chunk;
   if (chunk <= 0) {
@@ -2177,8 +2196,8 @@ int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
     long nch = (target + rows_of_wgs - 1) / rows_of_wgs;
     if (nch < 1) nch = 1;
     chunk = (int)((span + nch - 1) / nch);
-    chunk = (chunk + align - 1) / align * align;
   }
+  chunk = (chunk + align - 1) / align * align;
   if (chunk > kMaxChunk) chunk = kMaxChunk;
   if (chunk < 8) chunk = 8;
   return chunk;
@@ -2186,18 +2205,36 @@ int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
 
 // Chunking + workspace of one launch.  `span` bounds every sequence's row
 // range tiled by chunks (cache rows only when the kernel folds in the new
-// token); B * nkv * subgroups slots share each chunk index.
+// token); B * nkv * subgroups slots share each chunk index.  `cyclic`: the
+// kernel deals `align`-row tiles to the chunks round robin (the matrix-core
+// kernel on a contiguous cache), so only the chunk count matters: the
+// workgroup target's, at most one chunk per tile (a.chunk is then nominal).
 int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int align, int wpc,
-                void* stream) {
+                void* stream, bool cyclic = false) {
   const int rows = a.nkv * nsubs * B;
-  a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, wpc);
-  a.nchunks = span > 0 ? (span + a.chunk - 1) / a.chunk : 1;
-  // bound the chunk count (grid x, and the combine's per-pair loop)
-  while (a.nchunks > kMaxChunks && a.chunk < kMaxChunk) {
-    a.chunk *= 2;
-    a.nchunks = (span + a.chunk - 1) / a.chunk;
+  if (cyclic) {
+    const long tiles = span > 0 ? ((long)span + align - 1) / align : 1;
+    long nch;
+    if (g_split_chunk > 0) {
+      const long ch = ((long)g_split_chunk + align - 1) / align * align;
+      nch = span > 0 ? (span + ch - 1) / ch : 1;
+    } else {
+      const long target = (long)(g_wgs_per_cu > 0 ? g_wgs_per_cu : wpc) * num_cus();
+      nch = (target + rows - 1) / rows;
+    }
+    nch = std::max(1L, std::min({nch, tiles, (long)kMaxChunks}));
+    a.nchunks = (int)nch;
+    a.chunk = (int)((tiles + nch - 1) / nch * align);
+  } else {
+    a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, wpc);
+    a.nchunks = span > 0 ? (span + a.chunk - 1) / a.chunk : 1;
+    // bound the chunk count (grid x, and the combine's per-pair loop)
+    while (a.nchunks > kMaxChunks && a.chunk < kMaxChunk) {
+      a.chunk *= 2;
+      a.nchunks = (span + a.chunk - 1) / a.chunk;
+    }
+    if (a.nchunks > kMaxChunks) return MOLOT_ENOTSUP;
   }
-  if (a.nchunks > kMaxChunks) return MOLOT_ENOTSUP;
   a.part_o = nullptr;
   a.part_ml = nullptr;
   a.qrot = nullptr;
@@ -2308,7 +2345,7 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
 // length, and more, shorter chunks even out the CUs' shares).
 template <int D, int GH, bool PAGED, bool ROPE, bool Q8>
 int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
-  int st = plan_launch(a, D, span, GH, nsubs, B, kTile, PAGED ? 8 : 2, stream);
+  int st = plan_launch(a, D, span, GH, nsubs, B, kTile, PAGED ? 8 : 2, stream, !PAGED);
   if (st) return st;
   a.chunk_fast = Q8 && !PAGED && B == 1;
   const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8);
