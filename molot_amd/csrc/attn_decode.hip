@@ -749,24 +749,48 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   V16 kA[KS][NV], vA[VS], kB[KS][NV], vB[VS];
   // Every wave issues the same sequence of global loads on every path: the
   // compiler counts outstanding loads per path and, where paths merge with
-  // different counts, waits for all of them.  Rows past the chunk end (a
-  // partial block, or a block past the last) load the chunk's last row
-  // instead (row tb of an empty chunk): no branch around the loads, no extra
-  // HBM traffic (lines of a row already read), and a probability of
-  // e^-inf = 0 where they are scored at all.
-  const int rmax = max(cntg - 1, 0);
+  // different counts, waits for all of them.  Rows past the end (a partial
+  // block, or a block past the last) load the last row instead (the first
+  // of an empty range): no branch around the loads, no extra HBM traffic
+  // (lines of a row already read), and a probability of e^-inf = 0 where
+  // they are scored at all.
+  // Row mapping.  Paged: the chunk's rows [tb, tb + cntg), in order.  A
+  // contiguous cache: the chunk's local row lr lies in its (lr/32)-th 32-row
+  // group, the range's group c + (lr/32)*nch (groups dealt round robin, so
+  // the launch's workgroups read neighbouring rows at any moment; blocks of
+  // RB rows never straddle a group).
+  static_assert(32 % RB == 0, "blocks within 32-row groups");
+  const int rlim = PAGED ? cntg : cend - t0;  // rows of the chunk / of the whole range
+  const int rfirst = PAGED ? tb : t0;
+  const int rmax = max(rlim - 1, 0);
+  auto gmap = [&](int lr) -> int {  // local row -> row from rfirst
+    return PAGED ? lr : (c + (lr >> 5) * nch) * 32 + (lr & 31);
+  };
+  // Local rows of this chunk: its valid rows come first, so every block
+  // below nblk starts with a valid row (a block of no valid rows would meet
+  // m_run = -inf with a -inf score: e^(-inf - -inf) is NaN).  The chunk
+  // holding the range's last group counts only that group's valid rows.
+  int nrows = cntg;
+  if constexpr (!PAGED) {
+    const int groups = (rlim + 31) / 32;
+    nrows = 0;
+    if (c < groups) {
+      const int last = (groups - 1 - c) / nch;  // local index of the chunk's last group
+      nrows = 32 * last + min(32, rlim - 32 * (c + last * nch));
+    }
+  }
   auto load_block = [&](V16 (&kr)[KS][NV], V16 (&vr)[VS], int rbase) {
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-      const T* p = row_ptr(Kb, tb + min(rbase + k * RPS + rr, rmax));
+      const T* p = row_ptr(Kb, rfirst + min(gmap(rbase + k * RPS + rr), rmax));
 #pragma unroll
       for (int v = 0; v < NV; ++v) kr[k][v] = load16(p + (v * LPR + s) * VW);
     }
 #pragma unroll
     for (int k = 0; k < VS; ++k)
-      vr[k] = load16(row_ptr(Vb, tb + min(rbase + k * RPI + rs, rmax)) + cs * VW);
+      vr[k] = load16(row_ptr(Vb, rfirst + min(gmap(rbase + k * RPI + rs), rmax)) + cs * VW);
   };
-  const int nblk = (cntg + RB - 1) / RB;
+  const int nblk = (nrows + RB - 1) / RB;
   // The prologue's own global loads go first: loads retire in order, so
   // waiting for them does not also wait for the K/V blocks issued next.
   constexpr int QV = GH * D / 4;  // float4s of q of the group
@@ -913,7 +937,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
           for (int g = 0; g < GH; ++g) d[g] = fmaf(qr[g][v * VW + e], x[e], d[g]);
       }
-      const bool valid = rbase + k * RPS + rr < cntg;
+      const bool valid = rbase + k * RPS + rr < nrows;
 #pragma unroll
       for (int g = 0; g < GH; ++g) {
         const float t = group_sum<LPR>(d[g]) * a.scale;
@@ -2333,7 +2357,8 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
 
 template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
 int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
-  int st = plan_launch(a, D, span, GH, nsubs, B, C::RB, 1, stream);
+  // contiguous caches: 32-row groups dealt round robin (the kernel's gmap)
+  int st = plan_launch(a, D, span, GH, nsubs, B, PAGED ? C::RB : 32, 1, stream, !PAGED);
   if (st) return st;
   const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED);
   return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, C>, C::NT, sizeof(float) * (size_t)L.total,
