@@ -153,6 +153,27 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
+// Wave-wide max / sum with DPP only (no LDS round trips): the quad and
+// mirror steps reduce each row of 16 lanes, row_bcast:15 and row_bcast:31
+// carry the partial results up to lane 63, which readlane broadcasts.
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+  auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
+  v = op(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+  v = op(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+  v = op(v, dpp_f<0x141>(v));  // row_half_mirror
+  v = op(v, dpp_f<0x140>(v));  // row_mirror
+  // row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3; rows
+  // outside the mask keep their value (old = v)
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(MAX ? -INFINITY : 0.f),
+                                                       __float_as_int(v), 0x142, 0xA, 0xF,
+                                                       false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(MAX ? -INFINITY : 0.f),
+                                                       __float_as_int(v), 0x143, 0xC, 0xF,
+                                                       false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // exp used by the softmax (full-accuracy device expf).
 __device__ __forceinline__ float softmax_exp(float x) { return expf(x); }
 
@@ -1026,43 +1047,37 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     }
   }
 
-  // ---- 3. the new token: appended to the cache (subgroup 0; no workgroup
-  // reads that slot in this launch) and folded in by wave 0 from LDS ----
-  if (is_new && sub == 0 && tid < D) {
-    const int slot_row = n - 1;
-    int64_t off;
-    if constexpr (PAGED) {
-      const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
-      off = blk * a.block_stride + hoff +
-            (int64_t)(slot_row & ((1 << a.page_shift) - 1)) * a.tok_stride;
-    } else {
-      off = (int64_t)slot_row * a.tok_stride + hoff;
-    }
-    if constexpr (sizeof(T) == 2) {  // exact bf16 values: the rounding returns their bits
-      reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
-      reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
-    } else {
-      reinterpret_cast<float*>(a.k)[off + tid] = knew[tid];
-      reinterpret_cast<float*>(a.v)[off + tid] = vnew[tid];
-    }
-  }
+  // ---- 3. the new token, folded in by wave 0 from LDS (its append to the
+  // cache comes last, below) ----
   if (is_new && w == 0) {
+    // LDS reads first, unconditional and vector-wide: the lanes of PV row 0
+    // add the row's values, the others add 0 (a select per element, not a
+    // branch around each read)
+    const float one = rs == 0 ? 1.f : 0.f;
+    float vx[VW];
+#pragma unroll
+    for (int e4 = 0; e4 < VW; e4 += 4) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(vnew + cs * VW + e4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) vx[e4 + e] = t[e] * one;
+    }
+    float part[GH];
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
-      float part = 0.f;
+      part[g] = 0.f;
 #pragma unroll
-      for (int j = lane; j < D; j += 64) part = fmaf(qs[g * D + j], knew[j], part);
+      for (int j = lane; j < D; j += 64) part[g] = fmaf(qs[g * D + j], knew[j], part[g]);
+    }
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
-      const float snew = part * a.scale;
+    for (int g = 0; g < GH; ++g) {
+      const float snew = wave_reduce<false>(part[g]) * a.scale;
       const float mn = fmaxf(m_run[g], snew);
       const float alpha = softmax_exp(m_run[g] - mn);
       const float p = softmax_exp(snew - mn);
       m_run[g] = mn;
-      l_run[g] = l_run[g] * alpha + (rs == 0 ? p : 0.f);
+      l_run[g] = l_run[g] * alpha + p * one;
 #pragma unroll
-      for (int e = 0; e < VW; ++e)
-        acc[g][e] = acc[g][e] * alpha + (rs == 0 ? p * vnew[cs * VW + e] : 0.f);
+      for (int e = 0; e < VW; ++e) acc[g][e] = acc[g][e] * alpha + p * vx[e];
     }
   }
 
@@ -1093,6 +1108,29 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   }
   lds_barrier();
   finish_chunk<D, GH, NW, NT, ROPE>(a, wm, wl, red, P, qs, tid, lane, split, slot, c, qrow0);
+
+  // ---- 6. the append (subgroup 0; no workgroup reads that slot in this
+  // launch).  Last, because nothing may wait for these stores: vmcnt counts
+  // stores too, and a wait placed after them for an older load would hold
+  // the fold and the merge until the stores complete. ----
+  if (is_new && sub == 0 && tid < D) {
+    const int slot_row = n - 1;
+    int64_t off;
+    if constexpr (PAGED) {
+      const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
+      off = blk * a.block_stride + hoff +
+            (int64_t)(slot_row & ((1 << a.page_shift) - 1)) * a.tok_stride;
+    } else {
+      off = (int64_t)slot_row * a.tok_stride + hoff;
+    }
+    if constexpr (sizeof(T) == 2) {  // exact bf16 values: the rounding returns their bits
+      reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
+      reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
+    } else {
+      reinterpret_cast<float*>(a.k)[off + tid] = knew[tid];
+      reinterpret_cast<float*>(a.v)[off + tid] = vnew[tid];
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1628,55 +1666,34 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     tile = nx;
   }
 
-  // ---- the new token: appended by subgroup 0, folded in by wave 0 ----
-  const bool store_new = is_new && sub == 0 && (Q8 ? w == 0 : tid < D);
-  int64_t off = 0;                    // element (Q8: byte) offset of the new row
-  [[maybe_unused]] int64_t soff = 0;  // Q8: byte offset of its scale
-  if (store_new) {
-    const int slot_row = n - 1;
-    if constexpr (PAGED) {
-      const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
-      const int sl = slot_row & ((1 << a.page_shift) - 1);
-      off = blk * a.block_stride + hoff + (int64_t)sl * a.tok_stride;
-      soff = blk * a.block_stride + a.sc_off + h * a.sc_head + 4 * sl;
-    } else {
-      off = (int64_t)slot_row * a.tok_stride + hoff;
-      soff = (int64_t)slot_row * a.tok_stride + a.sc_off + h * a.sc_head;
-    }
-  }
-  if constexpr (!Q8) {
-    if (store_new) {
-      reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
-      reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
-    }
-  } else if (is_new && w == 0) {
-    // quantize the k and v rows as the cache holds them; LDS gets code * s
-    constexpr int EPL = D / 64;
-    float kx[EPL], vx[EPL];
-    float ka = 0.f, va = 0.f;
+  // ---- the new token: folded in by wave 0 (appended by subgroup 0 at the
+  // very end, like attn_kernel's append: nothing may wait for those stores) ----
+  [[maybe_unused]] int kcode[D / 64], vcode[D / 64];  // Q8: the row's codes
+  [[maybe_unused]] float kscale = 0.f, vscale = 0.f;  // Q8: and scales
+  if constexpr (Q8) {
+    if (is_new && w == 0) {
+      // quantize the k and v rows as the cache holds them; LDS gets code * s
+      constexpr int EPL = D / 64;
+      float kx[EPL], vx[EPL];
+      float ka = 0.f, va = 0.f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      kx[e] = knew[lane + 64 * e];
-      vx[e] = vnew[lane + 64 * e];
-      ka = fmaxf(ka, fabsf(kx[e]));
-      va = fmaxf(va, fabsf(vx[e]));
-    }
-    const float ks = q8_scale(group_max<64>(ka)), vs = q8_scale(group_max<64>(va));
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      const int kc = q8_code(kx[e], ks), vc = q8_code(vx[e], vs);
-      knew[lane + 64 * e] = (float)kc * ks;
-      vnew[lane + 64 * e] = (float)vc * vs;
-      if (store_new) {
-        reinterpret_cast<int8_t*>(a.k)[off + lane + 64 * e] = (int8_t)kc;
-        reinterpret_cast<int8_t*>(a.v)[off + lane + 64 * e] = (int8_t)vc;
+      for (int e = 0; e < EPL; ++e) {
+        kx[e] = knew[lane + 64 * e];
+        vx[e] = vnew[lane + 64 * e];
+        ka = fmaxf(ka, fabsf(kx[e]));
+        va = fmaxf(va, fabsf(vx[e]));
       }
+      kscale = q8_scale(group_max<64>(ka));
+      vscale = q8_scale(group_max<64>(va));
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        kcode[e] = q8_code(kx[e], kscale);
+        vcode[e] = q8_code(vx[e], vscale);
+        knew[lane + 64 * e] = (float)kcode[e] * kscale;
+        vnew[lane + 64 * e] = (float)vcode[e] * vscale;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the fold reads other lanes' rows
     }
-    if (store_new && lane == 0) {
-      *reinterpret_cast<float*>(reinterpret_cast<char*>(a.k) + soff) = ks;
-      *reinterpret_cast<float*>(reinterpret_cast<char*>(a.v) + soff) = vs;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the fold reads other lanes' rows
   }
   if (is_new && w == 0) {
     float part = 0.f;
@@ -1716,6 +1733,36 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   }
   lds_barrier();
   finish_chunk<D, GH, NW, NT, ROPE>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c, qrow0);
+
+  // ---- the append, last ----
+  const bool store_new = is_new && sub == 0 && (Q8 ? w == 0 : tid < D);
+  if (store_new) {
+    const int slot_row = n - 1;
+    int64_t off, soff;  // element (Q8: byte) offset of the row; Q8: of its scale
+    if constexpr (PAGED) {
+      const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
+      const int sl = slot_row & ((1 << a.page_shift) - 1);
+      off = blk * a.block_stride + hoff + (int64_t)sl * a.tok_stride;
+      soff = blk * a.block_stride + a.sc_off + h * a.sc_head + 4 * sl;
+    } else {
+      off = (int64_t)slot_row * a.tok_stride + hoff;
+      soff = (int64_t)slot_row * a.tok_stride + a.sc_off + h * a.sc_head;
+    }
+    if constexpr (!Q8) {
+      reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
+      reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) {
+        reinterpret_cast<int8_t*>(a.k)[off + lane + 64 * e] = (int8_t)kcode[e];
+        reinterpret_cast<int8_t*>(a.v)[off + lane + 64 * e] = (int8_t)vcode[e];
+      }
+      if (lane == 0) {
+        *reinterpret_cast<float*>(reinterpret_cast<char*>(a.k) + soff) = kscale;
+        *reinterpret_cast<float*>(reinterpret_cast<char*>(a.v) + soff) = vscale;
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1988,27 +2035,6 @@ constexpr int kCombPairs = 64;                          // pairs per workgroup
 constexpr int kCombPhases = kCombThreads / kCombPairs;  // threads per pair
 constexpr int kCombRound = 8;                           // o loads in flight per thread
 constexpr int kMaxChunks = 4096;
-
-// Wave-wide max / sum with DPP only (no LDS round trips): the quad and
-// mirror steps reduce each row of 16 lanes, row_bcast:15 and row_bcast:31
-// carry the partial results up to lane 63, which readlane broadcasts.
-template <bool MAX>
-__device__ __forceinline__ float wave_reduce(float v) {
-  auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
-  v = op(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
-  v = op(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
-  v = op(v, dpp_f<0x141>(v));  // row_half_mirror
-  v = op(v, dpp_f<0x140>(v));  // row_mirror
-  // row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3; rows
-  // outside the mask keep their value (old = v)
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(MAX ? -INFINITY : 0.f),
-                                                       __float_as_int(v), 0x142, 0xA, 0xF,
-                                                       false)));
-  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(MAX ? -INFINITY : 0.f),
-                                                       __float_as_int(v), 0x143, 0xC, 0xF,
-                                                       false)));
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 
 __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
   __shared__ float wts[kMaxChunks];  // m_c, then the chunk weight e^(m_c - M)
