@@ -2036,17 +2036,41 @@ constexpr int kCombPhases = kCombThreads / kCombPairs;  // threads per pair
 constexpr int kCombRound = 8;                           // o loads in flight per thread
 constexpr int kMaxChunks = 4096;
 
+// LDS of one combine workgroup, in floats: the chunk weights and sums of
+// the launch's chunk count, the phases' partial sums and L.
+__host__ __device__ constexpr int comb_lds_floats(int nchunks) { return 2 * nchunks + kCombThreads + 4; }
+
 __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
-  __shared__ float wts[kMaxChunks];  // m_c, then the chunk weight e^(m_c - M)
-  __shared__ float lsv[kMaxChunks];  // l_c
-  __shared__ float s_l;              // L = sum_c e^(m_c - M) l_c
-  __shared__ float pacc[kCombThreads];
+  extern __shared__ float csm[];
+  float* wts = csm;                  // [nchunks] m_c, then the chunk weight e^(m_c - M)
+  float* lsv = csm + a.nchunks;      // [nchunks] l_c
+  float* pacc = lsv + a.nchunks;     // [kCombThreads]
+  float& s_l = pacc[kCombThreads];   // L = sum_c e^(m_c - M) l_c
   const int P = a.gh * a.d;
   const int slot = blockIdx.y;
   const int pb = blockIdx.x * kCombPairs;
   const int t = threadIdx.x;
   const int rows = a.nkv * a.nsub;  // slots per sequence
   const int b = slot / rows, y = slot - b * rows;
+  const int pl = t % kCombPairs, ph = t / kCombPairs;
+  const int pair = pb + pl;  // < P: P is a multiple of 64
+  const int g = pb / a.d;    // one head per workgroup
+  const float* po = a.part_o + (int64_t)slot * a.nchunks * P + pair;
+  const float* pml = a.part_ml + (int64_t)slot * a.nchunks * a.gh * 2 + 2 * g;
+  // The first round of o loads and wave 0's first statistics go out before
+  // this sequence's chunk count is known (paged: it needs seq_lens, another
+  // round trip): they stay within the launch's nchunks slots of the
+  // workspace, and only chunks below the count are used.
+  float ov[kCombRound];
+#pragma unroll
+  for (int u = 0; u < kCombRound; ++u)
+    ov[u] = po[(int64_t)min(ph + kCombPhases * u, a.nchunks - 1) * P];
+  float m1 = -INFINITY, l1 = 0.f;
+  if (t < 64) {
+    const int c1 = min(t, a.nchunks - 1);
+    m1 = pml[(int64_t)c1 * a.gh * 2];
+    l1 = pml[(int64_t)c1 * a.gh * 2 + 1];
+  }
   int nch = a.nchunks;
   if (a.paged) {  // this sequence's chunk count, as the attention kernel derives it
     const int n = a.seq_lens[b];
@@ -2058,22 +2082,12 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
     if (nch > a.nchunks) nch = a.nchunks;
   }
   if (nch <= 1) return;  // uniform over the workgroup
-  const int pl = t % kCombPairs, ph = t / kCombPairs;
-  const int pair = pb + pl;  // < P: P is a multiple of 64
-  const int g = pb / a.d;    // one head per workgroup
-  const float* po = a.part_o + (int64_t)slot * a.nchunks * P + pair;
-  const float* pml = a.part_ml + (int64_t)slot * a.nchunks * a.gh * 2 + 2 * g;
-  // first round of o loads, issued before the statistics
-  float ov[kCombRound];
-#pragma unroll
-  for (int u = 0; u < kCombRound; ++u)
-    ov[u] = po[(int64_t)min(ph + kCombPhases * u, nch - 1) * P];
-  if (t < 64) {  // wave 0: chunk weights and L of head g (one global round trip)
+  if (t < 64) {  // wave 0: chunk weights and L of head g
     float mloc = -INFINITY;
     for (int cc = t; cc < nch; cc += 64) {
-      const float m = pml[(int64_t)cc * a.gh * 2];
+      const float m = cc == t ? m1 : pml[(int64_t)cc * a.gh * 2];
       wts[cc] = m;
-      lsv[cc] = pml[(int64_t)cc * a.gh * 2 + 1];
+      lsv[cc] = cc == t ? l1 : pml[(int64_t)cc * a.gh * 2 + 1];
       mloc = fmaxf(mloc, m);
     }
     const float M = wave_reduce<true>(mloc);
@@ -2115,6 +2129,57 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
     a.o[orow + pair] = o / s_l;
     if (a.rope && a.q_out) a.q_out[orow + pair] = a.qrot[(int64_t)slot * P + pair];
   }
+}
+
+// The merge for a few chunks per slot (R >= nchunks, R <= 64), one wave per
+// 64 output pairs of one head, with no LDS and no barrier: lane c holds chunk c's (m, l), DPP
+// reductions give the max M and L = sum_c e^(m_c - M) l_c, and every lane
+// sums its pair over the chunks with the weights broadcast by readlane.
+// All R >= nchunks o loads and the statistics go out at once, before this
+// sequence's chunk count is known (paged: it needs seq_lens): they stay
+// within the launch's nchunks slots of the workspace, and only chunks below
+// the count are used.
+constexpr int kCombWaveThreads = 256;
+template <int R>
+__global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs a) {
+  const int P = a.gh * a.d;
+  const int slot = blockIdx.y;
+  const int pair = blockIdx.x * blockDim.x + threadIdx.x;  // < P: blockDim divides P
+  const int lane = threadIdx.x & 63;
+  const int g = __builtin_amdgcn_readfirstlane(pair / a.d);  // d % 64 == 0: one head per wave
+  const int rows = a.nkv * a.nsub;  // slots per sequence
+  const int b = slot / rows, y = slot - b * rows;
+  const float* po = a.part_o + (int64_t)slot * a.nchunks * P + pair;
+  const float* pml = a.part_ml + (int64_t)slot * a.nchunks * a.gh * 2 + 2 * g;
+  float ov[R];
+#pragma unroll
+  for (int u = 0; u < R; ++u) ov[u] = po[(int64_t)min(u, a.nchunks - 1) * P];
+  const int cl = min(lane, a.nchunks - 1);
+  const float mc = pml[(int64_t)cl * a.gh * 2], lc = pml[(int64_t)cl * a.gh * 2 + 1];
+  int nch = a.nchunks;
+  if (a.paged) {  // this sequence's chunk count, as the attention kernel derives it
+    const int n = a.seq_lens[b];
+    const int pos = a.pos_arr ? a.pos_arr[b] : n - 1;
+    int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
+    if (t0 > n) t0 = n;
+    const int span = (a.rope ? n - 1 : n) - t0;
+    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.rope ? 1 : 0);
+    if (nch > a.nchunks) nch = a.nchunks;
+  }
+  if (nch <= 1) return;  // uniform over the workgroup
+  const bool live = lane < nch;
+  const float M = wave_reduce<true>(live ? mc : -INFINITY);
+  const float wc = live ? softmax_exp(mc - M) : 0.f;
+  const float L = wave_reduce<false>(live ? wc * lc : 0.f);
+  float acc = 0.f;
+#pragma unroll
+  for (int u = 0; u < R; ++u)
+    if (u < nch) acc = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wc), u)), ov[u], acc);
+  const int G = a.nq / a.nkv;
+  const int h = y / a.nsub, sub = y - h * a.nsub;
+  const int64_t orow = ((int64_t)b * a.nq + h * G + sub * a.gh) * a.d;
+  a.o[orow + pair] = acc / L;
+  if (a.rope && a.q_out) a.q_out[orow + pair] = a.qrot[(int64_t)slot * P + pair];
 }
 
 __global__ void vexp_kernel(const float* x, float* y, int64_t n) {
@@ -2368,15 +2433,29 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   cb.window = a.window;
   cb.rope = rope ? 1 : 0;
   cb.paged = paged ? 1 : 0;
-  dim3 cgrid(gh * d / kCombPairs, a.nkv * nsubs * B);
+  // At most 8 chunks (batches of sequences: many slots, few chunks): one
+  // wave per 64 pairs (combine_wave_kernel<R>, R = 4 or 8 o loads per lane).
+  // More chunks: combine_kernel, whose 4 phases per pair keep the loads per
+  // lane at 8 a round (the wave kernel issued 32-64 per lane and was 0.4 us
+  // slower at 32 and 64 chunks).
+  const int P = gh * d;
+  const int wthreads = P % 256 == 0 ? 256 : (P % 128 == 0 ? 128 : 64);
+  const int slots = a.nkv * nsubs * B;
+  using CombFn = void (*)(CombArgs);
+  const bool wave = a.nchunks <= 8;
+  const CombFn ck = a.nchunks <= 4 ? combine_wave_kernel<4>
+                    : wave         ? combine_wave_kernel<8>
+                                   : combine_kernel;
+  const dim3 cgrid = wave ? dim3(P / wthreads, slots) : dim3(P / kCombPairs, slots);
+  const dim3 cblock = wave ? dim3(wthreads) : dim3(kCombThreads);
+  const size_t clds = wave ? 0 : sizeof(float) * (size_t)comb_lds_floats(a.nchunks);  // <= 33 KB
   if (prof) {
     pr.c0 = prof_event();
     pr.c1 = prof_event();
-    hipExtLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), 0, (hipStream_t)stream,
-                          pr.c0, pr.c1, 0, cb);
+    hipExtLaunchKernelGGL(ck, cgrid, cblock, clds, (hipStream_t)stream, pr.c0, pr.c1, 0, cb);
     g_prof.push_back(pr);
   } else {
-    hipLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), 0, (hipStream_t)stream, cb);
+    hipLaunchKernelGGL(ck, cgrid, cblock, clds, (hipStream_t)stream, cb);
   }
   return (int)hipGetLastError();
 }
