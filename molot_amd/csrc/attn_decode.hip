@@ -333,10 +333,11 @@ __global__ void rope_append_kernel(RopeArgs a) {
 // ---------------------------------------------------------------------------
 // Fused decode attention.
 //
-// Grid (nkv * subgroups, sequences, chunks).  Workgroup (h/sub, b, c) owns the
-// context rows [tb, tb + cnt) of KV head h and the GH query heads
-// hq0 .. hq0+GH-1 of that head's group; the workgroups sharing (b, h/sub)
-// form a "slot".
+// Grid (nkv * subgroups, sequences, chunks).  Workgroup (h/sub, b, c) owns
+// chunk c of the context rows of KV head h and the GH query heads
+// hq0 .. hq0+GH-1 of that head's group: a paged cache's rows [tb, tb + cnt),
+// a contiguous cache's 32-row groups c, c + nchunks, c + 2*nchunks, ... of the
+// range.  The workgroups sharing (b, h/sub) form a "slot".
 //   1. prologue: the first block(s) of K/V rows of every wave, then q of the
 //      GH heads into LDS; with ROPE, q is rotated there, and the workgroup
 //      holding the chunk that contains the new token rotates k_new and
@@ -350,9 +351,9 @@ __global__ void rope_append_kernel(RopeArgs a) {
 //      wave (running max, rescale of the accumulators); probabilities through
 //      a per-wave LDS slice to the PV lanes (LPR2 lanes per V row, 16 bytes
 //      each);
-//   3. the new token (ROPE, last chunk): stored into the cache slot n-1 by
-//      subgroup 0 (no workgroup reads that slot in this launch) and folded in
-//      by wave 0 from LDS;
+//   3. the new token (ROPE, last chunk): folded in by wave 0 from LDS, and
+//      stored into the cache slot n-1 by subgroup 0 as the kernel's last
+//      step (no workgroup reads that slot in this launch);
 //   4. the waves' (max, sum, o) are merged through LDS; every thread derives
 //      its own outputs' chunk partial.  A single-chunk problem writes
 //      o / sum (and the rotated q) directly;
