@@ -2471,12 +2471,16 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
                      a, GH, D, nsubs, B, PAGED, ROPE, stream);
 }
 
-// bf16 KV, D = 64 or 128: the matrix-core kernel.  Two workgroups of four
-// waves per CU; paged batches are cut finer (their sequences differ in
-// length, and more, shorter chunks even out the CUs' shares).
+// bf16 or Q8 KV, D = 64 or 128: the matrix-core kernel.  Workgroups per CU
+// in the plan (measured): a contiguous cache 1 (c5 kernel 96.0 -> 93.2 us
+// against 2; with two per CU the one dispatched second streams at about
+// half the rate of the first, and the chunks left to it form the tail);
+// paged batches are cut finer, their sequences differing in length: bf16
+// 16 (c4 240.2 -> 235.6 us against 8), Q8 8 (c4q8: 141.5 us, 150.1 at 16).
 template <int D, int GH, bool PAGED, bool ROPE, bool Q8>
 int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
-  int st = plan_launch(a, D, span, GH, nsubs, B, kTile, PAGED ? 8 : 2, stream, !PAGED);
+  constexpr int kWpc = PAGED ? (Q8 ? 8 : 16) : 1;
+  int st = plan_launch(a, D, span, GH, nsubs, B, kTile, kWpc, stream, !PAGED);
   if (st) return st;
   a.chunk_fast = Q8 && !PAGED && B == 1;
   const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8);
