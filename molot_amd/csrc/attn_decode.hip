@@ -1786,8 +1786,9 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 //   that key's probability (its rows 4g + r, r = j): P is the B operand in
 //   place, and V^T comes four keys per ds_read_b128.
 // The reference's exps are libm expf summed in double with the weights
-// normalised before PV; here device expf, fp32 running sums with the usual
-// max rescaling, and one division at the end (fp32 rounding differences).
+// normalised before PV; here the hardware base-2 exp of scores pre-scaled by
+// log2(e), fp32 running sums with a lazy max rescale, and one division at
+// the end (fp32 rounding differences).
 struct PfArgs {
   const float* q;  // [M][nq][D]
   const void* k;   // token-major cache [N][nkv*D], or pages [block][nkv][page][D]
@@ -1847,14 +1848,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
   const int rt0 = rv ? t0_of(m) : 0, rnn = rv ? nn_of(m) : 0;
   const int64_t qoff = ((int64_t)m * a.nq + h * G + g) * D;
 
-  // Q^T in the k order of the score product
+  // Q^T in the k order of the score product, pre-scaled by scale*log2(e):
+  // the scores come out in base-2 units (the softmax below)
   float qv[JS];
+  const float qsc = a.scale * kLog2e;
 #pragma unroll
   for (int J = 0; J < D / 16; ++J) {
     f32x4 x = rv ? *reinterpret_cast<const f32x4*>(a.q + qoff + 16 * J + 4 * g4)
                  : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qv[4 * J + i] = x[i];
+    for (int i = 0; i < 4; ++i) qv[4 * J + i] = x[i] * qsc;
   }
 
   // tile loads: chunk c = tid + NT*i.  Within a wave, lanes l and l + 16*x
@@ -1947,21 +1950,27 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
     store_tile();
     __syncthreads();
     if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
-    // scores of the KH 16-key halves
+    // scores of the KH 16-key halves (the halves' accumulator chains
+    // interleaved)
     f32x4 sacc[KH];
 #pragma unroll
-    for (int u = 0; u < KH; ++u) {
-      sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < KH; ++u) sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int J = 0; J < D / 16; ++J) {
-        const f32x4 kx = *reinterpret_cast<const f32x4*>(ks + (16 * u + c16) * KSR + 16 * J +
-                                                         4 * g4);
+    for (int J = 0; J < D / 16; ++J) {
+      f32x4 kx[KH];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[i], qv[4 * J + i], sacc[u], 0, 0, 0);
-      }
+      for (int u = 0; u < KH; ++u)
+        kx[u] = *reinterpret_cast<const f32x4*>(ks + (16 * u + c16) * KSR + 16 * J + 4 * g4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int u = 0; u < KH; ++u)
+          sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[u][i], qv[4 * J + i], sacc[u], 0, 0, 0);
     }
-    // online softmax of this lane's row over its 4*KH keys of the tile
+    // online softmax (base 2) of this lane's row over its 4*KH keys of the
+    // tile.  Lazy rescale, as in the decode kernel: the running max moves
+    // only when a score exceeds it by more than kLazyMax (p <= 2^8
+    // otherwise); o and l always share the max they were formed with.
     float sv[KH][4];
     float tmax = -INFINITY;
 #pragma unroll
@@ -1969,26 +1978,31 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tk + 16 * u + 4 * g4 + r;
-        sv[u][r] = (t >= rt0 && t < rnn) ? sacc[u][r] * a.scale : -INFINITY;
+        sv[u][r] = (t >= rt0 && t < rnn) ? sacc[u][r] : -INFINITY;
         tmax = fmaxf(tmax, sv[u][r]);
       }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float mn = fmaxf(m_run, tmax);
-    // a row with no key yet keeps max -inf: nothing to rescale, p = 0
-    const float alpha = mn == -INFINITY ? 1.f : softmax_exp(m_run - mn);
-    m_run = mn;
+    const bool grow = tmax > m_run + kLazyMax;  // false while the row has no key (-inf)
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float mn = grow ? fmaxf(m_run, tmax) : m_run;
+      // a row's first keys: nothing to rescale
+      const float alpha = m_run == -INFINITY ? 1.f : exp2_hw(m_run - mn);
+      m_run = mn;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
     float ps = 0.f;
 #pragma unroll
     for (int u = 0; u < KH; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sv[u][r] = sv[u][r] == -INFINITY ? 0.f : softmax_exp(sv[u][r] - mn);
+        // masked keys (and a row with no key yet, max -inf): p = 0
+        sv[u][r] = sv[u][r] == -INFINITY ? 0.f : exp2_hw(sv[u][r] - m_run);
         ps += sv[u][r];
       }
-    l_run = l_run * alpha + ps;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    l_run += ps;
     // PV
 #pragma unroll
     for (int u = 0; u < KH; ++u)
