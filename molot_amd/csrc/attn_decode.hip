@@ -1164,6 +1164,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 //           V[tau(g, e)][16*dt + i]: the A operand.
 // Prologue, new token and chunk output are those of attn_kernel.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaWaves = 4;                  // waves per workgroup
@@ -2014,6 +2015,302 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
         for (int j = 0; j < 4; ++j)
           o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vx[j], sv[u][j], o[dt], 0, 0, 0);
       }
+    __syncthreads();  // the tile's LDS is rewritten next
+  }
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+  if (rv) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;  // no key: O = 0 (gemm.h:438)
+    float* orow = a.o + qoff;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4*>(orow + 16 * dt + 4 * g4) = o[dt] * inv;
+  }
+}
+
+// Causal prefill on the bf16 matrix cores (D = 64, 128): prefill_kernel's
+// work mapping, rows, masking and softmax, with every fp32 product taken as
+// bf16 pieces on v_mfma_f32_16x16x32_bf16 (16x the fp32 matrix rate).
+// x = hi + mid + lo (split3) carries x's 24-bit significand; a product keeps
+// the six piece products down to 2^-16 of its size (hi*hi, hi*mid, mid*hi,
+// hi*lo, lo*hi, mid*mid), so the dropped ones are ~2^-24 of it, an fp32
+// rounding.  A bf16 cache needs one K/V piece (its values are exact): three
+// products.  Tiles of 32 keys are staged into LDS as pieces:
+//   K [KP][32 keys][D] bf16, rows padded by 16 bytes (the 16 lanes of a
+//     ds_read_b128 then hit 16 distinct groups of 4 banks), read as the A
+//     operand of S^T = K . Q^T: lane l key 16u + l%16, elements
+//     32s + 8(l/16) .. +7, Q^T in the same element order in registers;
+//   V [KP][32 keys][D] bf16, 32-byte segments XOR-swizzled by key, read as
+//     V^T by ds_read_b64_tr_b16 as in attn_mfma_kernel: the A operand of
+//     O^T += V^T . P^T, with P in the registers the score accumulator left
+//     it in (key 16u + 4(l/16) + r of lane l, slot 4u + r).
+template <int D, typename T, bool PAGED>
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a) {
+  static_assert(D == 64 || D == 128, "bf16-piece prefill: D = 64 or 128");
+  constexpr int NT = kPfThreads, QB = 16 * kPfWaves;
+  constexpr int KT = 32, KH = 2;
+  constexpr int KP = sizeof(T) == 2 ? 1 : 3;  // staged pieces of K and V
+  constexpr int KRB = 2 * D + 16;             // bytes of a staged K row
+  constexpr int VRB = 2 * D;                  // bytes of a staged V row
+  constexpr int NSEG = D / 16;                // 32-byte segments of a V row
+  constexpr int QS = D / 32;                  // 32-element steps of the scores
+  constexpr int DT = D / 16;
+  constexpr int VW = KVT<T>::VW;              // elements per 16-byte load
+  constexpr int CH = KT * D / VW;             // 16-byte chunks per tile (K or V)
+  constexpr int CPT = (CH + NT - 1) / NT;
+  constexpr bool Q8 = std::is_same<T, q8_t>::value;
+  static_assert(CH % NT == 0 || CH < NT, "whole chunks per thread");
+  static_assert((D / VW) % 4 == 0 && CH % 64 == 0 && 16 % VW == 0, "chunk mapping");
+  __shared__ __attribute__((aligned(16))) char kp_s[KP * KT * KRB];
+  __shared__ __attribute__((aligned(16))) char vp_s[KP * KT * VRB];
+
+  const int G = a.nq / a.nkv;
+  const int h = blockIdx.x % a.nkv;  // heads fastest: every XCD gets every head's share
+  const int qb = a.nqb - 1 - (int)(blockIdx.x / a.nkv);  // latest rows (most keys) first
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c16 = lane & 15, g4 = lane >> 4;
+  const int rows = a.M * G;
+  const int r0 = qb * QB;
+  const int rl = min(r0 + QB, rows) - 1;
+  auto t0_of = [&](int m) {
+    const int pos = a.pos0 + m;
+    int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
+    return t0 > a.N ? a.N : t0;
+  };
+  auto nn_of = [&](int m) { return a.pos0 + m + 1 < a.N ? a.pos0 + m + 1 : a.N; };
+  const int kt_lo = t0_of(r0 / G);
+  const int kt_hi = nn_of(rl / G);
+  const int ntile = kt_hi > kt_lo ? (kt_hi - kt_lo + KT - 1) / KT : 0;
+  const int row = r0 + 16 * w + c16;
+  const bool rv = row < rows;
+  const int m = rv ? row / G : 0;
+  const int g = rv ? row - m * G : 0;
+  const int rt0 = rv ? t0_of(m) : 0, rnn = rv ? nn_of(m) : 0;
+  const int64_t qoff = ((int64_t)m * a.nq + h * G + g) * D;
+
+  // Q^T pieces (B operand): lane l row c16, elements 32s + 8*g4 + e, scaled
+  // by scale*log2(e) (base-2 scores)
+  const float qsc = a.scale * kLog2e;
+  bf16x8_t qh[QS], qm[QS], ql[QS];
+#pragma unroll
+  for (int s = 0; s < QS; ++s) {
+    const float* qp = a.q + qoff + 32 * s + 8 * g4;
+    const f32x4 x0 = rv ? *reinterpret_cast<const f32x4*>(qp) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 x1 = rv ? *reinterpret_cast<const f32x4*>(qp + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 hi, mid, lo;
+      split3((e < 4 ? x0[e] : x1[e - 4]) * qsc, hi, mid, lo);
+      qh[s][e] = hi;
+      qm[s][e] = mid;
+      ql[s][e] = lo;
+    }
+  }
+
+  // tile loads: prefill_kernel's chunk mapping (16 consecutive lanes hold 16
+  // keys of one element group)
+  auto chunk_of = [&](int c, int& key, int& e) {
+    constexpr int KT16 = KT / 16;
+    key = (c & 15) + 16 * ((c >> 6) % KT16);
+    e = VW * (((c >> 4) & 3) + 4 * ((c >> 6) / KT16));
+  };
+  const T* Kb = reinterpret_cast<const T*>(a.k);
+  const T* Vb = reinterpret_cast<const T*>(a.v);
+  const int pg = 1 << a.page_shift;
+  const int64_t R = (int64_t)a.nkv * D + ((4 * a.nkv + 15) & ~15);
+  const int64_t BB = (int64_t)a.nkv * pg * (D + 4);
+  auto row_off = [&](int t, int64_t& soff) -> int64_t {
+    if constexpr (PAGED) {
+      const int64_t blk = a.block_table[t >> a.page_shift];
+      const int sl = t & (pg - 1);
+      if constexpr (Q8) {
+        soff = blk * BB + (int64_t)a.nkv * pg * D + 4 * ((int64_t)h * pg + sl);
+        return blk * BB + ((int64_t)h * pg + sl) * D;
+      }
+      return (blk * a.nkv + h) * pg * D + (int64_t)sl * D;
+    } else {
+      if constexpr (Q8) {
+        soff = (int64_t)t * R + (int64_t)a.nkv * D + 4 * h;
+        return (int64_t)t * R + (int64_t)h * D;
+      }
+      return (int64_t)t * a.nkv * D + (int64_t)h * D;
+    }
+  };
+  typename KVT<T>::vec kreg[CPT], vreg[CPT];
+  [[maybe_unused]] float ksc[CPT], vsc[CPT];
+  auto load_tile = [&](int tk) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + NT * i;
+      if (CH < NT && c >= CH) break;
+      int key, e;
+      chunk_of(c, key, e);
+      const int t = min(tk + key, kt_hi - 1);  // rows past the range: the last one (masked)
+      int64_t soff = 0;
+      const int64_t off = row_off(t, soff) + e;
+      if constexpr (Q8) {
+        ksc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.k) + soff);
+        vsc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v) + soff);
+      }
+      kreg[i] = load16(Kb + off);
+      vreg[i] = load16(Vb + off);
+    }
+  };
+  // the chunk's values as KP bf16 pieces, 4 elements (8 bytes) at a time
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + NT * i;
+      if (CH < NT && c >= CH) break;
+      int key, e;
+      chunk_of(c, key, e);
+      float kx[VW], vx[VW];
+      KVT<T>::unpack(kreg[i], kx);
+      KVT<T>::unpack(vreg[i], vx);
+      if constexpr (Q8) {  // code * s, the dequantized value
+#pragma unroll
+        for (int j = 0; j < VW; ++j) {
+          kx[j] *= ksc[i];
+          vx[j] *= vsc[i];
+        }
+      }
+#pragma unroll
+      for (int j4 = 0; j4 < VW; j4 += 4) {
+        const int ej = e + j4;
+        bf16x4_t kpc[KP], vpc[KP];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (KP == 3) {
+            __bf16 hi, mid, lo;
+            split3(kx[j4 + j], hi, mid, lo);
+            kpc[0][j] = hi;
+            kpc[1][j] = mid;
+            kpc[2][j] = lo;
+            split3(vx[j4 + j], hi, mid, lo);
+            vpc[0][j] = hi;
+            vpc[1][j] = mid;
+            vpc[2][j] = lo;
+          } else {  // exact bf16 values
+            kpc[0][j] = (__bf16)kx[j4 + j];
+            vpc[0][j] = (__bf16)vx[j4 + j];
+          }
+        }
+        const int kofs = key * KRB + 2 * ej;
+        const int vofs = key * VRB + 32 * ((ej >> 4) ^ (key & (NSEG - 1))) + 2 * (ej & 15);
+#pragma unroll
+        for (int p = 0; p < KP; ++p) {
+          *reinterpret_cast<bf16x4_t*>(kp_s + p * KT * KRB + kofs) = kpc[p];
+          *reinterpret_cast<bf16x4_t*>(vp_s + p * KT * VRB + vofs) = vpc[p];
+        }
+      }
+    }
+  };
+
+  f32x4 o[DT];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+  if (ntile > 0) load_tile(kt_lo);
+  for (int it = 0; it < ntile; ++it) {
+    const int tk = kt_lo + it * KT;
+    store_tile();
+    __syncthreads();
+    if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
+    // scores of the two 16-key halves, smallest piece products first
+    f32x4 sacc[KH];
+#pragma unroll
+    for (int u = 0; u < KH; ++u) sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < QS; ++s)
+#pragma unroll
+      for (int u = 0; u < KH; ++u) {
+        const char* kb = kp_s + (16 * u + c16) * KRB + 2 * (32 * s + 8 * g4);
+        const bf16x8_t k0 = *reinterpret_cast<const bf16x8_t*>(kb);
+        if constexpr (KP == 3) {
+          const bf16x8_t k1 = *reinterpret_cast<const bf16x8_t*>(kb + KT * KRB);
+          const bf16x8_t k2 = *reinterpret_cast<const bf16x8_t*>(kb + 2 * KT * KRB);
+          sacc[u] = mfma_bf16(k1, qm[s], sacc[u]);
+          sacc[u] = mfma_bf16(k2, qh[s], sacc[u]);
+          sacc[u] = mfma_bf16(k0, ql[s], sacc[u]);
+          sacc[u] = mfma_bf16(k1, qh[s], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qm[s], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qh[s], sacc[u]);
+        } else {
+          sacc[u] = mfma_bf16(k0, ql[s], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qm[s], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qh[s], sacc[u]);
+        }
+      }
+    // online softmax (base 2, lazy rescale) of this lane's row over its 8
+    // keys of the tile, as in prefill_kernel
+    float sv[KH][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < KH; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = tk + 16 * u + 4 * g4 + r;
+        sv[u][r] = (t >= rt0 && t < rnn) ? sacc[u][r] : -INFINITY;
+        tmax = fmaxf(tmax, sv[u][r]);
+      }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const bool grow = tmax > m_run + kLazyMax;  // false while the row has no key (-inf)
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float mn = grow ? fmaxf(m_run, tmax) : m_run;
+      const float alpha = m_run == -INFINITY ? 1.f : exp2_hw(m_run - mn);
+      m_run = mn;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
+    // P^T pieces (B operand): slot 4u + r holds key 16u + 4*g4 + r
+    bf16x8_t ph, pm, pl;
+    float ps = 0.f;
+#pragma unroll
+    for (int u = 0; u < KH; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = sv[u][r] == -INFINITY ? 0.f : exp2_hw(sv[u][r] - m_run);
+        ps += p;
+        __bf16 hi, mid, lo;
+        split3(p, hi, mid, lo);
+        ph[4 * u + r] = hi;
+        pm[4 * u + r] = mid;
+        pl[4 * u + r] = lo;
+      }
+    l_run += ps;
+    // PV: V^T of the 16-row block dt by two transposed reads per piece
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      bf16x8_t av[KP];
+#pragma unroll
+      for (int p = 0; p < KP; ++p) {
+        i16x4_t t2[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int r = (lane >> 2) + 16 * u;
+          t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(
+                  vp_s + p * KT * VRB + r * VRB + 32 * (dt ^ (r & (NSEG - 1))) + 8 * (lane & 3)));
+        }
+        av[p] = __builtin_bit_cast(
+            bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+      if constexpr (KP == 3) {
+        o[dt] = mfma_bf16(av[1], pm, o[dt]);
+        o[dt] = mfma_bf16(av[2], ph, o[dt]);
+        o[dt] = mfma_bf16(av[0], pl, o[dt]);
+        o[dt] = mfma_bf16(av[1], ph, o[dt]);
+        o[dt] = mfma_bf16(av[0], pm, o[dt]);
+        o[dt] = mfma_bf16(av[0], ph, o[dt]);
+      } else {
+        o[dt] = mfma_bf16(av[0], pl, o[dt]);
+        o[dt] = mfma_bf16(av[0], pm, o[dt]);
+        o[dt] = mfma_bf16(av[0], ph, o[dt]);
+      }
+    }
     __syncthreads();  // the tile's LDS is rewritten next
   }
   l_run += __shfl_xor(l_run, 16);
@@ -3131,26 +3428,30 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
       return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
+  // D = 64, 128: bf16 pieces on the bf16 matrix cores; D = 256 (whose
+  // staged pieces would leave one workgroup per CU): fp32 matrix cores
   using PfFn = void (*)(PfArgs);
   PfFn pk;
   if (kv_dtype == MOLOT_KV_Q8)  // D = 64, 128 (check_common)
-    pk = block_row ? (d == 64 ? prefill_kernel<64, q8_t, true> : prefill_kernel<128, q8_t, true>)
-                   : (d == 64 ? prefill_kernel<64, q8_t, false> : prefill_kernel<128, q8_t, false>);
+    pk = block_row ? (d == 64 ? prefill_mfma16_kernel<64, q8_t, true>
+                              : prefill_mfma16_kernel<128, q8_t, true>)
+                   : (d == 64 ? prefill_mfma16_kernel<64, q8_t, false>
+                              : prefill_mfma16_kernel<128, q8_t, false>);
   else if (!block_row)
     pk = kv_dtype == MOLOT_KV_F32
-             ? (d == 64 ? prefill_kernel<64, float, false>
-                        : d == 128 ? prefill_kernel<128, float, false>
+             ? (d == 64 ? prefill_mfma16_kernel<64, float, false>
+                        : d == 128 ? prefill_mfma16_kernel<128, float, false>
                                    : prefill_kernel<256, float, false>)
-             : (d == 64 ? prefill_kernel<64, bf16_t, false>
-                        : d == 128 ? prefill_kernel<128, bf16_t, false>
+             : (d == 64 ? prefill_mfma16_kernel<64, bf16_t, false>
+                        : d == 128 ? prefill_mfma16_kernel<128, bf16_t, false>
                                    : prefill_kernel<256, bf16_t, false>);
   else
     pk = kv_dtype == MOLOT_KV_F32
-             ? (d == 64 ? prefill_kernel<64, float, true>
-                        : d == 128 ? prefill_kernel<128, float, true>
+             ? (d == 64 ? prefill_mfma16_kernel<64, float, true>
+                        : d == 128 ? prefill_mfma16_kernel<128, float, true>
                                    : prefill_kernel<256, float, true>)
-             : (d == 64 ? prefill_kernel<64, bf16_t, true>
-                        : d == 128 ? prefill_kernel<128, bf16_t, true>
+             : (d == 64 ? prefill_mfma16_kernel<64, bf16_t, true>
+                        : d == 128 ? prefill_mfma16_kernel<128, bf16_t, true>
                                    : prefill_kernel<256, bf16_t, true>);
   const dim3 grid((unsigned)(nqb * nkv));
   std::lock_guard<std::mutex> plk(g_prof_mu);
