@@ -36,6 +36,7 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------------------
 // KV element traits: one 16-byte vector = VW elements.
@@ -1242,6 +1243,20 @@ __device__ __forceinline__ void i8x16_to_bf16(const u32x4& x, u32x4& lo, u32x4& 
   }
 }
 
+// split3 of two values at once: each piece of the pair is one
+// v_cvt_pk_bf16_f32 (round to nearest even, as split3), element a in the
+// low half.  The same pieces as split3 on each value.
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) { return bf16_pair_exact(a, b); }
+__device__ __forceinline__ void split3x2(float a, float b, uint32_t& hi, uint32_t& mid,
+                                         uint32_t& lo) {
+  hi = bf16_pair(a, b);
+  float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
+  mid = bf16_pair(ra, rb);
+  ra -= __uint_as_float(mid << 16);
+  rb -= __uint_as_float(mid & 0xFFFF0000u);
+  lo = bf16_pair(ra, rb);
+}
+
 // Matrix-core decode over a bf16 (Q8 = false) or Q8 (Q8 = true) cache.
 //
 // Q8: each lane reads 16 codes per 16-byte load, covering two k-steps: load
@@ -2098,14 +2113,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
     const float* qp = a.q + qoff + 32 * s + 8 * g4;
     const f32x4 x0 = rv ? *reinterpret_cast<const f32x4*>(qp) : f32x4{0.f, 0.f, 0.f, 0.f};
     const f32x4 x1 = rv ? *reinterpret_cast<const f32x4*>(qp + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    uint32_t h4[4], m4[4], l4[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 hi, mid, lo;
-      split3((e < 4 ? x0[e] : x1[e - 4]) * qsc, hi, mid, lo);
-      qh[s][e] = hi;
-      qm[s][e] = mid;
-      ql[s][e] = lo;
+    for (int e = 0; e < 8; e += 2) {
+      const float xa = (e < 4 ? x0[e] : x1[e - 4]) * qsc, xb = (e < 4 ? x0[e + 1] : x1[e - 3]) * qsc;
+      split3x2(xa, xb, h4[e / 2], m4[e / 2], l4[e / 2]);
     }
+    qh[s] = __builtin_bit_cast(bf16x8_t, u32x4{h4[0], h4[1], h4[2], h4[3]});
+    qm[s] = __builtin_bit_cast(bf16x8_t, u32x4{m4[0], m4[1], m4[2], m4[3]});
+    ql[s] = __builtin_bit_cast(bf16x8_t, u32x4{l4[0], l4[1], l4[2], l4[3]});
   }
 
   // tile loads: prefill_kernel's chunk mapping (16 consecutive lanes hold 16
@@ -2178,30 +2194,23 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
 #pragma unroll
       for (int j4 = 0; j4 < VW; j4 += 4) {
         const int ej = e + j4;
-        bf16x4_t kpc[KP], vpc[KP];
+        uint32_t kpc[KP][2], vpc[KP][2];  // 4 elements of each piece
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 4; j += 2) {
           if constexpr (KP == 3) {
-            __bf16 hi, mid, lo;
-            split3(kx[j4 + j], hi, mid, lo);
-            kpc[0][j] = hi;
-            kpc[1][j] = mid;
-            kpc[2][j] = lo;
-            split3(vx[j4 + j], hi, mid, lo);
-            vpc[0][j] = hi;
-            vpc[1][j] = mid;
-            vpc[2][j] = lo;
+            split3x2(kx[j4 + j], kx[j4 + j + 1], kpc[0][j / 2], kpc[1][j / 2], kpc[2][j / 2]);
+            split3x2(vx[j4 + j], vx[j4 + j + 1], vpc[0][j / 2], vpc[1][j / 2], vpc[2][j / 2]);
           } else {  // exact bf16 values
-            kpc[0][j] = (__bf16)kx[j4 + j];
-            vpc[0][j] = (__bf16)vx[j4 + j];
+            kpc[0][j / 2] = bf16_pair(kx[j4 + j], kx[j4 + j + 1]);
+            vpc[0][j / 2] = bf16_pair(vx[j4 + j], vx[j4 + j + 1]);
           }
         }
         const int kofs = key * KRB + 2 * ej;
         const int vofs = key * VRB + 32 * ((ej >> 4) ^ (key & (NSEG - 1))) + 2 * (ej & 15);
 #pragma unroll
         for (int p = 0; p < KP; ++p) {
-          *reinterpret_cast<bf16x4_t*>(kp_s + p * KT * KRB + kofs) = kpc[p];
-          *reinterpret_cast<bf16x4_t*>(vp_s + p * KT * VRB + vofs) = vpc[p];
+          *reinterpret_cast<u32x2*>(kp_s + p * KT * KRB + kofs) = u32x2{kpc[p][0], kpc[p][1]};
+          *reinterpret_cast<u32x2*>(vp_s + p * KT * VRB + vofs) = u32x2{vpc[p][0], vpc[p][1]};
         }
       }
     }
@@ -2266,21 +2275,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
       for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
     }
     // P^T pieces (B operand): slot 4u + r holds key 16u + 4*g4 + r
-    bf16x8_t ph, pm, pl;
+    float pv[4 * KH];
     float ps = 0.f;
 #pragma unroll
     for (int u = 0; u < KH; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float p = sv[u][r] == -INFINITY ? 0.f : exp2_hw(sv[u][r] - m_run);
-        ps += p;
-        __bf16 hi, mid, lo;
-        split3(p, hi, mid, lo);
-        ph[4 * u + r] = hi;
-        pm[4 * u + r] = mid;
-        pl[4 * u + r] = lo;
+        pv[4 * u + r] = sv[u][r] == -INFINITY ? 0.f : exp2_hw(sv[u][r] - m_run);
+        ps += pv[4 * u + r];
       }
     l_run += ps;
+    uint32_t ph4[4], pm4[4], pl4[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) split3x2(pv[e], pv[e + 1], ph4[e / 2], pm4[e / 2], pl4[e / 2]);
+    const bf16x8_t ph = __builtin_bit_cast(bf16x8_t, u32x4{ph4[0], ph4[1], ph4[2], ph4[3]});
+    const bf16x8_t pm = __builtin_bit_cast(bf16x8_t, u32x4{pm4[0], pm4[1], pm4[2], pm4[3]});
+    const bf16x8_t pl = __builtin_bit_cast(bf16x8_t, u32x4{pl4[0], pl4[1], pl4[2], pl4[3]});
     // PV: V^T of the 16-row block dt by two transposed reads per piece
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
