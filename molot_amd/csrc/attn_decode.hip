@@ -2068,6 +2068,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
   constexpr int KRB = 2 * D + 16;             // bytes of a staged K row
   constexpr int VRB = 2 * D;                  // bytes of a staged V row
   constexpr int NSEG = D / 16;                // 32-byte segments of a V row
+  // fp32 caches: a half-wave stages 16 keys x 2 element groups of one
+  // segment (16 of its 32 bytes per key); rows with key bit log2(NSEG) set
+  // keep their segments rotated by 16 bytes, so keys k and k + NSEG (same
+  // swizzled segment) use different banks
+  constexpr int VROT = KVT<T>::VW == 4 ? 16 : 0;
   constexpr int QS = D / 32;                  // 32-element steps of the scores
   constexpr int DT = D / 16;
   constexpr int VW = KVT<T>::VW;              // elements per 16-byte load
@@ -2206,7 +2211,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
           }
         }
         const int kofs = key * KRB + 2 * ej;
-        const int vofs = key * VRB + 32 * ((ej >> 4) ^ (key & (NSEG - 1))) + 2 * (ej & 15);
+        const int vofs = key * VRB + 32 * ((ej >> 4) ^ (key & (NSEG - 1))) +
+                         ((2 * (ej & 15) + VROT * ((key / NSEG) & 1)) & 31);
 #pragma unroll
         for (int p = 0; p < KP; ++p) {
           *reinterpret_cast<u32x2*>(kp_s + p * KT * KRB + kofs) = u32x2{kpc[p][0], kpc[p][1]};
@@ -2303,7 +2309,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
           const int r = (lane >> 2) + 16 * u;
           t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) i16x4_t*)(
-                  vp_s + p * KT * VRB + r * VRB + 32 * (dt ^ (r & (NSEG - 1))) + 8 * (lane & 3)));
+                  vp_s + p * KT * VRB + r * VRB + 32 * (dt ^ (r & (NSEG - 1))) +
+                  ((8 * (lane & 3) + VROT * ((r / NSEG) & 1)) & 31)));
         }
         av[p] = __builtin_bit_cast(
             bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
