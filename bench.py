@@ -71,6 +71,7 @@ CONFIGS = {
                n0=16384),
 }
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
+BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, published
 DESCR = {
     "c1": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 fp32 KV, pos 4096 (n=4097), batch 1",
     "c2": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 fp32 KV, ctx 16384 (n=16385), batch 1",
@@ -654,7 +655,8 @@ def run_prefill(args, cfg, lib, L, torch, np):
                                       ctypes.byref(nc)), "profile_end")
     k_us = am.value / max(1, na.value) * 1e3
     achieved = flops / (k_us * 1e-6) / 1e12
-    log(args, f"prefill_kernel {k_us:.1f} us/launch -> {achieved:.1f} TFLOP/s")
+    kname = "prefill_mfma16_kernel" if d <= 128 else "prefill_kernel"
+    log(args, f"{kname} {k_us:.1f} us/launch -> {achieved:.1f} TFLOP/s")
     out = {
         "metric": "prefill attention TFLOP/s (causal, 4*d flops per head x query x key)",
         "value": round(value, 2),
@@ -672,10 +674,14 @@ def run_prefill(args, cfg, lib, L, torch, np):
                    "head_dim": d, "prompt": M, "cached": n0, "window": window,
                    "rope_theta": theta, "timing": "eager"},
         "flops_per_step": flops,
-        "roofline": {"bound": "mfma", "kernel": "prefill_kernel<%d,float>" % d,
+        # peak: the fp32 matrix peak, the precision the products keep.  d <= 128
+        # takes each fp32 product as six bf16 piece products on the bf16 matrix
+        # cores, whose instruction ceiling for that is 2500 / 6 TFLOP/s.
+        "roofline": {"bound": "mfma", "kernel": "%s<%d,float>" % (kname, d),
                      "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
-                     "traffic": None, "launch_us": round(k_us, 2)},
+                     "traffic": None, "launch_us": round(k_us, 2),
+                     "bf16_piece_ceiling": round(BF16_MFMA_PEAK_TFLOPS / 6, 1) if d <= 128 else None},
     }
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline_prefill(args, q_h, K_h, V_h, nq, nkv, d, M, N, n0,
