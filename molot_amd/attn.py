@@ -311,6 +311,40 @@ def prefill_step(q, k_new, v_new, K, V, O, nq, nkv, d, M, slot0, pos0, inv_freq,
     return O
 
 
+def prefill_step_paged(q, k_new, v_new, K, V, O, block_row, max_blocks, page, nq, nkv, d, M,
+                       slot0, pos0, inv_freq, scale, window=0, q_norm=None, k_norm=None,
+                       v_norm=False, eps=1e-6):
+    """prefill_step for one sequence of a paged cache [blocks][nkv][page][d]
+    (Q8: the paged block layout): block_row [max_blocks] int32 is that
+    sequence's row of the block table; the prompt's rows land in slots
+    slot0 .. slot0+M-1 (no reference counterpart: the paged manager's
+    per-sequence prefill)."""
+    kvd = kv_dtype_of(K)
+    if slot0 < 0 or slot0 + M > max_blocks * page:
+        raise RuntimeError("fwd: KV cache full")
+    _need(q, "q", torch.float32, M * nq * d)
+    _need(k_new, "k_new", torch.float32, M * nkv * d)
+    _need(v_new, "v_new", torch.float32, M * nkv * d)
+    _need(O, "O", torch.float32, M * nq * d)
+    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need(block_row, "block_row", torch.int32, max_blocks)
+    bu = _block_units(kvd, nkv, d, page)
+    nblocks = K.numel() // bu
+    _need(K, "K", _KV_DTYPES, nblocks * bu)
+    _need(V, "V", K.dtype, nblocks * bu)
+    used = (slot0 + M + page - 1) // page
+    row = block_row.cpu()
+    if used and (int(row[:used].min()) < 0 or int(row[:used].max()) >= nblocks):
+        raise ValueError("block_row names a block outside the pool")
+    _need_norms(q_norm, k_norm, d)
+    check(_lib.load().molot_hip_prefill_step_paged(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), _ptr(block_row),
+        int(max_blocks), int(page), nq, nkv, d, int(M), int(slot0), int(pos0), _ptr(q_norm),
+        _ptr(k_norm), int(bool(v_norm)), float(eps), _ptr(inv_freq), float(scale), int(window),
+        kvd, _stream()), "prefill_step_paged")
+    return O
+
+
 def rope_append_paged(q, k_new, v_new, K, V, block_table, seq_lens, pos, B, max_blocks, nq, nkv,
                       d, page, inv_freq):
     """RoPE + append of one token per sequence into its page slot seq_lens[b]-1."""

@@ -162,6 +162,54 @@ def test_prefill_step_vs_oracle(gpu, bf16):
         assert normwise_err(host(O), oO) < TOL
 
 
+@pytest.mark.parametrize("nq,nkv,d,bf16", [(32, 8, 128, False), (32, 8, 128, True),
+                                           (8, 2, 64, False)])
+def test_prefill_step_paged_matches_contiguous(gpu, nq, nkv, d, bf16):
+    """The paged prefill step (shuffled 16-row pages, spare blocks) on the
+    same logical rows as the contiguous one: the same kernel arithmetic, so
+    O, the rotated q and the appended rows agree bit for bit; O also against
+    the oracle on the contiguous cache."""
+    announce(f"paged prefill step {nq}/{nkv}/{d} bf16={bf16}")
+    st = Stream(91 + d + bf16)
+    M, n0, page, spare = 77, 300, 16, 5
+    cap = n0 + M
+    q = st.normal((M, nq, d))
+    k = st.normal((M, nkv, d))
+    v = st.normal((M, nkv, d))
+    K, V = cache(st, cap, nkv, d, bf16)
+    K[n0:] = 0
+    V[n0:] = 0
+    nb = (cap + page - 1) // page
+    nblk = nb + spare
+    row = st.permutation(nblk)[:nb].astype(np.int32)
+    Kp = np.zeros((nblk, nkv, page, d), K.dtype)
+    Vp = np.zeros((nblk, nkv, page, d), V.dtype)
+    for t in range(n0):
+        Kp[row[t // page], :, t % page] = K[t].reshape(nkv, d)
+        Vp[row[t // page], :, t % page] = V[t].reshape(nkv, d)
+    inv = dev(oracle.rope_inv_freq(500000.0, d))
+    s = 1 / math.sqrt(d)
+    qc, qp = dev(q), dev(q)
+    Kc, Vc = on_dev(K), on_dev(V)
+    Kpd, Vpd = on_dev(Kp.reshape(nblk, -1)), on_dev(Vp.reshape(nblk, -1))
+    Oc = torch.empty((M, nq, d), device="cuda")
+    Op = torch.empty((M, nq, d), device="cuda")
+    attn.prefill_step(qc, dev(k), dev(v), Kc, Vc, Oc, nq, nkv, d, M, n0, n0, inv, s, 0)
+    attn.prefill_step_paged(qp, dev(k), dev(v), Kpd, Vpd, Op, torch.from_numpy(row).cuda(), nb,
+                            page, nq, nkv, d, M, n0, n0, inv, s, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(qp, qc)
+    assert torch.equal(Op, Oc)
+    Kph = host(Kpd.view(torch.int16) if bf16 else Kpd).reshape(nblk, nkv, page, d)
+    Kch = host(Kc.view(torch.int16) if bf16 else Kc)
+    for t in range(n0, cap):
+        assert np.array_equal(Kph[row[t // page], :, t % page].reshape(-1), Kch[t]), t
+    R = oracle.attn_prefill(host(qc), host(Kc.view(torch.int16)).view(np.uint16) if bf16 else
+                            host(Kc), host(Vc.view(torch.int16)).view(np.uint16) if bf16 else
+                            host(Vc), nq, nkv, M, cap, d, s, n0, 0)
+    assert normwise_err(host(Oc), R) < TOL
+
+
 def test_prefill_2k_prompt(gpu):
     """A 2048-token prompt at the headline head shape (the bench workload)."""
     announce("prefill 32q/8kv/d128 M=2048 fresh")
