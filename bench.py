@@ -380,7 +380,7 @@ def main() -> int:
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the path shards by KV head across GPUs with no exchange (see DESIGN.md), "
+              "the path would shard by KV head across GPUs with no exchange, "
               "but nothing here launches on more than one device.", file=sys.stderr)
         return 2
 

@@ -37,7 +37,7 @@ extern "C" {
 /* Q8: each KV head row of d values is quantized as quantize_q8_row
  * (include/molot/quant.h:34-50): fp32 scale s = absmax/127 (1 when not > 0),
  * int8 codes clamp(nearbyint(x/s), -127, 127); it dequantizes as code * s.
- * The reference plans an int8 KV cache (DESIGN.md:48, exp/README.md:36-39)
+ * The reference plans an int8 KV cache (its DESIGN.md:48, exp/README.md:36-39)
  * without fixing a layout; this library's layouts, in bytes:
  *   token-major  row t = [nkv][d] codes, then nkv fp32 scales, padded to 16
  *                bytes: molot_hip_q8_row_bytes(nkv, d) bytes per token;

@@ -5,8 +5,9 @@
 // No reference counterpart: the reference keeps one contiguous fp32 cache
 // per layer and sequence (Runner::KVC, include/molot/forward.h:48-51, one
 // Runner per chat); its design notes plan vLLM-style 16-token pages
-// (DESIGN.md:47-48) and its README lists them as not implemented
-// (README.md:112-114).  This class is that caller side:
+// (the reference's DESIGN.md:47-48) and its README lists them as not
+// implemented (the reference's README.md:112-114).  This class is that
+// caller side:
 //   * one pool of pages per layer, [num_blocks][nkv][page][hd] (a Q8 pool:
 //     MOLOT_KV_Q8 blocks of molot_hip_q8_block_bytes each), all layers
 //     sharing one block allocator, so a sequence's block ids are the same in
