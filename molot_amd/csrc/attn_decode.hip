@@ -37,7 +37,6 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // ---------------------------------------------------------------------------
 // KV element traits: one 16-byte vector = VW elements.
@@ -1530,69 +1529,18 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   // by scale*log2(e), in three bf16 pieces
   const float qsc = a.scale * kLog2e;
   bf16x8_t qh[KK], qm[KK], ql[KK];
-  if constexpr (!Q8) {
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
+  for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int di = 32 * kk + 8 * g4 + e;
-        const float x = m16 < GH ? qs[m16 * D + di] * qsc : 0.f;
-        __bf16 hi, mid, lo;
-        split3(x, hi, mid, lo);
-        qh[kk][e] = hi;
-        qm[kk][e] = mid;
-        ql[kk][e] = lo;
-      }
-  }
-  // Q8: q^T as the B operand of v_mfma_i32_16x16x64_i8, whose A operand is
-  // the K codes as they load: lane l holds head l%16 (zero past GH), bytes
-  // 64j + 16*(l/16) + b, as three int8 pieces of one per-head scale sq =
-  // max|q|/127: q = (c1 + c2/128 + c3/16384) * sq to 2^-22 of max|q|.  The
-  // products are exact int32 sums, one accumulator per piece.
-  [[maybe_unused]] i32x4 qi[3][Q8 ? KL : 1];
-  [[maybe_unused]] float qs1 = 0.f, qs2 = 0.f, qs3 = 0.f;
-  if constexpr (Q8) {
-    float xv[KL][16];
-    float amax = 0.f;
-#pragma unroll
-    for (int j = 0; j < KL; ++j)
-#pragma unroll
-      for (int b = 0; b < 16; ++b) {
-        xv[j][b] = m16 < GH ? qs[m16 * D + 64 * j + 16 * g4 + b] * qsc : 0.f;
-        amax = fmaxf(amax, fabsf(xv[j][b]));
-      }
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
-    const float sq = amax > 0.f ? amax / 127.f : 1.f;
-    qs1 = sq;
-    qs2 = sq * (1.f / 128.f);
-    qs3 = sq * (1.f / 16384.f);
-    const float rq = 1.f / sq;
-    auto code = [](float c) -> uint32_t { return (uint32_t)(int)fminf(fmaxf(c, -127.f), 127.f) & 0xFFu; };
-#pragma unroll
-    for (int j = 0; j < KL; ++j)
-#pragma unroll
-      for (int w4 = 0; w4 < 4; ++w4) {
-        uint32_t p1 = 0, p2 = 0, p3 = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // codes by one reciprocal: any rounding of a code is taken up by
-          // the next piece (the representation is c1*qs1 + c2*qs2 + c3*qs3)
-          const float x = xv[j][4 * w4 + e];
-          const float c1 = rintf(x * rq);
-          float r = x - c1 * qs1;
-          const float c2 = rintf(r * (128.f * rq));
-          r -= c2 * qs2;
-          const float c3 = rintf(r * (16384.f * rq));
-          p1 |= code(c1) << (8 * e);
-          p2 |= code(c2) << (8 * e);
-          p3 |= code(c3) << (8 * e);
-        }
-        qi[0][j][w4] = (int)p1;
-        qi[1][j][w4] = (int)p2;
-        qi[2][j][w4] = (int)p3;
-      }
-  }
+    for (int e = 0; e < 8; ++e) {
+      const int di = Q8 ? 64 * (kk >> 1) + 16 * g4 + 8 * (kk & 1) + e : 32 * kk + 8 * g4 + e;
+      const float x = m16 < GH ? qs[m16 * D + di] * qsc : 0.f;
+      __bf16 hi, mid, lo;
+      split3(x, hi, mid, lo);
+      qh[kk][e] = hi;
+      qm[kk][e] = mid;
+      ql[kk][e] = lo;
+    }
 
   // ---- stream ----
   char* vt = reinterpret_cast<char*>(smem + L.vt + w * RS);
@@ -1649,17 +1597,19 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     for (int u = 0; u < 2; ++u) {
       sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
       if constexpr (Q8) {
-        i32x4 a1 = {0, 0, 0, 0}, a2 = {0, 0, 0, 0}, a3 = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < KL; ++j) {
-          const i32x4 kc = __builtin_bit_cast(i32x4, kr[u][j]);
-          a3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kc, qi[2][j], a3, 0, 0, 0);
-          a2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kc, qi[1][j], a2, 0, 0, 0);
-          a1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(kc, qi[0][j], a1, 0, 0, 0);
+          u32x4 lo, hi;
+          i8x16_to_bf16(kr[u][j], lo, hi);
+          const bf16x8_t k0 = __builtin_bit_cast(bf16x8_t, lo);
+          const bf16x8_t k1 = __builtin_bit_cast(bf16x8_t, hi);
+          sacc[u] = mfma_bf16(k0, ql[2 * j], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qm[2 * j], sacc[u]);
+          sacc[u] = mfma_bf16(k0, qh[2 * j], sacc[u]);
+          sacc[u] = mfma_bf16(k1, ql[2 * j + 1], sacc[u]);
+          sacc[u] = mfma_bf16(k1, qm[2 * j + 1], sacc[u]);
+          sacc[u] = mfma_bf16(k1, qh[2 * j + 1], sacc[u]);
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r)  // exact integers (|a| < 2^21), smallest piece first
-          sacc[u][r] = fmaf((float)a1[r], qs1, fmaf((float)a2[r], qs2, (float)a3[r] * qs3));
       } else {
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {

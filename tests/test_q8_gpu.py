@@ -93,6 +93,26 @@ def test_q8_decode_vs_oracle(gpu, nq, nkv, d, n, pos, window):
     assert err < TOL
 
 
+@pytest.mark.parametrize("factor", [100.0, 1000.0])
+def test_q8_decode_outlier_q_channels(gpu, factor):
+    """q with a few channels factor x the rest (LLM activations have such
+    outliers), at the usual 1/sqrt(d) scale: the scores' int8 pieces share
+    one scale per head, so this is where their resolution would show."""
+    announce(f"q8 decode with {factor:g}x outlier q channels")
+    st = Stream(int(factor) + 5)
+    nq, nkv, d, n = 32, 8, 128, 3000
+    Q = st.normal((nq, d))
+    Q[:, [3, 40, 77, 100]] *= factor
+    Kq, Vq = q8_caches(st, n, nkv, d)
+    O = torch.empty((nq, d), device="cuda")
+    s = 1 / math.sqrt(d)
+    attn.attn_decode_gqa_cache(dev(Q), dev_u8(Kq), dev_u8(Vq), O, nq, nkv, n, d, s, n - 1, 0)
+    R = oracle.attn_decode_gqa_cache(Q, Kq, Vq, nq, nkv, n, d, s, n - 1, 0)
+    err = normwise_err(host(O), R)
+    print(f"q8 outlier normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
 def test_q8_equals_fp32_on_dequantized_rows(gpu):
     """Q8 attention == fp32-cache attention on the dequantized rows (the
     fp32 vector-ALU kernel), to fp32 rounding."""
