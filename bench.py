@@ -8,7 +8,7 @@ scale 1/sqrt(128), batch 1, q/K/V ~ N(0,1) from the repo's seeded generator.
 `--config c1|c3|c4|c5` measures the other BASELINE configs the same way
 (c4: 64 sequences over a paged bf16 cache, molot_hip_decode_step_paged);
 c2q8|c4q8|c5q8 run c2, c4 and c5 over Q8 caches (int8 codes + an fp32 scale
-per KV head row); p1|p2 time the layer prefill.
+per KV head row); p1|p2|p3 time the layer prefill (p3: d = 256, windowed).
 
 One step = one layer-step of the hot path through the C ABI
 (molot_hip_decode_step): RoPE of q and k, append of k/v into the cache,
@@ -69,6 +69,8 @@ CONFIGS = {
                n0=0),
     "p2": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=0, sigma=1.0, prompt=512,
                n0=16384),
+    "p3": dict(nq=8, nkv=4, d=256, theta=10000.0, window=1024, kvd=0, sigma=1.0, prompt=2048,
+               n0=0),
 }
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, published
@@ -86,6 +88,7 @@ DESCR = {
     "p1": "layer prefill (RoPE + append + causal attention), 2048-token prompt, 32q/8kv/d128 "
           "fp32 KV",
     "p2": "layer prefill, 512-token prompt after 16384 cached tokens, 32q/8kv/d128 fp32 KV",
+    "p3": "layer prefill, 2048-token prompt, Gemma-style 8q/4kv/d256, window 1024, fp32 KV",
 }
 
 
@@ -655,7 +658,7 @@ def run_prefill(args, cfg, lib, L, torch, np):
                                       ctypes.byref(nc)), "profile_end")
     k_us = am.value / max(1, na.value) * 1e3
     achieved = flops / (k_us * 1e-6) / 1e12
-    kname = "prefill_mfma16_kernel" if d <= 128 else "prefill_kernel"
+    kname = "prefill_mfma16_kernel"
     log(args, f"{kname} {k_us:.1f} us/launch -> {achieved:.1f} TFLOP/s")
     out = {
         "metric": "prefill attention TFLOP/s (causal, 4*d flops per head x query x key)",
@@ -674,14 +677,14 @@ def run_prefill(args, cfg, lib, L, torch, np):
                    "head_dim": d, "prompt": M, "cached": n0, "window": window,
                    "rope_theta": theta, "timing": "eager"},
         "flops_per_step": flops,
-        # peak: the fp32 matrix peak, the precision the products keep.  d <= 128
-        # takes each fp32 product as six bf16 piece products on the bf16 matrix
-        # cores, whose instruction ceiling for that is 2500 / 6 TFLOP/s.
+        # peak: the fp32 matrix peak, the precision the products keep.  The
+        # kernel takes each fp32 product as six bf16 piece products on the bf16
+        # matrix cores, whose instruction ceiling for that is 2500 / 6 TFLOP/s.
         "roofline": {"bound": "mfma", "kernel": "%s<%d,float>" % (kname, d),
                      "achieved": round(achieved, 2), "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
                      "traffic": None, "launch_us": round(k_us, 2),
-                     "bf16_piece_ceiling": round(BF16_MFMA_PEAK_TFLOPS / 6, 1) if d <= 128 else None},
+                     "bf16_piece_ceiling": round(BF16_MFMA_PEAK_TFLOPS / 6, 1)},
     }
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline_prefill(args, q_h, K_h, V_h, nq, nkv, d, M, N, n0,

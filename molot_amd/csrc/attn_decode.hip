@@ -1787,20 +1787,12 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 //
 // The query rows of one KV head are r = m*G + g: token m (position pos0 + m)
 // and q head h*G + g of the group.  A workgroup of 4 waves owns 64
-// consecutive rows, wave w the 16 rows w*16.. on the 16 columns of
-// v_mfma_f32_16x16x4f32 (fp32 operands: exact products).  It streams the keys
-// its rows attend, KT per tile, through LDS -- K row-major [KT][D+4], V
-// transposed [D][KT+4] (the padding spreads rows over the banks) -- with the
-// next tile's global loads in flight while the current one is used:
-//   S^T (KT keys x 16 rows) = K . Q^T per 16-key half: A = K from LDS (lane:
-//   key l%16; one ds_read_b128 of d = 16J + 4*(l/16) .. +3 feeds four
-//   k-steps), B = Q^T held in registers in that same d order.
-//   Online softmax per row (accumulator column l%16), each row masked to its
-//   own causal end min(pos+1, N) and window start.
-//   O^T (D x 16) += V^T . P^T per 16-row block of D: k-step j of half u pairs
-//   lane group g with key 16u + 4g + j, where the score accumulator left
-//   that key's probability (its rows 4g + r, r = j): P is the B operand in
-//   place, and V^T comes four keys per ds_read_b128.
+// consecutive rows, wave w the 16 rows w*16.. on the 16 columns of the
+// matrix instructions.  It streams the keys its rows attend, 32 per tile,
+// through LDS, with the next tile's global loads in flight while the
+// current one is used; each row is masked to its own causal end
+// min(pos+1, N) and window start.  Query blocks run from the last (most
+// keys) to the first, heads fastest across the grid.
 // The reference's exps are libm expf summed in double with the weights
 // normalised before PV; here the hardware base-2 exp of scores pre-scaled by
 // log2(e), fp32 running sums with a lazy max rescale, and one division at
@@ -1819,238 +1811,13 @@ struct PfArgs {
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = kPfWaves * 64;
 
-template <int D, typename T, bool PAGED>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
-  constexpr int NT = kPfThreads, QB = 16 * kPfWaves;
-  constexpr int KT = D == 256 ? 16 : 32;  // keys per tile (LDS under 64 KiB)
-  constexpr int KH = KT / 16;             // 16-key halves per tile
-  constexpr int KSR = D + 4, VSR = KT + 4;
-  constexpr int JS = D / 4, DT = D / 16;
-  constexpr int VW = KVT<T>::VW;          // elements per 16-byte load
-  constexpr int CH = KT * D / VW;         // 16-byte chunks per tile (K or V)
-  constexpr int CPT = (CH + NT - 1) / NT;
-  constexpr bool Q8 = std::is_same<T, q8_t>::value;
-  static_assert(CH % NT == 0 || CH < NT, "whole chunks per thread");
-  static_assert(KT % 16 == 0 && (D / VW) % 4 == 0 && CH % 64 == 0, "chunk mapping");
-  __shared__ __attribute__((aligned(16))) float ks[KT * KSR];
-  __shared__ __attribute__((aligned(16))) float vs[D * VSR];
-
-  const int G = a.nq / a.nkv;
-  const int h = blockIdx.x % a.nkv;  // heads fastest: every XCD gets every head's share
-  const int qb = a.nqb - 1 - (int)(blockIdx.x / a.nkv);  // latest rows (most keys) first
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c16 = lane & 15, g4 = lane >> 4;
-  const int rows = a.M * G;
-  const int r0 = qb * QB;  // first row of the workgroup (< rows)
-  const int rl = min(r0 + QB, rows) - 1;
-
-  auto t0_of = [&](int m) {
-    const int pos = a.pos0 + m;
-    int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
-    return t0 > a.N ? a.N : t0;
-  };
-  auto nn_of = [&](int m) { return a.pos0 + m + 1 < a.N ? a.pos0 + m + 1 : a.N; };
-  // the workgroup's key range: t0 and the causal end grow with the token
-  const int kt_lo = t0_of(r0 / G);
-  const int kt_hi = nn_of(rl / G);
-  const int ntile = kt_hi > kt_lo ? (kt_hi - kt_lo + KT - 1) / KT : 0;
-
-  // this lane's query row (column c16 of wave w)
-  const int row = r0 + 16 * w + c16;
-  const bool rv = row < rows;
-  const int m = rv ? row / G : 0;
-  const int g = rv ? row - m * G : 0;
-  const int rt0 = rv ? t0_of(m) : 0, rnn = rv ? nn_of(m) : 0;
-  const int64_t qoff = ((int64_t)m * a.nq + h * G + g) * D;
-
-  // Q^T in the k order of the score product, pre-scaled by scale*log2(e):
-  // the scores come out in base-2 units (the softmax below)
-  float qv[JS];
-  const float qsc = a.scale * kLog2e;
-#pragma unroll
-  for (int J = 0; J < D / 16; ++J) {
-    f32x4 x = rv ? *reinterpret_cast<const f32x4*>(a.q + qoff + 16 * J + 4 * g4)
-                 : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qv[4 * J + i] = x[i] * qsc;
-  }
-
-  // tile loads: chunk c = tid + NT*i.  Within a wave, lanes l and l + 16*x
-  // hold keys l%16 (+16 per 64 chunks, up to KT) and element groups l/16 + 4
-  // per KT/16 such blocks: each load instruction reads 64 contiguous bytes
-  // of 16 rows, and the transposed V stores of 16 lanes hit 16 banks (one
-  // key per lane; a key-major mapping put 16 lanes of one key on one bank).
-  auto chunk_of = [&](int c, int& key, int& e) {
-    constexpr int KT16 = KT / 16;
-    key = (c & 15) + 16 * ((c >> 6) % KT16);
-    e = VW * (((c >> 4) & 3) + 4 * ((c >> 6) / KT16));
-  };
-  const T* Kb = reinterpret_cast<const T*>(a.k);
-  const T* Vb = reinterpret_cast<const T*>(a.v);
-  // Q8 byte layouts: token-major rows of R bytes, paged blocks of BB bytes
-  const int pg = 1 << a.page_shift;
-  const int64_t R = (int64_t)a.nkv * D + ((4 * a.nkv + 15) & ~15);
-  const int64_t BB = (int64_t)a.nkv * pg * (D + 4);
-  // element (Q8: byte) offset of row t of head h, and (Q8) of its scale
-  auto row_off = [&](int t, int64_t& soff) -> int64_t {
-    if constexpr (PAGED) {
-      const int64_t blk = a.block_table[t >> a.page_shift];
-      const int sl = t & (pg - 1);
-      if constexpr (Q8) {
-        soff = blk * BB + (int64_t)a.nkv * pg * D + 4 * ((int64_t)h * pg + sl);
-        return blk * BB + ((int64_t)h * pg + sl) * D;
-      }
-      return (blk * a.nkv + h) * pg * D + (int64_t)sl * D;
-    } else {
-      if constexpr (Q8) {
-        soff = (int64_t)t * R + (int64_t)a.nkv * D + 4 * h;
-        return (int64_t)t * R + (int64_t)h * D;
-      }
-      return (int64_t)t * a.nkv * D + (int64_t)h * D;
-    }
-  };
-  typename KVT<T>::vec kreg[CPT], vreg[CPT];
-  [[maybe_unused]] float ksc[CPT], vsc[CPT];  // Q8: the chunks' row scales
-  auto load_tile = [&](int tk) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + NT * i;
-      if (CH < NT && c >= CH) break;
-      int key, e;
-      chunk_of(c, key, e);
-      const int t = min(tk + key, kt_hi - 1);  // rows past the range: the last one (masked)
-      int64_t soff = 0;
-      const int64_t off = row_off(t, soff) + e;
-      if constexpr (Q8) {
-        ksc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.k) + soff);
-        vsc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v) + soff);
-      }
-      kreg[i] = load16(Kb + off);
-      vreg[i] = load16(Vb + off);
-    }
-  };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int c = tid + NT * i;
-      if (CH < NT && c >= CH) break;
-      int key, e;
-      chunk_of(c, key, e);
-      float kx[VW], vx[VW];
-      KVT<T>::unpack(kreg[i], kx);
-      KVT<T>::unpack(vreg[i], vx);
-      if constexpr (Q8) {  // code * s, the dequantized value
-#pragma unroll
-        for (int j = 0; j < VW; ++j) {
-          kx[j] *= ksc[i];
-          vx[j] *= vsc[i];
-        }
-      }
-#pragma unroll
-      for (int e4 = 0; e4 < VW; e4 += 4)
-        *reinterpret_cast<f32x4*>(ks + key * KSR + e + e4) =
-            f32x4{kx[e4], kx[e4 + 1], kx[e4 + 2], kx[e4 + 3]};
-#pragma unroll
-      for (int j = 0; j < VW; ++j) vs[(e + j) * VSR + key] = vx[j];
-    }
-  };
-
-  f32x4 o[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-  if (ntile > 0) load_tile(kt_lo);
-  for (int it = 0; it < ntile; ++it) {
-    const int tk = kt_lo + it * KT;
-    store_tile();
-    __syncthreads();
-    if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
-    // scores of the KH 16-key halves (the halves' accumulator chains
-    // interleaved)
-    f32x4 sacc[KH];
-#pragma unroll
-    for (int u = 0; u < KH; ++u) sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int J = 0; J < D / 16; ++J) {
-      f32x4 kx[KH];
-#pragma unroll
-      for (int u = 0; u < KH; ++u)
-        kx[u] = *reinterpret_cast<const f32x4*>(ks + (16 * u + c16) * KSR + 16 * J + 4 * g4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int u = 0; u < KH; ++u)
-          sacc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(kx[u][i], qv[4 * J + i], sacc[u], 0, 0, 0);
-    }
-    // online softmax (base 2) of this lane's row over its 4*KH keys of the
-    // tile.  Lazy rescale, as in the decode kernel: the running max moves
-    // only when a score exceeds it by more than kLazyMax (p <= 2^8
-    // otherwise); o and l always share the max they were formed with.
-    float sv[KH][4];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < KH; ++u)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = tk + 16 * u + 4 * g4 + r;
-        sv[u][r] = (t >= rt0 && t < rnn) ? sacc[u][r] : -INFINITY;
-        tmax = fmaxf(tmax, sv[u][r]);
-      }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const bool grow = tmax > m_run + kLazyMax;  // false while the row has no key (-inf)
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float mn = grow ? fmaxf(m_run, tmax) : m_run;
-      // a row's first keys: nothing to rescale
-      const float alpha = m_run == -INFINITY ? 1.f : exp2_hw(m_run - mn);
-      m_run = mn;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-    }
-    float ps = 0.f;
-#pragma unroll
-    for (int u = 0; u < KH; ++u)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        // masked keys (and a row with no key yet, max -inf): p = 0
-        sv[u][r] = sv[u][r] == -INFINITY ? 0.f : exp2_hw(sv[u][r] - m_run);
-        ps += sv[u][r];
-      }
-    l_run += ps;
-    // PV
-#pragma unroll
-    for (int u = 0; u < KH; ++u)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const f32x4 vx = *reinterpret_cast<const f32x4*>(vs + (16 * dt + c16) * VSR + 16 * u +
-                                                         4 * g4);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(vx[j], sv[u][j], o[dt], 0, 0, 0);
-      }
-    __syncthreads();  // the tile's LDS is rewritten next
-  }
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
-  if (rv) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;  // no key: O = 0 (gemm.h:438)
-    float* orow = a.o + qoff;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<f32x4*>(orow + 16 * dt + 4 * g4) = o[dt] * inv;
-  }
-}
-
-// Causal prefill on the bf16 matrix cores (D = 64, 128): prefill_kernel's
-// work mapping, rows, masking and softmax, with every fp32 product taken as
-// bf16 pieces on v_mfma_f32_16x16x32_bf16 (16x the fp32 matrix rate).
-// x = hi + mid + lo (split3) carries x's 24-bit significand; a product keeps
-// the six piece products down to 2^-16 of its size (hi*hi, hi*mid, mid*hi,
-// hi*lo, lo*hi, mid*mid), so the dropped ones are ~2^-24 of it, an fp32
-// rounding.  A bf16 cache needs one K/V piece (its values are exact): three
-// products.  Tiles of 32 keys are staged into LDS as pieces:
+// The kernel: every fp32 product is taken as bf16 pieces on
+// v_mfma_f32_16x16x32_bf16 (16x the fp32 matrix rate).  x = hi + mid + lo
+// (split3) carries x's 24-bit significand; a product keeps the six piece
+// products down to 2^-16 of its size (hi*hi, hi*mid, mid*hi, hi*lo, lo*hi,
+// mid*mid), so the dropped ones are ~2^-24 of it, an fp32 rounding.  A bf16
+// cache needs one K/V piece (its values are exact): three products.  Tiles
+// of 32 keys are staged into LDS as pieces:
 //   K [KP][32 keys][D] bf16, rows padded by 16 bytes (the 16 lanes of a
 //     ds_read_b128 then hit 16 distinct groups of 4 banks), read as the A
 //     operand of S^T = K . Q^T: lane l key 16u + l%16, elements
@@ -2059,9 +1826,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PfArgs a) {
 //     V^T by ds_read_b64_tr_b16 as in attn_mfma_kernel: the A operand of
 //     O^T += V^T . P^T, with P in the registers the score accumulator left
 //     it in (key 16u + 4(l/16) + r of lane l, slot 4u + r).
+// D = 256 stages 100 KB (fp32 pieces) and runs one workgroup per CU.
 template <int D, typename T, bool PAGED>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a) {
-  static_assert(D == 64 || D == 128, "bf16-piece prefill: D = 64 or 128");
+__global__ __launch_bounds__(kPfThreads, D == 256 ? 1 : 2) void prefill_mfma16_kernel(PfArgs a) {
+  static_assert(D == 64 || D == 128 || D == 256, "bf16-piece prefill: D = 64, 128, 256");
   constexpr int NT = kPfThreads, QB = 16 * kPfWaves;
   constexpr int KT = 32, KH = 2;
   constexpr int KP = sizeof(T) == 2 ? 1 : 3;  // staged pieces of K and V
@@ -2129,8 +1897,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
     ql[s] = __builtin_bit_cast(bf16x8_t, u32x4{l4[0], l4[1], l4[2], l4[3]});
   }
 
-  // tile loads: prefill_kernel's chunk mapping (16 consecutive lanes hold 16
-  // keys of one element group)
+  // tile loads: 16 consecutive lanes hold 16 keys of one element group, so
+  // each load instruction reads 64 contiguous bytes of 16 rows
   auto chunk_of = [&](int c, int& key, int& e) {
     constexpr int KT16 = KT / 16;
     key = (c & 15) + 16 * ((c >> 6) % KT16);
@@ -2257,8 +2025,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_mfma16_kernel(PfArgs a)
           sacc[u] = mfma_bf16(k0, qh[s], sacc[u]);
         }
       }
-    // online softmax (base 2, lazy rescale) of this lane's row over its 8
-    // keys of the tile, as in prefill_kernel
+    // online softmax (base 2) of this lane's row over its 8 keys of the tile.
+    // Lazy rescale, as in the decode kernel: the running max moves only when
+    // a score exceeds it by more than kLazyMax (p <= 2^8 otherwise); o and l
+    // always share the max they were formed with.
     float sv[KH][4];
     float tmax = -INFINITY;
 #pragma unroll
@@ -3445,8 +3215,6 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
       return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
-  // D = 64, 128: bf16 pieces on the bf16 matrix cores; D = 256 (whose
-  // staged pieces would leave one workgroup per CU): fp32 matrix cores
   using PfFn = void (*)(PfArgs);
   PfFn pk;
   if (kv_dtype == MOLOT_KV_Q8)  // D = 64, 128 (check_common)
@@ -3458,18 +3226,18 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     pk = kv_dtype == MOLOT_KV_F32
              ? (d == 64 ? prefill_mfma16_kernel<64, float, false>
                         : d == 128 ? prefill_mfma16_kernel<128, float, false>
-                                   : prefill_kernel<256, float, false>)
+                                   : prefill_mfma16_kernel<256, float, false>)
              : (d == 64 ? prefill_mfma16_kernel<64, bf16_t, false>
                         : d == 128 ? prefill_mfma16_kernel<128, bf16_t, false>
-                                   : prefill_kernel<256, bf16_t, false>);
+                                   : prefill_mfma16_kernel<256, bf16_t, false>);
   else
     pk = kv_dtype == MOLOT_KV_F32
              ? (d == 64 ? prefill_mfma16_kernel<64, float, true>
                         : d == 128 ? prefill_mfma16_kernel<128, float, true>
-                                   : prefill_kernel<256, float, true>)
+                                   : prefill_mfma16_kernel<256, float, true>)
              : (d == 64 ? prefill_mfma16_kernel<64, bf16_t, true>
                         : d == 128 ? prefill_mfma16_kernel<128, bf16_t, true>
-                                   : prefill_kernel<256, bf16_t, true>);
+                                   : prefill_mfma16_kernel<256, bf16_t, true>);
   const dim3 grid((unsigned)(nqb * nkv));
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {
