@@ -108,7 +108,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--split-chunk", type=int, default=0, help="tokens per chunk (0 = auto)")
     ap.add_argument("--wgs-per-cu", type=int, default=0, help="workgroups per CU (0 = auto)")
-    ap.add_argument("--variant", type=int, default=0, help="kernel mapping variant (0 = default)")
+    ap.add_argument("--merge", type=int, default=0,
+                    help="1 = split-K partials merged inside the attention launch where possible, "
+                         "0 = by the combine kernel (default)")
     ap.add_argument("--norms", action="store_true",
                     help="the step with the layer's q/k/v RMS norms fused in (forward.h:554-563)")
     ap.add_argument("--block-order", type=int, default=1,
@@ -400,8 +402,9 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.split_chunk:
         attn.set_split_chunk(args.split_chunk)
-    if args.wgs_per_cu or args.variant:
-        lib.molot_hip_set_tuning(args.wgs_per_cu, args.variant)
+    if args.wgs_per_cu:
+        lib.molot_hip_set_tuning(args.wgs_per_cu)
+    lib.molot_hip_set_merge(args.merge)
     lib.molot_hip_set_block_order(args.block_order)
 
     cfg = CONFIGS[args.config]

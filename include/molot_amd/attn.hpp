@@ -7,7 +7,10 @@
 //   molot::amd::rope_apply             <- include/molot/attn.h:19
 //   molot::amd::rope_inv_freq          <- include/molot/attn.h:31
 //   molot::amd::DeviceKV               <- Runner::KVC, include/molot/forward.h:48-51,
-//                                         with the decode block forward.h:556-591
+//                                         with the decode block forward.h:554-591
+//                                         and the prefill block :367-399, for
+//                                         layers with their own KV and layers
+//                                         reading another layer's (shared KV)
 // The reference's ThreadPool& argument is accepted and ignored.  Calls are
 // synchronous like the reference's (outputs are valid on return); Q/O may be
 // host or device pointers (host ones are staged through per-thread device
@@ -150,7 +153,9 @@ struct LayerNorms {
 };
 
 // Device KV cache of one layer (Runner::KVC, forward.h:48-51) with the
-// decode-attention block of forward.h:556-591 in one fused launch.
+// decode-attention block of forward.h:554-591 in one fused launch, the
+// layer prefill (forward.h:367-399), and the same blocks for layers that
+// read this cache as shared KV (forward.h:578-591, :394-398).
 class DeviceKV {
  public:
   int n = 0, cap = 0, nkv = 0, hd = 0, kv_dtype = MOLOT_KV_F32;
@@ -180,7 +185,8 @@ class DeviceKV {
   // forward.h:556-591 for a layer that owns its KV: q (nq heads) rotated in
   // place, k rotated and appended with v at slot n, n++, then attention into
   // ao.  q, k, v, ao may be host or device pointers; inv_freq is a device
-  // table of hd/2 floats (the layer's L.freq).
+  // table of hd/2 floats (the layer's L.freq), or NULL for a layer without
+  // RoPE (an empty L.freq: forward.h:556, :566 skip the rotation).
   void decode(float* q, const float* knew, const float* vnew, float* ao, int nq, int pos,
               const float* inv_freq, float scale, int window, hipStream_t s = nullptr) {
     decode(q, knew, vnew, ao, nq, pos, inv_freq, scale, window, LayerNorms{}, s);
@@ -218,7 +224,53 @@ class DeviceKV {
     view.finish(s);
   }
 
-  // forward.h:589-590 alone (e.g. a layer reading this cache as shared KV).
+  // forward.h:554-558 and 578-591 for a layer without its own KV (L.has_kv
+  // false) reading this cache: q (nq heads) normed with nm.q_norm and
+  // rotated at pos (inv_freq NULL: a layer without RoPE) in place, then
+  // attention over this cache's n slots into ao; nothing appended.  q, ao
+  // may be host or device pointers.
+  void decode_shared(float* q, float* ao, int nq, int pos, const float* inv_freq, float scale,
+                     int window, const LayerNorms& nm = LayerNorms{},
+                     hipStream_t s = nullptr) const {
+    if (n == 0) throw std::runtime_error("fwd: shared KV empty");  // forward.h:580
+    QOView view(q, ao, (size_t)nq * hd, (size_t)nq * hd, s);
+    if (!view.q_dev) view.q_host_rot = q;
+    check(molot_hip_decode_step_shared(const_cast<float*>(view.q), k, v, view.o, nq, nkv, hd, n,
+                                       pos, nm.q_norm, nm.eps, inv_freq, scale, window, kv_dtype,
+                                       s),
+          "decode_step_shared");
+    view.finish(s);
+  }
+
+  // forward.h:367-399 for a layer that owns this cache: M prompt tokens'
+  // Q [M][nq][hd] (normed, rotated in place), K_new/V_new [M][nkv][hd]
+  // (normed, rotated, appended at slots n .. n+M-1), AO [M][nq][hd]: device
+  // pointers.  Positions pos0 .. pos0+M-1; asynchronous on s.
+  void prefill(float* Q, const float* K_new, const float* V_new, float* AO, int nq, int M,
+               int pos0, const float* inv_freq, float scale, int window,
+               const LayerNorms& nm = LayerNorms{}, hipStream_t s = nullptr) {
+    if (n + M > cap) throw std::runtime_error("fwd: KV cache full");  // forward.h:385
+    check(molot_hip_prefill_step(Q, K_new, V_new, k, v, AO, nq, nkv, hd, M, n, pos0, nm.q_norm,
+                                 nm.k_norm, nm.v_norm ? 1 : 0, nm.eps, inv_freq, scale, window,
+                                 kv_dtype, s),
+          "prefill_step");
+    n += M;
+  }
+
+  // forward.h:367-399 for a layer without its own KV reading this cache
+  // (which already holds the prompt: the source layer ran first): Q
+  // [M][nq][hd] normed and rotated in place, causal attention over this
+  // cache's n slots into AO; device pointers, asynchronous on s.
+  void prefill_shared(float* Q, float* AO, int nq, int M, int pos0, const float* inv_freq,
+                      float scale, int window, const LayerNorms& nm = LayerNorms{},
+                      hipStream_t s = nullptr) const {
+    check(molot_hip_prefill_q(Q, nq, hd, M, pos0, nm.q_norm, nm.eps, inv_freq, s), "prefill_q");
+    check(molot_hip_attn_prefill_gqa(Q, k, v, AO, nq, nkv, M, n, hd, scale, pos0, window,
+                                     kv_dtype, s),
+          "attn_prefill_gqa");
+  }
+
+  // forward.h:589-590 alone (attention over this cache, q as given).
   void attend(const float* q, float* ao, int nq, float scale, int pos_cur, int window,
               hipStream_t s = nullptr) const {
     if (n == 0) throw std::runtime_error("fwd: shared KV empty");  // forward.h:580

@@ -21,6 +21,12 @@
  * Semantics (include/molot/attn.h:125-177): n = valid slots after the
  * append, window <= 0 attends [0, n), otherwise [t0, n) with
  * t0 = max(0, pos_cur - window + 1); an empty range yields o = 0.
+ *
+ * RoPE tables: every entry that rotates takes inv_freq, a device table of
+ * d/2 floats (the layer's L.freq, include/molot/model.h:530-549).  Except
+ * for molot_hip_rope_apply, inv_freq may be NULL: the layer has no RoPE
+ * (an empty L.freq, model.h:535-536), and q and k pass unrotated, as
+ * forward.h:373, :381, :556 and :566 skip rope_apply for such layers.
  */
 #ifndef MOLOT_AMD_ATTN_HIP_H_
 #define MOLOT_AMD_ATTN_HIP_H_
@@ -218,20 +224,77 @@ int molot_hip_prefill_step_paged(float* q, const float* k_new, const float* v_ne
                                  const float* inv_freq, float scale, int window, int kv_dtype,
                                  void* stream);
 
+/* Layers that read another layer's KV cache (L.has_kv false: the shared-KV
+ * tail of include/molot/model.h:562-583).  The reference norms and rotates
+ * q as for any layer and attends the source layer's cache kv[L.kv_src]
+ * over its n = src.n slots, appending nothing (forward.h:554-558, 578-591
+ * for decode; :370-375, 394-398 for prefill). */
+
+/* Decode step of such a layer over a token-major cache: q[nq][d] RMS-normed
+ * per head with q_norm (NULL: no norm; eps >= 0) and rotated at pos
+ * (inv_freq NULL: no RoPE), in place, then attention over the source cache
+ * K/V's n slots (n >= 1: forward.h:580 throws "shared KV empty" at 0) into
+ * O, with pos_cur = pos.  One launch (two with a split context that cannot
+ * be merged in the launch). */
+int molot_hip_decode_step_shared(float* q, const void* K, const void* V, float* O, int nq,
+                                 int nkv, int d, int n, int pos, const float* q_norm, float eps,
+                                 const float* inv_freq, float scale, int window, int kv_dtype,
+                                 void* stream);
+
+/* The same per sequence of a batch over a paged cache (no reference
+ * counterpart): sequence b attends the rows [t0_b, seq_lens[b]) of the
+ * source layer's pages (seq_lens[b] >= 1), pos[b] as in
+ * molot_hip_attn_decode_paged. */
+int molot_hip_decode_step_paged_shared(float* q, const void* K, const void* V, float* O,
+                                       const int32_t* block_table, const int32_t* seq_lens,
+                                       const int32_t* pos, int B, int max_blocks, int max_seq_len,
+                                       int nq, int nkv, int d, int page, const float* q_norm,
+                                       float eps, const float* inv_freq, float scale, int window,
+                                       int kv_dtype, void* stream);
+
+/* Query prologue of a prefill without an append (forward.h:370-375 for a
+ * layer without its own KV): the nq heads of row m of q[M][nq][d] RMS-normed
+ * with q_norm and rotated at pos0 + m, in place; NULL skips either.  Then
+ * molot_hip_attn_prefill_gqa (or _paged) over the source layer's cache is
+ * forward.h:394-398. */
+int molot_hip_prefill_q(float* q, int nq, int d, int M, int pos0, const float* q_norm, float eps,
+                        const float* inv_freq, void* stream);
+
+/* molot_hip_attn_prefill_gqa over one sequence of a paged cache (no
+ * reference counterpart): pages [num_blocks][nkv][page][d] through its
+ * block-table row block_row[max_blocks] (device int32), N <= max_blocks*page
+ * valid slots. */
+int molot_hip_attn_prefill_paged(const float* Qm, const void* K, const void* V, float* Om,
+                                 const int32_t* block_row, int max_blocks, int page, int nq,
+                                 int nkv, int M, int N, int d, float scale, int pos0, int window,
+                                 int kv_dtype, void* stream);
+
 /* Softmax exponential used by the attention kernels, applied elementwise
  * (x, y device [n]).  Counterpart of exp_avx512_ps, include/molot/norm.h:35-47,
  * exposed so its accuracy can be checked against the reference's
  * known-answer points (bench/bench.cc:220-234). */
 int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream);
 
-/* Split-K tuning knob (0 = automatic): tokens per workgroup chunk.  Applies
- * to subsequent launches from this process. */
+/* Process-wide settings (no reference counterpart; for measurement and
+ * tests).  Each is an atomic that launches read when they are planned, so
+ * setting one while other host threads launch is safe; it applies to
+ * launches planned afterwards. */
+
+/* Split-K chunk size in tokens (0 = automatic). */
 void molot_hip_set_split_chunk(int tokens);
 
-/* Tuning knobs for measurement sweeps (0 = default): workgroups per CU of
- * the split-K launch, and an alternative work mapping of the 32q/8kv/d128
- * fp32 kernels (1..6).  Process-wide; apply to subsequent launches. */
-void molot_hip_set_tuning(int wgs_per_cu, int variant);
+/* Workgroups per CU the split-K plan targets (0 = the plan's own). */
+void molot_hip_set_tuning(int wgs_per_cu);
+
+/* How a split context's chunk partials are merged.  in_launch = 0
+ * (default): by a second kernel (combine_kernel) on the same stream.
+ * in_launch = 1: inside the attention launch, by the workgroup that
+ * completes a (sequence, KV head group) slot, where the device dispatches
+ * workgroup i to XCD i % 8 (checked once per device) and the launch can
+ * keep a slot's chunks on one XCD; other launches use the combine kernel.
+ * Both give the same result to fp32 rounding; on the measured MI355X boxes
+ * the second launch was the faster of the two. */
+void molot_hip_set_merge(int in_launch);
 
 /* Order in which the waves of a workgroup take their chunk's row blocks.
  * dynamic = 1 (default): a wave takes the next free block when it has one

@@ -92,8 +92,10 @@ class PagedKVCache {
   // ---- decode: one new token for each sequence of a batch ----
   // Reserves a slot per sequence and uploads the batch's block table
   // [B][max_blocks] and lengths (counting the new token) on stream s.
+  // Throws "fwd: KV cache full" (forward.h:570) before any state of the
+  // step is set when the pool cannot hold the batch's new tokens.
   void begin_decode(const std::vector<int>& ids, hipStream_t s = nullptr) {
-    batch_ = ids;
+    if (mode_ != Mode::None) throw std::runtime_error("PagedKVCache: a step is in progress");
     std::vector<int32_t> lens(ids.size());
     int maxb = 1;
     for (size_t i = 0; i < ids.size(); ++i) {
@@ -102,6 +104,7 @@ class PagedKVCache {
       maxb = std::max(maxb, (int)seq(ids[i]).blocks.size());
     }
     upload(ids, maxb, lens, s);
+    batch_ = ids;
     mode_ = Mode::Decode;
   }
   // forward.h:554-591 for one layer over the batch: q [B][nq][hd] (normed
@@ -117,14 +120,31 @@ class PagedKVCache {
               nm.v_norm ? 1 : 0, nm.eps, inv_freq, scale, window, kv_dtype_, s),
           "decode_step_paged");
   }
+  // forward.h:554-558, 578-591 for a layer without its own KV (L.has_kv
+  // false) reading layer `src`'s pages: q normed and rotated in place
+  // (inv_freq NULL: no RoPE), attention over the batch's rows, which count
+  // this step's token (src appended it earlier in the step); nothing appended.
+  void decode_shared(int src, float* q, float* o, int nq, const float* inv_freq, float scale,
+                     int window, const LayerNorms& nm = LayerNorms{},
+                     hipStream_t s = nullptr) const {
+    if (mode_ != Mode::Decode) throw std::runtime_error("PagedKVCache: decode outside a step");
+    check(molot_hip_decode_step_paged_shared(
+              q, k_.at(src), v_.at(src), o, d_table_, d_lens_, nullptr, (int)batch_.size(), maxb_,
+              max_len_, nq, nkv_, hd_, page_, nm.q_norm, nm.eps, inv_freq, scale, window,
+              kv_dtype_, s),
+          "decode_step_paged_shared");
+  }
   // The batch's token is in every layer's pages: lengths advance by one.
   void end_decode() {
+    if (mode_ != Mode::Decode) throw std::runtime_error("PagedKVCache: no decode step to end");
     for (int id : batch_) seq(id).len += 1;
+    batch_.clear();
     mode_ = Mode::None;
   }
 
   // ---- prefill: M prompt tokens of one sequence ----
   void begin_prefill(int id, int M, hipStream_t s = nullptr) {
+    if (mode_ != Mode::None) throw std::runtime_error("PagedKVCache: a step is in progress");
     if (M <= 0) throw std::runtime_error("PagedKVCache: empty prompt");
     reserve(id, M);
     batch_ = {id};
@@ -145,8 +165,25 @@ class PagedKVCache {
                                        inv_freq, scale, window, kv_dtype_, s),
           "prefill_step_paged");
   }
+  // forward.h:367-399 for a layer without its own KV reading layer `src`'s
+  // pages: the prompt's q [M][nq][hd] normed and rotated in place, causal
+  // attention over the sequence's rows so far (src appended the prompt
+  // earlier in the step); nothing appended.
+  void prefill_shared(int src, float* q, float* o, int nq, int pos0, const float* inv_freq,
+                      float scale, int window, const LayerNorms& nm = LayerNorms{},
+                      hipStream_t s = nullptr) const {
+    if (mode_ != Mode::Prefill) throw std::runtime_error("PagedKVCache: prefill outside a step");
+    check(molot_hip_prefill_q(q, nq, hd_, prefill_m_, pos0, nm.q_norm, nm.eps, inv_freq, s),
+          "prefill_q");
+    check(molot_hip_attn_prefill_paged(q, k_.at(src), v_.at(src), o, d_table_, maxb_, page_, nq,
+                                       nkv_, prefill_m_, seq(batch_[0]).len + prefill_m_, hd_,
+                                       scale, pos0, window, kv_dtype_, s),
+          "attn_prefill_paged");
+  }
   void end_prefill() {
+    if (mode_ != Mode::Prefill) throw std::runtime_error("PagedKVCache: no prefill step to end");
     seq(batch_[0]).len += prefill_m_;
+    batch_.clear();
     mode_ = Mode::None;
   }
 

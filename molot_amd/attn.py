@@ -23,7 +23,8 @@ __all__ = [
     "KV_F32", "KV_BF16", "KV_Q8", "q8_row_bytes", "q8_block_bytes", "rope_inv_freq", "rope_apply", "rope_append", "attn_decode_gqa_cache",
     "attn_decode_gqa", "attn_decode_gqa_win", "attn_decode_head", "attn_decode_head_win",
     "attn_decode_strided", "decode_step", "attn_decode_paged", "decode_step_paged",
-    "rope_append_paged", "vexp",
+    "rope_append_paged", "vexp", "decode_step_shared", "decode_step_paged_shared", "prefill_q",
+    "attn_prefill_paged", "set_merge",
     "last_plan", "set_split_chunk", "attn_prefill_gqa", "prefill_step", "KVCache", "kv_dtype_of",
 ]
 
@@ -114,7 +115,7 @@ def rope_append(q, k_new, v_new, K, V, nq, nkv, d, slot, pos, inv_freq, cap=None
     _need(v_new, "v_new", torch.float32, nkv * d)
     _need(K, "K", _KV_DTYPES, (slot + 1) * row)
     _need(V, "V", K.dtype, (slot + 1) * row)
-    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need_table(inv_freq, d)
     check(_lib.load().molot_hip_rope_append(_ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V),
                                             nq, nkv, d, int(slot), int(pos), _ptr(inv_freq), kvd,
                                             _stream()), "rope_append")
@@ -184,7 +185,7 @@ def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale
     _need(K, "K", _KV_DTYPES, (slot + 1) * row)
     _need(V, "V", K.dtype, (slot + 1) * row)
     _need(O, "O", torch.float32, nq * d)
-    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need_table(inv_freq, d)
     if q_norm is None and k_norm is None and not v_norm:
         check(_lib.load().molot_hip_decode_step(
             _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), nq, nkv, d, int(slot),
@@ -196,6 +197,13 @@ def decode_step(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale
         int(pos), _ptr(q_norm), _ptr(k_norm), int(bool(v_norm)), float(eps), _ptr(inv_freq),
         float(scale), int(window), kvd, _stream()), "decode_step_norm")
     return O
+
+
+def _need_table(inv_freq, d):
+    """A RoPE table of d/2 floats, or None: a layer without RoPE (an empty
+    L.freq, model.h:535-536), whose q and k forward.h leaves unrotated."""
+    if inv_freq is not None:
+        _need(inv_freq, "inv_freq", torch.float32, d // 2)
 
 
 def _need_norms(q_norm, k_norm, d):
@@ -252,7 +260,7 @@ def decode_step_paged(q, k_new, v_new, K, V, O, block_table, seq_lens, pos, B, m
     _need(O, "O", torch.float32, B * nq * d)
     _need(k_new, "k_new", torch.float32, B * nkv * d)
     _need(v_new, "v_new", torch.float32, B * nkv * d)
-    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need_table(inv_freq, d)
     max_len = _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V)
     if B and int(seq_lens.min()) < 1:
         raise ValueError("decode_step_paged: every sequence needs seq_lens >= 1")
@@ -302,7 +310,7 @@ def prefill_step(q, k_new, v_new, K, V, O, nq, nkv, d, M, slot0, pos0, inv_freq,
     _need(O, "O", torch.float32, M * nq * d)
     _need(K, "K", _KV_DTYPES, cap * row)
     _need(V, "V", K.dtype, cap * row)
-    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need_table(inv_freq, d)
     _need_norms(q_norm, k_norm, d)
     check(_lib.load().molot_hip_prefill_step(
         _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(K), _ptr(V), _ptr(O), nq, nkv, d, int(M),
@@ -326,7 +334,7 @@ def prefill_step_paged(q, k_new, v_new, K, V, O, block_row, max_blocks, page, nq
     _need(k_new, "k_new", torch.float32, M * nkv * d)
     _need(v_new, "v_new", torch.float32, M * nkv * d)
     _need(O, "O", torch.float32, M * nq * d)
-    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need_table(inv_freq, d)
     _need(block_row, "block_row", torch.int32, max_blocks)
     bu = _block_units(kvd, nkv, d, page)
     nblocks = K.numel() // bu
@@ -345,6 +353,81 @@ def prefill_step_paged(q, k_new, v_new, K, V, O, block_row, max_blocks, page, nq
     return O
 
 
+def decode_step_shared(q, K, V, O, nq, nkv, d, n, pos, inv_freq, scale, window=0, q_norm=None,
+                       eps=1e-6):
+    """forward.h:554-558, 578-591 for a layer reading another layer's cache
+    K/V (token-major, n >= 1 valid slots): q normed (q_norm) and rotated
+    (inv_freq; None: no RoPE) in place, attention into O; nothing appended."""
+    kvd = kv_dtype_of(K)
+    row = _row_units(kvd, nkv, d)
+    if n < 1:
+        raise RuntimeError("fwd: shared KV empty")  # forward.h:580
+    _need(q, "q", torch.float32, nq * d)
+    _need(O, "O", torch.float32, nq * d)
+    _need(K, "K", _KV_DTYPES, n * row)
+    _need(V, "V", K.dtype, n * row)
+    _need_table(inv_freq, d)
+    _need_norms(q_norm, None, d)
+    check(_lib.load().molot_hip_decode_step_shared(
+        _ptr(q), _ptr(K), _ptr(V), _ptr(O), nq, nkv, d, int(n), int(pos), _ptr(q_norm), float(eps),
+        _ptr(inv_freq), float(scale), int(window), kvd, _stream()), "decode_step_shared")
+    return O
+
+
+def decode_step_paged_shared(q, K, V, O, block_table, seq_lens, pos, B, max_blocks, nq, nkv, d,
+                             page, inv_freq, scale, window=0, q_norm=None, eps=1e-6):
+    """decode_step_shared per sequence of a batch over the source layer's
+    pages: sequence b attends its seq_lens[b] >= 1 rows."""
+    kvd = kv_dtype_of(K)
+    _need(q, "q", torch.float32, B * nq * d)
+    _need(O, "O", torch.float32, B * nq * d)
+    _need_table(inv_freq, d)
+    _need_norms(q_norm, None, d)
+    max_len = _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V)
+    if B and int(seq_lens.min()) < 1:
+        raise RuntimeError("fwd: shared KV empty")
+    check(_lib.load().molot_hip_decode_step_paged_shared(
+        _ptr(q), _ptr(K), _ptr(V), _ptr(O), _ptr(block_table), _ptr(seq_lens), _ptr(pos), B,
+        max_blocks, max_len, nq, nkv, d, page, _ptr(q_norm), float(eps), _ptr(inv_freq),
+        float(scale), int(window), kvd, _stream()), "decode_step_paged_shared")
+    return O
+
+
+def prefill_q(q, nq, d, M, pos0, inv_freq, q_norm=None, eps=1e-6):
+    """forward.h:370-375 for a layer without its own KV: the q heads of M
+    prompt tokens [M][nq][d] normed and rotated at pos0 + m, in place."""
+    _need(q, "q", torch.float32, M * nq * d)
+    _need_table(inv_freq, d)
+    _need_norms(q_norm, None, d)
+    check(_lib.load().molot_hip_prefill_q(_ptr(q), nq, d, int(M), int(pos0), _ptr(q_norm),
+                                          float(eps), _ptr(inv_freq), _stream()), "prefill_q")
+    return q
+
+
+def attn_prefill_paged(Qm, K, V, Om, block_row, max_blocks, page, nq, nkv, M, N, d, scale, pos0,
+                       window=0):
+    """attn_prefill_gqa over one sequence's pages (no reference counterpart)."""
+    kvd = kv_dtype_of(K)
+    _need(Qm, "Qm", torch.float32, M * nq * d)
+    _need(Om, "Om", torch.float32, M * nq * d)
+    _need(block_row, "block_row", torch.int32, max_blocks)
+    bu = _block_units(kvd, nkv, d, page)
+    nblocks = K.numel() // bu
+    _need(K, "K", _KV_DTYPES, nblocks * bu)
+    _need(V, "V", K.dtype, nblocks * bu)
+    if N < 0 or N > max_blocks * page:
+        raise ValueError("N outside [0, max_blocks*page]")
+    used = (N + page - 1) // page
+    row = block_row.cpu()
+    if used and (int(row[:used].min()) < 0 or int(row[:used].max()) >= nblocks):
+        raise ValueError("block_row names a block outside the pool")
+    check(_lib.load().molot_hip_attn_prefill_paged(
+        _ptr(Qm), _ptr(K), _ptr(V), _ptr(Om), _ptr(block_row), int(max_blocks), int(page), nq,
+        nkv, int(M), int(N), d, float(scale), int(pos0), int(window), kvd, _stream()),
+        "attn_prefill_paged")
+    return Om
+
+
 def rope_append_paged(q, k_new, v_new, K, V, block_table, seq_lens, pos, B, max_blocks, nq, nkv,
                       d, page, inv_freq):
     """RoPE + append of one token per sequence into its page slot seq_lens[b]-1."""
@@ -352,7 +435,7 @@ def rope_append_paged(q, k_new, v_new, K, V, block_table, seq_lens, pos, B, max_
     _need(q, "q", torch.float32, B * nq * d)
     _need(k_new, "k_new", torch.float32, B * nkv * d)
     _need(v_new, "v_new", torch.float32, B * nkv * d)
-    _need(inv_freq, "inv_freq", torch.float32, d // 2)
+    _need_table(inv_freq, d)
     _check_paged(block_table, seq_lens, pos, B, max_blocks, nkv, d, page, K, V)
     if B and int(seq_lens.min()) < 1:
         raise ValueError("rope_append_paged: every sequence needs seq_lens >= 1")
@@ -381,6 +464,25 @@ def last_plan():
 
 def set_split_chunk(tokens: int) -> None:
     _lib.load().molot_hip_set_split_chunk(int(tokens))
+
+
+def set_merge(in_launch: bool) -> None:
+    """Split-K chunks merged inside the attention launch (True) or by the
+    combine kernel (False, the default); see molot_hip_set_merge."""
+    _lib.load().molot_hip_set_merge(1 if in_launch else 0)
+
+
+def profile(fn, launches: int = 64):
+    """Run fn() with launch profiling on; returns (attention launches,
+    launches that needed the combine kernel) among them."""
+    L = _lib.load()
+    _lib.check(L.molot_hip_profile_begin(launches), "profile_begin")
+    fn()
+    am, cm = ctypes.c_float(), ctypes.c_float()
+    na, nc = ctypes.c_int(), ctypes.c_int()
+    _lib.check(L.molot_hip_profile_end(ctypes.byref(am), ctypes.byref(cm), ctypes.byref(na),
+                                       ctypes.byref(nc)), "profile_end")
+    return na.value, nc.value
 
 
 class KVCache:

@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -246,10 +247,15 @@ __global__ void rope_append_kernel(RopeArgs a) {
     slot += b;
     pos += b;
   }
-  const float ang = (float)pos * a.inv_freq[ic];
-  double sd, cd;
-  sincos((double)ang, &sd, &cd);
-  const float c = (float)cd, s = (float)sd;
+  const bool rot = a.inv_freq != nullptr;  // a NoPE layer (inv_freq NULL) is not rotated
+  float c = 1.f, s = 0.f;
+  if (rot) {
+    const float ang = (float)pos * a.inv_freq[ic];
+    double sd, cd;
+    sincos((double)ang, &sd, &cd);
+    c = (float)cd;
+    s = (float)sd;
+  }
   auto rms_inv = [&](float ss, int n) { return 1.0f / sqrtf(ss / (float)n + a.eps); };
   if (hh < a.nq) {
     if (!a.q) return;
@@ -261,8 +267,8 @@ __global__ void rope_append_kernel(RopeArgs a) {
       x1 = x1 * inv * a.q_norm[ic + half];
     }
     if (act) {
-      x[i] = x0 * c - x1 * s;
-      x[i + half] = x0 * s + x1 * c;
+      x[i] = rot ? x0 * c - x1 * s : x0;
+      x[i + half] = rot ? x0 * s + x1 * c : x1;
     }
     return;
   }
@@ -285,8 +291,8 @@ __global__ void rope_append_kernel(RopeArgs a) {
     v0 *= inv;
     v1 *= inv;
   }
-  const float r0 = k0 * c - k1 * s;  // 0 on the threads past the pairs
-  const float r1 = k0 * s + k1 * c;
+  const float r0 = rot ? k0 * c - k1 * s : k0;  // 0 on the threads past the pairs
+  const float r1 = rot ? k0 * s + k1 * c : k1;
   float ks = 0.f, vs = 0.f;
   if (a.kv_dtype == MOLOT_KV_Q8) {  // uniform: every thread takes the maxima
     ks = q8_scale(block_max(fmaxf(fabsf(r0), fabsf(r1)), sh));
@@ -382,6 +388,15 @@ struct AttnArgs {
   int nq, nkv, n, t0, pos, chunk, nchunks, max_blocks, page_shift, window;
   int dynamic;           // 1: waves claim blocks from a workgroup counter; 0: fixed order
   int chunk_fast;        // 1-D grid, the KV heads of a chunk on one XCD (B = 1; see launch_pair)
+  // In-launch merge (see arrive_and_merge): every chunk of a slot runs on one
+  // XCD, and the workgroup that completes a slot merges its chunk partials.
+  int fold;              // ROPE: 1 = the step appends the new token (folded into the last
+                         // chunk, slot n-1); 0 = q prologue only (a layer reading another
+                         // layer's KV: all n slots come from the cache)
+  int* ctr;              // [slots] arrival counters, zero between launches (NULL: combine kernel)
+  int xmap;              // 1-D grid of 8 * nchunks: slot id % 8 on XCD id % 8 (fewer than 8 slots)
+  int slots;             // slots of the launch (xmap)
+  int mrg;               // floats of LDS for the merge's chunk statistics (0: no in-launch merge)
   float scale;
   // the layer's norms of the fresh vectors (ROPE only; NULL / 0: none)
   const float* q_norm;   // [D] weights of the per-head q RMS norm
@@ -473,8 +488,9 @@ struct Tune {
 
 // Dynamic LDS layout shared by host (size) and device (offsets), in floats.
 struct Lds {
-  int qs, cs, sn, knew, vnew, nw, pw, wm, wl, red, blk, misc, total;
-  __host__ __device__ Lds(int D, int GH, int NW, int RB, int chunk, int page_shift, bool paged) {
+  int qs, cs, sn, knew, vnew, nw, pw, wm, wl, red, blk, misc, mrg, total;
+  __host__ __device__ Lds(int D, int GH, int NW, int RB, int chunk, int page_shift, bool paged,
+                          int merge) {
     int o = 0;
     qs = o; o += GH * D;
     cs = o; o += D / 2;
@@ -487,7 +503,8 @@ struct Lds {
     wl = o; o += NW * GH;
     red = o; o += NW * GH * D;       // per-wave o
     blk = o; o += paged ? ((chunk >> page_shift) + 2) : 0;
-    misc = o; o += 8;                // block claim counter
+    misc = o; o += 8;                // block claim counter, merge flag
+    mrg = o; o += merge;             // in-launch merge: chunk statistics
     total = o;
   }
 };
@@ -612,11 +629,172 @@ __device__ __forceinline__ void v_norm_share(const AttnArgs& a, int b, int tid, 
 // of wave w (waves without rows hold max -inf).  A single-chunk problem
 // writes O = o / l (and, with ROPE, the rotated q from qs) directly;
 // otherwise (o, max, sum) goes to the workspace for combine_kernel.
-template <int D, int GH, int NW, int NT, bool ROPE>
+// ---------------------------------------------------------------------------
+// In-launch merge of the split-K chunk partials.
+//
+// Workgroup i runs on XCD i % 8 (the dispatch order of MI355X in its
+// single-partition mode, checked once per device by xcd_map_ok() before the
+// library relies on it), and the launch places every chunk of a slot on the
+// same XCD.  The slot's partials therefore meet in one L2, the coherence
+// point of that XCD's CUs, and the hand-off needs no cache writeback:
+//   - each workgroup stores its partial (plain stores, which write through
+//     the CU's L1 into the L2), waits until the L2 has acknowledged them
+//     (s_waitcnt vmcnt(0) in every thread, then a barrier) and adds one
+//     arrival to the slot's counter (a global atomic, performed past the L1);
+//   - the workgroup whose add returns nch - 1 arrived last: every other
+//     chunk's stores were acknowledged before its arrival.  It resets the
+//     counter to 0 for the next launch and reads the partials back with
+//     loads that miss the L1 (cache policy sc0), so they come from the L2;
+//   - it merges them with log-sum-exp weights as combine_kernel does and
+//     writes O and, with ROPE, the rotated q (every workgroup of the slot
+//     has read q by the time it arrives).
+// No workgroup waits for another: nothing spins, and a launch's arrivals
+// are exactly its slots' chunk counts, so the counters are back at zero when
+// it ends (they are zeroed when the workspace is allocated).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_rsrc(const float* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
+// Loads at a byte offset of a resource, missing the L1 (cache policy sc0).
+__device__ __forceinline__ float ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 1));
+}
+__device__ __forceinline__ f32x4 ld_l2x4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 1));
+}
+
+constexpr int kMergeMaxStats = 2048;  // chunks x heads of a slot merged in the launch
+constexpr int kMergeInFlight = 16;    // 16-byte o loads in flight per thread
+
+// RED: floats of LDS at mred (the phases' partial sums).
+template <int D, int GH, int NW, int NT, bool ROPE, int RED>
+__device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot, int nch,
+                                                 int64_t qrow0, const float* qs, float* mst,
+                                                 float* mred, int* flag, int tid, int lane) {
+  constexpr int P = GH * D;
+  wait_vmcnt<0>();  // this thread's partial stores are in the L2
+  lds_barrier();
+  if (tid == 0) {
+    const int old = atomicAdd(a.ctr + slot, 1);
+    const int last = old == nch - 1;
+    if (last) atomicExch(a.ctr + slot, 0);  // ready for the next launch
+    flag[0] = last;
+  }
+  lds_barrier();
+  if (!flag[0]) return;  // uniform over the workgroup
+
+  // Work split over float4 quads of the partial (QV per chunk): with QV <= NT,
+  // thread t folds quad t % QV over the chunks t / QV + PH*j (PH phases,
+  // summed through LDS at the end); otherwise PH = 1 and thread t takes
+  // quads t, t + NT, ...  CB chunks per quad are loaded per round.
+  constexpr int QV = P / 4;
+  constexpr int PH0 = NT >= QV ? NT / QV : 1;
+  constexpr int PH = PH0 * P <= RED ? PH0 : (RED / P > 0 ? RED / P : 1);
+  constexpr int NQ = NT >= QV ? 1 : (QV + NT - 1) / NT;
+  constexpr int CB = kMergeInFlight / NQ > 0 ? kMergeInFlight / NQ : 1;
+  constexpr int SPT = (kMergeMaxStats + NT - 1) / NT;
+  static_assert(P % 4 == 0, "float4 quads");
+  const int ph = NT >= QV ? tid / QV : 0;
+  const bool act = ph < PH;
+  const __amdgpu_buffer_rsrc_t ro = l2_rsrc(a.part_o + slot * a.nchunks * P);
+  const __amdgpu_buffer_rsrc_t rm = l2_rsrc(a.part_ml + slot * a.nchunks * (GH * 2));
+  const int ns = nch * GH;
+  // the chunk statistics first, then the first round of o: the statistics
+  // loads retire first, so they are used while the o loads are in flight
+  float sm[SPT], sl[SPT];
+#pragma unroll
+  for (int u = 0; u < SPT; ++u) {
+    const int i = min(tid + u * NT, ns - 1);
+    sm[u] = ld_l2(rm, 8 * i);
+    sl[u] = ld_l2(rm, 8 * i + 4);
+  }
+  int qd[NQ];
+  f32x4 ov[NQ][CB];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    qd[i] = NT >= QV ? tid % QV : min(tid + i * NT, QV - 1);
+#pragma unroll
+    for (int u = 0; u < CB; ++u) {
+      const int cc = min(ph + PH * u, nch - 1);
+      ov[i][u] = ld_l2x4(ro, 16 * (cc * QV + qd[i]));
+    }
+  }
+  float* wts = mst;              // [nch][GH] chunk max, then its weight e^(m_c - M)
+  float* lsv = mst + ns;         // [nch][GH] chunk sum
+  float* Lg = mst + 2 * ns;      // [GH] L = sum_c e^(m_c - M) l_c
+#pragma unroll
+  for (int u = 0; u < SPT; ++u) {
+    const int i = tid + u * NT;
+    if (i < ns) {
+      wts[i] = sm[u];
+      lsv[i] = sl[u];
+    }
+  }
+  lds_barrier();
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int g = w; g < GH; g += NW) {  // wave w: the weights of head g
+    float mloc = -INFINITY;
+    for (int cc = lane; cc < nch; cc += 64) mloc = fmaxf(mloc, wts[cc * GH + g]);
+    const float M = wave_reduce<true>(mloc);
+    float lloc = 0.f;
+    for (int cc = lane; cc < nch; cc += 64) {
+      const float wc = softmax_exp(wts[cc * GH + g] - M);
+      wts[cc * GH + g] = wc;
+      lloc = fmaf(wc, lsv[cc * GH + g], lloc);
+    }
+    const float Ls = wave_reduce<false>(lloc);
+    if (lane == 0) Lg[g] = Ls;
+  }
+  lds_barrier();
+  f32x4 acc[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int c0 = 0;; c0 += PH * CB) {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int g = 4 * qd[i] / D;
+#pragma unroll
+      for (int u = 0; u < CB; ++u) {
+        const int cc = c0 + ph + PH * u;
+        if (act && cc < nch) acc[i] += wts[cc * GH + g] * ov[i][u];
+      }
+    }
+    if (c0 + PH * CB >= nch) break;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i)
+#pragma unroll
+      for (int u = 0; u < CB; ++u) {
+        const int cc = min(c0 + PH * CB + ph + PH * u, nch - 1);
+        ov[i][u] = ld_l2x4(ro, 16 * (cc * QV + qd[i]));
+      }
+  }
+  if constexpr (PH > 1) {
+    if (act) reinterpret_cast<f32x4*>(mred)[ph * QV + qd[0]] = acc[0];
+    lds_barrier();
+    if (tid < QV) {
+      f32x4 o = reinterpret_cast<const f32x4*>(mred)[tid];
+#pragma unroll
+      for (int q2 = 1; q2 < PH; ++q2) o += reinterpret_cast<const f32x4*>(mred)[q2 * QV + tid];
+      reinterpret_cast<f32x4*>(a.o + qrow0 * D)[tid] = o / Lg[4 * tid / D];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+      const int q4 = NT >= QV ? tid : tid + i * NT;
+      if (act && q4 < QV) reinterpret_cast<f32x4*>(a.o + qrow0 * D)[q4] = acc[i] / Lg[4 * q4 / D];
+    }
+  }
+  if constexpr (ROPE) {
+    if (a.q_out)
+      for (int i = tid; i < P; i += NT) a.q_out[qrow0 * D + i] = qs[i];
+  }
+}
+
+template <int D, int GH, int NW, int NT, bool ROPE, int RED>
 __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm, const float* wl,
                                              const float* red, int RS, const float* qs, int tid,
                                              int lane, bool split, int64_t slot, int c,
-                                             int64_t qrow0) {
+                                             int64_t qrow0, int nch, float* mst, float* mred,
+                                             int* flag) {
   constexpr int P = GH * D;
   // Every thread derives the chunk partial of its own output pairs from the
   // wave partials (wave weights e^(m_w - M); waves without rows weigh
@@ -678,6 +856,11 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
       pml_s[2 * g_[i] + 1] = pl[i];
     }
   }
+  if (a.ctr) {  // in-launch merge: the workgroup completing the slot merges it
+    arrive_and_merge<D, GH, NW, NT, ROPE, RED>(a, slot, nch, qrow0, qs, mst, mred, flag, tid,
+                                               lane);
+    return;
+  }
   if constexpr (ROPE) {  // the rotated q leaves through the combine kernel
     if (c == 0 && a.q_out)
       for (int i = tid; i < P; i += NT) a.qrot[slot * P + i] = qs[i];
@@ -692,19 +875,29 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   constexpr int NW = C::NW, NT = C::NT, P = C::P;
 
   extern __shared__ float smem[];
-  const Lds L(D, GH, NW, RB, a.chunk, a.page_shift, PAGED);
+  const Lds L(D, GH, NW, RB, a.chunk, a.page_shift, PAGED, a.mrg);
   float* qs = smem + L.qs;
   float* knew = smem + L.knew;
   float* vnew = smem + L.vnew;
   int* misc = reinterpret_cast<int*>(smem + L.misc);
 
-  const int z = blockIdx.z;  // chunk slot; chunk c = nch - 1 - z (below)
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
-  const int sub = blockIdx.x % nsub;
-  const int h = blockIdx.x / nsub;
+  // chunk slot z (chunk c = nch - 1 - z, below), (KV head, subgroup) index
+  // hs and sequence b of this workgroup; X (KV head, subgroup) pairs per
+  // sequence
+  const int X = a.nkv * nsub;
+  int z = blockIdx.z, hs = blockIdx.x, b = blockIdx.y;
+  if (a.xmap) {  // slot id % 8 runs on XCD id % 8 (launch_pair); padding ids exit
+    const int s8 = (int)(blockIdx.x & 7);
+    if (s8 >= a.slots) return;
+    z = (int)(blockIdx.x >> 3);
+    hs = s8 % X;
+    b = s8 / X;
+  }
+  const int sub = hs % nsub;
+  const int h = hs / nsub;
   const int hq0 = h * G + sub * GH;
-  const int b = blockIdx.y;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -716,13 +909,14 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
     if (t0 > n) t0 = n;
   }
-  // Chunks tile the cache rows [t0, cend); with ROPE the new token (slot
+  // Chunks tile the cache rows [t0, cend); a fused step's new token (slot
   // n-1) is not read from the cache but folded into the last chunk.
-  const int cend = ROPE ? n - 1 : n;
+  const bool fold = ROPE && a.fold;  // this launch appends and folds in the new token
+  const int cend = fold ? n - 1 : n;
   int nch = a.nchunks;
   if constexpr (PAGED) {
     const int span = cend - t0;
-    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (ROPE ? 1 : 0);
+    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (fold ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
   if (z >= nch) {  // whole workgroup: chunk past this sequence's end (never arrives)
@@ -735,9 +929,9 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const int c = nch - 1 - z;
   const int tb = t0 + c * a.chunk;
   const int cntg = max(0, min(a.chunk, cend - tb));  // rows read from the cache
-  const bool is_new = ROPE && c == nch - 1;          // this chunk folds in the new token
+  const bool is_new = fold && c == nch - 1;          // this chunk folds in the new token
   const bool split = nch > 1;
-  const int64_t slot = (int64_t)b * gridDim.x + blockIdx.x;
+  const int64_t slot = (int64_t)b * X + hs;
 
   const T* __restrict__ Kb = reinterpret_cast<const T*>(a.k);
   const T* __restrict__ Vb = reinterpret_cast<const T*>(a.v);
@@ -826,9 +1020,14 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   float invf = 0.f, knv = 0.f, vnv = 0.f, kwv = 0.f;
   f32x4 qwt[QPT];  // q norm weights of this thread's q elements
   if constexpr (ROPE) {
-    invf = a.inv_freq[min(tid, D / 2 - 1)];
-    knv = a.k_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
-    vnv = a.v_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    // every path issues these loads: a layer without RoPE (inv_freq NULL)
+    // or without an append reads q in their place (nq >= nkv rows), unused
+    const float* ivp = a.inv_freq ? a.inv_freq : a.q;
+    const float* knp = fold ? a.k_new : a.q;
+    const float* vnp = fold ? a.v_new : a.q;
+    invf = ivp[min(tid, D / 2 - 1)];
+    knv = knp[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    vnv = vnp[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
     if (a.q_norm) {
 #pragma unroll
       for (int u = 0; u < QPT; ++u)
@@ -857,7 +1056,8 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   if constexpr (ROPE) {
     float* csn = smem + L.cs;
     float* sn = smem + L.sn;
-    if (tid < D / 2) {
+    const bool rot = a.inv_freq != nullptr;  // uniform: no RoPE on a NoPE layer
+    if (rot && tid < D / 2) {
       const float ang = (float)pos * invf;
       double sd, cd;
       sincos((double)ang, &sd, &cd);
@@ -872,7 +1072,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     if (tid < D) smem[L.nw + tid] = kwv;
     if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
     lds_barrier();
-    for (int i = tid; i < GH * (D / 2); i += NT) {
+    for (int i = tid; rot && i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
       const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
       qs[g * D + j] = x0 * csn[j] - x1 * sn[j];
@@ -887,8 +1087,8 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
         float k0 = knew[j], k1 = knew[j + D / 2];
         float v0 = vnew[j], v1 = vnew[j + D / 2];
         nn.apply(a, smem + L.nw, j, D / 2, k0, k1, v0, v1);
-        float r0 = k0 * csn[j] - k1 * sn[j];
-        float r1 = k0 * sn[j] + k1 * csn[j];
+        float r0 = rot ? k0 * csn[j] - k1 * sn[j] : k0;
+        float r1 = rot ? k0 * sn[j] + k1 * csn[j] : k1;
         if constexpr (sizeof(T) == 2) {
           r0 = __uint_as_float((uint32_t)f32_to_bf16(r0) << 16);
           r1 = __uint_as_float((uint32_t)f32_to_bf16(r1) << 16);
@@ -1109,7 +1309,9 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       for (int e = 0; e < VW; ++e) red[(w * GH + g) * D + cs * VW + e] = acc[g][e];
   }
   lds_barrier();
-  finish_chunk<D, GH, NW, NT, ROPE>(a, wm, wl, red, P, qs, tid, lane, split, slot, c, qrow0);
+  finish_chunk<D, GH, NW, NT, ROPE, NW * P>(a, wm, wl, red, P, qs, tid, lane, split, slot, c,
+                                             qrow0, nch,
+                                    smem + L.mrg, red, misc + 1);
 
   // ---- 6. the append (subgroup 0; no workgroup reads that slot in this
   // launch).  Last, because nothing may wait for these stores: vmcnt counts
@@ -1188,8 +1390,9 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // bf16 (16*D floats), which after the stream hold the wave's partial o;
 // sc (Q8): per wave, the K then the V row scales of its current tile.
 struct LdsM {
-  int qs, cs, sn, knew, vnew, nw, wm, wl, sc, vt, blk, misc, total;
-  __host__ __device__ LdsM(int D, int GH, int chunk, int page_shift, bool paged, bool q8) {
+  int qs, cs, sn, knew, vnew, nw, wm, wl, sc, vt, blk, misc, mrg, total;
+  __host__ __device__ LdsM(int D, int GH, int chunk, int page_shift, bool paged, bool q8,
+                           int merge) {
     int o = 0;
     qs = o; o += GH * D;
     cs = o; o += D / 2;
@@ -1204,7 +1407,8 @@ struct LdsM {
     o = (o + 63) & ~63;  // 256-byte aligned: the swizzle's bank pattern
     vt = o; o += kMfmaWaves * kTile * D / 2;
     blk = o; o += paged ? ((chunk >> page_shift) + 2) : 0;
-    misc = o; o += 8;
+    misc = o; o += 8;  // tile claim counter, merge flag
+    mrg = o; o += merge;  // in-launch merge: chunk statistics
     total = o;
   }
 };
@@ -1282,7 +1486,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   using E = typename std::conditional<Q8, int8_t, bf16_t>::type;
 
   extern __shared__ float smem[];
-  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8);
+  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg);
   float* qs = smem + L.qs;
   float* knew = smem + L.knew;
   float* vnew = smem + L.vnew;
@@ -1299,6 +1503,12 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     z = (k / HS) * 8 + (int)(blockIdx.x & 7);  // padded ids (z >= nchunks) exit below
     hs = k % HS;
     b = 0;
+  } else if (a.xmap) {  // slot id % 8 runs on XCD id % 8 (launch_pair); padding ids exit
+    const int s8 = (int)(blockIdx.x & 7);
+    if (s8 >= a.slots) return;
+    z = (int)(blockIdx.x >> 3);
+    hs = s8 % (a.nkv * nsub);
+    b = s8 / (a.nkv * nsub);
   } else {
     z = blockIdx.z;
     hs = blockIdx.x;
@@ -1319,11 +1529,12 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
     if (t0 > n) t0 = n;
   }
-  const int cend = ROPE ? n - 1 : n;
+  const bool fold = ROPE && a.fold;  // this launch appends and folds in the new token
+  const int cend = fold ? n - 1 : n;
   int nch = a.nchunks;
   if constexpr (PAGED) {
     const int span = cend - t0;
-    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (ROPE ? 1 : 0);
+    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (fold ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
   if (z >= nch) {
@@ -1334,7 +1545,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   const int c = nch - 1 - z;  // the new token's chunk first, as in attn_kernel
   const int tb = t0 + c * a.chunk;
   const int cntg = max(0, min(a.chunk, cend - tb));
-  const bool is_new = ROPE && c == nch - 1;
+  const bool is_new = fold && c == nch - 1;
   const bool split = nch > 1;
   const int64_t slot = (int64_t)b * a.nkv * nsub + hs;
 
@@ -1440,9 +1651,14 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   float invf = 0.f, knv = 0.f, vnv = 0.f, kwv = 0.f;
   f32x4 qwt[QPT];  // q norm weights of this thread's q elements
   if constexpr (ROPE) {
-    invf = a.inv_freq[min(tid, D / 2 - 1)];
-    knv = a.k_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
-    vnv = a.v_new[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    // every path issues these loads: a layer without RoPE (inv_freq NULL)
+    // or without an append reads q in their place (nq >= nkv rows), unused
+    const float* ivp = a.inv_freq ? a.inv_freq : a.q;
+    const float* knp = fold ? a.k_new : a.q;
+    const float* vnp = fold ? a.v_new : a.q;
+    invf = ivp[min(tid, D / 2 - 1)];
+    knv = knp[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    vnv = vnp[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
     if (a.q_norm) {
 #pragma unroll
       for (int u = 0; u < QPT; ++u)
@@ -1467,7 +1683,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   if constexpr (ROPE) {
     float* csn = smem + L.cs;
     float* sn = smem + L.sn;
-    if (tid < D / 2) {
+    const bool rot = a.inv_freq != nullptr;  // uniform: no RoPE on a NoPE layer
+    if (rot && tid < D / 2) {
       const float ang = (float)pos * invf;
       double sd, cd;
       sincos((double)ang, &sd, &cd);
@@ -1482,7 +1699,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     if (tid < D) smem[L.nw + tid] = kwv;
     if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
     lds_barrier();
-    for (int i = tid; i < GH * (D / 2); i += NT) {
+    for (int i = tid; rot && i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
       const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
       qs[g * D + j] = x0 * csn[j] - x1 * sn[j];
@@ -1494,8 +1711,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
         float k0 = knew[j], k1 = knew[j + D / 2];
         float v0 = vnew[j], v1 = vnew[j + D / 2];
         nn.apply(a, smem + L.nw, j, D / 2, k0, k1, v0, v1);
-        const float r0 = k0 * csn[j] - k1 * sn[j];
-        const float r1 = k0 * sn[j] + k1 * csn[j];
+        const float r0 = rot ? k0 * csn[j] - k1 * sn[j] : k0;
+        const float r1 = rot ? k0 * sn[j] + k1 * csn[j] : k1;
         if constexpr (Q8) {  // quantized after the stream (whole rows)
           knew[j] = r0;
           knew[j + D / 2] = r1;
@@ -1749,7 +1966,9 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       *reinterpret_cast<f32x4*>(red + w * RS + m16 * D + 16 * dt + 4 * g4) = o[dt];
   }
   lds_barrier();
-  finish_chunk<D, GH, NW, NT, ROPE>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c, qrow0);
+  finish_chunk<D, GH, NW, NT, ROPE, NW * RS>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c,
+                                              qrow0, nch,
+                                    smem + L.mrg, red, misc + 1);
 
   // ---- the append, last ----
   const bool store_new = is_new && sub == 0 && (Q8 ? w == 0 : tid < D);
@@ -1828,7 +2047,7 @@ constexpr int kPfThreads = kPfWaves * 64;
 //     it in (key 16u + 4(l/16) + r of lane l, slot 4u + r).
 // D = 256 stages 100 KB (fp32 pieces) and runs one workgroup per CU.
 template <int D, typename T, bool PAGED>
-__global__ __launch_bounds__(kPfThreads, D == 256 ? 1 : 2) void prefill_mfma16_kernel(PfArgs a) {
+__global__ __launch_bounds__(kPfThreads, (D == 256 && sizeof(T) == 4) ? 1 : 2) void prefill_mfma16_kernel(PfArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "bf16-piece prefill: D = 64, 128, 256");
   constexpr int NT = kPfThreads, QB = 16 * kPfWaves;
   constexpr int KT = 32, KH = 2;
@@ -2127,6 +2346,7 @@ struct CombArgs {
   const int32_t* seq_lens;
   const int32_t* pos_arr;
   int nq, nkv, gh, nsub, d, nchunks, chunk, window, rope, paged;
+  int fold;  // the attention launch folded in a new token (its chunks tile n - 1 rows)
 };
 
 constexpr int kCombThreads = 256;
@@ -2176,8 +2396,8 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
     const int pos = a.pos_arr ? a.pos_arr[b] : n - 1;
     int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
     if (t0 > n) t0 = n;
-    const int span = (a.rope ? n - 1 : n) - t0;
-    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.rope ? 1 : 0);
+    const int span = (a.fold ? n - 1 : n) - t0;
+    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.fold ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
   if (nch <= 1) return;  // uniform over the workgroup
@@ -2261,8 +2481,8 @@ __global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs
     const int pos = a.pos_arr ? a.pos_arr[b] : n - 1;
     int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
     if (t0 > n) t0 = n;
-    const int span = (a.rope ? n - 1 : n) - t0;
-    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.rope ? 1 : 0);
+    const int span = (a.fold ? n - 1 : n) - t0;
+    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.fold ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
   if (nch <= 1) return;  // uniform over the workgroup
@@ -2297,11 +2517,15 @@ __global__ void zero_kernel(float* p, int64_t n) {
 constexpr int kMaxChunk = 2048;
 constexpr int kMaxSlots = 1 << 16;  // combine grid y: (sequence, head group) pairs per launch
 
-int g_split_chunk = 0;  // tokens per chunk, 0 = automatic
-int g_wgs_per_cu = 0;   // workgroups per CU, 0 = one
-int g_variant = 0;      // mapping variant of the 32q/8kv/d128 fp32 kernels (tuning sweeps)
-int g_dynamic = 1;      // block order: 1 = claimed by waves as they free up, 0 = fixed
-int g_bf16_mfma = 1;    // bf16 KV (D = 64, 128) on the matrix-core kernel
+// Process-wide settings (molot_hip_set_*): atomics, so a setter racing with
+// launches on other host threads is well defined; a launch reads each once.
+std::atomic<int> g_split_chunk{0};  // tokens per chunk, 0 = automatic
+std::atomic<int> g_wgs_per_cu{0};   // workgroups per CU, 0 = the plan's own
+std::atomic<int> g_dynamic{1};      // block order: 1 = claimed by waves as they free up, 0 = fixed
+std::atomic<int> g_bf16_mfma{1};    // bf16 KV (D = 64, 128) on the matrix-core kernel
+std::atomic<int> g_merge{0};        // 1: split-K partials merged in the launch where possible
+
+int knob(const std::atomic<int>& k) { return k.load(std::memory_order_relaxed); }
 
 // Launch profiling (off by default): while on, every attention launch
 // outside graph capture goes through hipExtLaunchKernelGGL with a start and
@@ -2343,40 +2567,101 @@ struct WsKey {
   }
 };
 // Per-(device, stream) workspace of the split-K partials, grown on demand.
-// The attention kernel fills it and the combine kernel, next on the same
-// stream, reads it, so it needs no clearing and holds nothing between
-// steps.  An outgrown buffer is retired, never freed: a graph captured
-// earlier on the stream still points at it (workspaces are small).
+// Layout: [int ctr[kMaxSlots] | partials].  The arrival counters of the
+// in-launch merge are zeroed once, when the buffer is allocated (a fill
+// kernel on the stream, ordered before any launch that uses them), and
+// every launch leaves them at zero.  The partials are filled and read
+// within a step (by the attention kernel, or by it and the combine kernel
+// next on the same stream), so they need no clearing and hold nothing
+// between steps.  An outgrown buffer is retired, never freed: a graph
+// captured earlier on the stream still points at it (workspaces are small).
+constexpr size_t kCtrBytes = sizeof(int) * (size_t)kMaxSlots;
 struct WsBuf {
   void* ptr = nullptr;
-  size_t bytes = 0;
+  size_t bytes = 0;  // partials
 };
 std::mutex g_ws_mu;
 std::map<WsKey, WsBuf> g_ws;
 std::vector<void*> g_retired;
 
-int workspace(void* stream, size_t bytes, void** out) {
+__global__ void zero_kernel(float* p, int64_t n);
+bool xcd_map_ok(int dev);
+
+int workspace(void* stream, size_t bytes, int** ctr, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
   std::lock_guard<std::mutex> lk(g_ws_mu);
   WsBuf& w = g_ws[WsKey{dev, stream}];
-  if (w.bytes < bytes) {
+  if (!w.ptr || w.bytes < bytes) {
     // a graph being captured cannot allocate: the caller sizes the
     // workspace with one launch of the shape before capturing
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     e = hipStreamIsCapturing((hipStream_t)stream, &cap);
     if (e != hipSuccess) return (int)e;
     if (cap != hipStreamCaptureStatusNone) return MOLOT_ENOWS;
+    (void)xcd_map_ok(dev);  // the one-time dispatch check, outside any capture
     if (w.ptr) g_retired.push_back(w.ptr);
     w = WsBuf{};
     const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-    e = hipMalloc(&w.ptr, want);
+    void* p = nullptr;
+    e = hipMalloc(&p, kCtrBytes + want);
     if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)(kMaxSlots / 256)), dim3(256), 0,
+                       (hipStream_t)stream, reinterpret_cast<float*>(p), (int64_t)kMaxSlots);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      return (int)e;
+    }
+    w.ptr = p;
     w.bytes = want;
   }
-  *out = w.ptr;
+  *ctr = reinterpret_cast<int*>(w.ptr);
+  *out = reinterpret_cast<char*>(w.ptr) + kCtrBytes;
   return 0;
+}
+
+// Dispatch check for the in-launch merge, once per device: a probe launch
+// records the XCD (hardware register XCC_ID) of every workgroup of a 4096-
+// workgroup grid, and the merge is used only if workgroup i always ran on
+// the same XCD as workgroup i % 8 (MI355X's round-robin dispatch in its
+// single-partition mode; with one XCD per device the check holds
+// trivially).  Read-only after the first call for a device.
+__device__ int g_xcc_probe[4096];
+__global__ void xcc_probe_kernel() {
+  if (threadIdx.x == 0)
+    g_xcc_probe[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) & 15);
+}
+std::mutex g_xcd_mu;
+std::map<int, bool> g_xcd_ok;
+
+bool xcd_map_ok(int dev) {
+  std::lock_guard<std::mutex> lk(g_xcd_mu);
+  auto it = g_xcd_ok.find(dev);
+  if (it != g_xcd_ok.end()) return it->second;
+  bool ok = false;
+  std::vector<int> xcc(4096, -1);
+  hipStream_t st = nullptr;
+  if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) == hipSuccess) {
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(4096), dim3(64), 0, st);
+    if (hipGetLastError() == hipSuccess &&
+        hipMemcpyFromSymbolAsync(xcc.data(), HIP_SYMBOL(g_xcc_probe), sizeof(int) * 4096, 0,
+                                 hipMemcpyDeviceToHost, st) == hipSuccess &&
+        hipStreamSynchronize(st) == hipSuccess) {
+      ok = true;
+      for (int i = 0; i < 4096; ++i) ok = ok && xcc[i] >= 0 && xcc[i] == xcc[i % 8];
+    }
+    (void)hipStreamDestroy(st);
+  }
+  g_xcd_ok[dev] = ok;
+  return ok;
+}
+
+bool xcd_ok_cached(int dev) {
+  std::lock_guard<std::mutex> lk(g_xcd_mu);
+  auto it = g_xcd_ok.find(dev);
+  return it != g_xcd_ok.end() && it->second;
 }
 
 int g_num_cus = 0;
@@ -2403,10 +2688,10 @@ int pick_gh(int G) {
 // per CU (one by default: a workgroup fills its CU), rounded up to a
 // multiple of `align` rows (a forced size too: the matrix-core kernel deals
 // 32-row tiles to the chunks, and every chunk must get one).
-int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
-  int chunk = g_split_chunk;
+int plan_chunk(int span, int rows_of_wgs, int align, int wpc, int split, int wpcu) {
+  int chunk = split;
   if (chunk <= 0) {
-    const long target = (long)(g_wgs_per_cu > 0 ? g_wgs_per_cu : wpc) * num_cus();
+    const long target = (long)(wpcu > 0 ? wpcu : wpc) * num_cus();
     long nch = (target + rows_of_wgs - 1) / rows_of_wgs;
     if (nch < 1) nch = 1;
     chunk = (int)((span + nch - 1) / nch);
@@ -2423,24 +2708,33 @@ int plan_chunk(int span, int rows_of_wgs, int align, int wpc) {
 // kernel deals `align`-row tiles to the chunks round robin (the matrix-core
 // kernel on a contiguous cache), so only the chunk count matters: the
 // workgroup target's, at most one chunk per tile (a.chunk is then nominal).
+//
+// A split context is merged in the launch itself (arrive_and_merge) when the
+// device dispatches workgroup i to XCD i % 8 and every chunk of a slot can
+// run on one XCD: with the grid's slot index fastest that holds when the
+// slot count is a multiple of 8; fewer than 8 slots take a 1-D grid that
+// puts slot s on XCD s (xmap).  Other slot counts, token-major Q8 launches
+// (whose grid groups the heads of a chunk on one XCD instead) and slots of
+// more than kMergeMaxStats chunk statistics use combine_kernel.
 int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int align, int wpc,
                 void* stream, bool cyclic = false) {
   const int rows = a.nkv * nsubs * B;
+  const int split = knob(g_split_chunk), wpcu = knob(g_wgs_per_cu);
   if (cyclic) {
     const long tiles = span > 0 ? ((long)span + align - 1) / align : 1;
     long nch;
-    if (g_split_chunk > 0) {
-      const long ch = ((long)g_split_chunk + align - 1) / align * align;
+    if (split > 0) {
+      const long ch = ((long)split + align - 1) / align * align;
       nch = span > 0 ? (span + ch - 1) / ch : 1;
     } else {
-      const long target = (long)(g_wgs_per_cu > 0 ? g_wgs_per_cu : wpc) * num_cus();
+      const long target = (long)(wpcu > 0 ? wpcu : wpc) * num_cus();
       nch = (target + rows - 1) / rows;
     }
     nch = std::max(1L, std::min({nch, tiles, (long)kMaxChunks}));
     a.nchunks = (int)nch;
     a.chunk = (int)((tiles + nch - 1) / nch * align);
   } else {
-    a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, wpc);
+    a.chunk = plan_chunk(span > 0 ? span : 1, rows, align, wpc, split, wpcu);
     a.nchunks = span > 0 ? (span + a.chunk - 1) / a.chunk : 1;
     // bound the chunk count (grid x, and the combine's per-pair loop)
     while (a.nchunks > kMaxChunks && a.chunk < kMaxChunk) {
@@ -2452,6 +2746,10 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   a.part_o = nullptr;
   a.part_ml = nullptr;
   a.qrot = nullptr;
+  a.ctr = nullptr;
+  a.xmap = 0;
+  a.slots = rows;
+  a.mrg = 0;
   if (a.nchunks == 1) return 0;  // single chunk: written directly, no combine
   if ((long)rows > kMaxSlots) return MOLOT_ENOTSUP;
   const size_t P = (size_t)gh * d;
@@ -2459,12 +2757,29 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   const size_t pml = (size_t)rows * a.nchunks * gh * 2;
   const size_t qr = (size_t)rows * P;
   void* ws = nullptr;
-  const int st = workspace(stream, sizeof(float) * (po + pml + qr), &ws);
+  int* ctr = nullptr;
+  const int st = workspace(stream, sizeof(float) * (po + pml + qr), &ctr, &ws);
   if (st) return st;
   a.part_o = reinterpret_cast<float*>(ws);
   a.part_ml = a.part_o + po;
   a.qrot = a.part_ml + pml;
+  int dev = 0;
+  const bool merge = knob(g_merge) && !a.chunk_fast && (rows % 8 == 0 || rows < 8) &&
+                     (long)a.nchunks * gh <= kMergeMaxStats && hipGetDevice(&dev) == hipSuccess &&
+                     xcd_ok_cached(dev);
+  if (merge) {
+    a.ctr = ctr;
+    a.xmap = rows % 8 != 0;
+    a.mrg = 2 * a.nchunks * gh + gh;
+  }
   return 0;
+}
+
+// The combine kernel merges this launch's chunks instead.
+void no_merge(AttnArgs& a) {
+  a.ctr = nullptr;
+  a.xmap = 0;
+  a.mrg = 0;
 }
 
 using AttnFn = void (*)(AttnArgs);
@@ -2481,10 +2796,11 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   if ((gh * d) % kCombPairs || d % kCombPairs) return MOLOT_ENOTSUP;  // combine tiling
   t_last_nchunks = a.nchunks;
   t_last_chunk = a.chunk;
-  a.dynamic = g_dynamic;
+  a.dynamic = knob(g_dynamic);
   std::lock_guard<std::mutex> plk(g_prof_mu);
   const bool prof = prof_active(stream);
-  ProfRec pr{nullptr, nullptr, nullptr, nullptr, a.nchunks > 1};
+  const bool combine = a.nchunks > 1 && !a.ctr;  // a second launch merges the chunks
+  ProfRec pr{nullptr, nullptr, nullptr, nullptr, combine};
   // Workgroup i runs on XCD i % 8 (its L2 and its share of the CUs), and
   // workgroups are dispatched in linear order.  With the (KV head, subgroup)
   // index fastest, every XCD gets the same heads' share of every chunk and
@@ -2498,9 +2814,13 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   // (id / 8 / heads) * 8 + id % 8 and head (id / 8) % heads, so chunk slot z
   // is on XCD z % 8 whatever the chunk count, each XCD's heads of a chunk are
   // dispatched together, and the padding ids exit at once.
+  // xmap (in-launch merge, fewer than 8 slots): a 1-D grid of 8 * nchunks
+  // workgroups, id running chunk slot id / 8 of slot id % 8, so each slot's
+  // chunks share an XCD; ids of absent slots exit at once.
   const dim3 grid = a.chunk_fast
                         ? dim3((unsigned)((a.nchunks + 7) / 8 * 8 * a.nkv * nsubs), 1, 1)
-                        : dim3(a.nkv * nsubs, B, a.nchunks);
+                        : a.xmap ? dim3((unsigned)(8 * a.nchunks), 1, 1)
+                                 : dim3(a.nkv * nsubs, B, a.nchunks);
   if (prof) {
     pr.a0 = prof_event();
     pr.a1 = prof_event();
@@ -2510,7 +2830,7 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
     hipLaunchKernelGGL(kern, grid, dim3(threads), lds, (hipStream_t)stream, a);
   }
   int st = (int)hipGetLastError();
-  if (st || a.nchunks == 1) {
+  if (st || !combine) {
     if (prof) g_prof.push_back(pr);
     return st;
   }
@@ -2532,6 +2852,7 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   cb.window = a.window;
   cb.rope = rope ? 1 : 0;
   cb.paged = paged ? 1 : 0;
+  cb.fold = rope && a.fold ? 1 : 0;
   // At most 8 chunks (batches of sequences: many slots, few chunks): one
   // wave per 64 pairs (combine_wave_kernel<R>, R = 4 or 8 o loads per lane).
   // More chunks: combine_kernel, whose 4 phases per pair keep the loads per
@@ -2564,7 +2885,10 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
   // contiguous caches: 32-row groups dealt round robin (the kernel's gmap)
   int st = plan_launch(a, D, span, GH, nsubs, B, PAGED ? C::RB : 32, 1, stream, !PAGED);
   if (st) return st;
-  const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED);
+  if (a.mrg && sizeof(float) * (size_t)Lds(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED,
+                                           a.mrg).total > 65536)
+    no_merge(a);  // the merge's statistics do not fit beside the kernel's LDS
+  const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED, a.mrg);
   return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, C>, C::NT, sizeof(float) * (size_t)L.total,
                      a, GH, D, nsubs, B, PAGED, ROPE, stream);
 }
@@ -2578,27 +2902,19 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
 template <int D, int GH, bool PAGED, bool ROPE, bool Q8>
 int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
   constexpr int kWpc = PAGED ? (Q8 ? 8 : 16) : 1;
+  a.chunk_fast = Q8 && !PAGED && B == 1;
   int st = plan_launch(a, D, span, GH, nsubs, B, kTile, kWpc, stream, !PAGED);
   if (st) return st;
-  a.chunk_fast = Q8 && !PAGED && B == 1;
-  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8);
+  if (a.mrg && sizeof(float) * (size_t)LdsM(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg).total >
+                   65536)
+    no_merge(a);
+  const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg);
   return launch_pair(attn_mfma_kernel<D, GH, PAGED, ROPE, Q8>, kMfmaThreads,
                      sizeof(float) * (size_t)L.total, a, GH, D, nsubs, B, PAGED, ROPE, stream);
 }
 
 template <int D, int GH, typename T, bool PAGED, bool ROPE>
 int launch_attn(const AttnArgs& a, int span, int nsubs, int B, void* stream) {
-  if constexpr (D == 128 && GH == 4 && sizeof(T) == 4 && !PAGED) {
-    switch (g_variant) {  // alternative mappings of the headline shape, for sweeps
-      case 1: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 16, 8>>(a, span, nsubs, B, stream);
-      case 2: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 8, 12>>(a, span, nsubs, B, stream);
-      case 3: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 4, 12, 2>>(a, span, nsubs, B, stream);
-      case 4: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 8, 8, 2>>(a, span, nsubs, B, stream);
-      case 5: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 4, 16>>(a, span, nsubs, B, stream);
-      case 6: return launch_cfg<D, GH, T, PAGED, ROPE, Cfg<D, GH, T, 16, 8, 16>>(a, span, nsubs, B, stream);
-      default: break;
-    }
-  }
   return launch_cfg<D, GH, T, PAGED, ROPE, typename Tune<D, GH, T>::C>(a, span, nsubs, B, stream);
 }
 
@@ -2829,10 +3145,9 @@ int molot_hip_profile_end(float* attn_ms, float* combine_ms, int* launches, int*
   return st;
 }
 
-void molot_hip_set_tuning(int wgs_per_cu, int variant) {
-  g_wgs_per_cu = wgs_per_cu > 0 ? wgs_per_cu : 0;
-  g_variant = variant > 0 ? variant : 0;
-}
+void molot_hip_set_tuning(int wgs_per_cu) { g_wgs_per_cu = wgs_per_cu > 0 ? wgs_per_cu : 0; }
+
+void molot_hip_set_merge(int in_launch) { g_merge = in_launch ? 1 : 0; }
 
 int molot_hip_rope_apply(float* x, int nheads, int d, int pos, const float* inv_freq,
                          void* stream) {
@@ -2854,8 +3169,10 @@ static int rope_append_impl(float* q, const float* k_new, const float* v_new, vo
                             int kv_dtype, const Norms& nm, void* stream) {
   if (nq < 0 || nkv <= 0 || d <= 0 || (d & 1) || d > 2048 || slot < 0) return MOLOT_EINVAL;
   if (!norms_ok(nm)) return MOLOT_EINVAL;
-  if ((nq > 0 && !q) || !k_new || !v_new || !K || !V || !inv_freq) return MOLOT_EINVAL;
+  if ((nq > 0 && !q) || !k_new || !v_new || !K || !V) return MOLOT_EINVAL;
   if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
+  // rows only the attention kernels can read back (their Q8 head dims)
+  if (kv_dtype == MOLOT_KV_Q8 && check_common(nkv, nkv, d, kv_dtype)) return MOLOT_ENOTSUP;
   RopeArgs a{};
   a.q = q;
   a.k_new = k_new;
@@ -2959,7 +3276,7 @@ static int decode_step_impl(float* q, const float* k_new, const float* v_new, vo
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   if (!norms_ok(nm)) return MOLOT_EINVAL;
-  if (!q || !k_new || !v_new || !K || !V || !O || !inv_freq || slot < 0) return MOLOT_EINVAL;
+  if (!q || !k_new || !v_new || !K || !V || !O || slot < 0) return MOLOT_EINVAL;
   if (!aligned16(K) || !aligned16(V) || !aligned16(q) || !aligned16(O)) return MOLOT_EINVAL;
   const int n = slot + 1;
   int t0 = (window > 0 && pos - window + 1 > 0) ? pos - window + 1 : 0;
@@ -2992,6 +3309,7 @@ static int decode_step_impl(float* q, const float* k_new, const float* v_new, vo
   a.pos = pos;
   a.window = window;
   a.scale = scale;
+  a.fold = 1;
   return run_attn<false, true>(a, d, kv_dtype, n - 1 - t0, 1, stream);  // cache rows
 }
 
@@ -3085,7 +3403,7 @@ static int decode_step_paged_impl(float* q, const float* k_new, const float* v_n
   int st = paged_args(a, q, K, V, O, block_table, seq_lens, pos, B, max_blocks, max_seq_len, nq,
                       nkv, d, page, scale, window, kv_dtype, &span);
   if (st) return st;
-  if (!k_new || !v_new || !inv_freq) return MOLOT_EINVAL;
+  if (!k_new || !v_new) return MOLOT_EINVAL;
   if (B == 0) return 0;
   if (pos) {
     // a position behind the cache end can leave the new slot outside the
@@ -3104,6 +3422,7 @@ static int decode_step_paged_impl(float* q, const float* k_new, const float* v_n
   a.k_new = k_new;
   a.v_new = v_new;
   a.inv_freq = inv_freq;
+  a.fold = 1;
   return run_attn<true, true>(a, d, kv_dtype, span, B, stream);  // span >= cache rows
 }
 
@@ -3152,9 +3471,12 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
   if (nq < 0 || nkv <= 0 || d <= 0 || (d & 1) || d > 2048 || B < 0 || max_blocks <= 0 ||
       page <= 0)
     return MOLOT_EINVAL;
-  if ((nq > 0 && !q) || !k_new || !v_new || !K || !V || !inv_freq || !block_table || !seq_lens)
+  if ((nq > 0 && !q) || !k_new || !v_new || !K || !V || !block_table || !seq_lens)
     return MOLOT_EINVAL;
   if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
+  // the page layout every paged attention entry accepts
+  if ((page & (page - 1)) || !q8_pages_ok(nkv, page, kv_dtype)) return MOLOT_EINVAL;
+  if (kv_dtype == MOLOT_KV_Q8 && check_common(nkv, nkv, d, kv_dtype)) return MOLOT_ENOTSUP;
   if (B == 0) return 0;
   RopeArgs a{};
   a.q = q;
@@ -3271,7 +3593,7 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   nm.eps = eps;
   if (!norms_ok(nm) || M < 0 || slot0 < 0 || pos0 < 0) return MOLOT_EINVAL;
   if (M == 0) return 0;
-  if (!q || !k_new || !v_new || !K || !V || !O || !inv_freq) return MOLOT_EINVAL;
+  if (!q || !k_new || !v_new || !K || !V || !O) return MOLOT_EINVAL;
   if ((int64_t)M > 65535) return MOLOT_ENOTSUP;  // one grid row per token
   if (block_row && ((int64_t)slot0 + M > (int64_t)max_blocks * page || page <= 0 ||
                     (page & (page - 1)) || !q8_pages_ok(nkv, page, kv_dtype)))
@@ -3330,6 +3652,104 @@ int molot_hip_prefill_step_paged(float* q, const float* k_new, const float* v_ne
   return prefill_step_impl(q, k_new, v_new, K, V, O, nq, nkv, d, M, slot0, pos0, q_norm, k_norm,
                            v_norm, eps, inv_freq, scale, window, kv_dtype, block_row, page,
                            max_blocks, stream);
+}
+
+// Norm and RoPE of M rows of queries [M][nq][d] at positions pos0 + m, in
+// place, no append (the RoPE/append kernel with its KV part off).
+static int q_prologue(float* q, int nq, int d, int M, int pos0, const float* q_norm, float eps,
+                      const float* inv_freq, void* stream) {
+  if (nq < 0 || M < 0 || d <= 0 || (d & 1) || d > 2048 || pos0 < 0) return MOLOT_EINVAL;
+  if (!(eps >= 0.f && eps < INFINITY)) return MOLOT_EINVAL;
+  if (nq == 0 || M == 0) return 0;
+  if (!q) return MOLOT_EINVAL;
+  if ((int64_t)M > 65535) return MOLOT_ENOTSUP;  // one grid row per token
+  if (!q_norm && !inv_freq) return 0;            // nothing to apply
+  RopeArgs r{};
+  r.q = q;
+  r.inv_freq = inv_freq;
+  r.nq = nq;
+  r.nkv = 1;
+  r.d = d;
+  r.pos = pos0;
+  r.tokens = 1;
+  r.q_norm = q_norm;
+  r.eps = eps;
+  hipLaunchKernelGGL(rope_append_kernel, dim3(nq, M), dim3(((d / 2) + 63) / 64 * 64), 0,
+                     (hipStream_t)stream, r);
+  return (int)hipGetLastError();
+}
+
+int molot_hip_prefill_q(float* q, int nq, int d, int M, int pos0, const float* q_norm, float eps,
+                        const float* inv_freq, void* stream) {
+  return q_prologue(q, nq, d, M, pos0, q_norm, eps, inv_freq, stream);
+}
+
+int molot_hip_decode_step_shared(float* q, const void* K, const void* V, float* O, int nq,
+                                 int nkv, int d, int n, int pos, const float* q_norm, float eps,
+                                 const float* inv_freq, float scale, int window, int kv_dtype,
+                                 void* stream) {
+  int st = check_common(nq, nkv, d, kv_dtype);
+  if (st) return st;
+  if (!q || !K || !V || !O || n <= 0 || pos < 0) return MOLOT_EINVAL;  // n = 0: forward.h:580
+  if (!(eps >= 0.f && eps < INFINITY)) return MOLOT_EINVAL;
+  if (!aligned16(K) || !aligned16(V) || !aligned16(q) || !aligned16(O)) return MOLOT_EINVAL;
+  int t0 = (window > 0 && pos - window + 1 > 0) ? pos - window + 1 : 0;
+  if (t0 >= n) {  // nothing attended: q still gets its norm and RoPE, o = 0
+    st = q_prologue(q, nq, d, 1, pos, q_norm, eps, inv_freq, stream);
+    if (st) return st;
+    return zero_out(O, (int64_t)nq * d, (hipStream_t)stream);
+  }
+  AttnArgs a{};
+  a.q = q;
+  a.q_out = q;
+  a.k = const_cast<void*>(K);
+  a.v = const_cast<void*>(V);
+  a.inv_freq = inv_freq;
+  a.o = O;
+  token_major(a, nkv, d, kv_dtype);
+  a.nq = nq;
+  a.nkv = nkv;
+  a.n = n;
+  a.t0 = t0;
+  a.pos = pos;
+  a.window = window;
+  a.scale = scale;
+  a.q_norm = q_norm;
+  a.eps = eps;
+  a.fold = 0;  // all n slots are the source layer's; nothing appended
+  return run_attn<false, true>(a, d, kv_dtype, n - t0, 1, stream);
+}
+
+int molot_hip_decode_step_paged_shared(float* q, const void* K, const void* V, float* O,
+                                       const int32_t* block_table, const int32_t* seq_lens,
+                                       const int32_t* pos, int B, int max_blocks, int max_seq_len,
+                                       int nq, int nkv, int d, int page, const float* q_norm,
+                                       float eps, const float* inv_freq, float scale, int window,
+                                       int kv_dtype, void* stream) {
+  if (!(eps >= 0.f && eps < INFINITY)) return MOLOT_EINVAL;
+  AttnArgs a{};
+  int span = 0;
+  int st = paged_args(a, q, const_cast<void*>(K), const_cast<void*>(V), O, block_table, seq_lens,
+                      pos, B, max_blocks, max_seq_len, nq, nkv, d, page, scale, window, kv_dtype,
+                      &span);
+  if (st) return st;
+  if (B == 0) return 0;
+  a.q_out = q;
+  a.inv_freq = inv_freq;
+  a.q_norm = q_norm;
+  a.eps = eps;
+  a.fold = 0;
+  return run_attn<true, true>(a, d, kv_dtype, span, B, stream);
+}
+
+int molot_hip_attn_prefill_paged(const float* Qm, const void* K, const void* V, float* Om,
+                                 const int32_t* block_row, int max_blocks, int page, int nq,
+                                 int nkv, int M, int N, int d, float scale, int pos0, int window,
+                                 int kv_dtype, void* stream) {
+  if (!block_row || max_blocks <= 0 || N < 0 || (int64_t)N > (int64_t)max_blocks * page)
+    return MOLOT_EINVAL;
+  return attn_prefill_impl(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window, kv_dtype,
+                           block_row, page, stream);
 }
 
 int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream) {

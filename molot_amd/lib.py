@@ -58,6 +58,13 @@ _SIGS = {
                                _F, _I, _I, _P],
     "molot_hip_prefill_step_paged": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
                                      _P, _P, _I, _F, _P, _F, _I, _I, _P],
+    "molot_hip_decode_step_shared": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P, _F, _I, _I,
+                                     _P],
+    "molot_hip_decode_step_paged_shared": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                           _I, _P, _F, _P, _F, _I, _I, _P],
+    "molot_hip_prefill_q": [_P, _I, _I, _I, _I, _P, _F, _P, _P],
+    "molot_hip_attn_prefill_paged": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F, _I, _I,
+                                     _I, _P],
     "molot_hip_last_plan": [ctypes.POINTER(_I), ctypes.POINTER(_I)],
     "molot_hip_q8_row_bytes": [_I, _I],
     "molot_hip_profile_begin": [_I],
@@ -70,7 +77,8 @@ _SIGS = {
 _VOID = {
     "molot_rope_inv_freq": [_F, _I, ctypes.POINTER(ctypes.c_float)],
     "molot_hip_set_split_chunk": [_I],
-    "molot_hip_set_tuning": [_I, _I],
+    "molot_hip_set_tuning": [_I],
+    "molot_hip_set_merge": [_I],
     "molot_hip_set_block_order": [_I],
     "molot_hip_set_bf16_path": [_I],
 }

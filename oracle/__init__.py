@@ -74,6 +74,9 @@ def lib() -> ctypes.CDLL:
             "orc_attn_prefill": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _I]),
             "orc_decode_step_norm": (None, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P,
                                             _I, _F, _P, _F, _I, _I, _I]),
+            "orc_prefill_q": (None, [_P, _I, _I, _I, _I, _P, _F, _P]),
+            "orc_decode_step_shared": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P, _F,
+                                              _I, _I, _I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -129,6 +132,10 @@ def ref() -> ctypes.CDLL:
             "ref_rmsnorm_plain": (None, [_P, _P, _I, _F]),
             "ref_decode_step_norm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P,
                                           _I, _F, _P, _F, _I, _P]),
+            "ref_decode_step_shared": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _P, _F,
+                                            _I, _P]),
+            "ref_prefill_shared": (None, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _F, _P, _F,
+                                          _I, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(R, name)
@@ -258,15 +265,21 @@ def attn_decode_paged(Q, Kp, Vp, block_table, seq_lens, pos, B, max_blocks, nq, 
     return O
 
 
+def _table(inv_freq):
+    """A RoPE table, or None for a layer without RoPE (an empty L.freq)."""
+    return None if inv_freq is None else _f32(inv_freq)
+
+
 def decode_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, slot, pos, inv_freq, scale, window,
                 nthreads=0):
-    """forward.h:556-591: returns (q_rot, k_rot, O); Kc/Vc are updated in place."""
+    """forward.h:556-591: returns (q_rot, k_rot, O); Kc/Vc are updated in place.
+    inv_freq None: no RoPE (forward.h:556, :566)."""
     q = _f32(q).copy()
     k = _f32(k_new).copy()
     v = _f32(v_new)
     O = np.empty((nq, d), dtype=np.float32)
     lib().orc_decode_step(_p(q), _p(k), _p(v), _p(Kc), _p(Vc), _p(O), nq, nkv, d, int(slot),
-                          int(pos), _p(_f32(inv_freq)), float(scale), int(window), _kv_code(Kc),
+                          int(pos), _p(_table(inv_freq)), float(scale), int(window), _kv_code(Kc),
                           int(nthreads))
     return q, k, O
 
@@ -295,7 +308,7 @@ def decode_step_norm(q, k_new, v_new, Kc, Vc, nq, nkv, d, slot, pos, q_norm, k_n
     kn = None if k_norm is None else _f32(k_norm)
     lib().orc_decode_step_norm(_p(q), _p(k), _p(v), _p(Kc), _p(Vc), _p(O), nq, nkv, d, int(slot),
                                int(pos), _p(qn), _p(kn), int(v_norm), float(eps),
-                               _p(_f32(inv_freq)), float(scale), int(window), _kv_code(Kc),
+                               _p(_table(inv_freq)), float(scale), int(window), _kv_code(Kc),
                                int(nthreads))
     return q, k, O
 
@@ -322,16 +335,18 @@ def prefill_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, M, slot0, pos0, q_norm, k_
     q = _f32(q).copy().reshape(M, nq, d)
     k = _f32(k_new).copy().reshape(M, nkv, d)
     v = _f32(v_new).copy().reshape(M, nkv, d)
-    inv = _f32(inv_freq)
+    inv = _table(inv_freq)
     for m in range(M):
         if q_norm is not None:
             q[m] = rmsnorm(q[m], q_norm, eps)
-        q[m] = rope_apply(q[m], pos0 + m, inv)
+        if inv is not None:  # forward.h:373
+            q[m] = rope_apply(q[m], pos0 + m, inv)
         if k_norm is not None:
             k[m] = rmsnorm(k[m], k_norm, eps)
         if v_norm:
             v[m] = rmsnorm(v[m].reshape(-1), None, eps).reshape(nkv, d)
-        k[m] = rope_apply(k[m], pos0 + m, inv)
+        if inv is not None:  # forward.h:381
+            k[m] = rope_apply(k[m], pos0 + m, inv)
         if Kc.dtype == np.uint16:
             Kc[slot0 + m] = f32_to_bf16(k[m].reshape(-1))
             Vc[slot0 + m] = f32_to_bf16(v[m].reshape(-1))
@@ -342,6 +357,32 @@ def prefill_step(q, k_new, v_new, Kc, Vc, nq, nkv, d, M, slot0, pos0, q_norm, k_
             Kc[slot0 + m] = k[m].reshape(-1)
             Vc[slot0 + m] = v[m].reshape(-1)
     O = attn_prefill(q, Kc, Vc, nq, nkv, M, slot0 + M, d, scale, pos0, window, nthreads)
+    return q, O
+
+
+def prefill_q(q, nq, d, M, pos0, q_norm, eps, inv_freq):
+    """The query prologue of a layer without its own KV (forward.h:370-375):
+    rows [M][nq][d] normed (q_norm None: no norm) and rotated at pos0 + m
+    (inv_freq None: no RoPE).  Returns the new rows."""
+    q = _f32(q).copy().reshape(M, nq, d)
+    lib().orc_prefill_q(_p(q), nq, d, int(M), int(pos0), _p(None if q_norm is None else
+                                                            _f32(q_norm)), float(eps),
+                        _p(_table(inv_freq)))
+    return q
+
+
+def decode_step_shared(q, Kc, Vc, nq, nkv, d, n, pos, q_norm, eps, inv_freq, scale, window,
+                       nthreads=0):
+    """forward.h:554-558, 578-591 for a layer reading another layer's cache
+    Kc/Vc (token-major; n valid slots): returns (q_rot, O), appends nothing."""
+    q = _f32(q).copy()
+    O = np.empty((nq, d), dtype=np.float32)
+    Kc = np.ascontiguousarray(Kc)
+    Vc = np.ascontiguousarray(Vc)
+    lib().orc_decode_step_shared(_p(q), _p(Kc), _p(Vc), _p(O), nq, nkv, d, int(n), int(pos),
+                                 _p(None if q_norm is None else _f32(q_norm)), float(eps),
+                                 _p(_table(inv_freq)), float(scale), int(window), _kv_code(Kc),
+                                 int(nthreads))
     return q, O
 
 

@@ -19,7 +19,12 @@
  *                              to strided / bf16 / paged K,V so the same
  *                              algorithm covers attn.h:57-120 and :178-187.
  *       orc_decode_step     <- include/molot/forward.h:556-591 (rope q, rope k,
- *                              append, attention)
+ *                              append, attention; no rope without a table,
+ *                              :556/:566)
+ *       orc_decode_step_shared, orc_prefill_q
+ *                           <- include/molot/forward.h:554-558, 578-591 and
+ *                              :370-375, 394-398 (a layer reading another
+ *                              layer's KV: q norm and rope, no append)
  *       orc_attn_prefill    <- include/molot/gemm.h:409-446 (causal prefill:
  *                              scalar expf, double denominator)
  *       orc_quantize_q8_row <- include/molot/quant.h:34-50 (quantize_q8_row), the
@@ -369,12 +374,16 @@ void orc_attn_decode_paged(const float* Q, const void* Kp, const void* Vp, float
 
 /* forward.h:556-591 for one layer: rope q heads and k heads at `pos`,
  * append k (rotated) and v into slot `slot` of the token-major cache
- * (bf16-rounded when kv_dtype is bf16), then attention over n = slot + 1. */
+ * (bf16-rounded when kv_dtype is bf16), then attention over n = slot + 1.
+ * inv_freq NULL: a layer without RoPE (an empty L.freq, model.h:535-536),
+ * whose q and k forward.h:556 and :566 leave unrotated. */
 void orc_decode_step(float* q, float* k_new, const float* v_new, void* Kc, void* Vc, float* O,
                      int nq, int nkv, int d, int slot, int pos, const float* inv_freq,
                      float scale, int window, int kv_dtype, int nthreads) {
-  orc_rope_apply_heads(q, nq, d, pos, inv_freq);
-  orc_rope_apply_heads(k_new, nkv, d, pos, inv_freq);
+  if (inv_freq) {
+    orc_rope_apply_heads(q, nq, d, pos, inv_freq);
+    orc_rope_apply_heads(k_new, nkv, d, pos, inv_freq);
+  }
   size_t S = (size_t)nkv * d;
   if (kv_dtype == ORC_KV_F32) {
     memcpy((float*)Kc + (size_t)slot * S, k_new, S * 4);
@@ -411,6 +420,34 @@ void orc_decode_step_norm(float* q, float* k_new, const float* v_new, void* Kc, 
   orc_decode_step(q, k_new, v, Kc, Vc, O, nq, nkv, d, slot, pos, inv_freq, scale, window,
                   kv_dtype, nthreads);
   free(v);
+}
+
+/* The query prologue of one token of a layer without its own KV
+ * (forward.h:554-558 / :370-375): q heads RMS-normed with q_norm (NULL:
+ * none), then rotated at pos when inv_freq is given.  Rows [M][nq][d], row m
+ * at pos0 + m. */
+void orc_prefill_q(float* q, int nq, int d, int M, int pos0, const float* q_norm, float eps,
+                   const float* inv_freq) {
+  for (int m = 0; m < M; ++m) {
+    float* qm = q + (size_t)m * nq * d;
+    if (q_norm)
+      for (int h = 0; h < nq; ++h)
+        orc_rmsnorm(qm + (size_t)h * d, q_norm, qm + (size_t)h * d, d, eps);
+    if (inv_freq) orc_rope_apply_heads(qm, nq, d, pos0 + m, inv_freq);
+  }
+}
+
+/* forward.h:554-558 and :578-591 for a layer that reads another layer's KV
+ * (L.has_kv false): the query prologue at pos, then attention over the n
+ * slots of the source cache (token-major, any kv_dtype); nothing appended. */
+void orc_decode_step_shared(float* q, const void* Kc, const void* Vc, float* O, int nq, int nkv,
+                            int d, int n, int pos, const float* q_norm, float eps,
+                            const float* inv_freq, float scale, int window, int kv_dtype,
+                            int nthreads) {
+  orc_prefill_q(q, nq, d, 1, pos, q_norm, eps, inv_freq);
+  const int64_t tok = kv_dtype == ORC_KV_Q8 ? orc_q8_row_bytes(nkv, d) : (int64_t)nkv * d;
+  orc_attn_decode(q, Kc, Vc, O, nq, nkv, n, d, scale, pos, window, kv_dtype, tok, d, 0, NULL, 0,
+                  nthreads);
 }
 
 /* Causal prefill attention (gemm.h:409-446) over the token-major cache

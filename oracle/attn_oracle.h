@@ -41,6 +41,12 @@ void orc_decode_step_norm(float* q, float* k_new, const float* v_new, void* Kc, 
                           const float* q_norm, const float* k_norm, int v_norm, float eps,
                           const float* inv_freq, float scale, int window, int kv_dtype,
                           int nthreads);
+void orc_prefill_q(float* q, int nq, int d, int M, int pos0, const float* q_norm, float eps,
+                   const float* inv_freq);
+void orc_decode_step_shared(float* q, const void* Kc, const void* Vc, float* O, int nq, int nkv,
+                            int d, int n, int pos, const float* q_norm, float eps,
+                            const float* inv_freq, float scale, int window, int kv_dtype,
+                            int nthreads);
 void orc_attn_prefill(const float* Qm, const void* K, const void* V, float* Om, int nq, int nkv,
                       int M, int N, int d, float scale, int pos0, int window, int kv_dtype,
                       int nthreads);

@@ -75,12 +75,16 @@ void ref_attn_decode_gqa_win(const float* Q, const float* K, const float* V, flo
 // The decode-attention block of Runner::forward_token (forward.h:556-591)
 // for one layer with its own KV: rope q heads, rope k heads, append k/v at
 // slot `slot` of the [cap][nkv*d] cache, attention over n = slot + 1.
-// Returns 0, or -1 where forward.h:570 would throw "KV cache full".
+// A NULL inv_freq is a layer without RoPE (an empty L.freq): forward.h:556
+// and :566 then skip rope_apply.  Returns 0, or -1 where forward.h:570
+// would throw "KV cache full".
 int ref_decode_step(float* q, float* k, const float* v, float* Kc, float* Vc, float* O, int nq,
                     int nkv, int d, int slot, int cap, int pos, const float* inv_freq, float scale,
                     int window, void* pool) {
-  for (int hh = 0; hh < nq; ++hh) molot::rope_apply(q + (size_t)hh * d, d, pos, inv_freq);
-  for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(k + (size_t)hh * d, d, pos, inv_freq);
+  if (inv_freq)  // forward.h:556, :566: no rotation for a layer without RoPE
+    for (int hh = 0; hh < nq; ++hh) molot::rope_apply(q + (size_t)hh * d, d, pos, inv_freq);
+  if (inv_freq)
+    for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(k + (size_t)hh * d, d, pos, inv_freq);
   if (slot >= cap) return -1;
   std::memcpy(Kc + (size_t)slot * nkv * d, k, (size_t)nkv * d * 4);
   std::memcpy(Vc + (size_t)slot * nkv * d, v, (size_t)nkv * d * 4);
@@ -101,7 +105,8 @@ void ref_attn_prefill_gqa(const float* Qm, const float* K, const float* V, float
 // with k_norm, v normed over its nkv*d values when v_norm, k rotated, k/v
 // appended at slot slot0 + m; then attn_prefill_gqa over N = slot0 + M.
 // NULL weights skip a norm (forward.h always has them; the shim lets tests
-// isolate RoPE + append).  Returns -1 where forward.h:380 would throw.
+// isolate RoPE + append); a NULL inv_freq skips RoPE, as forward.h:373 and
+// :381 do for a layer without it.  Returns -1 where forward.h:380 would throw.
 int ref_prefill_step(float* Q, float* Kn, float* Vn, float* Kc, float* Vc, float* O, int nq,
                      int nkv, int d, int M, int slot0, int cap, int pos0, const float* q_norm,
                      const float* k_norm, int v_norm, float eps, const float* inv_freq,
@@ -113,13 +118,15 @@ int ref_prefill_step(float* Q, float* Kn, float* Vn, float* Kc, float* Vc, float
     float* vv = Vn + (size_t)mm * nkv * d;
     for (int hh = 0; hh < nq; ++hh) {
       if (q_norm) molot::rmsnorm(qq + (size_t)hh * d, q_norm, qq + (size_t)hh * d, d, eps);
-      molot::rope_apply(qq + (size_t)hh * d, d, pos0 + mm, inv_freq);
+      if (inv_freq) molot::rope_apply(qq + (size_t)hh * d, d, pos0 + mm, inv_freq);  // :373
     }
     if (k_norm)
       for (int hh = 0; hh < nkv; ++hh)
         molot::rmsnorm(kk + (size_t)hh * d, k_norm, kk + (size_t)hh * d, d, eps);
     if (v_norm) molot::rmsnorm_plain(vv, vv, nkv * d, eps);
-    for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(kk + (size_t)hh * d, d, pos0 + mm, inv_freq);
+    if (inv_freq)  // forward.h:381
+      for (int hh = 0; hh < nkv; ++hh)
+        molot::rope_apply(kk + (size_t)hh * d, d, pos0 + mm, inv_freq);
     std::memcpy(Kc + (size_t)(slot0 + mm) * nkv * d, kk, (size_t)nkv * d * 4);
     std::memcpy(Vc + (size_t)(slot0 + mm) * nkv * d, vv, (size_t)nkv * d * 4);
   }
@@ -148,24 +155,65 @@ void ref_rmsnorm_plain(const float* x, float* y, int n, float eps) {
 // forward.h:554-591 with the layer's norms, in forward.h's order: q heads
 // RMS-normed with q_norm (Runner::rms_per_head, forward.h:138-140) and
 // rotated; k heads normed with k_norm, v normed over all its nkv*d values
-// when v_norm (forward.h:562-563), k rotated; append; attention.
+// when v_norm (forward.h:562-563), k rotated; append; attention.  A NULL
+// inv_freq skips both rotations (forward.h:556, :566).
 int ref_decode_step_norm(float* q, float* k, float* v, float* Kc, float* Vc, float* O, int nq,
                          int nkv, int d, int slot, int cap, int pos, const float* q_norm,
                          const float* k_norm, int v_norm, float eps, const float* inv_freq,
                          float scale, int window, void* pool) {
   for (int hh = 0; hh < nq; ++hh)
     molot::rmsnorm(q + (size_t)hh * d, q_norm, q + (size_t)hh * d, d, eps);
-  for (int hh = 0; hh < nq; ++hh) molot::rope_apply(q + (size_t)hh * d, d, pos, inv_freq);
+  if (inv_freq)  // forward.h:556
+    for (int hh = 0; hh < nq; ++hh) molot::rope_apply(q + (size_t)hh * d, d, pos, inv_freq);
   for (int hh = 0; hh < nkv; ++hh)
     molot::rmsnorm(k + (size_t)hh * d, k_norm, k + (size_t)hh * d, d, eps);
   if (v_norm) molot::rmsnorm_plain(v, v, nkv * d, eps);
-  for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(k + (size_t)hh * d, d, pos, inv_freq);
+  if (inv_freq)  // forward.h:566
+    for (int hh = 0; hh < nkv; ++hh) molot::rope_apply(k + (size_t)hh * d, d, pos, inv_freq);
   if (slot >= cap) return -1;
   std::memcpy(Kc + (size_t)slot * nkv * d, k, (size_t)nkv * d * 4);
   std::memcpy(Vc + (size_t)slot * nkv * d, v, (size_t)nkv * d * 4);
   molot::attn_decode_gqa_cache(q, Kc, Vc, O, nq, nkv, slot + 1, d, scale, pos, window,
                                *static_cast<molot::ThreadPool*>(pool));
   return 0;
+}
+
+// A decode step of a layer without its own KV (L.has_kv false), in
+// forward.h's order: q heads RMS-normed with q_norm (forward.h:554; NULL
+// skips it) and rotated at pos when inv_freq is given (:556-558), then
+// attn_decode_gqa_cache over the source layer's cache Kc/Vc and its n
+// slots (:578-591).  Returns -1 where forward.h:580 would throw "shared KV
+// empty" (n == 0).
+int ref_decode_step_shared(float* q, const float* Kc, const float* Vc, float* O, int nq, int nkv,
+                           int d, int n, int pos, const float* q_norm, float eps,
+                           const float* inv_freq, float scale, int window, void* pool) {
+  if (n == 0) return -1;
+  if (q_norm)
+    for (int hh = 0; hh < nq; ++hh)
+      molot::rmsnorm(q + (size_t)hh * d, q_norm, q + (size_t)hh * d, d, eps);
+  if (inv_freq)
+    for (int hh = 0; hh < nq; ++hh) molot::rope_apply(q + (size_t)hh * d, d, pos, inv_freq);
+  molot::attn_decode_gqa_cache(q, Kc, Vc, O, nq, nkv, n, d, scale, pos, window,
+                               *static_cast<molot::ThreadPool*>(pool));
+  return 0;
+}
+
+// The prefill of a layer without its own KV (forward.h:367-399 with
+// L.has_kv false): per token m the q heads normed with q_norm (NULL: none)
+// and rotated at pos0 + m when inv_freq is given (:370-375), nothing
+// appended, then attn_prefill_gqa over the source cache's N slots (:394-398).
+void ref_prefill_shared(float* Q, const float* Kc, const float* Vc, float* O, int nq, int nkv,
+                        int d, int M, int N, int pos0, const float* q_norm, float eps,
+                        const float* inv_freq, float scale, int window, void* pool) {
+  for (int mm = 0; mm < M; ++mm) {
+    float* qq = Q + (size_t)mm * nq * d;
+    for (int hh = 0; hh < nq; ++hh) {
+      if (q_norm) molot::rmsnorm(qq + (size_t)hh * d, q_norm, qq + (size_t)hh * d, d, eps);
+      if (inv_freq) molot::rope_apply(qq + (size_t)hh * d, d, pos0 + mm, inv_freq);
+    }
+  }
+  molot::attn_prefill_gqa(Q, Kc, Vc, O, nq, nkv, M, N, d, scale, pos0, window,
+                          *static_cast<molot::ThreadPool*>(pool));
 }
 
 }  // extern "C"

@@ -150,6 +150,38 @@ int main() {
                   (wq < 1e-5 && cdiff <= 1 && sdiff <= 1e-6) ? "ok" : "FAIL", wq, cdiff);
     }
 
+    // ---- 1d. a layer without RoPE, and a layer reading this cache (shared KV) ----
+    {
+      molot::amd::DeviceKV kvn(cap, nkv, d);
+      std::vector<float> Kn((size_t)cap * nkv * d, 0.f), Vn((size_t)cap * nkv * d, 0.f);
+      double wn = 0, ws = 0;
+      for (int pos = 0; pos < 40; ++pos) {
+        std::vector<float> q(nq * d), k(nkv * d), v(nkv * d), ao(nq * d), ao_ref(nq * d);
+        rng.normal(q);
+        rng.normal(k);
+        rng.normal(v);
+        std::vector<float> q_ref = q, k_ref = k;
+        kvn.decode(q.data(), k.data(), v.data(), ao.data(), nq, pos, nullptr, scale, 0);
+        orc_decode_step(q_ref.data(), k_ref.data(), v.data(), Kn.data(), Vn.data(), ao_ref.data(),
+                        nq, nkv, d, pos, pos, nullptr, scale, 0, ORC_KV_F32, 1);
+        wn = std::fmax(wn, normwise(ao, ao_ref));
+        CHECK(q == q_ref, "NoPE decode rotated q at pos %d", pos);
+        // a shared-KV layer over the same cache, with RoPE
+        std::vector<float> q2(nq * d), ao2(nq * d), ao2_ref(nq * d);
+        rng.normal(q2);
+        std::vector<float> q2_ref = q2;
+        kvn.decode_shared(q2.data(), ao2.data(), nq, pos, inv_d, scale, 0);
+        orc_decode_step_shared(q2_ref.data(), Kn.data(), Vn.data(), ao2_ref.data(), nq, nkv, d,
+                               pos + 1, pos, nullptr, 0.f, inv.data(), scale, 0, ORC_KV_F32, 1);
+        ws = std::fmax(ws, normwise(ao2, ao2_ref));
+        CHECK(normwise(q2, q2_ref) < 1e-6, "shared decode q at pos %d", pos);
+      }
+      CHECK(wn < 1e-5, "DeviceKV NoPE decode normwise err %g", wn);
+      CHECK(ws < 1e-5, "DeviceKV shared decode normwise err %g", ws);
+      std::printf("[%s] DeviceKV NoPE decode and shared-KV decode, 40 steps: %.2e, %.2e\n",
+                  (wn < 1e-5 && ws < 1e-5) ? "ok" : "FAIL", wn, ws);
+    }
+
     // ---- 2. attn.h drop-in on the same cache, host q/o, sliding window ----
     std::vector<float> q(nq * d), o(nq * d), o_ref(nq * d);
     rng.normal(q);

@@ -1,6 +1,7 @@
 // Self-check of the paged-KV manager (include/molot_amd/paged_kv.hpp) on
 // the GPU: sequences prefilled and decoded as a continuous batch across two
-// layers, one freed and its blocks reused by a new one, against the CPU
+// layers and a third layer reading layer 0's pages (shared KV), one freed
+// and its blocks reused by a new one, the step state machine, against the CPU
 // oracle (oracle/attn_oracle.c) on per-sequence contiguous caches of the
 // same element type -- once over bf16 pages and once over Q8 pages.  The
 // oracle's attention runs on the rows the GPU appended (read back from the
@@ -228,6 +229,23 @@ int run_scenario(int kv_dtype, const char* name) {
       worst_o = std::fmax(worst_o, normwise(dO.get(O.size()), O));
       CHECK(normwise(dq.get(q.size()), q) < 2e-6, "%s prefill q seq %d layer %d", name, id, l);
     }
+    {  // a layer reading layer 0's pages (shared KV): q norm + RoPE, no append
+      std::vector<float> q((size_t)M * kNq * kD);
+      rng.normal(q);
+      Dev dq(q.size()), dO(q.size());
+      dq.put(q);
+      molot::amd::LayerNorms sn;
+      sn.q_norm = d_w.p;
+      sn.eps = kEps;
+      kv.prefill_shared(0, dq.p, dO.p, kNq, pos0, d_inv.p, kScale, 0, sn);
+      molot::amd::check_hip(hipDeviceSynchronize(), "sync");
+      orc_prefill_q(q.data(), kNq, kD, M, pos0, qn.data(), kEps, inv.data());
+      std::vector<float> O((size_t)M * kNq * kD);
+      orc_attn_prefill(q.data(), r.K[0].data(), r.V[0].data(), O.data(), kNq, kNkv, M, pos0 + M,
+                       kD, kScale, pos0, 0, odt, 0);
+      worst_o = std::fmax(worst_o, normwise(dO.get(O.size()), O));
+      CHECK(normwise(dq.get(q.size()), q) < 2e-6, "%s shared prefill q seq %d", name, id);
+    }
     kv.end_prefill();
     r.len += M;
   };
@@ -268,6 +286,32 @@ int run_scenario(int kv_dtype, const char* name) {
         worst_o = std::fmax(worst_o, normwise(g, O));
       }
     }
+    {  // a layer reading layer 0's pages (shared KV): its rows count this token
+      std::vector<float> q((size_t)B * kNq * kD);
+      rng.normal(q);
+      Dev dq(q.size()), dO(q.size());
+      dq.put(q);
+      molot::amd::LayerNorms sn;
+      sn.q_norm = d_w.p;
+      sn.eps = kEps;
+      kv.decode_shared(0, dq.p, dO.p, kNq, d_inv.p, kScale, 0, sn);
+      molot::amd::check_hip(hipDeviceSynchronize(), "sync");
+      const std::vector<float> got = dO.get(q.size()), gq = dq.get(q.size());
+      for (int b = 0; b < B; ++b) {
+        RefSeq& r = ref[ids[b]];
+        float* qb = q.data() + (size_t)b * kNq * kD;
+        std::vector<float> O((size_t)kNq * kD);
+        orc_decode_step_shared(qb, r.K[0].data(), r.V[0].data(), O.data(), kNq, kNkv, kD,
+                               r.len + 1, r.len, qn.data(), kEps, inv.data(), kScale, 0, odt, 0);
+        std::vector<float> g(got.begin() + (size_t)b * kNq * kD,
+                             got.begin() + (size_t)(b + 1) * kNq * kD);
+        worst_o = std::fmax(worst_o, normwise(g, O));
+        std::vector<float> gqb(gq.begin() + (size_t)b * kNq * kD,
+                               gq.begin() + (size_t)(b + 1) * kNq * kD);
+        std::vector<float> rq(qb, qb + (size_t)kNq * kD);
+        CHECK(normwise(gqb, rq) < 2e-6, "%s shared decode q seq %d", name, ids[b]);
+      }
+    }
     kv.end_decode();
     for (int id : ids) ref[id].len += 1;
   };
@@ -296,6 +340,32 @@ int run_scenario(int kv_dtype, const char* name) {
               "reuse: max normwise err %.2e, rows within %.2f of the allowed deviation\n",
               failures > failures0 ? "FAIL" : "ok", name, worst_o, worst_row);
 
+  // step state: a step is begun once and ended once; a begin that finds the
+  // pool full leaves no step behind
+  {
+    molot::amd::PagedKVCache st(1, 3, kNkv, kD, kPage, kv_dtype);
+    const int a = st.add_sequence(), b2 = st.add_sequence();
+    auto throws = [](auto&& fn) {
+      try {
+        fn();
+      } catch (const std::runtime_error&) {
+        return true;
+      }
+      return false;
+    };
+    CHECK(throws([&] { st.end_decode(); }), "%s end_decode without a step", name);
+    CHECK(throws([&] { st.end_prefill(); }), "%s end_prefill without a step", name);
+    st.begin_prefill(a, 30);  // 2 of the 3 blocks
+    CHECK(throws([&] { st.begin_decode({a}); }), "%s begin inside a step", name);
+    CHECK(throws([&] { st.end_decode(); }), "%s end_decode inside a prefill", name);
+    st.end_prefill();
+    CHECK(throws([&] { st.end_prefill(); }), "%s second end_prefill", name);
+    CHECK(throws([&] { st.begin_prefill(b2, 20); }), "%s prefill beyond the pool", name);
+    st.begin_decode({a});  // no step was left open by the failed begin
+    st.end_decode();
+    CHECK(st.length(a) == 31 && st.length(b2) == 0, "%s lengths after the state checks %d %d",
+          name, st.length(a), st.length(b2));
+  }
   // a full pool reports what a full contiguous cache does (forward.h:570)
   {
     molot::amd::PagedKVCache small(1, 2, kNkv, kD, kPage, kv_dtype);

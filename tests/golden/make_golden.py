@@ -143,6 +143,105 @@ def gen_prefill(name, nq, nkv, d, M, n0, base, window, scale, eps, norms, seed, 
           seed=seed)
 
 
+def gen_decode_step_nope(name, nq, nkv, d, n0, window, scale, eps, seed, pool):
+    """forward.h:554-591 for a layer without RoPE (an empty L.freq:
+    rope_swa_only models' global layers, model.h:535-536), through the
+    reference with the norms: q/k rmsnorm, v rmsnorm_plain, no rope_apply
+    (forward.h:556, :566 skip it), append, attention."""
+    R = oracle.ref()
+    st = Stream(seed)
+    q = st.normal((nq, d), 2.0)
+    k = st.normal((nkv, d), 2.0)
+    v = st.normal((nkv, d), 2.0)
+    q_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    k_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    cap = n0 + 1
+    Kc = np.zeros((cap, nkv * d), np.float32)
+    Vc = np.zeros((cap, nkv * d), np.float32)
+    Kc[:n0] = st.normal((n0, nkv * d))
+    Vc[:n0] = st.normal((n0, nkv * d))
+    q_out, k_out, v_out = q.copy(), k.copy(), v.copy()
+    Kout, Vout = Kc.copy(), Vc.copy()
+    O = np.empty((nq, d), np.float32)
+    rc = R.ref_decode_step_norm(P(q_out), P(k_out), P(v_out), P(Kout), P(Vout), P(O), nq, nkv,
+                                d, n0, cap, n0, P(q_norm), P(k_norm), 1, float(eps), None,
+                                float(scale), int(window), pool.h)
+    assert rc == 0
+    _save(name, q=q, k_new=k, v_new=v, K=Kc[:n0], V=Vc[:n0], q_norm=q_norm, k_norm=k_norm,
+          q_out=q_out, k_out=k_out, v_normed=v_out, O=O, nq=nq, nkv=nkv, d=d, pos=n0,
+          window=window, scale=scale, eps=eps, seed=seed)
+
+
+def gen_decode_step_shared(name, nq, nkv, d, n, pos, base, window, scale, eps, rope, seed,
+                           pool):
+    """forward.h:554-558, 578-591 for a layer reading another layer's cache
+    (L.has_kv false) through the reference: q rmsnorm, rope_apply when the
+    layer has a table, attn_decode_gqa_cache over the source's n slots."""
+    R = oracle.ref()
+    st = Stream(seed)
+    q = st.normal((nq, d), 2.0)
+    q_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    Kc = st.normal((n, nkv * d))
+    Vc = st.normal((n, nkv * d))
+    inv = ref_inv_freq(base, d) if rope else None
+    q_out = q.copy()
+    O = np.empty((nq, d), np.float32)
+    rc = R.ref_decode_step_shared(P(q_out), P(Kc), P(Vc), P(O), nq, nkv, d, n, pos, P(q_norm),
+                                  float(eps), P(inv) if rope else None, float(scale),
+                                  int(window), pool.h)
+    assert rc == 0
+    extra = {"inv_freq": inv} if rope else {}
+    _save(name, q=q, K=Kc, V=Vc, q_norm=q_norm, q_out=q_out, O=O, nq=nq, nkv=nkv, d=d, n=n,
+          pos=pos, window=window, scale=scale, eps=eps, rope=int(rope), seed=seed, **extra)
+
+
+def gen_prefill_nope(name, nq, nkv, d, M, n0, window, scale, eps, seed, pool):
+    """forward.h:367-399 for a layer without RoPE through the reference:
+    per-token norms, no rotation (forward.h:373, :381), append, causal
+    attention."""
+    R = oracle.ref()
+    st = Stream(seed)
+    q = st.normal((M, nq, d), 2.0)
+    k = st.normal((M, nkv, d), 2.0)
+    v = st.normal((M, nkv, d), 2.0)
+    q_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    k_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    cap = n0 + M
+    Kc = np.zeros((cap, nkv * d), np.float32)
+    Vc = np.zeros((cap, nkv * d), np.float32)
+    Kc[:n0] = st.normal((n0, nkv * d))
+    Vc[:n0] = st.normal((n0, nkv * d))
+    q_out, k_out, v_out = q.copy(), k.copy(), v.copy()
+    Kout, Vout = Kc.copy(), Vc.copy()
+    O = np.empty((M, nq, d), np.float32)
+    rc = R.ref_prefill_step(P(q_out), P(k_out), P(v_out), P(Kout), P(Vout), P(O), nq, nkv, d, M,
+                            n0, cap, n0, P(q_norm), P(k_norm), 1, float(eps), None, float(scale),
+                            int(window), pool.h)
+    assert rc == 0
+    _save(name, q=q, k_new=k, v_new=v, K=Kc[:n0], V=Vc[:n0], q_norm=q_norm, k_norm=k_norm,
+          q_out=q_out, K_after=Kout[n0:], V_after=Vout[n0:], O=O, nq=nq, nkv=nkv, d=d, M=M,
+          pos0=n0, window=window, scale=scale, eps=eps, seed=seed)
+
+
+def gen_prefill_shared(name, nq, nkv, d, M, N, pos0, base, window, scale, eps, seed, pool):
+    """forward.h:367-399 for a layer without its own KV through the
+    reference: per-token q rmsnorm and rope_apply, no append, then
+    attn_prefill_gqa over the source cache's N slots at pos0."""
+    R = oracle.ref()
+    st = Stream(seed)
+    q = st.normal((M, nq, d), 2.0)
+    q_norm = (1.0 + st.normal((d,), 0.2)).astype(np.float32)
+    Kc = st.normal((N, nkv * d))
+    Vc = st.normal((N, nkv * d))
+    inv = ref_inv_freq(base, d)
+    q_out = q.copy()
+    O = np.empty((M, nq, d), np.float32)
+    R.ref_prefill_shared(P(q_out), P(Kc), P(Vc), P(O), nq, nkv, d, M, N, pos0, P(q_norm),
+                         float(eps), P(inv), float(scale), int(window), pool.h)
+    _save(name, q=q, K=Kc, V=Vc, q_norm=q_norm, inv_freq=inv, q_out=q_out, O=O, nq=nq, nkv=nkv,
+          d=d, M=M, N=N, pos0=pos0, window=window, scale=scale, eps=eps, seed=seed)
+
+
 def gen_q8_rows(name, d, seed):
     """quantize_q8_row (quant.h:34-50) through the reference on rows that
     probe its edges: Gaussian rows of two scales, an all-zero row (scale 1),
@@ -279,6 +378,24 @@ def main() -> None:
         if want("prefill_norm_win_d128"):
             gen_prefill("prefill_norm_win_d128", nq=4, nkv=2, d=128, M=12, n0=20, base=10000.0,
                         window=8, scale=1.0, eps=1e-6, norms=True, seed=24, pool=pool)
+        if want("decode_step_nope_g4_d128"):
+            gen_decode_step_nope("decode_step_nope_g4_d128", nq=8, nkv=2, d=128, n0=77,
+                                 window=0, scale=1.0, eps=1e-6, seed=26, pool=pool)
+        if want("decode_step_shared_g4_d128"):
+            gen_decode_step_shared("decode_step_shared_g4_d128", nq=8, nkv=2, d=128, n=120,
+                                   pos=119, base=500000.0, window=0, scale=1.0, eps=1e-6,
+                                   rope=True, seed=27, pool=pool)
+        if want("decode_step_shared_nope_win_d256"):
+            gen_decode_step_shared("decode_step_shared_nope_win_d256", nq=4, nkv=2, d=256, n=70,
+                                   pos=69, base=10000.0, window=20, scale=1.0, eps=1e-6,
+                                   rope=False, seed=28, pool=pool)
+        if want("prefill_nope_d128"):
+            gen_prefill_nope("prefill_nope_d128", nq=4, nkv=2, d=128, M=13, n0=25, window=0,
+                             scale=1.0, eps=1e-6, seed=29, pool=pool)
+        if want("prefill_shared_win_d128"):
+            gen_prefill_shared("prefill_shared_win_d128", nq=4, nkv=2, d=128, M=10, N=40,
+                               pos0=30, base=10000.0, window=12, scale=1.0, eps=1e-6, seed=30,
+                               pool=pool)
         if want("head_bench_check"):
             gen_head("head_bench_check", n=160, d=128, sigma=0.2, seed=1234)
         if want("gqa_headmajor_d64"):

@@ -97,3 +97,26 @@ def make_paged(B, nq, nkv, d, lmin, lmax, page=16, seed=1234, bf16=True, spare_b
         Kp, Vp = f32_to_bf16(Kp), f32_to_bf16(Vp)
     return dict(q=q, k_new=k_new, v_new=v_new, n=n, bt=bt, Kp=Kp, Vp=Vp, page=page,
                 max_blocks=max_blocks, B=B, nq=nq, nkv=nkv, d=d)
+
+
+def oracle_paged(P, inv, scale, window=0, pos=None):
+    """The oracle's fused step per sequence of a make_paged batch: (q_rot, K pages, V pages, O)."""
+    Kp, Vp = P["Kp"].copy(), P["Vp"].copy()
+    B, nq, nkv, d, page = P["B"], P["nq"], P["nkv"], P["d"], P["page"]
+    q = np.empty_like(P["q"])
+    for b in range(B):
+        n = int(P["n"][b])
+        p = n - 1 if pos is None else int(pos[b])
+        q[b] = P["q"][b] if inv is None else oracle.rope_apply(P["q"][b], p, inv)
+        k = P["k_new"][b] if inv is None else oracle.rope_apply(P["k_new"][b], p, inv)
+        slot = n - 1
+        blk = P["bt"][b, slot // page]
+        if Kp.dtype == np.uint16:
+            Kp[blk, :, slot % page] = oracle.f32_to_bf16(k)
+            Vp[blk, :, slot % page] = oracle.f32_to_bf16(P["v_new"][b])
+        else:
+            Kp[blk, :, slot % page] = k
+            Vp[blk, :, slot % page] = P["v_new"][b]
+    O = oracle.attn_decode_paged(q, Kp, Vp, P["bt"], P["n"], pos, B, P["max_blocks"], nq, nkv, d,
+                                 page, scale, window)
+    return q, Kp, Vp, O

@@ -141,6 +141,35 @@ def test_q8_validation_before_launch():
                                            1, 64, 2, 0.1, 0, Q8, s) == L.EINVAL
     assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 256, 0.1, 6, 0,
                                           Q8, s) == L.ENOTSUP
+    # the RoPE/append entries write only rows the attention entries read back
+    assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 2, 256, 5, 5, _p(), Q8,
+                                     s) == L.ENOTSUP
+    assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,
+                                           8, 2, 256, 16, _p(), Q8, s) == L.ENOTSUP
+    assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,
+                                           8, 1, 64, 2, _p(), Q8, s) == L.EINVAL
+    assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,
+                                           8, 2, 64, 12, _p(), 0, s) == L.EINVAL
+
+
+def test_shared_kv_entries_validate_before_launch():
+    lib = L.load()
+    s = ctypes.c_void_p(0)
+    # an empty source cache (forward.h:580 throws "shared KV empty")
+    assert lib.molot_hip_decode_step_shared(_p(), _p(), _p(), _p(), 8, 2, 128, 0, 0, None, 1e-6,
+                                            None, 0.1, 0, 0, s) == L.EINVAL
+    # negative eps, odd head dim
+    assert lib.molot_hip_decode_step_shared(_p(), _p(), _p(), _p(), 8, 2, 128, 5, 4, None, -1.0,
+                                            None, 0.1, 0, 0, s) == L.EINVAL
+    assert lib.molot_hip_prefill_q(_p(), 8, 127, 3, 0, None, 1e-6, _p(), s) == L.EINVAL
+    # nothing to apply: no launch, success
+    assert lib.molot_hip_prefill_q(_p(), 8, 128, 3, 0, None, 1e-6, None, s) == 0
+    # paged prefill: N beyond the block-table row
+    assert lib.molot_hip_attn_prefill_paged(_p(), _p(), _p(), _p(), _p(), 4, 16, 8, 2, 3, 65, 128,
+                                            0.1, 62, 0, 0, s) == L.EINVAL
+    assert lib.molot_hip_decode_step_paged_shared(_p(), _p(), _p(), _p(), _p(), _p(), None, 2, 4,
+                                                  40, 8, 4, 128, 12, None, 1e-6, None, 0.1, 0, 0,
+                                                  s) == L.EINVAL
 
 
 def test_python_kv_dtype_codes():

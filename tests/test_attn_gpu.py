@@ -15,7 +15,8 @@ import torch
 
 import oracle
 from conftest import normwise_err
-from gpu_util import dev, dev_bf16, host, make_decode, make_paged, oracle_decode, widen
+from gpu_util import (dev, dev_bf16, host, make_decode, make_paged, oracle_decode,
+                      oracle_paged, widen)
 from molot_amd import attn
 from molot_amd.synth import Stream, bf16_to_f32, f32_to_bf16
 
@@ -578,28 +579,6 @@ def run_paged(P, inv, scale, window=0, pos=None):
     return host(q), Kh, Vh, host(O)
 
 
-def oracle_paged(P, inv, scale, window=0, pos=None):
-    Kp, Vp = P["Kp"].copy(), P["Vp"].copy()
-    B, nq, nkv, d, page = P["B"], P["nq"], P["nkv"], P["d"], P["page"]
-    q = np.empty_like(P["q"])
-    for b in range(B):
-        n = int(P["n"][b])
-        p = n - 1 if pos is None else int(pos[b])
-        q[b] = oracle.rope_apply(P["q"][b], p, inv)
-        k = oracle.rope_apply(P["k_new"][b], p, inv)
-        slot = n - 1
-        blk = P["bt"][b, slot // page]
-        if Kp.dtype == np.uint16:
-            Kp[blk, :, slot % page] = oracle.f32_to_bf16(k)
-            Vp[blk, :, slot % page] = oracle.f32_to_bf16(P["v_new"][b])
-        else:
-            Kp[blk, :, slot % page] = k
-            Vp[blk, :, slot % page] = P["v_new"][b]
-    O = oracle.attn_decode_paged(q, Kp, Vp, P["bt"], P["n"], pos, B, P["max_blocks"], nq, nkv, d,
-                                 page, scale, window)
-    return q, Kp, Vp, O
-
-
 def test_c4_continuous_batching_paged_bf16(gpu):
     announce("c4 64 seqs U[512,8192] paged16 shuffled bf16")
     P = make_paged(64, 32, 8, 128, 512, 8192)
@@ -643,12 +622,14 @@ def run_paged_fused(P, inv, scale, window=0):
 
 @pytest.mark.parametrize("bf16", [False, True])
 @pytest.mark.parametrize("window", [0, 100])
-def test_paged_fused_step(gpu, bf16, window):
+@pytest.mark.parametrize("shape", [(32, 8, 128), (8, 4, 256)], ids=["d128", "d256"])
+def test_paged_fused_step(gpu, bf16, window, shape):
     """molot_hip_decode_step_paged (one launch) == oracle rope + append + attention."""
-    announce(f"paged fused bf16={bf16} window={window}")
-    P = make_paged(17, 32, 8, 128, 0, 2000, seed=5 + window, bf16=bf16)
-    inv = oracle.rope_inv_freq(500000.0, 128)
-    s = 1 / math.sqrt(128)
+    nq, nkv, d = shape
+    announce(f"paged fused {nq}/{nkv}/{d} bf16={bf16} window={window}")
+    P = make_paged(17, nq, nkv, d, 0, 2000, seed=5 + window + d, bf16=bf16)
+    inv = oracle.rope_inv_freq(500000.0, d)
+    s = 1 / math.sqrt(d)
     q, Kh, Vh, O = run_paged_fused(P, inv, s, window)
     oq, oK, oV, oO = oracle_paged(P, inv, s, window)
     np.testing.assert_allclose(q, oq, atol=4e-6, rtol=2e-6)

@@ -290,6 +290,103 @@ def test_v_norm_is_over_all_kv_heads():
 
 
 # ---------------------------------------------------------------------------
+# Layers without RoPE (an empty L.freq: forward.h:556, :566, :373, :381 skip
+# rope_apply) and layers reading another layer's KV (forward.h:578-591,
+# :394-398), against fixtures written from the compiled forward.h sequences
+
+def test_decode_step_nope_golden():
+    g = golden("decode_step_nope_g4_d128")
+    nq, nkv, d, pos = int(g["nq"]), int(g["nkv"]), int(g["d"]), int(g["pos"])
+    Kc = np.zeros((pos + 1, nkv * d), np.float32)
+    Vc = np.zeros_like(Kc)
+    Kc[:pos], Vc[:pos] = g["K"], g["V"]
+    q_out, k_out, O = oracle.decode_step_norm(g["q"], g["k_new"], g["v_new"], Kc, Vc, nq, nkv, d,
+                                              pos, pos, g["q_norm"], g["k_norm"], 1,
+                                              float(g["eps"]), None, float(g["scale"]),
+                                              int(g["window"]))
+    np.testing.assert_allclose(q_out, g["q_out"], rtol=5e-7, atol=1e-7)  # normed, unrotated
+    np.testing.assert_allclose(k_out, g["k_out"], rtol=5e-7, atol=1e-7)
+    np.testing.assert_array_equal(Kc[pos], k_out.reshape(-1))
+    np.testing.assert_allclose(Vc[pos], g["v_normed"].reshape(-1), rtol=5e-7, atol=0)
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+def test_planted_rope_on_nope_layer_is_caught():
+    """Rotating a NoPE layer's q and k (with any table, here the model's
+    usual one) misses the reference's step, which leaves them unrotated."""
+    g = golden("decode_step_nope_g4_d128")
+    nq, nkv, d, pos = int(g["nq"]), int(g["nkv"]), int(g["d"]), int(g["pos"])
+    Kc = np.zeros((pos + 1, nkv * d), np.float32)
+    Vc = np.zeros_like(Kc)
+    Kc[:pos], Vc[:pos] = g["K"], g["V"]
+    q_out, _, O = oracle.decode_step_norm(g["q"], g["k_new"], g["v_new"], Kc, Vc, nq, nkv, d, pos,
+                                          pos, g["q_norm"], g["k_norm"], 1, float(g["eps"]),
+                                          oracle.rope_inv_freq(500000.0, d), float(g["scale"]),
+                                          int(g["window"]))
+    assert np.max(np.abs(q_out - g["q_out"])) > 1e-2
+    assert normwise_err(O, g["O"]) > 1e-4
+
+
+@pytest.mark.parametrize("name", ["decode_step_shared_g4_d128", "decode_step_shared_nope_win_d256"])
+def test_decode_step_shared_golden(name):
+    g = golden(name)
+    nq, nkv, d, n, pos = (int(g[k]) for k in ("nq", "nkv", "d", "n", "pos"))
+    inv = g["inv_freq"] if int(g["rope"]) else None
+    K, V = g["K"].copy(), g["V"].copy()
+    q_out, O = oracle.decode_step_shared(g["q"], K, V, nq, nkv, d, n, pos, g["q_norm"],
+                                         float(g["eps"]), inv, float(g["scale"]), int(g["window"]))
+    np.testing.assert_allclose(q_out, g["q_out"], rtol=2e-6, atol=2e-6)
+    np.testing.assert_array_equal(K, g["K"])  # nothing appended
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+def test_shared_step_equals_owning_step():
+    """A layer reading a cache that already holds this token's row (the
+    source layer appended it earlier in the step) gets the owning layer's
+    output and rotated q: the shared step is the decode step minus its
+    append."""
+    st = Stream(41)
+    nq, nkv, d, pos, window = 8, 2, 128, 300, 0
+    q, k, v = st.normal((nq, d)), st.normal((nkv, d)), st.normal((nkv, d))
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    K = np.zeros((pos + 1, nkv * d), np.float32)
+    V = np.zeros_like(K)
+    K[:pos], V[:pos] = kv_token_major(st, pos, nkv, d)
+    inv = oracle.rope_inv_freq(500000.0, d)
+    q1, _, O1 = oracle.decode_step_norm(q, k, v, K, V, nq, nkv, d, pos, pos, qn, None, 0, 1e-6,
+                                        inv, 0.1, window)
+    q2, O2 = oracle.decode_step_shared(q, K, V, nq, nkv, d, pos + 1, pos, qn, 1e-6, inv, 0.1,
+                                       window)
+    np.testing.assert_array_equal(q1, q2)
+    np.testing.assert_array_equal(O1, O2)
+
+
+def test_prefill_nope_golden():
+    g = golden("prefill_nope_d128")
+    nq, nkv, d, M, pos0 = (int(g[k]) for k in ("nq", "nkv", "d", "M", "pos0"))
+    Kc = np.zeros((pos0 + M, nkv * d), np.float32)
+    Vc = np.zeros_like(Kc)
+    Kc[:pos0], Vc[:pos0] = g["K"], g["V"]
+    q_out, O = oracle.prefill_step(g["q"], g["k_new"], g["v_new"], Kc, Vc, nq, nkv, d, M, pos0,
+                                   pos0, g["q_norm"], g["k_norm"], 1, float(g["eps"]), None,
+                                   float(g["scale"]), int(g["window"]))
+    np.testing.assert_allclose(q_out, g["q_out"], rtol=5e-7, atol=1e-7)
+    np.testing.assert_allclose(Kc[pos0:], g["K_after"], rtol=5e-7, atol=1e-7)
+    np.testing.assert_allclose(Vc[pos0:], g["V_after"], rtol=1e-6, atol=1e-7)
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+def test_prefill_shared_golden():
+    g = golden("prefill_shared_win_d128")
+    nq, nkv, d, M, N, pos0 = (int(g[k]) for k in ("nq", "nkv", "d", "M", "N", "pos0"))
+    q_out = oracle.prefill_q(g["q"], nq, d, M, pos0, g["q_norm"], float(g["eps"]), g["inv_freq"])
+    O = oracle.attn_prefill(q_out, g["K"], g["V"], nq, nkv, M, N, d, float(g["scale"]), pos0,
+                            int(g["window"]))
+    np.testing.assert_allclose(q_out, g["q_out"], rtol=2e-6, atol=4e-6)
+    assert normwise_err(O, g["O"]) < 2e-6
+
+
+# ---------------------------------------------------------------------------
 # prefill attention (gemm.h:409-446) and the layer's prefill (forward.h:367-399)
 
 def _prefill_f64(Q, K, V, nq, nkv, M, N, d, scale, pos0, window):
@@ -740,3 +837,41 @@ def test_vexp_vs_reference_random():
     for i in range(0, x.size, 16):
         oracle.ref().ref_exp16(oracle._p(x[i:i + 16]), oracle._p(r[i:i + 16]))
     np.testing.assert_allclose(y, r, rtol=2e-7, atol=1.2e-38)  # reference flushes denormals
+
+
+@needs_ref
+def test_nope_and_shared_steps_vs_reference():
+    """The restated NoPE step and shared-KV step against the compiled
+    forward.h sequences at the headline head shape, with a window."""
+    st = Stream(43)
+    nq, nkv, d, pos, window = 32, 8, 128, 1200, 500
+    q, k, v = st.normal((nq, d), 2.0), st.normal((nkv, d), 2.0), st.normal((nkv, d), 2.0)
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    kn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    K = np.zeros((pos + 1, nkv * d), np.float32)
+    V = np.zeros_like(K)
+    K[:pos], V[:pos] = kv_token_major(st, pos, nkv, d)
+    P = oracle._p
+    Ko, Vo = K.copy(), V.copy()
+    q1, _, O1 = oracle.decode_step_norm(q, k, v, Ko, Vo, nq, nkv, d, pos, pos, qn, kn, 1, 1e-6,
+                                        None, 1.0, window)
+    qr, kr, vr, Kr, Vr = q.copy(), k.copy(), v.copy(), K.copy(), V.copy()
+    R1 = np.empty((nq, d), np.float32)
+    inv = oracle.rope_inv_freq(10000.0, d)
+    q2, O2 = oracle.decode_step_shared(q, Ko, Vo, nq, nkv, d, pos + 1, pos, qn, 1e-6, inv, 1.0,
+                                       window)
+    qs_ = q.copy()
+    R2 = np.empty((nq, d), np.float32)
+    with oracle.RefPool(4) as pool:
+        rc = oracle.ref().ref_decode_step_norm(P(qr), P(kr), P(vr), P(Kr), P(Vr), P(R1), nq, nkv,
+                                               d, pos, pos + 1, pos, P(qn), P(kn), 1, 1e-6, None,
+                                               1.0, window, pool.h)
+        assert rc == 0
+        rc = oracle.ref().ref_decode_step_shared(P(qs_), P(Kr), P(Vr), P(R2), nq, nkv, d, pos + 1,
+                                                 pos, P(qn), 1e-6, P(inv), 1.0, window, pool.h)
+        assert rc == 0
+    np.testing.assert_allclose(q1, qr, rtol=5e-7, atol=1e-7)
+    np.testing.assert_allclose(Vo[pos], Vr[pos], rtol=5e-7, atol=0)
+    assert normwise_err(O1, R1) < 2e-6
+    np.testing.assert_allclose(q2, qs_, rtol=2e-6, atol=2e-6)
+    assert normwise_err(O2, R2) < 2e-6

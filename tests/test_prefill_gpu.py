@@ -163,7 +163,8 @@ def test_prefill_step_vs_oracle(gpu, bf16):
 
 
 @pytest.mark.parametrize("nq,nkv,d,bf16", [(32, 8, 128, False), (32, 8, 128, True),
-                                           (8, 2, 64, False)])
+                                           (8, 2, 64, False), (8, 4, 256, False),
+                                           (8, 4, 256, True)])
 def test_prefill_step_paged_matches_contiguous(gpu, nq, nkv, d, bf16):
     """The paged prefill step (shuffled 16-row pages, spare blocks) on the
     same logical rows as the contiguous one: the same kernel arithmetic, so
