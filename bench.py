@@ -108,9 +108,9 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--split-chunk", type=int, default=0, help="tokens per chunk (0 = auto)")
     ap.add_argument("--wgs-per-cu", type=int, default=0, help="workgroups per CU (0 = auto)")
-    ap.add_argument("--merge", type=int, default=0,
+    ap.add_argument("--merge", type=int, default=-1,
                     help="1 = split-K partials merged inside the attention launch where possible, "
-                         "0 = by the combine kernel (default)")
+                         "0 = by the combine kernel, -1 = the library's choice (default)")
     ap.add_argument("--norms", action="store_true",
                     help="the step with the layer's q/k/v RMS norms fused in (forward.h:554-563)")
     ap.add_argument("--block-order", type=int, default=1,

@@ -286,14 +286,17 @@ void molot_hip_set_split_chunk(int tokens);
 /* Workgroups per CU the split-K plan targets (0 = the plan's own). */
 void molot_hip_set_tuning(int wgs_per_cu);
 
-/* How a split context's chunk partials are merged.  in_launch = 0
- * (default): by a second kernel (combine_kernel) on the same stream.
- * in_launch = 1: inside the attention launch, by the workgroup that
- * completes a (sequence, KV head group) slot, where the device dispatches
- * workgroup i to XCD i % 8 (checked once per device) and the launch can
- * keep a slot's chunks on one XCD; other launches use the combine kernel.
- * Both give the same result to fp32 rounding; on the measured MI355X boxes
- * the second launch was the faster of the two. */
+/* How a split context's chunk partials are merged.  in_launch = 0: by a
+ * second kernel (combine_kernel) on the same stream.  in_launch = 1: inside
+ * the attention launch, by the workgroup that completes a (sequence, KV
+ * head group) slot, where the device dispatches workgroup i to XCD i % 8
+ * (checked once per device) and the launch can keep a slot's chunks on one
+ * XCD; other launches use the combine kernel.  in_launch < 0 (default):
+ * in the launch for the fp32 vector-ALU kernel when the slots are a
+ * multiple of 8 on a contiguous cache (every XCD busy) and the attended
+ * context spans at least 8192 rows, else the combine kernel.  Both give the same result to
+ * fp32 rounding.  If a launch ever found a slot's chunks on different XCDs
+ * its merged output would be NaN rather than a stale merge. */
 void molot_hip_set_merge(int in_launch);
 
 /* Order in which the waves of a workgroup take their chunk's row blocks.

@@ -466,10 +466,11 @@ def set_split_chunk(tokens: int) -> None:
     _lib.load().molot_hip_set_split_chunk(int(tokens))
 
 
-def set_merge(in_launch: bool) -> None:
-    """Split-K chunks merged inside the attention launch (True) or by the
-    combine kernel (False, the default); see molot_hip_set_merge."""
-    _lib.load().molot_hip_set_merge(1 if in_launch else 0)
+def set_merge(in_launch) -> None:
+    """Split-K chunks merged inside the attention launch (True), by the
+    combine kernel (False), or as the library chooses (None, the default);
+    see molot_hip_set_merge."""
+    _lib.load().molot_hip_set_merge(-1 if in_launch is None else (1 if in_launch else 0))
 
 
 def profile(fn, launches: int = 64):

@@ -381,6 +381,7 @@ struct AttnArgs {
   float* part_o;         // [slots][nchunks][GH*D] chunk partial o (split-K)
   float* part_ml;        // [slots][nchunks][GH][2] chunk partial (max, sum)
   float* qrot;           // [slots][GH*D] rotated q for the combine kernel (ROPE)
+  int* part_x;           // [slots][nchunks] XCD of each chunk's workgroup (in-launch merge)
   const int32_t* block_table;
   const int32_t* seq_lens;
   const int32_t* pos_arr;
@@ -442,9 +443,10 @@ struct Cfg {
 };
 
 // Default mapping: q registers (GH x D/LPR) kept at <= 32 where the 16-byte
-// vector allows it; one block in flight per wave; then the block size and
-// wave count with the most waves per SIMD (register estimate), preferring
-// 8-row blocks; one workgroup per CU (NW = 4 x waves per SIMD, at most 16).
+// vector allows it; one block in flight per wave; 8-row blocks at two waves
+// per SIMD where D <= 128 and the register estimate allows, else the block size with the
+// most waves per SIMD; one workgroup per CU (NW = 4 x waves per SIMD, at
+// most 16).
 template <int D, int GH, typename T>
 struct Tune {
   static constexpr int VW = KVT<T>::VW;
@@ -468,16 +470,23 @@ struct Tune {
   static constexpr bool ok(int rb) {
     return rb % RPS == 0 && rb % RPI == 0 && loads(rb) <= 16 && wps(rb) >= 2;
   }
+  // 8-row blocks and two waves per SIMD where the registers allow (D <= 128):
+  // the same bytes in flight per CU as 4-row blocks at four waves per SIMD,
+  // with half the waves to merge at the chunk's end (measured, 32q/8kv/d128
+  // fp32: step 28.8 -> 27.3 us at n = 16385, 14.0 -> 13.3 us at n = 4097;
+  // at d = 256, 8q/4kv with a 1024 window, 12 waves of 4-row blocks stay
+  // faster: 9.3 against 9.6 us).
   static constexpr int rb() {
+    if (D <= 128 && ok(8)) return 8;
     int best = 0;
-    for (int r : {8, 16, 4})
+    for (int r : {16, 4})
       if (ok(r) && (best == 0 || wps(r) > wps(best))) best = r;
     if (best) return best;
     return RPS > RPI ? RPS : RPI;
   }
   static constexpr int RB = rb();
   static constexpr int nw() {
-    const int w = wps(RB) >= 1 ? wps(RB) : 1;
+    const int w = RB == 8 ? 2 : (wps(RB) >= 1 ? wps(RB) : 1);
     int nw = 4 * w;
     while (nw > 4 && nw * GH * D > 8192) nw -= 4;  // wave-merge buffer <= 32 KiB
     return nw;
@@ -655,17 +664,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_rsrc(const float* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7FFFFFFF, 0x00020000);
 }
 // Loads at a byte offset of a resource, missing the L1 (cache policy sc0).
-__device__ __forceinline__ float ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 1));
-}
 __device__ __forceinline__ f32x4 ld_l2x4(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 1));
 }
 
-constexpr int kMergeMaxStats = 2048;  // chunks x heads of a slot merged in the launch
-constexpr int kMergeInFlight = 16;    // 16-byte o loads in flight per thread
+__device__ __forceinline__ float2 ld_l2x2(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 1));
+}
 
-// RED: floats of LDS at mred (the phases' partial sums).
+// XCD (accelerator complex) of the calling wave: hardware register XCC_ID.
+__device__ __forceinline__ int xcc_id() {
+  return (int)(__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) & 15);
+}
+
+constexpr int kMergeMaxChunks = 4096;  // chunks of a slot merged in the launch
+constexpr int kMergeAutoSpan = 8192;   // rows from which the default merges in the launch
+constexpr int kMergeMaxPhases = 64;    // threads per float4 quad of the output (NT / quads)
+constexpr int kMergeRound = 8;         // chunks per thread whose loads are in flight together
+
+// LDS floats of the in-launch merge's phase statistics (Lds::mrg, LdsM::mrg).
+__host__ __device__ constexpr int merge_lds_floats(int gh) { return 2 * kMergeMaxPhases * gh; }
+
+// The merge of the workgroup that completes a slot.  Thread t owns float4
+// quad q = t % QV of the slot's output (head g = 4q / D) in phase
+// ph = t / QV; it folds chunks ph, ph + PH, ph + 2*PH, ... with a running
+// log-sum-exp, kMergeRound chunks' loads in flight at a time and only the
+// chunks that exist loaded.  The PH phases of a quad then merge once
+// through LDS: their (max, sum) per head at mst, their o at mred.
+// RED: floats of LDS at mred (the phase sums: PH*P floats).
 template <int D, int GH, int NW, int NT, bool ROPE, int RED>
 __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot, int nch,
                                                  int64_t qrow0, const float* qs, float* mst,
@@ -678,109 +704,105 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
     const int last = old == nch - 1;
     if (last) atomicExch(a.ctr + slot, 0);  // ready for the next launch
     flag[0] = last;
+    flag[1] = 0;  // set below if a chunk ran on another XCD
   }
   lds_barrier();
   if (!flag[0]) return;  // uniform over the workgroup
+  const int my_xcc = xcc_id();
+  bool other_xcd = false;
 
-  // Work split over float4 quads of the partial (QV per chunk): with QV <= NT,
-  // thread t folds quad t % QV over the chunks t / QV + PH*j (PH phases,
-  // summed through LDS at the end); otherwise PH = 1 and thread t takes
-  // quads t, t + NT, ...  CB chunks per quad are loaded per round.
-  constexpr int QV = P / 4;
+  constexpr int QV = P / 4;                     // float4 quads of the slot's output
+  // phases per quad: as many as the threads allow and the phase sums' LDS holds
   constexpr int PH0 = NT >= QV ? NT / QV : 1;
-  constexpr int PH = PH0 * P <= RED ? PH0 : (RED / P > 0 ? RED / P : 1);
-  constexpr int NQ = NT >= QV ? 1 : (QV + NT - 1) / NT;
-  constexpr int CB = kMergeInFlight / NQ > 0 ? kMergeInFlight / NQ : 1;
-  constexpr int SPT = (kMergeMaxStats + NT - 1) / NT;
-  static_assert(P % 4 == 0, "float4 quads");
+  constexpr int PH = PH0 * P <= RED ? PH0 : (RED / P > 1 ? RED / P : 1);
+  constexpr int NQ = NT >= QV ? 1 : (QV + NT - 1) / NT;  // quads per thread
+  static_assert(P % 4 == 0 && D % 4 == 0, "float4 quads");
+  static_assert(PH <= kMergeMaxPhases, "phase statistics fit their LDS");
   const int ph = NT >= QV ? tid / QV : 0;
-  const bool act = ph < PH;
+  const bool act = ph < PH;  // threads past PH * QV idle (NT not a multiple of QV)
   const __amdgpu_buffer_rsrc_t ro = l2_rsrc(a.part_o + slot * a.nchunks * P);
   const __amdgpu_buffer_rsrc_t rm = l2_rsrc(a.part_ml + slot * a.nchunks * (GH * 2));
-  const int ns = nch * GH;
-  // the chunk statistics first, then the first round of o: the statistics
-  // loads retire first, so they are used while the o loads are in flight
-  float sm[SPT], sl[SPT];
-#pragma unroll
-  for (int u = 0; u < SPT; ++u) {
-    const int i = min(tid + u * NT, ns - 1);
-    sm[u] = ld_l2(rm, 8 * i);
-    sl[u] = ld_l2(rm, 8 * i + 4);
-  }
-  int qd[NQ];
-  f32x4 ov[NQ][CB];
+  int qd[NQ], g[NQ];
+  float m[NQ], l[NQ];
+  f32x4 o[NQ];
 #pragma unroll
   for (int i = 0; i < NQ; ++i) {
     qd[i] = NT >= QV ? tid % QV : min(tid + i * NT, QV - 1);
-#pragma unroll
-    for (int u = 0; u < CB; ++u) {
-      const int cc = min(ph + PH * u, nch - 1);
-      ov[i][u] = ld_l2x4(ro, 16 * (cc * QV + qd[i]));
-    }
+    g[i] = 4 * qd[i] / D;
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+    o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float* wts = mst;              // [nch][GH] chunk max, then its weight e^(m_c - M)
-  float* lsv = mst + ns;         // [nch][GH] chunk sum
-  float* Lg = mst + 2 * ns;      // [GH] L = sum_c e^(m_c - M) l_c
+  for (int c0 = act ? ph : nch; c0 < nch; c0 += PH * kMergeRound) {
+    float2 st[NQ][kMergeRound];
+    f32x4 ov[NQ][kMergeRound];
 #pragma unroll
-  for (int u = 0; u < SPT; ++u) {
-    const int i = tid + u * NT;
-    if (i < ns) {
-      wts[i] = sm[u];
-      lsv[i] = sl[u];
-    }
-  }
-  lds_barrier();
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  for (int g = w; g < GH; g += NW) {  // wave w: the weights of head g
-    float mloc = -INFINITY;
-    for (int cc = lane; cc < nch; cc += 64) mloc = fmaxf(mloc, wts[cc * GH + g]);
-    const float M = wave_reduce<true>(mloc);
-    float lloc = 0.f;
-    for (int cc = lane; cc < nch; cc += 64) {
-      const float wc = softmax_exp(wts[cc * GH + g] - M);
-      wts[cc * GH + g] = wc;
-      lloc = fmaf(wc, lsv[cc * GH + g], lloc);
-    }
-    const float Ls = wave_reduce<false>(lloc);
-    if (lane == 0) Lg[g] = Ls;
-  }
-  lds_barrier();
-  f32x4 acc[NQ];
+    for (int u = 0; u < kMergeRound; ++u) {
+      const int cc = c0 + PH * u;
 #pragma unroll
-  for (int i = 0; i < NQ; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0;; c0 += PH * CB) {
+      for (int i = 0; i < NQ; ++i) {
+        if (cc < nch) {
+          st[i][u] = ld_l2x2(rm, 8 * (cc * GH + g[i]));
+          ov[i][u] = ld_l2x4(ro, 16 * (cc * QV + qd[i]));
+          if (i == 0) other_xcd |= a.part_x[slot * a.nchunks + cc] != my_xcc;
+        } else {
+          st[i][u] = float2{-INFINITY, 0.f};
+          ov[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
-      const int g = 4 * qd[i] / D;
+      float mn = m[i];
 #pragma unroll
-      for (int u = 0; u < CB; ++u) {
-        const int cc = c0 + ph + PH * u;
-        if (act && cc < nch) acc[i] += wts[cc * GH + g] * ov[i][u];
+      for (int u = 0; u < kMergeRound; ++u) mn = fmaxf(mn, st[i][u].x);
+      const float al = softmax_exp(m[i] - mn);  // m = -inf on the first round: 0
+      l[i] *= al;
+      o[i] *= al;
+#pragma unroll
+      for (int u = 0; u < kMergeRound; ++u) {
+        const float wc = softmax_exp(st[i][u].x - mn);  // absent chunks: e^-inf = 0
+        l[i] = fmaf(wc, st[i][u].y, l[i]);
+        o[i] += wc * ov[i][u];
+      }
+      m[i] = mn;
+    }
+  }
+  // The hand-off above holds only if every chunk of the slot ran on this
+  // XCD (one L2): otherwise the output is NaN, never a silently stale merge.
+  if (other_xcd) flag[1] = 1;
+  lds_barrier();
+  const float bad = flag[1] ? __builtin_nanf("") : 0.f;
+  if constexpr (PH > 1) {
+    // a phase's (max, sum) is the same for every quad of a head: the
+    // thread holding the head's first quad publishes it
+    if (act) {
+      reinterpret_cast<f32x4*>(mred)[ph * QV + qd[0]] = o[0];
+      if ((4 * qd[0]) % D == 0) {
+        mst[(ph * GH + g[0]) * 2] = m[0];
+        mst[(ph * GH + g[0]) * 2 + 1] = l[0];
       }
     }
-    if (c0 + PH * CB >= nch) break;
-#pragma unroll
-    for (int i = 0; i < NQ; ++i)
-#pragma unroll
-      for (int u = 0; u < CB; ++u) {
-        const int cc = min(c0 + PH * CB + ph + PH * u, nch - 1);
-        ov[i][u] = ld_l2x4(ro, 16 * (cc * QV + qd[i]));
-      }
-  }
-  if constexpr (PH > 1) {
-    if (act) reinterpret_cast<f32x4*>(mred)[ph * QV + qd[0]] = acc[0];
     lds_barrier();
     if (tid < QV) {
-      f32x4 o = reinterpret_cast<const f32x4*>(mred)[tid];
+      float M = -INFINITY;
 #pragma unroll
-      for (int q2 = 1; q2 < PH; ++q2) o += reinterpret_cast<const f32x4*>(mred)[q2 * QV + tid];
-      reinterpret_cast<f32x4*>(a.o + qrow0 * D)[tid] = o / Lg[4 * tid / D];
+      for (int q2 = 0; q2 < PH; ++q2) M = fmaxf(M, mst[(q2 * GH + g[0]) * 2]);
+      float Ls = 0.f;
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q2 = 0; q2 < PH; ++q2) {
+        const float wq = softmax_exp(mst[(q2 * GH + g[0]) * 2] - M);  // phases with no chunk: 0
+        Ls = fmaf(wq, mst[(q2 * GH + g[0]) * 2 + 1], Ls);
+        acc += wq * reinterpret_cast<const f32x4*>(mred)[q2 * QV + tid];
+      }
+      reinterpret_cast<f32x4*>(a.o + qrow0 * D)[tid] = acc / Ls + bad;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int q4 = NT >= QV ? tid : tid + i * NT;
-      if (act && q4 < QV) reinterpret_cast<f32x4*>(a.o + qrow0 * D)[q4] = acc[i] / Lg[4 * q4 / D];
+      if (act && q4 < QV) reinterpret_cast<f32x4*>(a.o + qrow0 * D)[q4] = o[i] / l[i] + bad;
     }
   }
   if constexpr (ROPE) {
@@ -857,6 +879,7 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
     }
   }
   if (a.ctr) {  // in-launch merge: the workgroup completing the slot merges it
+    if (tid == 0) a.part_x[slot * a.nchunks + c] = xcc_id();
     arrive_and_merge<D, GH, NW, NT, ROPE, RED>(a, slot, nch, qrow0, qs, mst, mred, flag, tid,
                                                lane);
     return;
@@ -2523,7 +2546,7 @@ std::atomic<int> g_split_chunk{0};  // tokens per chunk, 0 = automatic
 std::atomic<int> g_wgs_per_cu{0};   // workgroups per CU, 0 = the plan's own
 std::atomic<int> g_dynamic{1};      // block order: 1 = claimed by waves as they free up, 0 = fixed
 std::atomic<int> g_bf16_mfma{1};    // bf16 KV (D = 64, 128) on the matrix-core kernel
-std::atomic<int> g_merge{0};        // 1: split-K partials merged in the launch where possible
+std::atomic<int> g_merge{-1};       // split-K merge: -1 automatic, 0 combine kernel, 1 in the launch
 
 int knob(const std::atomic<int>& k) { return k.load(std::memory_order_relaxed); }
 
@@ -2631,7 +2654,7 @@ int workspace(void* stream, size_t bytes, int** ctr, void** out) {
 __device__ int g_xcc_probe[4096];
 __global__ void xcc_probe_kernel() {
   if (threadIdx.x == 0)
-    g_xcc_probe[blockIdx.x] = (int)(__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) & 15);
+    g_xcc_probe[blockIdx.x] = xcc_id();
 }
 std::mutex g_xcd_mu;
 std::map<int, bool> g_xcd_ok;
@@ -2715,7 +2738,7 @@ int plan_chunk(int span, int rows_of_wgs, int align, int wpc, int split, int wpc
 // slot count is a multiple of 8; fewer than 8 slots take a 1-D grid that
 // puts slot s on XCD s (xmap).  Other slot counts, token-major Q8 launches
 // (whose grid groups the heads of a chunk on one XCD instead) and slots of
-// more than kMergeMaxStats chunk statistics use combine_kernel.
+// more than kMergeMaxChunks chunks use combine_kernel.
 int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int align, int wpc,
                 void* stream, bool cyclic = false) {
   const int rows = a.nkv * nsubs * B;
@@ -2746,6 +2769,7 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   a.part_o = nullptr;
   a.part_ml = nullptr;
   a.qrot = nullptr;
+  a.part_x = nullptr;
   a.ctr = nullptr;
   a.xmap = 0;
   a.slots = rows;
@@ -2756,21 +2780,33 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   const size_t po = (size_t)rows * a.nchunks * P;
   const size_t pml = (size_t)rows * a.nchunks * gh * 2;
   const size_t qr = (size_t)rows * P;
+  const size_t px = (size_t)rows * a.nchunks;  // ints
   void* ws = nullptr;
   int* ctr = nullptr;
-  const int st = workspace(stream, sizeof(float) * (po + pml + qr), &ctr, &ws);
+  const int st = workspace(stream, sizeof(float) * (po + pml + qr + px), &ctr, &ws);
   if (st) return st;
   a.part_o = reinterpret_cast<float*>(ws);
   a.part_ml = a.part_o + po;
   a.qrot = a.part_ml + pml;
+  a.part_x = reinterpret_cast<int*>(a.qrot + qr);
   int dev = 0;
-  const bool merge = knob(g_merge) && !a.chunk_fast && (rows % 8 == 0 || rows < 8) &&
-                     (long)a.nchunks * gh <= kMergeMaxStats && hipGetDevice(&dev) == hipSuccess &&
+  // automatic: in the launch when the slots fill the 8 XCDs evenly on a
+  // contiguous cache and the context is long (measured, 32q/8kv/d128 fp32:
+  // step 27.3 -> 26.4 us at n = 16385; at n = 4097 the combine kernel is
+  // 0.1 us faster; fewer slots would leave XCDs idle under the 1-D map, and
+  // batches of short paged sequences merge few chunks cheaply in the
+  // combine kernel: c4 234.8 against 239.3 us).  The matrix-core kernel
+  // keeps the combine kernel (launch_mfma).
+  const int mk = knob(g_merge);
+  const bool want =
+      mk > 0 || (mk < 0 && rows % 8 == 0 && !a.block_table && span >= kMergeAutoSpan);
+  const bool merge = want && !a.chunk_fast && (rows % 8 == 0 || rows < 8) &&
+                     a.nchunks <= kMergeMaxChunks && hipGetDevice(&dev) == hipSuccess &&
                      xcd_ok_cached(dev);
   if (merge) {
     a.ctr = ctr;
     a.xmap = rows % 8 != 0;
-    a.mrg = 2 * a.nchunks * gh + gh;
+    a.mrg = merge_lds_floats(gh);
   }
   return 0;
 }
@@ -2905,6 +2941,9 @@ int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
   a.chunk_fast = Q8 && !PAGED && B == 1;
   int st = plan_launch(a, D, span, GH, nsubs, B, kTile, kWpc, stream, !PAGED);
   if (st) return st;
+  // by default the combine kernel: its four waves per workgroup would fold
+  // the chunks in sequential rounds (c5: 111.7 against 99.5 us per step)
+  if (knob(g_merge) < 0) no_merge(a);
   if (a.mrg && sizeof(float) * (size_t)LdsM(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg).total >
                    65536)
     no_merge(a);
@@ -3147,7 +3186,7 @@ int molot_hip_profile_end(float* attn_ms, float* combine_ms, int* launches, int*
 
 void molot_hip_set_tuning(int wgs_per_cu) { g_wgs_per_cu = wgs_per_cu > 0 ? wgs_per_cu : 0; }
 
-void molot_hip_set_merge(int in_launch) { g_merge = in_launch ? 1 : 0; }
+void molot_hip_set_merge(int in_launch) { g_merge = in_launch < 0 ? -1 : (in_launch ? 1 : 0); }
 
 int molot_hip_rope_apply(float* x, int nheads, int d, int pos, const float* inv_freq,
                          void* stream) {

@@ -1,10 +1,11 @@
 """The split-K merge inside the attention launch (MI355X only).
 
 A split context's chunk partials are merged either by the combine kernel
-launched after the attention kernel (the default), or, with
-molot_hip_set_merge(1), by the workgroup that completes a slot, inside the
-attention launch (where the device dispatches workgroup i to XCD i % 8 and
-a slot's chunks can share an XCD).  Both must give the
+launched after the attention kernel, or by the workgroup that completes a
+slot, inside the attention launch (where the device dispatches workgroup i
+to XCD i % 8 and a slot's chunks can share an XCD).  molot_hip_set_merge
+forces either; by default a contiguous cache whose slots are a multiple of 8
+merges in the launch and everything else uses the combine kernel.  Both must give the
 oracle's result; they differ only in the summation order of the merge.
 The arrival counters the in-launch merge uses must be back at zero after
 every launch, whatever shapes follow one another on a stream.
@@ -42,7 +43,7 @@ def step(p, merge, window=None):
                                                        p.scale, w))
         return host(O), host(q), na, nc
     finally:
-        attn.set_merge(False)  # the library's default
+        attn.set_merge(None)  # the library's default
 
 
 # (nq, nkv, d, pos, window, bf16): slots = nkv * subgroups; 8 | slots keeps
@@ -80,6 +81,30 @@ def test_merge_in_launch_matches_combine(gpu, shape):
     q_rot, _, O_ref, _, _ = oracle_decode(p)
     assert normwise_err(o1, O_ref) < FP32_TOL
     np.testing.assert_allclose(q1, q_rot, atol=2e-6)
+
+
+@pytest.mark.parametrize("shape,in_launch", [((32, 8, 128, 9000, 0, False), True),
+                                              ((64, 16, 64, 8500, 0, False), True),
+                                              ((32, 8, 128, 6000, 0, False), False),
+                                              ((8, 4, 256, 9000, 0, False), False),
+                                              ((24, 12, 128, 9000, 0, False), False),
+                                              ((64, 8, 128, 9000, 0, True), False)],
+                         ids=["8slots", "16slots", "8slots_short", "4slots", "12slots",
+                              "8slots_bf16"])
+def test_merge_default_choice(gpu, shape, in_launch):
+    """The library's default: an fp32 contiguous cache whose slots are a
+    multiple of 8 and whose context spans at least 8192 rows merges in the
+    launch (no combine launch); shorter contexts, other slot counts and the
+    matrix-core kernel use the combine kernel; all match the oracle."""
+    nq, nkv, d, pos, window, bf16 = shape
+    announce(f"default merge {shape}")
+    p = make_decode(nq, nkv, d, pos, window=window, seed=pos + 1, bf16=bf16)
+    o, q, na, nc = step(p, None)
+    assert na == 1
+    assert nc == (0 if in_launch else 1)
+    q_rot, _, O_ref, _, _ = oracle_decode(p)
+    assert normwise_err(o, O_ref) < FP32_TOL
+    np.testing.assert_allclose(q, q_rot, atol=2e-6)
 
 
 def test_merge_counters_across_shapes(gpu):
@@ -139,7 +164,7 @@ def test_merge_paged_batch(gpu):
             outs.append(host(O))
         finally:
             attn.set_split_chunk(0)
-            attn.set_merge(False)
+            attn.set_merge(None)
     assert normwise_err(outs[0], outs[1]) < 1e-6
     _, _, _, O_ref = oracle_paged(pg, inv, scale)
     assert normwise_err(outs[0], O_ref) < FP32_TOL
