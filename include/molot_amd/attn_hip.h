@@ -63,6 +63,7 @@ int64_t molot_hip_q8_block_bytes(int nkv, int d, int page);
 #define MOLOT_ENOTSUP (-95) /* shape the kernels are not built for */
 #define MOLOT_ENOSPC (-28)  /* append beyond the cache capacity */
 #define MOLOT_ENOWS (-16)   /* workspace not sized for a launch being captured in a graph */
+#define MOLOT_E2BIG (-7)    /* partials exceed the no-allocation entry point's scratch */
 
 const char* molot_hip_strerror(int status);
 /* Library version string ("molot_amd <major>.<minor>"). */
@@ -136,6 +137,22 @@ int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void
                           float* O, int nq, int nkv, int d, int slot, int pos,
                           const float* inv_freq, float scale, int window, int kv_dtype,
                           void* stream);
+
+/* molot_hip_decode_step that allocates nothing.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, semantics and kernels as
+ * molot_hip_decode_step; the split-K partials go to a fixed 4 MiB device
+ * array that each device holds from module load to process end, always
+ * merged by the combine kernel.  A shape whose partials exceed it returns
+ * MOLOT_E2BIG (for example 32q/8kv/d128 uses 0.5 MiB at any context under
+ * the automatic chunking; 64q/8kv/d128 bf16 1 MiB).  Every call on a
+ * device shares that array: calls that overlap on one device (two streams,
+ * or two host threads) race and must be ordered by the caller. */
+int molot_hip_decode_step_noalloc(float* q, const float* k_new, const float* v_new, void* K,
+                                  void* V, float* O, int nq, int nkv, int d, int slot, int pos,
+                                  const float* inv_freq, float scale, int window, int kv_dtype,
+                                  void* stream);
 
 /* molot_hip_decode_step with the layer's norms fused in, in forward.h's
  * order (include/molot/forward.h:554-568): each q head and each new k head

@@ -382,6 +382,8 @@ struct AttnArgs {
   float* part_ml;        // [slots][nchunks][GH][2] chunk partial (max, sum)
   float* qrot;           // [slots][GH*D] rotated q for the combine kernel (ROPE)
   int* part_x;           // [slots][nchunks] XCD of each chunk's workgroup (in-launch merge)
+  void* ext_ws;          // host side only: caller-provided workspace (NULL: the library's)
+  int64_t ext_ws_bytes;
   const int32_t* block_table;
   const int32_t* seq_lens;
   const int32_t* pos_arr;
@@ -2687,6 +2689,37 @@ bool xcd_ok_cached(int dev) {
   return it != g_xcd_ok.end() && it->second;
 }
 
+// Scratch of the no-allocation entry point (molot_hip_decode_step_noalloc):
+// the split-K partials of one launch, in device memory that exists from
+// module load to process end on every device the library runs on.  Host
+// code never passes `scratch` itself (on the host it is only a stand-in
+// for the symbol): noalloc_scratch() resolves the device's address once per
+// device with hipGetSymbolAddress and hands out that pointer.  Every call
+// on a device shares its array; the partials are written and read within
+// one step, so nothing needs clearing between calls, and calls that
+// overlap on one device race on it.
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_mu;
+std::map<int, void*> g_scratch_ptr;
+
+int noalloc_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it == g_scratch_ptr.end()) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));  // this device is current
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return (int)hipErrorInvalidSymbol;
+    it = g_scratch_ptr.emplace(dev, ptr).first;
+  }
+  *out = it->second;
+  return 0;
+}
+
 int g_num_cus = 0;
 int num_cus() {
   if (g_num_cus) return g_num_cus;
@@ -2783,7 +2816,18 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   const size_t px = (size_t)rows * a.nchunks;  // ints
   void* ws = nullptr;
   int* ctr = nullptr;
-  const int st = workspace(stream, sizeof(float) * (po + pml + qr + px), &ctr, &ws);
+  const size_t need = sizeof(float) * (po + pml + qr + px);
+  if (a.ext_ws) {
+    // a caller-provided workspace (molot_hip_decode_step_noalloc): no
+    // allocation, and the combine kernel merges (no counters to keep)
+    if ((int64_t)need > a.ext_ws_bytes) return MOLOT_E2BIG;
+    a.part_o = reinterpret_cast<float*>(a.ext_ws);
+    a.part_ml = a.part_o + po;
+    a.qrot = a.part_ml + pml;
+    a.part_x = reinterpret_cast<int*>(a.qrot + qr);
+    return 0;
+  }
+  const int st = workspace(stream, need, &ctr, &ws);
   if (st) return st;
   a.part_o = reinterpret_cast<float*>(ws);
   a.part_ml = a.part_o + po;
@@ -2834,7 +2878,7 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   t_last_chunk = a.chunk;
   a.dynamic = knob(g_dynamic);
   std::lock_guard<std::mutex> plk(g_prof_mu);
-  const bool prof = prof_active(stream);
+  const bool prof = !a.ext_ws && prof_active(stream);
   const bool combine = a.nchunks > 1 && !a.ctr;  // a second launch merges the chunks
   ProfRec pr{nullptr, nullptr, nullptr, nullptr, combine};
   // Workgroup i runs on XCD i % 8 (its L2 and its share of the CUs), and
@@ -3102,6 +3146,9 @@ const char* molot_hip_strerror(int status) {
     case MOLOT_ENOWS:
       return "molot_amd: workspace not sized for this shape on a capturing stream (launch the "
              "shape once before capturing)";
+    case MOLOT_E2BIG:
+      return "molot_amd: the split-K partials of this shape exceed the 4 MiB scratch of "
+             "molot_hip_decode_step_noalloc";
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
   return "molot_amd: unknown status";
@@ -3311,7 +3358,8 @@ int molot_hip_attn_decode_head_win(const float* Q, const void* K, const void* V,
 static int decode_step_impl(float* q, const float* k_new, const float* v_new, void* K, void* V,
                             float* O, int nq, int nkv, int d, int slot, int pos,
                             const float* inv_freq, float scale, int window, int kv_dtype,
-                            const Norms& nm, void* stream) {
+                            const Norms& nm, void* stream, void* ext_ws = nullptr,
+                            int64_t ext_ws_bytes = 0) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   if (!norms_ok(nm)) return MOLOT_EINVAL;
@@ -3349,6 +3397,8 @@ static int decode_step_impl(float* q, const float* k_new, const float* v_new, vo
   a.window = window;
   a.scale = scale;
   a.fold = 1;
+  a.ext_ws = ext_ws;
+  a.ext_ws_bytes = ext_ws_bytes;
   return run_attn<false, true>(a, d, kv_dtype, n - 1 - t0, 1, stream);  // cache rows
 }
 
@@ -3358,6 +3408,17 @@ int molot_hip_decode_step(float* q, const float* k_new, const float* v_new, void
                           void* stream) {
   return decode_step_impl(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale,
                           window, kv_dtype, Norms{}, stream);
+}
+
+int molot_hip_decode_step_noalloc(float* q, const float* k_new, const float* v_new, void* K,
+                                  void* V, float* O, int nq, int nkv, int d, int slot, int pos,
+                                  const float* inv_freq, float scale, int window, int kv_dtype,
+                                  void* stream) {
+  void* ws = nullptr;
+  const int st = noalloc_scratch(&ws);
+  if (st) return st;
+  return decode_step_impl(q, k_new, v_new, K, V, O, nq, nkv, d, slot, pos, inv_freq, scale,
+                          window, kv_dtype, Norms{}, stream, ws, (int64_t)kScratchBytes);
 }
 
 int molot_hip_decode_step_norm(float* q, const float* k_new, const float* v_new, void* K,

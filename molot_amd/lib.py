@@ -22,6 +22,7 @@ EINVAL = -22
 ENOTSUP = -95
 ENOSPC = -28
 ENOWS = -16
+E2BIG = -7
 
 _lock = threading.Lock()
 _lib = None
@@ -42,6 +43,8 @@ _SIGS = {
     "molot_hip_attn_decode_strided": [_P, _P, _P, _P, _I, _I, _I, _I, _I64, _I64, _F, _I, _I,
                                       _I, _P],
     "molot_hip_decode_step": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _I, _P],
+    "molot_hip_decode_step_noalloc": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _F, _I, _I,
+                                      _P],
     "molot_hip_decode_step_norm": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P,
                                    _F, _I, _I, _P],
     "molot_hip_attn_decode_paged": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _F,

@@ -56,6 +56,7 @@ def test_status_strings():
     assert b"invalid" in lib.molot_hip_strerror(L.EINVAL)
     assert b"unsupported" in lib.molot_hip_strerror(L.ENOTSUP)
     assert b"full" in lib.molot_hip_strerror(L.ENOSPC)
+    assert b"4 MiB scratch" in lib.molot_hip_strerror(L.E2BIG)
 
 
 @pytest.mark.parametrize("base,d", [(500000.0, 128), (10000.0, 256), (10000.0, 64)])

@@ -1,0 +1,90 @@
+"""molot_hip_decode_step_noalloc, the entry point that allocates nothing
+(MI355X only).
+
+It is molot_hip_decode_step with the split-K partials in the library's
+fixed device scratch array instead of a workspace it allocates.  Called
+through the C ABI, twice in a row (the second call on a smaller problem, so
+the scratch still holds the first call's partials), it must give the
+existing entry point's result on copies of the same inputs: the same
+appended cache row and rotated q, and the same attention output to the fp32
+bar (1e-5 normwise; only the in-launch merge's summation order can differ),
+which is also the oracle's.  A shape whose partials exceed the scratch is
+refused with MOLOT_E2BIG before anything is launched.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import normwise_err
+from gpu_util import dev, dev_bf16, host, make_decode, oracle_decode
+from molot_amd import attn
+from molot_amd import lib as L
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 1e-5  # the oracle runs on the same bf16 values: summation order only
+
+
+def announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def run(entry, p):
+    """One decode step of problem p through the named C entry point on fresh
+    device copies; returns (rc, O, q, K, V) on the host."""
+    q = dev(p.q)
+    K = dev_bf16(p.K) if p.kv_dtype else dev(p.K)
+    V = dev_bf16(p.V) if p.kv_dtype else dev(p.V)
+    kn, vn, inv = dev(p.k_new), dev(p.v_new), dev(p.inv_freq)
+    O = torch.full((p.nq, p.d), float("nan"), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    rc = getattr(L.load(), entry)(_p(q), _p(kn), _p(vn), _p(K), _p(V), _p(O), p.nq, p.nkv, p.d,
+                                  p.pos, p.pos, _p(inv), float(p.scale), p.window, p.kv_dtype,
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    bits = (lambda t: t.view(torch.int16)) if p.kv_dtype else (lambda t: t)
+    return rc, host(O), host(q), host(bits(K)), host(bits(V))
+
+
+@pytest.mark.parametrize("first,second", [
+    ((32, 8, 128, 16384, 0, False), (32, 8, 128, 3000, 0, False)),
+    ((64, 8, 128, 20000, 0, True), (8, 4, 256, 5000, 700, False)),
+], ids=["c2_then_short", "c5_bf16_then_c3_window"])
+def test_noalloc_matches_decode_step(gpu, first, second):
+    for i, (nq, nkv, d, pos, window, bf16) in enumerate((first, second)):
+        announce(f"noalloc call {i}: nq={nq} nkv={nkv} d={d} pos={pos} window={window} bf16={bf16}")
+        p = make_decode(nq, nkv, d, pos, window=window, seed=pos + 7, bf16=bf16)
+        rc_n, O_n, q_n, K_n, V_n = run("molot_hip_decode_step_noalloc", p)
+        assert rc_n == 0, L.load().molot_hip_strerror(rc_n)
+        rc_e, O_e, q_e, K_e, V_e = run("molot_hip_decode_step", p)
+        assert rc_e == 0
+        np.testing.assert_array_equal(q_n, q_e)  # the rotated q
+        np.testing.assert_array_equal(K_n, K_e)  # the appended row, and nothing else
+        np.testing.assert_array_equal(V_n, V_e)
+        assert np.isfinite(O_n).all()
+        assert normwise_err(O_n, O_e) < FP32_TOL
+        _, _, O_ref, _, _ = oracle_decode(p)
+        assert normwise_err(O_n, O_ref) < (BF16_TOL if bf16 else FP32_TOL)
+
+
+def test_noalloc_refuses_partials_beyond_scratch(gpu):
+    """512 chunks of 32 tokens x 8 slots x 4 heads x 128: 8 MiB of partials
+    against the 4 MiB scratch: MOLOT_E2BIG, nothing launched (O untouched)."""
+    p = make_decode(32, 8, 128, 16384, seed=5)
+    attn.set_split_chunk(32)
+    try:
+        announce("noalloc refusal: forced 32-token chunks at n=16385")
+        rc, O, q, K, _ = run("molot_hip_decode_step_noalloc", p)
+    finally:
+        attn.set_split_chunk(0)
+    assert rc == L.E2BIG
+    assert np.isnan(O).all()
+    np.testing.assert_array_equal(q, p.q)
+    np.testing.assert_array_equal(K[p.pos], p.K[p.pos])  # no append
