@@ -13,7 +13,9 @@ per KV head row); p1|p2|p3 time the layer prefill (p3: d = 256, windowed).
 One step = one layer-step of the hot path through the C ABI
 (molot_hip_decode_step): RoPE of q and k, append of k/v into the cache,
 split-K attention (attn_kernel) and, when the context spans more than one
-chunk, its log-sum-exp combine (combine_kernel), launches on one stream.
+chunk, its log-sum-exp merge: inside the same launch for long fp32 contexts
+(the workgroup that completes a KV head's chunks merges them), else a
+second launch on the stream (combine_kernel).
 Steps cycle over enough layers' KV caches (>= 1 GiB of attended KV in
 total) that the 256 MB Infinity Cache cannot serve the stream: every step
 reads its layer's KV from HBM, as consecutive layers of a real decode do.
@@ -28,7 +30,8 @@ hipExtLaunchKernelGGL while molot_hip_profile_* is on; eager launches on
 the bench stream after the timed region); achieved = the step's algorithmic
 bytes (all of which that kernel moves) / that duration; traffic =
 calibrated rocprofv3 FETCH_SIZE + WRITE_SIZE per launch
-(profiles/traffic.json, per config).
+(profiles/traffic.json, per config, written by molot_amd.rocprof; null when
+that record was measured on another version of the kernel source).
 cpu_baseline = the reference's own attn.h decode step (oracle/_ref, built
 from the reference headers) on the host cores, same workload, bounded sample.
 """
@@ -47,7 +50,64 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
-METRIC = ("KV-stream HBM GB/s (% of peak) + µs/layer, 32q/8kv/d128 @16k ctx, 1 GPU")
+BOX_CPU_SHARE = 16  # host cores a one-GPU job is allotted on the GPU boxes
+
+
+def metric_name(cfg):
+    """BASELINE.json's metric, naming the configuration measured."""
+    kv = {0: "", 1: " bf16", 2: " Q8"}[cfg["kvd"]]  # fp32 KV: BASELINE.json's own wording
+    shape = f"{cfg['nq']}q/{cfg['nkv']}kv/d{cfg['d']}{kv}"
+    if "batch" in cfg:
+        where = f"{cfg['batch']} paged seqs of ctx U[{cfg['lmin']},{cfg['lmax']}]"
+    else:
+        ctx = cfg["pos"]
+        where = f"@{ctx // 1024}k ctx" if ctx % 1024 == 0 else f"@{ctx} ctx"
+        if cfg["window"]:
+            where += f", window {cfg['window']}"
+    return f"KV-stream HBM GB/s (% of peak) + µs/layer, {shape} {where}, 1 GPU"
+
+
+def host_cpu():
+    """The host cores the CPU baseline runs on, and what the machine reports.
+
+    The reference's ThreadPool defaults to every hardware thread
+    (include/molot/thread_pool.h:19-23).  Here the pool takes every core this
+    process may run on (its affinity set, bounded by a cgroup CPU quota if
+    one is set), at most the BOX_CPU_SHARE cores a one-GPU job is allotted on
+    the GPU boxes."""
+    nproc = os.cpu_count() or 1
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, per = f.read().split()[:2]
+            if q != "max":
+                quota = int(q) / int(per)
+    except (OSError, ValueError):
+        pass
+    threads = aff if quota is None else max(1, min(aff, int(quota)))
+    threads = min(threads, BOX_CPU_SHARE)
+    model, llc = "unknown", "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    for idx in (3, 2):
+        try:
+            with open(f"/sys/devices/system/cpu/cpu0/cache/index{idx}/size") as f:
+                llc = f"L{idx} {f.read().strip()}"
+            break
+        except OSError:
+            continue
+    info = {"nproc": nproc, "affinity_cores": aff, "cgroup_cpu_quota": quota,
+            "threads": threads, "cpu_model": model, "llc": llc,
+            "thread_rule": f"every core in the process's affinity set and CPU quota, at most "
+                           f"{BOX_CPU_SHARE} (a one-GPU job's share of the GPU box)"}
+    return threads, info
 COLD_BYTES = 1 << 30  # attended KV cycled per timed pass (> 256 MB Infinity Cache)
 
 CONFIGS = {
@@ -104,7 +164,8 @@ def parse():
                     help="individually timed attention launches for the roofline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="budget of the CPU-baseline sample (0 disables it)")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cores available)")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="0 = every core the process may use, at most the box's 16-core share")
     ap.add_argument("--no-graph", action="store_true", help="time eager launches instead")
     ap.add_argument("--split-chunk", type=int, default=0, help="tokens per chunk (0 = auto)")
     ap.add_argument("--wgs-per-cu", type=int, default=0, help="workgroups per CU (0 = auto)")
@@ -144,7 +205,7 @@ def algorithmic_bytes(nq, nkv, d, n_att, rb):
     return kv, kv + other
 
 
-def kernel_label(d, nq, nkv, kvd, paged, nchunks):
+def kernel_label(d, nq, nkv, kvd, paged, nchunks, combined):
     G = nq // nkv
     pg = "true" if paged else "false"
     if kvd and d in (64, 128):  # the matrix-core kernel (bf16 and Q8 caches)
@@ -155,7 +216,10 @@ def kernel_label(d, nq, nkv, kvd, paged, nchunks):
         gh = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
         t = "float" if kvd == 0 else "bf16"
         s = f"attn_kernel<{d},{gh},{t},paged={pg},rope=true>"
-    return s + (" (then combine_kernel: split-K merge)" if nchunks > 1 else " (single chunk)")
+    if nchunks <= 1:
+        return s + " (single chunk)"
+    return s + (" (then combine_kernel: split-K merge)" if combined else
+                " (split-K chunks merged in the same launch)")
 
 
 def synthetic_q8(st, rows, nkv, d, sigma, np):
@@ -532,12 +596,18 @@ def main() -> int:
     del buf
     log(args, f"streaming-read probe: {read_peak:.0f} GB/s")
 
-    # ---- traffic measured by rocprofv3 PMC runs (committed summary), if present ----
-    traffic = None
+    # ---- traffic measured by rocprofv3 PMC runs (committed summary), if it was
+    # measured on this kernel source (molot_amd.rocprof stamps each entry) ----
+    traffic, traffic_note = None, "no rocprofv3 PMC record for this config"
     try:
+        from molot_amd.rocprof import source_hash
         with open(args.traffic) as f:
-            tr = json.load(f)
-        traffic = tr.get(args.config, {}).get("traffic_bytes_per_launch")
+            ent = json.load(f).get(args.config, {})
+        if ent and ent.get("source_sha256") == source_hash():
+            traffic = ent.get("traffic_bytes_per_launch")
+            traffic_note = "FETCH_SIZE + WRITE_SIZE (profiles/traffic.json, this kernel source)"
+        elif ent:
+            traffic_note = "profiles/traffic.json was measured on another kernel source"
     except (OSError, ValueError, AttributeError):
         pass
 
@@ -546,7 +616,7 @@ def main() -> int:
     config.update({"kv_layers_cycled": wl.layers, "timing": mode, "split_chunks": nch,
                    "chunk_rows": chk})
     out = {
-        "metric": METRIC,
+        "metric": metric_name(cfg),
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -571,12 +641,13 @@ def main() -> int:
         "head_traffic_gbps": round(wl.head_traffic / (ms_per_step * 1e-3) / 1e9, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": kernel_label(cfg["d"], cfg["nq"], cfg["nkv"], kvd, wl.paged, nch),
+            "kernel": kernel_label(cfg["d"], cfg["nq"], cfg["nkv"], kvd, wl.paged, nch, k2_us > 0),
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_source": traffic_note,
             "launch_us": round(k1_us, 3),
             "algorithmic_bytes_per_launch": step_bytes,
             "combine_launch_us": round(k2_us, 3),
@@ -703,7 +774,8 @@ def cpu_baseline_prefill(args, q_h, K_h, V_h, nq, nkv, d, M, N, n0, scale, windo
     import numpy as np
 
     import oracle
-    cores = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+    cores, host = host_cpu()
+    cores = args.cpu_threads or cores
     O = np.empty_like(q_h)
     P = oracle._p
     kind = "reference" if oracle.ref_available() else "port"
@@ -724,7 +796,7 @@ def cpu_baseline_prefill(args, q_h, K_h, V_h, nq, nkv, d, M, N, n0, scale, windo
     tf = flops / (ms * 1e-3) / 1e12
     log(args, f"cpu baseline ({kind}, {cores} threads): {ms:.1f} ms/step -> {tf * 1e3:.1f} GFLOP/s")
     return {"value": round(tf, 5), "unit": "TFLOP/s", "cores": cores, "kind": kind,
-            "ms_per_step": round(ms, 3),
+            "ms_per_step": round(ms, 3), "host": host,
             "sample": f"{steps} calls of attn_prefill_gqa on the {args.config} workload, "
                       f"{el:.1f} s, ThreadPool" if kind == "reference" else
                       f"{steps} calls of the oracle's prefill, {el:.1f} s, OpenMP"}
@@ -757,7 +829,8 @@ def cpu_baseline_contiguous(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window,
     import oracle
     from molot_amd.synth import Stream, bf16_to_f32, f32_to_bf16
 
-    cores = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+    cores, host = host_cpu()
+    cores = args.cpu_threads or cores
     n = pos + 1
     t0 = max(0, pos - window + 1) if window > 0 else 0
     st = Stream(4321)
@@ -810,6 +883,7 @@ def cpu_baseline_contiguous(args, q_h, k_h, v_h, nq, nkv, d, pos, theta, window,
         "cores": cores,
         "kind": kind,
         "ms_per_step": round(ms, 4),
+        "host": host,
         "sample": (f"{steps} layer-steps of {args.config} (rope q/k + append + "
                    f"attn_decode_gqa_cache, n={n}, rows {t0}..{n - 1}) cycling {copies} KV "
                    f"copies of {per_copy / 2**20:.0f} MiB attended, {el:.1f} s; "
@@ -836,7 +910,8 @@ def cpu_baseline_paged(args, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page,
     import oracle
     from molot_amd.synth import bf16_to_f32
 
-    cores = args.cpu_threads or min(16, len(os.sched_getaffinity(0)))
+    cores, host = host_cpu()
+    cores = args.cpu_threads or cores
     B = len(n)
     S = nkv * d
     Kc, Vc = [], []
@@ -888,6 +963,7 @@ def cpu_baseline_paged(args, q_h, k_h, v_h, Kp_h, Vp_h, bt, n, nq, nkv, d, page,
         "cores": cores,
         "kind": kind,
         "ms_per_step": round(ms, 4),
+        "host": host,
         "sample": (f"{steps} batch-steps of {args.config} ({B} sequences, each rope q/k + append + "
                    f"attn_decode_gqa_cache over its contiguous fp32 cache, {fp32_mib:.0f} MiB in "
                    f"all), {el:.1f} s; "

@@ -591,6 +591,13 @@ def test_c4_continuous_batching_paged_bf16(gpu):
     err = normwise_err(O, oO)
     print(f"c4 normwise err {err:.3e}", flush=True)
     assert err < FP32_TOL
+    # against the fp32 originals (the same draws, not rounded to bf16): the
+    # quantization band of the north star, 2e-2
+    Pf = make_paged(64, 32, 8, 128, 512, 8192, bf16=False)
+    _, _, _, Of = oracle_paged(Pf, inv, s)
+    errf = normwise_err(O, Of)
+    print(f"c4 vs fp32 originals {errf:.3e}", flush=True)
+    assert errf < BF16_TOL
 
 
 @pytest.mark.parametrize("bf16", [False, True])
@@ -646,6 +653,8 @@ def test_c4_fused_step(gpu):
     oq, oK, oV, oO = oracle_paged(P, inv, s)
     np.testing.assert_array_equal(Vh, oV)
     assert normwise_err(O, oO) < FP32_TOL
+    _, _, _, Of = oracle_paged(make_paged(64, 32, 8, 128, 512, 8192, bf16=False), inv, s)
+    assert normwise_err(O, Of) < BF16_TOL  # against the fp32 originals
 
 
 @pytest.mark.parametrize("bf16", [False, True])
