@@ -36,6 +36,7 @@
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
@@ -98,6 +99,36 @@ struct KVT<q8_t> {
 template <typename T>
 __device__ __forceinline__ typename KVT<T>::vec load16(const T* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const typename KVT<T>::vec*>(p));
+}
+
+// A 16-byte vector of row elements [e, e + VW) of a head row of dh
+// elements (dh even, possibly not a multiple of VW), read as VW/2 pieces of
+// two elements.  Pieces at or past dh read the row's first two elements
+// instead: they stay inside the row, their K products meet q's zero padding
+// and their V products land in output elements that are never stored.
+template <typename T>
+__device__ __forceinline__ typename KVT<T>::vec load_pad(const T* row, int e, int dh) {
+  using V = typename KVT<T>::vec;
+  constexpr int PB = 2 * (int)sizeof(T);  // bytes per two-element piece
+  V v;
+  const char* r = reinterpret_cast<const char*>(row);
+  if constexpr (PB == 8) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ee = e + 2 * i < dh ? e + 2 * i : 0;
+      const f32x2 x = __builtin_nontemporal_load(reinterpret_cast<const f32x2*>(r + ee * 4));
+      v[2 * i] = x[0];
+      v[2 * i + 1] = x[1];
+    }
+  } else {
+    static_assert(PB == 4, "fp32 or bf16 rows");
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ee = e + 2 * i < dh ? e + 2 * i : 0;
+      v[i] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(r + ee * 2));
+    }
+  }
+  return v;
 }
 
 // Round-to-nearest-even fp32 -> bf16 (include/molot/quant.h:192-198).
@@ -389,6 +420,7 @@ struct AttnArgs {
   const int32_t* pos_arr;
   int64_t tok_stride, head_stride, block_stride;
   int nq, nkv, n, t0, pos, chunk, nchunks, max_blocks, page_shift, window;
+  int dh;                // head dim as stored (< D: the kernel runs padded to its D)
   int dynamic;           // 1: waves claim blocks from a workgroup counter; 0: fixed order
   int chunk_fast;        // 1-D grid, the KV heads of a chunk on one XCD (B = 1; see launch_pair)
   // In-launch merge (see arrive_and_merge): every chunk of a slot runs on one
@@ -548,7 +580,7 @@ __device__ __forceinline__ void lds_barrier() {
 // its sum of squares a group sum, with no LDS round trip and no barrier.
 template <int D, int QPT>
 __device__ __forceinline__ void q_norm_regs(const AttnArgs& a, f32x4 (&qv)[QPT],
-                                            const f32x4 (&qw)[QPT]) {
+                                            const f32x4 (&qw)[QPT], int dh) {
   static_assert(D / 4 <= 64 && 64 % (D / 4) == 0, "a q row within one wave");
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
@@ -556,7 +588,7 @@ __device__ __forceinline__ void q_norm_regs(const AttnArgs& a, f32x4 (&qv)[QPT],
     ss = fmaf(qv[u][1], qv[u][1], ss);
     ss = fmaf(qv[u][2], qv[u][2], ss);
     ss = fmaf(qv[u][3], qv[u][3], ss);
-    const float inv = 1.0f / sqrtf(group_sum<D / 4>(ss) / (float)D + a.eps);
+    const float inv = 1.0f / sqrtf(group_sum<D / 4>(ss) / (float)dh + a.eps);
 #pragma unroll
     for (int e = 0; e < 4; ++e) qv[u][e] = qv[u][e] * inv * qw[u][e];
   }
@@ -591,19 +623,19 @@ struct NewNorms {
 
 template <int D, int NW>
 __device__ __forceinline__ NewNorms new_norms(const AttnArgs& a, const float* ksum,
-                                              const float* vsum) {
+                                              const float* vsum, int dh) {
   NewNorms r{1.f, 1.f};
   if (a.k_norm) {
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < NW; ++k) ss += ksum[k];
-    r.kinv = 1.0f / sqrtf(ss / (float)D + a.eps);
+    r.kinv = 1.0f / sqrtf(ss / (float)dh + a.eps);
   }
   if (a.v_norm) {
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < NW; ++k) ss += vsum[k];
-    r.vinv = 1.0f / sqrtf(ss / (float)(a.nkv * D) + a.eps);
+    r.vinv = 1.0f / sqrtf(ss / (float)(a.nkv * dh) + a.eps);
   }
   return r;
 }
@@ -615,9 +647,10 @@ __device__ __forceinline__ NewNorms new_norms(const AttnArgs& a, const float* ks
 constexpr int kVnPT = 8;
 
 template <int D, int NT>
-__device__ __forceinline__ void v_norm_load(const AttnArgs& a, int b, int tid, float (&vq)[kVnPT]) {
-  const float* vx = a.v_new + (int64_t)b * a.nkv * D;
-  const int nv = a.nkv * D;
+__device__ __forceinline__ void v_norm_load(const AttnArgs& a, int b, int tid, float (&vq)[kVnPT],
+                                            int dh) {
+  const float* vx = a.v_new + (int64_t)b * a.nkv * dh;
+  const int nv = a.nkv * dh;
 #pragma unroll
   for (int u = 0; u < kVnPT; ++u) vq[u] = tid + u * NT < nv ? vx[tid + u * NT] : 0.f;
 }
@@ -625,12 +658,12 @@ __device__ __forceinline__ void v_norm_load(const AttnArgs& a, int b, int tid, f
 // The wave's sum of squares of its threads' shares into vsum[w].
 template <int D, int NT>
 __device__ __forceinline__ void v_norm_share(const AttnArgs& a, int b, int tid, int w, int lane,
-                                             const float (&vq)[kVnPT], float* vsum) {
+                                             const float (&vq)[kVnPT], float* vsum, int dh) {
   float ss = 0.f;
 #pragma unroll
   for (int u = 0; u < kVnPT; ++u) ss = fmaf(vq[u], vq[u], ss);
-  const float* vx = a.v_new + (int64_t)b * a.nkv * D;
-  for (int j = tid + kVnPT * NT; j < a.nkv * D; j += NT) ss = fmaf(vx[j], vx[j], ss);
+  const float* vx = a.v_new + (int64_t)b * a.nkv * dh;
+  for (int j = tid + kVnPT * NT; j < a.nkv * dh; j += NT) ss = fmaf(vx[j], vx[j], ss);
   ss = group_sum<64>(ss);
   if (lane == 0) vsum[w] = ss;
 }
@@ -679,6 +712,31 @@ __device__ __forceinline__ int xcc_id() {
   return (int)(__builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11)) & 15);
 }
 
+// Output element pr of a head group's GH x D tile (head g = pr / D, element
+// j = pr % D) in the caller's [..][dh] rows: its index from qrow0's row, or
+// -1 for the padding (j >= dh) of a padded launch.
+__device__ __forceinline__ int64_t out_index(int64_t qrow0, int pr, int D, int dh) {
+  const int g = pr / D, j = pr - g * D;
+  return j < dh ? (qrow0 + g) * dh + j : -1;
+}
+
+// Stores float4 quad q (elements 4q .. 4q+3 of the GH x D tile) of a head
+// group's output; dh is even, so a quad is whole or half inside a row.
+__device__ __forceinline__ void store_quad(float* o, int64_t qrow0, int q, f32x4 v, int D, int dh) {
+  const int64_t i0 = out_index(qrow0, 4 * q, D, dh);
+  if (i0 < 0) return;
+  if (dh == D || 4 * q % D + 4 <= dh) {
+    if ((i0 & 3) == 0) {
+      *reinterpret_cast<f32x4*>(o + i0) = v;
+    } else {  // dh % 4 == 2: an 8-byte aligned row start
+      *reinterpret_cast<float2*>(o + i0) = float2{v[0], v[1]};
+      *reinterpret_cast<float2*>(o + i0 + 2) = float2{v[2], v[3]};
+    }
+  } else {
+    *reinterpret_cast<float2*>(o + i0) = float2{v[0], v[1]};
+  }
+}
+
 constexpr int kMergeMaxChunks = 4096;  // chunks of a slot merged in the launch
 constexpr int kMergeAutoSpan = 8192;   // rows from which the default merges in the launch
 constexpr int kMergeMaxPhases = 64;    // threads per float4 quad of the output (NT / quads)
@@ -697,7 +755,8 @@ __host__ __device__ constexpr int merge_lds_floats(int gh) { return 2 * kMergeMa
 template <int D, int GH, int NW, int NT, bool ROPE, int RED>
 __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot, int nch,
                                                  int64_t qrow0, const float* qs, float* mst,
-                                                 float* mred, int* flag, int tid, int lane) {
+                                                 float* mred, int* flag, int tid, int lane,
+                                                 int dh) {
   constexpr int P = GH * D;
   wait_vmcnt<0>();  // this thread's partial stores are in the L2
   lds_barrier();
@@ -798,18 +857,21 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
         Ls = fmaf(wq, mst[(q2 * GH + g[0]) * 2 + 1], Ls);
         acc += wq * reinterpret_cast<const f32x4*>(mred)[q2 * QV + tid];
       }
-      reinterpret_cast<f32x4*>(a.o + qrow0 * D)[tid] = acc / Ls + bad;
+      store_quad(a.o, qrow0, tid, acc / Ls + bad, D, dh);
     }
   } else {
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
       const int q4 = NT >= QV ? tid : tid + i * NT;
-      if (act && q4 < QV) reinterpret_cast<f32x4*>(a.o + qrow0 * D)[q4] = o[i] / l[i] + bad;
+      if (act && q4 < QV) store_quad(a.o, qrow0, q4, o[i] / l[i] + bad, D, dh);
     }
   }
   if constexpr (ROPE) {
     if (a.q_out)
-      for (int i = tid; i < P; i += NT) a.q_out[qrow0 * D + i] = qs[i];
+      for (int i = tid; i < P; i += NT) {
+        const int64_t oi = out_index(qrow0, i, D, dh);
+        if (oi >= 0) a.q_out[oi] = qs[i];
+      }
   }
 }
 
@@ -818,7 +880,7 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
                                              const float* red, int RS, const float* qs, int tid,
                                              int lane, bool split, int64_t slot, int c,
                                              int64_t qrow0, int nch, float* mst, float* mred,
-                                             int* flag) {
+                                             int* flag, int dh) {
   constexpr int P = GH * D;
   // Every thread derives the chunk partial of its own output pairs from the
   // wave partials (wave weights e^(m_w - M); waves without rows weigh
@@ -856,11 +918,16 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
   const bool lead = ph == 0;  // phase 0 threads own the chunk partial's outputs
   if (!split) {
 #pragma unroll
-    for (int i = 0; i < PP; ++i)
-      if (lead && pv_[i]) a.o[qrow0 * D + pr_[i]] = po[i] / pl[i];
+    for (int i = 0; i < PP; ++i) {
+      const int64_t oi = lead && pv_[i] ? out_index(qrow0, pr_[i], D, dh) : -1;
+      if (oi >= 0) a.o[oi] = po[i] / pl[i];
+    }
     if constexpr (ROPE) {
       if (a.q_out)
-        for (int i = tid; i < P; i += NT) a.q_out[qrow0 * D + i] = qs[i];
+        for (int i = tid; i < P; i += NT) {
+          const int64_t oi = out_index(qrow0, i, D, dh);
+          if (oi >= 0) a.q_out[oi] = qs[i];
+        }
     }
     return;
   }
@@ -883,7 +950,7 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
   if (a.ctr) {  // in-launch merge: the workgroup completing the slot merges it
     if (tid == 0) a.part_x[slot * a.nchunks + c] = xcc_id();
     arrive_and_merge<D, GH, NW, NT, ROPE, RED>(a, slot, nch, qrow0, qs, mst, mred, flag, tid,
-                                               lane);
+                                               lane, dh);
     return;
   }
   if constexpr (ROPE) {  // the rotated q leaves through the combine kernel
@@ -892,7 +959,7 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
   }
 }
 
-template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
+template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD, typename C>
 __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   using V16 = typename KVT<T>::vec;
   constexpr int VW = C::VW, LPR = C::LPR, NV = C::NV, EPL = C::EPL, RPS = C::RPS;
@@ -906,6 +973,8 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   float* vnew = smem + L.vnew;
   int* misc = reinterpret_cast<int*>(smem + L.misc);
 
+  // PAD: heads of DH < D elements, run as D with q zero-padded (load_pad)
+  const int DH = PAD ? a.dh : D;
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
   // chunk slot z (chunk c = nch - 1 - z, below), (KV head, subgroup) index
@@ -946,7 +1015,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   }
   if (z >= nch) {  // whole workgroup: chunk past this sequence's end (never arrives)
     if (z == 0)    // empty attended range: o = 0 (include/molot/attn.h:162 with no rows)
-      for (int i = tid; i < GH * D; i += NT) a.o[((int64_t)b * a.nq + hq0) * D + i] = 0.f;
+      for (int i = tid; i < GH * DH; i += NT) a.o[((int64_t)b * a.nq + hq0) * DH + i] = 0.f;
     return;
   }
   // Chunks in reverse: the last one, which holds the new token (and with it
@@ -1026,11 +1095,14 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     for (int k = 0; k < KS; ++k) {
       const T* p = row_ptr(Kb, rfirst + min(gmap(rbase + k * RPS + rr), rmax));
 #pragma unroll
-      for (int v = 0; v < NV; ++v) kr[k][v] = load16(p + (v * LPR + s) * VW);
+      for (int v = 0; v < NV; ++v)
+        kr[k][v] = PAD ? load_pad(p, (v * LPR + s) * VW, DH) : load16(p + (v * LPR + s) * VW);
     }
 #pragma unroll
-    for (int k = 0; k < VS; ++k)
-      vr[k] = load16(row_ptr(Vb, rfirst + min(gmap(rbase + k * RPI + rs), rmax)) + cs * VW);
+    for (int k = 0; k < VS; ++k) {
+      const T* p = row_ptr(Vb, rfirst + min(gmap(rbase + k * RPI + rs), rmax));
+      vr[k] = PAD ? load_pad(p, cs * VW, DH) : load16(p + cs * VW);
+    }
   };
   const int nblk = (nrows + RB - 1) / RB;
   // The prologue's own global loads go first: loads retire in order, so
@@ -1039,9 +1111,23 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   constexpr int QPT = (QV + NT - 1) / NT;
   static_assert(D <= NT, "one thread per head-dim element in the prologue");
   f32x4 qv[QPT];
+  // A padded launch reads the q rows (and the q norm weights) at their
+  // stored length DH, in two-element pieces, each selected to 0 past DH:
+  // q's zero padding to D.
+  auto row_quad = [&](const float* base, int i, int64_t stride) -> f32x4 {
+    if constexpr (!PAD) {
+      return reinterpret_cast<const f32x4*>(base)[i];
+    } else {
+      const int g = i / (D / 4), j = 4 * (i - g * (D / 4));
+      const float* r = base + g * stride;
+      const float2 lo = *reinterpret_cast<const float2*>(r + (j < DH ? j : 0));
+      const float2 hi = *reinterpret_cast<const float2*>(r + (j + 2 < DH ? j + 2 : 0));
+      return f32x4{j < DH ? lo.x : 0.f, j < DH ? lo.y : 0.f, j + 2 < DH ? hi.x : 0.f,
+                   j + 2 < DH ? hi.y : 0.f};
+    }
+  };
 #pragma unroll
-  for (int u = 0; u < QPT; ++u)
-    qv[u] = reinterpret_cast<const f32x4*>(a.q + qrow0 * D)[min(tid + u * NT, QV - 1)];
+  for (int u = 0; u < QPT; ++u) qv[u] = row_quad(a.q + qrow0 * DH, min(tid + u * NT, QV - 1), DH);
   float invf = 0.f, knv = 0.f, vnv = 0.f, kwv = 0.f;
   f32x4 qwt[QPT];  // q norm weights of this thread's q elements
   if constexpr (ROPE) {
@@ -1050,19 +1136,20 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     const float* ivp = a.inv_freq ? a.inv_freq : a.q;
     const float* knp = fold ? a.k_new : a.q;
     const float* vnp = fold ? a.v_new : a.q;
-    invf = ivp[min(tid, D / 2 - 1)];
-    knv = knp[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
-    vnv = vnp[((int64_t)b * a.nkv + h) * D + min(tid, D - 1)];
+    invf = ivp[min(tid, DH / 2 - 1)];
+    knv = knp[((int64_t)b * a.nkv + h) * DH + min(tid, DH - 1)];
+    vnv = vnp[((int64_t)b * a.nkv + h) * DH + min(tid, DH - 1)];
+    if (PAD && tid >= DH) knv = vnv = 0.f;  // the padding of the new k and v rows
     if (a.q_norm) {
 #pragma unroll
       for (int u = 0; u < QPT; ++u)
-        qwt[u] = reinterpret_cast<const f32x4*>(a.q_norm)[min(tid + u * NT, QV - 1) % (D / 4)];
+        qwt[u] = row_quad(a.q_norm, min(tid + u * NT, QV - 1) % (D / 4), 0);
     }
-    if (is_new && a.k_norm) kwv = a.k_norm[min(tid, D - 1)];
+    if (is_new && a.k_norm) kwv = a.k_norm[min(tid, DH - 1)];
   }
   float vq[kVnPT];
   const bool vn = ROPE && is_new && a.v_norm;  // uniform over the workgroup
-  if (vn) v_norm_load<D, NT>(a, b, tid, vq);
+  if (vn) v_norm_load<D, NT>(a, b, tid, vq, DH);
   // each wave's first NBUF blocks: w (and w + NW); the rest are claimed
   int bA = w, bB = w + NW;
   load_block(kA, vA, bA * RB);
@@ -1071,7 +1158,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     misc[0] = C::NBUF * NW;  // next block to claim
   }
   if constexpr (ROPE) {
-    if (a.q_norm) q_norm_regs<D, QPT>(a, qv, qwt);
+    if (a.q_norm) q_norm_regs<D, QPT>(a, qv, qwt, DH);
   }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
@@ -1082,7 +1169,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     float* csn = smem + L.cs;
     float* sn = smem + L.sn;
     const bool rot = a.inv_freq != nullptr;  // uniform: no RoPE on a NoPE layer
-    if (rot && tid < D / 2) {
+    if (rot && tid < DH / 2) {
       const float ang = (float)pos * invf;
       double sd, cd;
       sincos((double)ang, &sd, &cd);
@@ -1093,25 +1180,27 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       knew[tid] = knv;
       vnew[tid] = vnv;
     }
-    if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl);
+    if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl, DH);
     if (tid < D) smem[L.nw + tid] = kwv;
     if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
     lds_barrier();
-    for (int i = tid; rot && i < GH * (D / 2); i += NT) {
-      const int g = i / (D / 2), j = i - g * (D / 2);
-      const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
+    // NEOX pairs (j, j + DH/2) of the stored head (attn.h:17-28)
+    const int half = DH / 2;
+    for (int i = tid; rot && i < GH * half; i += NT) {
+      const int g = i / half, j = i - g * half;
+      const float x0 = qs[g * D + j], x1 = qs[g * D + j + half];
       qs[g * D + j] = x0 * csn[j] - x1 * sn[j];
-      qs[g * D + j + D / 2] = x0 * sn[j] + x1 * csn[j];
+      qs[g * D + j + half] = x0 * sn[j] + x1 * csn[j];
     }
     if (is_new) {
       // the appended row as the cache will hold it: normed (as configured),
       // rotated k, k and v rounded to the cache type (stored into the cache
       // after the stream)
-      const NewNorms nn = new_norms<D, NW>(a, smem + L.wm, smem + L.wl);
-      for (int j = tid; j < D / 2; j += NT) {
-        float k0 = knew[j], k1 = knew[j + D / 2];
-        float v0 = vnew[j], v1 = vnew[j + D / 2];
-        nn.apply(a, smem + L.nw, j, D / 2, k0, k1, v0, v1);
+      const NewNorms nn = new_norms<D, NW>(a, smem + L.wm, smem + L.wl, DH);
+      for (int j = tid; j < half; j += NT) {
+        float k0 = knew[j], k1 = knew[j + half];
+        float v0 = vnew[j], v1 = vnew[j + half];
+        nn.apply(a, smem + L.nw, j, half, k0, k1, v0, v1);
         float r0 = rot ? k0 * csn[j] - k1 * sn[j] : k0;
         float r1 = rot ? k0 * sn[j] + k1 * csn[j] : k1;
         if constexpr (sizeof(T) == 2) {
@@ -1121,9 +1210,9 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
           v1 = __uint_as_float((uint32_t)f32_to_bf16(v1) << 16);
         }
         knew[j] = r0;
-        knew[j + D / 2] = r1;
+        knew[j + half] = r1;
         vnew[j] = v0;
-        vnew[j + D / 2] = v1;
+        vnew[j + half] = v1;
       }
     }
   }
@@ -1336,13 +1425,13 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   lds_barrier();
   finish_chunk<D, GH, NW, NT, ROPE, NW * P>(a, wm, wl, red, P, qs, tid, lane, split, slot, c,
                                              qrow0, nch,
-                                    smem + L.mrg, red, misc + 1);
+                                    smem + L.mrg, red, misc + 1, DH);
 
   // ---- 6. the append (subgroup 0; no workgroup reads that slot in this
   // launch).  Last, because nothing may wait for these stores: vmcnt counts
   // stores too, and a wait placed after them for an older load would hold
   // the fold and the merge until the stores complete. ----
-  if (is_new && sub == 0 && tid < D) {
+  if (is_new && sub == 0 && tid < DH) {
     const int slot_row = n - 1;
     int64_t off;
     if constexpr (PAGED) {
@@ -1510,6 +1599,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   constexpr int KL = Q8 ? D / 64 : KK;  // 16-byte loads per row and lane (K or V)
   using E = typename std::conditional<Q8, int8_t, bf16_t>::type;
 
+  constexpr int DH = D;  // never padded
   extern __shared__ float smem[];
   const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg);
   float* qs = smem + L.qs;
@@ -1693,12 +1783,12 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   }
   float vq[kVnPT];
   const bool vn = ROPE && is_new && a.v_norm;  // uniform over the workgroup
-  if (vn) v_norm_load<D, NT>(a, b, tid, vq);
+  if (vn) v_norm_load<D, NT>(a, b, tid, vq, DH);
   int tile = w;  // each wave's first tile; the rest are claimed
   load_tile(tile);
   if (tid == 0) misc[0] = NW;
   if constexpr (ROPE) {
-    if (a.q_norm) q_norm_regs<D, QPT>(a, qv, qwt);
+    if (a.q_norm) q_norm_regs<D, QPT>(a, qv, qwt, DH);
   }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
@@ -1720,7 +1810,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       knew[tid] = knv;
       vnew[tid] = vnv;
     }
-    if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl);
+    if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl, DH);
     if (tid < D) smem[L.nw + tid] = kwv;
     if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
     lds_barrier();
@@ -1731,7 +1821,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       qs[g * D + j + D / 2] = x0 * sn[j] + x1 * csn[j];
     }
     if (is_new) {
-      const NewNorms nn = new_norms<D, NW>(a, smem + L.wm, smem + L.wl);
+      const NewNorms nn = new_norms<D, NW>(a, smem + L.wm, smem + L.wl, DH);
       for (int j = tid; j < D / 2; j += NT) {
         float k0 = knew[j], k1 = knew[j + D / 2];
         float v0 = vnew[j], v1 = vnew[j + D / 2];
@@ -1993,7 +2083,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   lds_barrier();
   finish_chunk<D, GH, NW, NT, ROPE, NW * RS>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c,
                                               qrow0, nch,
-                                    smem + L.mrg, red, misc + 1);
+                                    smem + L.mrg, red, misc + 1, DH);
 
   // ---- the append, last ----
   const bool store_new = is_new && sub == 0 && (Q8 ? w == 0 : tid < D);
@@ -2372,6 +2462,7 @@ struct CombArgs {
   const int32_t* pos_arr;
   int nq, nkv, gh, nsub, d, nchunks, chunk, window, rope, paged;
   int fold;  // the attention launch folded in a new token (its chunks tile n - 1 rows)
+  int dh;    // head dim as stored (d: the partials' padded head dim)
 };
 
 constexpr int kCombThreads = 256;
@@ -2469,9 +2560,11 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
     for (int q2 = 1; q2 < kCombPhases; ++q2) o += pacc[q2 * kCombPairs + pl];
     const int G = a.nq / a.nkv;
     const int h = y / a.nsub, sub = y - h * a.nsub;
-    const int64_t orow = ((int64_t)b * a.nq + h * G + sub * a.gh) * a.d;
-    a.o[orow + pair] = o / s_l;
-    if (a.rope && a.q_out) a.q_out[orow + pair] = a.qrot[(int64_t)slot * P + pair];
+    const int64_t oi = out_index((int64_t)b * a.nq + h * G + sub * a.gh, pair, a.d, a.dh);
+    if (oi >= 0) {
+      a.o[oi] = o / s_l;
+      if (a.rope && a.q_out) a.q_out[oi] = a.qrot[(int64_t)slot * P + pair];
+    }
   }
 }
 
@@ -2521,9 +2614,11 @@ __global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs
     if (u < nch) acc = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(wc), u)), ov[u], acc);
   const int G = a.nq / a.nkv;
   const int h = y / a.nsub, sub = y - h * a.nsub;
-  const int64_t orow = ((int64_t)b * a.nq + h * G + sub * a.gh) * a.d;
-  a.o[orow + pair] = acc / L;
-  if (a.rope && a.q_out) a.q_out[orow + pair] = a.qrot[(int64_t)slot * P + pair];
+  const int64_t oi = out_index((int64_t)b * a.nq + h * G + sub * a.gh, pair, a.d, a.dh);
+  if (oi >= 0) {
+    a.o[oi] = acc / L;
+    if (a.rope && a.q_out) a.q_out[oi] = a.qrot[(int64_t)slot * P + pair];
+  }
 }
 
 __global__ void vexp_kernel(const float* x, float* y, int64_t n) {
@@ -2927,6 +3022,7 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   cb.gh = gh;
   cb.nsub = nsubs;
   cb.d = d;
+  cb.dh = a.dh;
   cb.nchunks = a.nchunks;
   cb.chunk = a.chunk;
   cb.window = a.window;
@@ -2960,7 +3056,7 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   return (int)hipGetLastError();
 }
 
-template <int D, int GH, typename T, bool PAGED, bool ROPE, typename C>
+template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD, typename C>
 int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
   // contiguous caches: 32-row groups dealt round robin (the kernel's gmap)
   int st = plan_launch(a, D, span, GH, nsubs, B, PAGED ? C::RB : 32, 1, stream, !PAGED);
@@ -2969,7 +3065,7 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
                                            a.mrg).total > 65536)
     no_merge(a);  // the merge's statistics do not fit beside the kernel's LDS
   const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED, a.mrg);
-  return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, C>, C::NT, sizeof(float) * (size_t)L.total,
+  return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, PAD, C>, C::NT, sizeof(float) * (size_t)L.total,
                      a, GH, D, nsubs, B, PAGED, ROPE, stream);
 }
 
@@ -2996,42 +3092,50 @@ int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
                      sizeof(float) * (size_t)L.total, a, GH, D, nsubs, B, PAGED, ROPE, stream);
 }
 
-template <int D, int GH, typename T, bool PAGED, bool ROPE>
+template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD>
 int launch_attn(const AttnArgs& a, int span, int nsubs, int B, void* stream) {
-  return launch_cfg<D, GH, T, PAGED, ROPE, typename Tune<D, GH, T>::C>(a, span, nsubs, B, stream);
+  return launch_cfg<D, GH, T, PAGED, ROPE, PAD, typename Tune<D, GH, T>::C>(a, span, nsubs, B,
+                                                                           stream);
 }
 
-template <int D, typename T, bool PAGED, bool ROPE>
+template <int D, typename T, bool PAGED, bool ROPE, bool PAD>
 int dispatch_gh(int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
   switch (gh) {
-    case 1: return launch_attn<D, 1, T, PAGED, ROPE>(a, span, nsubs, B, st);
-    case 2: return launch_attn<D, 2, T, PAGED, ROPE>(a, span, nsubs, B, st);
-    case 4: return launch_attn<D, 4, T, PAGED, ROPE>(a, span, nsubs, B, st);
-    case 8: return launch_attn<D, 8, T, PAGED, ROPE>(a, span, nsubs, B, st);
+    case 1: return launch_attn<D, 1, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
+    case 2: return launch_attn<D, 2, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
+    case 4: return launch_attn<D, 4, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
+    case 8: return launch_attn<D, 8, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
   }
   return MOLOT_EINVAL;
+}
+
+// The vector-ALU kernels are built for D = 64, 128 and 256; any other even
+// head dim d <= 256 runs padded in the next of them (q zero-padded to D,
+// K/V rows read at their stored length d).
+template <int D, typename T, bool PAGED, bool ROPE>
+int dispatch_pad(int d, int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
+  return d == D ? dispatch_gh<D, T, PAGED, ROPE, false>(gh, a, span, nsubs, B, st)
+                : dispatch_gh<D, T, PAGED, ROPE, true>(gh, a, span, nsubs, B, st);
+}
+
+template <typename T, bool PAGED, bool ROPE>
+int dispatch_d(int d, int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
+  if (d <= 64) return dispatch_pad<64, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  if (d <= 128) return dispatch_pad<128, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  return dispatch_pad<256, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
 }
 
 template <bool PAGED, bool ROPE>
 int dispatch_attn(int d, int kv_dtype, int gh, const AttnArgs& a, int span, int nsubs, int B,
                   void* st) {
-  if (kv_dtype == MOLOT_KV_F32) {
-    switch (d) {
-      case 64: return dispatch_gh<64, float, PAGED, ROPE>(gh, a, span, nsubs, B, st);
-      case 128: return dispatch_gh<128, float, PAGED, ROPE>(gh, a, span, nsubs, B, st);
-      case 256: return dispatch_gh<256, float, PAGED, ROPE>(gh, a, span, nsubs, B, st);
-    }
-  } else {
-    switch (d) {
-      case 64: return dispatch_gh<64, bf16_t, PAGED, ROPE>(gh, a, span, nsubs, B, st);
-      case 128: return dispatch_gh<128, bf16_t, PAGED, ROPE>(gh, a, span, nsubs, B, st);
-      case 256: return dispatch_gh<256, bf16_t, PAGED, ROPE>(gh, a, span, nsubs, B, st);
-    }
-  }
-  return MOLOT_ENOTSUP;
+  if (kv_dtype == MOLOT_KV_F32) return dispatch_d<float, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  return dispatch_d<bf16_t, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
 }
 
+// Head dims the kernels are built for (the prefill and the Q8 matrix-core
+// kernels); decode on fp32 and bf16 caches takes any even d up to 256.
 bool supported_d(int d) { return d == 64 || d == 128 || d == 256; }
+bool decode_d(int d) { return d >= 2 && d <= 256 && d % 2 == 0; }
 
 bool valid_kv(int kv_dtype) {
   return kv_dtype == MOLOT_KV_F32 || kv_dtype == MOLOT_KV_BF16 || kv_dtype == MOLOT_KV_Q8;
@@ -3048,8 +3152,8 @@ int64_t q8_block_bytes(int nkv, int d, int page) { return (int64_t)nkv * page * 
 int check_common(int nq, int nkv, int d, int kv_dtype) {
   if (nq <= 0 || nkv <= 0 || nq % nkv != 0) return MOLOT_EINVAL;
   if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
-  if (!supported_d(d)) return MOLOT_ENOTSUP;
-  if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // matrix-core kernels only
+  if (!decode_d(d)) return MOLOT_ENOTSUP;
+  if (kv_dtype == MOLOT_KV_Q8 && d != 64 && d != 128) return MOLOT_ENOTSUP;  // matrix cores only
   return 0;
 }
 
@@ -3103,6 +3207,7 @@ int dispatch_mfma(int gh, const AttnArgs& a, int span, int nsubs, int B, void* s
 
 template <bool PAGED, bool ROPE>
 int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
+  a.dh = d;
   const int G = a.nq / a.nkv;
   const bool q8 = kv_dtype == MOLOT_KV_Q8;
   if (q8 || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128))) {
@@ -3141,7 +3246,9 @@ const char* molot_hip_strerror(int status) {
   switch (status) {
     case MOLOT_OK: return "ok";
     case MOLOT_EINVAL: return "molot_amd: invalid argument";
-    case MOLOT_ENOTSUP: return "molot_amd: unsupported shape (head dim must be 64, 128 or 256)";
+    case MOLOT_ENOTSUP:
+      return "molot_amd: unsupported shape (decode: an even head dim up to 256; Q8 caches: 64 or "
+             "128; prefill: 64, 128 or 256)";
     case MOLOT_ENOSPC: return "molot_amd: KV cache full";
     case MOLOT_ENOWS:
       return "molot_amd: workspace not sized for this shape on a capturing stream (launch the "
@@ -3446,8 +3553,9 @@ static int paged_args(AttnArgs& a, const float* Q, void* K, void* V, float* O,
     return MOLOT_EINVAL;
   if ((int64_t)max_seq_len > (int64_t)max_blocks * page) return MOLOT_EINVAL;
   if (!aligned16(K) || !aligned16(V) || !aligned16(Q) || !aligned16(O)) return MOLOT_EINVAL;
-  const int esz = kv_esz(kv_dtype);
-  if (((int64_t)d * esz) % 16 || !q8_pages_ok(nkv, page, kv_dtype)) return MOLOT_EINVAL;
+  // head rows of the built dims are whole 16-byte vectors; other even dims
+  // run padded, reading two-element pieces (4- or 8-byte aligned)
+  if (!q8_pages_ok(nkv, page, kv_dtype)) return MOLOT_EINVAL;
   int shift = 0;
   while ((1 << shift) < page) ++shift;
   a.q = Q;
@@ -3610,6 +3718,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
                              int kv_dtype, const int32_t* block_row, int page, void* stream) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
+  if (!supported_d(d)) return MOLOT_ENOTSUP;  // the prefill kernels: D = 64, 128, 256
   if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
   if (M == 0) return 0;
   if (N == 0) return zero_out(Om, (int64_t)M * nq * d, (hipStream_t)stream);
@@ -3686,6 +3795,7 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
                              const int32_t* block_row, int page, int max_blocks, void* stream) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
+  if (!supported_d(d)) return MOLOT_ENOTSUP;  // the prefill kernels: D = 64, 128, 256
   Norms nm;
   nm.q = q_norm;
   nm.k = k_norm;

@@ -214,17 +214,17 @@ int main() {
     (void)hipFree(inv_d);
   }
 
-  // ---- 4. unsupported head dim surfaces as std::runtime_error ----
+  // ---- 4. an unsupported (odd) head dim surfaces as std::runtime_error ----
   {
     bool threw = false;
     try {
       float* dq = nullptr;
       molot::amd::check_hip(hipMalloc(&dq, 4 * 96 * 4), "");
-      molot::amd::attn_decode_gqa_cache(dq, dq, dq, dq, 4, 4, 1, 96, 0.1f, 0, 0, *no_pool);
+      molot::amd::attn_decode_gqa_cache(dq, dq, dq, dq, 4, 4, 1, 95, 0.1f, 0, 0, *no_pool);
     } catch (const std::runtime_error& e) {
       threw = std::string(e.what()).find("unsupported") != std::string::npos;
     }
-    CHECK(threw, "head dim 96 did not raise");
+    CHECK(threw, "head dim 95 did not raise");
     std::printf("[%s] unsupported head dim raises\n", threw ? "ok" : "FAIL");
   }
 

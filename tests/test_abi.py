@@ -80,9 +80,15 @@ def test_validation_before_launch():
     # unknown kv dtype
     assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, 128, 0.1, 9, 0,
                                                7, s) == L.EINVAL
-    # head dim without kernels
-    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, 96, 0.1, 9, 0,
-                                               0, s) == L.ENOTSUP
+    # head dims without kernels: decode takes any even d up to 256
+    for d in (97, 258, 0):
+        assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, d, 0.1, 9,
+                                                   0, 0, s) == L.ENOTSUP
+    # prefill only at 64, 128, 256; Q8 caches only at 64, 128
+    assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 96, 0.1, 6, 0, 0,
+                                          s) == L.ENOTSUP
+    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 96, 0.1, 9, 0,
+                                               L.KV_Q8, s) == L.ENOTSUP
     # null output
     assert lib.molot_hip_attn_decode_strided(_p(), _p(), _p(), None, 8, 4, 10, 128, 512, 128,
                                              0.1, 9, 0, 0, s) == L.EINVAL

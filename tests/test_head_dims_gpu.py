@@ -1,0 +1,150 @@
+"""Head dims other than 64, 128 and 256 on the decode path (MI355X only).
+
+The reference takes any head dim (include/molot/attn.h:99, :174 and
+gemm.h:26 run scalar tails; model.h:518 derives qhd from the weights).  The
+vector-ALU decode kernels are built for D = 64, 128 and 256; an even head
+dim d runs padded in the next of them: q is zero-padded to D, the K/V rows
+are read at their stored length d, and every output is written at d.  These
+tests hold every decode entry at such dims to the oracle (1e-5 normwise for
+fp32, and for bf16 on the same bf16 values), covering d % 4 == 2, single and
+split chunks, the in-launch merge and the combine kernel, windows, norms,
+the paged cache and the head-major layout.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import normwise_err
+from gpu_util import dev, dev_bf16, host, make_decode, make_paged, oracle_decode, oracle_paged
+from molot_amd import attn
+from molot_amd.synth import Stream, bf16_to_f32
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+
+
+def announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def run_step(p, qn=None, kn=None, v_norm=False):
+    q = dev(p.q)
+    K = dev_bf16(p.K) if p.kv_dtype else dev(p.K)
+    V = dev_bf16(p.V) if p.kv_dtype else dev(p.V)
+    O = torch.full((p.nq, p.d), float("nan"), device="cuda")
+    attn.decode_step(q, dev(p.k_new), dev(p.v_new), K, V, O, p.nq, p.nkv, p.d, p.pos, p.pos,
+                     dev(p.inv_freq), p.scale, p.window,
+                     q_norm=None if qn is None else dev(qn), k_norm=None if kn is None else dev(kn),
+                     v_norm=v_norm, eps=1e-6)
+    bits = (lambda t: host(t.view(torch.int16)).view(np.uint16)) if p.kv_dtype else host
+    return host(q), bits(K), bits(V), host(O)
+
+
+def check_rows(p, Kh, Vh, oK, oV):
+    """The appended row as the oracle stores it; no other row touched."""
+    np.testing.assert_array_equal(Kh[:p.pos], p.K[:p.pos])
+    np.testing.assert_array_equal(Vh[:p.pos], p.V[:p.pos])
+    if p.kv_dtype:
+        for X, R in ((Kh, oK), (Vh, oV)):
+            dx = np.abs(bf16_to_f32(X[p.pos]) - bf16_to_f32(R[p.pos]))
+            assert np.max(dx) <= 8e-3 * max(1.0, float(np.max(np.abs(bf16_to_f32(R[p.pos])))))
+    else:
+        np.testing.assert_allclose(Kh[p.pos], oK[p.pos], atol=4e-6, rtol=2e-6)
+        np.testing.assert_allclose(Vh[p.pos], oV[p.pos], atol=1e-6, rtol=1e-6)
+
+
+# (nq, nkv, d, pos, window, bf16): slot counts of 8 at pos >= 8192 merge in
+# the launch, others use the combine kernel; pos 10 is one chunk
+STEPS = [
+    (32, 8, 80, 3000, 0, False),
+    (32, 8, 96, 9000, 0, False),     # in-launch merge
+    (32, 8, 112, 2500, 0, False),
+    (16, 4, 160, 2000, 0, False),
+    (8, 4, 192, 5000, 1024, False),  # Gemma-like window
+    (8, 2, 192, 10, 0, False),       # one chunk
+    (32, 8, 66, 9000, 0, False),     # d % 4 == 2, in-launch merge
+    (12, 4, 250, 1500, 300, False),  # d % 4 == 2, D = 256
+    (8, 8, 2, 700, 0, False),        # the smallest even head dim
+    (32, 8, 80, 3000, 0, True),      # bf16 caches of these dims take the vector-ALU kernel
+    (64, 8, 96, 2000, 0, True),
+    (8, 4, 200, 1200, 0, True),
+    (16, 4, 34, 900, 0, True),       # bf16 with d % 8 == 2
+]
+
+
+@pytest.mark.parametrize("shape", STEPS, ids=[f"{s[0]}q{s[1]}kv_d{s[2]}_n{s[3]}"
+                                              f"{'_w' + str(s[4]) if s[4] else ''}"
+                                              f"{'_bf16' if s[5] else ''}" for s in STEPS])
+def test_decode_step_head_dims(gpu, shape):
+    nq, nkv, d, pos, window, bf16 = shape
+    announce(f"decode step {shape}")
+    p = make_decode(nq, nkv, d, pos, window=window, seed=pos + 3 * d, bf16=bf16)
+    q, Kh, Vh, O = run_step(p)
+    oq, _, oO, oK, oV = oracle_decode(p)
+    np.testing.assert_allclose(q, oq, atol=4e-6, rtol=2e-6)
+    check_rows(p, Kh, Vh, oK, oV)
+    assert np.isfinite(O).all()
+    err = normwise_err(O, oO)
+    print(f"d={d}: normwise err {err:.3e}", flush=True)
+    assert err < FP32_TOL
+
+
+@pytest.mark.parametrize("d,bf16", [(80, False), (96, True), (250, False)])
+def test_decode_step_norms_head_dims(gpu, d, bf16):
+    """The layer's norms at the stored head dim (means over d, not D)."""
+    announce(f"decode step with norms d={d} bf16={bf16}")
+    p = make_decode(16, 4, d, 1500, seed=d + 5, bf16=bf16)
+    st = Stream(d)
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    kn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    q, Kh, Vh, O = run_step(p, qn, kn, True)
+    Kc, Vc = p.K.copy(), p.V.copy()
+    oq, _, oO = oracle.decode_step_norm(p.q, p.k_new, p.v_new, Kc, Vc, p.nq, p.nkv, d, p.pos,
+                                        p.pos, qn, kn, True, 1e-6, p.inv_freq, p.scale, 0)
+    np.testing.assert_allclose(q, oq, atol=4e-6, rtol=2e-6)
+    check_rows(p, Kh, Vh, Kc, Vc)
+    assert normwise_err(O, oO) < FP32_TOL
+
+
+@pytest.mark.parametrize("d", [72, 112])
+def test_attention_entries_head_dims(gpu, d):
+    """attn_decode_gqa_cache (token-major) and attn_decode_gqa (head-major)."""
+    announce(f"attention-only entries d={d}")
+    st = Stream(40 + d)
+    nq, nkv, n = 16, 4, 2345
+    Q = st.normal((nq, d))
+    K = st.normal((n, nkv * d))
+    V = st.normal((n, nkv * d))
+    s = 1.0 / math.sqrt(d)
+    O = torch.empty((nq, d), device="cuda")
+    attn.attn_decode_gqa_cache(dev(Q), dev(K), dev(V), O, nq, nkv, n, d, s, n - 1, 0)
+    ref = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, s, n - 1, 0)
+    assert normwise_err(host(O), ref) < FP32_TOL
+    Kh = np.ascontiguousarray(K.reshape(n, nkv, d).transpose(1, 0, 2))
+    Vh = np.ascontiguousarray(V.reshape(n, nkv, d).transpose(1, 0, 2))
+    O2 = torch.empty((nq, d), device="cuda")
+    attn.attn_decode_gqa(dev(Q), dev(Kh), dev(Vh), O2, nq, nkv, n, d, s)
+    assert normwise_err(host(O2), ref) < FP32_TOL
+
+
+@pytest.mark.parametrize("d,bf16", [(96, True), (80, False), (130, True)])
+def test_paged_head_dims(gpu, d, bf16):
+    """A shuffled paged batch at the stored head dim."""
+    announce(f"paged d={d} bf16={bf16}")
+    P = make_paged(7, 16, 4, d, 0, 900, seed=d + 11, bf16=bf16)
+    inv = oracle.rope_inv_freq(10000.0, d)
+    s = 1.0 / math.sqrt(d)
+    B, nq, nkv, page = P["B"], P["nq"], P["nkv"], P["page"]
+    K = dev_bf16(P["Kp"]) if bf16 else dev(P["Kp"])
+    V = dev_bf16(P["Vp"]) if bf16 else dev(P["Vp"])
+    q = dev(P["q"])
+    O = torch.empty((B, nq, d), device="cuda")
+    attn.decode_step_paged(q, dev(P["k_new"]), dev(P["v_new"]), K, V, O, dev(P["bt"].reshape(-1)),
+                           dev(P["n"]), None, B, P["max_blocks"], nq, nkv, d, page, dev(inv), s, 0)
+    oq, oK, oV, oO = oracle_paged(P, inv, s)
+    np.testing.assert_allclose(host(q), oq, atol=4e-6, rtol=2e-6)
+    assert normwise_err(host(O), oO) < FP32_TOL
