@@ -19,8 +19,9 @@
  *                   (no reference counterpart: the reference cache is not
  *                   paged)
  * Head dims: the decode entries take any even d from 2 to 256 for fp32 and
- * bf16 caches (attn.h takes any qhd, attn.h:99, :174); Q8 caches d = 64 or
- * 128; the prefill entries d = 64, 128 or 256 (else MOLOT_ENOTSUP).
+ * bf16 caches (attn.h takes any qhd, attn.h:99, :174) and d = 64, 128 or
+ * 256 for Q8 caches; the prefill entries d = 64, 128 or 256 (Q8: 64 or
+ * 128); anything else returns MOLOT_ENOTSUP before launching.
  * Semantics (include/molot/attn.h:125-177): n = valid slots after the
  * append, window <= 0 attends [0, n), otherwise [t0, n) with
  * t0 = max(0, pos_cur - window + 1); an empty range yields o = 0.

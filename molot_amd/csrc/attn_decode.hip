@@ -975,6 +975,11 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 
   // PAD: heads of DH < D elements, run as D with q zero-padded (load_pad)
   const int DH = PAD ? a.dh : D;
+  // Q8 (D = 256; the matrix-core kernel takes 64 and 128): 16 codes per
+  // 16-byte load, an fp32 scale per K and V row, applied to the row's score
+  // and to its probability in PV
+  constexpr bool Q8 = sizeof(T) == 1;
+  static_assert(!(Q8 && PAD), "Q8 heads are whole 16-byte vectors");
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
   // chunk slot z (chunk c = nch - 1 - z, below), (KV head, subgroup) index
@@ -1053,11 +1058,23 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       return base + (int64_t)t * a.tok_stride + hoff;
     }
   };
+  // Q8: the fp32 scale of row t of head h
+  auto sc_ptr = [&](const T* base, int t) -> const float* {
+    const char* p = reinterpret_cast<const char*>(base) + a.sc_off + h * a.sc_head;
+    if constexpr (PAGED) {
+      const int pg = (t >> a.page_shift) - (tb >> a.page_shift);
+      return reinterpret_cast<const float*>(p + (int64_t)sblk[pg] * a.block_stride) +
+             (t & ((1 << a.page_shift) - 1));
+    } else {
+      return reinterpret_cast<const float*>(p + (int64_t)t * a.tok_stride);
+    }
+  };
   const int s = lane % LPR;    // scores: lane within a K row group
   const int rr = lane / LPR;   // scores: row of the group within a K step
   const int cs = lane % LPR2;  // PV: columns cs*VW .. cs*VW+VW-1
   const int rs = lane / LPR2;  // PV: row within a V step
   V16 kA[KS][NV], vA[VS], kB[KS][NV], vB[VS];
+  float ksA[KS], vsA[VS], ksB[KS], vsB[VS];  // Q8 row scales (unused otherwise)
   // Every wave issues the same sequence of global loads on every path: the
   // compiler counts outstanding loads per path and, where paths merge with
   // different counts, waits for all of them.  Rows past the end (a partial
@@ -1090,18 +1107,30 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       nrows = 32 * last + min(32, rlim - 32 * (c + last * nch));
     }
   }
-  auto load_block = [&](V16 (&kr)[KS][NV], V16 (&vr)[VS], int rbase) {
+  auto load_block = [&](V16 (&kr)[KS][NV], V16 (&vr)[VS], float (&ksr)[KS], float (&vsr)[VS],
+                        int rbase) {
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-      const T* p = row_ptr(Kb, rfirst + min(gmap(rbase + k * RPS + rr), rmax));
+      const int t = rfirst + min(gmap(rbase + k * RPS + rr), rmax);
+      const T* p = row_ptr(Kb, t);
 #pragma unroll
-      for (int v = 0; v < NV; ++v)
-        kr[k][v] = PAD ? load_pad(p, (v * LPR + s) * VW, DH) : load16(p + (v * LPR + s) * VW);
+      for (int v = 0; v < NV; ++v) {
+        if constexpr (PAD)
+          kr[k][v] = load_pad(p, (v * LPR + s) * VW, DH);
+        else
+          kr[k][v] = load16(p + (v * LPR + s) * VW);
+      }
+      if constexpr (Q8) ksr[k] = *sc_ptr(Kb, t);
     }
 #pragma unroll
     for (int k = 0; k < VS; ++k) {
-      const T* p = row_ptr(Vb, rfirst + min(gmap(rbase + k * RPI + rs), rmax));
-      vr[k] = PAD ? load_pad(p, cs * VW, DH) : load16(p + cs * VW);
+      const int t = rfirst + min(gmap(rbase + k * RPI + rs), rmax);
+      const T* p = row_ptr(Vb, t);
+      if constexpr (PAD)
+        vr[k] = load_pad(p, cs * VW, DH);
+      else
+        vr[k] = load16(p + cs * VW);
+      if constexpr (Q8) vsr[k] = *sc_ptr(Vb, t);
     }
   };
   const int nblk = (nrows + RB - 1) / RB;
@@ -1152,8 +1181,8 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   if (vn) v_norm_load<D, NT>(a, b, tid, vq, DH);
   // each wave's first NBUF blocks: w (and w + NW); the rest are claimed
   int bA = w, bB = w + NW;
-  load_block(kA, vA, bA * RB);
-  if constexpr (C::NBUF == 2) load_block(kB, vB, bB * RB);
+  load_block(kA, vA, ksA, vsA, bA * RB);
+  if constexpr (C::NBUF == 2) load_block(kB, vB, ksB, vsB, bB * RB);
   if (tid == 0) {
     misc[0] = C::NBUF * NW;  // next block to claim
   }
@@ -1254,7 +1283,8 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     if (lane == 0) v = atomicAdd(&misc[0], 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
-  auto consume = [&](const V16 (&kr)[KS][NV], const V16 (&vr)[VS], int rbase) {
+  auto consume = [&](const V16 (&kr)[KS][NV], const V16 (&vr)[VS], const float (&ksr)[KS],
+                     const float (&vsr)[VS], int rbase) {
     // scores of this lane group's rows
     float sc[KS][GH];
     float bmax[GH];
@@ -1277,7 +1307,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       const bool valid = rbase + k * RPS + rr < nrows;
 #pragma unroll
       for (int g = 0; g < GH; ++g) {
-        const float t = group_sum<LPR>(d[g]) * a.scale;
+        const float t = group_sum<LPR>(d[g]) * (Q8 ? a.scale * ksr[k] : a.scale);
         sc[k][g] = valid ? t : -INFINITY;
         bmax[g] = fmaxf(bmax[g], sc[k][g]);
       }
@@ -1312,8 +1342,9 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int g = 0; g < GH; ++g) {
         l_run[g] += p[g];
+        const float pv = Q8 ? p[g] * vsr[k] : p[g];  // Q8: codes times the V row's scale
 #pragma unroll
-        for (int e = 0; e < VW; ++e) acc[g][e] = fmaf(p[g], x[e], acc[g][e]);
+        for (int e = 0; e < VW; ++e) acc[g][e] = fmaf(pv, x[e], acc[g][e]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -1332,39 +1363,68 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     // one block in flight: score it, claim and load the next
     while (bA < nblk) {
       const int nx = claim();
-      consume(kA, vA, bA * RB);
+      consume(kA, vA, ksA, vsA, bA * RB);
       bA = nx;
-      if (bA < nblk) load_block(kA, vA, bA * RB);
+      if (bA < nblk) load_block(kA, vA, ksA, vsA, bA * RB);
     }
   } else if (bA < nblk) {
     if (bB >= nblk) {
-      consume(kA, vA, bA * RB);
+      consume(kA, vA, ksA, vsA, bA * RB);
     } else {
       for (;;) {
         int nx = claim();
         wait_vmcnt<LB>();
-        consume(kA, vA, bA * RB);
+        consume(kA, vA, ksA, vsA, bA * RB);
         if (nx >= nblk) {
-          consume(kB, vB, bB * RB);
+          consume(kB, vB, ksB, vsB, bB * RB);
           break;
         }
         bA = nx;
-        load_block(kA, vA, bA * RB);
+        load_block(kA, vA, ksA, vsA, bA * RB);
         nx = claim();
         wait_vmcnt<LB>();
-        consume(kB, vB, bB * RB);
+        consume(kB, vB, ksB, vsB, bB * RB);
         if (nx >= nblk) {
-          consume(kA, vA, bA * RB);
+          consume(kA, vA, ksA, vsA, bA * RB);
           break;
         }
         bB = nx;
-        load_block(kB, vB, bB * RB);
+        load_block(kB, vB, ksB, vsB, bB * RB);
       }
     }
   }
 
   // ---- 3. the new token, folded in by wave 0 from LDS (its append to the
   // cache comes last, below) ----
+  // Q8: wave 0 quantizes the k and v rows as the cache will hold them (the
+  // reference quantizer, quant.h:34-50: s = absmax / 127, codes round(x/s))
+  // and leaves code * s in LDS for the fold
+  [[maybe_unused]] int kcode[Q8 ? D / 64 : 1], vcode[Q8 ? D / 64 : 1];
+  [[maybe_unused]] float kscale = 0.f, vscale = 0.f;
+  if constexpr (Q8) {
+    if (is_new && w == 0) {
+      constexpr int EPL = D / 64;
+      float kx[EPL], vx[EPL];
+      float ka = 0.f, va = 0.f;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        kx[e] = knew[lane + 64 * e];
+        vx[e] = vnew[lane + 64 * e];
+        ka = fmaxf(ka, fabsf(kx[e]));
+        va = fmaxf(va, fabsf(vx[e]));
+      }
+      kscale = q8_scale(group_max<64>(ka));
+      vscale = q8_scale(group_max<64>(va));
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        kcode[e] = q8_code(kx[e], kscale);
+        vcode[e] = q8_code(vx[e], vscale);
+        knew[lane + 64 * e] = (float)kcode[e] * kscale;
+        vnew[lane + 64 * e] = (float)vcode[e] * vscale;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");  // the fold reads other lanes' rows
+    }
+  }
   if (is_new && w == 0) {
     // LDS reads first, unconditional and vector-wide: the lanes of PV row 0
     // add the row's values, the others add 0 (a select per element, not a
@@ -1431,17 +1491,29 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   // launch).  Last, because nothing may wait for these stores: vmcnt counts
   // stores too, and a wait placed after them for an older load would hold
   // the fold and the merge until the stores complete. ----
-  if (is_new && sub == 0 && tid < DH) {
+  if (is_new && sub == 0 && (Q8 ? w == 0 : tid < DH)) {
     const int slot_row = n - 1;
-    int64_t off;
+    int64_t off, soff;  // element (Q8: byte) offset of the row; Q8: of its scale
     if constexpr (PAGED) {
       const int64_t blk = a.block_table[(int64_t)b * a.max_blocks + (slot_row >> a.page_shift)];
-      off = blk * a.block_stride + hoff +
-            (int64_t)(slot_row & ((1 << a.page_shift) - 1)) * a.tok_stride;
+      const int sl = slot_row & ((1 << a.page_shift) - 1);
+      off = blk * a.block_stride + hoff + (int64_t)sl * a.tok_stride;
+      soff = blk * a.block_stride + a.sc_off + h * a.sc_head + 4 * sl;
     } else {
       off = (int64_t)slot_row * a.tok_stride + hoff;
+      soff = (int64_t)slot_row * a.tok_stride + a.sc_off + h * a.sc_head;
     }
-    if constexpr (sizeof(T) == 2) {  // exact bf16 values: the rounding returns their bits
+    if constexpr (Q8) {
+#pragma unroll
+      for (int e = 0; e < D / 64; ++e) {
+        reinterpret_cast<int8_t*>(a.k)[off + lane + 64 * e] = (int8_t)kcode[e];
+        reinterpret_cast<int8_t*>(a.v)[off + lane + 64 * e] = (int8_t)vcode[e];
+      }
+      if (lane == 0) {
+        *reinterpret_cast<float*>(reinterpret_cast<char*>(a.k) + soff) = kscale;
+        *reinterpret_cast<float*>(reinterpret_cast<char*>(a.v) + soff) = vscale;
+      }
+    } else if constexpr (sizeof(T) == 2) {  // exact bf16 values: the rounding returns their bits
       reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
       reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
     } else {
@@ -3129,6 +3201,8 @@ template <bool PAGED, bool ROPE>
 int dispatch_attn(int d, int kv_dtype, int gh, const AttnArgs& a, int span, int nsubs, int B,
                   void* st) {
   if (kv_dtype == MOLOT_KV_F32) return dispatch_d<float, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  if (kv_dtype == MOLOT_KV_Q8)  // D = 256 (check_common; 64 and 128 take the matrix cores)
+    return dispatch_gh<256, q8_t, PAGED, ROPE, false>(gh, a, span, nsubs, B, st);
   return dispatch_d<bf16_t, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
 }
 
@@ -3153,7 +3227,7 @@ int check_common(int nq, int nkv, int d, int kv_dtype) {
   if (nq <= 0 || nkv <= 0 || nq % nkv != 0) return MOLOT_EINVAL;
   if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
   if (!decode_d(d)) return MOLOT_ENOTSUP;
-  if (kv_dtype == MOLOT_KV_Q8 && d != 64 && d != 128) return MOLOT_ENOTSUP;  // matrix cores only
+  if (kv_dtype == MOLOT_KV_Q8 && !supported_d(d)) return MOLOT_ENOTSUP;  // Q8: 64, 128, 256
   return 0;
 }
 
@@ -3210,9 +3284,9 @@ int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
   a.dh = d;
   const int G = a.nq / a.nkv;
   const bool q8 = kv_dtype == MOLOT_KV_Q8;
-  if (q8 || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128))) {
+  if ((q8 && d != 256) || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128))) {
     // up to 16 q heads of a group share each K/V tile on the MFMA columns;
-    // Q8 caches (D = 64, 128: checked by the entry points) only run here
+    // Q8 caches of D = 64, 128 run here, D = 256 on the vector-ALU kernel
     const int gh = G % 16 == 0 ? 16 : pick_gh(G);
     const int nsubs = G / gh;
     if (q8)
@@ -3247,8 +3321,8 @@ const char* molot_hip_strerror(int status) {
     case MOLOT_OK: return "ok";
     case MOLOT_EINVAL: return "molot_amd: invalid argument";
     case MOLOT_ENOTSUP:
-      return "molot_amd: unsupported shape (decode: an even head dim up to 256; Q8 caches: 64 or "
-             "128; prefill: 64, 128 or 256)";
+      return "molot_amd: unsupported shape (decode: an even head dim up to 256, Q8 caches 64, "
+             "128 or 256; prefill: 64, 128 or 256, Q8 caches 64 or 128)";
     case MOLOT_ENOSPC: return "molot_amd: KV cache full";
     case MOLOT_ENOWS:
       return "molot_amd: workspace not sized for this shape on a capturing stream (launch the "
@@ -3719,6 +3793,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   if (!supported_d(d)) return MOLOT_ENOTSUP;  // the prefill kernels: D = 64, 128, 256
+  if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // Q8 prefill: 64, 128
   if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
   if (M == 0) return 0;
   if (N == 0) return zero_out(Om, (int64_t)M * nq * d, (hipStream_t)stream);
@@ -3796,6 +3871,7 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   if (!supported_d(d)) return MOLOT_ENOTSUP;  // the prefill kernels: D = 64, 128, 256
+  if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // Q8 prefill: 64, 128
   Norms nm;
   nm.q = q_norm;
   nm.k = k_norm;

@@ -134,8 +134,8 @@ def test_q8_validation_before_launch():
     lib = L.load()
     s = ctypes.c_void_p(0)
     Q8 = L.KV_Q8
-    # d = 256: no Q8 kernels
-    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 256, 0.1, 9, 0,
+    # Q8 caches: d = 64, 128, 256 for decode
+    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 192, 0.1, 9, 0,
                                                Q8, s) == L.ENOTSUP
     # element strides instead of the token-major Q8 byte layout
     assert lib.molot_hip_attn_decode_strided(_p(), _p(), _p(), _p(), 8, 2, 10, 128, 256, 128,
@@ -147,12 +147,12 @@ def test_q8_validation_before_launch():
     assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4, 4, 8,
                                            1, 64, 2, 0.1, 0, Q8, s) == L.EINVAL
     assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 256, 0.1, 6, 0,
-                                          Q8, s) == L.ENOTSUP
+                                          Q8, s) == L.ENOTSUP  # Q8 prefill: 64, 128
     # the RoPE/append entries write only rows the attention entries read back
-    assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 2, 256, 5, 5, _p(), Q8,
+    assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 2, 192, 5, 5, _p(), Q8,
                                      s) == L.ENOTSUP
     assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,
-                                           8, 2, 256, 16, _p(), Q8, s) == L.ENOTSUP
+                                           8, 2, 192, 16, _p(), Q8, s) == L.ENOTSUP
     assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,
                                            8, 1, 64, 2, _p(), Q8, s) == L.EINVAL
     assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,

@@ -78,6 +78,9 @@ def assert_rows_close(got, ref, nkv, d):
     (32, 2, 64, 50, 49, 0),          # G = 16, one short chunk
     (32, 8, 128, 20000, 19999, 4096),
     (8, 2, 128, 1, 0, 0),            # a single row
+    (8, 4, 256, 32769, 32768, 1024),  # Gemma-shaped c3 layer: d = 256 on the vector-ALU kernel
+    (16, 2, 256, 3000, 2999, 0),     # d = 256, G = 8
+    (8, 8, 256, 40, 39, 0),          # d = 256, one chunk
 ])
 def test_q8_decode_vs_oracle(gpu, nq, nkv, d, n, pos, window):
     announce(f"q8 decode {nq}/{nkv}/{d} n={n} window={window}")
@@ -157,9 +160,8 @@ def test_q8_split_plans_agree(gpu):
     (128, 5000, 1024, True),
     (128, 2000, 1, False),   # the window holds the new token only
 ])
-def test_q8_decode_step_vs_oracle(gpu, d, pos, window, norms):
-    announce(f"q8 decode_step d={d} pos={pos} window={window} norms={norms}")
-    nq, nkv = 32, 8
+def test_q8_decode_step_vs_oracle(gpu, d, pos, window, norms, nq=32, nkv=8):
+    announce(f"q8 decode_step {nq}/{nkv}/{d} pos={pos} window={window} norms={norms}")
     st = Stream(pos + d + window)
     q = st.normal((nq, d), 2.0)
     k = st.normal((nkv, d), 2.0)
@@ -197,6 +199,16 @@ def test_q8_decode_step_vs_oracle(gpu, d, pos, window, norms):
           flush=True)
     assert err < TOL
     assert normwise_err(host(O), oO) < 1e-3  # a code off by one moves o by ~1e-5 of its scale
+
+
+@pytest.mark.parametrize("nq,nkv,pos,window,norms", [
+    (8, 4, 0, 0, False),        # RoPE is the identity: every byte exact
+    (8, 4, 32768, 1024, False),  # the Gemma-shaped c3 layer over a Q8 cache
+    (16, 4, 3000, 0, True),
+])
+def test_q8_decode_step_d256_vs_oracle(gpu, nq, nkv, pos, window, norms):
+    """d = 256 Q8 caches (the vector-ALU kernel quantizes the new row)."""
+    test_q8_decode_step_vs_oracle(gpu, 256, pos, window, norms, nq=nq, nkv=nkv)
 
 
 def test_q8_rope_append_vs_oracle(gpu):
@@ -292,7 +304,7 @@ def oracle_paged_q8(P, inv, scale, window=0, qn=None, kn=None, v_norm=False):
     return q, Kp, Vp, O
 
 
-@pytest.mark.parametrize("d,window", [(128, 0), (64, 0), (128, 300)])
+@pytest.mark.parametrize("d,window", [(128, 0), (64, 0), (128, 300), (256, 0), (256, 300)])
 def test_q8_paged_attention_vs_oracle(gpu, d, window):
     announce(f"q8 paged attention d={d} window={window}")
     P = q8_paged_problem(11, 32, 8, d, 0, 2500, seed=20 + d + window)
@@ -466,11 +478,11 @@ def test_q8_prefill_step_vs_oracle(gpu):
 
 def test_q8_errors(gpu):
     st = Stream(60)
-    Q = dev(st.normal((8, 256)))
-    O = torch.empty((8, 256), device="cuda")
-    C = torch.zeros(10 * oracle.q8_row_bytes(2, 256), dtype=torch.uint8, device="cuda")
-    with pytest.raises(MolotHipError) as e:  # d = 256: no Q8 kernel
-        attn.attn_decode_gqa_cache(Q, C, C, O, 8, 2, 10, 256, 0.1, 9, 0)
+    Q = dev(st.normal((8, 96)))
+    O = torch.empty((8, 96), device="cuda")
+    C = torch.zeros(10 * oracle.q8_row_bytes(2, 96), dtype=torch.uint8, device="cuda")
+    with pytest.raises(MolotHipError) as e:  # Q8 caches: d = 64, 128, 256 only
+        attn.attn_decode_gqa_cache(Q, C, C, O, 8, 2, 10, 96, 0.1, 9, 0)
     assert e.value.status == ENOTSUP
     Q = dev(st.normal((8, 64)))
     O = torch.empty((8, 64), device="cuda")
