@@ -698,6 +698,9 @@ __device__ __forceinline__ void v_norm_share(const AttnArgs& a, int b, int tid, 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_rsrc(const float* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7FFFFFFF, 0x00020000);
 }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_rsrc_i(const int* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(base), 0, 0x7FFFFFFF, 0x00020000);
+}
 // Loads at a byte offset of a resource, missing the L1 (cache policy sc0).
 __device__ __forceinline__ f32x4 ld_l2x4(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 1));
@@ -750,7 +753,10 @@ __host__ __device__ constexpr int merge_lds_floats(int gh) { return 2 * kMergeMa
 // ph = t / QV; it folds chunks ph, ph + PH, ph + 2*PH, ... with a running
 // log-sum-exp, kMergeRound chunks' loads in flight at a time and only the
 // chunks that exist loaded.  The PH phases of a quad then merge once
-// through LDS: their (max, sum) per head at mst, their o at mred.
+// through LDS: their (max, sum) per head at mst, their o at mred.  Wave 0
+// alone reads the chunks' XCD records (lane c: chunks c, c + 64, ...): with
+// a record load per chunk in every thread the merge took 0.4 us longer
+// (32q/8kv/d128 fp32, n = 16385).
 // RED: floats of LDS at mred (the phase sums: PH*P floats).
 template <int D, int GH, int NW, int NT, bool ROPE, int RED>
 __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot, int nch,
@@ -769,8 +775,6 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
   }
   lds_barrier();
   if (!flag[0]) return;  // uniform over the workgroup
-  const int my_xcc = xcc_id();
-  bool other_xcd = false;
 
   constexpr int QV = P / 4;                     // float4 quads of the slot's output
   // phases per quad: as many as the threads allow and the phase sums' LDS holds
@@ -805,7 +809,6 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
         if (cc < nch) {
           st[i][u] = ld_l2x2(rm, 8 * (cc * GH + g[i]));
           ov[i][u] = ld_l2x4(ro, 16 * (cc * QV + qd[i]));
-          if (i == 0) other_xcd |= a.part_x[slot * a.nchunks + cc] != my_xcc;
         } else {
           st[i][u] = float2{-INFINITY, 0.f};
           ov[i][u] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -831,7 +834,14 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
   }
   // The hand-off above holds only if every chunk of the slot ran on this
   // XCD (one L2): otherwise the output is NaN, never a silently stale merge.
-  if (other_xcd) flag[1] = 1;
+  if (tid < 64) {
+    const __amdgpu_buffer_rsrc_t rx = l2_rsrc_i(a.part_x + slot * a.nchunks);
+    const int my_xcc = xcc_id();
+    bool other_xcd = false;
+    for (int cc = lane; cc < nch; cc += 64)
+      other_xcd |= __builtin_amdgcn_raw_buffer_load_b32(rx, 4 * cc, 0, 1) != my_xcc;
+    if (__builtin_amdgcn_ballot_w64(other_xcd) != 0 && lane == 0) flag[1] = 1;
+  }
   lds_barrier();
   const float bad = flag[1] ? __builtin_nanf("") : 0.f;
   if constexpr (PH > 1) {
