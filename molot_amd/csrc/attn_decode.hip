@@ -885,7 +885,7 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
   }
 }
 
-template <int D, int GH, int NW, int NT, bool ROPE, int RED>
+template <int D, int GH, int NW, int NT, bool ROPE, int RED, bool XSW = false>
 __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm, const float* wl,
                                              const float* red, int RS, const float* qs, int tid,
                                              int lane, bool split, int64_t slot, int c,
@@ -917,10 +917,14 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
     const float e_l = lane < NW && mw_l != -INFINITY ? softmax_exp(mw_l - m) : 0.f;
     const float l = group_sum<NW <= 16 ? 16 : 64>(lane < NW ? e_l * wl[lane * GH + g] : 0.f);
     float o = 0.f;
+    // XSW: head g's element j at g*D + (j ^ 4*(g % 8)) (the matrix-core
+    // kernel's conflict-free layout)
+    const int ri =
+        !pv_[i] ? 0 : XSW ? g_[i] * D + ((pr_[i] - g_[i] * D) ^ (4 * (g_[i] & 7))) : pr_[i];
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww)
       o = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(e_l), ww)),
-               red[ww * RS + (pv_[i] ? pr_[i] : 0)], o);
+               red[ww * RS + ri], o);
     po[i] = o;
     pm[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
     pl[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(l)));
@@ -1555,12 +1559,11 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 //           the order tau(g, e) = 16*(e/4) + 4g + e%4 (g = l/16): exactly the
 //           8 probabilities lane l already holds, so P is the B operand as it
 //           stands (again as bf16 hi + mid + lo).  V is staged in LDS
-//           (row-major, 32-byte segments XOR-swizzled by row so the
-//           transposed reads below hit distinct banks) and read back with
-//           ds_read_b64_tr_b16: lane l reads 8 bytes of row l/4 (+16) at
-//           column 16*dt + 4*(l%4), and the transpose hands lane i of each
-//           16-lane group element i%4 of lane 4e+i/4's read as slot e, i.e.
-//           V[tau(g, e)][16*dt + i]: the A operand.
+//           (row-major, 16-byte units XOR-swizzled by row: vt_off) and read
+//           back with ds_read_b64_tr_b16: lane l reads 8 bytes of row l/4
+//           (+16) at column 16*dt + 4*(l%4), and the transpose hands lane i of
+//           each 16-lane group element i%4 of lane 4e+i/4's read as slot e,
+//           i.e. V[tau(g, e)][16*dt + i]: the A operand.
 // Prologue, new token and chunk output are those of attn_kernel.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -1608,6 +1611,24 @@ struct LdsM {
     total = o;
   }
 };
+
+// Byte offset of 16-byte unit ch (elements 8ch .. 8ch+7) of staged V row r:
+// unit ch of the row is stored at unit ch ^ f(r).  Measured on MI355X
+// (SQ_LDS_BANK_CONFLICT of each access pattern alone), a 16-byte LDS store
+// serves 8 lanes a cycle and conflicts unless their addresses fall in
+// distinct 16-byte slots mod 128 bytes, and ds_read_b64_tr_b16 serves 32
+// lanes a cycle, distinct 8-byte slots mod 256 bytes.  The stores put rows
+// r0 .. r0+7 of one unit ch in 8 lanes: distinct when the low 3 bits of f
+// run over 8 values; a transposed read takes units 2dt and 2dt+1 of 8 rows:
+// 16 distinct units of a 256-byte span when f >> 1 runs over 8 values.
+// D = 128 (16 units a row): f(r) = 2(r%8) + (r/4)%2 meets both; D = 64
+// (8 units, 2 rows per 256 bytes): f(r) = r%8.  The 32-byte-segment swizzle
+// this replaces conflicted 2-way on every store.
+template <int D>
+__device__ __forceinline__ int vt_off(int r, int ch) {
+  const int f = D == 128 ? (((r & 7) << 1) | ((r >> 2) & 1)) : (r & 7);
+  return r * (2 * D) + 16 * (ch ^ f);
+}
 
 // x = hi + mid + lo in bf16 (round to nearest even at each step); the three
 // pieces carry the full fp32 significand.
@@ -1675,8 +1696,6 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   constexpr int NW = kMfmaWaves, NT = kMfmaThreads;
   constexpr int KK = D / 32;  // k-steps of the score product
   constexpr int DT = D / 16;  // 16-row blocks of O^T
-  constexpr int NSEG = D / 16;  // 32-byte segments of a staged V row
-  constexpr int RBY = 2 * D;  // bytes of a staged V row
   constexpr int RS = kTile * D / 2;  // floats of a wave's LDS region
   constexpr int KL = Q8 ? D / 64 : KK;  // 16-byte loads per row and lane (K or V)
   using E = typename std::conditional<Q8, int8_t, bf16_t>::type;
@@ -1965,7 +1984,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   float* scw = smem + L.sc + w * (2 * kTile);  // Q8: this wave's scale slots
   while (tile < ntiles) {
     // V rows into this wave's LDS region (lane: row 16u + l%16, 16-byte
-    // chunks l/16 + 4q), 32-byte segment s of row r stored at s ^ (r % NSEG)
+    // units l/16 + 4q), swizzled by vt_off
     f32x4 sk4[2], sv4[2];  // Q8: scales of accumulator rows 16u + 4*(l/16) + r
     if constexpr (Q8) {
 #pragma unroll
@@ -1976,9 +1995,8 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
           const int r = 16 * u + m16, s = g4 + 4 * j;
           u32x4 lo, hi;
           i8x16_to_bf16(vr[u][j], lo, hi);
-          char* dst = vt + r * RBY + 32 * (s ^ (r & (NSEG - 1)));
-          *reinterpret_cast<u32x4*>(dst) = lo;
-          *reinterpret_cast<u32x4*>(dst + 16) = hi;
+          *reinterpret_cast<u32x4*>(vt + vt_off<D>(r, 2 * s)) = lo;
+          *reinterpret_cast<u32x4*>(vt + vt_off<D>(r, 2 * s + 1)) = hi;
         }
       if (g4 == 0) {
 #pragma unroll
@@ -2001,8 +2019,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 #pragma unroll
         for (int q = 0; q < KK; ++q) {
           const int r = 16 * u + m16, ch = g4 + 4 * q;
-          *reinterpret_cast<u32x4*>(vt + r * RBY + 32 * ((ch >> 1) ^ (r & (NSEG - 1))) +
-                                    16 * (ch & 1)) = vr[u][q];
+          *reinterpret_cast<u32x4*>(vt + vt_off<D>(r, ch)) = vr[u][q];
         }
     }
     // scores of the two 16-row halves
@@ -2085,7 +2102,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
         const int r = (lane >> 2) + 16 * u;
         t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
             (__attribute__((address_space(3))) i16x4_t*)(
-                vt + r * RBY + 32 * (dt ^ (r & (NSEG - 1))) + 8 * (lane & 3)));
+                vt + vt_off<D>(r, 2 * dt + ((lane & 3) >> 1)) + 8 * (lane & 1)));
       }
       const bf16x8_t av = __builtin_bit_cast(
           bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
@@ -2158,12 +2175,15 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       wm[w * GH + m16] = m_run * kLn2;  // natural units for the merge
       wl[w * GH + m16] = l_run;
     }
+    // head m16's row with its float index XOR 4*(m16 % 8): the 8 lanes of a
+    // store then hit distinct 16-byte slots (rows of D floats alone: 8-way)
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<f32x4*>(red + w * RS + m16 * D + 16 * dt + 4 * g4) = o[dt];
+      *reinterpret_cast<f32x4*>(red + w * RS + m16 * D + ((16 * dt + 4 * g4) ^ (4 * (m16 & 7)))) =
+          o[dt];
   }
   lds_barrier();
-  finish_chunk<D, GH, NW, NT, ROPE, NW * RS>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c,
+  finish_chunk<D, GH, NW, NT, ROPE, NW * RS, true>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c,
                                               qrow0, nch,
                                     smem + L.mrg, red, misc + 1, DH);
 
