@@ -2239,13 +2239,18 @@ struct PfArgs {
   const void* v;
   float* o;        // [M][nq][D]
   const int32_t* block_table;  // paged: the sequence's row of block ids
-  int nq, nkv, M, N, pos0, window, nqb;  // nqb: 64-row blocks per KV head
+  int nq, nkv, M, N, pos0, window, nqb;  // nqb: blocks of 16 * pf_waves query rows per KV head
   int page_shift;
   float scale;
 };
 
-constexpr int kPfWaves = 4;
-constexpr int kPfThreads = kPfWaves * 64;
+// Waves per prefill workgroup (16 query rows each): 8, so that 128 rows
+// share each staged key tile and its split into pieces (32q/8kv/d128 fp32,
+// 2048-token prompt: 285 -> 237 us), except fp32 d = 256, whose 379
+// registers a lane leave room for 4 waves a CU.  A launch whose 8-wave grid
+// would leave CUs idle takes 4 waves (512-token prompt after 16384 cached
+// tokens: 1452 us on 8 waves, 1414 on 4).
+__host__ __device__ constexpr int pf_waves(int D, int esz) { return D == 256 && esz == 4 ? 4 : 8; }
 
 // The kernel: every fp32 product is taken as bf16 pieces on
 // v_mfma_f32_16x16x32_bf16 (16x the fp32 matrix rate).  x = hi + mid + lo
@@ -2263,10 +2268,12 @@ constexpr int kPfThreads = kPfWaves * 64;
 //     O^T += V^T . P^T, with P in the registers the score accumulator left
 //     it in (key 16u + 4(l/16) + r of lane l, slot 4u + r).
 // D = 256 stages 100 KB (fp32 pieces) and runs one workgroup per CU.
-template <int D, typename T, bool PAGED>
-__global__ __launch_bounds__(kPfThreads, (D == 256 && sizeof(T) == 4) ? 1 : 2) void prefill_mfma16_kernel(PfArgs a) {
+template <int D, typename T, bool PAGED, int PW>
+__global__ __launch_bounds__(64 * PW, PW == 4 && D < 256 ? 2 : 1)
+void prefill_mfma16_kernel(PfArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "bf16-piece prefill: D = 64, 128, 256");
-  constexpr int NT = kPfThreads, QB = 16 * kPfWaves;
+  static_assert(PW == 4 || PW == 8, "4 or 8 waves");
+  constexpr int NT = 64 * PW, QB = NT / 4;
   constexpr int KT = 32, KH = 2;
   constexpr int KP = sizeof(T) == 2 ? 1 : 3;  // staged pieces of K and V
   constexpr int KRB = 2 * D + 16;             // bytes of a staged K row
@@ -2285,8 +2292,13 @@ __global__ __launch_bounds__(kPfThreads, (D == 256 && sizeof(T) == 4) ? 1 : 2) v
   constexpr bool Q8 = std::is_same<T, q8_t>::value;
   static_assert(CH % NT == 0 || CH < NT, "whole chunks per thread");
   static_assert((D / VW) % 4 == 0 && CH % 64 == 0 && 16 % VW == 0, "chunk mapping");
-  __shared__ __attribute__((aligned(16))) char kp_s[KP * KT * KRB];
-  __shared__ __attribute__((aligned(16))) char vp_s[KP * KT * VRB];
+  // 8 waves (one workgroup a CU): two tile buffers where they fit, one
+  // barrier a tile (a buffer is rewritten only after every wave has passed
+  // the barrier that follows its last use); 4 waves: one buffer, so that two
+  // workgroups share a CU's LDS
+  constexpr int NBUF = PW == 8 && 2 * KP * KT * (KRB + VRB) <= 160 * 1024 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) char kp_buf[NBUF][KP * KT * KRB];
+  __shared__ __attribute__((aligned(16))) char vp_buf[NBUF][KP * KT * VRB];
 
   const int G = a.nq / a.nkv;
   const int h = blockIdx.x % a.nkv;  // heads fastest: every XCD gets every head's share
@@ -2383,7 +2395,7 @@ __global__ __launch_bounds__(kPfThreads, (D == 256 && sizeof(T) == 4) ? 1 : 2) v
     }
   };
   // the chunk's values as KP bf16 pieces, 4 elements (8 bytes) at a time
-  auto store_tile = [&]() {
+  auto store_tile = [&](char* kp_s, char* vp_s) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + NT * i;
@@ -2433,7 +2445,9 @@ __global__ __launch_bounds__(kPfThreads, (D == 256 && sizeof(T) == 4) ? 1 : 2) v
   if (ntile > 0) load_tile(kt_lo);
   for (int it = 0; it < ntile; ++it) {
     const int tk = kt_lo + it * KT;
-    store_tile();
+    const char* kp_s = kp_buf[NBUF == 2 ? (it & 1) : 0];
+    const char* vp_s = vp_buf[NBUF == 2 ? (it & 1) : 0];
+    store_tile(kp_buf[NBUF == 2 ? (it & 1) : 0], vp_buf[NBUF == 2 ? (it & 1) : 0]);
     __syncthreads();
     if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
     // scores of the two 16-key halves, smallest piece products first
@@ -2534,7 +2548,7 @@ __global__ __launch_bounds__(kPfThreads, (D == 256 && sizeof(T) == 4) ? 1 : 2) v
         o[dt] = mfma_bf16(av[0], ph, o[dt]);
       }
     }
-    __syncthreads();  // the tile's LDS is rewritten next
+    if constexpr (NBUF == 1) __syncthreads();  // the tile's LDS is rewritten next
   }
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
@@ -3344,6 +3358,33 @@ bool norms_ok(const Norms& nm) { return nm.eps >= 0.f && nm.eps < INFINITY; }
 
 // ===========================================================================
 // C ABI
+using PfFn = void (*)(PfArgs);
+
+template <int D, typename T, bool PAGED>
+PfFn pf_kernel_w(int pw) {
+  if constexpr (pf_waves(D, sizeof(T)) == 8)
+    if (pw == 8) return prefill_mfma16_kernel<D, T, PAGED, 8>;
+  return prefill_mfma16_kernel<D, T, PAGED, 4>;
+}
+
+template <typename T, bool PAGED>
+PfFn pf_kernel_d(int d, int pw) {
+  if (d == 64) return pf_kernel_w<64, T, PAGED>(pw);
+  if (d == 128) return pf_kernel_w<128, T, PAGED>(pw);
+  if constexpr (!std::is_same<T, q8_t>::value) return pf_kernel_w<256, T, PAGED>(pw);
+  return nullptr;  // Q8 prefill: d = 64, 128
+}
+
+// The prefill kernel of a head dim (64, 128, 256), cache type, layout and
+// wave count (pw: 4, or 8 where the instance has it).
+PfFn pf_kernel(int d, int kv_dtype, bool paged, int pw) {
+  if (kv_dtype == MOLOT_KV_Q8)
+    return paged ? pf_kernel_d<q8_t, true>(d, pw) : pf_kernel_d<q8_t, false>(d, pw);
+  if (kv_dtype == MOLOT_KV_F32)
+    return paged ? pf_kernel_d<float, true>(d, pw) : pf_kernel_d<float, false>(d, pw);
+  return paged ? pf_kernel_d<bf16_t, true>(d, pw) : pf_kernel_d<bf16_t, false>(d, pw);
+}
+
 extern "C" {
 
 const char* molot_hip_strerror(int status) {
@@ -3830,7 +3871,11 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   if (!K || !V || !aligned16(K) || !aligned16(V) || !aligned16(Qm) || !aligned16(Om))
     return MOLOT_EINVAL;
   const int64_t rows = (int64_t)M * (nq / nkv);
-  const int64_t nqb = (rows + 16 * kPfWaves - 1) / (16 * kPfWaves);
+  const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1;
+  const int64_t rows8 = (rows + 127) / 128;
+  const int pw = pf_waves(d, esz) == 8 && rows8 * nkv >= num_cus() ? 8 : 4;
+  const int pf_threads = 64 * pw, qrows = pf_threads / 4;
+  const int64_t nqb = (rows + qrows - 1) / qrows;
   if (nqb * nkv > (int64_t)0x7FFFFFFF) return MOLOT_ENOTSUP;
   PfArgs a{};
   a.q = Qm;
@@ -3851,37 +3896,16 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
       return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
-  using PfFn = void (*)(PfArgs);
-  PfFn pk;
-  if (kv_dtype == MOLOT_KV_Q8)  // D = 64, 128 (check_common)
-    pk = block_row ? (d == 64 ? prefill_mfma16_kernel<64, q8_t, true>
-                              : prefill_mfma16_kernel<128, q8_t, true>)
-                   : (d == 64 ? prefill_mfma16_kernel<64, q8_t, false>
-                              : prefill_mfma16_kernel<128, q8_t, false>);
-  else if (!block_row)
-    pk = kv_dtype == MOLOT_KV_F32
-             ? (d == 64 ? prefill_mfma16_kernel<64, float, false>
-                        : d == 128 ? prefill_mfma16_kernel<128, float, false>
-                                   : prefill_mfma16_kernel<256, float, false>)
-             : (d == 64 ? prefill_mfma16_kernel<64, bf16_t, false>
-                        : d == 128 ? prefill_mfma16_kernel<128, bf16_t, false>
-                                   : prefill_mfma16_kernel<256, bf16_t, false>);
-  else
-    pk = kv_dtype == MOLOT_KV_F32
-             ? (d == 64 ? prefill_mfma16_kernel<64, float, true>
-                        : d == 128 ? prefill_mfma16_kernel<128, float, true>
-                                   : prefill_mfma16_kernel<256, float, true>)
-             : (d == 64 ? prefill_mfma16_kernel<64, bf16_t, true>
-                        : d == 128 ? prefill_mfma16_kernel<128, bf16_t, true>
-                                   : prefill_mfma16_kernel<256, bf16_t, true>);
+  const PfFn pk = pf_kernel(d, kv_dtype, block_row != nullptr, pw);
+  if (!pk) return MOLOT_ENOTSUP;
   const dim3 grid((unsigned)(nqb * nkv));
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {
     ProfRec pr{prof_event(), prof_event(), nullptr, nullptr, false};
-    hipExtLaunchKernelGGL(pk, grid, dim3(kPfThreads), 0, (hipStream_t)stream, pr.a0, pr.a1, 0, a);
+    hipExtLaunchKernelGGL(pk, grid, dim3(pf_threads), 0, (hipStream_t)stream, pr.a0, pr.a1, 0, a);
     g_prof.push_back(pr);
   } else {
-    hipLaunchKernelGGL(pk, grid, dim3(kPfThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(pk, grid, dim3(pf_threads), 0, (hipStream_t)stream, a);
   }
   return (int)hipGetLastError();
 }
