@@ -758,7 +758,7 @@ __host__ __device__ constexpr int merge_lds_floats(int gh) { return 2 * kMergeMa
 // a record load per chunk in every thread the merge took 0.4 us longer
 // (32q/8kv/d128 fp32, n = 16385).
 // RED: floats of LDS at mred (the phase sums: PH*P floats).
-template <int D, int GH, int NW, int NT, bool ROPE, int RED>
+template <int D, int GH, int NW, int NT, bool ROPE, int RED, int QSTR = D>
 __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot, int nch,
                                                  int64_t qrow0, const float* qs, float* mst,
                                                  float* mred, int* flag, int tid, int lane,
@@ -880,12 +880,12 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
     if (a.q_out)
       for (int i = tid; i < P; i += NT) {
         const int64_t oi = out_index(qrow0, i, D, dh);
-        if (oi >= 0) a.q_out[oi] = qs[i];
+        if (oi >= 0) a.q_out[oi] = qs[(i / D) * QSTR + i % D];
       }
   }
 }
 
-template <int D, int GH, int NW, int NT, bool ROPE, int RED, bool XSW = false>
+template <int D, int GH, int NW, int NT, bool ROPE, int RED, bool XSW = false, int QSTR = D>
 __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm, const float* wl,
                                              const float* red, int RS, const float* qs, int tid,
                                              int lane, bool split, int64_t slot, int c,
@@ -940,7 +940,7 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
       if (a.q_out)
         for (int i = tid; i < P; i += NT) {
           const int64_t oi = out_index(qrow0, i, D, dh);
-          if (oi >= 0) a.q_out[oi] = qs[i];
+          if (oi >= 0) a.q_out[oi] = qs[(i / D) * QSTR + i % D];
         }
     }
     return;
@@ -963,13 +963,13 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
   }
   if (a.ctr) {  // in-launch merge: the workgroup completing the slot merges it
     if (tid == 0) a.part_x[slot * a.nchunks + c] = xcc_id();
-    arrive_and_merge<D, GH, NW, NT, ROPE, RED>(a, slot, nch, qrow0, qs, mst, mred, flag, tid,
+    arrive_and_merge<D, GH, NW, NT, ROPE, RED, QSTR>(a, slot, nch, qrow0, qs, mst, mred, flag, tid,
                                                lane, dh);
     return;
   }
   if constexpr (ROPE) {  // the rotated q leaves through the combine kernel
     if (c == 0 && a.q_out)
-      for (int i = tid; i < P; i += NT) a.qrot[slot * P + i] = qs[i];
+      for (int i = tid; i < P; i += NT) a.qrot[slot * P + i] = qs[(i / D) * QSTR + i % D];
   }
 }
 
@@ -1585,6 +1585,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLazyMax = 8.f;
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+template <int D>
+constexpr int kMfmaQStride = D + 4;
+
 // LDS of attn_mfma_kernel, in floats.  vt: per wave, 32 staged V rows of D
 // bf16 (16*D floats), which after the stream hold the wave's partial o;
 // sc (Q8): per wave, the K then the V row scales of its current tile.
@@ -1593,7 +1596,7 @@ struct LdsM {
   __host__ __device__ LdsM(int D, int GH, int chunk, int page_shift, bool paged, bool q8,
                            int merge) {
     int o = 0;
-    qs = o; o += GH * D;
+    qs = o; o += GH * (D + 4);  // rows kMfmaQStride<D> = D + 4 floats apart
     cs = o; o += D / 2;
     sn = o; o += D / 2;
     knew = o; o += D;
@@ -1621,13 +1624,22 @@ struct LdsM {
 // r0 .. r0+7 of one unit ch in 8 lanes: distinct when the low 3 bits of f
 // run over 8 values; a transposed read takes units 2dt and 2dt+1 of 8 rows:
 // 16 distinct units of a 256-byte span when f >> 1 runs over 8 values.
-// D = 128 (16 units a row): f(r) = 2(r%8) + (r/4)%2 meets both; D = 64
-// (8 units, 2 rows per 256 bytes): f(r) = r%8.  The 32-byte-segment swizzle
-// this replaces conflicted 2-way on every store.
+// D = 128 or 256 (16 or 32 units a row): f(r) = 2(r%8) + (r/4)%2 meets
+// both; D = 64 (8 units, 2 rows per 256 bytes): f(r) = r%8.  The
+// 32-byte-segment swizzle this replaces conflicted 2-way on every store.
 template <int D>
 __device__ __forceinline__ int vt_off(int r, int ch) {
-  const int f = D == 128 ? (((r & 7) << 1) | ((r >> 2) & 1)) : (r & 7);
+  const int f = D != 64 ? (((r & 7) << 1) | ((r >> 2) & 1)) : (r & 7);
   return r * (2 * D) + 16 * (ch ^ f);
+}
+
+// Byte offset of 16-byte unit ch of a staged K row (the prefill's A operand
+// of the scores, read by 16-byte loads of 16 keys at one unit): unit ch of
+// key r at ch ^ (r % 16) (D = 64: r % 8).  Measured, a 16-byte LDS read
+// serves 16 lanes a cycle, conflict-free on 16 distinct units mod 256 bytes.
+template <int D>
+__device__ __forceinline__ int kt_off(int r, int ch) {
+  return r * (2 * D) + 16 * (ch ^ (D == 64 ? (r & 7) : (r & 15)));
 }
 
 // x = hi + mid + lo in bf16 (round to nearest even at each step); the three
@@ -1701,6 +1713,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   using E = typename std::conditional<Q8, int8_t, bf16_t>::type;
 
   constexpr int DH = D;  // never padded
+  constexpr int QSTR = kMfmaQStride<D>;  // floats between q rows in LDS
   extern __shared__ float smem[];
   const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg);
   float* qs = smem + L.qs;
@@ -1894,7 +1907,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
     const int i = tid + u * NT;
-    if (i < QV) reinterpret_cast<f32x4*>(qs)[i] = qv[u];
+    if (i < QV) *reinterpret_cast<f32x4*>(qs + (i / (D / 4)) * QSTR + 4 * (i % (D / 4))) = qv[u];
   }
   if constexpr (ROPE) {
     float* csn = smem + L.cs;
@@ -1917,9 +1930,9 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     lds_barrier();
     for (int i = tid; rot && i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
-      const float x0 = qs[g * D + j], x1 = qs[g * D + j + D / 2];
-      qs[g * D + j] = x0 * csn[j] - x1 * sn[j];
-      qs[g * D + j + D / 2] = x0 * sn[j] + x1 * csn[j];
+      const float x0 = qs[g * QSTR + j], x1 = qs[g * QSTR + j + D / 2];
+      qs[g * QSTR + j] = x0 * csn[j] - x1 * sn[j];
+      qs[g * QSTR + j + D / 2] = x0 * sn[j] + x1 * csn[j];
     }
     if (is_new) {
       const NewNorms nn = new_norms<D, NW>(a, smem + L.wm, smem + L.wl, DH);
@@ -1959,20 +1972,26 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
 
   // q^T as the B operand: lane l holds head l%16 (zero past GH), elements
   // 32*kk + 8*(l/16) + e (Q8: 64*(kk/2) + 16*(l/16) + 8*(kk%2) + e), scaled
-  // by scale*log2(e), in three bf16 pieces
+  // by scale*log2(e), in three bf16 pieces.  16-byte reads of rows QSTR =
+  // D + 4 floats apart: the 8 lanes of a read (heads r .. r+7) fall in 8
+  // distinct 16-byte slots (rows of D floats: one slot, 8-way conflicts).
   const float qsc = a.scale * kLog2e;
   bf16x8_t qh[KK], qm[KK], ql[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int di = Q8 ? 64 * (kk >> 1) + 16 * g4 + 8 * (kk & 1) + e : 32 * kk + 8 * g4 + e;
-      const float x = m16 < GH ? qs[m16 * D + di] * qsc : 0.f;
-      __bf16 hi, mid, lo;
-      split3(x, hi, mid, lo);
-      qh[kk][e] = hi;
-      qm[kk][e] = mid;
-      ql[kk][e] = lo;
+    for (int e4 = 0; e4 < 8; e4 += 4) {
+      const int di = Q8 ? 64 * (kk >> 1) + 16 * g4 + 8 * (kk & 1) + e4 : 32 * kk + 8 * g4 + e4;
+      const f32x4 x4 = m16 < GH ? *reinterpret_cast<const f32x4*>(qs + m16 * QSTR + di)
+                                : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        __bf16 hi, mid, lo;
+        split3(x4[e] * qsc, hi, mid, lo);
+        qh[kk][e4 + e] = hi;
+        qm[kk][e4 + e] = mid;
+        ql[kk][e4 + e] = lo;
+      }
     }
 
   // ---- stream ----
@@ -2148,7 +2167,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     if (m16 < GH) {
 #pragma unroll 8
       for (int d = g4 * (D / 4); d < (g4 + 1) * (D / 4); ++d)
-        part = fmaf(qs[m16 * D + d], knew[d], part);
+        part = fmaf(qs[m16 * QSTR + d], knew[d], part);
     }
     part += __shfl_xor(part, 16);
     part += __shfl_xor(part, 32);
@@ -2183,7 +2202,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
           o[dt];
   }
   lds_barrier();
-  finish_chunk<D, GH, NW, NT, ROPE, NW * RS, true>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c,
+  finish_chunk<D, GH, NW, NT, ROPE, NW * RS, true, QSTR>(a, wm, wl, red, RS, qs, tid, lane, split, slot, c,
                                               qrow0, nch,
                                     smem + L.mrg, red, misc + 1, DH);
 
@@ -2259,14 +2278,17 @@ __host__ __device__ constexpr int pf_waves(int D, int esz) { return D == 256 && 
 // mid*mid), so the dropped ones are ~2^-24 of it, an fp32 rounding.  A bf16
 // cache needs one K/V piece (its values are exact): three products.  Tiles
 // of 32 keys are staged into LDS as pieces:
-//   K [KP][32 keys][D] bf16, rows padded by 16 bytes (the 16 lanes of a
-//     ds_read_b128 then hit 16 distinct groups of 4 banks), read as the A
-//     operand of S^T = K . Q^T: lane l key 16u + l%16, elements
-//     32s + 8(l/16) .. +7, Q^T in the same element order in registers;
-//   V [KP][32 keys][D] bf16, 32-byte segments XOR-swizzled by key, read as
-//     V^T by ds_read_b64_tr_b16 as in attn_mfma_kernel: the A operand of
-//     O^T += V^T . P^T, with P in the registers the score accumulator left
-//     it in (key 16u + 4(l/16) + r of lane l, slot 4u + r).
+//   K [KP][32 keys][D] bf16, 16-byte units XOR-swizzled by key (kt_off),
+//     read as the A operand of S^T = K . Q^T: lane l key 16u + l%16,
+//     elements 32s + 8(l/16) .. +7, Q^T in the same element order in
+//     registers;
+//   V [KP][32 keys][D] bf16, 16-byte units XOR-swizzled by key (vt_off),
+//     read as V^T by ds_read_b64_tr_b16 as in attn_mfma_kernel: the A
+//     operand of O^T += V^T . P^T, with P in the registers the score
+//     accumulator left it in (key 16u + 4(l/16) + r of lane l, slot 4u + r).
+// A tile's loads put keys 0..7 of one 16-byte column in lanes 0..7 and the
+// next column in lanes 8..15 (128 contiguous bytes of each of 8 rows per 64
+// lanes), so every LDS store of a piece is conflict-free too.
 // D = 256 stages 100 KB (fp32 pieces) and runs one workgroup per CU.
 template <int D, typename T, bool PAGED, int PW>
 __global__ __launch_bounds__(64 * PW, PW == 4 && D < 256 ? 2 : 1)
@@ -2276,14 +2298,8 @@ void prefill_mfma16_kernel(PfArgs a) {
   constexpr int NT = 64 * PW, QB = NT / 4;
   constexpr int KT = 32, KH = 2;
   constexpr int KP = sizeof(T) == 2 ? 1 : 3;  // staged pieces of K and V
-  constexpr int KRB = 2 * D + 16;             // bytes of a staged K row
+  constexpr int KRB = 2 * D;                  // bytes of a staged K row
   constexpr int VRB = 2 * D;                  // bytes of a staged V row
-  constexpr int NSEG = D / 16;                // 32-byte segments of a V row
-  // fp32 caches: a half-wave stages 16 keys x 2 element groups of one
-  // segment (16 of its 32 bytes per key); rows with key bit log2(NSEG) set
-  // keep their segments rotated by 16 bytes, so keys k and k + NSEG (same
-  // swizzled segment) use different banks
-  constexpr int VROT = KVT<T>::VW == 4 ? 16 : 0;
   constexpr int QS = D / 32;                  // 32-element steps of the scores
   constexpr int DT = D / 16;
   constexpr int VW = KVT<T>::VW;              // elements per 16-byte load
@@ -2345,12 +2361,12 @@ void prefill_mfma16_kernel(PfArgs a) {
     ql[s] = __builtin_bit_cast(bf16x8_t, u32x4{l4[0], l4[1], l4[2], l4[3]});
   }
 
-  // tile loads: 16 consecutive lanes hold 16 keys of one element group, so
-  // each load instruction reads 64 contiguous bytes of 16 rows
+  // tile loads: chunk c (16 bytes of the cache type) is key c%8 of its
+  // key octet, column (c/8) % (D/VW) of the row, octet c / (8*D/VW)
   auto chunk_of = [&](int c, int& key, int& e) {
-    constexpr int KT16 = KT / 16;
-    key = (c & 15) + 16 * ((c >> 6) % KT16);
-    e = VW * (((c >> 4) & 3) + 4 * ((c >> 6) / KT16));
+    constexpr int NCR = D / VW;  // chunks per row
+    key = (c & 7) + 8 * (c / (8 * NCR));
+    e = VW * ((c >> 3) % NCR);
   };
   const T* Kb = reinterpret_cast<const T*>(a.k);
   const T* Vb = reinterpret_cast<const T*>(a.v);
@@ -2426,9 +2442,8 @@ void prefill_mfma16_kernel(PfArgs a) {
             vpc[0][j / 2] = bf16_pair(vx[j4 + j], vx[j4 + j + 1]);
           }
         }
-        const int kofs = key * KRB + 2 * ej;
-        const int vofs = key * VRB + 32 * ((ej >> 4) ^ (key & (NSEG - 1))) +
-                         ((2 * (ej & 15) + VROT * ((key / NSEG) & 1)) & 31);
+        const int kofs = kt_off<D>(key, ej >> 3) + 8 * ((ej >> 2) & 1);
+        const int vofs = vt_off<D>(key, ej >> 3) + 8 * ((ej >> 2) & 1);
 #pragma unroll
         for (int p = 0; p < KP; ++p) {
           *reinterpret_cast<u32x2*>(kp_s + p * KT * KRB + kofs) = u32x2{kpc[p][0], kpc[p][1]};
@@ -2458,7 +2473,7 @@ void prefill_mfma16_kernel(PfArgs a) {
     for (int s = 0; s < QS; ++s)
 #pragma unroll
       for (int u = 0; u < KH; ++u) {
-        const char* kb = kp_s + (16 * u + c16) * KRB + 2 * (32 * s + 8 * g4);
+        const char* kb = kp_s + kt_off<D>(16 * u + c16, 4 * s + g4);
         const bf16x8_t k0 = *reinterpret_cast<const bf16x8_t*>(kb);
         if constexpr (KP == 3) {
           const bf16x8_t k1 = *reinterpret_cast<const bf16x8_t*>(kb + KT * KRB);
@@ -2529,8 +2544,8 @@ void prefill_mfma16_kernel(PfArgs a) {
           const int r = (lane >> 2) + 16 * u;
           t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) i16x4_t*)(
-                  vp_s + p * KT * VRB + r * VRB + 32 * (dt ^ (r & (NSEG - 1))) +
-                  ((8 * (lane & 3) + VROT * ((r / NSEG) & 1)) & 31)));
+                  vp_s + p * KT * VRB + vt_off<D>(r, 2 * dt + ((lane & 3) >> 1)) +
+                  8 * (lane & 1)));
         }
         av[p] = __builtin_bit_cast(
             bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
