@@ -2465,31 +2465,37 @@ void prefill_mfma16_kernel(PfArgs a) {
     store_tile(kp_buf[NBUF == 2 ? (it & 1) : 0], vp_buf[NBUF == 2 ? (it & 1) : 0]);
     __syncthreads();
     if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
-    // scores of the two 16-key halves, smallest piece products first
-    f32x4 sacc[KH];
+    // scores of the two 16-key halves, smallest piece products first; even
+    // and odd 32-element steps into separate accumulators (four independent
+    // MFMA chains, added at the end)
+    f32x4 sacc2[KH][2];
 #pragma unroll
-    for (int u = 0; u < KH; ++u) sacc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < KH; ++u) sacc2[u][0] = sacc2[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < QS; ++s)
 #pragma unroll
       for (int u = 0; u < KH; ++u) {
         const char* kb = kp_s + kt_off<D>(16 * u + c16, 4 * s + g4);
         const bf16x8_t k0 = *reinterpret_cast<const bf16x8_t*>(kb);
+        f32x4& acc = sacc2[u][s & 1];
         if constexpr (KP == 3) {
           const bf16x8_t k1 = *reinterpret_cast<const bf16x8_t*>(kb + KT * KRB);
           const bf16x8_t k2 = *reinterpret_cast<const bf16x8_t*>(kb + 2 * KT * KRB);
-          sacc[u] = mfma_bf16(k1, qm[s], sacc[u]);
-          sacc[u] = mfma_bf16(k2, qh[s], sacc[u]);
-          sacc[u] = mfma_bf16(k0, ql[s], sacc[u]);
-          sacc[u] = mfma_bf16(k1, qh[s], sacc[u]);
-          sacc[u] = mfma_bf16(k0, qm[s], sacc[u]);
-          sacc[u] = mfma_bf16(k0, qh[s], sacc[u]);
+          acc = mfma_bf16(k1, qm[s], acc);
+          acc = mfma_bf16(k2, qh[s], acc);
+          acc = mfma_bf16(k0, ql[s], acc);
+          acc = mfma_bf16(k1, qh[s], acc);
+          acc = mfma_bf16(k0, qm[s], acc);
+          acc = mfma_bf16(k0, qh[s], acc);
         } else {
-          sacc[u] = mfma_bf16(k0, ql[s], sacc[u]);
-          sacc[u] = mfma_bf16(k0, qm[s], sacc[u]);
-          sacc[u] = mfma_bf16(k0, qh[s], sacc[u]);
+          acc = mfma_bf16(k0, ql[s], acc);
+          acc = mfma_bf16(k0, qm[s], acc);
+          acc = mfma_bf16(k0, qh[s], acc);
         }
       }
+    f32x4 sacc[KH];
+#pragma unroll
+    for (int u = 0; u < KH; ++u) sacc[u] = sacc2[u][0] + sacc2[u][1];
     // online softmax (base 2) of this lane's row over its 8 keys of the tile.
     // Lazy rescale, as in the decode kernel: the running max moves only when
     // a score exceeds it by more than kLazyMax (p <= 2^8 otherwise); o and l
