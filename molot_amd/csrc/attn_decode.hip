@@ -422,7 +422,8 @@ struct AttnArgs {
   int nq, nkv, n, t0, pos, chunk, nchunks, max_blocks, page_shift, window;
   int dh;                // head dim as stored (< D: the kernel runs padded to its D)
   int dynamic;           // 1: waves claim blocks from a workgroup counter; 0: fixed order
-  int chunk_fast;        // 1-D grid, the KV heads of a chunk on one XCD (B = 1; see launch_pair)
+  int chunk_fast;        // 1-D grid, the KV heads of a chunk on one XCD (Q8; see launch_pair)
+  int nseq;              // chunk_fast: sequences of the launch
   // In-launch merge (see arrive_and_merge): every chunk of a slot runs on one
   // XCD, and the workgroup that completes a slot merges its chunk partials.
   int fold;              // ROPE: 1 = the step appends the new token (folded into the last
@@ -1729,9 +1730,12 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   if (a.chunk_fast) {  // workgroup id runs on XCD id % 8 (launch_pair)
     const int HS = a.nkv * nsub;
     const int k = (int)(blockIdx.x >> 3);
-    z = (k / HS) * 8 + (int)(blockIdx.x & 7);  // padded ids (z >= nchunks) exit below
+    // (sequence, chunk) pair pi = (k / HS) * 8 + id % 8, chunk slot slowest;
+    // padded ids (z >= nchunks) exit below
+    const int pi = (k / HS) * 8 + (int)(blockIdx.x & 7);
+    z = pi / a.nseq;
+    b = pi - z * a.nseq;
     hs = k % HS;
-    b = 0;
   } else if (a.xmap) {  // slot id % 8 runs on XCD id % 8 (launch_pair); padding ids exit
     const int s8 = (int)(blockIdx.x & 7);
     if (s8 >= a.slots) return;
@@ -3118,19 +3122,21 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   // index fastest, every XCD gets the same heads' share of every chunk and
   // sequence (equal work however the chunks of a batch differ in length),
   // and the chunk index slowest makes the XCDs stream the same rows at the
-  // same time.  chunk_fast (token-major Q8, one sequence) groups by chunk
-  // instead: the KV heads of one token share 128-byte lines (head rows of d
-  // bytes at t*R + h*d, the token's scales after them), so all heads of a
-  // chunk go to one XCD, whose L2 then fetches each shared line once.  A 1-D
-  // grid of 8 * ceil(nchunks / 8) * heads workgroups: id runs chunk slot
-  // (id / 8 / heads) * 8 + id % 8 and head (id / 8) % heads, so chunk slot z
-  // is on XCD z % 8 whatever the chunk count, each XCD's heads of a chunk are
-  // dispatched together, and the padding ids exit at once.
+  // same time.  chunk_fast (Q8 caches) groups by chunk instead: the KV heads
+  // of one token share 128-byte lines (token-major: head rows of d bytes at
+  // t*R + h*d, the token's scales after them; paged: the page's scales
+  // after its codes, 64 bytes a head), so all heads of a (sequence, chunk)
+  // pair go to one XCD, whose L2 then fetches each shared line once.  A 1-D
+  // grid of 8 * ceil(pairs / 8) * heads workgroups: id runs pair
+  // (id / 8 / heads) * 8 + id % 8 (chunk slot pair / B of sequence pair % B)
+  // and head (id / 8) % heads, so each pair is on one XCD whatever the
+  // counts, its heads are dispatched together, and the padding ids exit at
+  // once.
   // xmap (in-launch merge, fewer than 8 slots): a 1-D grid of 8 * nchunks
   // workgroups, id running chunk slot id / 8 of slot id % 8, so each slot's
   // chunks share an XCD; ids of absent slots exit at once.
   const dim3 grid = a.chunk_fast
-                        ? dim3((unsigned)((a.nchunks + 7) / 8 * 8 * a.nkv * nsubs), 1, 1)
+                        ? dim3((unsigned)(((int64_t)B * a.nchunks + 7) / 8 * 8 * a.nkv * nsubs), 1, 1)
                         : a.xmap ? dim3((unsigned)(8 * a.nchunks), 1, 1)
                                  : dim3(a.nkv * nsubs, B, a.nchunks);
   if (prof) {
@@ -3215,7 +3221,8 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
 template <int D, int GH, bool PAGED, bool ROPE, bool Q8>
 int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
   constexpr int kWpc = PAGED ? (Q8 ? 8 : 16) : 1;
-  a.chunk_fast = Q8 && !PAGED && B == 1;
+  a.chunk_fast = Q8;
+  a.nseq = B;
   int st = plan_launch(a, D, span, GH, nsubs, B, kTile, kWpc, stream, !PAGED);
   if (st) return st;
   // by default the combine kernel: its four waves per workgroup would fold
