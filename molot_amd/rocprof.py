@@ -61,10 +61,15 @@ def _cmd_block(cmds) -> str:
     return "```\n" + "\n".join(cmds) + "\n```\n" if cmds else ""
 
 
+def _source_line() -> str:
+    return (f"Kernel source: `molot_amd/csrc/attn_decode.hip`, sha256[:16] `{source_hash()}` "
+            "(the tree the summary was written from).\n")
+
+
 def trace(args) -> str:
     rows = _rows(_find(args.dir, "_kernel_stats.csv"))
     out = [f"# {args.title}\n", "Commands (repository root of the GPU box):\n",
-           _cmd_block(args.cmd), args.note + "\n" if args.note else "",
+           _cmd_block(args.cmd), _source_line(), args.note + "\n" if args.note else "",
            "| kernel | calls | avg us | min us | max us | % time |", "|---|---|---|---|---|---|"]
     for r in rows[: args.top]:
         out.append(f"| `{short_name(r['Name'])}` | {r['Calls']} | "
@@ -136,6 +141,7 @@ def traffic(args) -> str:
             f.write("\n")
     ratio = total / args.algorithmic if args.algorithmic else float("nan")
     out = [f"# {args.title}\n", "Commands (repository root of the GPU box):\n", _cmd_block(args.cmd),
+           _source_line(),
            "`bench.py --pmc-run` launches eager steps, then three copies of 1 GiB through "
            "`molot_probe_copy` (a plain copy kernel), whose readings calibrate the counters.\n",
            "| counter | kernel KiB/dispatch (n) | copy_kernel KiB/dispatch (n) | bytes per counted KiB |",
@@ -164,7 +170,7 @@ def counters(args) -> str:
                     names.add(ctr)
     cols = sorted(names)
     out = [f"# {args.title}\n", "Commands (repository root of the GPU box):\n", _cmd_block(args.cmd),
-           "Per-dispatch means (number of dispatches in parentheses).\n",
+           _source_line(), "Per-dispatch means (number of dispatches in parentheses).\n",
            "| kernel | " + " | ".join(cols) + " |", "|---|" + "---|" * len(cols)]
     for k in sorted(table):
         cells = [f"{table[k][c][0]:.4g} ({table[k][c][1]})" if c in table[k] else "" for c in cols]
