@@ -576,8 +576,9 @@ def main() -> int:
     k1_us, k2_us = kernel_times(step, J)
     a1_us, a2_us = kernel_times(attention, J)
     achieved = step_bytes / (k1_us * 1e-6) / 1e9
-    log(args, f"attn_kernel {k1_us:.2f} us/launch -> {achieved:.0f} GB/s "
-        f"(chunks {nch} x {chk} rows); combine_kernel {k2_us:.2f} us; "
+    kname = "attn_mfma_kernel" if kvd and cfg["d"] in (64, 128) else "attn_kernel"
+    log(args, f"{kname} {k1_us:.2f} us/launch -> {achieved:.0f} GB/s "
+        f"(chunks {nch} x {chk} rows); combine {k2_us:.2f} us; "
         f"attention-only entry: {a1_us:.2f} + {a2_us:.2f} us")
 
     # ---- achievable streaming-read peak on this box (probe kernel, 4 GiB) ----
