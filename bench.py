@@ -176,6 +176,8 @@ def parse():
     ap.add_argument("--merge", type=int, default=-1,
                     help="1 = split-K partials merged inside the attention launch where possible, "
                          "0 = by the combine kernel, -1 = the library's choice (default)")
+    ap.add_argument("--prefill-presplit", type=int, default=1,
+                    help="prefill: 1 = keys split into pieces once per launch, 0 = per tile")
     ap.add_argument("--norms", action="store_true",
                     help="the step with the layer's q/k/v RMS norms fused in (forward.h:554-563)")
     ap.add_argument("--block-order", type=int, default=1,
@@ -473,6 +475,7 @@ def main() -> int:
     if args.wgs_per_cu:
         lib.molot_hip_set_tuning(args.wgs_per_cu)
     lib.molot_hip_set_merge(args.merge)
+    lib.molot_hip_set_prefill_presplit(args.prefill_presplit)
     lib.molot_hip_set_block_order(args.block_order)
 
     cfg = CONFIGS[args.config]

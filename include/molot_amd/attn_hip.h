@@ -320,6 +320,15 @@ void molot_hip_set_tuning(int wgs_per_cu);
  * its merged output would be NaN rather than a stale merge. */
 void molot_hip_set_merge(int in_launch);
 
+/* How the prefill entries feed fp32 and Q8 caches to the matrix cores.
+ * on = 1 (default): the attended keys of every KV head are split into bf16
+ * pieces once per launch, into a per-stream workspace of
+ * 12 * nkv * (N - t0) * d bytes (at most 1 GiB; it grows outside stream
+ * capture only), and the attention kernel copies them into LDS.  on = 0, or
+ * when that workspace is unavailable: the attention kernel splits each
+ * staged tile itself.  Both give the same bits. */
+void molot_hip_set_prefill_presplit(int on);
+
 /* Order in which the waves of a workgroup take their chunk's row blocks.
  * dynamic = 1 (default): a wave takes the next free block when it has one
  * to spare, so faster-served waves take more; the fp32 summation order then

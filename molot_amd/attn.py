@@ -24,7 +24,7 @@ __all__ = [
     "attn_decode_gqa", "attn_decode_gqa_win", "attn_decode_head", "attn_decode_head_win",
     "attn_decode_strided", "decode_step", "attn_decode_paged", "decode_step_paged",
     "rope_append_paged", "vexp", "decode_step_shared", "decode_step_paged_shared", "prefill_q",
-    "attn_prefill_paged", "set_merge",
+    "attn_prefill_paged", "set_merge", "set_prefill_presplit",
     "last_plan", "set_split_chunk", "attn_prefill_gqa", "prefill_step", "KVCache", "kv_dtype_of",
 ]
 
@@ -471,6 +471,13 @@ def set_merge(in_launch) -> None:
     combine kernel (False), or as the library chooses (None, the default);
     see molot_hip_set_merge."""
     _lib.load().molot_hip_set_merge(-1 if in_launch is None else (1 if in_launch else 0))
+
+
+def set_prefill_presplit(on: bool) -> None:
+    """Prefill over fp32/Q8 caches from keys split into pieces once per
+    launch (True, the default) or split per staged tile (False); see
+    molot_hip_set_prefill_presplit.  Both give the same bits."""
+    _lib.load().molot_hip_set_prefill_presplit(1 if on else 0)
 
 
 def profile(fn, launches: int = 64):

@@ -1629,9 +1629,12 @@ struct LdsM {
 // both; D = 64 (8 units, 2 rows per 256 bytes): f(r) = r%8.  The
 // 32-byte-segment swizzle this replaces conflicted 2-way on every store.
 template <int D>
+__device__ __forceinline__ int vt_f(int r) {
+  return D != 64 ? (((r & 7) << 1) | ((r >> 2) & 1)) : (r & 7);
+}
+template <int D>
 __device__ __forceinline__ int vt_off(int r, int ch) {
-  const int f = D != 64 ? (((r & 7) << 1) | ((r >> 2) & 1)) : (r & 7);
-  return r * (2 * D) + 16 * (ch ^ f);
+  return r * (2 * D) + 16 * (ch ^ vt_f<D>(r));
 }
 
 // Byte offset of 16-byte unit ch of a staged K row (the prefill's A operand
@@ -1639,8 +1642,12 @@ __device__ __forceinline__ int vt_off(int r, int ch) {
 // key r at ch ^ (r % 16) (D = 64: r % 8).  Measured, a 16-byte LDS read
 // serves 16 lanes a cycle, conflict-free on 16 distinct units mod 256 bytes.
 template <int D>
+__device__ __forceinline__ int kt_f(int r) {
+  return D == 64 ? (r & 7) : (r & 15);
+}
+template <int D>
 __device__ __forceinline__ int kt_off(int r, int ch) {
-  return r * (2 * D) + 16 * (ch ^ (D == 64 ? (r & 7) : (r & 15)));
+  return r * (2 * D) + 16 * (ch ^ kt_f<D>(r));
 }
 
 // x = hi + mid + lo in bf16 (round to nearest even at each step); the three
@@ -2265,7 +2272,80 @@ struct PfArgs {
   int nq, nkv, M, N, pos0, window, nqb;  // nqb: blocks of 16 * pf_waves query rows per KV head
   int page_shift;
   float scale;
+  // the attended keys [T0, T0 + R) of every KV head split into bf16 pieces
+  // once for the launch (pf_split_kernel): [K, V][nkv][3 pieces][R][D]; NULL:
+  // the kernel splits each staged tile itself
+  const uint16_t* pieces;
+  int T0, R;
 };
+
+// Cache offset (elements of T; Q8: bytes) of row t of KV head h, and for Q8
+// the byte offset of its scale (soff).  Token-major: [N][nkv*D] (Q8 rows of
+// nkv*D codes, then nkv scales padded to 16 bytes); paged: blocks of
+// [nkv][page][D] (Q8: [nkv][page][D] codes, then [nkv][page] scales).
+template <int D, typename T, bool PAGED>
+__device__ __forceinline__ int64_t pf_row_off(const PfArgs& a, int h, int t, int64_t& soff) {
+  constexpr bool Q8 = std::is_same<T, q8_t>::value;
+  const int pg = 1 << a.page_shift;
+  const int64_t R = (int64_t)a.nkv * D + ((4 * a.nkv + 15) & ~15);
+  const int64_t BB = (int64_t)a.nkv * pg * (D + 4);
+  if constexpr (PAGED) {
+    const int64_t blk = a.block_table[t >> a.page_shift];
+    const int sl = t & (pg - 1);
+    if constexpr (Q8) {
+      soff = blk * BB + (int64_t)a.nkv * pg * D + 4 * ((int64_t)h * pg + sl);
+      return blk * BB + ((int64_t)h * pg + sl) * D;
+    }
+    return (blk * a.nkv + h) * pg * D + (int64_t)sl * D;
+  } else {
+    if constexpr (Q8) {
+      soff = (int64_t)t * R + (int64_t)a.nkv * D + 4 * h;
+      return (int64_t)t * R + (int64_t)h * D;
+    }
+    return (int64_t)t * a.nkv * D + (int64_t)h * D;
+  }
+}
+
+// K and V of the keys [T0, T0 + R) as three bf16 pieces (split3x2, the
+// values the prefill kernel would split per tile: fp32 rows, or Q8 code * s),
+// into [K, V][nkv][3][R][D].  Thread: one 8-element unit of one row; grid
+// (units / 256, nkv, 2).
+template <int D, typename T, bool PAGED>
+__global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) {
+  constexpr bool Q8 = std::is_same<T, q8_t>::value;
+  static_assert(sizeof(T) != 2, "bf16 caches are exact in one piece");
+  constexpr int UPR = D / 8;
+  const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= (int64_t)a.R * UPR) return;
+  const int h = blockIdx.y, kv = blockIdx.z;
+  const int r = (int)(u / UPR), j = (int)(u - (int64_t)r * UPR);
+  int64_t soff = 0;
+  const int64_t off = pf_row_off<D, T, PAGED>(a, h, a.T0 + r, soff) + 8 * j;
+  const void* base = kv ? a.v : a.k;
+  float x[8];
+  if constexpr (Q8) {
+    const uint2 c = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(base) + off);
+    const float s = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + soff);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      x[e] = (float)(int8_t)(((e < 4 ? c.x : c.y) >> (8 * (e & 3))) & 0xFF) * s;
+  } else {
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + off);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + off + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = x0[e];
+      x[4 + e] = x1[e];
+    }
+  }
+  uint32_t pc[3][4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) split3x2(x[e], x[e + 1], pc[0][e / 2], pc[1][e / 2], pc[2][e / 2]);
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+    *reinterpret_cast<u32x4*>(out + ((((int64_t)kv * a.nkv + h) * 3 + p) * a.R + r) * D + 8 * j) =
+        u32x4{pc[p][0], pc[p][1], pc[p][2], pc[p][3]};
+}
 
 // Waves per prefill workgroup (16 query rows each): 8, so that 128 rows
 // share each staged key tile and its split into pieces (32q/8kv/d128 fp32,
@@ -2294,11 +2374,12 @@ __host__ __device__ constexpr int pf_waves(int D, int esz) { return D == 256 && 
 // next column in lanes 8..15 (128 contiguous bytes of each of 8 rows per 64
 // lanes), so every LDS store of a piece is conflict-free too.
 // D = 256 stages 100 KB (fp32 pieces) and runs one workgroup per CU.
-template <int D, typename T, bool PAGED, int PW>
+template <int D, typename T, bool PAGED, int PW, bool PRE = false>
 __global__ __launch_bounds__(64 * PW, PW == 4 && D < 256 ? 2 : 1)
 void prefill_mfma16_kernel(PfArgs a) {
   static_assert(D == 64 || D == 128 || D == 256, "bf16-piece prefill: D = 64, 128, 256");
   static_assert(PW == 4 || PW == 8, "4 or 8 waves");
+  static_assert(!PRE || (sizeof(T) == 4 && !PAGED), "PRE: one instance per D and PW (pieces)");
   constexpr int NT = 64 * PW, QB = NT / 4;
   constexpr int KT = 32, KH = 2;
   constexpr int KP = sizeof(T) == 2 ? 1 : 3;  // staged pieces of K and V
@@ -2374,24 +2455,34 @@ void prefill_mfma16_kernel(PfArgs a) {
   };
   const T* Kb = reinterpret_cast<const T*>(a.k);
   const T* Vb = reinterpret_cast<const T*>(a.v);
-  const int pg = 1 << a.page_shift;
-  const int64_t R = (int64_t)a.nkv * D + ((4 * a.nkv + 15) & ~15);
-  const int64_t BB = (int64_t)a.nkv * pg * (D + 4);
   auto row_off = [&](int t, int64_t& soff) -> int64_t {
-    if constexpr (PAGED) {
-      const int64_t blk = a.block_table[t >> a.page_shift];
-      const int sl = t & (pg - 1);
-      if constexpr (Q8) {
-        soff = blk * BB + (int64_t)a.nkv * pg * D + 4 * ((int64_t)h * pg + sl);
-        return blk * BB + ((int64_t)h * pg + sl) * D;
-      }
-      return (blk * a.nkv + h) * pg * D + (int64_t)sl * D;
-    } else {
-      if constexpr (Q8) {
-        soff = (int64_t)t * R + (int64_t)a.nkv * D + 4 * h;
-        return (int64_t)t * R + (int64_t)h * D;
-      }
-      return (int64_t)t * a.nkv * D + (int64_t)h * D;
+    return pf_row_off<D, T, PAGED>(a, h, t, soff);
+  };
+  // PRE: the tile's pieces straight from the split workspace into LDS, with
+  // global_load_lds_dwordx4: lane l of a wave's load lands at the 16 bytes
+  // base + 16*l of a 1 KB block (checked on the GPU), so lane l loads the
+  // unit the swizzled layout keeps there (unit ch of key r at ch ^ f(r):
+  // slot j holds unit j ^ f(r)).  No registers and no arithmetic per element.
+  auto dload = [&](int tk, char* kbuf, char* vbuf) {
+    constexpr int UPR = D / 8;             // 16-byte units per row
+    constexpr int KPB = 64 / UPR;          // keys per 1 KB block
+    constexpr int BPP = KT / KPB;          // blocks per piece
+    constexpr int NBL = 2 * 3 * BPP;       // blocks per tile (K, V; 3 pieces)
+    const int r_in = lane / UPR, jpos = lane % UPR;
+#pragma unroll
+    for (int bi0 = 0; bi0 < NBL; bi0 += PW) {
+      const int bi = bi0 + w;  // wave-uniform
+      if (NBL % PW != 0 && bi >= NBL) break;
+      const int kv = bi / (3 * BPP), rem = bi - kv * 3 * BPP;
+      const int pc = rem / BPP, kb = rem - pc * BPP;
+      const int r = kb * KPB + r_in;
+      const int ch = jpos ^ (kv ? vt_f<D>(r) : kt_f<D>(r));
+      const int t = min(tk + r, kt_hi - 1) - a.T0;
+      const uint16_t* src =
+          a.pieces + ((((int64_t)kv * a.nkv + h) * 3 + pc) * a.R + t) * D + 8 * ch;
+      char* dst = (kv ? vbuf : kbuf) + pc * KT * (2 * D) + kb * 1024;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0,
+                                       0);
     }
   };
   typename KVT<T>::vec kreg[CPT], vreg[CPT];
@@ -2461,14 +2552,27 @@ void prefill_mfma16_kernel(PfArgs a) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-  if (ntile > 0) load_tile(kt_lo);
+  if constexpr (PRE) {
+    if (ntile > 0) dload(kt_lo, kp_buf[0], vp_buf[0]);
+    wait_vmcnt<0>();  // this wave's direct loads are in LDS
+    __syncthreads();
+  } else {
+    if (ntile > 0) load_tile(kt_lo);
+  }
   for (int it = 0; it < ntile; ++it) {
     const int tk = kt_lo + it * KT;
-    const char* kp_s = kp_buf[NBUF == 2 ? (it & 1) : 0];
-    const char* vp_s = vp_buf[NBUF == 2 ? (it & 1) : 0];
-    store_tile(kp_buf[NBUF == 2 ? (it & 1) : 0], vp_buf[NBUF == 2 ? (it & 1) : 0]);
-    __syncthreads();
-    if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
+    const int bf = NBUF == 2 ? (it & 1) : 0;
+    const char* kp_s = kp_buf[bf];
+    const char* vp_s = vp_buf[bf];
+    if constexpr (PRE) {
+      // the other buffer was last read in the previous tile, which every
+      // wave finished before the barrier that ended it
+      if (NBUF == 2 && it + 1 < ntile) dload(tk + KT, kp_buf[bf ^ 1], vp_buf[bf ^ 1]);
+    } else {
+      store_tile(kp_buf[bf], vp_buf[bf]);
+      __syncthreads();
+      if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
+    }
     // scores of the two 16-key halves, smallest piece products first; even
     // and odd 32-element steps into separate accumulators (four independent
     // MFMA chains, added at the end)
@@ -2573,7 +2677,16 @@ void prefill_mfma16_kernel(PfArgs a) {
         o[dt] = mfma_bf16(av[0], ph, o[dt]);
       }
     }
-    if constexpr (NBUF == 1) __syncthreads();  // the tile's LDS is rewritten next
+    if constexpr (PRE) {
+      if constexpr (NBUF == 1) {
+        __syncthreads();  // every wave is done with the buffer
+        if (it + 1 < ntile) dload(tk + KT, kp_buf[0], vp_buf[0]);
+      }
+      wait_vmcnt<0>();  // this wave's direct loads of the next tile are in LDS
+      __syncthreads();
+    } else {
+      if constexpr (NBUF == 1) __syncthreads();  // the tile's LDS is rewritten next
+    }
   }
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
@@ -2880,6 +2993,35 @@ int workspace(void* stream, size_t bytes, int** ctr, void** out) {
   }
   *ctr = reinterpret_cast<int*>(w.ptr);
   *out = reinterpret_cast<char*>(w.ptr) + kCtrBytes;
+  return 0;
+}
+
+// Per-(device, stream) workspace of the prefill's pre-split K/V pieces,
+// grown to at least twice its last size (so the retired buffers, which a
+// captured graph may still point at, total less than the live one).  Under
+// stream capture it cannot grow: the caller then splits per tile instead.
+std::map<WsKey, WsBuf> g_pieces_ws;
+
+int pieces_workspace(void* stream, size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  std::lock_guard<std::mutex> lk(g_ws_mu);
+  WsBuf& w = g_pieces_ws[WsKey{dev, stream}];
+  if (!w.ptr || w.bytes < bytes) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing((hipStream_t)stream, &cap);
+    if (e != hipSuccess) return (int)e;
+    if (cap != hipStreamCaptureStatusNone) return MOLOT_ENOWS;
+    const size_t want = std::max(bytes, 2 * w.bytes);
+    void* p = nullptr;
+    e = hipMalloc(&p, want);
+    if (e != hipSuccess) return (int)e;
+    if (w.ptr) g_retired.push_back(w.ptr);
+    w.ptr = p;
+    w.bytes = want;
+  }
+  *out = w.ptr;
   return 0;
 }
 
@@ -3382,11 +3524,9 @@ struct Norms {
 
 bool norms_ok(const Norms& nm) { return nm.eps >= 0.f && nm.eps < INFINITY; }
 
-}  // namespace
-
-// ===========================================================================
-// C ABI
 using PfFn = void (*)(PfArgs);
+constexpr size_t kMaxPiecesBytes = (size_t)1 << 30;  // the prefill's pre-split workspace
+std::atomic<int> g_presplit{1};  // molot_hip_set_prefill_presplit
 
 template <int D, typename T, bool PAGED>
 PfFn pf_kernel_w(int pw) {
@@ -3403,6 +3543,26 @@ PfFn pf_kernel_d(int d, int pw) {
   return nullptr;  // Q8 prefill: d = 64, 128
 }
 
+// The prefill kernel over pre-split pieces (any cache type but bf16).
+PfFn pf_kernel_pre(int d, int pw) {
+  if (d == 64) return pw == 8 ? prefill_mfma16_kernel<64, float, false, 8, true>
+                              : prefill_mfma16_kernel<64, float, false, 4, true>;
+  if (d == 128) return pw == 8 ? prefill_mfma16_kernel<128, float, false, 8, true>
+                               : prefill_mfma16_kernel<128, float, false, 4, true>;
+  return prefill_mfma16_kernel<256, float, false, 4, true>;
+}
+
+using SplitFn = void (*)(PfArgs, uint16_t*);
+SplitFn pf_split(int d, int kv_dtype, bool paged) {
+  if (kv_dtype == MOLOT_KV_Q8) {
+    if (d == 64) return paged ? pf_split_kernel<64, q8_t, true> : pf_split_kernel<64, q8_t, false>;
+    return paged ? pf_split_kernel<128, q8_t, true> : pf_split_kernel<128, q8_t, false>;
+  }
+  if (d == 64) return paged ? pf_split_kernel<64, float, true> : pf_split_kernel<64, float, false>;
+  if (d == 128) return paged ? pf_split_kernel<128, float, true> : pf_split_kernel<128, float, false>;
+  return paged ? pf_split_kernel<256, float, true> : pf_split_kernel<256, float, false>;
+}
+
 // The prefill kernel of a head dim (64, 128, 256), cache type, layout and
 // wave count (pw: 4, or 8 where the instance has it).
 PfFn pf_kernel(int d, int kv_dtype, bool paged, int pw) {
@@ -3413,6 +3573,10 @@ PfFn pf_kernel(int d, int kv_dtype, bool paged, int pw) {
   return paged ? pf_kernel_d<bf16_t, true>(d, pw) : pf_kernel_d<bf16_t, false>(d, pw);
 }
 
+}  // namespace
+
+// ===========================================================================
+// C ABI
 extern "C" {
 
 const char* molot_hip_strerror(int status) {
@@ -3514,6 +3678,8 @@ int molot_hip_profile_end(float* attn_ms, float* combine_ms, int* launches, int*
 void molot_hip_set_tuning(int wgs_per_cu) { g_wgs_per_cu = wgs_per_cu > 0 ? wgs_per_cu : 0; }
 
 void molot_hip_set_merge(int in_launch) { g_merge = in_launch < 0 ? -1 : (in_launch ? 1 : 0); }
+
+void molot_hip_set_prefill_presplit(int on) { g_presplit = on ? 1 : 0; }
 
 int molot_hip_rope_apply(float* x, int nheads, int d, int pos, const float* inv_freq,
                          void* stream) {
@@ -3924,8 +4090,34 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
       return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
-  const PfFn pk = pf_kernel(d, kv_dtype, block_row != nullptr, pw);
+  PfFn pk = pf_kernel(d, kv_dtype, block_row != nullptr, pw);
   if (!pk) return MOLOT_ENOTSUP;
+  // fp32 and Q8 caches: split the attended keys into bf16 pieces once
+  // (pf_split_kernel), and let the attention kernel copy them into LDS.
+  // Every query attends keys in [t0(query 0), N).  Not under stream capture
+  // when the workspace would have to grow, nor past kMaxPiecesBytes: the
+  // kernel then splits each staged tile itself.
+  if (kv_dtype != MOLOT_KV_BF16 && g_presplit.load(std::memory_order_relaxed)) {
+    const int T0 = window > 0 && pos0 - window + 1 > 0 ? std::min(pos0 - window + 1, N) : 0;
+    const int64_t R = (int64_t)N - T0;
+    const size_t need = (size_t)2 * nkv * 3 * R * d * sizeof(uint16_t);
+    void* ws = nullptr;
+    st = R > 0 && need <= kMaxPiecesBytes ? pieces_workspace(stream, need, &ws) : MOLOT_ENOWS;
+    if (st && st != MOLOT_ENOWS) return st;
+    if (!st) {
+      a.pieces = reinterpret_cast<const uint16_t*>(ws);
+      a.T0 = T0;
+      a.R = (int)R;
+      const int64_t units = R * (d / 8);
+      hipLaunchKernelGGL(pf_split(d, kv_dtype, block_row != nullptr),
+                         dim3((unsigned)((units + 255) / 256), nkv, 2), dim3(256), 0,
+                         (hipStream_t)stream, a, reinterpret_cast<uint16_t*>(ws));
+      st = (int)hipGetLastError();
+      if (st) return st;
+      pk = pf_kernel_pre(d, pw);
+    }
+    st = 0;
+  }
   const dim3 grid((unsigned)(nqb * nkv));
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {

@@ -82,6 +82,7 @@ _VOID = {
     "molot_hip_set_split_chunk": [_I],
     "molot_hip_set_tuning": [_I],
     "molot_hip_set_merge": [_I],
+    "molot_hip_set_prefill_presplit": [_I],
     "molot_hip_set_block_order": [_I],
     "molot_hip_set_bf16_path": [_I],
 }

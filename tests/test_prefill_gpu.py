@@ -211,6 +211,98 @@ def test_prefill_step_paged_matches_contiguous(gpu, nq, nkv, d, bf16):
     assert normwise_err(host(Oc), R) < TOL
 
 
+def _prefill_both(run):
+    """run() with the keys split once per launch (the default) and per
+    staged tile; returns both outputs."""
+    try:
+        attn.set_prefill_presplit(True)
+        o1 = run()
+        attn.set_prefill_presplit(False)
+        o0 = run()
+    finally:
+        attn.set_prefill_presplit(True)
+    return o1, o0
+
+
+@pytest.mark.parametrize("nq,nkv,d,M,N,pos0,window,kv", [
+    (32, 8, 128, 300, 1300, 1000, 0, "f32"),    # 8 waves, two tile buffers
+    (8, 4, 256, 70, 3070, 3000, 1024, "f32"),   # fp32 d256: 4 waves, one buffer, window
+    (32, 2, 64, 40, 90, 50, 0, "f32"),          # d64
+    (8, 2, 128, 5, 40, 35, 0, "f32"),           # few rows: the 4-wave grid
+    (8, 4, 256, 33, 233, 200, 37, "f32"),       # window cutting inside a tile
+    (32, 8, 128, 77, 1077, 1000, 0, "q8"),
+    (8, 2, 64, 50, 3050, 3000, 1024, "q8"),
+])
+def test_prefill_presplit_matches_per_tile(gpu, nq, nkv, d, M, N, pos0, window, kv):
+    """fp32 and Q8 caches: the keys split into bf16 pieces once per launch
+    (pf_split_kernel) and copied into LDS by direct loads give the bits of
+    the per-tile split (the same pieces, the same products), and the
+    oracle's result."""
+    announce(f"presplit {nq}/{nkv}/{d} M={M} N={N} pos0={pos0} win={window} {kv}")
+    st = Stream(M + N + 3 * d + nq)
+    Q = st.normal((M, nq, d))
+    if kv == "q8":
+        K, V = (oracle.q8_cache(st.normal((N, nkv * d)), nkv, d) for _ in range(2))
+        Kd, Vd = (torch.from_numpy(np.ascontiguousarray(x, dtype=np.uint8)).cuda() for x in (K, V))
+    else:
+        K, V = cache(st, N, nkv, d, False)
+        Kd, Vd = dev(K), dev(V)
+    s = 1 / math.sqrt(d)
+    Qd = dev(Q)
+
+    def run():
+        O = torch.full((M, nq, d), float("nan"), device="cuda")
+        attn.attn_prefill_gqa(Qd, Kd, Vd, O, nq, nkv, M, N, d, s, pos0, window)
+        return host(O)
+
+    o1, o0 = _prefill_both(run)
+    assert np.array_equal(o1, o0)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, window)
+    err = normwise_err(o1, R)
+    print(f"presplit normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
+@pytest.mark.parametrize("d,q8", [(128, False), (256, False), (64, True)])
+def test_prefill_presplit_paged(gpu, d, q8):
+    """The paged prefill over shuffled pages: pieces gathered through the
+    block table once per launch, the same bits as the per-tile split."""
+    announce(f"presplit paged d={d} q8={q8}")
+    st = Stream(300 + d + q8)
+    nq, nkv, M, n0, page, spare = 16, 4, 60, 400, 16, 3
+    N = n0 + M
+    nb = (N + page - 1) // page
+    nblk = nb + spare
+    row = st.permutation(nblk)[:nb].astype(np.int32)
+    Q = st.normal((M, nq, d))
+    if q8:
+        rb = oracle.q8_block_bytes(nkv, d, page)
+        Kp = np.zeros((nblk, rb), np.uint8)
+        Vp = np.zeros((nblk, rb), np.uint8)
+        for X in (Kp, Vp):
+            codes = np.clip(np.rint(st.normal((nblk, nkv, page, d)) * 32), -127, 127).astype(np.int8)
+            scales = (np.abs(st.normal((nblk, nkv, page))) * 0.03 + 0.01).astype(np.float32)
+            X[:, :nkv * page * d] = codes.reshape(nblk, -1).view(np.uint8)
+            X[:, nkv * page * d:nkv * page * d + 4 * nkv * page] = scales.reshape(nblk, -1).view(np.uint8)
+        Kd, Vd = (torch.from_numpy(x).cuda() for x in (Kp, Vp))
+    else:
+        Kp = st.normal((nblk, nkv * page * d))
+        Vp = st.normal((nblk, nkv * page * d))
+        Kd, Vd = dev(Kp), dev(Vp)
+    bt = torch.from_numpy(row).cuda()
+    s = 1 / math.sqrt(d)
+    Qd = dev(Q)
+
+    def run():
+        O = torch.full((M, nq, d), float("nan"), device="cuda")
+        attn.attn_prefill_paged(Qd, Kd, Vd, O, bt, nb, page, nq, nkv, M, N, d, s, n0, 0)
+        return host(O)
+
+    o1, o0 = _prefill_both(run)
+    assert np.isfinite(o1).all()
+    assert np.array_equal(o1, o0)
+
+
 def test_prefill_2k_prompt(gpu):
     """A 2048-token prompt at the headline head shape (the bench workload)."""
     announce("prefill 32q/8kv/d128 M=2048 fresh")
