@@ -368,6 +368,165 @@ __global__ void rope_append_kernel(RopeArgs a) {
   }
 }
 
+// The prefill's RoPE/append (and the q prologue): one workgroup of 4 waves
+// per token instead of one per (head, token).  The token's sine and cosine
+// are taken once (in double, as rope_append_kernel) into LDS; wave w takes
+// heads w, w + 4, ..., lane l the pairs l, l + 64, ... of a head, so a head's
+// norm sum and Q8 maximum stay in its wave.  Sums run as rope_append_kernel's
+// (per 64 pairs, added in order), so rows of d <= 128 come out bit-identical.
+// 2048 tokens of 32q/8kv/d128: 81920 single-wave workgroups became 2048.
+constexpr int kRopeTokThreads = 256;
+constexpr int kRopeMaxPairs = 1024;  // d <= 2048
+template <int KMAX>  // pair groups of 64 a head holds at most (d <= 128 KMAX)
+__global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeArgs a) {
+  __shared__ float cs_s[kRopeMaxPairs], sn_s[kRopeMaxPairs];
+  __shared__ float sh[16];
+  const int b = blockIdx.x;
+  const int half = a.d >> 1;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int pos = a.pos + b, slot = a.slot + b;
+  const bool rot = a.inv_freq != nullptr;
+  for (int i = tid; rot && i < half; i += kRopeTokThreads) {
+    const float ang = (float)pos * a.inv_freq[i];
+    double sd, cd;
+    sincos((double)ang, &sd, &cd);
+    cs_s[i] = (float)cd;
+    sn_s[i] = (float)sd;
+  }
+  auto rms_inv = [&](float ss, int n) { return 1.0f / sqrtf(ss / (float)n + a.eps); };
+  // the v norm: one RMS over the token's nkv*d values (wave 0, stride 64)
+  if (a.append && a.v_norm && w == 0) {
+    const float* vall = a.v_new + (int64_t)b * a.nkv * a.d;
+    float part = 0.f;
+    for (int j = lane; j < a.nkv * a.d; j += 64) part = fmaf(vall[j], vall[j], part);
+    part = group_sum<64>(part);
+    if (lane == 0) sh[0] = rms_inv(part, a.nkv * a.d);
+  }
+  __syncthreads();
+  const float vinv = a.append && a.v_norm ? sh[0] : 1.f;
+  const int nk = (half + 63) / 64;  // pair groups of 64 per head
+  for (int hh = w; hh < a.nq + a.nkv; hh += kRopeTokThreads / 64) {
+    if (hh < a.nq) {
+      if (!a.q) continue;
+      float* x = a.q + ((int64_t)b * a.nq + hh) * a.d;
+      float x0[KMAX], x1[KMAX];
+      float ss = 0.f;
+      #pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k >= nk) break;
+        const int j = lane + 64 * k;
+        x0[k] = j < half ? x[j] : 0.f;
+        x1[k] = j < half ? x[j + half] : 0.f;
+        if (a.q_norm) ss += group_sum<64>(x0[k] * x0[k] + x1[k] * x1[k]);
+      }
+      const float inv = a.q_norm ? rms_inv(ss, a.d) : 1.f;
+      #pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k >= nk) break;
+        const int j = lane + 64 * k;
+        if (j >= half) continue;
+        float y0 = x0[k], y1 = x1[k];
+        if (a.q_norm) {
+          y0 = y0 * inv * a.q_norm[j];
+          y1 = y1 * inv * a.q_norm[j + half];
+        }
+        x[j] = rot ? y0 * cs_s[j] - y1 * sn_s[j] : y0;
+        x[j + half] = rot ? y0 * sn_s[j] + y1 * cs_s[j] : y1;
+      }
+      continue;
+    }
+    if (!a.append) continue;
+    const int kh = hh - a.nq;
+    const float* kx = a.k_new + ((int64_t)b * a.nkv + kh) * a.d;
+    const float* vx = a.v_new + ((int64_t)b * a.nkv + kh) * a.d;
+    float r0[KMAX], r1[KMAX], v0[KMAX], v1[KMAX];
+    float ss = 0.f;
+    #pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k >= nk) break;
+      const int j = lane + 64 * k;
+      r0[k] = j < half ? kx[j] : 0.f;
+      r1[k] = j < half ? kx[j + half] : 0.f;
+      v0[k] = j < half ? vx[j] * vinv : 0.f;
+      v1[k] = j < half ? vx[j + half] * vinv : 0.f;
+      if (a.k_norm) ss += group_sum<64>(r0[k] * r0[k] + r1[k] * r1[k]);
+    }
+    const float kinv = a.k_norm ? rms_inv(ss, a.d) : 1.f;
+    float kmax = 0.f, vmax = 0.f;
+    #pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k >= nk) break;
+      const int j = lane + 64 * k;
+      const int jc = j < half ? j : 0;
+      float k0 = r0[k], k1 = r1[k];
+      if (a.k_norm) {
+        k0 = k0 * kinv * a.k_norm[jc];
+        k1 = k1 * kinv * a.k_norm[jc + half];
+      }
+      r0[k] = rot ? k0 * cs_s[jc] - k1 * sn_s[jc] : k0;  // 0 past the pairs
+      r1[k] = rot ? k0 * sn_s[jc] + k1 * cs_s[jc] : k1;
+      kmax = fmaxf(kmax, fmaxf(fabsf(r0[k]), fabsf(r1[k])));
+      vmax = fmaxf(vmax, fmaxf(fabsf(v0[k]), fabsf(v1[k])));
+    }
+    float ks = 0.f, vs = 0.f;
+    if (a.kv_dtype == MOLOT_KV_Q8) {
+      ks = q8_scale(group_max<64>(kmax));
+      vs = q8_scale(group_max<64>(vmax));
+    }
+    int64_t off, soff;
+    if (a.block_table) {
+      const int64_t blk = a.block_table[slot / a.page];
+      off = blk * a.block_stride + (int64_t)kh * a.head_stride + (int64_t)(slot % a.page) * a.tok_stride;
+      soff = blk * a.block_stride + a.sc_off + kh * a.sc_head + 4 * (int64_t)(slot % a.page);
+    } else {
+      off = (int64_t)slot * a.tok_stride + (int64_t)kh * a.head_stride;
+      soff = (int64_t)slot * a.tok_stride + a.sc_off + kh * a.sc_head;
+    }
+    #pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      if (k >= nk) break;
+      const int j = lane + 64 * k;
+      if (j >= half) continue;
+      if (a.kv_dtype == MOLOT_KV_Q8) {
+        int8_t* kd = (int8_t*)a.K + off;
+        int8_t* vd = (int8_t*)a.V + off;
+        kd[j] = (int8_t)q8_code(r0[k], ks);
+        kd[j + half] = (int8_t)q8_code(r1[k], ks);
+        vd[j] = (int8_t)q8_code(v0[k], vs);
+        vd[j + half] = (int8_t)q8_code(v1[k], vs);
+      } else if (a.kv_dtype == MOLOT_KV_F32) {
+        float* kd = (float*)a.K + off;
+        float* vd = (float*)a.V + off;
+        kd[j] = r0[k];
+        kd[j + half] = r1[k];
+        vd[j] = v0[k];
+        vd[j + half] = v1[k];
+      } else {
+        uint16_t* kd = (uint16_t*)a.K + off;
+        uint16_t* vd = (uint16_t*)a.V + off;
+        kd[j] = f32_to_bf16(r0[k]);
+        kd[j + half] = f32_to_bf16(r1[k]);
+        vd[j] = f32_to_bf16(v0[k]);
+        vd[j + half] = f32_to_bf16(v1[k]);
+      }
+    }
+    if (a.kv_dtype == MOLOT_KV_Q8 && lane == 0) {
+      *(float*)((char*)a.K + soff) = ks;
+      *(float*)((char*)a.V + soff) = vs;
+    }
+  }
+}
+
+// rope_append_tok_kernel for M tokens of head dim d (<= 2048).
+int launch_rope_tok(const RopeArgs& r, int M, void* stream) {
+  const int half = r.d / 2;
+  auto k = half <= 64 ? rope_append_tok_kernel<1>
+           : half <= 128 ? rope_append_tok_kernel<2>
+                         : rope_append_tok_kernel<kRopeMaxPairs / 64>;
+  hipLaunchKernelGGL(k, dim3(M), dim3(kRopeTokThreads), 0, (hipStream_t)stream, r);
+  return (int)hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Fused decode attention.
 //
@@ -4185,9 +4344,7 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   r.k_norm = nm.k;
   r.v_norm = nm.v;
   r.eps = nm.eps;
-  hipLaunchKernelGGL(rope_append_kernel, dim3(nq + nkv, M), dim3(((d / 2) + 63) / 64 * 64), 0,
-                     (hipStream_t)stream, r);
-  st = (int)hipGetLastError();
+  st = launch_rope_tok(r, M, stream);
   if (st) return st;
   return attn_prefill_impl(q, K, V, O, nq, nkv, M, slot0 + M, d, scale, pos0, window, kv_dtype,
                            block_row, page, stream);
@@ -4234,9 +4391,7 @@ static int q_prologue(float* q, int nq, int d, int M, int pos0, const float* q_n
   r.tokens = 1;
   r.q_norm = q_norm;
   r.eps = eps;
-  hipLaunchKernelGGL(rope_append_kernel, dim3(nq, M), dim3(((d / 2) + 63) / 64 * 64), 0,
-                     (hipStream_t)stream, r);
-  return (int)hipGetLastError();
+  return launch_rope_tok(r, M, stream);
 }
 
 int molot_hip_prefill_q(float* q, int nq, int d, int M, int pos0, const float* q_norm, float eps,
