@@ -1167,6 +1167,12 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     z = (int)(blockIdx.x >> 3);
     hs = s8 % X;
     b = s8 / X;
+  } else if (a.chunk_fast) {  // Q8: a chunk's heads on one XCD, as attn_mfma_kernel
+    const int k = (int)(blockIdx.x >> 3);
+    const int pi = (k / X) * 8 + (int)(blockIdx.x & 7);  // padded ids (z >= nchunks) exit below
+    z = pi / a.nseq;
+    b = pi - z * a.nseq;
+    hs = k % X;
   }
   const int sub = hs % nsub;
   const int h = hs / nsub;
@@ -3502,6 +3508,9 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
 
 template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD, typename C>
 int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
+  // Q8 (d = 256): the heads of a token share 128-byte lines (see launch_pair)
+  a.chunk_fast = sizeof(T) == 1;
+  a.nseq = B;
   // contiguous caches: 32-row groups dealt round robin (the kernel's gmap)
   int st = plan_launch(a, D, span, GH, nsubs, B, PAGED ? C::RB : 32, 1, stream, !PAGED);
   if (st) return st;

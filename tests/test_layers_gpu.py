@@ -275,6 +275,26 @@ def test_shared_prefill_paged_matches_contiguous(gpu, rope):
     assert normwise_err(host(Oc), R) < FP32_TOL
 
 
+@pytest.mark.parametrize("d,norm,rope", [(512, True, True), (2048, True, False),
+                                         (300, False, True), (192, True, True), (64, True, True)])
+def test_prefill_q_head_dims(gpu, d, norm, rope):
+    """molot_hip_prefill_q at any even d up to 2048 (one 4-wave workgroup per
+    token; lane l of a head's wave takes pairs l, l + 64, ...; instances for
+    up to 64, 128 and 1024 pairs), with and without the norm and the
+    rotation, against the oracle."""
+    announce(f"prefill_q d={d} norm={norm} rope={rope}")
+    st = Stream(500 + d)
+    nq, M, pos0 = 4, 37, 1000
+    q = st.normal((M, nq, d))
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32) if norm else None
+    inv = oracle.rope_inv_freq(10000.0, d) if rope else None
+    qd = dev(q)
+    attn.prefill_q(qd, nq, d, M, pos0, None if inv is None else dev(inv),
+                   q_norm=None if qn is None else dev(qn))
+    q_ref = oracle.prefill_q(q, nq, d, M, pos0, qn, 1e-6, inv)
+    np.testing.assert_allclose(host(qd), q_ref, rtol=2e-6, atol=4e-6)
+
+
 def test_shared_step_equals_owning_step(gpu):
     """After the owning layer's fused step appended this token, a layer
     sharing its cache (same q, norm and table) gets the owning layer's O
