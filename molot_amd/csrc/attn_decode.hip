@@ -3506,6 +3506,17 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   return (int)hipGetLastError();
 }
 
+// A planned launch of attn_kernel with configuration C.
+template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD, typename C>
+int launch_planned(AttnArgs a, int nsubs, int B, void* stream) {
+  if (a.mrg && sizeof(float) * (size_t)Lds(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED,
+                                           a.mrg).total > 65536)
+    no_merge(a);  // the merge's statistics do not fit beside the kernel's LDS
+  const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED, a.mrg);
+  return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, PAD, C>, C::NT, sizeof(float) * (size_t)L.total,
+                     a, GH, D, nsubs, B, PAGED, ROPE, stream);
+}
+
 template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD, typename C>
 int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
   // Q8 (d = 256): the heads of a token share 128-byte lines (see launch_pair)
@@ -3514,12 +3525,15 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
   // contiguous caches: 32-row groups dealt round robin (the kernel's gmap)
   int st = plan_launch(a, D, span, GH, nsubs, B, PAGED ? C::RB : 32, 1, stream, !PAGED);
   if (st) return st;
-  if (a.mrg && sizeof(float) * (size_t)Lds(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED,
-                                           a.mrg).total > 65536)
-    no_merge(a);  // the merge's statistics do not fit beside the kernel's LDS
-  const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED, a.mrg);
-  return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, PAD, C>, C::NT, sizeof(float) * (size_t)L.total,
-                     a, GH, D, nsubs, B, PAGED, ROPE, stream);
+  if constexpr (sizeof(T) == 1 && C::NW > 8) {
+    // Q8 chunks of at most 4 blocks a wave on 8 waves: a 1024-token window
+    // of 8q/4kv/d256 (32-row chunks) 14.45 -> 10.9 us per step; 512-row
+    // chunks (32k tokens, no window) stay on 16 waves (26.0 against 27.8 us)
+    if (a.chunk <= 8 * 4 * C::RB)
+      return launch_planned<D, GH, T, PAGED, ROPE, PAD,
+                            Cfg<D, GH, T, C::LPR, C::RB, 8, C::NBUF>>(a, nsubs, B, stream);
+  }
+  return launch_planned<D, GH, T, PAGED, ROPE, PAD, C>(a, nsubs, B, stream);
 }
 
 // bf16 or Q8 KV, D = 64 or 128: the matrix-core kernel.  Workgroups per CU
