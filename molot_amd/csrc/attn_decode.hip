@@ -2442,6 +2442,13 @@ struct PfArgs {
   // the kernel splits each staged tile itself
   const uint16_t* pieces;
   int T0, R;
+  // split-K over the key tiles (nsplit > 1): split s of a query block takes
+  // its share of the tiles and writes unnormalised o and (max, sum) per query
+  // row, slot m*nq + head, to part_o [slot][nsplit][D] and part_ml
+  // [slot][nsplit][2]; combine_kernel merges them into O
+  int nsplit;
+  float* part_o;
+  float* part_ml;
 };
 
 // Cache offset (elements of T; Q8: bytes) of row t of KV head h, and for Q8
@@ -2568,7 +2575,9 @@ void prefill_mfma16_kernel(PfArgs a) {
 
   const int G = a.nq / a.nkv;
   const int h = blockIdx.x % a.nkv;  // heads fastest: every XCD gets every head's share
-  const int qb = a.nqb - 1 - (int)(blockIdx.x / a.nkv);  // latest rows (most keys) first
+  const int rest = (int)(blockIdx.x / a.nkv);
+  const int sp = rest % a.nsplit;               // key split
+  const int qb = a.nqb - 1 - rest / a.nsplit;  // latest rows (most keys) first
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, g4 = lane >> 4;
@@ -2583,7 +2592,11 @@ void prefill_mfma16_kernel(PfArgs a) {
   auto nn_of = [&](int m) { return a.pos0 + m + 1 < a.N ? a.pos0 + m + 1 : a.N; };
   const int kt_lo = t0_of(r0 / G);
   const int kt_hi = nn_of(rl / G);
-  const int ntile = kt_hi > kt_lo ? (kt_hi - kt_lo + KT - 1) / KT : 0;
+  const int ntile_all = kt_hi > kt_lo ? (kt_hi - kt_lo + KT - 1) / KT : 0;
+  // this split's tiles [tb0, tb0 + ntile) of the block's range
+  const int tb0 = (int)((int64_t)sp * ntile_all / a.nsplit);
+  const int ntile = (int)((int64_t)(sp + 1) * ntile_all / a.nsplit) - tb0;
+  const int kt_s = kt_lo + tb0 * KT;  // this split's first key
   const int row = r0 + 16 * w + c16;
   const bool rv = row < rows;
   const int m = rv ? row / G : 0;
@@ -2718,14 +2731,14 @@ void prefill_mfma16_kernel(PfArgs a) {
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
   if constexpr (PRE) {
-    if (ntile > 0) dload(kt_lo, kp_buf[0], vp_buf[0]);
+    if (ntile > 0) dload(kt_s, kp_buf[0], vp_buf[0]);
     wait_vmcnt<0>();  // this wave's direct loads are in LDS
     __syncthreads();
   } else {
-    if (ntile > 0) load_tile(kt_lo);
+    if (ntile > 0) load_tile(kt_s);
   }
   for (int it = 0; it < ntile; ++it) {
-    const int tk = kt_lo + it * KT;
+    const int tk = kt_s + it * KT;
     const int bf = NBUF == 2 ? (it & 1) : 0;
     const char* kp_s = kp_buf[bf];
     const char* vp_s = vp_buf[bf];
@@ -2855,7 +2868,16 @@ void prefill_mfma16_kernel(PfArgs a) {
   }
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
-  if (rv) {
+  if (rv && a.nsplit > 1) {  // the split's partial: unnormalised o, max in natural units, sum
+    const int64_t ps = ((int64_t)m * a.nq + h * G + g) * a.nsplit + sp;
+    float* po = a.part_o + ps * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * g4) = o[dt];
+    if (g4 == 0) {
+      a.part_ml[2 * ps] = m_run == -INFINITY ? -INFINITY : m_run * kLn2;
+      a.part_ml[2 * ps + 1] = l_run;
+    }
+  } else if (rv) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;  // no key: O = 0 (gemm.h:438)
     float* orow = a.o + qoff;
 #pragma unroll
@@ -2947,7 +2969,8 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
     const float M = wave_reduce<true>(mloc);
     float lloc = 0.f;
     for (int cc = t; cc < nch; cc += 64) {  // the lane's own LDS entries
-      const float wgt = softmax_exp(wts[cc] - M);
+      // a prefill row no split attended: M = -inf, weights 0, O = 0 below
+      const float wgt = M == -INFINITY ? 0.f : softmax_exp(wts[cc] - M);
       wts[cc] = wgt;
       lloc = fmaf(wgt, lsv[cc], lloc);
     }
@@ -2981,7 +3004,7 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
     const int h = y / a.nsub, sub = y - h * a.nsub;
     const int64_t oi = out_index((int64_t)b * a.nq + h * G + sub * a.gh, pair, a.d, a.dh);
     if (oi >= 0) {
-      a.o[oi] = o / s_l;
+      a.o[oi] = s_l > 0.f ? o / s_l : 0.f;
       if (a.rope && a.q_out) a.q_out[oi] = a.qrot[(int64_t)slot * P + pair];
     }
   }
@@ -4248,11 +4271,37 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     return MOLOT_EINVAL;
   const int64_t rows = (int64_t)M * (nq / nkv);
   const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1;
-  const int64_t rows8 = (rows + 127) / 128;
-  const int pw = pf_waves(d, esz) == 8 && rows8 * nkv >= num_cus() ? 8 : 4;
-  const int pf_threads = 64 * pw, qrows = pf_threads / 4;
-  const int64_t nqb = (rows + qrows - 1) / qrows;
-  if (nqb * nkv > (int64_t)0x7FFFFFFF) return MOLOT_ENOTSUP;
+  auto nqb_of = [&](int w) { return (rows + 16 * w - 1) / (16 * w); };
+  int pw = pf_waves(d, esz);
+  int64_t nqb = nqb_of(pw);
+  // A grid of fewer workgroups than CUs (few query rows over a long cache,
+  // e.g. a prompt chunk after a long context) splits each query block's key
+  // tiles over nsplit workgroups, at least 4 tiles each, and combine_kernel
+  // merges their partials (slots: one query row of one head).
+  int nsplit = 1;
+  float* part = nullptr;
+  if (nqb * nkv < num_cus() && (int64_t)M * nq <= 65535) {
+    const int last = pos0 + M - 1;  // the query attending the most keys
+    const int t0l = window > 0 && last - window + 1 > 0 ? std::min(last - window + 1, N) : 0;
+    const int64_t tiles = (std::min(last + 1, N) - t0l + 31) / 32;
+    const int64_t want = (num_cus() + nqb * nkv - 1) / (nqb * nkv);
+    nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({16, want, tiles / 4}));
+    if (nsplit > 1) {
+      int* ctr = nullptr;
+      void* ws = nullptr;
+      st = workspace(stream, sizeof(float) * (size_t)M * nq * nsplit * (d + 2), &ctr, &ws);
+      if (st && st != MOLOT_ENOWS) return st;
+      if (st) nsplit = 1;  // under capture the workspace cannot grow
+      else part = reinterpret_cast<float*>(ws);
+      st = 0;
+    }
+  }
+  if (nsplit == 1 && pw == 8 && nqb * nkv < num_cus()) {
+    pw = 4;  // no split: twice the workgroups on 4 waves
+    nqb = nqb_of(4);
+  }
+  const int pf_threads = 64 * pw;
+  if (nqb * nkv * nsplit > (int64_t)0x7FFFFFFF) return MOLOT_ENOTSUP;
   PfArgs a{};
   a.q = Qm;
   a.k = K;
@@ -4267,6 +4316,9 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   a.nqb = (int)nqb;
   a.scale = scale;
   a.block_table = block_row;
+  a.nsplit = nsplit;
+  a.part_o = part;
+  a.part_ml = part ? part + (size_t)M * nq * nsplit * d : nullptr;
   if (block_row) {
     if (page <= 0 || (page & (page - 1)) || !q8_pages_ok(nkv, page, kv_dtype))
       return MOLOT_EINVAL;
@@ -4300,15 +4352,40 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     }
     st = 0;
   }
-  const dim3 grid((unsigned)(nqb * nkv));
+  const dim3 grid((unsigned)(nqb * nkv * nsplit));
+  CombArgs cb{};  // split-K: (token, q head) rows as slots of one head each
+  cb.part_o = a.part_o;
+  cb.part_ml = a.part_ml;
+  cb.o = Om;
+  cb.nq = nq;
+  cb.nkv = nq;
+  cb.gh = 1;
+  cb.nsub = 1;
+  cb.d = d;
+  cb.dh = d;
+  cb.nchunks = nsplit;
+  cb.chunk = 1;
+  const dim3 cgrid((unsigned)(d / kCombPairs), (unsigned)((int64_t)M * nq));
+  const size_t clds = sizeof(float) * (size_t)comb_lds_floats(nsplit);
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {
-    ProfRec pr{prof_event(), prof_event(), nullptr, nullptr, false};
+    ProfRec pr{prof_event(), prof_event(), nullptr, nullptr, nsplit > 1};
     hipExtLaunchKernelGGL(pk, grid, dim3(pf_threads), 0, (hipStream_t)stream, pr.a0, pr.a1, 0, a);
+    st = (int)hipGetLastError();
+    if (!st && nsplit > 1) {
+      pr.c0 = prof_event();
+      pr.c1 = prof_event();
+      hipExtLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), clds, (hipStream_t)stream,
+                            pr.c0, pr.c1, 0, cb);
+      st = (int)hipGetLastError();
+    }
     g_prof.push_back(pr);
-  } else {
-    hipLaunchKernelGGL(pk, grid, dim3(pf_threads), 0, (hipStream_t)stream, a);
+    return st;
   }
+  hipLaunchKernelGGL(pk, grid, dim3(pf_threads), 0, (hipStream_t)stream, a);
+  st = (int)hipGetLastError();
+  if (st || nsplit == 1) return st;
+  hipLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), clds, (hipStream_t)stream, cb);
   return (int)hipGetLastError();
 }
 
