@@ -207,8 +207,17 @@ __device__ __forceinline__ float wave_reduce(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// exp used by the softmax (full-accuracy device expf).
+// exp used by the split-K merges (full-accuracy device expf).
 __device__ __forceinline__ float softmax_exp(float x) { return expf(x); }
+
+// The decode kernels' softmax runs in base 2: a score is q.k * scale*log2(e)
+// (the matrix-core kernel pre-scales q, the vector-ALU kernel each score), so
+// p = 2^(s - m) is one v_exp_f32 (relative error ~|s - m| * 2^-24, within
+// the reference's own exp, exp_avx512_ps at 1.5e-6).  The maxima leave the
+// kernels in natural units (m * ln 2) for the split-K merges.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------------------
 // RoPE + append.
@@ -1429,6 +1438,12 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 
   // q registers: lane s of a K row group holds elements (v*LPR + s)*VW + e
   float qr[GH][EPL];
+  // Base-2 scores: the dot products are scaled by scale*log2(e) as a whole
+  // (one rounding per score, as the natural-units scale), not through a
+  // pre-scaled q, whose per-element rounding perturbs q itself: with q
+  // channels 1000x the rest that was 1.7e-5 normwise off float64, outside
+  // the 1e-5 bar the score-scaled form meets.
+  const float qsc = a.scale * kLog2e;
 #pragma unroll
   for (int g = 0; g < GH; ++g)
 #pragma unroll
@@ -1487,7 +1502,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       const bool valid = rbase + k * RPS + rr < nrows;
 #pragma unroll
       for (int g = 0; g < GH; ++g) {
-        const float t = group_sum<LPR>(d[g]) * (Q8 ? a.scale * ksr[k] : a.scale);
+        const float t = group_sum<LPR>(d[g]) * (Q8 ? qsc * ksr[k] : qsc);
         sc[k][g] = valid ? t : -INFINITY;
         bmax[g] = fmaxf(bmax[g], sc[k][g]);
       }
@@ -1498,7 +1513,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int off = LPR; off < 64; off <<= 1) bmax[g] = fmaxf(bmax[g], __shfl_xor(bmax[g], off));
       const float mn = fmaxf(m_run[g], bmax[g]);
-      const float alpha = softmax_exp(m_run[g] - mn);  // m_run = -inf -> 0
+      const float alpha = exp2_hw(m_run[g] - mn);  // m_run = -inf -> 0
       m_run[g] = mn;
       l_run[g] *= alpha;
 #pragma unroll
@@ -1508,7 +1523,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     for (int k = 0; k < KS; ++k) {
       if (s == 0) {
 #pragma unroll
-        for (int g = 0; g < GH; ++g) pw[(k * RPS + rr) * GH + g] = softmax_exp(sc[k][g] - m_run[g]);
+        for (int g = 0; g < GH; ++g) pw[(k * RPS + rr) * GH + g] = exp2_hw(sc[k][g] - m_run[g]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -1626,10 +1641,10 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
-      const float snew = wave_reduce<false>(part[g]) * a.scale;
+      const float snew = wave_reduce<false>(part[g]) * qsc;
       const float mn = fmaxf(m_run[g], snew);
-      const float alpha = softmax_exp(m_run[g] - mn);
-      const float p = softmax_exp(snew - mn);
+      const float alpha = exp2_hw(m_run[g] - mn);
+      const float p = exp2_hw(snew - mn);
       m_run[g] = mn;
       l_run[g] = l_run[g] * alpha + p * one;
 #pragma unroll
@@ -1652,7 +1667,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   if (lane == 0) {
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
-      wm[w * GH + g] = m_run[g];
+      wm[w * GH + g] = m_run[g] * kLn2;  // natural units for the merges
       wl[w * GH + g] = l_run[g];
     }
   }
@@ -1738,18 +1753,11 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 constexpr int kMfmaWaves = 4;                  // waves per workgroup
 constexpr int kMfmaThreads = kMfmaWaves * 64;
 constexpr int kTile = 32;                      // cache rows per wave step
-// The matrix-core kernel's softmax runs in base 2: q is pre-scaled by
-// scale*log2(e), so a score is already x*log2(e) and p = 2^(s - m) is one
-// v_exp_f32 (relative error ~|s - m| * 2^-24, within the reference's own
-// exp, exp_avx512_ps at 1.5e-6).  Its running max moves only when a score
-// exceeds it by more than kLazyMax (p <= 2^8 otherwise): o and l always
-// share the max they were formed with, so the result is exact either way,
-// and most tiles skip the rescale.  The maxima leave the kernel in natural
-// units (m * ln 2) for the split-K merge.
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.6931471805599453f;
+// The matrix-core kernel's softmax runs in base 2 (kLog2e above).  Its
+// running max moves only when a score exceeds it by more than kLazyMax
+// (p <= 2^8 otherwise): o and l always share the max they were formed with,
+// so the result is exact either way, and most tiles skip the rescale.
 constexpr float kLazyMax = 8.f;
-__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int D>
 constexpr int kMfmaQStride = D + 4;
