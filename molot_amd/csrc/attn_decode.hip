@@ -218,6 +218,10 @@ __device__ __forceinline__ float softmax_exp(float x) { return expf(x); }
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+// A running max moves only when a score exceeds it by more than kLazyMax
+// (p <= 2^8 otherwise): o and l always share the max they were formed with,
+// so the result is exact either way, and most blocks skip the rescale.
+constexpr float kLazyMax = 8.f;
 
 // ---------------------------------------------------------------------------
 // RoPE + append.
@@ -1507,17 +1511,26 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
         bmax[g] = fmaxf(bmax[g], sc[k][g]);
       }
     }
-    // block max across the wave's row groups, then the online update
+    // The running max moves only when a score passes it by more than
+    // kLazyMax (p <= 2^8 otherwise; o and l always share the max they were
+    // formed with): most blocks skip the block max across the wave's row
+    // groups and the rescale.
+    bool grow = false;
 #pragma unroll
-    for (int g = 0; g < GH; ++g) {
+    for (int g = 0; g < GH; ++g) grow |= bmax[g] > m_run[g] + kLazyMax;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform
 #pragma unroll
-      for (int off = LPR; off < 64; off <<= 1) bmax[g] = fmaxf(bmax[g], __shfl_xor(bmax[g], off));
-      const float mn = fmaxf(m_run[g], bmax[g]);
-      const float alpha = exp2_hw(m_run[g] - mn);  // m_run = -inf -> 0
-      m_run[g] = mn;
-      l_run[g] *= alpha;
+      for (int g = 0; g < GH; ++g) {
 #pragma unroll
-      for (int e = 0; e < VW; ++e) acc[g][e] *= alpha;
+        for (int off = LPR; off < 64; off <<= 1)
+          bmax[g] = fmaxf(bmax[g], __shfl_xor(bmax[g], off));
+        const float mn = fmaxf(m_run[g], bmax[g]);
+        const float alpha = exp2_hw(m_run[g] - mn);  // m_run = -inf -> 0
+        m_run[g] = mn;
+        l_run[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < VW; ++e) acc[g][e] *= alpha;
+      }
     }
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
@@ -1753,11 +1766,6 @@ typedef short i16x4_t __attribute__((ext_vector_type(4)));
 constexpr int kMfmaWaves = 4;                  // waves per workgroup
 constexpr int kMfmaThreads = kMfmaWaves * 64;
 constexpr int kTile = 32;                      // cache rows per wave step
-// The matrix-core kernel's softmax runs in base 2 (kLog2e above).  Its
-// running max moves only when a score exceeds it by more than kLazyMax
-// (p <= 2^8 otherwise): o and l always share the max they were formed with,
-// so the result is exact either way, and most tiles skip the rescale.
-constexpr float kLazyMax = 8.f;
 
 template <int D>
 constexpr int kMfmaQStride = D + 4;

@@ -55,6 +55,7 @@ SHAPES = [
     (16, 2, 128, 4000, 0, False),    # 2 slots of 8 heads
     (64, 16, 64, 2500, 0, False),    # 16 slots
     (24, 12, 128, 3000, 0, False),   # 12 slots: combine kernel
+    (8, 8, 128, 3000, 0, False),     # one q head per slot (odd GH in the merge)
     (64, 8, 128, 20000, 0, True),    # c5 shape, bf16 on the matrix cores
     (32, 8, 64, 900, 0, True),       # bf16, few chunks
 ]
