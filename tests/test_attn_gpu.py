@@ -455,6 +455,45 @@ def test_headmajor_equals_token_major(gpu):
     assert normwise_err(o1, R) < FP32_TOL
 
 
+@pytest.mark.parametrize("kind", ["up", "down", "saw"])
+@pytest.mark.parametrize("n,bf16", [(16385, False), (3000, False), (5000, True)])
+def test_running_max_ramps(gpu, kind, n, bf16):
+    """Scores that climb through the context move the running max block after
+    block (the kernels rescale only when a score passes the max by more than
+    2^8 in base 2); falling and sawtooth scores keep it put or move it in
+    jumps.  All q heads share one direction u and every cached key is
+    noise + lam_t * u, so the score of row t is lam_t*|q|*scale plus noise,
+    spanning ~60 (natural units).  Against the float64 brute force on the
+    same (bf16-rounded) values."""
+    announce(f"running-max ramp {kind} n={n} bf16={bf16}")
+    nq, nkv, d = 32, 8, 128
+    st = Stream(91 + n + bf16 + len(kind))
+    q0 = st.normal((d,))
+    Q = np.repeat(q0[None, :], nq, 0).astype(np.float32)
+    scale = 1.0 / math.sqrt(d)
+    u = q0 / np.linalg.norm(q0)
+    t = np.arange(n, dtype=np.float64)
+    span = 60.0 / (np.linalg.norm(q0) * scale)
+    lam = {"up": span * t / n, "down": span * (1 - t / n),
+           "saw": span * ((t % 700) / 700) * (0.5 + 0.5 * t / n)}[kind]
+    K = (0.1 * st.normal((n, nkv * d))).astype(np.float64)
+    K += np.tile(lam[:, None] * u[None, :], (1, nkv))
+    K = K.astype(np.float32)
+    V = st.normal((n, nkv * d))
+    if bf16:
+        Kb, Vb = f32_to_bf16(K), f32_to_bf16(V)
+        Kd, Vd = dev_bf16(Kb), dev_bf16(Vb)
+        K, V = bf16_to_f32(Kb), bf16_to_f32(Vb)
+    else:
+        Kd, Vd = dev(K), dev(V)
+    O = torch.empty((nq, d), device="cuda")
+    attn.attn_decode_gqa_cache(dev(Q), Kd, Vd, O, nq, nkv, n, d, scale, n - 1, 0)
+    ref = oracle.attn_decode_f64(Q, K, V, nq, nkv, n, d, scale, n - 1, 0, nkv * d, d)
+    err = normwise_err(host(O), ref)
+    print(f"ramp {kind} n={n} bf16={bf16}: normwise err vs f64 {err:.3e}", flush=True)
+    assert err < FP32_TOL
+
+
 # ---------------------------------------------------------------------------
 # size-independent properties at the headline size
 
