@@ -223,6 +223,26 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // so the result is exact either way, and most blocks skip the rescale.
 constexpr float kLazyMax = 8.f;
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t bf16_pair_exact(float a, float b) {
+  const bf16x2_t p = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+// split3 of two values at once: each piece of the pair is one
+// v_cvt_pk_bf16_f32 (round to nearest even, as split3), element a in the
+// low half.  The same pieces as split3 on each value.
+__device__ __forceinline__ uint32_t bf16_pair(float a, float b) { return bf16_pair_exact(a, b); }
+__device__ __forceinline__ void split3x2(float a, float b, uint32_t& hi, uint32_t& mid,
+                                         uint32_t& lo) {
+  hi = bf16_pair(a, b);
+  float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
+  mid = bf16_pair(ra, rb);
+  ra -= __uint_as_float(mid << 16);
+  rb -= __uint_as_float(mid & 0xFFFF0000u);
+  lo = bf16_pair(ra, rb);
+}
+
 // ---------------------------------------------------------------------------
 // RoPE + append.
 struct RopeArgs {
@@ -243,6 +263,11 @@ struct RopeArgs {
   float eps;
   int tokens;           // grid row b = token b of a prefill: slot + b at pos + b
   int64_t sc_off, sc_head;  // Q8 scales, as AttnArgs::sc_off / sc_head
+  // prefill over an fp32 or Q8 cache: the appended rows also leave their bf16
+  // pieces (as pf_split_kernel writes them) at row slot - pc_T0 of
+  // [K, V][nkv][3][pc_R][d], when that row lies in [0, pc_R) (NULL: none)
+  uint16_t* pieces;
+  int pc_T0, pc_R;
 };
 
 // Sum over the workgroup (at most 16 waves); every thread gets the total.
@@ -526,6 +551,37 @@ __global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeAr
     if (a.kv_dtype == MOLOT_KV_Q8 && lane == 0) {
       *(float*)((char*)a.K + soff) = ks;
       *(float*)((char*)a.V + soff) = vs;
+    }
+    // the row's bf16 pieces for the prefill (split3 of the cached values:
+    // fp32 as stored, Q8 as code * scale), the bits pf_split_kernel writes
+    const int pr = slot - a.pc_T0;
+    if (a.pieces && a.kv_dtype != MOLOT_KV_BF16 && pr >= 0 && pr < a.pc_R) {
+      const int64_t pstride = (int64_t)a.pc_R * a.d;  // one piece of one head
+      #pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        if (k >= nk) break;
+        const int j = lane + 64 * k;
+        if (j >= half) continue;
+        float kx0 = r0[k], kx1 = r1[k], vx0 = v0[k], vx1 = v1[k];
+        if (a.kv_dtype == MOLOT_KV_Q8) {
+          kx0 = (float)q8_code(kx0, ks) * ks;
+          kx1 = (float)q8_code(kx1, ks) * ks;
+          vx0 = (float)q8_code(vx0, vs) * vs;
+          vx1 = (float)q8_code(vx1, vs) * vs;
+        }
+        uint32_t pk[3], pv[3];
+        split3x2(kx0, kx1, pk[0], pk[1], pk[2]);
+        split3x2(vx0, vx1, pv[0], pv[1], pv[2]);
+        uint16_t* ok = a.pieces + (int64_t)kh * 3 * pstride + (int64_t)pr * a.d;
+        uint16_t* ov = ok + (int64_t)a.nkv * 3 * pstride;
+        #pragma unroll
+        for (int pc = 0; pc < 3; ++pc) {
+          ok[pc * pstride + j] = (uint16_t)(pk[pc] & 0xFFFF);
+          ok[pc * pstride + j + half] = (uint16_t)(pk[pc] >> 16);
+          ov[pc * pstride + j] = (uint16_t)(pv[pc] & 0xFFFF);
+          ov[pc * pstride + j + half] = (uint16_t)(pv[pc] >> 16);
+        }
+      }
     }
   }
 }
@@ -1848,11 +1904,6 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4 c) {
 // 16 int8 codes -> 16 bf16 (exact: |code| <= 127), bytes 0-7 into lo, 8-15
 // into hi, each in memory order.  One v_cvt_pk_bf16_f32 per pair (its
 // rounding is the identity on these values).
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t bf16_pair_exact(float a, float b) {
-  const bf16x2_t p = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, p);
-}
 __device__ __forceinline__ void i8x16_to_bf16(const u32x4& x, u32x4& lo, u32x4& hi) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -1863,20 +1914,6 @@ __device__ __forceinline__ void i8x16_to_bf16(const u32x4& x, u32x4& lo, u32x4& 
     dst[2 * (i & 1)] = bf16_pair_exact(f0, f1);
     dst[2 * (i & 1) + 1] = bf16_pair_exact(f2, f3);
   }
-}
-
-// split3 of two values at once: each piece of the pair is one
-// v_cvt_pk_bf16_f32 (round to nearest even, as split3), element a in the
-// low half.  The same pieces as split3 on each value.
-__device__ __forceinline__ uint32_t bf16_pair(float a, float b) { return bf16_pair_exact(a, b); }
-__device__ __forceinline__ void split3x2(float a, float b, uint32_t& hi, uint32_t& mid,
-                                         uint32_t& lo) {
-  hi = bf16_pair(a, b);
-  float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
-  mid = bf16_pair(ra, rb);
-  ra -= __uint_as_float(mid << 16);
-  rb -= __uint_as_float(mid & 0xFFFF0000u);
-  lo = bf16_pair(ra, rb);
 }
 
 // Matrix-core decode over a bf16 (Q8 = false) or Q8 (Q8 = true) cache.
@@ -2458,6 +2495,7 @@ struct PfArgs {
   // the kernel splits each staged tile itself
   const uint16_t* pieces;
   int T0, R;
+  int Rsplit;  // pf_split_kernel splits rows [T0, T0 + Rsplit); the appending step wrote the rest
   // split-K over the key tiles (nsplit > 1): split s of a query block takes
   // its share of the tiles and writes unnormalised o and (max, sum) per query
   // row, slot m*nq + head, to part_o [slot][nsplit][D] and part_ml
@@ -2504,7 +2542,7 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
   static_assert(sizeof(T) != 2, "bf16 caches are exact in one piece");
   constexpr int UPR = D / 8;
   const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (u >= (int64_t)a.R * UPR) return;
+  if (u >= (int64_t)a.Rsplit * UPR) return;
   const int h = blockIdx.y, kv = blockIdx.z;
   const int r = (int)(u / UPR), j = (int)(u - (int64_t)r * UPR);
   int64_t soff = 0;
@@ -4273,9 +4311,31 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
   return (int)hipGetLastError();
 }
 
+// The attended keys of a prefill: [T0, N) with T0 the window start of its
+// first query (pos0), split into bf16 pieces once per launch for fp32 and
+// Q8 caches when the pieces fit (kMaxPiecesBytes) and the workspace need not
+// grow under capture.  Returns the pieces buffer (NULL: the attention kernel
+// splits each staged tile itself) and sets T0 and R.
+static int prefill_pieces(int nkv, int N, int d, int pos0, int window, int kv_dtype, void* stream,
+                          void** ws, int* T0, int64_t* R) {
+  *ws = nullptr;
+  *T0 = window > 0 && pos0 - window + 1 > 0 ? std::min(pos0 - window + 1, N) : 0;
+  *R = (int64_t)N - *T0;
+  if (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed)) return 0;
+  const size_t need = (size_t)2 * nkv * 3 * *R * d * sizeof(uint16_t);
+  void* p = nullptr;
+  const int st = *R > 0 && need <= kMaxPiecesBytes ? pieces_workspace(stream, need, &p) : MOLOT_ENOWS;
+  if (st && st != MOLOT_ENOWS) return st;
+  if (!st) *ws = p;
+  return 0;
+}
+
+// split_rows: rows of [T0, N) pf_split_kernel still has to split (the
+// appending step wrote the pieces of the others; -1: all of them)
 static int attn_prefill_impl(const float* Qm, const void* K, const void* V, float* Om, int nq,
                              int nkv, int M, int N, int d, float scale, int pos0, int window,
-                             int kv_dtype, const int32_t* block_row, int page, void* stream) {
+                             int kv_dtype, const int32_t* block_row, int page, void* stream,
+                             int split_rows = -1) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   if (!supported_d(d)) return MOLOT_ENOTSUP;  // the prefill kernels: D = 64, 128, 256
@@ -4347,26 +4407,27 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   // Every query attends keys in [t0(query 0), N).  Not under stream capture
   // when the workspace would have to grow, nor past kMaxPiecesBytes: the
   // kernel then splits each staged tile itself.
-  if (kv_dtype != MOLOT_KV_BF16 && g_presplit.load(std::memory_order_relaxed)) {
-    const int T0 = window > 0 && pos0 - window + 1 > 0 ? std::min(pos0 - window + 1, N) : 0;
-    const int64_t R = (int64_t)N - T0;
-    const size_t need = (size_t)2 * nkv * 3 * R * d * sizeof(uint16_t);
+  {
     void* ws = nullptr;
-    st = R > 0 && need <= kMaxPiecesBytes ? pieces_workspace(stream, need, &ws) : MOLOT_ENOWS;
-    if (st && st != MOLOT_ENOWS) return st;
-    if (!st) {
+    int T0 = 0;
+    int64_t R = 0;
+    st = prefill_pieces(nkv, N, d, pos0, window, kv_dtype, stream, &ws, &T0, &R);
+    if (st) return st;
+    if (ws) {
       a.pieces = reinterpret_cast<const uint16_t*>(ws);
       a.T0 = T0;
       a.R = (int)R;
-      const int64_t units = R * (d / 8);
-      hipLaunchKernelGGL(pf_split(d, kv_dtype, block_row != nullptr),
-                         dim3((unsigned)((units + 255) / 256), nkv, 2), dim3(256), 0,
-                         (hipStream_t)stream, a, reinterpret_cast<uint16_t*>(ws));
-      st = (int)hipGetLastError();
-      if (st) return st;
+      a.Rsplit = split_rows < 0 ? (int)R : (int)std::min<int64_t>(split_rows, R);
+      if (a.Rsplit > 0) {
+        const int64_t units = (int64_t)a.Rsplit * (d / 8);
+        hipLaunchKernelGGL(pf_split(d, kv_dtype, block_row != nullptr),
+                           dim3((unsigned)((units + 255) / 256), nkv, 2), dim3(256), 0,
+                           (hipStream_t)stream, a, reinterpret_cast<uint16_t*>(ws));
+        st = (int)hipGetLastError();
+        if (st) return st;
+      }
       pk = pf_kernel_pre(d, pw);
     }
-    st = 0;
   }
   const dim3 grid((unsigned)(nqb * nkv * nsplit));
   CombArgs cb{};  // split-K: (token, q head) rows as slots of one head each
@@ -4460,10 +4521,28 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   r.k_norm = nm.k;
   r.v_norm = nm.v;
   r.eps = nm.eps;
+  // the appended rows leave their pieces as they are stored; the split
+  // kernel then covers only the cached rows before them, and a fresh prompt
+  // needs no split launch (eager steps of 2048-token prompts: 32q/8kv/d128
+  // fp32 252 -> 249 us, 8q/4kv/d256 window 1024 164.7 -> 161.6 us)
+  void* pws = nullptr;
+  int T0 = 0;
+  int64_t R = 0;
+  int split_rows = -1;
+  if (supported_d(d) && !(kv_dtype == MOLOT_KV_Q8 && d == 256)) {
+    st = prefill_pieces(nkv, slot0 + M, d, pos0, window, kv_dtype, stream, &pws, &T0, &R);
+    if (st) return st;
+    if (pws) {
+      r.pieces = reinterpret_cast<uint16_t*>(pws);
+      r.pc_T0 = T0;
+      r.pc_R = (int)R;
+      split_rows = std::max(0, slot0 - T0);
+    }
+  }
   st = launch_rope_tok(r, M, stream);
   if (st) return st;
   return attn_prefill_impl(q, K, V, O, nq, nkv, M, slot0 + M, d, scale, pos0, window, kv_dtype,
-                           block_row, page, stream);
+                           block_row, page, stream, split_rows);
 }
 
 int molot_hip_prefill_step(float* q, const float* k_new, const float* v_new, void* K, void* V,
