@@ -235,6 +235,12 @@ __device__ __forceinline__ uint32_t bf16_pair_exact(float a, float b) {
 __device__ __forceinline__ uint32_t bf16_pair(float a, float b) { return bf16_pair_exact(a, b); }
 __device__ __forceinline__ void split3x2(float a, float b, uint32_t& hi, uint32_t& mid,
                                          uint32_t& lo) {
+  // The residuals are taken of a and b as rounded to fp32: a product that
+  // formed them (a Q8 code times its scale, q times the score scale) must
+  // not fuse into the first subtraction, or the pieces would split the
+  // unrounded product and differ between the kernels that form a and b
+  // differently.
+#pragma clang fp contract(off)
   hi = bf16_pair(a, b);
   float ra = a - __uint_as_float(hi << 16), rb = b - __uint_as_float(hi & 0xFFFF0000u);
   mid = bf16_pair(ra, rb);
@@ -2488,6 +2494,7 @@ struct PfArgs {
   float* o;        // [M][nq][D]
   const int32_t* block_table;  // paged: the sequence's row of block ids
   int nq, nkv, M, N, pos0, window, nqb;  // nqb: blocks of 16 * pf_waves query rows per KV head
+  int dh;  // head dim as stored (< D: the launch runs padded to D, through the pieces)
   int page_shift;
   float scale;
   // the attended keys [T0, T0 + R) of every KV head split into bf16 pieces
@@ -2522,13 +2529,13 @@ __device__ __forceinline__ int64_t pf_row_off(const PfArgs& a, int h, int t, int
       soff = blk * BB + (int64_t)a.nkv * pg * D + 4 * ((int64_t)h * pg + sl);
       return blk * BB + ((int64_t)h * pg + sl) * D;
     }
-    return (blk * a.nkv + h) * pg * D + (int64_t)sl * D;
+    return ((blk * a.nkv + h) * pg + sl) * (int64_t)a.dh;
   } else {
     if constexpr (Q8) {
       soff = (int64_t)t * R + (int64_t)a.nkv * D + 4 * h;
       return (int64_t)t * R + (int64_t)h * D;
     }
-    return (int64_t)t * a.nkv * D + (int64_t)h * D;
+    return ((int64_t)t * a.nkv + h) * (int64_t)a.dh;
   }
 }
 
@@ -2539,7 +2546,6 @@ __device__ __forceinline__ int64_t pf_row_off(const PfArgs& a, int h, int t, int
 template <int D, typename T, bool PAGED>
 __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) {
   constexpr bool Q8 = std::is_same<T, q8_t>::value;
-  static_assert(sizeof(T) != 2, "bf16 caches are exact in one piece");
   constexpr int UPR = D / 8;
   const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (u >= (int64_t)a.Rsplit * UPR) return;
@@ -2549,7 +2555,15 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
   const int64_t off = pf_row_off<D, T, PAGED>(a, h, a.T0 + r, soff) + 8 * j;
   const void* base = kv ? a.v : a.k;
   float x[8];
-  if constexpr (Q8) {
+  if (8 * j >= a.dh) {  // the padding of a head dim below D (a multiple of 8): zero pieces
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = 0.f;
+  } else if constexpr (sizeof(T) == 2) {  // bf16: exact in the first piece
+    const u32x4 c = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      x[e] = __uint_as_float(((c[e / 2] >> (16 * (e & 1))) & 0xFFFFu) << 16);
+  } else if constexpr (Q8) {
     const uint2 c = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(base) + off);
     const float s = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + soff);
 #pragma unroll
@@ -2656,7 +2670,7 @@ void prefill_mfma16_kernel(PfArgs a) {
   const int m = rv ? row / G : 0;
   const int g = rv ? row - m * G : 0;
   const int rt0 = rv ? t0_of(m) : 0, rnn = rv ? nn_of(m) : 0;
-  const int64_t qoff = ((int64_t)m * a.nq + h * G + g) * D;
+  const int64_t qoff = ((int64_t)m * a.nq + h * G + g) * a.dh;  // q and O rows of dh elements
 
   // Q^T pieces (B operand): lane l row c16, elements 32s + 8*g4 + e, scaled
   // by scale*log2(e) (base-2 scores)
@@ -2665,8 +2679,9 @@ void prefill_mfma16_kernel(PfArgs a) {
 #pragma unroll
   for (int s = 0; s < QS; ++s) {
     const float* qp = a.q + qoff + 32 * s + 8 * g4;
-    const f32x4 x0 = rv ? *reinterpret_cast<const f32x4*>(qp) : f32x4{0.f, 0.f, 0.f, 0.f};
-    const f32x4 x1 = rv ? *reinterpret_cast<const f32x4*>(qp + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool qin = rv && 32 * s + 8 * g4 < a.dh;  // zero padding past dh (a multiple of 8)
+    const f32x4 x0 = qin ? *reinterpret_cast<const f32x4*>(qp) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 x1 = qin ? *reinterpret_cast<const f32x4*>(qp + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
     uint32_t h4[4], m4[4], l4[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -2936,7 +2951,7 @@ void prefill_mfma16_kernel(PfArgs a) {
     float* orow = a.o + qoff;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<f32x4*>(orow + 16 * dt + 4 * g4) = o[dt] * inv;
+      if (16 * dt + 4 * g4 < a.dh) *reinterpret_cast<f32x4*>(orow + 16 * dt + 4 * g4) = o[dt] * inv;
   }
 }
 
@@ -3817,6 +3832,12 @@ SplitFn pf_split(int d, int kv_dtype, bool paged) {
     if (d == 64) return paged ? pf_split_kernel<64, q8_t, true> : pf_split_kernel<64, q8_t, false>;
     return paged ? pf_split_kernel<128, q8_t, true> : pf_split_kernel<128, q8_t, false>;
   }
+  if (kv_dtype == MOLOT_KV_BF16) {  // padded head dims only: bf16 prefills otherwise stage directly
+    if (d == 64) return paged ? pf_split_kernel<64, bf16_t, true> : pf_split_kernel<64, bf16_t, false>;
+    if (d == 128)
+      return paged ? pf_split_kernel<128, bf16_t, true> : pf_split_kernel<128, bf16_t, false>;
+    return paged ? pf_split_kernel<256, bf16_t, true> : pf_split_kernel<256, bf16_t, false>;
+  }
   if (d == 64) return paged ? pf_split_kernel<64, float, true> : pf_split_kernel<64, float, false>;
   if (d == 128) return paged ? pf_split_kernel<128, float, true> : pf_split_kernel<128, float, false>;
   return paged ? pf_split_kernel<256, float, true> : pf_split_kernel<256, float, false>;
@@ -4316,12 +4337,15 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
 // Q8 caches when the pieces fit (kMaxPiecesBytes) and the workspace need not
 // grow under capture.  Returns the pieces buffer (NULL: the attention kernel
 // splits each staged tile itself) and sets T0 and R.
+// force: a padded head dim, which only the pieces path serves (any cache
+// type, whatever the presplit knob says).
 static int prefill_pieces(int nkv, int N, int d, int pos0, int window, int kv_dtype, void* stream,
-                          void** ws, int* T0, int64_t* R) {
+                          void** ws, int* T0, int64_t* R, bool force = false) {
   *ws = nullptr;
   *T0 = window > 0 && pos0 - window + 1 > 0 ? std::min(pos0 - window + 1, N) : 0;
   *R = (int64_t)N - *T0;
-  if (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed)) return 0;
+  if (!force && (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed)))
+    return 0;
   const size_t need = (size_t)2 * nkv * 3 * *R * d * sizeof(uint16_t);
   void* p = nullptr;
   const int st = *R > 0 && need <= kMaxPiecesBytes ? pieces_workspace(stream, need, &p) : MOLOT_ENOWS;
@@ -4338,8 +4362,14 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
                              int split_rows = -1) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
-  if (!supported_d(d)) return MOLOT_ENOTSUP;  // the prefill kernels: D = 64, 128, 256
+  // The prefill kernels are built for D = 64, 128, 256 (Q8: 64, 128).  Any
+  // other head dim that is a multiple of 8 below 256 (fp32 or bf16) runs
+  // padded to the next D through the pieces: the split zero-fills each row
+  // past d, q is read and O written at d.
+  const bool padded = !supported_d(d);
+  if (padded && (d % 8 || d > 256 || kv_dtype == MOLOT_KV_Q8)) return MOLOT_ENOTSUP;
   if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // Q8 prefill: 64, 128
+  const int D = padded ? (d <= 64 ? 64 : d <= 128 ? 128 : 256) : d;
   if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
   if (M == 0) return 0;
   if (N == 0) return zero_out(Om, (int64_t)M * nq * d, (hipStream_t)stream);
@@ -4348,7 +4378,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   const int64_t rows = (int64_t)M * (nq / nkv);
   const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1;
   auto nqb_of = [&](int w) { return (rows + 16 * w - 1) / (16 * w); };
-  int pw = pf_waves(d, esz);
+  int pw = pf_waves(D, padded ? 4 : esz);  // padded: the fp32-piece kernel
   int64_t nqb = nqb_of(pw);
   // A grid of fewer workgroups than CUs (few query rows over a long cache,
   // e.g. a prompt chunk after a long context) splits each query block's key
@@ -4365,7 +4395,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     if (nsplit > 1) {
       int* ctr = nullptr;
       void* ws = nullptr;
-      st = workspace(stream, sizeof(float) * (size_t)M * nq * nsplit * (d + 2), &ctr, &ws);
+      st = workspace(stream, sizeof(float) * (size_t)M * nq * nsplit * (D + 2), &ctr, &ws);
       if (st && st != MOLOT_ENOWS) return st;
       if (st) nsplit = 1;  // under capture the workspace cannot grow
       else part = reinterpret_cast<float*>(ws);
@@ -4394,14 +4424,15 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   a.block_table = block_row;
   a.nsplit = nsplit;
   a.part_o = part;
-  a.part_ml = part ? part + (size_t)M * nq * nsplit * d : nullptr;
+  a.part_ml = part ? part + (size_t)M * nq * nsplit * D : nullptr;
+  a.dh = d;
   if (block_row) {
     if (page <= 0 || (page & (page - 1)) || !q8_pages_ok(nkv, page, kv_dtype))
       return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
-  PfFn pk = pf_kernel(d, kv_dtype, block_row != nullptr, pw);
-  if (!pk) return MOLOT_ENOTSUP;
+  PfFn pk = padded ? nullptr : pf_kernel(d, kv_dtype, block_row != nullptr, pw);
+  if (!pk && !padded) return MOLOT_ENOTSUP;
   // fp32 and Q8 caches: split the attended keys into bf16 pieces once
   // (pf_split_kernel), and let the attention kernel copy them into LDS.
   // Every query attends keys in [t0(query 0), N).  Not under stream capture
@@ -4411,22 +4442,23 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     void* ws = nullptr;
     int T0 = 0;
     int64_t R = 0;
-    st = prefill_pieces(nkv, N, d, pos0, window, kv_dtype, stream, &ws, &T0, &R);
+    st = prefill_pieces(nkv, N, D, pos0, window, kv_dtype, stream, &ws, &T0, &R, padded);
     if (st) return st;
+    if (!ws && padded) return MOLOT_ENOTSUP;  // pieces out of reach (capture, size)
     if (ws) {
       a.pieces = reinterpret_cast<const uint16_t*>(ws);
       a.T0 = T0;
       a.R = (int)R;
       a.Rsplit = split_rows < 0 ? (int)R : (int)std::min<int64_t>(split_rows, R);
       if (a.Rsplit > 0) {
-        const int64_t units = (int64_t)a.Rsplit * (d / 8);
-        hipLaunchKernelGGL(pf_split(d, kv_dtype, block_row != nullptr),
+        const int64_t units = (int64_t)a.Rsplit * (D / 8);
+        hipLaunchKernelGGL(pf_split(D, kv_dtype, block_row != nullptr),
                            dim3((unsigned)((units + 255) / 256), nkv, 2), dim3(256), 0,
                            (hipStream_t)stream, a, reinterpret_cast<uint16_t*>(ws));
         st = (int)hipGetLastError();
         if (st) return st;
       }
-      pk = pf_kernel_pre(d, pw);
+      pk = pf_kernel_pre(D, pw);
     }
   }
   const dim3 grid((unsigned)(nqb * nkv * nsplit));
@@ -4438,11 +4470,11 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   cb.nkv = nq;
   cb.gh = 1;
   cb.nsub = 1;
-  cb.d = d;
+  cb.d = D;
   cb.dh = d;
   cb.nchunks = nsplit;
   cb.chunk = 1;
-  const dim3 cgrid((unsigned)(d / kCombPairs), (unsigned)((int64_t)M * nq));
+  const dim3 cgrid((unsigned)(D / kCombPairs), (unsigned)((int64_t)M * nq));
   const size_t clds = sizeof(float) * (size_t)comb_lds_floats(nsplit);
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {
@@ -4480,7 +4512,8 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
                              const int32_t* block_row, int page, int max_blocks, void* stream) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
-  if (!supported_d(d)) return MOLOT_ENOTSUP;  // the prefill kernels: D = 64, 128, 256
+  // the prefill kernels' head dims, or a multiple of 8 below 256 run padded
+  if (!supported_d(d) && (d % 8 || d > 256 || kv_dtype == MOLOT_KV_Q8)) return MOLOT_ENOTSUP;
   if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // Q8 prefill: 64, 128
   Norms nm;
   nm.q = q_norm;

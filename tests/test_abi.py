@@ -84,8 +84,13 @@ def test_validation_before_launch():
     for d in (97, 258, 0):
         assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, d, 0.1, 9,
                                                    0, 0, s) == L.ENOTSUP
-    # prefill only at 64, 128, 256; Q8 caches only at 64, 128
-    assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 96, 0.1, 6, 0, 0,
+    # prefill: 64, 128, 256, or a multiple of 8 below 256 run padded (not Q8);
+    # Q8 caches only at 64, 128
+    for d, kvd in ((90, 0), (90, L.KV_BF16), (96, L.KV_Q8), (250, 0)):
+        assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, d, 0.1, 6, 0,
+                                              kvd, s) == L.ENOTSUP
+        assert lib.molot_hip_prefill_step(_p(), _p(), _p(), _p(), _p(), _p(), 8, 2, d, 4, 6, 6,
+                                          None, None, 0, 1e-6, _p(), 0.1, 0, kvd,
                                           s) == L.ENOTSUP
     assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 96, 0.1, 9, 0,
                                                L.KV_Q8, s) == L.ENOTSUP

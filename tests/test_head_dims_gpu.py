@@ -1,4 +1,5 @@
-"""Head dims other than 64, 128 and 256 on the decode path (MI355X only).
+"""Head dims other than 64, 128 and 256 on the decode and prefill paths
+(MI355X only).
 
 The reference takes any head dim (include/molot/attn.h:99, :174 and
 gemm.h:26 run scalar tails; model.h:518 derives qhd from the weights).  The
@@ -8,7 +9,10 @@ are read at their stored length d, and every output is written at d.  These
 tests hold every decode entry at such dims to the oracle (1e-5 normwise for
 fp32, and for bf16 on the same bf16 values), covering d % 4 == 2, single and
 split chunks, the in-launch merge and the combine kernel, windows, norms,
-the paged cache and the head-major layout.
+the paged cache and the head-major layout.  The prefill kernels take a
+multiple of 8 below 256 (fp32 or bf16 caches) padded the same way, through
+the bf16 pieces of the keys; those tests hold the prefill attention, the
+fused prefill step and its paged form to the oracle at the same bar.
 """
 import math
 
@@ -20,7 +24,7 @@ import oracle
 from conftest import normwise_err
 from gpu_util import dev, dev_bf16, host, make_decode, make_paged, oracle_decode, oracle_paged
 from molot_amd import attn
-from molot_amd.synth import Stream, bf16_to_f32
+from molot_amd.synth import Stream, bf16_to_f32, f32_to_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -148,3 +152,117 @@ def test_paged_head_dims(gpu, d, bf16):
     oq, oK, oV, oO = oracle_paged(P, inv, s)
     np.testing.assert_allclose(host(q), oq, atol=4e-6, rtol=2e-6)
     assert normwise_err(host(O), oO) < FP32_TOL
+
+
+# Prefill at padded head dims: the prefill kernels are built for D = 64, 128
+# and 256; a multiple of 8 below 256 (fp32 or bf16 cache) runs padded to the
+# next D through the bf16 pieces (the split zero-fills each row past d).
+def prefill_cache(st, N, nkv, d, bf16):
+    K = st.normal((N, nkv * d))
+    V = st.normal((N, nkv * d))
+    if bf16:
+        return f32_to_bf16(K), f32_to_bf16(V)
+    return K, V
+
+
+def on_dev(x):
+    return dev_bf16(x) if x.dtype == np.uint16 else dev(x)
+
+
+@pytest.mark.parametrize("nq,nkv,d,M,N,pos0,window,bf16", [
+    (16, 4, 96, 100, 100, 0, 0, False),      # fresh prompt
+    (16, 4, 80, 60, 1060, 1000, 0, True),    # appended to a context
+    (8, 2, 112, 50, 3050, 3000, 1024, False),  # window, split key tiles
+    (8, 4, 192, 70, 170, 100, 33, True),     # D = 256
+    (32, 8, 72, 33, 533, 500, 0, False),     # G = 4
+    (8, 8, 200, 1, 700, 699, 0, True),       # a single query
+    (8, 2, 40, 12, 30, 25, 0, False),        # D = 64, causal end clipped at N
+])
+def test_prefill_head_dims(gpu, nq, nkv, d, M, N, pos0, window, bf16):
+    announce(f"prefill {nq}/{nkv}/d{d} M={M} N={N} pos0={pos0} win={window} bf16={bf16}")
+    st = Stream(M + N + d + nq + 5)
+    Q = st.normal((M, nq, d))
+    K, V = prefill_cache(st, N, nkv, d, bf16)
+    O = torch.full((M, nq, d), float("nan"), device="cuda")
+    scale = 1 / math.sqrt(d)
+    attn.attn_prefill_gqa(dev(Q), on_dev(K), on_dev(V), O, nq, nkv, M, N, d, scale, pos0, window)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, scale, pos0, window)
+    err = normwise_err(host(O), R)
+    print(f"prefill normwise err {err:.3e}", flush=True)
+    assert err < FP32_TOL
+
+
+@pytest.mark.parametrize("d,bf16", [(96, False), (120, True), (208, False)])
+def test_prefill_step_head_dims(gpu, d, bf16):
+    """One layer's prefill with norms at a padded head dim: 90 prompt tokens
+    after 150 cached, against the oracle's forward.h:367-399 sequence."""
+    announce(f"prefill step 16q/4kv/d{d} M=90 after 150 bf16={bf16}")
+    st = Stream(170 + d + bf16)
+    nq, nkv, M, n0 = 16, 4, 90, 150
+    q = st.normal((M, nq, d), 2.0)
+    k = st.normal((M, nkv, d), 2.0)
+    v = st.normal((M, nkv, d), 2.0)
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    kn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    K, V = prefill_cache(st, n0 + M, nkv, d, bf16)
+    K[n0:] = 0
+    V[n0:] = 0
+    inv = oracle.rope_inv_freq(1000000.0, d)
+    s = 1 / math.sqrt(d)
+    qd, Kd, Vd = dev(q), on_dev(K), on_dev(V)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.prefill_step(qd, dev(k), dev(v), Kd, Vd, O, nq, nkv, d, M, n0, n0, dev(inv), s, 0,
+                      q_norm=dev(qn), k_norm=dev(kn), v_norm=True, eps=1e-6)
+    Kc, Vc = K.copy(), V.copy()
+    oq, oO = oracle.prefill_step(q, k, v, Kc, Vc, nq, nkv, d, M, n0, n0, qn, kn, 1, 1e-6, inv, s,
+                                 0)
+    np.testing.assert_allclose(host(qd), oq, rtol=2e-6, atol=4e-6)
+    if bf16:  # the attention on the GPU's own bf16 rows (normed rows may differ by an ulp)
+        bits = lambda t: host(t.view(torch.int16)).view(np.uint16)
+        R = oracle.attn_prefill(host(qd), bits(Kd), bits(Vd), nq, nkv, M, n0 + M, d, s, n0, 0)
+        assert normwise_err(host(O), R) < FP32_TOL
+        assert normwise_err(host(O), oO) < 2e-2
+    else:
+        np.testing.assert_allclose(host(Kd), Kc, rtol=2e-6, atol=4e-6)
+        np.testing.assert_allclose(host(Vd), Vc, rtol=1e-6, atol=1e-7)
+        assert normwise_err(host(O), oO) < FP32_TOL
+
+
+@pytest.mark.parametrize("d,bf16", [(96, True), (160, False)])
+def test_prefill_step_paged_head_dims(gpu, d, bf16):
+    """The paged prefill step (shuffled 16-row pages) at a padded head dim
+    equals the contiguous one bit for bit."""
+    announce(f"paged prefill step 8/2/d{d} bf16={bf16}")
+    st = Stream(191 + d + bf16)
+    nq, nkv, M, n0, page, spare = 8, 2, 45, 200, 16, 3
+    cap = n0 + M
+    q = st.normal((M, nq, d))
+    k = st.normal((M, nkv, d))
+    v = st.normal((M, nkv, d))
+    K, V = prefill_cache(st, cap, nkv, d, bf16)
+    K[n0:] = 0
+    V[n0:] = 0
+    nb = (cap + page - 1) // page
+    nblk = nb + spare
+    row = st.permutation(nblk)[:nb].astype(np.int32)
+    Kp = np.zeros((nblk, nkv, page, d), K.dtype)
+    Vp = np.zeros((nblk, nkv, page, d), V.dtype)
+    for t in range(n0):
+        Kp[row[t // page], :, t % page] = K[t].reshape(nkv, d)
+        Vp[row[t // page], :, t % page] = V[t].reshape(nkv, d)
+    inv = dev(oracle.rope_inv_freq(10000.0, d))
+    s = 1 / math.sqrt(d)
+    qc, qp = dev(q), dev(q)
+    Kc, Vc = on_dev(K), on_dev(V)
+    Kpd, Vpd = on_dev(Kp.reshape(nblk, -1)), on_dev(Vp.reshape(nblk, -1))
+    Oc = torch.empty((M, nq, d), device="cuda")
+    Op = torch.empty((M, nq, d), device="cuda")
+    attn.prefill_step(qc, dev(k), dev(v), Kc, Vc, Oc, nq, nkv, d, M, n0, n0, inv, s, 0)
+    attn.prefill_step_paged(qp, dev(k), dev(v), Kpd, Vpd, Op, torch.from_numpy(row).cuda(), nb,
+                            page, nq, nkv, d, M, n0, n0, inv, s, 0)
+    assert torch.equal(Oc, Op)
+    assert torch.equal(qc, qp)
+    R = oracle.attn_prefill(host(qc), host(Kc.view(torch.int16)).view(np.uint16) if bf16
+                            else host(Kc), host(Vc.view(torch.int16)).view(np.uint16) if bf16
+                            else host(Vc), nq, nkv, M, cap, d, s, n0, 0)
+    assert normwise_err(host(Oc), R) < FP32_TOL
