@@ -2546,6 +2546,7 @@ __device__ __forceinline__ int64_t pf_row_off(const PfArgs& a, int h, int t, int
 template <int D, typename T, bool PAGED>
 __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) {
   constexpr bool Q8 = std::is_same<T, q8_t>::value;
+  static_assert(sizeof(T) != 2, "bf16 caches are exact in one piece");
   constexpr int UPR = D / 8;
   const int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (u >= (int64_t)a.Rsplit * UPR) return;
@@ -2558,11 +2559,6 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
   if (8 * j >= a.dh) {  // the padding of a head dim below D (a multiple of 8): zero pieces
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = 0.f;
-  } else if constexpr (sizeof(T) == 2) {  // bf16: exact in the first piece
-    const u32x4 c = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      x[e] = __uint_as_float(((c[e / 2] >> (16 * (e & 1))) & 0xFFFFu) << 16);
   } else if constexpr (Q8) {
     const uint2 c = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(base) + off);
     const float s = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + soff);
@@ -2748,8 +2744,13 @@ void prefill_mfma16_kernel(PfArgs a) {
         ksc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.k) + soff);
         vsc[i] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(a.v) + soff);
       }
-      kreg[i] = load16(Kb + off);
-      vreg[i] = load16(Vb + off);
+      if (e < a.dh) {  // a padded launch: columns past the stored head dim read as 0
+        kreg[i] = load16(Kb + off);
+        vreg[i] = load16(Vb + off);
+      } else {
+        kreg[i] = typename KVT<T>::vec{};
+        vreg[i] = typename KVT<T>::vec{};
+      }
     }
   };
   // the chunk's values as KP bf16 pieces, 4 elements (8 bytes) at a time
@@ -3832,12 +3833,6 @@ SplitFn pf_split(int d, int kv_dtype, bool paged) {
     if (d == 64) return paged ? pf_split_kernel<64, q8_t, true> : pf_split_kernel<64, q8_t, false>;
     return paged ? pf_split_kernel<128, q8_t, true> : pf_split_kernel<128, q8_t, false>;
   }
-  if (kv_dtype == MOLOT_KV_BF16) {  // padded head dims only: bf16 prefills otherwise stage directly
-    if (d == 64) return paged ? pf_split_kernel<64, bf16_t, true> : pf_split_kernel<64, bf16_t, false>;
-    if (d == 128)
-      return paged ? pf_split_kernel<128, bf16_t, true> : pf_split_kernel<128, bf16_t, false>;
-    return paged ? pf_split_kernel<256, bf16_t, true> : pf_split_kernel<256, bf16_t, false>;
-  }
   if (d == 64) return paged ? pf_split_kernel<64, float, true> : pf_split_kernel<64, float, false>;
   if (d == 128) return paged ? pf_split_kernel<128, float, true> : pf_split_kernel<128, float, false>;
   return paged ? pf_split_kernel<256, float, true> : pf_split_kernel<256, float, false>;
@@ -4337,15 +4332,12 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
 // Q8 caches when the pieces fit (kMaxPiecesBytes) and the workspace need not
 // grow under capture.  Returns the pieces buffer (NULL: the attention kernel
 // splits each staged tile itself) and sets T0 and R.
-// force: a padded head dim, which only the pieces path serves (any cache
-// type, whatever the presplit knob says).
 static int prefill_pieces(int nkv, int N, int d, int pos0, int window, int kv_dtype, void* stream,
-                          void** ws, int* T0, int64_t* R, bool force = false) {
+                          void** ws, int* T0, int64_t* R) {
   *ws = nullptr;
   *T0 = window > 0 && pos0 - window + 1 > 0 ? std::min(pos0 - window + 1, N) : 0;
   *R = (int64_t)N - *T0;
-  if (!force && (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed)))
-    return 0;
+  if (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed)) return 0;
   const size_t need = (size_t)2 * nkv * 3 * *R * d * sizeof(uint16_t);
   void* p = nullptr;
   const int st = *R > 0 && need <= kMaxPiecesBytes ? pieces_workspace(stream, need, &p) : MOLOT_ENOWS;
@@ -4364,8 +4356,9 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   if (st) return st;
   // The prefill kernels are built for D = 64, 128, 256 (Q8: 64, 128).  Any
   // other head dim that is a multiple of 8 below 256 (fp32 or bf16) runs
-  // padded to the next D through the pieces: the split zero-fills each row
-  // past d, q is read and O written at d.
+  // padded to the next D: the split kernel and the per-tile loads read each
+  // row at its stored length d and fill the columns past it with 0, q is
+  // read and O written at d.
   const bool padded = !supported_d(d);
   if (padded && (d % 8 || d > 256 || kv_dtype == MOLOT_KV_Q8)) return MOLOT_ENOTSUP;
   if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // Q8 prefill: 64, 128
@@ -4378,7 +4371,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   const int64_t rows = (int64_t)M * (nq / nkv);
   const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1;
   auto nqb_of = [&](int w) { return (rows + 16 * w - 1) / (16 * w); };
-  int pw = pf_waves(D, padded ? 4 : esz);  // padded: the fp32-piece kernel
+  int pw = pf_waves(D, esz);
   int64_t nqb = nqb_of(pw);
   // A grid of fewer workgroups than CUs (few query rows over a long cache,
   // e.g. a prompt chunk after a long context) splits each query block's key
@@ -4431,8 +4424,8 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
       return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
-  PfFn pk = padded ? nullptr : pf_kernel(d, kv_dtype, block_row != nullptr, pw);
-  if (!pk && !padded) return MOLOT_ENOTSUP;
+  PfFn pk = pf_kernel(D, kv_dtype, block_row != nullptr, pw);
+  if (!pk) return MOLOT_ENOTSUP;
   // fp32 and Q8 caches: split the attended keys into bf16 pieces once
   // (pf_split_kernel), and let the attention kernel copy them into LDS.
   // Every query attends keys in [t0(query 0), N).  Not under stream capture
@@ -4442,9 +4435,8 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     void* ws = nullptr;
     int T0 = 0;
     int64_t R = 0;
-    st = prefill_pieces(nkv, N, D, pos0, window, kv_dtype, stream, &ws, &T0, &R, padded);
+    st = prefill_pieces(nkv, N, D, pos0, window, kv_dtype, stream, &ws, &T0, &R);
     if (st) return st;
-    if (!ws && padded) return MOLOT_ENOTSUP;  // pieces out of reach (capture, size)
     if (ws) {
       a.pieces = reinterpret_cast<const uint16_t*>(ws);
       a.T0 = T0;

@@ -266,3 +266,28 @@ def test_prefill_step_paged_head_dims(gpu, d, bf16):
                             else host(Kc), host(Vc.view(torch.int16)).view(np.uint16) if bf16
                             else host(Vc), nq, nkv, M, cap, d, s, n0, 0)
     assert normwise_err(host(Oc), R) < FP32_TOL
+
+
+@pytest.mark.parametrize("nq,nkv,d,M,N,pos0,window", [
+    (16, 4, 96, 70, 1070, 1000, 0), (8, 4, 200, 40, 540, 500, 100), (8, 2, 56, 33, 33, 0, 0)])
+def test_prefill_head_dims_per_tile_split(gpu, nq, nkv, d, M, N, pos0, window):
+    """An fp32 cache at a padded head dim: the keys split once per launch and
+    split per staged tile (the path under stream capture and past the pieces
+    workspace's limit) give the same bits, and the oracle's result."""
+    announce(f"prefill per-tile split {nq}/{nkv}/d{d} M={M} N={N} win={window}")
+    st = Stream(300 + d)
+    Q = st.normal((M, nq, d))
+    K, V = prefill_cache(st, N, nkv, d, False)
+    s = 1 / math.sqrt(d)
+    outs = []
+    try:
+        for pre in (True, False):
+            attn.set_prefill_presplit(pre)
+            O = torch.full((M, nq, d), float("nan"), device="cuda")
+            attn.attn_prefill_gqa(dev(Q), dev(K), dev(V), O, nq, nkv, M, N, d, s, pos0, window)
+            outs.append(host(O))
+    finally:
+        attn.set_prefill_presplit(True)
+    assert np.array_equal(outs[0], outs[1])
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, window)
+    assert normwise_err(outs[1], R) < FP32_TOL
