@@ -316,3 +316,43 @@ def test_prefill_2k_prompt(gpu):
     err = normwise_err(host(O), R)
     print(f"prefill 2k normwise err {err:.3e}", flush=True)
     assert err < TOL
+
+
+@pytest.mark.parametrize("d,bf16", [(128, False), (96, False), (80, True)])
+def test_prefill_graph_replays_match_eager(gpu, d, bf16):
+    """The prefill attention captured in a HIP graph: 40 queries after 3000
+    cached rows (the key-split grid and its combine kernel; fp32 with the
+    once-per-launch key split, bf16 staged per tile, 96 and 80 padded).
+    The stream's workspaces are sized by one launch before the capture and
+    reused by every replay; each replay, with eager work and
+    synchronisations between them, equals the eager result bit for bit."""
+    announce(f"prefill graph d={d} bf16={bf16}")
+    nq, nkv, M, N, pos0 = 16, 4, 40, 3040, 3000
+    st = Stream(400 + d + bf16)
+    Q = st.normal((M, nq, d))
+    K, V = cache(st, N, nkv, d, bf16)
+    Qd, Kd, Vd = dev(Q), on_dev(K), on_dev(V)
+    s = 1 / math.sqrt(d)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.attn_prefill_gqa(Qd, Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)
+    eager = host(O)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        attn.attn_prefill_gqa(Qd, Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        attn.attn_prefill_gqa(Qd, Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)
+    O2 = torch.empty((8, nq, d), device="cuda")
+    for r in range(4):
+        O.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(host(O), eager), f"replay {r}"
+        # eager work in between replays: another prefill on the current stream
+        attn.attn_prefill_gqa(Qd[:8].contiguous(), Kd, Vd, O2, nq, nkv, 8, 2008, d, s, 2000, 0)
+        torch.cuda.synchronize()
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, 0)
+    assert normwise_err(eager, R) < TOL
