@@ -21,7 +21,7 @@
  * Head dims: the decode entries take any even d from 2 to 256 for fp32 and
  * bf16 caches (attn.h takes any qhd, attn.h:99, :174) and d = 64, 128 or
  * 256 for Q8 caches; the prefill entries d = 64, 128 or 256, or any
- * multiple of 8 below 256 for fp32 and bf16 caches (Q8: 64 or 128);
+ * multiple of 8 below 256 for fp32 and bf16 caches (Q8: 64, 128 or 256);
  * anything else returns MOLOT_ENOTSUP before launching.
  * Semantics (include/molot/attn.h:125-177): n = valid slots after the
  * append, window <= 0 attends [0, n), otherwise [t0, n) with

@@ -3801,6 +3801,8 @@ bool norms_ok(const Norms& nm) { return nm.eps >= 0.f && nm.eps < INFINITY; }
 
 using PfFn = void (*)(PfArgs);
 constexpr size_t kMaxPiecesBytes = (size_t)1 << 30;  // the prefill's pre-split workspace
+// ... and its cap where no per-tile kernel stands behind it (Q8 at d = 256)
+constexpr size_t kMaxPiecesOnlyBytes = (size_t)8 << 30;
 std::atomic<int> g_presplit{1};  // molot_hip_set_prefill_presplit
 
 template <int D, typename T, bool PAGED>
@@ -3831,7 +3833,9 @@ using SplitFn = void (*)(PfArgs, uint16_t*);
 SplitFn pf_split(int d, int kv_dtype, bool paged) {
   if (kv_dtype == MOLOT_KV_Q8) {
     if (d == 64) return paged ? pf_split_kernel<64, q8_t, true> : pf_split_kernel<64, q8_t, false>;
-    return paged ? pf_split_kernel<128, q8_t, true> : pf_split_kernel<128, q8_t, false>;
+    if (d == 128)
+      return paged ? pf_split_kernel<128, q8_t, true> : pf_split_kernel<128, q8_t, false>;
+    return paged ? pf_split_kernel<256, q8_t, true> : pf_split_kernel<256, q8_t, false>;
   }
   if (d == 64) return paged ? pf_split_kernel<64, float, true> : pf_split_kernel<64, float, false>;
   if (d == 128) return paged ? pf_split_kernel<128, float, true> : pf_split_kernel<128, float, false>;
@@ -4332,15 +4336,18 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
 // Q8 caches when the pieces fit (kMaxPiecesBytes) and the workspace need not
 // grow under capture.  Returns the pieces buffer (NULL: the attention kernel
 // splits each staged tile itself) and sets T0 and R.
+// only: the launch has no per-tile kernel (a Q8 cache at d = 256): the
+// pieces are made whatever the presplit switch says, up to kMaxPiecesOnlyBytes.
 static int prefill_pieces(int nkv, int N, int d, int pos0, int window, int kv_dtype, void* stream,
-                          void** ws, int* T0, int64_t* R) {
+                          void** ws, int* T0, int64_t* R, bool only = false) {
   *ws = nullptr;
   *T0 = window > 0 && pos0 - window + 1 > 0 ? std::min(pos0 - window + 1, N) : 0;
   *R = (int64_t)N - *T0;
-  if (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed)) return 0;
+  if (!only && (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed))) return 0;
   const size_t need = (size_t)2 * nkv * 3 * *R * d * sizeof(uint16_t);
+  const size_t cap = only ? kMaxPiecesOnlyBytes : kMaxPiecesBytes;
   void* p = nullptr;
-  const int st = *R > 0 && need <= kMaxPiecesBytes ? pieces_workspace(stream, need, &p) : MOLOT_ENOWS;
+  const int st = *R > 0 && need <= cap ? pieces_workspace(stream, need, &p) : MOLOT_ENOWS;
   if (st && st != MOLOT_ENOWS) return st;
   if (!st) *ws = p;
   return 0;
@@ -4354,14 +4361,15 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
                              int split_rows = -1) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
-  // The prefill kernels are built for D = 64, 128, 256 (Q8: 64, 128).  Any
-  // other head dim that is a multiple of 8 below 256 (fp32 or bf16) runs
-  // padded to the next D: the split kernel and the per-tile loads read each
-  // row at its stored length d and fill the columns past it with 0, q is
-  // read and O written at d.
+  // The prefill kernels are built for D = 64, 128, 256.  Any other head dim
+  // that is a multiple of 8 below 256 (fp32 or bf16) runs padded to the next
+  // D: the split kernel and the per-tile loads read each row at its stored
+  // length d and fill the columns past it with 0, q is read and O written
+  // at d.  A Q8 cache at d = 256 runs only through the pieces (the kernel
+  // that splits staged Q8 tiles itself is built for 64 and 128).
   const bool padded = !supported_d(d);
   if (padded && (d % 8 || d > 256 || kv_dtype == MOLOT_KV_Q8)) return MOLOT_ENOTSUP;
-  if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // Q8 prefill: 64, 128
+  const bool pieces_only = kv_dtype == MOLOT_KV_Q8 && d == 256;
   const int D = padded ? (d <= 64 ? 64 : d <= 128 ? 128 : 256) : d;
   if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
   if (M == 0) return 0;
@@ -4371,7 +4379,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   const int64_t rows = (int64_t)M * (nq / nkv);
   const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1;
   auto nqb_of = [&](int w) { return (rows + 16 * w - 1) / (16 * w); };
-  int pw = pf_waves(D, esz);
+  int pw = pf_waves(D, pieces_only ? 4 : esz);  // pieces_only: the fp32-piece kernel's waves
   int64_t nqb = nqb_of(pw);
   // A grid of fewer workgroups than CUs (few query rows over a long cache,
   // e.g. a prompt chunk after a long context) splits each query block's key
@@ -4424,8 +4432,8 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
       return MOLOT_EINVAL;
     while ((1 << a.page_shift) < page) ++a.page_shift;
   }
-  PfFn pk = pf_kernel(D, kv_dtype, block_row != nullptr, pw);
-  if (!pk) return MOLOT_ENOTSUP;
+  PfFn pk = pieces_only ? nullptr : pf_kernel(D, kv_dtype, block_row != nullptr, pw);
+  if (!pk && !pieces_only) return MOLOT_ENOTSUP;
   // fp32 and Q8 caches: split the attended keys into bf16 pieces once
   // (pf_split_kernel), and let the attention kernel copy them into LDS.
   // Every query attends keys in [t0(query 0), N).  Not under stream capture
@@ -4435,8 +4443,12 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     void* ws = nullptr;
     int T0 = 0;
     int64_t R = 0;
-    st = prefill_pieces(nkv, N, D, pos0, window, kv_dtype, stream, &ws, &T0, &R);
+    st = prefill_pieces(nkv, N, D, pos0, window, kv_dtype, stream, &ws, &T0, &R, pieces_only);
     if (st) return st;
+    if (!ws && pieces_only) {
+      if (R == 0) return zero_out(Om, (int64_t)M * nq * d, (hipStream_t)stream);  // no key attended
+      return MOLOT_ENOTSUP;  // a capture that would have to grow them, or past the cap
+    }
     if (ws) {
       a.pieces = reinterpret_cast<const uint16_t*>(ws);
       a.T0 = T0;
@@ -4506,7 +4518,7 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   if (st) return st;
   // the prefill kernels' head dims, or a multiple of 8 below 256 run padded
   if (!supported_d(d) && (d % 8 || d > 256 || kv_dtype == MOLOT_KV_Q8)) return MOLOT_ENOTSUP;
-  if (kv_dtype == MOLOT_KV_Q8 && d == 256) return MOLOT_ENOTSUP;  // Q8 prefill: 64, 128
+  const bool pieces_only = kv_dtype == MOLOT_KV_Q8 && d == 256;  // no per-tile kernel
   Norms nm;
   nm.q = q_norm;
   nm.k = k_norm;
@@ -4554,9 +4566,12 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   int T0 = 0;
   int64_t R = 0;
   int split_rows = -1;
-  if (supported_d(d) && !(kv_dtype == MOLOT_KV_Q8 && d == 256)) {
-    st = prefill_pieces(nkv, slot0 + M, d, pos0, window, kv_dtype, stream, &pws, &T0, &R);
+  if (supported_d(d)) {
+    st = prefill_pieces(nkv, slot0 + M, d, pos0, window, kv_dtype, stream, &pws, &T0, &R,
+                        pieces_only);
     if (st) return st;
+    // nothing appended when the attention could not run
+    if (!pws && pieces_only && R > 0) return MOLOT_ENOTSUP;
     if (pws) {
       r.pieces = reinterpret_cast<uint16_t*>(pws);
       r.pc_T0 = T0;

@@ -84,8 +84,7 @@ def test_validation_before_launch():
     for d in (97, 258, 0):
         assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, d, 0.1, 9,
                                                    0, 0, s) == L.ENOTSUP
-    # prefill: 64, 128, 256, or a multiple of 8 below 256 run padded (not Q8);
-    # Q8 caches only at 64, 128
+    # prefill: 64, 128, 256, or a multiple of 8 below 256 run padded (not Q8)
     for d, kvd in ((90, 0), (90, L.KV_BF16), (96, L.KV_Q8), (250, 0)):
         assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, d, 0.1, 6, 0,
                                               kvd, s) == L.ENOTSUP
@@ -151,8 +150,8 @@ def test_q8_validation_before_launch():
     # paged Q8 blocks stay 16-byte aligned only when nkv * page is a multiple of 4
     assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4, 4, 8,
                                            1, 64, 2, 0.1, 0, Q8, s) == L.EINVAL
-    assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 256, 0.1, 6, 0,
-                                          Q8, s) == L.ENOTSUP  # Q8 prefill: 64, 128
+    assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 192, 0.1, 6, 0,
+                                          Q8, s) == L.ENOTSUP  # Q8 prefill: 64, 128, 256
     # the RoPE/append entries write only rows the attention entries read back
     assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 2, 192, 5, 5, _p(), Q8,
                                      s) == L.ENOTSUP

@@ -425,6 +425,9 @@ def test_q8_c4_continuous_batching(gpu):
     (8, 2, 64, 50, 3050, 3000, 1024),
     (16, 16, 64, 65, 65, 0, 0),      # G = 1
     (12, 4, 128, 30, 60, 30, 7),     # G = 3
+    (8, 4, 256, 70, 3070, 3000, 1024),  # d = 256 (pieces only), window, split keys
+    (8, 4, 256, 100, 100, 0, 0),
+    (8, 4, 256, 4, 10, 40, 5),       # no query attends a key: O = 0
 ])
 def test_q8_prefill_vs_oracle(gpu, nq, nkv, d, M, N, pos0, window):
     announce(f"q8 prefill {nq}/{nkv}/{d} M={M} N={N} pos0={pos0} win={window}")
@@ -440,11 +443,11 @@ def test_q8_prefill_vs_oracle(gpu, nq, nkv, d, M, N, pos0, window):
     assert err < TOL
 
 
-def test_q8_prefill_step_vs_oracle(gpu):
-    """One layer's prefill with norms on a Q8 cache: 200 tokens after 300."""
-    announce("q8 prefill step 32q/8kv/d128 M=200 after 300")
-    st = Stream(50)
-    nq, nkv, d, M, n0 = 32, 8, 128, 200, 300
+@pytest.mark.parametrize("nq,nkv,d,M,n0", [(32, 8, 128, 200, 300), (8, 4, 256, 90, 150)])
+def test_q8_prefill_step_vs_oracle(gpu, nq, nkv, d, M, n0):
+    """One layer's prefill with norms on a Q8 cache: M tokens after n0."""
+    announce(f"q8 prefill step {nq}q/{nkv}kv/d{d} M={M} after {n0}")
+    st = Stream(50 + d)
     q = st.normal((M, nq, d), 2.0)
     k = st.normal((M, nkv, d), 2.0)
     v = st.normal((M, nkv, d), 2.0)
@@ -471,6 +474,42 @@ def test_q8_prefill_step_vs_oracle(gpu):
     R = oracle.attn_prefill(host(qd), Kh, Vh, nq, nkv, M, n0 + M, d, 0.088, n0, 0)
     assert normwise_err(host(O), R) < TOL
     assert normwise_err(host(O), oO) < 1e-3
+
+
+def test_q8_prefill_d256_paged_matches_contiguous(gpu):
+    """A Q8 cache at d = 256 in shuffled 16-row pages: the same rows as the
+    contiguous cache, the same pieces and products, the same bits."""
+    announce("q8 prefill paged d256")
+    st = Stream(58)
+    nq, nkv, d, M, n0, page, spare = 8, 4, 256, 50, 400, 16, 3
+    N = n0 + M
+    Q = st.normal((M, nq, d))
+    Kq, Vq = q8_caches(st, N, nkv, d)
+    nb = (N + page - 1) // page
+    nblk = nb + spare
+    row = st.permutation(nblk)[:nb].astype(np.int32)
+    rb = oracle.q8_block_bytes(nkv, d, page)
+    pools = []
+    for C in (Kq, Vq):
+        codes = np.zeros((nblk, nkv, page, d), np.int8)
+        scales = np.zeros((nblk, nkv, page), np.float32)
+        for t in range(N):
+            c, sc = split_row(C[t], nkv, d)
+            codes[row[t // page], :, t % page] = c
+            scales[row[t // page], :, t % page] = sc
+        X = np.zeros((nblk, rb), np.uint8)
+        X[:, :nkv * page * d] = codes.reshape(nblk, -1).view(np.uint8)
+        X[:, nkv * page * d:nkv * page * d + 4 * nkv * page] = scales.reshape(nblk, -1).view(np.uint8)
+        pools.append(X)
+    s = 1 / math.sqrt(d)
+    Oc = torch.full((M, nq, d), float("nan"), device="cuda")
+    Op = torch.full((M, nq, d), float("nan"), device="cuda")
+    attn.attn_prefill_gqa(dev(Q), dev_u8(Kq), dev_u8(Vq), Oc, nq, nkv, M, N, d, s, n0, 0)
+    attn.attn_prefill_paged(dev(Q), dev_u8(pools[0]), dev_u8(pools[1]), Op,
+                            torch.from_numpy(row).cuda(), nb, page, nq, nkv, M, N, d, s, n0, 0)
+    assert torch.equal(Oc, Op)
+    R = oracle.attn_prefill(Q, Kq, Vq, nq, nkv, M, N, d, s, n0, 0)
+    assert normwise_err(host(Oc), R) < TOL
 
 
 # ---------------------------------------------------------------------------
