@@ -430,7 +430,9 @@ def test_prefill_golden(name):
                                                       (4, 4, 128, 33, 33, 0, 0),
                                                       (16, 1, 64, 20, 70, 50, 16),
                                                       (6, 2, 256, 9, 200, 191, 0),
-                                                      (8, 2, 64, 12, 30, 25, 0)])
+                                                      (8, 2, 64, 12, 30, 25, 0),
+                                                      (8, 4, 96, 20, 120, 100, 33),
+                                                      (8, 2, 40, 12, 30, 25, 0)])
 def test_prefill_vs_f64(nq, nkv, d, M, N, pos0, window):
     """Causal masking, windows, a cache longer than the prompt's positions
     (pos0 + M > N clips at N) and every GQA grouping, against float64."""
@@ -523,6 +525,25 @@ def test_q8_attention_is_attention_on_dequantized_rows():
         np.testing.assert_array_equal(a, b)
     # and the quantization error of the cache is the 8-bit one
     assert np.max(np.abs(Kd - K)) <= np.abs(K).max() / 127 * 0.51
+
+
+@pytest.mark.parametrize("nkv,d", [(4, 256), (8, 128), (2, 64)])
+def test_q8_prefill_is_prefill_on_dequantized_rows(nkv, d):
+    """The prefill over a Q8 cache gives bit for bit the prefill over its
+    dequantized fp32 rows, at every Q8 head dim (d = 256: 1040-byte rows at
+    nkv = 4): pins the prefill's Q8 row and scale addressing."""
+    st = Stream(41 + d)
+    nq, M, N, pos0 = 2 * nkv, 17, 240, 223
+    Q = st.normal((M, nq, d))
+    K, V = kv_token_major(st, N, nkv, d, 2.0)
+    Kq, Vq = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
+    Kd, Vd = oracle.q8_dequant(Kq, nkv, d), oracle.q8_dequant(Vq, nkv, d)
+    for window in (0, 50):
+        a = oracle.attn_prefill(Q, Kq, Vq, nq, nkv, M, N, d, 0.0625, pos0, window)
+        b = oracle.attn_prefill(Q, Kd, Vd, nq, nkv, M, N, d, 0.0625, pos0, window)
+        np.testing.assert_array_equal(a, b)
+        assert normwise_err(a, _prefill_f64(Q, Kd, Vd, nq, nkv, M, N, d, 0.0625, pos0,
+                                            window)) < 1e-6
 
 
 def test_q8_decode_step_appends_quantized_row():
