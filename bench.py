@@ -507,8 +507,9 @@ def main() -> int:
         cb = 1 << 30
         src = torch.ones(cb // 4, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
+        probe = L.load_probe()
         for _ in range(3):
-            L.check(lib.molot_probe_copy(P(dst.data_ptr()), P(src.data_ptr()), cb, cur_stream()),
+            L.check(probe.molot_probe_copy(P(dst.data_ptr()), P(src.data_ptr()), cb, cur_stream()),
                     "probe_copy")
         torch.cuda.synchronize()
         print(json.dumps({"pmc_run": args.config, "steps": 20, "copy_bytes": cb,
@@ -589,15 +590,16 @@ def main() -> int:
     buf = torch.empty(probe_bytes // 4, dtype=torch.float32, device="cuda")
     buf.fill_(1.0)
     sink = torch.empty(1 << 16, dtype=torch.float32, device="cuda")
+    probe = L.load_probe()
     with torch.cuda.stream(s):
         for _ in range(3):
-            lib.molot_probe_read(P(buf.data_ptr()), probe_bytes, P(sink.data_ptr()), sink.numel(),
-                                 sp)
+            probe.molot_probe_read(P(buf.data_ptr()), probe_bytes, P(sink.data_ptr()), sink.numel(),
+                                   sp)
         torch.cuda.synchronize()
         start.record(s)
         for _ in range(10):
-            lib.molot_probe_read(P(buf.data_ptr()), probe_bytes, P(sink.data_ptr()), sink.numel(),
-                                 sp)
+            probe.molot_probe_read(P(buf.data_ptr()), probe_bytes, P(sink.data_ptr()), sink.numel(),
+                                   sp)
         end.record(s)
     torch.cuda.synchronize()
     read_peak = 10 * probe_bytes / (start.elapsed_time(end) * 1e-3) / 1e9

@@ -18,11 +18,11 @@
  *   paged           [block][nkv][page][d], block_table[b][max_blocks]
  *                   (no reference counterpart: the reference cache is not
  *                   paged)
- * Head dims: the decode entries take any even d from 2 to 256 for fp32 and
- * bf16 caches (attn.h takes any qhd, attn.h:99, :174) and d = 64, 128 or
- * 256 for Q8 caches; the prefill entries d = 64, 128 or 256, or any
- * multiple of 8 below 256 for fp32 and bf16 caches (Q8: 64, 128 or 256);
- * anything else returns MOLOT_ENOTSUP before launching.
+ * Head dims: every decode, shared-KV and prefill entry takes any even d
+ * from 2 to 512 for fp32 and bf16 caches (attn.h and gemm.h take any qhd,
+ * attn.h:99, :174, gemm.h:409-446; gemma4's global layers are 512 wide,
+ * model.h:562-564) and d = 64, 128, 256 or 512 for Q8 caches; anything else
+ * returns MOLOT_ENOTSUP before launching.
  * Semantics (include/molot/attn.h:125-177): n = valid slots after the
  * append, window <= 0 attends [0, n), otherwise [t0, n) with
  * t0 = max(0, pos_cur - window + 1); an empty range yields o = 0.
@@ -54,7 +54,7 @@ extern "C" {
  *                bytes: molot_hip_q8_row_bytes(nkv, d) bytes per token;
  *   paged        block = [nkv][page][d] codes, then [nkv][page] fp32 scales:
  *                molot_hip_q8_block_bytes(nkv, d, page) bytes per block.
- * Q8 runs on head dims 64 and 128 (MOLOT_ENOTSUP otherwise); the head-major
+ * Q8 runs on head dims 64, 128, 256 and 512 (MOLOT_ENOTSUP otherwise); the head-major
  * entry points take no Q8 cache (MOLOT_EINVAL). */
 #define MOLOT_KV_Q8 2
 
@@ -291,11 +291,20 @@ int molot_hip_attn_prefill_paged(const float* Qm, const void* K, const void* V, 
                                  int nkv, int M, int N, int d, float scale, int pos0, int window,
                                  int kv_dtype, void* stream);
 
-/* Softmax exponential used by the attention kernels, applied elementwise
- * (x, y device [n]).  Counterpart of exp_avx512_ps, include/molot/norm.h:35-47,
- * exposed so its accuracy can be checked against the reference's
- * known-answer points (bench/bench.cc:220-234). */
+/* The exponential of the split-K merges (the chunk weights e^(m_c - M),
+ * the device expf), applied elementwise (x, y device [n]).  Counterpart of
+ * exp_avx512_ps, include/molot/norm.h:35-47, exposed so its accuracy can be
+ * checked against the reference's known-answer points
+ * (bench/bench.cc:220-234). */
 int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream);
+
+/* The exponential the decode and prefill kernels take of every attention
+ * probability: y = 2^(x * log2(e)), the product rounded once to fp32 and
+ * one hardware v_exp_f32 (the kernels hold scores in base-2 units).  The
+ * other counterpart of exp_avx512_ps (norm.h:35-47), exposed for the same
+ * known-answer points; its relative error grows with |x| by the rounding
+ * of x * log2(e), ~|x| * 2^-24. */
+int molot_hip_prob_exp(const float* x, float* y, int64_t n, void* stream);
 
 /* Process-wide settings (no reference counterpart; for measurement and
  * tests).  Each is an atomic that launches read when they are planned, so
@@ -325,9 +334,14 @@ void molot_hip_set_merge(int in_launch);
  * on = 1 (default): the attended keys of every KV head are split into bf16
  * pieces once per launch, into a per-stream workspace of
  * 12 * nkv * (N - t0) * d bytes (at most 1 GiB; it grows outside stream
- * capture only), and the attention kernel copies them into LDS.  on = 0, or
- * when that workspace is unavailable: the attention kernel splits each
- * staged tile itself.  Both give the same bits. */
+ * capture only, and the buffers it outgrows stay allocated, under 1 GiB in
+ * all), and the attention kernel copies them into LDS.  on = 0, or when that
+ * workspace is unavailable: the attention kernel splits each staged tile
+ * itself.  Both give the same bits.  A Q8 cache at d = 256 always takes the
+ * pieces (its matrix-core kernel has no per-tile split); without them it
+ * runs on the vector-ALU kernel, each query row a sequence of its own (the
+ * path of d = 512 and of head dims that are not multiples of 8), which
+ * agrees to fp32 rounding. */
 void molot_hip_set_prefill_presplit(int on);
 
 /* Order in which the waves of a workgroup take their chunk's row blocks.

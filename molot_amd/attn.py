@@ -446,11 +446,22 @@ def rope_append_paged(q, k_new, v_new, K, V, block_table, seq_lens, pos, B, max_
 
 
 def vexp(x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
-    """The attention softmax's exp, elementwise (counterpart of norm.h:35-47)."""
+    """The split-K merges' exp (device expf), elementwise (counterpart of
+    norm.h:35-47)."""
     _need(x, "x", torch.float32)
     y = torch.empty_like(x) if y is None else y
     _need(y, "y", torch.float32, x.numel())
     check(_lib.load().molot_hip_vexp(_ptr(x), _ptr(y), x.numel(), _stream()), "vexp")
+    return y
+
+
+def prob_exp(x: torch.Tensor, y: torch.Tensor | None = None) -> torch.Tensor:
+    """The attention probabilities' exp as the kernels take it: 2^(x*log2 e)
+    with one v_exp_f32 (counterpart of norm.h:35-47)."""
+    _need(x, "x", torch.float32)
+    y = torch.empty_like(x) if y is None else y
+    _need(y, "y", torch.float32, x.numel())
+    check(_lib.load().molot_hip_prob_exp(_ptr(x), _ptr(y), x.numel(), _stream()), "prob_exp")
     return y
 
 

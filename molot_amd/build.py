@@ -1,7 +1,8 @@
 """Build recipes for the native parts of molot_amd (run on the CPU host).
 
 ``build_all()`` compiles, in-tree:
-  molot_amd/libmolot_amd.so   HIP kernels + C ABI (hipcc, gfx950)
+  molot_amd/libmolot_amd.so   HIP kernels + C ABI (hipcc, gfx950): the drop-in
+  molot_amd/libmolot_probe.so bench-only streaming probes (include/molot_amd/probe.h)
   tests/cpp/test_attn_cpp      C++ self-check of the header-only C++ layer
   tests/cpp/test_paged_kv      C++ self-check of the paged-KV manager
                               (include/molot_amd/attn.hpp), linked to the above
@@ -21,6 +22,7 @@ PKG = os.path.join(ROOT, "molot_amd")
 CSRC = os.path.join(PKG, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(PKG, "libmolot_amd.so")
+PROBE_LIB = os.path.join(PKG, "libmolot_probe.so")
 CPP_TEST = os.path.join(ROOT, "tests", "cpp", "test_attn_cpp")
 ARCH = os.environ.get("MOLOT_OFFLOAD_ARCH", "gfx950")
 
@@ -51,11 +53,19 @@ def _run(cmd: list[str]) -> None:
 
 
 def build_library() -> str:
-    srcs = [os.path.join(CSRC, "attn_decode.hip"), os.path.join(CSRC, "probe.hip")]
     tmp = LIB + ".tmp"
-    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", *srcs, "-o", tmp])
+    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", os.path.join(CSRC, "attn_decode.hip"),
+          "-o", tmp])
     os.replace(tmp, LIB)
     return LIB
+
+
+def build_probe_library() -> str:
+    tmp = PROBE_LIB + ".tmp"
+    _run([_hipcc(), *HIP_FLAGS, "-shared", f"-I{INCLUDE}", os.path.join(CSRC, "probe.hip"),
+          "-o", tmp])
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
 
 
 def build_cpp_test(name: str = "test_attn_cpp") -> str:
@@ -76,6 +86,7 @@ CPP_TESTS = ("test_attn_cpp", "test_paged_kv")
 
 def build_all() -> None:
     build_library()
+    build_probe_library()
     for name in CPP_TESTS:
         if os.path.exists(os.path.join(ROOT, "tests", "cpp", name + ".cpp")):
             build_cpp_test(name)

@@ -646,7 +646,6 @@ struct AttnArgs {
   float* part_o;         // [slots][nchunks][GH*D] chunk partial o (split-K)
   float* part_ml;        // [slots][nchunks][GH][2] chunk partial (max, sum)
   float* qrot;           // [slots][GH*D] rotated q for the combine kernel (ROPE)
-  int* part_x;           // [slots][nchunks] XCD of each chunk's workgroup (in-launch merge)
   void* ext_ws;          // host side only: caller-provided workspace (NULL: the library's)
   int64_t ext_ws_bytes;
   const int32_t* block_table;
@@ -657,13 +656,19 @@ struct AttnArgs {
   int dh;                // head dim as stored (< D: the kernel runs padded to its D)
   int dynamic;           // 1: waves claim blocks from a workgroup counter; 0: fixed order
   int chunk_fast;        // 1-D grid, the KV heads of a chunk on one XCD (Q8; see launch_pair)
+  // Prefill rows (attention-only launches): "sequence" b is query row b of a
+  // prompt, at position pos + b, attending [t0_b, min(pos + b + 1, n)) of the
+  // one cache (contiguous, or the prompt's block-table row: max_blocks = 0),
+  // t0_b from the window (include/molot/gemm.h:409-446).
+  int pf;
   int nseq;              // chunk_fast: sequences of the launch
   // In-launch merge (see arrive_and_merge): every chunk of a slot runs on one
   // XCD, and the workgroup that completes a slot merges its chunk partials.
   int fold;              // ROPE: 1 = the step appends the new token (folded into the last
                          // chunk, slot n-1); 0 = q prologue only (a layer reading another
                          // layer's KV: all n slots come from the cache)
-  int* ctr;              // [slots] arrival counters, zero between launches (NULL: combine kernel)
+  unsigned long long* ctr;  // [slots] arrival words (arrive_and_merge), zero between launches
+                            // (NULL: combine kernel)
   int xmap;              // 1-D grid of 8 * nchunks: slot id % 8 on XCD id % 8 (fewer than 8 slots)
   int slots;             // slots of the launch (xmap)
   int mrg;               // floats of LDS for the merge's chunk statistics (0: no in-launch merge)
@@ -694,8 +699,13 @@ struct Cfg {
   static constexpr int NV = D / (LPR * VW);  // 16-byte vectors per lane per K row
   static constexpr int EPL = NV * VW;        // q elements per lane
   static constexpr int RPS = 64 / LPR;       // K rows per wave step
-  static constexpr int LPR2 = D / VW;        // lanes per V row (PV)
-  static constexpr int RPI = 64 / LPR2;      // V rows per wave step
+  // PV: a V row is LPR2 <= 64 lanes of NV2 16-byte vectors each (NV2 = 2
+  // for fp32 rows of 512 elements); lane cs holds row elements
+  // (v2*LPR2 + cs)*VW .. +VW-1, so each v2 reads LPR2*16 contiguous bytes
+  static constexpr int NV2 = (D / VW + 63) / 64;
+  static constexpr int LPR2 = D / (VW * NV2);  // lanes per V row
+  static constexpr int AW = VW * NV2;          // o accumulators per head and lane
+  static constexpr int RPI = 64 / LPR2;        // V rows per wave step
   static constexpr int RB = RB_;
   static constexpr int KS = RB / RPS;  // K steps per block
   static constexpr int VS = RB / RPI;  // V steps per block
@@ -705,8 +715,8 @@ struct Cfg {
   // chunk partial: PP output pairs per thread (P > NT), Q threads per copy
   static constexpr int PP = (P + NT - 1) / NT;
   static constexpr int Q = P < NT ? P : NT;
-  static_assert(NV >= 1 && D % (LPR * VW) == 0, "bad score mapping");
-  static_assert(LPR2 <= 64 && 64 % LPR2 == 0, "bad PV mapping");
+  static_assert(NV >= 1 && D % (LPR * VW) == 0 && LPR <= 64, "bad score mapping");
+  static_assert(LPR2 * VW * NV2 == D && LPR2 <= 64 && 64 % LPR2 == 0, "bad PV mapping");
   static_assert(RB % RPS == 0 && RB % RPI == 0, "bad block");
   static_assert(P % 64 == 0 || P <= NT, "pairs per phase");
 };
@@ -721,15 +731,16 @@ struct Tune {
   static constexpr int VW = KVT<T>::VW;
   static constexpr int lpr() {
     int l = 8;
-    while (GH * D / l > 32 && l < D / VW) l *= 2;
+    while (GH * D / l > 32 && l < D / VW && l < 64) l *= 2;
     return l;
   }
   static constexpr int LPR = lpr();
   static constexpr int NV = D / (LPR * VW);
-  static constexpr int RPS = 64 / LPR, RPI = 64 / (D / VW);
-  static constexpr int loads(int rb) { return (rb / RPS) * NV + rb / RPI; }
+  static constexpr int NV2 = (D / VW + 63) / 64;
+  static constexpr int RPS = 64 / LPR, RPI = 64 / (D / (VW * NV2));
+  static constexpr int loads(int rb) { return (rb / RPS) * NV + (rb / RPI) * NV2; }
   static constexpr int regs(int rb) {  // one block of data + its addresses
-    return GH * NV * VW + GH * VW + 6 * loads(rb) + (rb / RPS) * GH + 3 * GH + 40;
+    return GH * NV * VW + GH * VW * NV2 + 6 * loads(rb) + (rb / RPS) * GH + 3 * GH + 40;
   }
   static constexpr int wps(int rb) {
     const int r = (regs(rb) + 7) / 8 * 8;
@@ -745,8 +756,18 @@ struct Tune {
   // fp32: step 28.8 -> 27.3 us at n = 16385, 14.0 -> 13.3 us at n = 4097;
   // at d = 256, 8q/4kv with a 1024 window, 12 waves of 4-row blocks stay
   // faster: 9.3 against 9.6 us).
+  // d = 512: the largest block whose loads fit at two waves per SIMD (fp32
+  // 4 rows = 16 KB of K and V a wave, bf16 8 rows), else at one.
+  static constexpr bool fits(int rb, int w) {
+    return rb % RPS == 0 && rb % RPI == 0 && loads(rb) <= 16 && wps(rb) >= w;
+  }
   static constexpr int rb() {
     if (D <= 128 && ok(8)) return 8;
+    if (D > 256) {
+      for (int w : {2, 1})
+        for (int r : {16, 8, 4, 2, 1})
+          if (fits(r, w)) return r;
+    }
     int best = 0;
     for (int r : {16, 4})
       if (ok(r) && (best == 0 || wps(r) > wps(best))) best = r;
@@ -766,11 +787,16 @@ struct Tune {
 
 // Dynamic LDS layout shared by host (size) and device (offsets), in floats.
 struct Lds {
-  int qs, cs, sn, knew, vnew, nw, pw, wm, wl, red, blk, misc, mrg, total;
+  int qs, cs, sn, knew, vnew, nw, pw, wm, wl, red, blk, misc, mrg, qw, psum, total;
   __host__ __device__ Lds(int D, int GH, int NW, int RB, int chunk, int page_shift, bool paged,
                           int merge) {
+    const bool wide = D / 4 > 64;  // a q row spans more than one wave (d = 512)
     int o = 0;
     qs = o; o += GH * D;
+    qw = o; o += wide ? D : 0;       // q norm weights
+    // q rows' sums of squares, per 64 quads (padded: later regions are read
+    // as 16-byte vectors)
+    psum = o; o += wide ? (GH * (D / 256) + 3) / 4 * 4 : 0;
     cs = o; o += D / 2;
     sn = o; o += D / 2;
     knew = o; o += D;
@@ -835,9 +861,8 @@ __device__ __forceinline__ void q_norm_regs(const AttnArgs& a, f32x4 (&qv)[QPT],
 // the threads that rotate k and round v after that barrier scale them:
 // k by 1/sqrt(mean(k^2) + eps) and its weights (staged in LDS), v by the RMS
 // of all of v_new without weights (rmsnorm_plain, norm.h:82-96).
-template <int D>
-__device__ __forceinline__ void k_norm_share(int tid, int w, int lane, float knv, float* ksum) {
-  const float ss = group_sum<64>(tid < D ? knv * knv : 0.f);
+__device__ __forceinline__ void k_norm_share(int w, int lane, float ss, float* ksum) {
+  ss = group_sum<64>(ss);
   if (lane == 0) ksum[w] = ss;
 }
 
@@ -918,23 +943,33 @@ __device__ __forceinline__ void v_norm_share(const AttnArgs& a, int b, int tid, 
 // point of that XCD's CUs, and the hand-off needs no cache writeback:
 //   - each workgroup stores its partial (plain stores, which write through
 //     the CU's L1 into the L2), waits until the L2 has acknowledged them
-//     (s_waitcnt vmcnt(0) in every thread, then a barrier) and adds one
-//     arrival to the slot's counter (a global atomic, performed past the L1);
-//   - the workgroup whose add returns nch - 1 arrived last: every other
-//     chunk's stores were acknowledged before its arrival.  It resets the
-//     counter to 0 for the next launch and reads the partials back with
-//     loads that miss the L1 (cache policy sc0), so they come from the L2;
-//   - it merges them with log-sum-exp weights as combine_kernel does and
-//     writes O and, with ROPE, the rotated q (every workgroup of the slot
-//     has read q by the time it arrives).
+//     (a workgroup-scope release fence, s_waitcnt vmcnt(0), in every thread,
+//     then a barrier) and adds one arrival to the slot's 64-bit arrival word
+//     (a device-scope atomic, coherent across the XCDs);
+//   - the arrival adds 1 + x*2^13 + x^2*2^29 for its XCD x = XCC_ID: the
+//     word counts the arrivals (bits 0-12), and sums x (bits 13-28) and x^2
+//     (bits 29-63).  The workgroup whose add completes the count arrived
+//     last: every other chunk's stores were acknowledged before its arrival.
+//     It resets the word to 0 for the next launch.  All nch chunks ran on
+//     its own XCD m exactly when the sums are nch*m and nch*m^2 (the
+//     variance of the XCDs is then 0), checked from the atomic's own
+//     return value, so a violated dispatch assumption can never be read
+//     from a stale record: the output is then NaN, never a stale merge;
+//   - it reads the partials back with loads that miss the L1 (cache policy
+//     sc0), so they come from the L2, merges them with log-sum-exp weights
+//     as combine_kernel does and writes O and, with ROPE, the rotated q
+//     (every workgroup of the slot has read q by the time it arrives).
 // No workgroup waits for another: nothing spins, and a launch's arrivals
-// are exactly its slots' chunk counts, so the counters are back at zero when
+// are exactly its slots' chunk counts, so the words are back at zero when
 // it ends (they are zeroed when the workspace is allocated).
+constexpr int kArriveCountBits = 13;  // arrivals of a slot: at most kMergeMaxChunks
+constexpr int kArriveSumBits = 16;    // sum of XCC_ID over the arrivals (<= 7 * 4096)
+__device__ __forceinline__ unsigned long long arrive_word(int x) {
+  const unsigned long long ux = (unsigned long long)x;
+  return 1ull | (ux << kArriveCountBits) | ((ux * ux) << (kArriveCountBits + kArriveSumBits));
+}
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_rsrc(const float* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7FFFFFFF, 0x00020000);
-}
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_rsrc_i(const int* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<int*>(base), 0, 0x7FFFFFFF, 0x00020000);
 }
 // Loads at a byte offset of a resource, missing the L1 (cache policy sc0).
 __device__ __forceinline__ f32x4 ld_l2x4(__amdgpu_buffer_rsrc_t r, int off) {
@@ -976,6 +1011,10 @@ __device__ __forceinline__ void store_quad(float* o, int64_t qrow0, int q, f32x4
 }
 
 constexpr int kMergeMaxChunks = 4096;  // chunks of a slot merged in the launch
+static_assert(kMergeMaxChunks < (1 << kArriveCountBits) &&
+                  7 * kMergeMaxChunks < (1 << kArriveSumBits) &&
+                  49ull * kMergeMaxChunks < (1ull << (64 - kArriveCountBits - kArriveSumBits)),
+              "arrival word fields");
 constexpr int kMergeAutoSpan = 8192;   // rows from which the default merges in the launch
 constexpr int kMergeMaxPhases = 64;    // threads per float4 quad of the output (NT / quads)
 constexpr int kMergeRound = 8;         // chunks per thread whose loads are in flight together
@@ -999,16 +1038,25 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
                                                  float* mred, int* flag, int tid, int lane,
                                                  int dh) {
   constexpr int P = GH * D;
-  wait_vmcnt<0>();  // this thread's partial stores are in the L2
+  // this thread's partial stores are acknowledged by the L2 (vmcnt(0):
+  // outside threadgroup-split mode the workgroup-scope release fence alone
+  // need not wait for them)
+  wait_vmcnt<0>();
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   lds_barrier();
   if (tid == 0) {
-    const int old = atomicAdd(a.ctr + slot, 1);
-    const int last = old == nch - 1;
-    if (last) atomicExch(a.ctr + slot, 0);  // ready for the next launch
+    const int x = xcc_id();
+    const unsigned long long tot = atomicAdd(a.ctr + slot, arrive_word(x)) + arrive_word(x);
+    const bool last = (int)(tot & ((1ull << kArriveCountBits) - 1)) == nch;
+    if (last) atomicExch(a.ctr + slot, 0ull);  // ready for the next launch
+    const unsigned long long n64 = (unsigned long long)nch, x64 = (unsigned long long)x;
+    const bool one_xcd = ((tot >> kArriveCountBits) & ((1ull << kArriveSumBits) - 1)) == n64 * x64 &&
+                         (tot >> (kArriveCountBits + kArriveSumBits)) == n64 * x64 * x64;
     flag[0] = last;
-    flag[1] = 0;  // set below if a chunk ran on another XCD
+    flag[1] = last && !one_xcd;  // a chunk of the slot ran on another XCD
   }
   lds_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   if (!flag[0]) return;  // uniform over the workgroup
 
   constexpr int QV = P / 4;                     // float4 quads of the slot's output
@@ -1069,15 +1117,6 @@ __device__ __forceinline__ void arrive_and_merge(const AttnArgs& a, int64_t slot
   }
   // The hand-off above holds only if every chunk of the slot ran on this
   // XCD (one L2): otherwise the output is NaN, never a silently stale merge.
-  if (tid < 64) {
-    const __amdgpu_buffer_rsrc_t rx = l2_rsrc_i(a.part_x + slot * a.nchunks);
-    const int my_xcc = xcc_id();
-    bool other_xcd = false;
-    for (int cc = lane; cc < nch; cc += 64)
-      other_xcd |= __builtin_amdgcn_raw_buffer_load_b32(rx, 4 * cc, 0, 1) != my_xcc;
-    if (__builtin_amdgcn_ballot_w64(other_xcd) != 0 && lane == 0) flag[1] = 1;
-  }
-  lds_barrier();
   const float bad = flag[1] ? __builtin_nanf("") : 0.f;
   if constexpr (PH > 1) {
     // a phase's (max, sum) is the same for every quad of a head: the
@@ -1197,7 +1236,6 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
     }
   }
   if (a.ctr) {  // in-launch merge: the workgroup completing the slot merges it
-    if (tid == 0) a.part_x[slot * a.nchunks + c] = xcc_id();
     arrive_and_merge<D, GH, NW, NT, ROPE, RED, QSTR>(a, slot, nch, qrow0, qs, mst, mred, flag, tid,
                                                lane, dh);
     return;
@@ -1208,11 +1246,56 @@ __device__ __forceinline__ void finish_chunk(const AttnArgs& a, const float* wm,
   }
 }
 
+// A sequence of a batch whose window leaves no cache row attended, in a
+// launch that appends nothing (a layer reading another layer's KV,
+// forward.h:578-585): its q rows are still normed and rotated in place, as
+// forward.h:554-558 does before every attention call, and its o is 0
+// (attn.h:162 with no rows).  The whole workgroup takes this path; nothing
+// else is in flight, so plain workgroup barriers are free here.  Same
+// arithmetic as rope_append_kernel: (x * 1/sqrt(mean(x^2) + eps)) * w, then
+// the NEOX rotation by the fp32 angle pos * inv_freq[j] (sine and cosine in
+// double, rounded).
+template <int NT>
+__device__ void empty_range_q(const AttnArgs& a, int64_t qrow0, int gh, int dh, int pos,
+                              float* sh) {
+  const int tid = threadIdx.x, half = dh / 2;
+  const bool rot = a.inv_freq != nullptr;
+  for (int g = 0; g < gh; ++g) {
+    const float* x = a.q + (qrow0 + g) * dh;
+    float* y = a.q_out + (qrow0 + g) * dh;
+    float inv = 1.f;
+    if (a.q_norm) {  // uniform
+      float ss = 0.f;
+      for (int j = tid; j < dh; j += NT) ss = fmaf(x[j], x[j], ss);
+      inv = 1.0f / sqrtf(block_sum(ss, sh) / (float)dh + a.eps);
+    }
+    for (int j = tid; j < half; j += NT) {
+      float x0 = x[j], x1 = x[j + half];
+      if (a.q_norm) {
+        x0 = x0 * inv * a.q_norm[j];
+        x1 = x1 * inv * a.q_norm[j + half];
+      }
+      if (rot) {
+        const float ang = (float)pos * a.inv_freq[j];
+        double sd, cd;
+        sincos((double)ang, &sd, &cd);
+        const float c = (float)cd, sn = (float)sd;
+        y[j] = x0 * c - x1 * sn;
+        y[j + half] = x0 * sn + x1 * c;
+      } else {
+        y[j] = x0;
+        y[j + half] = x1;
+      }
+    }
+  }
+}
+
 template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD, typename C>
 __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   using V16 = typename KVT<T>::vec;
   constexpr int VW = C::VW, LPR = C::LPR, NV = C::NV, EPL = C::EPL, RPS = C::RPS;
   constexpr int LPR2 = C::LPR2, RPI = C::RPI, RB = C::RB, KS = C::KS, VS = C::VS;
+  constexpr int NV2 = C::NV2, AW = C::AW;
   constexpr int NW = C::NW, NT = C::NT, P = C::P;
 
   extern __shared__ float smem[];
@@ -1257,9 +1340,17 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
 
   int n = a.n, t0 = a.t0, pos = a.pos;
-  if constexpr (PAGED) {
-    n = a.seq_lens[b];
-    pos = a.pos_arr ? a.pos_arr[b] : n - 1;
+  // per-sequence ranges in contiguous chunks: a paged batch, or prefill rows
+  bool perseq = PAGED;
+  if constexpr (!ROPE) perseq = PAGED || a.pf;  // uniform
+  if (perseq) {
+    if (!ROPE && a.pf) {
+      pos = a.pos + b;
+      n = min(pos + 1, a.n);
+    } else {
+      n = a.seq_lens[b];
+      pos = a.pos_arr ? a.pos_arr[b] : n - 1;
+    }
     t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
     if (t0 > n) t0 = n;
   }
@@ -1268,14 +1359,17 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const bool fold = ROPE && a.fold;  // this launch appends and folds in the new token
   const int cend = fold ? n - 1 : n;
   int nch = a.nchunks;
-  if constexpr (PAGED) {
+  if (perseq) {
     const int span = cend - t0;
     nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (fold ? 1 : 0);
     if (nch > a.nchunks) nch = a.nchunks;
   }
   if (z >= nch) {  // whole workgroup: chunk past this sequence's end (never arrives)
-    if (z == 0)    // empty attended range: o = 0 (include/molot/attn.h:162 with no rows)
+    if (z == 0) {  // empty attended range: o = 0 (include/molot/attn.h:162 with no rows)
       for (int i = tid; i < GH * DH; i += NT) a.o[((int64_t)b * a.nq + hq0) * DH + i] = 0.f;
+      if (ROPE && !fold && a.q_out)  // nothing appended: q still leaves normed and rotated
+        empty_range_q<NT>(a, (int64_t)b * a.nq + hq0, GH, DH, pos, smem);
+    }
     return;
   }
   // Chunks in reverse: the last one, which holds the new token (and with it
@@ -1328,7 +1422,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   const int rr = lane / LPR;   // scores: row of the group within a K step
   const int cs = lane % LPR2;  // PV: columns cs*VW .. cs*VW+VW-1
   const int rs = lane / LPR2;  // PV: row within a V step
-  V16 kA[KS][NV], vA[VS], kB[KS][NV], vB[VS];
+  V16 kA[KS][NV], vA[VS][NV2], kB[KS][NV], vB[VS][NV2];
   float ksA[KS], vsA[VS], ksB[KS], vsB[VS];  // Q8 row scales (unused otherwise)
   // Every wave issues the same sequence of global loads on every path: the
   // compiler counts outstanding loads per path and, where paths merge with
@@ -1343,18 +1437,18 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   // the launch's workgroups read neighbouring rows at any moment; blocks of
   // RB rows never straddle a group).
   static_assert(32 % RB == 0, "blocks within 32-row groups");
-  const int rlim = PAGED ? cntg : cend - t0;  // rows of the chunk / of the whole range
-  const int rfirst = PAGED ? tb : t0;
+  const int rlim = perseq ? cntg : cend - t0;  // rows of the chunk / of the whole range
+  const int rfirst = perseq ? tb : t0;
   const int rmax = max(rlim - 1, 0);
   auto gmap = [&](int lr) -> int {  // local row -> row from rfirst
-    return PAGED ? lr : (c + (lr >> 5) * nch) * 32 + (lr & 31);
+    return perseq ? lr : (c + (lr >> 5) * nch) * 32 + (lr & 31);
   };
   // Local rows of this chunk: its valid rows come first, so every block
   // below nblk starts with a valid row (a block of no valid rows would meet
   // m_run = -inf with a -inf score: e^(-inf - -inf) is NaN).  The chunk
   // holding the range's last group counts only that group's valid rows.
   int nrows = cntg;
-  if constexpr (!PAGED) {
+  if (!perseq) {
     const int groups = (rlim + 31) / 32;
     nrows = 0;
     if (c < groups) {
@@ -1362,7 +1456,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       nrows = 32 * last + min(32, rlim - 32 * (c + last * nch));
     }
   }
-  auto load_block = [&](V16 (&kr)[KS][NV], V16 (&vr)[VS], float (&ksr)[KS], float (&vsr)[VS],
+  auto load_block = [&](V16 (&kr)[KS][NV], V16 (&vr)[VS][NV2], float (&ksr)[KS], float (&vsr)[VS],
                         int rbase) {
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
@@ -1381,10 +1475,13 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     for (int k = 0; k < VS; ++k) {
       const int t = rfirst + min(gmap(rbase + k * RPI + rs), rmax);
       const T* p = row_ptr(Vb, t);
-      if constexpr (PAD)
-        vr[k] = load_pad(p, cs * VW, DH);
-      else
-        vr[k] = load16(p + cs * VW);
+#pragma unroll
+      for (int v2 = 0; v2 < NV2; ++v2) {
+        if constexpr (PAD)
+          vr[k][v2] = load_pad(p, (v2 * LPR2 + cs) * VW, DH);
+        else
+          vr[k][v2] = load16(p + (v2 * LPR2 + cs) * VW);
+      }
       if constexpr (Q8) vsr[k] = *sc_ptr(Vb, t);
     }
   };
@@ -1393,7 +1490,11 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   // waiting for them does not also wait for the K/V blocks issued next.
   constexpr int QV = GH * D / 4;  // float4s of q of the group
   constexpr int QPT = (QV + NT - 1) / NT;
-  static_assert(D <= NT, "one thread per head-dim element in the prologue");
+  // the fresh k and v rows: KPT elements a thread (two at d = 512 on 4 waves)
+  constexpr int KPT = (D + NT - 1) / NT;
+  static_assert(D / 2 <= NT, "one thread per rotation pair in the prologue");
+  // a q row wider than a wave (d = 512): its norm sums through LDS (psum)
+  constexpr bool QWIDE = D / 4 > 64;
   f32x4 qv[QPT];
   // A padded launch reads the q rows (and the q norm weights) at their
   // stored length DH, in two-element pieces, each selected to 0 past DH:
@@ -1412,7 +1513,9 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   };
 #pragma unroll
   for (int u = 0; u < QPT; ++u) qv[u] = row_quad(a.q + qrow0 * DH, min(tid + u * NT, QV - 1), DH);
-  float invf = 0.f, knv = 0.f, vnv = 0.f, kwv = 0.f;
+  float invf = 0.f, knv[KPT], vnv[KPT], kwv[KPT];
+#pragma unroll
+  for (int u = 0; u < KPT; ++u) knv[u] = vnv[u] = kwv[u] = 0.f;
   f32x4 qwt[QPT];  // q norm weights of this thread's q elements
   if constexpr (ROPE) {
     // every path issues these loads: a layer without RoPE (inv_freq NULL)
@@ -1421,15 +1524,22 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     const float* knp = fold ? a.k_new : a.q;
     const float* vnp = fold ? a.v_new : a.q;
     invf = ivp[min(tid, DH / 2 - 1)];
-    knv = knp[((int64_t)b * a.nkv + h) * DH + min(tid, DH - 1)];
-    vnv = vnp[((int64_t)b * a.nkv + h) * DH + min(tid, DH - 1)];
-    if (PAD && tid >= DH) knv = vnv = 0.f;  // the padding of the new k and v rows
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int j = tid + u * NT;
+      knv[u] = knp[((int64_t)b * a.nkv + h) * DH + min(j, DH - 1)];
+      vnv[u] = vnp[((int64_t)b * a.nkv + h) * DH + min(j, DH - 1)];
+      if (j >= DH) knv[u] = vnv[u] = 0.f;  // the padding of the new k and v rows
+    }
     if (a.q_norm) {
 #pragma unroll
       for (int u = 0; u < QPT; ++u)
         qwt[u] = row_quad(a.q_norm, min(tid + u * NT, QV - 1) % (D / 4), 0);
     }
-    if (is_new && a.k_norm) kwv = a.k_norm[min(tid, DH - 1)];
+    if (is_new && a.k_norm) {
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) kwv[u] = a.k_norm[min(tid + u * NT, DH - 1)];
+    }
   }
   float vq[kVnPT];
   const bool vn = ROPE && is_new && a.v_norm;  // uniform over the workgroup
@@ -1442,7 +1552,28 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     misc[0] = C::NBUF * NW;  // next block to claim
   }
   if constexpr (ROPE) {
-    if (a.q_norm) q_norm_regs<D, QPT>(a, qv, qwt, DH);
+    if (a.q_norm) {
+      if constexpr (!QWIDE) {
+        q_norm_regs<D, QPT>(a, qv, qwt, DH);
+      } else {
+        // 64 consecutive quads (one wave's share of a u) lie in one row:
+        // their sum of squares to psum[row][part]; the weights to qw.  The
+        // rotation pass below applies the norm.
+#pragma unroll
+        for (int u = 0; u < QPT; ++u) {
+          const int i = tid + u * NT;
+          if (i < QV) {  // uniform over the wave: QV is a multiple of 64
+            float ss = qv[u][0] * qv[u][0];
+            ss = fmaf(qv[u][1], qv[u][1], ss);
+            ss = fmaf(qv[u][2], qv[u][2], ss);
+            ss = fmaf(qv[u][3], qv[u][3], ss);
+            ss = group_sum<64>(ss);
+            if (lane == 0) smem[L.psum + i / 64] = ss;
+            if (i < D / 4) reinterpret_cast<f32x4*>(smem + L.qw)[i] = qwt[u];
+          }
+        }
+      }
+    }
   }
 #pragma unroll
   for (int u = 0; u < QPT; ++u) {
@@ -1460,21 +1591,42 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       csn[tid] = (float)cd;
       sn[tid] = (float)sd;
     }
-    if (is_new && tid < D) {
-      knew[tid] = knv;
-      vnew[tid] = vnv;
+#pragma unroll
+    for (int u = 0; u < KPT; ++u) {
+      const int j = tid + u * NT;
+      if (j < D) {
+        if (is_new) {
+          knew[j] = knv[u];
+          vnew[j] = vnv[u];
+        }
+        smem[L.nw + j] = kwv[u];
+      }
     }
     if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl, DH);
-    if (tid < D) smem[L.nw + tid] = kwv;
-    if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
+    if (is_new && a.k_norm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int u = 0; u < KPT; ++u) ss = fmaf(knv[u], knv[u], ss);  // 0 past D
+      k_norm_share(w, lane, ss, smem + L.wm);
+    }
     lds_barrier();
-    // NEOX pairs (j, j + DH/2) of the stored head (attn.h:17-28)
+    // NEOX pairs (j, j + DH/2) of the stored head (attn.h:17-28); a q row
+    // wider than a wave takes its norm here: (x * inv) * w, as q_norm_regs
     const int half = DH / 2;
-    for (int i = tid; rot && i < GH * half; i += NT) {
+    const bool qwn = QWIDE && a.q_norm;
+    for (int i = tid; (rot || qwn) && i < GH * half; i += NT) {
       const int g = i / half, j = i - g * half;
-      const float x0 = qs[g * D + j], x1 = qs[g * D + j + half];
-      qs[g * D + j] = x0 * csn[j] - x1 * sn[j];
-      qs[g * D + j + half] = x0 * sn[j] + x1 * csn[j];
+      float x0 = qs[g * D + j], x1 = qs[g * D + j + half];
+      if (qwn) {
+        float ss = 0.f;
+#pragma unroll
+        for (int pt = 0; pt < D / 256; ++pt) ss += smem[L.psum + g * (D / 256) + pt];
+        const float inv = 1.0f / sqrtf(ss / (float)DH + a.eps);
+        x0 = x0 * inv * smem[L.qw + j];
+        x1 = x1 * inv * smem[L.qw + j + half];
+      }
+      qs[g * D + j] = rot ? x0 * csn[j] - x1 * sn[j] : x0;
+      qs[g * D + j + half] = rot ? x0 * sn[j] + x1 * csn[j] : x1;
     }
     if (is_new) {
       // the appended row as the cache will hold it: normed (as configured),
@@ -1525,13 +1677,13 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 
   // ---- 2. streaming blocks with a per-wave online softmax ----
   float* pw = smem + L.pw + w * RB * GH;
-  float m_run[GH], l_run[GH], acc[GH][VW];
+  float m_run[GH], l_run[GH], acc[GH][AW];
 #pragma unroll
   for (int g = 0; g < GH; ++g) {
     m_run[g] = -INFINITY;
     l_run[g] = 0.f;
 #pragma unroll
-    for (int e = 0; e < VW; ++e) acc[g][e] = 0.f;
+    for (int e = 0; e < AW; ++e) acc[g][e] = 0.f;
   }
   int next_fixed = w + C::NBUF * NW;  // fixed order: wave w takes blocks w, w+NW, w+2NW, ...
   auto claim = [&]() -> int {
@@ -1544,7 +1696,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     if (lane == 0) v = atomicAdd(&misc[0], 1);
     return __builtin_amdgcn_readfirstlane(v);
   };
-  auto consume = [&](const V16 (&kr)[KS][NV], const V16 (&vr)[VS], const float (&ksr)[KS],
+  auto consume = [&](const V16 (&kr)[KS][NV], const V16 (&vr)[VS][NV2], const float (&ksr)[KS],
                      const float (&vsr)[VS], int rbase) {
     // scores of this lane group's rows
     float sc[KS][GH];
@@ -1591,7 +1743,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
         m_run[g] = mn;
         l_run[g] *= alpha;
 #pragma unroll
-        for (int e = 0; e < VW; ++e) acc[g][e] *= alpha;
+        for (int e = 0; e < AW; ++e) acc[g][e] *= alpha;
       }
     }
 #pragma unroll
@@ -1604,8 +1756,9 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int k = 0; k < VS; ++k) {
-      float x[VW];
-      KVT<T>::unpack(vr[k], x);
+      float x[AW];
+#pragma unroll
+      for (int v2 = 0; v2 < NV2; ++v2) KVT<T>::unpack(vr[k][v2], x + v2 * VW);
       float p[GH];
 #pragma unroll
       for (int g = 0; g < GH; ++g) p[g] = pw[(k * RPI + rs) * GH + g];
@@ -1614,7 +1767,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
         l_run[g] += p[g];
         const float pv = Q8 ? p[g] * vsr[k] : p[g];  // Q8: codes times the V row's scale
 #pragma unroll
-        for (int e = 0; e < VW; ++e) acc[g][e] = fmaf(pv, x[e], acc[g][e]);
+        for (int e = 0; e < AW; ++e) acc[g][e] = fmaf(pv, x[e], acc[g][e]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -1700,13 +1853,15 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     // add the row's values, the others add 0 (a select per element, not a
     // branch around each read)
     const float one = rs == 0 ? 1.f : 0.f;
-    float vx[VW];
+    float vx[AW];
 #pragma unroll
-    for (int e4 = 0; e4 < VW; e4 += 4) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(vnew + cs * VW + e4);
+    for (int v2 = 0; v2 < NV2; ++v2)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) vx[e4 + e] = t[e] * one;
-    }
+      for (int e4 = 0; e4 < VW; e4 += 4) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(vnew + (v2 * LPR2 + cs) * VW + e4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vx[v2 * VW + e4 + e] = t[e] * one;
+      }
     float part[GH];
 #pragma unroll
     for (int g = 0; g < GH; ++g) {
@@ -1723,7 +1878,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
       m_run[g] = mn;
       l_run[g] = l_run[g] * alpha + p * one;
 #pragma unroll
-      for (int e = 0; e < VW; ++e) acc[g][e] = acc[g][e] * alpha + p * vx[e];
+      for (int e = 0; e < AW; ++e) acc[g][e] = acc[g][e] * alpha + p * vx[e];
     }
   }
 
@@ -1734,7 +1889,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     for (int g = 0; g < GH; ++g) {
       l_run[g] += __shfl_xor(l_run[g], off);
 #pragma unroll
-      for (int e = 0; e < VW; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+      for (int e = 0; e < AW; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
     }
   float* wm = smem + L.wm;
   float* wl = smem + L.wl;
@@ -1750,7 +1905,10 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int g = 0; g < GH; ++g)
 #pragma unroll
-      for (int e = 0; e < VW; ++e) red[(w * GH + g) * D + cs * VW + e] = acc[g][e];
+      for (int v2 = 0; v2 < NV2; ++v2)
+#pragma unroll
+        for (int e = 0; e < VW; ++e)
+          red[(w * GH + g) * D + (v2 * LPR2 + cs) * VW + e] = acc[g][v2 * VW + e];
   }
   lds_barrier();
   finish_chunk<D, GH, NW, NT, ROPE, NW * P>(a, wm, wl, red, P, qs, tid, lane, split, slot, c,
@@ -1761,7 +1919,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   // launch).  Last, because nothing may wait for these stores: vmcnt counts
   // stores too, and a wait placed after them for an older load would hold
   // the fold and the merge until the stores complete. ----
-  if (is_new && sub == 0 && (Q8 ? w == 0 : tid < DH)) {
+  if (is_new && sub == 0 && (Q8 ? w == 0 : tid < DH)) {  // (d = 512: tid, tid + NT)
     const int slot_row = n - 1;
     int64_t off, soff;  // element (Q8: byte) offset of the row; Q8: of its scale
     if constexpr (PAGED) {
@@ -1784,11 +1942,15 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
         *reinterpret_cast<float*>(reinterpret_cast<char*>(a.v) + soff) = vscale;
       }
     } else if constexpr (sizeof(T) == 2) {  // exact bf16 values: the rounding returns their bits
-      reinterpret_cast<uint16_t*>(a.k)[off + tid] = f32_to_bf16(knew[tid]);
-      reinterpret_cast<uint16_t*>(a.v)[off + tid] = f32_to_bf16(vnew[tid]);
+      for (int j = tid; j < DH; j += NT) {
+        reinterpret_cast<uint16_t*>(a.k)[off + j] = f32_to_bf16(knew[j]);
+        reinterpret_cast<uint16_t*>(a.v)[off + j] = f32_to_bf16(vnew[j]);
+      }
     } else {
-      reinterpret_cast<float*>(a.k)[off + tid] = knew[tid];
-      reinterpret_cast<float*>(a.v)[off + tid] = vnew[tid];
+      for (int j = tid; j < DH; j += NT) {
+        reinterpret_cast<float*>(a.k)[off + j] = knew[j];
+        reinterpret_cast<float*>(a.v)[off + j] = vnew[j];
+      }
     }
   }
 }
@@ -2002,8 +2164,10 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     if (nch > a.nchunks) nch = a.nchunks;
   }
   if (z >= nch) {
-    if (z == 0)
+    if (z == 0) {  // empty attended range: o = 0, and q normed and rotated (empty_range_q)
       for (int i = tid; i < GH * D; i += NT) a.o[((int64_t)b * a.nq + hq0) * D + i] = 0.f;
+      if (ROPE && !fold && a.q_out) empty_range_q<NT>(a, (int64_t)b * a.nq + hq0, GH, D, pos, smem);
+    }
     return;
   }
   const int c = nch - 1 - z;  // the new token's chunk first, as in attn_kernel
@@ -2161,7 +2325,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
     }
     if (vn) v_norm_share<D, NT>(a, b, tid, w, lane, vq, smem + L.wl, DH);
     if (tid < D) smem[L.nw + tid] = kwv;
-    if (is_new && a.k_norm) k_norm_share<D>(tid, w, lane, knv, smem + L.wm);
+    if (is_new && a.k_norm) k_norm_share(w, lane, tid < D ? knv * knv : 0.f, smem + L.wm);
     lds_barrier();
     for (int i = tid; rot && i < GH * (D / 2); i += NT) {
       const int g = i / (D / 2), j = i - g * (D / 2);
@@ -2974,7 +3138,26 @@ struct CombArgs {
   int nq, nkv, gh, nsub, d, nchunks, chunk, window, rope, paged;
   int fold;  // the attention launch folded in a new token (its chunks tile n - 1 rows)
   int dh;    // head dim as stored (d: the partials' padded head dim)
+  int pf, pos0, n;  // prefill rows (AttnArgs::pf): row b at pos0 + b of a cache of n rows
 };
+
+// Chunks of sequence b of a per-sequence launch (a paged batch, or prefill
+// rows), as the attention kernel derives them.
+__device__ __forceinline__ int comb_chunks(const CombArgs& a, int b) {
+  int n, pos;
+  if (a.pf) {
+    pos = a.pos0 + b;
+    n = pos + 1 < a.n ? pos + 1 : a.n;
+  } else {
+    n = a.seq_lens[b];
+    pos = a.pos_arr ? a.pos_arr[b] : n - 1;
+  }
+  int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
+  if (t0 > n) t0 = n;
+  const int span = (a.fold ? n - 1 : n) - t0;
+  const int nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.fold ? 1 : 0);
+  return nch > a.nchunks ? a.nchunks : nch;
+}
 
 constexpr int kCombThreads = 256;
 constexpr int kCombPairs = 64;                          // pairs per workgroup
@@ -3017,16 +3200,8 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
     m1 = pml[(int64_t)c1 * a.gh * 2];
     l1 = pml[(int64_t)c1 * a.gh * 2 + 1];
   }
-  int nch = a.nchunks;
-  if (a.paged) {  // this sequence's chunk count, as the attention kernel derives it
-    const int n = a.seq_lens[b];
-    const int pos = a.pos_arr ? a.pos_arr[b] : n - 1;
-    int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
-    if (t0 > n) t0 = n;
-    const int span = (a.fold ? n - 1 : n) - t0;
-    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.fold ? 1 : 0);
-    if (nch > a.nchunks) nch = a.nchunks;
-  }
+  // this sequence's chunk count, as the attention kernel derives it
+  const int nch = a.paged || a.pf ? comb_chunks(a, b) : a.nchunks;
   if (nch <= 1) return;  // uniform over the workgroup
   if (t < 64) {  // wave 0: chunk weights and L of head g
     float mloc = -INFINITY;
@@ -3105,16 +3280,8 @@ __global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs
   for (int u = 0; u < R; ++u) ov[u] = po[(int64_t)min(u, a.nchunks - 1) * P];
   const int cl = min(lane, a.nchunks - 1);
   const float mc = pml[(int64_t)cl * a.gh * 2], lc = pml[(int64_t)cl * a.gh * 2 + 1];
-  int nch = a.nchunks;
-  if (a.paged) {  // this sequence's chunk count, as the attention kernel derives it
-    const int n = a.seq_lens[b];
-    const int pos = a.pos_arr ? a.pos_arr[b] : n - 1;
-    int t0 = (a.window > 0 && pos - a.window + 1 > 0) ? pos - a.window + 1 : 0;
-    if (t0 > n) t0 = n;
-    const int span = (a.fold ? n - 1 : n) - t0;
-    nch = span > 0 ? (span + a.chunk - 1) / a.chunk : (a.fold ? 1 : 0);
-    if (nch > a.nchunks) nch = a.nchunks;
-  }
+  // this sequence's chunk count, as the attention kernel derives it
+  const int nch = a.paged || a.pf ? comb_chunks(a, b) : a.nchunks;
   if (nch <= 1) return;  // uniform over the workgroup
   const bool live = lane < nch;
   const float M = wave_reduce<true>(live ? mc : -INFINITY);
@@ -3136,6 +3303,13 @@ __global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs
 __global__ void vexp_kernel(const float* x, float* y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = softmax_exp(x[i]);
+}
+
+// The probabilities' exponential as the kernels take it: the natural-units
+// argument scaled to base 2 (one fp32 rounding), then v_exp_f32.
+__global__ void prob_exp_kernel(const float* x, float* y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = exp2_hw(x[i] * kLog2e);
 }
 
 __global__ void zero_kernel(float* p, int64_t n) {
@@ -3199,7 +3373,7 @@ struct WsKey {
   }
 };
 // Per-(device, stream) workspace of the split-K partials, grown on demand.
-// Layout: [int ctr[kMaxSlots] | partials].  The arrival counters of the
+// Layout: [u64 ctr[kMaxSlots] | partials].  The arrival words of the
 // in-launch merge are zeroed once, when the buffer is allocated (a fill
 // kernel on the stream, ordered before any launch that uses them), and
 // every launch leaves them at zero.  The partials are filled and read
@@ -3207,7 +3381,7 @@ struct WsKey {
 // next on the same stream), so they need no clearing and hold nothing
 // between steps.  An outgrown buffer is retired, never freed: a graph
 // captured earlier on the stream still points at it (workspaces are small).
-constexpr size_t kCtrBytes = sizeof(int) * (size_t)kMaxSlots;
+constexpr size_t kCtrBytes = sizeof(unsigned long long) * (size_t)kMaxSlots;
 struct WsBuf {
   void* ptr = nullptr;
   size_t bytes = 0;  // partials
@@ -3219,7 +3393,7 @@ std::vector<void*> g_retired;
 __global__ void zero_kernel(float* p, int64_t n);
 bool xcd_map_ok(int dev);
 
-int workspace(void* stream, size_t bytes, int** ctr, void** out) {
+int workspace(void* stream, size_t bytes, unsigned long long** ctr, void** out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return (int)e;
@@ -3239,8 +3413,8 @@ int workspace(void* stream, size_t bytes, int** ctr, void** out) {
     void* p = nullptr;
     e = hipMalloc(&p, kCtrBytes + want);
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)(kMaxSlots / 256)), dim3(256), 0,
-                       (hipStream_t)stream, reinterpret_cast<float*>(p), (int64_t)kMaxSlots);
+    hipLaunchKernelGGL(zero_kernel, dim3((unsigned)(kCtrBytes / 4 / 256)), dim3(256), 0,
+                       (hipStream_t)stream, reinterpret_cast<float*>(p), (int64_t)(kCtrBytes / 4));
     e = hipGetLastError();
     if (e != hipSuccess) {
       (void)hipFree(p);
@@ -3249,7 +3423,7 @@ int workspace(void* stream, size_t bytes, int** ctr, void** out) {
     w.ptr = p;
     w.bytes = want;
   }
-  *ctr = reinterpret_cast<int*>(w.ptr);
+  *ctr = reinterpret_cast<unsigned long long*>(w.ptr);
   *out = reinterpret_cast<char*>(w.ptr) + kCtrBytes;
   return 0;
 }
@@ -3259,6 +3433,7 @@ int workspace(void* stream, size_t bytes, int** ctr, void** out) {
 // captured graph may still point at, total less than the live one).  Under
 // stream capture it cannot grow: the caller then splits per tile instead.
 std::map<WsKey, WsBuf> g_pieces_ws;
+constexpr size_t kMaxPiecesBytes = (size_t)1 << 30;  // the prefill's pre-split workspace
 
 int pieces_workspace(void* stream, size_t bytes, void** out) {
   int dev = 0;
@@ -3271,7 +3446,9 @@ int pieces_workspace(void* stream, size_t bytes, void** out) {
     e = hipStreamIsCapturing((hipStream_t)stream, &cap);
     if (e != hipSuccess) return (int)e;
     if (cap != hipStreamCaptureStatusNone) return MOLOT_ENOWS;
-    const size_t want = std::max(bytes, 2 * w.bytes);
+    // at most kMaxPiecesBytes (bytes never exceeds it), so the live buffer
+    // and the retired ones a captured graph may still hold stay under 2 GiB
+    const size_t want = std::min(std::max(bytes, 2 * w.bytes), std::max(bytes, kMaxPiecesBytes));
     void* p = nullptr;
     e = hipMalloc(&p, want);
     if (e != hipSuccess) return (int)e;
@@ -3438,7 +3615,6 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   a.part_o = nullptr;
   a.part_ml = nullptr;
   a.qrot = nullptr;
-  a.part_x = nullptr;
   a.ctr = nullptr;
   a.xmap = 0;
   a.slots = rows;
@@ -3449,10 +3625,9 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   const size_t po = (size_t)rows * a.nchunks * P;
   const size_t pml = (size_t)rows * a.nchunks * gh * 2;
   const size_t qr = (size_t)rows * P;
-  const size_t px = (size_t)rows * a.nchunks;  // ints
   void* ws = nullptr;
-  int* ctr = nullptr;
-  const size_t need = sizeof(float) * (po + pml + qr + px);
+  unsigned long long* ctr = nullptr;
+  const size_t need = sizeof(float) * (po + pml + qr);
   if (a.ext_ws) {
     // a caller-provided workspace (molot_hip_decode_step_noalloc): no
     // allocation, and the combine kernel merges (no counters to keep)
@@ -3460,7 +3635,6 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
     a.part_o = reinterpret_cast<float*>(a.ext_ws);
     a.part_ml = a.part_o + po;
     a.qrot = a.part_ml + pml;
-    a.part_x = reinterpret_cast<int*>(a.qrot + qr);
     return 0;
   }
   const int st = workspace(stream, need, &ctr, &ws);
@@ -3468,7 +3642,6 @@ int plan_launch(AttnArgs& a, int d, int span, int gh, int nsubs, int B, int alig
   a.part_o = reinterpret_cast<float*>(ws);
   a.part_ml = a.part_o + po;
   a.qrot = a.part_ml + pml;
-  a.part_x = reinterpret_cast<int*>(a.qrot + qr);
   int dev = 0;
   // automatic: in the launch when the slots fill the 8 XCDs evenly on a
   // contiguous cache and the context is long (measured, 32q/8kv/d128 fp32:
@@ -3572,6 +3745,9 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   cb.rope = rope ? 1 : 0;
   cb.paged = paged ? 1 : 0;
   cb.fold = rope && a.fold ? 1 : 0;
+  cb.pf = rope ? 0 : a.pf;
+  cb.pos0 = a.pos;
+  cb.n = a.n;
   // At most 8 chunks (batches of sequences: many slots, few chunks): one
   // wave per 64 pairs (combine_wave_kernel<R>, R = 4 or 8 o loads per lane).
   // More chunks: combine_kernel, whose 4 phases per pair keep the loads per
@@ -3615,9 +3791,13 @@ int launch_cfg(AttnArgs a, int span, int nsubs, int B, void* stream) {
   // Q8 (d = 256): the heads of a token share 128-byte lines (see launch_pair)
   a.chunk_fast = sizeof(T) == 1;
   a.nseq = B;
-  // contiguous caches: 32-row groups dealt round robin (the kernel's gmap)
-  int st = plan_launch(a, D, span, GH, nsubs, B, PAGED ? C::RB : 32, 1, stream, !PAGED);
+  // contiguous caches: 32-row groups dealt round robin (the kernel's gmap);
+  // prefill rows, like paged batches, tile each row's range in contiguous
+  // chunks and merge them in the combine kernel
+  const bool perseq = PAGED || (!ROPE && a.pf);
+  int st = plan_launch(a, D, span, GH, nsubs, B, perseq ? C::RB : 32, 1, stream, !perseq);
   if (st) return st;
+  if (a.pf) no_merge(a);
   if constexpr (sizeof(T) == 1 && C::NW > 8) {
     // Q8 chunks of at most 4 blocks a wave on 8 waves: a 1024-token window
     // of 8q/4kv/d256 (32-row chunks) 14.45 -> 10.9 us per step; 512-row
@@ -3659,20 +3839,26 @@ int launch_attn(const AttnArgs& a, int span, int nsubs, int B, void* stream) {
                                                                            stream);
 }
 
+// Query heads per workgroup: up to 8 (d <= 256) or 4 (d = 512, whose
+// 8-head workgroup would need 99 KB of LDS for its waves' partial o; 8 q
+// heads of a KV head then run as two subgroups reading the rows twice).
+constexpr int kMaxGhWide = 4;
 template <int D, typename T, bool PAGED, bool ROPE, bool PAD>
 int dispatch_gh(int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
   switch (gh) {
     case 1: return launch_attn<D, 1, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
     case 2: return launch_attn<D, 2, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
     case 4: return launch_attn<D, 4, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
-    case 8: return launch_attn<D, 8, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
+    case 8:
+      if constexpr (D <= 256) return launch_attn<D, 8, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
+      break;
   }
   return MOLOT_EINVAL;
 }
 
-// The vector-ALU kernels are built for D = 64, 128 and 256; any other even
-// head dim d <= 256 runs padded in the next of them (q zero-padded to D,
-// K/V rows read at their stored length d).
+// The vector-ALU kernels are built for D = 64, 128, 256 and 512; any other
+// even head dim d <= 512 runs padded in the next of them (q zero-padded to
+// D, K/V rows read at their stored length d).
 template <int D, typename T, bool PAGED, bool ROPE>
 int dispatch_pad(int d, int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
   return d == D ? dispatch_gh<D, T, PAGED, ROPE, false>(gh, a, span, nsubs, B, st)
@@ -3683,22 +3869,25 @@ template <typename T, bool PAGED, bool ROPE>
 int dispatch_d(int d, int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
   if (d <= 64) return dispatch_pad<64, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
   if (d <= 128) return dispatch_pad<128, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
-  return dispatch_pad<256, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  if (d <= 256) return dispatch_pad<256, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  return dispatch_pad<512, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
 }
 
 template <bool PAGED, bool ROPE>
 int dispatch_attn(int d, int kv_dtype, int gh, const AttnArgs& a, int span, int nsubs, int B,
                   void* st) {
   if (kv_dtype == MOLOT_KV_F32) return dispatch_d<float, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
-  if (kv_dtype == MOLOT_KV_Q8)  // D = 256 (check_common; 64 and 128 take the matrix cores)
-    return dispatch_gh<256, q8_t, PAGED, ROPE, false>(gh, a, span, nsubs, B, st);
+  if (kv_dtype == MOLOT_KV_Q8)  // D = 256, 512 (check_common; 64 and 128 take the matrix cores)
+    return d == 512 ? dispatch_gh<512, q8_t, PAGED, ROPE, false>(gh, a, span, nsubs, B, st)
+                    : dispatch_gh<256, q8_t, PAGED, ROPE, false>(gh, a, span, nsubs, B, st);
   return dispatch_d<bf16_t, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
 }
 
-// Head dims the kernels are built for (the prefill and the Q8 matrix-core
-// kernels); decode on fp32 and bf16 caches takes any even d up to 256.
+// Head dims the prefill's matrix-core kernel is built for; decode on fp32
+// and bf16 caches takes any even d up to 512, Q8 caches q8_d.
 bool supported_d(int d) { return d == 64 || d == 128 || d == 256; }
-bool decode_d(int d) { return d >= 2 && d <= 256 && d % 2 == 0; }
+bool decode_d(int d) { return d >= 2 && d <= 512 && d % 2 == 0; }
+bool q8_d(int d) { return d == 64 || d == 128 || d == 256 || d == 512; }
 
 bool valid_kv(int kv_dtype) {
   return kv_dtype == MOLOT_KV_F32 || kv_dtype == MOLOT_KV_BF16 || kv_dtype == MOLOT_KV_Q8;
@@ -3716,7 +3905,7 @@ int check_common(int nq, int nkv, int d, int kv_dtype) {
   if (nq <= 0 || nkv <= 0 || nq % nkv != 0) return MOLOT_EINVAL;
   if (!valid_kv(kv_dtype)) return MOLOT_EINVAL;
   if (!decode_d(d)) return MOLOT_ENOTSUP;
-  if (kv_dtype == MOLOT_KV_Q8 && !supported_d(d)) return MOLOT_ENOTSUP;  // Q8: 64, 128, 256
+  if (kv_dtype == MOLOT_KV_Q8 && !q8_d(d)) return MOLOT_ENOTSUP;  // Q8: 64, 128, 256, 512
   return 0;
 }
 
@@ -3773,9 +3962,10 @@ int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
   a.dh = d;
   const int G = a.nq / a.nkv;
   const bool q8 = kv_dtype == MOLOT_KV_Q8;
-  if ((q8 && d != 256) || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128))) {
+  if ((q8 && d <= 128) || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128))) {
     // up to 16 q heads of a group share each K/V tile on the MFMA columns;
-    // Q8 caches of D = 64, 128 run here, D = 256 on the vector-ALU kernel
+    // Q8 caches of D = 64, 128 run here, D = 256 and 512 on the vector-ALU
+    // kernel
     const int gh = G % 16 == 0 ? 16 : pick_gh(G);
     const int nsubs = G / gh;
     if (q8)
@@ -3784,7 +3974,7 @@ int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
     return d == 64 ? dispatch_mfma<64, PAGED, ROPE, false>(gh, a, span, nsubs, B, stream)
                    : dispatch_mfma<128, PAGED, ROPE, false>(gh, a, span, nsubs, B, stream);
   }
-  const int gh = pick_gh(G);
+  const int gh = d > 256 ? std::min(pick_gh(G), kMaxGhWide) : pick_gh(G);
   const int nsubs = G / gh;
   return dispatch_attn<PAGED, ROPE>(d, kv_dtype, gh, a, span, nsubs, B, stream);
 }
@@ -3800,9 +3990,6 @@ struct Norms {
 bool norms_ok(const Norms& nm) { return nm.eps >= 0.f && nm.eps < INFINITY; }
 
 using PfFn = void (*)(PfArgs);
-constexpr size_t kMaxPiecesBytes = (size_t)1 << 30;  // the prefill's pre-split workspace
-// ... and its cap where no per-tile kernel stands behind it (Q8 at d = 256)
-constexpr size_t kMaxPiecesOnlyBytes = (size_t)8 << 30;
 std::atomic<int> g_presplit{1};  // molot_hip_set_prefill_presplit
 
 template <int D, typename T, bool PAGED>
@@ -3863,8 +4050,8 @@ const char* molot_hip_strerror(int status) {
     case MOLOT_OK: return "ok";
     case MOLOT_EINVAL: return "molot_amd: invalid argument";
     case MOLOT_ENOTSUP:
-      return "molot_amd: unsupported shape (decode: an even head dim up to 256, Q8 caches 64, "
-             "128 or 256; prefill: 64, 128 or 256, Q8 caches 64 or 128)";
+      return "molot_amd: unsupported shape (an even head dim up to 512; Q8 caches 64, 128, 256 "
+             "or 512)";
     case MOLOT_ENOSPC: return "molot_amd: KV cache full";
     case MOLOT_ENOWS:
       return "molot_amd: workspace not sized for this shape on a capturing stream (launch the "
@@ -4337,7 +4524,9 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
 // grow under capture.  Returns the pieces buffer (NULL: the attention kernel
 // splits each staged tile itself) and sets T0 and R.
 // only: the launch has no per-tile kernel (a Q8 cache at d = 256): the
-// pieces are made whatever the presplit switch says, up to kMaxPiecesOnlyBytes.
+// pieces are made whatever the presplit switch says (within the same cap;
+// past it, or under a capture that would grow them, such a prefill runs as
+// prefill rows).
 static int prefill_pieces(int nkv, int N, int d, int pos0, int window, int kv_dtype, void* stream,
                           void** ws, int* T0, int64_t* R, bool only = false) {
   *ws = nullptr;
@@ -4345,12 +4534,51 @@ static int prefill_pieces(int nkv, int N, int d, int pos0, int window, int kv_dt
   *R = (int64_t)N - *T0;
   if (!only && (kv_dtype == MOLOT_KV_BF16 || !g_presplit.load(std::memory_order_relaxed))) return 0;
   const size_t need = (size_t)2 * nkv * 3 * *R * d * sizeof(uint16_t);
-  const size_t cap = only ? kMaxPiecesOnlyBytes : kMaxPiecesBytes;
   void* p = nullptr;
-  const int st = *R > 0 && need <= cap ? pieces_workspace(stream, need, &p) : MOLOT_ENOWS;
+  const int st =
+      *R > 0 && need <= kMaxPiecesBytes ? pieces_workspace(stream, need, &p) : MOLOT_ENOWS;
   if (st && st != MOLOT_ENOWS) return st;
   if (!st) *ws = p;
   return 0;
+}
+
+// The prefill at a head dim the matrix-core prefill cannot tile (d = 512:
+// its three q pieces alone would take 192 registers a lane and a 32-key tile
+// of K and V pieces 192 KB of LDS; an even d that is not a multiple of 8):
+// the vector-ALU decode kernel with each query row as a sequence of its own
+// (AttnArgs::pf) over the one cache, contiguous or through the prompt's
+// block-table row.  Each query row streams its attended rows; neighbouring
+// rows of a prompt read the same keys, which the L2 and the Infinity Cache
+// serve after the first.
+static int prefill_rows(const float* Qm, const void* K, const void* V, float* Om, int nq,
+                        int nkv, int M, int N, int d, float scale, int pos0, int window,
+                        int kv_dtype, const int32_t* block_row, int page, void* stream) {
+  if ((int64_t)M > 65535) return MOLOT_ENOTSUP;  // grid rows: one per query
+  AttnArgs a{};
+  a.q = Qm;
+  a.k = const_cast<void*>(K);
+  a.v = const_cast<void*>(V);
+  a.o = Om;
+  if (block_row) {
+    if (page <= 0 || (page & (page - 1)) || !q8_pages_ok(nkv, page, kv_dtype)) return MOLOT_EINVAL;
+    paged_layout(a, nkv, d, page, kv_dtype);
+    a.block_table = block_row;
+    a.max_blocks = 0;  // every row reads the one block-table row
+    while ((1 << a.page_shift) < page) ++a.page_shift;
+  } else {
+    token_major(a, nkv, d, kv_dtype);
+  }
+  a.nq = nq;
+  a.nkv = nkv;
+  a.n = N;
+  a.pos = pos0;
+  a.window = window;
+  a.scale = scale;
+  a.pf = 1;
+  // the widest attended range of any query row
+  const int span = window > 0 && window < N ? window : N;
+  return block_row ? run_attn<true, false>(a, d, kv_dtype, span, M, stream)
+                   : run_attn<false, false>(a, d, kv_dtype, span, M, stream);
 }
 
 // split_rows: rows of [T0, N) pf_split_kernel still has to split (the
@@ -4366,9 +4594,12 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   // D: the split kernel and the per-tile loads read each row at its stored
   // length d and fill the columns past it with 0, q is read and O written
   // at d.  A Q8 cache at d = 256 runs only through the pieces (the kernel
-  // that splits staged Q8 tiles itself is built for 64 and 128).
+  // that splits staged Q8 tiles itself is built for 64 and 128).  Head dims
+  // above 256 and even ones that are not multiples of 8 run as prefill rows
+  // (prefill_rows).
+  const bool rows_path = d > 256 || d % 8 != 0;
   const bool padded = !supported_d(d);
-  if (padded && (d % 8 || d > 256 || kv_dtype == MOLOT_KV_Q8)) return MOLOT_ENOTSUP;
+  if (padded && !rows_path && kv_dtype == MOLOT_KV_Q8) return MOLOT_ENOTSUP;
   const bool pieces_only = kv_dtype == MOLOT_KV_Q8 && d == 256;
   const int D = padded ? (d <= 64 ? 64 : d <= 128 ? 128 : 256) : d;
   if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
@@ -4376,6 +4607,9 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   if (N == 0) return zero_out(Om, (int64_t)M * nq * d, (hipStream_t)stream);
   if (!K || !V || !aligned16(K) || !aligned16(V) || !aligned16(Qm) || !aligned16(Om))
     return MOLOT_EINVAL;
+  if (rows_path)
+    return prefill_rows(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window, kv_dtype, block_row,
+                        page, stream);
   const int64_t rows = (int64_t)M * (nq / nkv);
   const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1;
   auto nqb_of = [&](int w) { return (rows + 16 * w - 1) / (16 * w); };
@@ -4394,7 +4628,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     const int64_t want = (num_cus() + nqb * nkv - 1) / (nqb * nkv);
     nsplit = (int)std::max<int64_t>(1, std::min<int64_t>({16, want, tiles / 4}));
     if (nsplit > 1) {
-      int* ctr = nullptr;
+      unsigned long long* ctr = nullptr;
       void* ws = nullptr;
       st = workspace(stream, sizeof(float) * (size_t)M * nq * nsplit * (D + 2), &ctr, &ws);
       if (st && st != MOLOT_ENOWS) return st;
@@ -4447,7 +4681,10 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     if (st) return st;
     if (!ws && pieces_only) {
       if (R == 0) return zero_out(Om, (int64_t)M * nq * d, (hipStream_t)stream);  // no key attended
-      return MOLOT_ENOTSUP;  // a capture that would have to grow them, or past the cap
+      // a capture that would have to grow them, or past the cap: the vector-
+      // ALU kernel reads the Q8 rows itself
+      return prefill_rows(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window, kv_dtype,
+                          block_row, page, stream);
     }
     if (ws) {
       a.pieces = reinterpret_cast<const uint16_t*>(ws);
@@ -4516,8 +4753,9 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
                              const int32_t* block_row, int page, int max_blocks, void* stream) {
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
-  // the prefill kernels' head dims, or a multiple of 8 below 256 run padded
-  if (!supported_d(d) && (d % 8 || d > 256 || kv_dtype == MOLOT_KV_Q8)) return MOLOT_ENOTSUP;
+  // the prefill kernels' head dims, a multiple of 8 below 256 run padded, or
+  // prefill rows (d > 256, or not a multiple of 8; see attn_prefill_impl)
+  if (!supported_d(d) && d % 8 == 0 && d < 256 && kv_dtype == MOLOT_KV_Q8) return MOLOT_ENOTSUP;
   const bool pieces_only = kv_dtype == MOLOT_KV_Q8 && d == 256;  // no per-tile kernel
   Norms nm;
   nm.q = q_norm;
@@ -4570,8 +4808,6 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
     st = prefill_pieces(nkv, slot0 + M, d, pos0, window, kv_dtype, stream, &pws, &T0, &R,
                         pieces_only);
     if (st) return st;
-    // nothing appended when the attention could not run
-    if (!pws && pieces_only && R > 0) return MOLOT_ENOTSUP;
     if (pws) {
       r.pieces = reinterpret_cast<uint16_t*>(pws);
       r.pc_T0 = T0;
@@ -4708,6 +4944,15 @@ int molot_hip_vexp(const float* x, float* y, int64_t n, void* stream) {
   const int64_t blocks = (n + 255) / 256;
   hipLaunchKernelGGL(vexp_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x,
                      y, n);
+  return (int)hipGetLastError();
+}
+
+int molot_hip_prob_exp(const float* x, float* y, int64_t n, void* stream) {
+  if (n < 0 || (n > 0 && (!x || !y))) return MOLOT_EINVAL;
+  if (n == 0) return 0;
+  const int64_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(prob_exp_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     x, y, n);
   return (int)hipGetLastError();
 }
 

@@ -1,4 +1,5 @@
-"""ctypes binding of libmolot_amd.so (the C ABI in include/molot_amd/attn_hip.h).
+"""ctypes binding of libmolot_amd.so (the C ABI in include/molot_amd/attn_hip.h),
+and of the bench-only libmolot_probe.so (include/molot_amd/probe.h).
 
 The library is built in-tree by ``__graft_entry__.build()`` (or
 ``python -m molot_amd.build``).  There is no fallback: if the library is
@@ -12,6 +13,8 @@ import threading
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmolot_amd.so")
+# measurement probes, kept out of the drop-in library (bench.py only)
+PROBE_LIB_PATH = os.path.join(_HERE, "libmolot_probe.so")
 
 KV_F32 = 0
 KV_BF16 = 1
@@ -26,6 +29,7 @@ E2BIG = -7
 
 _lock = threading.Lock()
 _lib = None
+_probe = None
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -56,6 +60,7 @@ _SIGS = {
     "molot_hip_rope_append_paged": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P,
                                     _I, _P],
     "molot_hip_vexp": [_P, _P, _I64, _P],
+    "molot_hip_prob_exp": [_P, _P, _I64, _P],
     "molot_hip_attn_prefill_gqa": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _I, _I, _I, _P],
     "molot_hip_prefill_step": [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _F, _P,
                                _F, _I, _I, _P],
@@ -73,7 +78,9 @@ _SIGS = {
     "molot_hip_profile_begin": [_I],
     "molot_hip_profile_end": [ctypes.POINTER(_F), ctypes.POINTER(_F), ctypes.POINTER(_I),
                               ctypes.POINTER(_I)],
-    # include/molot_amd/probe.h
+}
+# include/molot_amd/probe.h (libmolot_probe.so)
+_PROBE_SIGS = {
     "molot_probe_read": [_P, _I64, _P, _I64, _P],
     "molot_probe_copy": [_P, _P, _I64, _P],
 }
@@ -94,8 +101,10 @@ _I64RET = {
     "molot_hip_q8_block_bytes": [_I, _I, _I],
 }
 
-# Every function include/molot_amd/*.h declares.
+# Every function include/molot_amd/attn_hip.h declares (libmolot_amd.so), and
+# every function include/molot_amd/probe.h declares (libmolot_probe.so).
 EXPORTS = sorted(list(_SIGS) + list(_VOID) + list(_STR) + list(_I64RET))
+PROBE_EXPORTS = sorted(_PROBE_SIGS)
 
 
 def load() -> ctypes.CDLL:
@@ -126,6 +135,23 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
             fn.restype = ctypes.c_int64
         _lib = lib
+        return lib
+
+
+def load_probe() -> ctypes.CDLL:
+    """Load the bench-only probe library (streaming read / copy kernels)."""
+    global _probe
+    with _lock:
+        if _probe is not None:
+            return _probe
+        if not os.path.exists(PROBE_LIB_PATH):
+            raise RuntimeError(f"molot_amd: probe library not built ({PROBE_LIB_PATH})")
+        lib = ctypes.CDLL(PROBE_LIB_PATH)
+        for name, args in _PROBE_SIGS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        _probe = lib
         return lib
 
 

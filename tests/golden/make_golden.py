@@ -404,6 +404,19 @@ def main() -> None:
         if want("gqa_win_headmajor_d64"):
             gen_gqa_headmajor("gqa_win_headmajor_d64", nq=4, nkv=2, n=90, d=64, pos_cur=89,
                               window=20, seed=15, pool=pool)
+        # head dim 512: the global layers of the reference's gemma4 models
+        # (model.h:562-564), attention scale 1 (model.h:39, forward.h:170-173)
+        if want("decode_step_norm_g4_d512_scale1"):
+            gen_decode_step_norm("decode_step_norm_g4_d512_scale1", nq=8, nkv=2, d=512, n0=24,
+                                 base=1000000.0, window=0, scale=1.0, eps=1e-6, v_norm=1,
+                                 seed=31, pool=pool)
+        if want("prefill_norm_d512"):
+            gen_prefill("prefill_norm_d512", nq=4, nkv=1, d=512, M=6, n0=10, base=1000000.0,
+                        window=0, scale=1.0, eps=1e-6, norms=True, seed=32, pool=pool)
+        if want("decode_step_shared_d512"):
+            gen_decode_step_shared("decode_step_shared_d512", nq=4, nkv=1, d=512, n=30, pos=29,
+                                   base=1000000.0, window=0, scale=1.0, eps=1e-6, rope=True,
+                                   seed=33, pool=pool)
         if want("bf16_cache_g8_d128"):
             gen_bf16_cache("bf16_cache_g8_d128", nq=8, nkv=1, n=70, d=128, sigma=1.0, seed=16,
                            pool=pool)
@@ -411,6 +424,10 @@ def main() -> None:
         gen_rope("rope_d128_theta5e5", 128, 500000.0, [0, 1, 7, 4096, 16384, 131072], seed=17)
     if want("rope_d256_theta1e4"):
         gen_rope("rope_d256_theta1e4", 256, 10000.0, [0, 3, 1023, 32768], seed=18)
+    if want("rope_d512_theta1e6"):
+        gen_rope("rope_d512_theta1e6", 512, 1000000.0, [0, 5, 4096, 131072], seed=34)
+    if want("q8_rows_d512"):
+        gen_q8_rows("q8_rows_d512", 512, seed=35)
     if want("vexp_points"):
         gen_vexp("vexp_points", seed=19)
     if want("q8_rows_d128"):

@@ -1,7 +1,9 @@
 """The C ABI boundary, checked on the CPU (no compute call needs a GPU here).
 
 - libmolot_amd.so loads and exports every function include/molot_amd/attn_hip.h
-  declares (and the Python binding knows each one);
+  declares (and the Python binding knows each one), and nothing else of this
+  library's namespace: the measurement probes (include/molot_amd/probe.h)
+  live in the bench-only libmolot_probe.so;
 - host-only functions (status strings, version, the RoPE table) work;
 - argument validation rejects bad shapes with status codes before anything
   touches the device.
@@ -19,28 +21,39 @@ import oracle
 from molot_amd import lib as L
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "molot_amd", "*.h")))
+INC = os.path.join(ROOT, "include", "molot_amd")
+HEADERS = sorted(glob.glob(os.path.join(INC, "*.h")))
+ABI_HEADER = os.path.join(INC, "attn_hip.h")
+PROBE_HEADER = os.path.join(INC, "probe.h")
 
 
-def declared_functions():
+def declared_functions(headers=(ABI_HEADER,)):
     names = set()
-    for h in HEADERS:
+    for h in headers:
         text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
         names.update(re.findall(r"\b(molot_\w+)\s*\(", text))
     return sorted(names)
 
 
+def exported(path):
+    out = subprocess.run(["nm", "-D", "--defined-only", path], check=True,
+                         capture_output=True, text=True).stdout
+    return set(re.findall(r" T (\w+)", out))
+
+
 def test_header_declarations_match_binding():
+    assert set(HEADERS) == {ABI_HEADER, PROBE_HEADER}, HEADERS
     decl = declared_functions()
     assert decl == sorted(L.EXPORTS), set(decl) ^ set(L.EXPORTS)
+    probes = declared_functions((PROBE_HEADER,))
+    assert probes == L.PROBE_EXPORTS, set(probes) ^ set(L.PROBE_EXPORTS)
 
 
 def test_library_exports_every_declared_symbol():
-    out = subprocess.run(["nm", "-D", "--defined-only", L.LIB_PATH], check=True,
-                         capture_output=True, text=True).stdout
-    exported = set(re.findall(r" T (\w+)", out))
-    missing = [f for f in declared_functions() if f not in exported]
-    assert not missing, missing
+    ours = {f for f in exported(L.LIB_PATH) if f.startswith("molot_")}
+    assert ours == set(declared_functions()), ours ^ set(declared_functions())
+    probes = {f for f in exported(L.PROBE_LIB_PATH) if f.startswith("molot_")}
+    assert probes == set(L.PROBE_EXPORTS), probes
 
 
 def test_library_loads_and_binds():
@@ -80,12 +93,12 @@ def test_validation_before_launch():
     # unknown kv dtype
     assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, 128, 0.1, 9, 0,
                                                7, s) == L.EINVAL
-    # head dims without kernels: decode takes any even d up to 256
-    for d in (97, 258, 0):
+    # head dims without kernels: decode and prefill take any even d up to 512
+    for d in (97, 514, 0, 1024):
         assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, d, 0.1, 9,
                                                    0, 0, s) == L.ENOTSUP
-    # prefill: 64, 128, 256, or a multiple of 8 below 256 run padded (not Q8)
-    for d, kvd in ((90, 0), (90, L.KV_BF16), (96, L.KV_Q8), (250, 0)):
+    # prefill: any even d up to 512 on fp32 and bf16 caches; Q8 64, 128, 256, 512
+    for d, kvd in ((514, 0), (514, L.KV_BF16), (96, L.KV_Q8), (90, L.KV_Q8), (7, 0)):
         assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, d, 0.1, 6, 0,
                                               kvd, s) == L.ENOTSUP
         assert lib.molot_hip_prefill_step(_p(), _p(), _p(), _p(), _p(), _p(), 8, 2, d, 4, 6, 6,
@@ -138,9 +151,10 @@ def test_q8_validation_before_launch():
     lib = L.load()
     s = ctypes.c_void_p(0)
     Q8 = L.KV_Q8
-    # Q8 caches: d = 64, 128, 256 for decode
-    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 192, 0.1, 9, 0,
-                                               Q8, s) == L.ENOTSUP
+    # Q8 caches: d = 64, 128, 256, 512 for decode
+    for d in (192, 384, 320):
+        assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, d, 0.1, 9,
+                                                   0, Q8, s) == L.ENOTSUP
     # element strides instead of the token-major Q8 byte layout
     assert lib.molot_hip_attn_decode_strided(_p(), _p(), _p(), _p(), 8, 2, 10, 128, 256, 128,
                                              0.1, 9, 0, Q8, s) == L.EINVAL
@@ -151,7 +165,7 @@ def test_q8_validation_before_launch():
     assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4, 4, 8,
                                            1, 64, 2, 0.1, 0, Q8, s) == L.EINVAL
     assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 192, 0.1, 6, 0,
-                                          Q8, s) == L.ENOTSUP  # Q8 prefill: 64, 128, 256
+                                          Q8, s) == L.ENOTSUP  # Q8 prefill: 64, 128, 256, 512
     # the RoPE/append entries write only rows the attention entries read back
     assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 2, 192, 5, 5, _p(), Q8,
                                      s) == L.ENOTSUP

@@ -134,6 +134,36 @@ def test_vexp_known_answers(gpu):
     np.testing.assert_allclose(yg[inside], np.exp(x[inside]), rtol=1e-5)
 
 
+def test_prob_exp_known_answers(gpu):
+    """The probabilities' exp (2^(x*log2 e), one v_exp_f32, as every decode
+    and prefill kernel takes it) at the bench/bench.cc:220-234 points and
+    the golden points (reference: norm.h:35-47's exp_avx512_ps), relerr
+    < 1e-5; and across |s - m| up to the range the kernels feed it: scores
+    sit at most 8 base-2 units above the running max (the lazy max), down to
+    where e^x leaves the normal floats."""
+    kat = np.array([-87., -20., -10., -5., -3., -2., -1.5, -1., -0.75, -0.5, -0.25, -0.1, -0.01,
+                    0., 1., 50.], np.float32)
+    y = host(attn.prob_exp(dev(kat)))
+    ref = np.exp(kat.astype(np.float64))
+    assert np.max(np.abs(y - ref) / ref) < 1e-5
+    g = golden("vexp_points")
+    yg = host(attn.prob_exp(dev(g["X"])))
+    x = g["X"].astype(np.float64)
+    inside = (x >= -87.3) & (x <= 88.0)  # both sides representable as normal floats
+    np.testing.assert_allclose(yg[inside], np.exp(x[inside]), rtol=1e-5)
+    # the kernels' own range, densely: x = s - m in [-87, 8 ln 2]
+    st = Stream(71)
+    u = (st.words(1 << 16) >> np.uint64(40)).astype(np.float64) / float(1 << 24)
+    xs = (-87.0 + (87.0 + 8 * math.log(2)) * u).astype(np.float32)
+    ys = host(attn.prob_exp(dev(xs))).astype(np.float64)
+    rel = np.abs(ys - np.exp(xs.astype(np.float64))) / np.exp(xs.astype(np.float64))
+    # the rounding of x*log2(e) bounds the error by ~|x| * 2^-24 (plus the
+    # instruction's own ~1 ulp): a planted natural-units exp2 (no log2 e)
+    # would miss by orders of magnitude
+    assert np.max(rel) < 1e-5
+    assert np.all(rel <= 2.0 ** -22 + np.abs(xs.astype(np.float64)) * 2.0 ** -23)
+
+
 def test_inv_freq_host_table(gpu):
     for base, d in ((500000.0, 128), (10000.0, 256)):
         got = attn.rope_inv_freq(base, d).numpy()

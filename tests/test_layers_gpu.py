@@ -225,6 +225,42 @@ def test_shared_paged_decode(gpu, bf16):
         assert normwise_err(Oh[b], O_ref) < FP32_TOL, b
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+def test_shared_paged_decode_empty_window(gpu, bf16):
+    """A shared-KV batch with positions given: sequences whose window starts
+    past their cache (pos - window + 1 >= n) attend nothing, so o = 0, yet
+    their q still leaves normed and rotated (forward.h:554-558 runs before
+    every attention call); the others equal the oracle's shared step."""
+    announce(f"shared paged decode, emptied windows, bf16={bf16}")
+    P = make_paged(9, 32, 8, 128, 50, 900, seed=85 + bf16, bf16=bf16)
+    B, nq, nkv, d, page, window = P["B"], 32, 8, 128, 16, 64
+    st = Stream(86)
+    qn = (1 + st.normal((d,), 0.2)).astype(np.float32)
+    inv = oracle.rope_inv_freq(500000.0, d)
+    # positions: some at the cache end, some far past it (window emptied)
+    pos = np.array([int(P["n"][b]) - 1 + (0 if b % 3 else 5000) for b in range(B)], np.int32)
+    K = dev_bf16(P["Kp"]) if bf16 else dev(P["Kp"])
+    V = dev_bf16(P["Vp"]) if bf16 else dev(P["Vp"])
+    q = dev(P["q"])
+    O = torch.full((B, nq, d), float("nan"), device="cuda")
+    attn.decode_step_paged_shared(q, K, V, O, dev(P["bt"].reshape(-1)), dev(P["n"]), dev(pos), B,
+                                  P["max_blocks"], nq, nkv, d, page, dev(inv), 0.088, window,
+                                  q_norm=dev(qn), eps=1e-6)
+    qh, Oh = host(q), host(O)
+    for b in range(B):
+        n = int(P["n"][b])
+        blk = P["bt"][b, :(n + page - 1) // page]
+        Kc = P["Kp"][blk].transpose(0, 2, 1, 3).reshape(-1, nkv * d)[:n]
+        Vc = P["Vp"][blk].transpose(0, 2, 1, 3).reshape(-1, nkv * d)[:n]
+        q_ref, O_ref = oracle.decode_step_shared(P["q"][b], Kc, Vc, nq, nkv, d, n, int(pos[b]), qn,
+                                                 1e-6, inv, 0.088, window)
+        np.testing.assert_allclose(qh[b], q_ref, rtol=2e-6, atol=4e-6, err_msg=f"seq {b}")
+        if b % 3 == 0:
+            assert np.all(Oh[b] == 0.0), b
+        else:
+            assert normwise_err(Oh[b], O_ref) < FP32_TOL, b
+
+
 def test_golden_prefill_shared(gpu):
     announce("golden prefill_shared_win_d128")
     g = golden("prefill_shared_win_d128")

@@ -107,7 +107,7 @@ def rope_adjacent_f64(x, pos, inv):
     return y
 
 
-@pytest.mark.parametrize("name", ["rope_d128_theta5e5", "rope_d256_theta1e4"])
+@pytest.mark.parametrize("name", ["rope_d128_theta5e5", "rope_d256_theta1e4", "rope_d512_theta1e6"])
 def test_rope_golden_and_closed_form(name):
     g = golden(name)
     inv = g["inv_freq"]
@@ -266,7 +266,8 @@ def _step_norm_from_golden(g):
     return q_rot, k_rot, O, Kc, Vc
 
 
-@pytest.mark.parametrize("name", ["decode_step_norm_g4_d128", "decode_step_norm_win_d256"])
+@pytest.mark.parametrize("name", ["decode_step_norm_g4_d128", "decode_step_norm_win_d256",
+                                  "decode_step_norm_g4_d512_scale1"])
 def test_decode_step_norm_golden(name):
     g = golden(name)
     pos = int(g["pos"])
@@ -327,7 +328,8 @@ def test_planted_rope_on_nope_layer_is_caught():
     assert normwise_err(O, g["O"]) > 1e-4
 
 
-@pytest.mark.parametrize("name", ["decode_step_shared_g4_d128", "decode_step_shared_nope_win_d256"])
+@pytest.mark.parametrize("name", ["decode_step_shared_g4_d128", "decode_step_shared_nope_win_d256",
+                                  "decode_step_shared_d512"])
 def test_decode_step_shared_golden(name):
     g = golden(name)
     nq, nkv, d, n, pos = (int(g[k]) for k in ("nq", "nkv", "d", "n", "pos"))
@@ -337,7 +339,10 @@ def test_decode_step_shared_golden(name):
                                          float(g["eps"]), inv, float(g["scale"]), int(g["window"]))
     np.testing.assert_allclose(q_out, g["q_out"], rtol=2e-6, atol=2e-6)
     np.testing.assert_array_equal(K, g["K"])  # nothing appended
-    assert normwise_err(O, g["O"]) < 2e-6
+    # d = 512 at scale 1 with a normed q and unnormed keys: scores ~ N(0, d),
+    # |s - max| up to ~60, where one fp32 ulp of a score moves its weight by
+    # ~4e-6 relative; the survey's 1e-5 bar applies there
+    assert normwise_err(O, g["O"]) < (2e-6 if d <= 256 else 1e-5)
 
 
 def test_shared_step_equals_owning_step():
@@ -408,7 +413,7 @@ def _prefill_f64(Q, K, V, nq, nkv, M, N, d, scale, pos0, window):
     return O
 
 
-@pytest.mark.parametrize("name", ["prefill_g4_d64", "prefill_norm_win_d128"])
+@pytest.mark.parametrize("name", ["prefill_g4_d64", "prefill_norm_win_d128", "prefill_norm_d512"])
 def test_prefill_golden(name):
     g = golden(name)
     nq, nkv, d, M, pos0 = (int(g[k]) for k in ("nq", "nkv", "d", "M", "pos0"))
@@ -432,7 +437,12 @@ def test_prefill_golden(name):
                                                       (6, 2, 256, 9, 200, 191, 0),
                                                       (8, 2, 64, 12, 30, 25, 0),
                                                       (8, 4, 96, 20, 120, 100, 33),
-                                                      (8, 2, 40, 12, 30, 25, 0)])
+                                                      (8, 2, 40, 12, 30, 25, 0),
+                                                      (4, 2, 512, 10, 60, 50, 0),
+                                                      (4, 1, 512, 7, 40, 33, 9),
+                                                      (6, 2, 36, 15, 40, 25, 0),
+                                                      (4, 2, 100, 9, 50, 41, 20),
+                                                      (4, 1, 250, 8, 30, 22, 0)])
 def test_prefill_vs_f64(nq, nkv, d, M, N, pos0, window):
     """Causal masking, windows, a cache longer than the prompt's positions
     (pos0 + M > N clips at N) and every GQA grouping, against float64."""
@@ -482,10 +492,11 @@ def test_planted_non_causal_prefill_is_caught():
 # ---------------------------------------------------------------------------
 # Q8 KV cache: quantize_q8_row (quant.h:34-50) per KV head row
 
-def test_q8_quantizer_golden():
+@pytest.mark.parametrize("name", ["q8_rows_d128", "q8_rows_d512"])
+def test_q8_quantizer_golden(name):
     """Bit-exact against the compiled reference on its edge cases (zero row,
     exact half-step ties, tiny values, the absmax element at +-127)."""
-    g = golden("q8_rows_d128")
+    g = golden(name)
     for i in range(g["X"].shape[0]):
         s, q = oracle.quantize_q8_row(g["X"][i])
         assert s == g["S"][i], i
@@ -623,7 +634,12 @@ def test_bf16_golden_attention():
 
 
 @pytest.mark.parametrize("nq,nkv,d,n,window", [(32, 8, 128, 4097, 0), (8, 4, 256, 3000, 1024),
-                                               (64, 8, 128, 2500, 0), (4, 4, 64, 333, 7)])
+                                               (64, 8, 128, 2500, 0), (4, 4, 64, 333, 7),
+                                               # head dims the GPU runs padded, and d = 512
+                                               (8, 2, 34, 900, 0), (16, 4, 80, 1200, 300),
+                                               (8, 4, 250, 700, 0), (8, 2, 512, 1500, 0),
+                                               (16, 2, 512, 800, 256), (4, 4, 300, 400, 0),
+                                               (8, 8, 2, 700, 0)])
 def test_restatement_vs_f64(nq, nkv, d, n, window):
     st = Stream(nq * 1000 + n)
     Q = st.normal((nq, d))
@@ -788,7 +804,12 @@ def test_ref_pool_coverage():
 @pytest.mark.parametrize("nq,nkv,d,n,window,pos_cur", [(32, 8, 128, 4097, 0, 4096),
                                                        (8, 4, 256, 2100, 1024, 2099),
                                                        (8, 8, 64, 17, 0, 16),
-                                                       (16, 2, 128, 1, 0, 0)])
+                                                       (16, 2, 128, 1, 0, 0),
+                                                       (8, 2, 34, 300, 0, 299),
+                                                       (16, 4, 80, 500, 100, 499),
+                                                       (8, 4, 250, 400, 0, 399),
+                                                       (8, 2, 512, 600, 0, 599),
+                                                       (16, 2, 512, 300, 128, 299)])
 def test_restatement_vs_reference(nq, nkv, d, n, window, pos_cur):
     st = Stream(n + d)
     Q = st.normal((nq, d))

@@ -512,6 +512,43 @@ def test_q8_prefill_d256_paged_matches_contiguous(gpu):
     assert normwise_err(host(Oc), R) < TOL
 
 
+def test_q8_d256_prefill_without_pieces_in_a_graph(gpu):
+    """A Q8 prefill at d = 256 reads its keys as bf16 pieces split once per
+    launch (its matrix-core kernel has no per-tile split).  Captured on a
+    stream whose pieces workspace is too small (it cannot grow under
+    capture), it runs on the vector-ALU kernel instead, each query row a
+    sequence of its own; every replay equals the oracle, and the eager
+    pieces path, to the 1e-5 bar."""
+    announce("q8 d256 prefill captured without its pieces")
+    nq, nkv, d, M, N, pos0 = 8, 4, 256, 40, 3040, 3000
+    st = Stream(66)
+    Q = st.normal((M, nq, d))
+    Kq, Vq = q8_caches(st, N, nkv, d)
+    Qd, Kd, Vd = dev(Q), dev_u8(Kq), dev_u8(Vq)
+    s = 1 / math.sqrt(d)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.attn_prefill_gqa(Qd, Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)  # pieces, eager
+    eager = host(O)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # sizes the side stream's workspaces for a shorter cache
+        attn.attn_prefill_gqa(Qd, Kd, Vd, O, nq, nkv, M, 1040, d, s, 1000, 0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        attn.attn_prefill_gqa(Qd, Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)
+    R = oracle.attn_prefill(Q, Kq, Vq, nq, nkv, M, N, d, s, pos0, 0)
+    for r in range(3):
+        O.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = host(O)
+        assert normwise_err(got, R) < TOL, f"replay {r}"
+        assert normwise_err(got, eager) < TOL, f"replay {r}"
+    assert normwise_err(eager, R) < TOL
+
+
 # ---------------------------------------------------------------------------
 # shapes the Q8 paths do not take: errors through the ABI, never a launch
 
@@ -520,7 +557,7 @@ def test_q8_errors(gpu):
     Q = dev(st.normal((8, 96)))
     O = torch.empty((8, 96), device="cuda")
     C = torch.zeros(10 * oracle.q8_row_bytes(2, 96), dtype=torch.uint8, device="cuda")
-    with pytest.raises(MolotHipError) as e:  # Q8 caches: d = 64, 128, 256 only
+    with pytest.raises(MolotHipError) as e:  # Q8 caches: d = 64, 128, 256, 512 only
         attn.attn_decode_gqa_cache(Q, C, C, O, 8, 2, 10, 96, 0.1, 9, 0)
     assert e.value.status == ENOTSUP
     Q = dev(st.normal((8, 64)))
