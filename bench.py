@@ -123,6 +123,9 @@ CONFIGS = {
     "c2q8": dict(nq=32, nkv=8, d=128, pos=16384, theta=500000.0, window=0, kvd=2, sigma=1.0),
     "c5q8": dict(nq=64, nkv=8, d=128, pos=131072, theta=500000.0, window=0, kvd=2, sigma=0.5),
     "c3q8": dict(nq=8, nkv=4, d=256, pos=32768, theta=10000.0, window=1024, kvd=2, sigma=1.0),
+    # a gemma4 global layer (model.h:562-564): head dim 512, 8q/2kv, 32k context
+    "c6": dict(nq=8, nkv=2, d=512, pos=32768, theta=1000000.0, window=0, kvd=0, sigma=1.0),
+    "c6q8": dict(nq=8, nkv=2, d=512, pos=32768, theta=1000000.0, window=0, kvd=2, sigma=1.0),
     "c4q8": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=2, sigma=1.0, batch=64,
                  lmin=512, lmax=8192, page=16),
     # prefill (gemm.h:409-446, forward.h:367-399): M prompt tokens after n0 cached
@@ -147,6 +150,8 @@ DESCR = {
     "c2q8": "fused RoPE+GQA decode layer-step, 32q/8kv/d128 Q8 KV, ctx 16384 (n=16385), batch 1",
     "c5q8": "long-context GQA decode layer-step, 64q/8kv/d128 Q8 KV, pos 131072 (n=131073)",
     "c3q8": "sliding-window GQA decode layer-step, 8q/4kv/d256 Q8 KV, pos 32768, window 1024",
+    "c6": "gemma4 global-layer decode step, 8q/2kv/d512 fp32 KV, ctx 32768 (n=32769), batch 1",
+    "c6q8": "gemma4 global-layer decode step, 8q/2kv/d512 Q8 KV, ctx 32768 (n=32769), batch 1",
     "c4q8": "continuous-batching decode step, 64 sequences of ctx U[512,8192], 32q/8kv/d128, "
             "Q8 KV in shuffled 16-token pages",
     "p1": "layer prefill (RoPE + append + causal attention), 2048-token prompt, 32q/8kv/d128 "
@@ -220,6 +225,7 @@ def kernel_label(d, nq, nkv, kvd, paged, nchunks, combined):
              f"q8={'true' if kvd == 2 else 'false'}>")
     else:
         gh = 8 if G % 8 == 0 else 4 if G % 4 == 0 else 2 if G % 2 == 0 else 1
+        gh = min(gh, 4) if d > 256 else gh  # at most 4 q heads a workgroup at d = 512
         t = {0: "float", 1: "bf16", 2: "q8"}[kvd]
         s = f"attn_kernel<{d},{gh},{t},paged={pg},rope=true>"
     if nchunks <= 1:

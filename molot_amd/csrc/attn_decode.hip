@@ -3121,12 +3121,15 @@ void prefill_mfma16_kernel(PfArgs a) {
 }
 
 // Log-sum-exp combine of the chunk partials of split-K launches.  Grid
-// (P/64, slots): a workgroup takes 64 output pairs of one head of a slot
-// (64 divides D) with 4 threads per pair, thread phase ph folding chunks
-// ph, ph+4, ...  The chunk weights e^(m_c - M) and the sum L are computed
-// once per workgroup into LDS; the first round of o loads is issued before
-// that, so a whole combine costs about one memory round trip.  Slots whose
-// sequence has a single chunk were written by the attention kernel itself.
+// (P/pairs, slots): a workgroup takes `pairs` output pairs of one head of a
+// slot (pairs divides D) with 256/pairs threads per pair, thread phase ph
+// folding chunks ph, ph + phases, ...  The chunk weights e^(m_c - M) and the
+// sum L are computed once per workgroup into LDS; the first round of o
+// loads is issued before that, so a whole combine costs about one memory
+// round trip when phases * kCombRound covers the chunks (comb_pairs picks
+// the pairs so: 64 pairs of 4 phases up to 32 chunks, 16 pairs of 16 phases
+// from 65).  Slots whose sequence has a single chunk were written by the
+// attention kernel itself.
 struct CombArgs {
   const float* part_o;
   const float* part_ml;
@@ -3139,6 +3142,7 @@ struct CombArgs {
   int fold;  // the attention launch folded in a new token (its chunks tile n - 1 rows)
   int dh;    // head dim as stored (d: the partials' padded head dim)
   int pf, pos0, n;  // prefill rows (AttnArgs::pf): row b at pos0 + b of a cache of n rows
+  int pairs;        // combine_kernel: output pairs per workgroup (16, 32 or 64)
 };
 
 // Chunks of sequence b of a per-sequence launch (a paged batch, or prefill
@@ -3160,9 +3164,17 @@ __device__ __forceinline__ int comb_chunks(const CombArgs& a, int b) {
 }
 
 constexpr int kCombThreads = 256;
-constexpr int kCombPairs = 64;                          // pairs per workgroup
-constexpr int kCombPhases = kCombThreads / kCombPairs;  // threads per pair
+constexpr int kCombPairs = 64;                          // most pairs per workgroup
 constexpr int kCombRound = 8;                           // o loads in flight per thread
+
+// Pairs per combine workgroup for nch chunks: the fewest phases (threads per
+// pair) whose one round of kCombRound loads each covers the chunks, at most
+// 16 (8q/2kv/d512, 128 chunks per KV head: 6.2 us on 64 pairs of 4 phases).
+__host__ __device__ constexpr int comb_pairs(int nch) {
+  int ph = 4;
+  while (ph < 16 && ph * kCombRound < nch) ph *= 2;
+  return kCombThreads / ph;
+}
 constexpr int kMaxChunks = 4096;
 
 // LDS of one combine workgroup, in floats: the chunk weights and sums of
@@ -3177,11 +3189,12 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
   float& s_l = pacc[kCombThreads];   // L = sum_c e^(m_c - M) l_c
   const int P = a.gh * a.d;
   const int slot = blockIdx.y;
-  const int pb = blockIdx.x * kCombPairs;
+  const int pairs = a.pairs, phases = kCombThreads / pairs;
+  const int pb = blockIdx.x * pairs;
   const int t = threadIdx.x;
   const int rows = a.nkv * a.nsub;  // slots per sequence
   const int b = slot / rows, y = slot - b * rows;
-  const int pl = t % kCombPairs, ph = t / kCombPairs;
+  const int pl = t % pairs, ph = t / pairs;
   const int pair = pb + pl;  // < P: P is a multiple of 64
   const int g = pb / a.d;    // one head per workgroup
   const float* po = a.part_o + (int64_t)slot * a.nchunks * P + pair;
@@ -3193,7 +3206,7 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
   float ov[kCombRound];
 #pragma unroll
   for (int u = 0; u < kCombRound; ++u)
-    ov[u] = po[(int64_t)min(ph + kCombPhases * u, a.nchunks - 1) * P];
+    ov[u] = po[(int64_t)min(ph + phases * u, a.nchunks - 1) * P];
   float m1 = -INFINITY, l1 = 0.f;
   if (t < 64) {
     const int c1 = min(t, a.nchunks - 1);
@@ -3226,16 +3239,16 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
   float acc = 0.f;
 #pragma unroll
   for (int u = 0; u < kCombRound; ++u) {
-    const int cc = ph + kCombPhases * u;
+    const int cc = ph + phases * u;
     if (cc < nch) acc = fmaf(wts[cc], ov[u], acc);
   }
-  for (int c0 = ph + kCombPhases * kCombRound; c0 < nch; c0 += kCombPhases * kCombRound) {
+  for (int c0 = ph + phases * kCombRound; c0 < nch; c0 += phases * kCombRound) {
 #pragma unroll
     for (int u = 0; u < kCombRound; ++u)
-      ov[u] = po[(int64_t)min(c0 + kCombPhases * u, nch - 1) * P];
+      ov[u] = po[(int64_t)min(c0 + phases * u, nch - 1) * P];
 #pragma unroll
     for (int u = 0; u < kCombRound; ++u) {
-      const int cc = c0 + kCombPhases * u;
+      const int cc = c0 + phases * u;
       if (cc < nch) acc = fmaf(wts[cc], ov[u], acc);
     }
   }
@@ -3243,8 +3256,7 @@ __global__ __launch_bounds__(kCombThreads) void combine_kernel(CombArgs a) {
   __syncthreads();
   if (ph == 0) {
     float o = acc;
-#pragma unroll
-    for (int q2 = 1; q2 < kCombPhases; ++q2) o += pacc[q2 * kCombPairs + pl];
+    for (int q2 = 1; q2 < phases; ++q2) o += pacc[q2 * pairs + pl];
     const int G = a.nq / a.nkv;
     const int h = y / a.nsub, sub = y - h * a.nsub;
     const int64_t oi = out_index((int64_t)b * a.nq + h * G + sub * a.gh, pair, a.d, a.dh);
@@ -3761,7 +3773,8 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
   const CombFn ck = a.nchunks <= 4 ? combine_wave_kernel<4>
                     : wave         ? combine_wave_kernel<8>
                                    : combine_kernel;
-  const dim3 cgrid = wave ? dim3(P / wthreads, slots) : dim3(P / kCombPairs, slots);
+  cb.pairs = comb_pairs(a.nchunks);
+  const dim3 cgrid = wave ? dim3(P / wthreads, slots) : dim3(P / cb.pairs, slots);
   const dim3 cblock = wave ? dim3(wthreads) : dim3(kCombThreads);
   const size_t clds = wave ? 0 : sizeof(float) * (size_t)comb_lds_floats(a.nchunks);  // <= 33 KB
   if (prof) {
@@ -4715,7 +4728,8 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   cb.dh = d;
   cb.nchunks = nsplit;
   cb.chunk = 1;
-  const dim3 cgrid((unsigned)(D / kCombPairs), (unsigned)((int64_t)M * nq));
+  cb.pairs = comb_pairs(nsplit);
+  const dim3 cgrid((unsigned)(D / cb.pairs), (unsigned)((int64_t)M * nq));
   const size_t clds = sizeof(float) * (size_t)comb_lds_floats(nsplit);
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {

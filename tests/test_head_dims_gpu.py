@@ -93,8 +93,14 @@ def test_decode_step_head_dims(gpu, shape):
     check_rows(p, Kh, Vh, oK, oV)
     assert np.isfinite(O).all()
     err = normwise_err(O, oO)
-    print(f"d={d}: normwise err {err:.3e}", flush=True)
+    # the oracle beside the float64 brute force on the GPU's own cache and q
+    Kw, Vw = (bf16_to_f32(Kh), bf16_to_f32(Vh)) if p.kv_dtype else (Kh, Vh)
+    R64 = oracle.attn_decode_f64(q, Kw, Vw, nq, nkv, pos + 1, d, p.scale, pos, window, nkv * d, d)
+    e64 = normwise_err(oO, R64)
+    print(f"d={d}: normwise err {err:.3e} (oracle vs f64 {e64:.3e})", flush=True)
     assert err < FP32_TOL
+    assert e64 < FP32_TOL
+    assert normwise_err(O, R64) < FP32_TOL
 
 
 @pytest.mark.parametrize("d,bf16", [(80, False), (96, True), (250, False)])
