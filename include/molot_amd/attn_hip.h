@@ -21,8 +21,9 @@
  * Head dims: every decode, shared-KV and prefill entry takes any even d
  * from 2 to 512 for fp32 and bf16 caches (attn.h and gemm.h take any qhd,
  * attn.h:99, :174, gemm.h:409-446; gemma4's global layers are 512 wide,
- * model.h:562-564) and d = 64, 128, 256 or 512 for Q8 caches; anything else
- * returns MOLOT_ENOTSUP before launching.
+ * model.h:562-564) and any d from 4 to 512 that is a multiple of 4 for Q8
+ * caches (4-byte aligned code rows); anything else returns MOLOT_ENOTSUP
+ * before launching.
  * Semantics (include/molot/attn.h:125-177): n = valid slots after the
  * append, window <= 0 attends [0, n), otherwise [t0, n) with
  * t0 = max(0, pos_cur - window + 1); an empty range yields o = 0.
@@ -54,8 +55,9 @@ extern "C" {
  *                bytes: molot_hip_q8_row_bytes(nkv, d) bytes per token;
  *   paged        block = [nkv][page][d] codes, then [nkv][page] fp32 scales:
  *                molot_hip_q8_block_bytes(nkv, d, page) bytes per block.
- * Q8 runs on head dims 64, 128, 256 and 512 (MOLOT_ENOTSUP otherwise); the head-major
- * entry points take no Q8 cache (MOLOT_EINVAL). */
+ * Q8 runs on head dims that are multiples of 4 up to 512 (MOLOT_ENOTSUP
+ * otherwise; 64 and 128 feed the matrix cores, the others the vector-ALU
+ * kernel); the head-major entry points take no Q8 cache (MOLOT_EINVAL). */
 #define MOLOT_KV_Q8 2
 
 /* Bytes of one token of a token-major Q8 cache, and of one paged Q8 block. */
@@ -340,8 +342,8 @@ void molot_hip_set_merge(int in_launch);
  * itself.  Both give the same bits.  A Q8 cache at d = 256 always takes the
  * pieces (its matrix-core kernel has no per-tile split); without them it
  * runs on the vector-ALU kernel, each query row a sequence of its own (the
- * path of d = 512 and of head dims that are not multiples of 8), which
- * agrees to fp32 rounding. */
+ * path of d = 512, of head dims that are not multiples of 8 and of Q8 caches
+ * at head dims other than 64, 128 and 256), which agrees to fp32 rounding. */
 void molot_hip_set_prefill_presplit(int on);
 
 /* Order in which the waves of a workgroup take their chunk's row blocks.

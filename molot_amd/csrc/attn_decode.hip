@@ -96,23 +96,36 @@ struct KVT<q8_t> {
 
 // K/V rows are read exactly once per step: non-temporal 16-byte loads (the
 // streaming hint measurably raises the sustained HBM read rate on gfx950).
+// Q8 rows excepted: the KV heads of a token share 128-byte lines (head rows
+// of d bytes at t*R + h*d, the token's scales after them), so a line one
+// head's workgroup fetched has to stay in the L2 for its neighbour's.
 template <typename T>
 __device__ __forceinline__ typename KVT<T>::vec load16(const T* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const typename KVT<T>::vec*>(p));
+  if constexpr (std::is_same<T, q8_t>::value)
+    return *reinterpret_cast<const typename KVT<T>::vec*>(p);
+  else
+    return __builtin_nontemporal_load(reinterpret_cast<const typename KVT<T>::vec*>(p));
 }
 
 // A 16-byte vector of row elements [e, e + VW) of a head row of dh
 // elements (dh even, possibly not a multiple of VW), read as VW/2 pieces of
-// two elements.  Pieces at or past dh read the row's first two elements
-// instead: they stay inside the row, their K products meet q's zero padding
-// and their V products land in output elements that are never stored.
+// two elements (Q8: VW/4 pieces of four codes, dh a multiple of 4).  Pieces
+// at or past dh read the row's first piece instead: they stay inside the
+// row, their K products meet q's zero padding and their V products land in
+// output elements that are never stored.
 template <typename T>
 __device__ __forceinline__ typename KVT<T>::vec load_pad(const T* row, int e, int dh) {
   using V = typename KVT<T>::vec;
   constexpr int PB = 2 * (int)sizeof(T);  // bytes per two-element piece
   V v;
   const char* r = reinterpret_cast<const char*>(row);
-  if constexpr (PB == 8) {
+  if constexpr (std::is_same<T, q8_t>::value) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ee = e + 4 * i < dh ? e + 4 * i : 0;
+      v[i] = *reinterpret_cast<const uint32_t*>(r + ee);  // plain: heads share lines
+    }
+  } else if constexpr (PB == 8) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int ee = e + 2 * i < dh ? e + 2 * i : 0;
@@ -730,7 +743,7 @@ template <int D, int GH, typename T>
 struct Tune {
   static constexpr int VW = KVT<T>::VW;
   static constexpr int lpr() {
-    int l = 8;
+    int l = D / VW < 8 ? D / VW : 8;  // Q8 at D = 64: 4 lanes of 16 codes a row
     while (GH * D / l > 32 && l < D / VW && l < 64) l *= 2;
     return l;
   }
@@ -1311,7 +1324,6 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   // 16-byte load, an fp32 scale per K and V row, applied to the row's score
   // and to its probability in PV
   constexpr bool Q8 = sizeof(T) == 1;
-  static_assert(!(Q8 && PAD), "Q8 heads are whole 16-byte vectors");
   const int G = a.nq / a.nkv;
   const int nsub = G / GH;
   // chunk slot z (chunk c = nch - 1 - z, below), (KV head, subgroup) index
@@ -1934,6 +1946,7 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     if constexpr (Q8) {
 #pragma unroll
       for (int e = 0; e < D / 64; ++e) {
+        if (lane + 64 * e >= DH) continue;  // a padded row ends at DH codes
         reinterpret_cast<int8_t*>(a.k)[off + lane + 64 * e] = (int8_t)kcode[e];
         reinterpret_cast<int8_t*>(a.v)[off + lane + 64 * e] = (int8_t)vcode[e];
       }
@@ -3863,7 +3876,8 @@ int dispatch_gh(int gh, const AttnArgs& a, int span, int nsubs, int B, void* st)
     case 2: return launch_attn<D, 2, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
     case 4: return launch_attn<D, 4, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
     case 8:
-      if constexpr (D <= 256) return launch_attn<D, 8, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
+      if constexpr (D <= 256 && !(sizeof(T) == 1 && D <= 128))
+        return launch_attn<D, 8, T, PAGED, ROPE, PAD>(a, span, nsubs, B, st);
       break;
   }
   return MOLOT_EINVAL;
@@ -3880,8 +3894,13 @@ int dispatch_pad(int d, int gh, const AttnArgs& a, int span, int nsubs, int B, v
 
 template <typename T, bool PAGED, bool ROPE>
 int dispatch_d(int d, int gh, const AttnArgs& a, int span, int nsubs, int B, void* st) {
-  if (d <= 64) return dispatch_pad<64, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
-  if (d <= 128) return dispatch_pad<128, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  if constexpr (sizeof(T) == 1) {  // Q8: 64 and 128 whole take the matrix cores (run_attn)
+    if (d < 64) return dispatch_gh<64, T, PAGED, ROPE, true>(gh, a, span, nsubs, B, st);
+    if (d < 128) return dispatch_gh<128, T, PAGED, ROPE, true>(gh, a, span, nsubs, B, st);
+  } else {
+    if (d <= 64) return dispatch_pad<64, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+    if (d <= 128) return dispatch_pad<128, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
+  }
   if (d <= 256) return dispatch_pad<256, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
   return dispatch_pad<512, T, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
 }
@@ -3890,17 +3909,17 @@ template <bool PAGED, bool ROPE>
 int dispatch_attn(int d, int kv_dtype, int gh, const AttnArgs& a, int span, int nsubs, int B,
                   void* st) {
   if (kv_dtype == MOLOT_KV_F32) return dispatch_d<float, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
-  if (kv_dtype == MOLOT_KV_Q8)  // D = 256, 512 (check_common; 64 and 128 take the matrix cores)
-    return d == 512 ? dispatch_gh<512, q8_t, PAGED, ROPE, false>(gh, a, span, nsubs, B, st)
-                    : dispatch_gh<256, q8_t, PAGED, ROPE, false>(gh, a, span, nsubs, B, st);
+  if (kv_dtype == MOLOT_KV_Q8)  // 64 and 128 take the matrix cores (run_attn)
+    return dispatch_d<q8_t, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
   return dispatch_d<bf16_t, PAGED, ROPE>(d, gh, a, span, nsubs, B, st);
 }
 
 // Head dims the prefill's matrix-core kernel is built for; decode on fp32
-// and bf16 caches takes any even d up to 512, Q8 caches q8_d.
+// and bf16 caches takes any even d up to 512, Q8 caches q8_d: any multiple
+// of 4 (a token's fp32 scales follow its nkv*d codes, 4-byte aligned).
 bool supported_d(int d) { return d == 64 || d == 128 || d == 256; }
 bool decode_d(int d) { return d >= 2 && d <= 512 && d % 2 == 0; }
-bool q8_d(int d) { return d == 64 || d == 128 || d == 256 || d == 512; }
+bool q8_d(int d) { return d >= 4 && d <= 512 && d % 4 == 0; }
 
 bool valid_kv(int kv_dtype) {
   return kv_dtype == MOLOT_KV_F32 || kv_dtype == MOLOT_KV_BF16 || kv_dtype == MOLOT_KV_Q8;
@@ -3975,7 +3994,7 @@ int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
   a.dh = d;
   const int G = a.nq / a.nkv;
   const bool q8 = kv_dtype == MOLOT_KV_Q8;
-  if ((q8 && d <= 128) || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma && (d == 64 || d == 128))) {
+  if ((q8 || (kv_dtype == MOLOT_KV_BF16 && g_bf16_mfma)) && (d == 64 || d == 128)) {
     // up to 16 q heads of a group share each K/V tile on the MFMA columns;
     // Q8 caches of D = 64, 128 run here, D = 256 and 512 on the vector-ALU
     // kernel
@@ -3987,7 +4006,9 @@ int run_attn(AttnArgs& a, int d, int kv_dtype, int span, int B, void* stream) {
     return d == 64 ? dispatch_mfma<64, PAGED, ROPE, false>(gh, a, span, nsubs, B, stream)
                    : dispatch_mfma<128, PAGED, ROPE, false>(gh, a, span, nsubs, B, stream);
   }
-  const int gh = d > 256 ? std::min(pick_gh(G), kMaxGhWide) : pick_gh(G);
+  // Q8 rows padded to D <= 128 hold 16 q elements a lane per head: at most
+  // 4 heads a workgroup there too
+  const int gh = d > 256 || (q8 && d < 128) ? std::min(pick_gh(G), kMaxGhWide) : pick_gh(G);
   const int nsubs = G / gh;
   return dispatch_attn<PAGED, ROPE>(d, kv_dtype, gh, a, span, nsubs, B, stream);
 }
@@ -4063,8 +4084,8 @@ const char* molot_hip_strerror(int status) {
     case MOLOT_OK: return "ok";
     case MOLOT_EINVAL: return "molot_amd: invalid argument";
     case MOLOT_ENOTSUP:
-      return "molot_amd: unsupported shape (an even head dim up to 512; Q8 caches 64, 128, 256 "
-             "or 512)";
+      return "molot_amd: unsupported shape (an even head dim up to 512; Q8 caches a multiple "
+             "of 4 up to 512)";
     case MOLOT_ENOSPC: return "molot_amd: KV cache full";
     case MOLOT_ENOWS:
       return "molot_amd: workspace not sized for this shape on a capturing stream (launch the "
@@ -4230,9 +4251,11 @@ int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, 
   if (n_att <= 0) return zero_out(O, (int64_t)nq * d, (hipStream_t)stream);  // o = 0
   if (!K || !V) return MOLOT_EINVAL;
   const int esz = kv_esz(kv_dtype);
+  // 16-byte vector loads of every row; a Q8 cache has the fixed layout
+  // checked above, whose head dims off 64/128/256/512 load 4-byte pieces
   if (!aligned16(K) || !aligned16(V) || !aligned16(Q) || !aligned16(O) ||
-      (tok_stride * esz) % 16 || (head_stride * esz) % 16)
-    return MOLOT_EINVAL;  // 16-byte vector loads of every row
+      (kv_dtype != MOLOT_KV_Q8 && ((tok_stride * esz) % 16 || (head_stride * esz) % 16)))
+    return MOLOT_EINVAL;
   AttnArgs a{};
   a.q = Q;
   a.k = const_cast<void*>(K);
@@ -4610,9 +4633,10 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   // that splits staged Q8 tiles itself is built for 64 and 128).  Head dims
   // above 256 and even ones that are not multiples of 8 run as prefill rows
   // (prefill_rows).
-  const bool rows_path = d > 256 || d % 8 != 0;
   const bool padded = !supported_d(d);
-  if (padded && !rows_path && kv_dtype == MOLOT_KV_Q8) return MOLOT_ENOTSUP;
+  // Q8 caches at padded dims too (the matrix-core prefill reads whole
+  // 16-code chunks of the built dims only)
+  const bool rows_path = d > 256 || d % 8 != 0 || (padded && kv_dtype == MOLOT_KV_Q8);
   const bool pieces_only = kv_dtype == MOLOT_KV_Q8 && d == 256;
   const int D = padded ? (d <= 64 ? 64 : d <= 128 ? 128 : 256) : d;
   if (M < 0 || N < 0 || pos0 < 0 || (M > 0 && (!Qm || !Om))) return MOLOT_EINVAL;
@@ -4768,8 +4792,8 @@ static int prefill_step_impl(float* q, const float* k_new, const float* v_new, v
   int st = check_common(nq, nkv, d, kv_dtype);
   if (st) return st;
   // the prefill kernels' head dims, a multiple of 8 below 256 run padded, or
-  // prefill rows (d > 256, or not a multiple of 8; see attn_prefill_impl)
-  if (!supported_d(d) && d % 8 == 0 && d < 256 && kv_dtype == MOLOT_KV_Q8) return MOLOT_ENOTSUP;
+  // prefill rows (d > 256, not a multiple of 8, or a padded Q8 cache; see
+  // attn_prefill_impl)
   const bool pieces_only = kv_dtype == MOLOT_KV_Q8 && d == 256;  // no per-tile kernel
   Norms nm;
   nm.q = q_norm;

@@ -97,14 +97,14 @@ def test_validation_before_launch():
     for d in (97, 514, 0, 1024):
         assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 4, 10, d, 0.1, 9,
                                                    0, 0, s) == L.ENOTSUP
-    # prefill: any even d up to 512 on fp32 and bf16 caches; Q8 64, 128, 256, 512
-    for d, kvd in ((514, 0), (514, L.KV_BF16), (96, L.KV_Q8), (90, L.KV_Q8), (7, 0)):
+    # prefill: any even d up to 512 on fp32 and bf16 caches; Q8 any multiple of 4
+    for d, kvd in ((514, 0), (514, L.KV_BF16), (90, L.KV_Q8), (34, L.KV_Q8), (7, 0)):
         assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, d, 0.1, 6, 0,
                                               kvd, s) == L.ENOTSUP
         assert lib.molot_hip_prefill_step(_p(), _p(), _p(), _p(), _p(), _p(), 8, 2, d, 4, 6, 6,
                                           None, None, 0, 1e-6, _p(), 0.1, 0, kvd,
                                           s) == L.ENOTSUP
-    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 96, 0.1, 9, 0,
+    assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, 98, 0.1, 9, 0,
                                                L.KV_Q8, s) == L.ENOTSUP
     # null output
     assert lib.molot_hip_attn_decode_strided(_p(), _p(), _p(), None, 8, 4, 10, 128, 512, 128,
@@ -151,8 +151,8 @@ def test_q8_validation_before_launch():
     lib = L.load()
     s = ctypes.c_void_p(0)
     Q8 = L.KV_Q8
-    # Q8 caches: d = 64, 128, 256, 512 for decode
-    for d in (192, 384, 320):
+    # Q8 caches: any multiple of 4 up to 512 (a token's fp32 scales follow its codes)
+    for d in (90, 34, 516, 2):
         assert lib.molot_hip_attn_decode_gqa_cache(_p(), _p(), _p(), _p(), 8, 2, 10, d, 0.1, 9,
                                                    0, Q8, s) == L.ENOTSUP
     # element strides instead of the token-major Q8 byte layout
@@ -164,13 +164,13 @@ def test_q8_validation_before_launch():
     # paged Q8 blocks stay 16-byte aligned only when nkv * page is a multiple of 4
     assert lib.molot_hip_attn_decode_paged(_p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4, 4, 8,
                                            1, 64, 2, 0.1, 0, Q8, s) == L.EINVAL
-    assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 192, 0.1, 6, 0,
-                                          Q8, s) == L.ENOTSUP  # Q8 prefill: 64, 128, 256, 512
+    assert lib.molot_hip_attn_prefill_gqa(_p(), _p(), _p(), _p(), 8, 2, 4, 10, 190, 0.1, 6, 0,
+                                          Q8, s) == L.ENOTSUP  # Q8 prefill: multiples of 4
     # the RoPE/append entries write only rows the attention entries read back
-    assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 2, 192, 5, 5, _p(), Q8,
+    assert lib.molot_hip_rope_append(_p(), _p(), _p(), _p(), _p(), 8, 2, 190, 5, 5, _p(), Q8,
                                      s) == L.ENOTSUP
     assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,
-                                           8, 2, 192, 16, _p(), Q8, s) == L.ENOTSUP
+                                           8, 2, 190, 16, _p(), Q8, s) == L.ENOTSUP
     assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,
                                            8, 1, 64, 2, _p(), Q8, s) == L.EINVAL
     assert lib.molot_hip_rope_append_paged(_p(), _p(), _p(), _p(), _p(), _p(), _p(), None, 1, 4,

@@ -519,16 +519,19 @@ def test_q8_quantizer_bounds():
     np.testing.assert_array_equal(q, k.astype(np.int8))
 
 
-def test_q8_attention_is_attention_on_dequantized_rows():
+@pytest.mark.parametrize("nkv,d", [(4, 128), (4, 100), (3, 36)])
+def test_q8_attention_is_attention_on_dequantized_rows(nkv, d):
     """The Q8 cache read through its byte layout (rows, then per-head scales)
     gives bit for bit the attention over its dequantized fp32 rows: pins the
-    scale addressing, which a wrong offset would break."""
-    st = Stream(39)
-    nq, nkv, d, n = 16, 4, 128, 301
+    scale addressing, which a wrong offset would break, also at head dims
+    whose rows end off a 16-byte boundary (nkv = 3, d = 36: 108 codes, 12
+    scale bytes, 8 bytes of padding)."""
+    st = Stream(39 + d)
+    nq, n = 4 * nkv, 301
     Q = st.normal((nq, d))
     K, V = kv_token_major(st, n, nkv, d, 2.0)
     Kq, Vq = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
-    assert Kq.shape == (n, nkv * d + 16)
+    assert Kq.shape == (n, nkv * d + (4 * nkv + 15) // 16 * 16)  # codes, then padded scales
     Kd, Vd = oracle.q8_dequant(Kq, nkv, d), oracle.q8_dequant(Vq, nkv, d)
     for window in (0, 77):
         a = oracle.attn_decode_gqa_cache(Q, Kq, Vq, nq, nkv, n, d, 0.088, n - 1, window)
@@ -538,11 +541,12 @@ def test_q8_attention_is_attention_on_dequantized_rows():
     assert np.max(np.abs(Kd - K)) <= np.abs(K).max() / 127 * 0.51
 
 
-@pytest.mark.parametrize("nkv,d", [(4, 256), (8, 128), (2, 64)])
+@pytest.mark.parametrize("nkv,d", [(4, 256), (8, 128), (2, 64), (2, 100), (1, 300)])
 def test_q8_prefill_is_prefill_on_dequantized_rows(nkv, d):
     """The prefill over a Q8 cache gives bit for bit the prefill over its
-    dequantized fp32 rows, at every Q8 head dim (d = 256: 1040-byte rows at
-    nkv = 4): pins the prefill's Q8 row and scale addressing."""
+    dequantized fp32 rows, at the matrix-core head dims (d = 256: 1040-byte
+    rows at nkv = 4) and at padded ones: pins the prefill's Q8 row and scale
+    addressing."""
     st = Stream(41 + d)
     nq, M, N, pos0 = 2 * nkv, 17, 240, 223
     Q = st.normal((M, nq, d))
@@ -569,12 +573,13 @@ def test_q8_decode_step_appends_quantized_row():
     np.testing.assert_array_equal(Vq[pos], oracle.q8_cache(v.reshape(1, -1), nkv, d)[0])
 
 
-def test_q8_paged_is_token_major_through_a_block_table():
+@pytest.mark.parametrize("d", [64, 100])
+def test_q8_paged_is_token_major_through_a_block_table(d):
     """Paged Q8 blocks ([nkv][page][d] codes, then [nkv][page] scales) read
     through a shuffled block table give bit for bit the token-major Q8
     attention on the same rows: pins the paged scale addressing."""
-    st = Stream(41)
-    nq, nkv, d, n, page = 16, 4, 64, 203, 16
+    st = Stream(41 + d)
+    nq, nkv, n, page = 16, 4, 203, 16
     Q = st.normal((nq, d))
     K, V = kv_token_major(st, n, nkv, d, 2.0)
     nblk = (n + page - 1) // page

@@ -550,15 +550,86 @@ def test_q8_d256_prefill_without_pieces_in_a_graph(gpu):
 
 
 # ---------------------------------------------------------------------------
+# Q8 caches at head dims other than 64, 128, 256 and 512: the vector-ALU
+# kernel for the next of them, each row read at its d codes in 4-code pieces
+
+@pytest.mark.parametrize("nq,nkv,d,n,window", [
+    (16, 4, 48, 900, 0),       # D = 64
+    (32, 8, 96, 3000, 0),      # D = 128
+    (16, 2, 100, 2000, 300),   # d % 8 == 4, window
+    (8, 4, 200, 1500, 0),      # D = 256
+    (8, 2, 300, 2500, 0),      # D = 512
+    (8, 8, 500, 40, 0),        # one chunk
+    (12, 3, 36, 1000, 0),      # 124-byte token rows: off 16-byte boundaries
+])
+def test_q8_padded_decode_vs_oracle(gpu, nq, nkv, d, n, window):
+    announce(f"q8 padded decode {nq}/{nkv}/{d} n={n} window={window}")
+    st = Stream(n + d + 17)
+    Q = st.normal((nq, d))
+    Kq, Vq = q8_caches(st, n, nkv, d)
+    O = torch.empty((nq, d), device="cuda")
+    s = 1 / math.sqrt(d)
+    attn.attn_decode_gqa_cache(dev(Q), dev_u8(Kq), dev_u8(Vq), O, nq, nkv, n, d, s, n - 1, window)
+    R = oracle.attn_decode_gqa_cache(Q, Kq, Vq, nq, nkv, n, d, s, n - 1, window)
+    err = normwise_err(host(O), R)
+    print(f"q8 padded normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
+@pytest.mark.parametrize("d,pos,norms,nkv", [(96, 0, False, 4), (96, 2000, True, 4),
+                                              (300, 1200, False, 4), (36, 700, True, 4),
+                                              (20, 900, False, 3)])
+def test_q8_padded_decode_step_vs_oracle(gpu, d, pos, norms, nkv):
+    """The fused step at a padded head dim: the kernel quantizes the new
+    rows over their d values (bit-exact bytes at position 0) and stores d
+    codes a head, never the padding.  nkv = 3, d = 20: 60 codes and 16 scale
+    bytes, so token rows start off 16-byte boundaries."""
+    test_q8_decode_step_vs_oracle(gpu, d, pos, 0, norms, nq=4 * nkv, nkv=nkv)
+
+
+def test_q8_padded_paged_and_prefill(gpu):
+    """Paged Q8 pages and the prefill (query rows on the vector-ALU kernel)
+    at d = 100, against the oracle on the same bytes."""
+    nq, nkv, d, page = 8, 4, 100, 16
+    announce("q8 padded paged decode d=100")
+    P = q8_paged_problem(5, nq, nkv, d, 50, 900, seed=77)
+    inv = oracle.rope_inv_freq(10000.0, d)
+    s = 1 / math.sqrt(d)
+    B = P["B"]
+    q, K, V = dev(P["q"]), dev_u8(P["Kp"]), dev_u8(P["Vp"])
+    O = torch.empty((B, nq, d), device="cuda")
+    attn.decode_step_paged(q, dev(P["k_new"]), dev(P["v_new"]), K, V, O,
+                           dev(P["bt"].reshape(-1)), dev(P["n"]), None, B, P["max_blocks"], nq,
+                           nkv, d, page, dev(inv), s, 0)
+    oq, oK, oV, oO = oracle_paged_q8(P, inv, s)
+    np.testing.assert_allclose(host(q), oq, rtol=2e-6, atol=4e-6)
+    Kh, Vh = host_u8(K).reshape(oK.shape), host_u8(V).reshape(oV.shape)
+    np.testing.assert_array_equal(Vh, oV)  # v's codes and scales, and no byte past d
+    R = oracle.attn_decode_paged(host(q), Kh, Vh, P["bt"], P["n"], None, B, P["max_blocks"], nq,
+                                 nkv, d, page, s, 0)
+    assert normwise_err(host(O), R) < TOL
+    assert normwise_err(host(O), oO) < 1e-3  # appended k may differ by a code (see above)
+    announce("q8 padded prefill d=100")
+    st = Stream(78)
+    M, N, pos0 = 30, 430, 400
+    Qm = st.normal((M, nq, d))
+    Kq, Vq = q8_caches(st, N, nkv, d)
+    Om = torch.full((M, nq, d), float("nan"), device="cuda")
+    attn.attn_prefill_gqa(dev(Qm), dev_u8(Kq), dev_u8(Vq), Om, nq, nkv, M, N, d, s, pos0, 64)
+    R = oracle.attn_prefill(Qm, Kq, Vq, nq, nkv, M, N, d, s, pos0, 64)
+    assert normwise_err(host(Om), R) < TOL
+
+
+# ---------------------------------------------------------------------------
 # shapes the Q8 paths do not take: errors through the ABI, never a launch
 
 def test_q8_errors(gpu):
     st = Stream(60)
-    Q = dev(st.normal((8, 96)))
-    O = torch.empty((8, 96), device="cuda")
-    C = torch.zeros(10 * oracle.q8_row_bytes(2, 96), dtype=torch.uint8, device="cuda")
-    with pytest.raises(MolotHipError) as e:  # Q8 caches: d = 64, 128, 256, 512 only
-        attn.attn_decode_gqa_cache(Q, C, C, O, 8, 2, 10, 96, 0.1, 9, 0)
+    Q = dev(st.normal((8, 90)))
+    O = torch.empty((8, 90), device="cuda")
+    C = torch.zeros(10 * oracle.q8_row_bytes(2, 90), dtype=torch.uint8, device="cuda")
+    with pytest.raises(MolotHipError) as e:  # Q8 caches: multiples of 4 only
+        attn.attn_decode_gqa_cache(Q, C, C, O, 8, 2, 10, 90, 0.1, 9, 0)
     assert e.value.status == ENOTSUP
     Q = dev(st.normal((8, 64)))
     O = torch.empty((8, 64), device="cuda")
