@@ -177,14 +177,56 @@ __device__ __forceinline__ float dpp_f(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
 }
 
+// x of lanes l and l ^ 16 (xor16), or l and l ^ 32 (xor32), as the pair
+// (lower lane's, upper lane's) in every lane: v_permlane16_swap and
+// v_permlane32_swap exchange 16- or 32-lane rows of two registers, so with
+// both operands x they leave the lower row's x in the first and the upper
+// row's in the second, in both rows (checked lane by lane on the GPU).
+// Reducing the pair gives every lane the same operands in the same order,
+// where a shuffle would take two LDS round trips.
+__device__ __forceinline__ float max_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// x combined with lane l ^ OFF's x (a sum in the shuffle's operand order)
+template <int OFF>
+__device__ __forceinline__ float sum_xor(float x) {
+  if constexpr (OFF == 16) return sum_xor16(x);
+  else if constexpr (OFF == 32) return sum_xor32(x);
+  else return x + __shfl_xor(x, OFF);
+}
+template <int OFF>
+__device__ __forceinline__ float max_xor(float x) {
+  if constexpr (OFF == 16) return max_xor16(x);
+  else if constexpr (OFF == 32) return max_xor32(x);
+  else return fmaxf(x, __shfl_xor(x, OFF));
+}
+
 template <int N>
 __device__ __forceinline__ float group_max(float v) {
   if constexpr (N >= 2) v = fmaxf(v, dpp_f<0xB1>(v));
   if constexpr (N >= 4) v = fmaxf(v, dpp_f<0x4E>(v));
   if constexpr (N >= 8) v = fmaxf(v, dpp_f<0x141>(v));
   if constexpr (N >= 16) v = fmaxf(v, dpp_f<0x140>(v));
-  if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16));
-  if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  if constexpr (N >= 32) v = max_xor16(v);
+  if constexpr (N >= 64) v = max_xor32(v);
   return v;
 }
 
@@ -194,8 +236,8 @@ __device__ __forceinline__ float group_sum(float v) {
   if constexpr (N >= 4) v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
   if constexpr (N >= 8) v += dpp_f<0x141>(v);  // row_half_mirror
   if constexpr (N >= 16) v += dpp_f<0x140>(v); // row_mirror
-  if constexpr (N >= 32) v += __shfl_xor(v, 16);
-  if constexpr (N >= 64) v += __shfl_xor(v, 32);
+  if constexpr (N >= 32) v = sum_xor16(v);
+  if constexpr (N >= 64) v = sum_xor32(v);
   return v;
 }
 
@@ -1747,9 +1789,16 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // wave-uniform
 #pragma unroll
       for (int g = 0; g < GH; ++g) {
-#pragma unroll
-        for (int off = LPR; off < 64; off <<= 1)
-          bmax[g] = fmaxf(bmax[g], __shfl_xor(bmax[g], off));
+        auto bmax_off = [&](auto OFFC) {
+          constexpr int off = decltype(OFFC)::value;
+          if constexpr (off >= LPR) bmax[g] = max_xor<off>(bmax[g]);
+        };
+        bmax_off(std::integral_constant<int, 1>{});
+        bmax_off(std::integral_constant<int, 2>{});
+        bmax_off(std::integral_constant<int, 4>{});
+        bmax_off(std::integral_constant<int, 8>{});
+        bmax_off(std::integral_constant<int, 16>{});
+        bmax_off(std::integral_constant<int, 32>{});
         const float mn = fmaxf(m_run[g], bmax[g]);
         const float alpha = exp2_hw(m_run[g] - mn);  // m_run = -inf -> 0
         m_run[g] = mn;
@@ -1895,14 +1944,25 @@ __global__ __launch_bounds__(C::NT) void attn_kernel(AttnArgs a) {
   }
 
   // ---- 4. merge the waves ----
+  // lanes LPR2 apart hold the same columns of other rows: sum them, in
+  // ascending offsets
+  auto merge_off = [&](auto OFFC) {
+    constexpr int off = decltype(OFFC)::value;
+    if constexpr (off >= LPR2) {
 #pragma unroll
-  for (int off = LPR2; off < 64; off <<= 1)
+      for (int g = 0; g < GH; ++g) {
+        l_run[g] = sum_xor<off>(l_run[g]);
 #pragma unroll
-    for (int g = 0; g < GH; ++g) {
-      l_run[g] += __shfl_xor(l_run[g], off);
-#pragma unroll
-      for (int e = 0; e < AW; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+        for (int e = 0; e < AW; ++e) acc[g][e] = sum_xor<off>(acc[g][e]);
+      }
     }
+  };
+  merge_off(std::integral_constant<int, 1>{});
+  merge_off(std::integral_constant<int, 2>{});
+  merge_off(std::integral_constant<int, 4>{});
+  merge_off(std::integral_constant<int, 8>{});
+  merge_off(std::integral_constant<int, 16>{});
+  merge_off(std::integral_constant<int, 32>{});
   float* wm = smem + L.wm;
   float* wl = smem + L.wl;
   float* red = smem + L.red;
@@ -2497,8 +2557,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
         sv[u][r] = row < rlim ? (Q8 ? sacc[u][r] * sk4[u][r] : sacc[u][r]) : -INFINITY;
         tmax = fmaxf(tmax, sv[u][r]);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = max_xor32(max_xor16(tmax));
     // finite: a claimed tile has a row; the first tile always moves the max
     if (__builtin_amdgcn_ballot_w64(tmax > m_run + kLazyMax) != 0) {
       const float mn = fmaxf(m_run, tmax);
@@ -2581,8 +2640,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
       for (int d = g4 * (D / 4); d < (g4 + 1) * (D / 4); ++d)
         part = fmaf(qs[m16 * QSTR + d], knew[d], part);
     }
-    part += __shfl_xor(part, 16);
-    part += __shfl_xor(part, 32);
+    part = sum_xor32(sum_xor16(part));
     const float snew = part * qsc;  // base 2, as the streamed scores
     const float mn = fmaxf(m_run, snew);
     const float alpha = exp2_hw(m_run - mn);
@@ -2596,8 +2654,7 @@ __global__ __launch_bounds__(kMfmaThreads, 2) void attn_mfma_kernel(AttnArgs a) 
   }
 
   // ---- the wave's partial into its own LDS region, then the chunk ----
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
+  l_run = sum_xor32(sum_xor16(l_run));
   float* wm = smem + L.wm;
   float* wl = smem + L.wl;
   float* red = smem + L.vt;
@@ -2883,12 +2940,17 @@ void prefill_mfma16_kernel(PfArgs a) {
   // base + 16*l of a 1 KB block (checked on the GPU), so lane l loads the
   // unit the swizzled layout keeps there (unit ch of key r at ch ^ f(r):
   // slot j holds unit j ^ f(r)).  No registers and no arithmetic per element.
+  // The source is a wave-uniform row base (the tile's first key) plus a
+  // 32-bit lane offset (key within the tile, clamped to the range's last
+  // key, and its unit), so the loads take a scalar base and the per-tile
+  // address arithmetic stays off the vector ALU.
   auto dload = [&](int tk, char* kbuf, char* vbuf) {
     constexpr int UPR = D / 8;             // 16-byte units per row
     constexpr int KPB = 64 / UPR;          // keys per 1 KB block
     constexpr int BPP = KT / KPB;          // blocks per piece
     constexpr int NBL = 2 * 3 * BPP;       // blocks per tile (K, V; 3 pieces)
     const int r_in = lane / UPR, jpos = lane % UPR;
+    const int lastr = kt_hi - 1 - tk;      // the range's last key, from the tile's first
 #pragma unroll
     for (int bi0 = 0; bi0 < NBL; bi0 += PW) {
       const int bi = bi0 + w;  // wave-uniform
@@ -2897,9 +2959,10 @@ void prefill_mfma16_kernel(PfArgs a) {
       const int pc = rem / BPP, kb = rem - pc * BPP;
       const int r = kb * KPB + r_in;
       const int ch = jpos ^ (kv ? vt_f<D>(r) : kt_f<D>(r));
-      const int t = min(tk + r, kt_hi - 1) - a.T0;
-      const uint16_t* src =
-          a.pieces + ((((int64_t)kv * a.nkv + h) * 3 + pc) * a.R + t) * D + 8 * ch;
+      const char* rows = reinterpret_cast<const char*>(
+          a.pieces + ((((int64_t)kv * a.nkv + h) * 3 + pc) * a.R + (tk - a.T0)) * D);
+      const uint32_t lo = (uint32_t)(min(r, lastr) * (2 * D) + 16 * ch);
+      const char* src = rows + lo;
       char* dst = (kv ? vbuf : kbuf) + pc * KT * (2 * D) + kb * 1024;
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0,
                                        0);
@@ -2977,30 +3040,11 @@ void prefill_mfma16_kernel(PfArgs a) {
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
-  if constexpr (PRE) {
-    if (ntile > 0) dload(kt_s, kp_buf[0], vp_buf[0]);
-    wait_vmcnt<0>();  // this wave's direct loads are in LDS
-    __syncthreads();
-  } else {
-    if (ntile > 0) load_tile(kt_s);
-  }
-  for (int it = 0; it < ntile; ++it) {
-    const int tk = kt_s + it * KT;
-    const int bf = NBUF == 2 ? (it & 1) : 0;
-    const char* kp_s = kp_buf[bf];
-    const char* vp_s = vp_buf[bf];
-    if constexpr (PRE) {
-      // the other buffer was last read in the previous tile, which every
-      // wave finished before the barrier that ended it
-      if (NBUF == 2 && it + 1 < ntile) dload(tk + KT, kp_buf[bf ^ 1], vp_buf[bf ^ 1]);
-    } else {
-      store_tile(kp_buf[bf], vp_buf[bf]);
-      __syncthreads();
-      if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
-    }
-    // scores of the two 16-key halves, smallest piece products first; even
-    // and odd 32-element steps into separate accumulators (four independent
-    // MFMA chains, added at the end)
+
+  // scores of the two 16-key halves of the tile at kp_s, smallest piece
+  // products first; even and odd 32-element steps into separate
+  // accumulators (four independent MFMA chains, added at the end)
+  auto scores = [&](const char* kp_s, f32x4 (&sacc)[KH]) {
     f32x4 sacc2[KH][2];
 #pragma unroll
     for (int u = 0; u < KH; ++u) sacc2[u][0] = sacc2[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -3026,13 +3070,21 @@ void prefill_mfma16_kernel(PfArgs a) {
           acc = mfma_bf16(k0, qh[s], acc);
         }
       }
-    f32x4 sacc[KH];
 #pragma unroll
     for (int u = 0; u < KH; ++u) sacc[u] = sacc2[u][0] + sacc2[u][1];
-    // online softmax (base 2) of this lane's row over its 8 keys of the tile.
-    // Lazy rescale, as in the decode kernel: the running max moves only when
-    // a score exceeds it by more than kLazyMax (p <= 2^8 otherwise); o and l
-    // always share the max they were formed with.
+  };
+  // online softmax (base 2) of this lane's row over its 8 keys of the tile
+  // at tk.  Lazy rescale, as in the decode kernel: the running max moves
+  // only when a score exceeds it by more than kLazyMax (p <= 2^8 otherwise);
+  // o and l always share the max they were formed with.  Leaves P^T as
+  // pieces (B operand: slot 4u + r holds key 16u + 4*g4 + r), the factor
+  // alpha that o and l take before P is added (1 unless the max moved) and
+  // the tile's row sum.
+  // FULL (a std::integral_constant): every key of the tile is in every
+  // row's range, so no key is masked and every probability is an exp.
+  auto softmax = [&](auto FULL, const f32x4 (&sacc)[KH], int tk, bf16x8_t& ph, bf16x8_t& pm,
+                     bf16x8_t& pl, float& alpha, bool& grow, float& ps) {
+    constexpr bool full = decltype(FULL)::value;
     float sv[KH][4];
     float tmax = -INFINITY;
 #pragma unroll
@@ -3040,38 +3092,34 @@ void prefill_mfma16_kernel(PfArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = tk + 16 * u + 4 * g4 + r;
-        sv[u][r] = (t >= rt0 && t < rnn) ? sacc[u][r] : -INFINITY;
+        sv[u][r] = (full || (t >= rt0 && t < rnn)) ? sacc[u][r] : -INFINITY;
         tmax = fmaxf(tmax, sv[u][r]);
       }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const bool grow = tmax > m_run + kLazyMax;  // false while the row has no key (-inf)
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-      const float mn = grow ? fmaxf(m_run, tmax) : m_run;
-      const float alpha = m_run == -INFINITY ? 1.f : exp2_hw(m_run - mn);
-      m_run = mn;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-    }
-    // P^T pieces (B operand): slot 4u + r holds key 16u + 4*g4 + r
+    tmax = max_xor32(max_xor16(tmax));
+    grow = tmax > m_run + kLazyMax;  // false while the row has no key (-inf)
+    const float mn = grow ? fmaxf(m_run, tmax) : m_run;
+    alpha = m_run == -INFINITY ? 1.f : exp2_hw(m_run - mn);  // exp2(0) = 1 exactly
+    m_run = mn;
     float pv[4 * KH];
-    float ps = 0.f;
+    ps = 0.f;
 #pragma unroll
     for (int u = 0; u < KH; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pv[4 * u + r] = sv[u][r] == -INFINITY ? 0.f : exp2_hw(sv[u][r] - m_run);
+        pv[4 * u + r] = (!full && sv[u][r] == -INFINITY) ? 0.f : exp2_hw(sv[u][r] - m_run);
         ps += pv[4 * u + r];
       }
-    l_run += ps;
     uint32_t ph4[4], pm4[4], pl4[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) split3x2(pv[e], pv[e + 1], ph4[e / 2], pm4[e / 2], pl4[e / 2]);
-    const bf16x8_t ph = __builtin_bit_cast(bf16x8_t, u32x4{ph4[0], ph4[1], ph4[2], ph4[3]});
-    const bf16x8_t pm = __builtin_bit_cast(bf16x8_t, u32x4{pm4[0], pm4[1], pm4[2], pm4[3]});
-    const bf16x8_t pl = __builtin_bit_cast(bf16x8_t, u32x4{pl4[0], pl4[1], pl4[2], pl4[3]});
-    // PV: V^T of the 16-row block dt by two transposed reads per piece
+    ph = __builtin_bit_cast(bf16x8_t, u32x4{ph4[0], ph4[1], ph4[2], ph4[3]});
+    pm = __builtin_bit_cast(bf16x8_t, u32x4{pm4[0], pm4[1], pm4[2], pm4[3]});
+    pl = __builtin_bit_cast(bf16x8_t, u32x4{pl4[0], pl4[1], pl4[2], pl4[3]});
+  };
+  // o += P V over the tile at vp_s: V^T of the 16-row block dt by two
+  // transposed reads per piece
+  auto pv_acc = [&](const char* vp_s, const bf16x8_t& ph, const bf16x8_t& pm,
+                    const bf16x8_t& pl) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       bf16x8_t av[KP];
@@ -3102,6 +3150,54 @@ void prefill_mfma16_kernel(PfArgs a) {
         o[dt] = mfma_bf16(av[0], ph, o[dt]);
       }
     }
+  };
+  // o and l take alpha, then l the tile's sum (two roundings, as the
+  // running sums of the decode kernels)
+  auto rescale = [&](float alpha, bool grow, float ps) {
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
+    }
+    {
+#pragma clang fp contract(off)
+      l_run = l_run * alpha + ps;
+    }
+  };
+
+  if constexpr (PRE) {
+    if (ntile > 0) dload(kt_s, kp_buf[0], vp_buf[0]);
+    wait_vmcnt<0>();  // this wave's direct loads are in LDS
+    __syncthreads();
+  } else {
+    if (ntile > 0) load_tile(kt_s);
+  }
+  for (int it = 0; it < ntile; ++it) {
+    const int tk = kt_s + it * KT;
+    const int bf = NBUF == 2 ? (it & 1) : 0;
+    const char* kp_s = kp_buf[bf];
+    const char* vp_s = vp_buf[bf];
+    if constexpr (PRE) {
+      // the other buffer was last read in the previous tile, which every
+      // wave finished before the barrier that ended it
+      if constexpr (NBUF == 2)
+        if (it + 1 < ntile) dload(tk + KT, kp_buf[bf ^ 1], vp_buf[bf ^ 1]);
+    } else {
+      store_tile(kp_buf[bf], vp_buf[bf]);
+      __syncthreads();
+      if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
+    }
+    f32x4 sacc[KH];
+    scores(kp_s, sacc);
+    bf16x8_t ph, pm, pl;
+    float alpha, ps;
+    bool grow;
+    // interior tile: every row of the wave attends all of its keys
+    if (__builtin_amdgcn_ballot_w64(!(rv && tk >= rt0 && tk + KT <= rnn)) == 0)
+      softmax(std::true_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+    else
+      softmax(std::false_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+    rescale(alpha, grow, ps);
+    pv_acc(vp_s, ph, pm, pl);
     if constexpr (PRE) {
       if constexpr (NBUF == 1) {
         __syncthreads();  // every wave is done with the buffer
@@ -3113,8 +3209,7 @@ void prefill_mfma16_kernel(PfArgs a) {
       if constexpr (NBUF == 1) __syncthreads();  // the tile's LDS is rewritten next
     }
   }
-  l_run += __shfl_xor(l_run, 16);
-  l_run += __shfl_xor(l_run, 32);
+  l_run = sum_xor32(sum_xor16(l_run));
   if (rv && a.nsplit > 1) {  // the split's partial: unnormalised o, max in natural units, sum
     const int64_t ps = ((int64_t)m * a.nq + h * G + g) * a.nsplit + sp;
     float* po = a.part_o + ps * D;
