@@ -833,7 +833,10 @@ struct Tune {
   static constexpr int nw() {
     const int w = RB == 8 ? 2 : (wps(RB) >= 1 ? wps(RB) : 1);
     int nw = 4 * w;
-    while (nw > 4 && nw * GH * D > 8192) nw -= 4;  // wave-merge buffer <= 32 KiB
+    // wave-merge buffer <= 32 KiB (64 KiB at d = 512, one workgroup a CU:
+    // two waves per SIMD instead of one: 8q/2kv/d512 Q8 step
+    // 32.7 -> 29.8 us, fp32 61.5 -> 60.9 us)
+    while (nw > 4 && nw * GH * D > (D > 256 ? 16384 : 8192)) nw -= 4;
     return nw;
   }
   static constexpr int NW = nw();
@@ -3797,11 +3800,14 @@ using AttnFn = void (*)(AttnArgs);
 thread_local int t_last_nchunks = 0;
 thread_local int t_last_chunk = 0;
 
+// Dynamic LDS a workgroup may take (the CU's 160 KiB).
+constexpr size_t kMaxLds = 160 * 1024;
+
 // Launches an attention kernel of a planned problem and, for a split
 // context, combine_kernel after it on the same stream.
 int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d, int nsubs,
                 int B, bool paged, bool rope, void* stream) {
-  if (lds > 65536) return (int)hipErrorInvalidConfiguration;
+  if (lds > kMaxLds) return (int)hipErrorInvalidConfiguration;
   if ((gh * d) % kCombPairs || d % kCombPairs) return MOLOT_ENOTSUP;  // combine tiling
   t_last_nchunks = a.nchunks;
   t_last_chunk = a.chunk;
@@ -3900,7 +3906,7 @@ int launch_pair(AttnFn kern, int threads, size_t lds, AttnArgs a, int gh, int d,
 template <int D, int GH, typename T, bool PAGED, bool ROPE, bool PAD, typename C>
 int launch_planned(AttnArgs a, int nsubs, int B, void* stream) {
   if (a.mrg && sizeof(float) * (size_t)Lds(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED,
-                                           a.mrg).total > 65536)
+                                           a.mrg).total > kMaxLds)
     no_merge(a);  // the merge's statistics do not fit beside the kernel's LDS
   const Lds L(D, GH, C::NW, C::RB, a.chunk, a.page_shift, PAGED, a.mrg);
   return launch_pair(attn_kernel<D, GH, T, PAGED, ROPE, PAD, C>, C::NT, sizeof(float) * (size_t)L.total,
@@ -3947,7 +3953,7 @@ int launch_mfma(AttnArgs a, int span, int nsubs, int B, void* stream) {
   // the chunks in sequential rounds (c5: 111.7 against 99.5 us per step)
   if (knob(g_merge) < 0) no_merge(a);
   if (a.mrg && sizeof(float) * (size_t)LdsM(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg).total >
-                   65536)
+                   kMaxLds)
     no_merge(a);
   const LdsM L(D, GH, a.chunk, a.page_shift, PAGED, Q8, a.mrg);
   return launch_pair(attn_mfma_kernel<D, GH, PAGED, ROPE, Q8>, kMfmaThreads,
