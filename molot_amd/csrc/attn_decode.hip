@@ -2820,6 +2820,22 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
         u32x4{pc[p][0], pc[p][1], pc[p][2], pc[p][3]};
 }
 
+// One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4, scalar
+// base + lane offset): lane l's 16 bytes land at LDS address lds + 16*l.
+// Written as inline assembly, so the compiler does not see an LDS store in
+// flight: with the builtin it put an s_waitcnt vmcnt(0) before the next LDS
+// reads it could not tell apart from the copy's destination (the transposed
+// V reads of the other tile buffer), which waited for the next tile's copies
+// halfway through every tile.  The kernel orders the copies itself
+// (wait_vmcnt, then a barrier, before a buffer is read).  m0 takes the LDS
+// address; one wait state after writing it.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(off), "s"(base)
+               : "memory", "m0");
+}
+
 // Waves per prefill workgroup (16 query rows each): 8, so that 128 rows
 // share each staged key tile and its split into pieces (32q/8kv/d128 fp32,
 // 2048-token prompt: 285 -> 237 us), except fp32 d = 256, whose 379
@@ -2965,10 +2981,8 @@ void prefill_mfma16_kernel(PfArgs a) {
       const char* rows = reinterpret_cast<const char*>(
           a.pieces + ((((int64_t)kv * a.nkv + h) * 3 + pc) * a.R + (tk - a.T0)) * D);
       const uint32_t lo = (uint32_t)(min(r, lastr) * (2 * D) + 16 * ch);
-      const char* src = rows + lo;
       char* dst = (kv ? vbuf : kbuf) + pc * KT * (2 * D) + kb * 1024;
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0,
-                                       0);
+      dma16(rows, lo, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)dst);
     }
   };
   typename KVT<T>::vec kreg[CPT], vreg[CPT];
