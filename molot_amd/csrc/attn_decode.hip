@@ -2828,12 +2828,13 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
 // V reads of the other tile buffer), which waited for the next tile's copies
 // halfway through every tile.  The kernel orders the copies itself
 // (wait_vmcnt, then a barrier, before a buffer is read).  m0 takes the LDS
-// address; one wait state after writing it.
+// address as an input operand (the compiler writes it); one wait state
+// between that write and the copy.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "s"(lds), "v"(off), "s"(base)
-               : "memory", "m0");
+               : "v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
 }
 
 // Waves per prefill workgroup (16 query rows each): 8, so that 128 rows
