@@ -2888,7 +2888,12 @@ void prefill_mfma16_kernel(PfArgs a) {
   // the barrier that follows its last use); 4 waves: one buffer, so that two
   // workgroups share a CU's LDS
   constexpr int NBUF = PW == 8 && 2 * KP * KT * (KRB + VRB) <= 160 * 1024 ? 2 : 1;
-  __shared__ __attribute__((aligned(16))) char kp_buf[NBUF][KP * KT * KRB];
+  // KKV (pieces from the workspace, one buffer of each): a second K buffer
+  // where it fits beside them, so that the next tile's K copies run under
+  // the whole tile and its V copies under the next tile's scores
+  constexpr bool KKV = PRE && NBUF == 1 && KP * KT * (2 * KRB + VRB) * (PW == 4 && D < 256 ? 2 : 1) <=
+                                              160 * 1024;
+  __shared__ __attribute__((aligned(16))) char kp_buf[KKV ? 2 : NBUF][KP * KT * KRB];
   __shared__ __attribute__((aligned(16))) char vp_buf[NBUF][KP * KT * VRB];
 
   const int G = a.nq / a.nkv;
@@ -2983,6 +2988,26 @@ void prefill_mfma16_kernel(PfArgs a) {
           a.pieces + ((((int64_t)kv * a.nkv + h) * 3 + pc) * a.R + (tk - a.T0)) * D);
       const uint32_t lo = (uint32_t)(min(r, lastr) * (2 * D) + 16 * ch);
       char* dst = (kv ? vbuf : kbuf) + pc * KT * (2 * D) + kb * 1024;
+      dma16(rows, lo, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)dst);
+    }
+  };
+  // K (kv = 0) or V (kv = 1) of a tile alone: NL copies a wave
+  constexpr int NL = 3 * (KT / (64 / (D / 8))) / PW;
+  auto dload1 = [&](int tk, char* buf, int kv) {
+    constexpr int UPR = D / 8, KPB = 64 / UPR, BPP = KT / KPB;
+    static_assert(!KKV || (3 * BPP) % PW == 0, "the same copies in every wave");
+    const int r_in = lane / UPR, jpos = lane % UPR;
+    const int lastr = kt_hi - 1 - tk;
+#pragma unroll
+    for (int bi0 = 0; bi0 < 3 * BPP; bi0 += PW) {
+      const int bi = bi0 + w;  // wave-uniform
+      const int pc = bi / BPP, kb = bi - pc * BPP;
+      const int r = kb * KPB + r_in;
+      const int ch = jpos ^ (kv ? vt_f<D>(r) : kt_f<D>(r));
+      const char* rows = reinterpret_cast<const char*>(
+          a.pieces + ((((int64_t)kv * a.nkv + h) * 3 + pc) * a.R + (tk - a.T0)) * D);
+      const uint32_t lo = (uint32_t)(min(r, lastr) * (2 * D) + 16 * ch);
+      char* dst = buf + pc * KT * (2 * D) + kb * 1024;
       dma16(rows, lo, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)dst);
     }
   };
@@ -3182,49 +3207,90 @@ void prefill_mfma16_kernel(PfArgs a) {
     }
   };
 
-  if constexpr (PRE) {
-    if (ntile > 0) dload(kt_s, kp_buf[0], vp_buf[0]);
-    wait_vmcnt<0>();  // this wave's direct loads are in LDS
-    __syncthreads();
-  } else {
-    if (ntile > 0) load_tile(kt_s);
-  }
-  for (int it = 0; it < ntile; ++it) {
-    const int tk = kt_s + it * KT;
-    const int bf = NBUF == 2 ? (it & 1) : 0;
-    const char* kp_s = kp_buf[bf];
-    const char* vp_s = vp_buf[bf];
-    if constexpr (PRE) {
-      // the other buffer was last read in the previous tile, which every
-      // wave finished before the barrier that ended it
-      if constexpr (NBUF == 2)
-        if (it + 1 < ntile) dload(tk + KT, kp_buf[bf ^ 1], vp_buf[bf ^ 1]);
-    } else {
-      store_tile(kp_buf[bf], vp_buf[bf]);
+  if constexpr (KKV) {
+    // Iteration it: the scores read K(it) while K(it+1) is copied into the
+    // other K buffer (last read by the scores of it-1, before the barrier
+    // that ended it-1); PV reads V(it), copied at the end of it-1 under the
+    // scores and softmax of it; V(it+1) is copied once every wave is past
+    // PV(it).  Each wave counts its own copies: NL for K or V of a tile.
+    if (ntile > 0) {
+      dload(kt_s, kp_buf[0], vp_buf[0]);
+      wait_vmcnt<0>();
       __syncthreads();
-      if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
     }
-    f32x4 sacc[KH];
-    scores(kp_s, sacc);
-    bf16x8_t ph, pm, pl;
-    float alpha, ps;
-    bool grow;
-    // interior tile: every row of the wave attends all of its keys
-    if (__builtin_amdgcn_ballot_w64(!(rv && tk >= rt0 && tk + KT <= rnn)) == 0)
-      softmax(std::true_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
-    else
-      softmax(std::false_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
-    rescale(alpha, grow, ps);
-    pv_acc(vp_s, ph, pm, pl);
-    if constexpr (PRE) {
-      if constexpr (NBUF == 1) {
-        __syncthreads();  // every wave is done with the buffer
-        if (it + 1 < ntile) dload(tk + KT, kp_buf[0], vp_buf[0]);
+    for (int it = 0; it < ntile; ++it) {
+      const int tk = kt_s + it * KT;
+      const bool more = it + 1 < ntile;
+      if (more) dload1(tk + KT, kp_buf[(it + 1) & 1], 0);
+      f32x4 sacc[KH];
+      scores(kp_buf[it & 1], sacc);
+      bf16x8_t ph, pm, pl;
+      float alpha, ps;
+      bool grow;
+      if (__builtin_amdgcn_ballot_w64(!(rv && tk >= rt0 && tk + KT <= rnn)) == 0)
+        softmax(std::true_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+      else
+        softmax(std::false_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+      rescale(alpha, grow, ps);
+      // V(it) is in LDS (K(it+1), copied after it, may still be in flight)
+      if (more)
+        wait_vmcnt<NL>();
+      else
+        wait_vmcnt<0>();
+      lds_barrier();
+      pv_acc(vp_buf[0], ph, pm, pl);
+      if (more) {
+        lds_barrier();  // every wave is past PV(it)
+        dload1(tk + KT, vp_buf[0], 1);
+        wait_vmcnt<NL>();  // K(it+1) is in LDS (V(it+1) may still be in flight)
+        lds_barrier();
       }
-      wait_vmcnt<0>();  // this wave's direct loads of the next tile are in LDS
+    }
+  } else {
+    if constexpr (PRE) {
+      if (ntile > 0) dload(kt_s, kp_buf[0], vp_buf[0]);
+      wait_vmcnt<0>();  // this wave's direct loads are in LDS
       __syncthreads();
     } else {
-      if constexpr (NBUF == 1) __syncthreads();  // the tile's LDS is rewritten next
+      if (ntile > 0) load_tile(kt_s);
+    }
+    for (int it = 0; it < ntile; ++it) {
+      const int tk = kt_s + it * KT;
+      const int bf = NBUF == 2 ? (it & 1) : 0;
+      const char* kp_s = kp_buf[bf];
+      const char* vp_s = vp_buf[bf];
+      if constexpr (PRE) {
+        // the other buffer was last read in the previous tile, which every
+        // wave finished before the barrier that ended it
+        if constexpr (NBUF == 2)
+          if (it + 1 < ntile) dload(tk + KT, kp_buf[bf ^ 1], vp_buf[bf ^ 1]);
+      } else {
+        store_tile(kp_buf[bf], vp_buf[bf]);
+        __syncthreads();
+        if (it + 1 < ntile) load_tile(tk + KT);  // in flight while this tile is used
+      }
+      f32x4 sacc[KH];
+      scores(kp_s, sacc);
+      bf16x8_t ph, pm, pl;
+      float alpha, ps;
+      bool grow;
+      // interior tile: every row of the wave attends all of its keys
+      if (__builtin_amdgcn_ballot_w64(!(rv && tk >= rt0 && tk + KT <= rnn)) == 0)
+        softmax(std::true_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+      else
+        softmax(std::false_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+      rescale(alpha, grow, ps);
+      pv_acc(vp_s, ph, pm, pl);
+      if constexpr (PRE) {
+        if constexpr (NBUF == 1) {
+          __syncthreads();  // every wave is done with the buffer
+          if (it + 1 < ntile) dload(tk + KT, kp_buf[0], vp_buf[0]);
+        }
+        wait_vmcnt<0>();  // this wave's direct loads of the next tile are in LDS
+        __syncthreads();
+      } else {
+        if constexpr (NBUF == 1) __syncthreads();  // the tile's LDS is rewritten next
+      }
     }
   }
   l_run = sum_xor32(sum_xor16(l_run));
