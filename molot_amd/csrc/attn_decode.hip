@@ -2730,7 +2730,7 @@ struct PfArgs {
   const void* v;
   float* o;        // [M][nq][D]
   const int32_t* block_table;  // paged: the sequence's row of block ids
-  int nq, nkv, M, N, pos0, window, nqb;  // nqb: blocks of 16 * pf_waves query rows per KV head
+  int nq, nkv, M, N, pos0, window, nqb;  // nqb: blocks of 16 * (waves) query rows per KV head
   int dh;  // head dim as stored (< D: the launch runs padded to D, through the pieces)
   int page_shift;
   float scale;
@@ -2839,11 +2839,12 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
 
 // Waves per prefill workgroup (16 query rows each): 8, so that 128 rows
 // share each staged key tile and its split into pieces (32q/8kv/d128 fp32,
-// 2048-token prompt: 285 -> 237 us), except fp32 d = 256, whose 379
-// registers a lane leave room for 4 waves a CU.  A launch whose 8-wave grid
-// would leave CUs idle takes 4 waves (512-token prompt after 16384 cached
-// tokens: 1452 us on 8 waves, 1414 on 4).
-__host__ __device__ constexpr int pf_waves(int D, int esz) { return D == 256 && esz == 4 ? 4 : 8; }
+// 2048-token prompt: 285 -> 237 us).  fp32 pieces at d = 256 too (two
+// waves a SIMD in 256 registers; 2048-token Gemma-style prompt: 127 ->
+// 104 us, its grid then split over the keys).  A launch whose 8-wave grid
+// would leave CUs idle and cannot be split takes 4 waves (512-token prompt
+// after 16384 cached tokens: 1452 us on 8 waves, 1414 on 4).
+constexpr int kPfWaves = 8;
 
 // The kernel: every fp32 product is taken as bf16 pieces on
 // v_mfma_f32_16x16x32_bf16 (16x the fp32 matrix rate).  x = hi + mid + lo
@@ -3489,7 +3490,8 @@ __global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs
   if (nch <= 1) return;  // uniform over the workgroup
   const bool live = lane < nch;
   const float M = wave_reduce<true>(live ? mc : -INFINITY);
-  const float wc = live ? softmax_exp(mc - M) : 0.f;
+  // a slot whose chunks all saw no key (max -inf) gets O = 0, as in combine_kernel
+  const float wc = live && M != -INFINITY ? softmax_exp(mc - M) : 0.f;
   const float L = wave_reduce<false>(live ? wc * lc : 0.f);
   float acc = 0.f;
 #pragma unroll
@@ -3499,7 +3501,7 @@ __global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs
   const int h = y / a.nsub, sub = y - h * a.nsub;
   const int64_t oi = out_index((int64_t)b * a.nq + h * G + sub * a.gh, pair, a.d, a.dh);
   if (oi >= 0) {
-    a.o[oi] = acc / L;
+    a.o[oi] = L > 0.f ? acc / L : 0.f;
     if (a.rope && a.q_out) a.q_out[oi] = a.qrot[(int64_t)slot * P + pair];
   }
 }
@@ -4210,8 +4212,7 @@ std::atomic<int> g_presplit{1};  // molot_hip_set_prefill_presplit
 
 template <int D, typename T, bool PAGED>
 PfFn pf_kernel_w(int pw) {
-  if constexpr (pf_waves(D, sizeof(T)) == 8)
-    if (pw == 8) return prefill_mfma16_kernel<D, T, PAGED, 8>;
+  if (pw == 8) return prefill_mfma16_kernel<D, T, PAGED, 8>;
   return prefill_mfma16_kernel<D, T, PAGED, 4>;
 }
 
@@ -4229,7 +4230,8 @@ PfFn pf_kernel_pre(int d, int pw) {
                               : prefill_mfma16_kernel<64, float, false, 4, true>;
   if (d == 128) return pw == 8 ? prefill_mfma16_kernel<128, float, false, 8, true>
                                : prefill_mfma16_kernel<128, float, false, 4, true>;
-  return prefill_mfma16_kernel<256, float, false, 4, true>;
+  return pw == 8 ? prefill_mfma16_kernel<256, float, false, 8, true>
+                 : prefill_mfma16_kernel<256, float, false, 4, true>;
 }
 
 using SplitFn = void (*)(PfArgs, uint16_t*);
@@ -4830,9 +4832,8 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     return prefill_rows(Qm, K, V, Om, nq, nkv, M, N, d, scale, pos0, window, kv_dtype, block_row,
                         page, stream);
   const int64_t rows = (int64_t)M * (nq / nkv);
-  const int esz = kv_dtype == MOLOT_KV_F32 ? 4 : kv_dtype == MOLOT_KV_BF16 ? 2 : 1;
   auto nqb_of = [&](int w) { return (rows + 16 * w - 1) / (16 * w); };
-  int pw = pf_waves(D, pieces_only ? 4 : esz);  // pieces_only: the fp32-piece kernel's waves
+  int pw = kPfWaves;
   int64_t nqb = nqb_of(pw);
   // A grid of fewer workgroups than CUs (few query rows over a long cache,
   // e.g. a prompt chunk after a long context) splits each query block's key
@@ -4935,8 +4936,17 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   cb.nchunks = nsplit;
   cb.chunk = 1;
   cb.pairs = comb_pairs(nsplit);
-  const dim3 cgrid((unsigned)(D / cb.pairs), (unsigned)((int64_t)M * nq));
-  const size_t clds = sizeof(float) * (size_t)comb_lds_floats(nsplit);
+  // at most 8 splits: the wave combine, one wave per 64 outputs of a slot
+  // (2048 tokens x 8 q heads at d = 256 over 2 splits: 82 us on
+  // combine_kernel's 4 workgroups a slot); more splits: combine_kernel
+  using CombFn = void (*)(CombArgs);
+  const bool cwave = nsplit <= 8;
+  const CombFn ck = nsplit <= 4 ? combine_wave_kernel<4> : cwave ? combine_wave_kernel<8> : combine_kernel;
+  const int wthreads = D % 256 == 0 ? 256 : (D % 128 == 0 ? 128 : 64);
+  const dim3 cgrid = cwave ? dim3((unsigned)(D / wthreads), (unsigned)((int64_t)M * nq))
+                           : dim3((unsigned)(D / cb.pairs), (unsigned)((int64_t)M * nq));
+  const dim3 cblock = cwave ? dim3((unsigned)wthreads) : dim3(kCombThreads);
+  const size_t clds = cwave ? 0 : sizeof(float) * (size_t)comb_lds_floats(nsplit);
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {
     ProfRec pr{prof_event(), prof_event(), nullptr, nullptr, nsplit > 1};
@@ -4945,8 +4955,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     if (!st && nsplit > 1) {
       pr.c0 = prof_event();
       pr.c1 = prof_event();
-      hipExtLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), clds, (hipStream_t)stream,
-                            pr.c0, pr.c1, 0, cb);
+      hipExtLaunchKernelGGL(ck, cgrid, cblock, clds, (hipStream_t)stream, pr.c0, pr.c1, 0, cb);
       st = (int)hipGetLastError();
     }
     g_prof.push_back(pr);
@@ -4955,7 +4964,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   hipLaunchKernelGGL(pk, grid, dim3(pf_threads), 0, (hipStream_t)stream, a);
   st = (int)hipGetLastError();
   if (st || nsplit == 1) return st;
-  hipLaunchKernelGGL(combine_kernel, cgrid, dim3(kCombThreads), clds, (hipStream_t)stream, cb);
+  hipLaunchKernelGGL(ck, cgrid, cblock, clds, (hipStream_t)stream, cb);
   return (int)hipGetLastError();
 }
 
