@@ -226,7 +226,7 @@ def _prefill_both(run):
 
 @pytest.mark.parametrize("nq,nkv,d,M,N,pos0,window,kv", [
     (32, 8, 128, 300, 1300, 1000, 0, "f32"),    # 8 waves, two tile buffers
-    (8, 4, 256, 70, 3070, 3000, 1024, "f32"),   # fp32 d256: 4 waves, one buffer, window
+    (8, 4, 256, 70, 3070, 3000, 1024, "f32"),   # fp32 d256: two K buffers and one V, window
     (32, 2, 64, 40, 90, 50, 0, "f32"),          # d64
     (8, 2, 128, 5, 40, 35, 0, "f32"),           # few rows: the 4-wave grid
     (8, 4, 256, 33, 233, 200, 37, "f32"),       # window cutting inside a tile
