@@ -56,7 +56,8 @@ def run(entry, p):
 @pytest.mark.parametrize("first,second", [
     ((32, 8, 128, 16384, 0, False), (32, 8, 128, 3000, 0, False)),
     ((64, 8, 128, 20000, 0, True), (8, 4, 256, 5000, 700, False)),
-], ids=["c2_then_short", "c5_bf16_then_c3_window"])
+    ((8, 2, 512, 12000, 0, False), (8, 8, 512, 900, 300, False)),
+], ids=["c2_then_short", "c5_bf16_then_c3_window", "d512_then_window"])
 def test_noalloc_matches_decode_step(gpu, first, second):
     for i, (nq, nkv, d, pos, window, bf16) in enumerate((first, second)):
         announce(f"noalloc call {i}: nq={nq} nkv={nkv} d={d} pos={pos} window={window} bf16={bf16}")
