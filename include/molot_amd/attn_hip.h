@@ -128,9 +128,11 @@ int molot_hip_attn_decode_head_win(const float* Q, const void* K, const void* V,
                                    int kv_dtype, void* stream);
 
 /* General strided form behind all of the above: row t of KV head h at
- * element offset t*tok_stride + h*head_stride.  Q8: the token-major Q8
- * layout only, tok_stride = molot_hip_q8_row_bytes(nkv, d) and
- * head_stride = d (bytes). */
+ * element offset t*tok_stride + h*head_stride.  At d = 64, 128, 256 and 512
+ * the strides keep every row 16-byte aligned (16-byte loads); at other
+ * head dims they are even (two-element loads); K, V, Q and O 16-byte
+ * aligned (MOLOT_EINVAL otherwise).  Q8: the token-major Q8 layout only,
+ * tok_stride = molot_hip_q8_row_bytes(nkv, d) and head_stride = d (bytes). */
 int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, float* O, int nq,
                                   int nkv, int n, int d, int64_t tok_stride, int64_t head_stride,
                                   float scale, int pos_cur, int window, int kv_dtype,

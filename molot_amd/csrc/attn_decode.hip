@@ -4435,10 +4435,15 @@ int molot_hip_attn_decode_strided(const float* Q, const void* K, const void* V, 
   if (n_att <= 0) return zero_out(O, (int64_t)nq * d, (hipStream_t)stream);  // o = 0
   if (!K || !V) return MOLOT_EINVAL;
   const int esz = kv_esz(kv_dtype);
-  // 16-byte vector loads of every row; a Q8 cache has the fixed layout
-  // checked above, whose head dims off 64/128/256/512 load 4-byte pieces
-  if (!aligned16(K) || !aligned16(V) || !aligned16(Q) || !aligned16(O) ||
-      (kv_dtype != MOLOT_KV_Q8 && ((tok_stride * esz) % 16 || (head_stride * esz) % 16)))
+  // Rows the kernels can load: at the kernels' head dims (64, 128, 256,
+  // 512) 16-byte vectors, so 16-byte aligned row starts; at a padded head
+  // dim two-element pieces, so even strides.  A Q8 cache has the fixed
+  // layout checked above, whose padded head dims load 4-code pieces.
+  const bool padded = d != 64 && d != 128 && d != 256 && d != 512;
+  const bool rows_ok = kv_dtype == MOLOT_KV_Q8 ||
+                       (padded ? tok_stride % 2 == 0 && head_stride % 2 == 0
+                               : (tok_stride * esz) % 16 == 0 && (head_stride * esz) % 16 == 0);
+  if (!aligned16(K) || !aligned16(V) || !aligned16(Q) || !aligned16(O) || !rows_ok)
     return MOLOT_EINVAL;
   AttnArgs a{};
   a.q = Q;

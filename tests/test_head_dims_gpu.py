@@ -120,7 +120,7 @@ def test_decode_step_norms_head_dims(gpu, d, bf16):
     assert normwise_err(O, oO) < FP32_TOL
 
 
-@pytest.mark.parametrize("d", [72, 112])
+@pytest.mark.parametrize("d", [72, 112, 66, 34])
 def test_attention_entries_head_dims(gpu, d):
     """attn_decode_gqa_cache (token-major) and attn_decode_gqa (head-major)."""
     announce(f"attention-only entries d={d}")
@@ -138,6 +138,30 @@ def test_attention_entries_head_dims(gpu, d):
     Vh = np.ascontiguousarray(V.reshape(n, nkv, d).transpose(1, 0, 2))
     O2 = torch.empty((nq, d), device="cuda")
     attn.attn_decode_gqa(dev(Q), dev(Kh), dev(Vh), O2, nq, nkv, n, d, s)
+    assert normwise_err(host(O2), ref) < FP32_TOL
+
+
+@pytest.mark.parametrize("d", [34, 66, 96])
+def test_attention_entries_head_dims_bf16(gpu, d):
+    """The attention-only entries over bf16 caches at padded head dims,
+    d % 4 == 2 included (4-byte rows of two elements): against the oracle on
+    the bf16 values, token-major and head-major."""
+    announce(f"attention-only entries bf16 d={d}")
+    st = Stream(60 + d)
+    nq, nkv, n = 8, 2, 1500
+    Q = st.normal((nq, d))
+    Kb = f32_to_bf16(st.normal((n, nkv * d)))
+    Vb = f32_to_bf16(st.normal((n, nkv * d)))
+    K, V = bf16_to_f32(Kb), bf16_to_f32(Vb)
+    s = 1.0 / math.sqrt(d)
+    ref = oracle.attn_decode_gqa_cache(Q, K, V, nq, nkv, n, d, s, n - 1, 300)
+    O = torch.empty((nq, d), device="cuda")
+    attn.attn_decode_gqa_cache(dev(Q), dev_bf16(Kb), dev_bf16(Vb), O, nq, nkv, n, d, s, n - 1, 300)
+    assert normwise_err(host(O), ref) < FP32_TOL
+    Kh = np.ascontiguousarray(Kb.reshape(n, nkv, d).transpose(1, 0, 2))
+    Vh = np.ascontiguousarray(Vb.reshape(n, nkv, d).transpose(1, 0, 2))
+    O2 = torch.empty((nq, d), device="cuda")
+    attn.attn_decode_gqa_win(dev(Q), dev_bf16(Kh), dev_bf16(Vh), O2, nq, nkv, n, d, s, n - 1, 300)
     assert normwise_err(host(O2), ref) < FP32_TOL
 
 
