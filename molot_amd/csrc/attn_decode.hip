@@ -3088,32 +3088,49 @@ void prefill_mfma16_kernel(PfArgs a) {
   // scores of the two 16-key halves of the tile at kp_s, smallest piece
   // products first; even and odd 32-element steps into separate
   // accumulators (four independent MFMA chains, added at the end)
+  // piece products in the order they enter an accumulator, smallest first:
+  // (K or V piece, q or P piece: 0 hi, 1 mid, 2 lo)
+  constexpr int NPR = KP == 3 ? 6 : 3;
+  // 32-element steps whose operands are read together, and 16-row V blocks
+  // (d = 256: fewer, to stay in 256 registers)
+  constexpr int SJ = D == 256 ? 1 : 2;
+  constexpr int NDT = D == 256 ? 2 : (DT >= 4 ? 4 : DT);
+  constexpr int PRK[6] = {KP == 3 ? 1 : 0, KP == 3 ? 2 : 0, 0, 1, 0, 0};
+  constexpr int PRQ[6] = {KP == 3 ? 1 : 2, KP == 3 ? 0 : 1, KP == 3 ? 2 : 0, 0, 1, 0};
+  // scores of the two 16-key halves of the tile at kp_s.  SJ 32-element
+  // steps at a time: their staged K operands (both halves, every piece) are
+  // read first, then the piece products go out piece by piece across the
+  // accumulators (even and odd steps of each half), so that consecutive
+  // matrix instructions are independent; each accumulator takes its
+  // products in the same order as one at a time.  The two step parities are
+  // added at the end.
   auto scores = [&](const char* kp_s, f32x4 (&sacc)[KH]) {
     f32x4 sacc2[KH][2];
 #pragma unroll
     for (int u = 0; u < KH; ++u) sacc2[u][0] = sacc2[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < QS; ++s)
+    for (int s0 = 0; s0 < QS; s0 += SJ) {
+      bf16x8_t kk[SJ][KH][KP];
 #pragma unroll
-      for (int u = 0; u < KH; ++u) {
-        const char* kb = kp_s + kt_off<D>(16 * u + c16, 4 * s + g4);
-        const bf16x8_t k0 = *reinterpret_cast<const bf16x8_t*>(kb);
-        f32x4& acc = sacc2[u][s & 1];
-        if constexpr (KP == 3) {
-          const bf16x8_t k1 = *reinterpret_cast<const bf16x8_t*>(kb + KT * KRB);
-          const bf16x8_t k2 = *reinterpret_cast<const bf16x8_t*>(kb + 2 * KT * KRB);
-          acc = mfma_bf16(k1, qm[s], acc);
-          acc = mfma_bf16(k2, qh[s], acc);
-          acc = mfma_bf16(k0, ql[s], acc);
-          acc = mfma_bf16(k1, qh[s], acc);
-          acc = mfma_bf16(k0, qm[s], acc);
-          acc = mfma_bf16(k0, qh[s], acc);
-        } else {
-          acc = mfma_bf16(k0, ql[s], acc);
-          acc = mfma_bf16(k0, qm[s], acc);
-          acc = mfma_bf16(k0, qh[s], acc);
+      for (int j = 0; j < SJ; ++j)
+#pragma unroll
+        for (int u = 0; u < KH; ++u) {
+          const char* kb = kp_s + kt_off<D>(16 * u + c16, 4 * (s0 + j) + g4);
+#pragma unroll
+          for (int p = 0; p < KP; ++p)
+            kk[j][u][p] = *reinterpret_cast<const bf16x8_t*>(kb + p * KT * KRB);
         }
-      }
+#pragma unroll
+      for (int t = 0; t < NPR; ++t)
+#pragma unroll
+        for (int j = 0; j < SJ; ++j)
+#pragma unroll
+          for (int u = 0; u < KH; ++u) {
+            const bf16x8_t& qp = PRQ[t] == 0 ? qh[s0 + j] : PRQ[t] == 1 ? qm[s0 + j] : ql[s0 + j];
+            f32x4& acc = sacc2[u][(s0 + j) & 1];
+            acc = mfma_bf16(kk[j][u][PRK[t]], qp, acc);
+          }
+    }
 #pragma unroll
     for (int u = 0; u < KH; ++u) sacc[u] = sacc2[u][0] + sacc2[u][1];
   };
@@ -3161,38 +3178,37 @@ void prefill_mfma16_kernel(PfArgs a) {
     pl = __builtin_bit_cast(bf16x8_t, u32x4{pl4[0], pl4[1], pl4[2], pl4[3]});
   };
   // o += P V over the tile at vp_s: V^T of the 16-row block dt by two
-  // transposed reads per piece
+  // transposed reads per piece, NDT blocks at a time: their operands first,
+  // then the piece products piece by piece across the NDT accumulators
+  // (each in the same order as one block at a time)
   auto pv_acc = [&](const char* vp_s, const bf16x8_t& ph, const bf16x8_t& pm,
                     const bf16x8_t& pl) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      bf16x8_t av[KP];
+    for (int dt0 = 0; dt0 < DT; dt0 += NDT) {
+      bf16x8_t av[NDT][KP];
 #pragma unroll
-      for (int p = 0; p < KP; ++p) {
-        i16x4_t t2[2];
+      for (int j = 0; j < NDT; ++j)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int r = (lane >> 2) + 16 * u;
-          t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) i16x4_t*)(
-                  vp_s + p * KT * VRB + vt_off<D>(r, 2 * dt + ((lane & 3) >> 1)) +
-                  8 * (lane & 1)));
+        for (int p = 0; p < KP; ++p) {
+          i16x4_t t2[2];
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int r = (lane >> 2) + 16 * u;
+            t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4_t*)(
+                    vp_s + p * KT * VRB + vt_off<D>(r, 2 * (dt0 + j) + ((lane & 3) >> 1)) +
+                    8 * (lane & 1)));
+          }
+          av[j][p] = __builtin_bit_cast(
+              bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
         }
-        av[p] = __builtin_bit_cast(
-            bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
-      }
-      if constexpr (KP == 3) {
-        o[dt] = mfma_bf16(av[1], pm, o[dt]);
-        o[dt] = mfma_bf16(av[2], ph, o[dt]);
-        o[dt] = mfma_bf16(av[0], pl, o[dt]);
-        o[dt] = mfma_bf16(av[1], ph, o[dt]);
-        o[dt] = mfma_bf16(av[0], pm, o[dt]);
-        o[dt] = mfma_bf16(av[0], ph, o[dt]);
-      } else {
-        o[dt] = mfma_bf16(av[0], pl, o[dt]);
-        o[dt] = mfma_bf16(av[0], pm, o[dt]);
-        o[dt] = mfma_bf16(av[0], ph, o[dt]);
-      }
+#pragma unroll
+      for (int t = 0; t < NPR; ++t)
+#pragma unroll
+        for (int j = 0; j < NDT; ++j) {
+          const bf16x8_t& pp = PRQ[t] == 0 ? ph : PRQ[t] == 1 ? pm : pl;
+          o[dt0 + j] = mfma_bf16(av[j][PRK[t]], pp, o[dt0 + j]);
+        }
     }
   };
   // o and l take alpha, then l the tile's sum (two roundings, as the
