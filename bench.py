@@ -126,6 +126,10 @@ CONFIGS = {
     # a gemma4 global layer (model.h:562-564): head dim 512, 8q/2kv, 32k context
     "c6": dict(nq=8, nkv=2, d=512, pos=32768, theta=1000000.0, window=0, kvd=0, sigma=1.0),
     "c6q8": dict(nq=8, nkv=2, d=512, pos=32768, theta=1000000.0, window=0, kvd=2, sigma=1.0),
+    # gemma4's two layer kinds over bf16 caches (a 256-wide sliding-window layer, a 512-wide
+    # global one)
+    "c3bf16": dict(nq=8, nkv=4, d=256, pos=32768, theta=10000.0, window=1024, kvd=1, sigma=1.0),
+    "c6bf16": dict(nq=8, nkv=2, d=512, pos=32768, theta=1000000.0, window=0, kvd=1, sigma=1.0),
     "c4q8": dict(nq=32, nkv=8, d=128, theta=500000.0, window=0, kvd=2, sigma=1.0, batch=64,
                  lmin=512, lmax=8192, page=16),
     # prefill (gemm.h:409-446, forward.h:367-399): M prompt tokens after n0 cached
@@ -152,6 +156,9 @@ DESCR = {
     "c3q8": "sliding-window GQA decode layer-step, 8q/4kv/d256 Q8 KV, pos 32768, window 1024",
     "c6": "gemma4 global-layer decode step, 8q/2kv/d512 fp32 KV, ctx 32768 (n=32769), batch 1",
     "c6q8": "gemma4 global-layer decode step, 8q/2kv/d512 Q8 KV, ctx 32768 (n=32769), batch 1",
+    "c3bf16": "sliding-window GQA decode layer-step, 8q/4kv/d256 bf16 KV, pos 32768, window 1024",
+    "c6bf16": "gemma4 global-layer decode step, 8q/2kv/d512 bf16 KV, ctx 32768 (n=32769), "
+              "batch 1",
     "c4q8": "continuous-batching decode step, 64 sequences of ctx U[512,8192], 32q/8kv/d128, "
             "Q8 KV in shuffled 16-token pages",
     "p1": "layer prefill (RoPE + append + causal attention), 2048-token prompt, 32q/8kv/d128 "
