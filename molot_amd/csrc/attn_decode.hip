@@ -504,24 +504,42 @@ __global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeAr
   __syncthreads();
   const float vinv = a.append && a.v_norm ? sh[0] : 1.f;
   const int nk = (half + 63) / 64;  // pair groups of 64 per head
-  for (int hh = w; hh < a.nq + a.nkv; hh += kRopeTokThreads / 64) {
-    if (hh < a.nq) {
-      if (!a.q) continue;
-      float* x = a.q + ((int64_t)b * a.nq + hh) * a.d;
-      float x0[KMAX], x1[KMAX];
-      float ss = 0.f;
-      #pragma unroll
+  // Each wave walks its heads with the next head's rows loaded before the
+  // current head's stores go out (heads own disjoint rows), so a wave waits
+  // for one load latency in all rather than one per head.
+  auto load_q = [&](int hh, float* y0, float* y1) {
+    const float* x = a.q + ((int64_t)b * a.nq + hh) * a.d;
+#pragma unroll
     for (int k = 0; k < KMAX; ++k) {
       if (k >= nk) break;
-        const int j = lane + 64 * k;
-        x0[k] = j < half ? x[j] : 0.f;
-        x1[k] = j < half ? x[j + half] : 0.f;
-        if (a.q_norm) ss += group_sum<64>(x0[k] * x0[k] + x1[k] * x1[k]);
+      const int j = lane + 64 * k;
+      y0[k] = j < half ? x[j] : 0.f;
+      y1[k] = j < half ? x[j + half] : 0.f;
+    }
+  };
+  if (a.q) {
+    float x0[KMAX], x1[KMAX], n0[KMAX] = {}, n1[KMAX] = {};
+    if (w < a.nq) load_q(w, n0, n1);
+    for (int hh = w; hh < a.nq; hh += kRopeTokThreads / 64) {
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        x0[k] = n0[k];
+        x1[k] = n1[k];
+      }
+      if (hh + kRopeTokThreads / 64 < a.nq) load_q(hh + kRopeTokThreads / 64, n0, n1);
+      float* x = a.q + ((int64_t)b * a.nq + hh) * a.d;
+      float ss = 0.f;
+      if (a.q_norm) {
+#pragma unroll
+        for (int k = 0; k < KMAX; ++k) {
+          if (k >= nk) break;
+          ss += group_sum<64>(x0[k] * x0[k] + x1[k] * x1[k]);
+        }
       }
       const float inv = a.q_norm ? rms_inv(ss, a.d) : 1.f;
-      #pragma unroll
-    for (int k = 0; k < KMAX; ++k) {
-      if (k >= nk) break;
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        if (k >= nk) break;
         const int j = lane + 64 * k;
         if (j >= half) continue;
         float y0 = x0[k], y1 = x1[k];
@@ -532,27 +550,48 @@ __global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeAr
         x[j] = rot ? y0 * cs_s[j] - y1 * sn_s[j] : y0;
         x[j + half] = rot ? y0 * sn_s[j] + y1 * cs_s[j] : y1;
       }
-      continue;
     }
-    if (!a.append) continue;
-    const int kh = hh - a.nq;
+  }
+  if (!a.append) return;
+  // KV heads: wave w takes heads kh with (nq + kh) % 4 == w
+  auto load_kv = [&](int kh, float* k0, float* k1, float* v0, float* v1) {
     const float* kx = a.k_new + ((int64_t)b * a.nkv + kh) * a.d;
     const float* vx = a.v_new + ((int64_t)b * a.nkv + kh) * a.d;
-    float r0[KMAX], r1[KMAX], v0[KMAX], v1[KMAX];
-    float ss = 0.f;
-    #pragma unroll
+#pragma unroll
     for (int k = 0; k < KMAX; ++k) {
       if (k >= nk) break;
       const int j = lane + 64 * k;
-      r0[k] = j < half ? kx[j] : 0.f;
-      r1[k] = j < half ? kx[j + half] : 0.f;
-      v0[k] = j < half ? vx[j] * vinv : 0.f;
-      v1[k] = j < half ? vx[j + half] * vinv : 0.f;
-      if (a.k_norm) ss += group_sum<64>(r0[k] * r0[k] + r1[k] * r1[k]);
+      k0[k] = j < half ? kx[j] : 0.f;
+      k1[k] = j < half ? kx[j + half] : 0.f;
+      v0[k] = j < half ? vx[j] : 0.f;
+      v1[k] = j < half ? vx[j + half] : 0.f;
+    }
+  };
+  constexpr int kWaves = kRopeTokThreads / 64;
+  const int kh0 = ((w - a.nq) % kWaves + kWaves) % kWaves;
+  float nk0[KMAX] = {}, nk1[KMAX] = {}, nv0[KMAX] = {}, nv1[KMAX] = {};
+  if (kh0 < a.nkv) load_kv(kh0, nk0, nk1, nv0, nv1);
+  for (int kh = kh0; kh < a.nkv; kh += kWaves) {
+    float r0[KMAX], r1[KMAX], v0[KMAX], v1[KMAX];
+#pragma unroll
+    for (int k = 0; k < KMAX; ++k) {
+      r0[k] = nk0[k];
+      r1[k] = nk1[k];
+      v0[k] = nv0[k] * vinv;
+      v1[k] = nv1[k] * vinv;
+    }
+    if (kh + kWaves < a.nkv) load_kv(kh + kWaves, nk0, nk1, nv0, nv1);
+    float ss = 0.f;
+    if (a.k_norm) {
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        if (k >= nk) break;
+        ss += group_sum<64>(r0[k] * r0[k] + r1[k] * r1[k]);
+      }
     }
     const float kinv = a.k_norm ? rms_inv(ss, a.d) : 1.f;
     float kmax = 0.f, vmax = 0.f;
-    #pragma unroll
+#pragma unroll
     for (int k = 0; k < KMAX; ++k) {
       if (k >= nk) break;
       const int j = lane + 64 * k;
