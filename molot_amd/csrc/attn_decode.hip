@@ -3566,6 +3566,78 @@ __global__ __launch_bounds__(kCombWaveThreads) void combine_wave_kernel(CombArgs
   }
 }
 
+// The prefill's key-split merge: slot s = (token, q head) of one head, P = D
+// partial outputs over R >= nchunks splits.  A wave takes 64V consecutive
+// outputs of one slot (V = 4 at D % 256 == 0, 2 at D % 128 == 0, else 1), so
+// a 2048-token prompt of 8 q heads at d = 256 runs 16384 waves instead of
+// 65536; the arithmetic and its order are combine_wave_kernel's (lane c
+// holds split c's (m, l), DPP reductions give M and L, the weights reach
+// every lane by readlane), so the outputs are the same bits.  Four waves a
+// workgroup, consecutive units (slot, 64V-span); units past the last exit.
+template <int V>
+__device__ __forceinline__ void load_v(const float* p, float* x) {
+  if constexpr (V == 4) {
+    const f32x4 t = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = t[e];
+  } else if constexpr (V == 2) {
+    const f32x2 t = *reinterpret_cast<const f32x2*>(p);
+    x[0] = t[0];
+    x[1] = t[1];
+  } else {
+    x[0] = *p;
+  }
+}
+template <int R, int V>
+__global__ __launch_bounds__(kCombWaveThreads) void combine_rows_kernel(CombArgs a, int64_t units) {
+  const int D = a.d;
+  const int spans = D / (64 * V);
+  const int64_t unit = (int64_t)blockIdx.x * (kCombWaveThreads / 64) + (threadIdx.x >> 6);
+  if (unit >= units) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int64_t slot = unit / spans;
+  const int pair = (int)(unit - slot * spans) * 64 * V + V * lane;
+  const float* po = a.part_o + slot * a.nchunks * D + pair;
+  const float* pml = a.part_ml + slot * a.nchunks * 2;
+  float ov[R][V];
+#pragma unroll
+  for (int u = 0; u < R; ++u) load_v<V>(po + (int64_t)min(u, a.nchunks - 1) * D, ov[u]);
+  const int cl = min(lane, a.nchunks - 1);
+  const f32x2 ml = *reinterpret_cast<const f32x2*>(pml + 2 * cl);
+  const int nch = a.nchunks;
+  const bool live = lane < nch;
+  const float M = wave_reduce<true>(live ? ml[0] : -INFINITY);
+  const float wc = live && M != -INFINITY ? softmax_exp(ml[0] - M) : 0.f;
+  const float L = wave_reduce<false>(live ? wc * ml[1] : 0.f);
+  float acc[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc[e] = 0.f;
+#pragma unroll
+  for (int u = 0; u < R; ++u)
+    if (u < nch) {
+      const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wc), u));
+#pragma unroll
+      for (int e = 0; e < V; ++e) acc[e] = fmaf(wu, ov[u][e], acc[e]);
+    }
+  float o[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) o[e] = L > 0.f ? acc[e] / L : 0.f;
+  if (a.dh == D) {
+    float* dst = a.o + slot * D + pair;
+    if constexpr (V == 4) {
+      *reinterpret_cast<f32x4*>(dst) = f32x4{o[0], o[1], o[2], o[3]};
+    } else if constexpr (V == 2) {
+      *reinterpret_cast<f32x2*>(dst) = f32x2{o[0], o[1]};
+    } else {
+      *dst = o[0];
+    }
+  } else {  // a padded launch: the stored head dim's outputs only
+#pragma unroll
+    for (int e = 0; e < V; ++e)
+      if (pair + e < a.dh) a.o[slot * a.dh + pair + e] = o[e];
+  }
+}
+
 __global__ void vexp_kernel(const float* x, float* y, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) y[i] = softmax_exp(x[i]);
@@ -5001,16 +5073,21 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   cb.nchunks = nsplit;
   cb.chunk = 1;
   cb.pairs = comb_pairs(nsplit);
-  // at most 8 splits: the wave combine, one wave per 64 outputs of a slot
-  // (2048 tokens x 8 q heads at d = 256 over 2 splits: 82 us on
+  // at most 8 splits: the row merge, one wave per 64V outputs of a slot
+  // (2048 tokens x 8 q heads at d = 256 over 4 splits: 9.2 us, against 22.2
+  // with a wave per 64 outputs and, over 2 splits, 82 us on
   // combine_kernel's 4 workgroups a slot); more splits: combine_kernel
-  using CombFn = void (*)(CombArgs);
   const bool cwave = nsplit <= 8;
-  const CombFn ck = nsplit <= 4 ? combine_wave_kernel<4> : cwave ? combine_wave_kernel<8> : combine_kernel;
-  const int wthreads = D % 256 == 0 ? 256 : (D % 128 == 0 ? 128 : 64);
-  const dim3 cgrid = cwave ? dim3((unsigned)((int64_t)M * nq), (unsigned)(D / wthreads))
+  const int cv = D % 256 == 0 ? 4 : (D % 128 == 0 ? 2 : 1);
+  const int64_t cunits = (int64_t)M * nq * (D / (64 * cv));
+  using RowsFn = void (*)(CombArgs, int64_t);
+  const RowsFn rk = nsplit <= 4 ? (cv == 4 ? combine_rows_kernel<4, 4>
+                                  : cv == 2 ? combine_rows_kernel<4, 2> : combine_rows_kernel<4, 1>)
+                                : (cv == 4 ? combine_rows_kernel<8, 4>
+                                  : cv == 2 ? combine_rows_kernel<8, 2> : combine_rows_kernel<8, 1>);
+  const dim3 cgrid = cwave ? dim3((unsigned)((cunits + 3) / 4))
                            : dim3((unsigned)((int64_t)M * nq), (unsigned)(D / cb.pairs));
-  const dim3 cblock = cwave ? dim3((unsigned)wthreads) : dim3(kCombThreads);
+  const dim3 cblock = cwave ? dim3((unsigned)kCombWaveThreads) : dim3(kCombThreads);
   const size_t clds = cwave ? 0 : sizeof(float) * (size_t)comb_lds_floats(nsplit);
   std::lock_guard<std::mutex> plk(g_prof_mu);
   if (prof_active(stream)) {
@@ -5020,7 +5097,12 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
     if (!st && nsplit > 1) {
       pr.c0 = prof_event();
       pr.c1 = prof_event();
-      hipExtLaunchKernelGGL(ck, cgrid, cblock, clds, (hipStream_t)stream, pr.c0, pr.c1, 0, cb);
+      if (cwave)
+        hipExtLaunchKernelGGL(rk, cgrid, cblock, 0, (hipStream_t)stream, pr.c0, pr.c1, 0, cb,
+                              cunits);
+      else
+        hipExtLaunchKernelGGL(combine_kernel, cgrid, cblock, clds, (hipStream_t)stream, pr.c0,
+                              pr.c1, 0, cb);
       st = (int)hipGetLastError();
     }
     g_prof.push_back(pr);
@@ -5029,7 +5111,10 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   hipLaunchKernelGGL(pk, grid, dim3(pf_threads), 0, (hipStream_t)stream, a);
   st = (int)hipGetLastError();
   if (st || nsplit == 1) return st;
-  hipLaunchKernelGGL(ck, cgrid, cblock, clds, (hipStream_t)stream, cb);
+  if (cwave)
+    hipLaunchKernelGGL(rk, cgrid, cblock, 0, (hipStream_t)stream, cb, cunits);
+  else
+    hipLaunchKernelGGL(combine_kernel, cgrid, cblock, clds, (hipStream_t)stream, cb);
   return (int)hipGetLastError();
 }
 
