@@ -303,6 +303,44 @@ def test_prefill_presplit_paged(gpu, d, q8):
     assert np.array_equal(o1, o0)
 
 
+def _key_splits(M, N, nq, nkv, pos0, cus):
+    """The launch's key split count for an unwindowed prefill on 8-wave
+    workgroups of 128 query rows: the query blocks' workgroups below the
+    CU count take ceil(cus / workgroups) splits, at most 16 and at least 4
+    key tiles of 32 each."""
+    nqb = -(-M * (nq // nkv) // 128)
+    if nqb * nkv >= cus:
+        return 1
+    tiles = (min(pos0 + M, N) + 31) // 32
+    return max(1, min(16, -(-cus // (nqb * nkv)), tiles // 4))
+
+
+@pytest.mark.parametrize("d,M,splits", [(64, 256, 8), (128, 352, 6), (256, 256, 8),
+                                        (96, 352, 6), (40, 256, 8), (128, 512, 4),
+                                        (256, 512, 4), (64, 512, 4)])
+def test_prefill_split_merge_widths(gpu, d, M, splits):
+    """The merge of a prompt's key splits (combine_rows_kernel) at each lane
+    width (4 outputs a lane at d = 256, 2 at 128, 1 at 64), over up to 4 and
+    up to 8 splits, and at padded head dims (96 in 128, 40 in 64): 16q/4kv
+    after 1000 cached rows against the oracle."""
+    nq, nkv, pos0 = 16, 4, 1000
+    N = pos0 + M
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if _key_splits(M, N, nq, nkv, pos0, cus) != splits:
+        pytest.skip(f"{cus} CUs: this shape takes another split count")
+    announce(f"prefill split merge d={d} M={M} splits={splits}")
+    st = Stream(900 + d + M)
+    Q = st.normal((M, nq, d))
+    K, V = cache(st, N, nkv, d, False)
+    s = 1 / math.sqrt(d)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.attn_prefill_gqa(dev(Q), dev(K), dev(V), O, nq, nkv, M, N, d, s, pos0, 0)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, 0)
+    err = normwise_err(host(O), R)
+    print(f"split merge normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
 def test_prefill_2k_prompt(gpu):
     """A 2048-token prompt at the headline head shape (the bench workload)."""
     announce("prefill 32q/8kv/d128 M=2048 fresh")
