@@ -879,13 +879,15 @@ struct Tune {
     return nw;
   }
   static constexpr int NW = nw();
-  // d = 512, fp32 and bf16: two blocks of half the rows in flight, so a
-  // wave's next loads go out before it scores the current block (same box,
-  // interleaved: 8q/2kv/d512 step fp32 60.9 -> 60.2 us, bf16 36.4 -> 34.4
-  // us).  Q8 keeps one block (2.6x slower with two of half the rows), and
-  // d = 256 gains nothing (8q/4kv window 1024: 9.28 against 9.28 us).
-  static constexpr bool H2 =
-      D > 256 && sizeof(T) != 1 && RB >= 2 && (RB / 2) % RPS == 0 && (RB / 2) % RPI == 0;
+  // d = 512 (fp32 and bf16) and d = 128 fp32: two blocks of half the rows
+  // in flight, so a wave's next loads go out before it scores the current
+  // block (same box, interleaved: 8q/2kv/d512 step fp32 60.9 -> 60.2 us,
+  // bf16 36.4 -> 34.4 us; 32q/8kv/d128 fp32 at n = 4097 12.11 -> 11.99 us,
+  // at n = 16385 25.88 against 25.85 us; two 8-row blocks 13.04 and 26.31).
+  // Q8 keeps one block (2.6x slower with two of half the rows), and d = 256
+  // gains nothing (8q/4kv window 1024: 9.28 against 9.28 us).
+  static constexpr bool H2 = (D > 256 || (D == 128 && sizeof(T) == 4)) && sizeof(T) != 1 &&
+                             RB >= 2 && (RB / 2) % RPS == 0 && (RB / 2) % RPI == 0;
   using C = Cfg<D, GH, T, LPR, H2 ? RB / 2 : RB, NW, H2 ? 2 : 1>;
 };
 
