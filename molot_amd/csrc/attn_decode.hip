@@ -5083,9 +5083,9 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   cb.chunk = 1;
   cb.pairs = comb_pairs(nsplit);
   // at most 8 splits: the row merge, one wave per 64V outputs of a slot
-  // (2048 tokens x 8 q heads at d = 256 over 4 splits: 9.2 us, against 22.2
-  // with a wave per 64 outputs and, over 2 splits, 82 us on
-  // combine_kernel's 4 workgroups a slot); more splits: combine_kernel
+  // (2048 tokens x 8 q heads at d = 256 over 2 splits: 9.2 us, against 22.2
+  // with a wave per 64 outputs and 82 us on combine_kernel's 4 workgroups a
+  // slot); more splits: combine_kernel
   const bool cwave = nsplit <= 8;
   const int cv = D % 256 == 0 ? 4 : (D % 128 == 0 ? 2 : 1);
   const int64_t cunits = (int64_t)M * nq * (D / (64 * cv));
