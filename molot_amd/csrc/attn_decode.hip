@@ -304,6 +304,33 @@ __device__ __forceinline__ void split3x2(float a, float b, uint32_t& hi, uint32_
   lo = bf16_pair(ra, rb);
 }
 
+// Two fp16 pieces of a row scaled by a power of two: with the row's largest
+// |x| in [2^(ex-1), 2^ex) (frexpf of it), y = x * 2^(14-ex) has |y| < 2^14,
+// hi = fp16(y), lo = fp16(y - hi), each rounded to nearest even.  hi + lo
+// holds y to 2^-22 of |y| while |y| >= 2^-3 (lo a normal fp16), and to
+// 2^-25 absolute below (2^-38 of the row's largest |y|); the scaling is
+// exact.  y's unit is 2^(ex-14) (f16_row_unit), the factor that takes a
+// dot product of such pieces back.  Non-finite values make NaN pieces.
+__device__ __forceinline__ int f16_row_shift(float amax) {
+  int ex = 0;
+  (void)frexpf(amax, &ex);
+  return 14 - ex;
+}
+__device__ __forceinline__ float f16_row_unit(int shift) { return ldexpf(1.f, -shift); }
+__device__ __forceinline__ uint32_t f16_pair(float a, float b) {
+  const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+  return (uint32_t)__builtin_bit_cast(uint16_t, ha) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, hb) << 16);
+}
+__device__ __forceinline__ void split2h(float a, float b, int shift, uint32_t& hi, uint32_t& lo) {
+#pragma clang fp contract(off)
+  const float ya = ldexpf(a, shift), yb = ldexpf(b, shift);
+  hi = f16_pair(ya, yb);
+  const float ra = ya - (float)__builtin_bit_cast(_Float16, (uint16_t)(hi & 0xFFFFu));
+  const float rb = yb - (float)__builtin_bit_cast(_Float16, (uint16_t)(hi >> 16));
+  lo = f16_pair(ra, rb);
+}
+
 // ---------------------------------------------------------------------------
 // RoPE + append.
 struct RopeArgs {
@@ -324,7 +351,7 @@ struct RopeArgs {
   float eps;
   int tokens;           // grid row b = token b of a prefill: slot + b at pos + b
   int64_t sc_off, sc_head;  // Q8 scales, as AttnArgs::sc_off / sc_head
-  // prefill over an fp32 or Q8 cache: the appended rows also leave their bf16
+  // prefill over an fp32 or Q8 cache: the appended rows also leave their
   // pieces (as pf_split_kernel writes them) at row slot - pc_T0 of
   // [K, V][nkv][3][pc_R][d], when that row lies in [0, pc_R) (NULL: none)
   uint16_t* pieces;
@@ -652,32 +679,43 @@ __global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeAr
       *(float*)((char*)a.K + soff) = ks;
       *(float*)((char*)a.V + soff) = vs;
     }
-    // the row's bf16 pieces for the prefill (split3 of the cached values:
-    // fp32 as stored, Q8 as code * scale), the bits pf_split_kernel writes
+    // the row's pieces for the prefill (of the cached values: fp32 as
+    // stored, Q8 as code * scale), the bits pf_split_kernel writes: K as
+    // two fp16 pieces of the row scaled by a power of two (split2h, the
+    // row's unit in the first 4 bytes of the third piece), V as three bf16
+    // pieces (split3x2)
     const int pr = slot - a.pc_T0;
     if (a.pieces && a.kv_dtype != MOLOT_KV_BF16 && pr >= 0 && pr < a.pc_R) {
       const int64_t pstride = (int64_t)a.pc_R * a.d;  // one piece of one head
-      #pragma unroll
+      auto cached = [&](float x, float sc) {
+        return a.kv_dtype == MOLOT_KV_Q8 ? (float)q8_code(x, sc) * sc : x;
+      };
+      float kpm = 0.f;  // the row's largest |k| as cached
+#pragma unroll
+      for (int k = 0; k < KMAX; ++k) {
+        if (k >= nk) break;
+        if (lane + 64 * k < half)
+          kpm = fmaxf(kpm, fmaxf(fabsf(cached(r0[k], ks)), fabsf(cached(r1[k], ks))));
+      }
+      const int kshift = f16_row_shift(group_max<64>(kpm));
+      uint16_t* ok = a.pieces + (int64_t)kh * 3 * pstride + (int64_t)pr * a.d;
+      uint16_t* ov = ok + (int64_t)a.nkv * 3 * pstride;
+      if (lane == 0) *reinterpret_cast<float*>(ok + 2 * pstride) = f16_row_unit(kshift);
+#pragma unroll
       for (int k = 0; k < KMAX; ++k) {
         if (k >= nk) break;
         const int j = lane + 64 * k;
         if (j >= half) continue;
-        float kx0 = r0[k], kx1 = r1[k], vx0 = v0[k], vx1 = v1[k];
-        if (a.kv_dtype == MOLOT_KV_Q8) {
-          kx0 = (float)q8_code(kx0, ks) * ks;
-          kx1 = (float)q8_code(kx1, ks) * ks;
-          vx0 = (float)q8_code(vx0, vs) * vs;
-          vx1 = (float)q8_code(vx1, vs) * vs;
-        }
-        uint32_t pk[3], pv[3];
-        split3x2(kx0, kx1, pk[0], pk[1], pk[2]);
-        split3x2(vx0, vx1, pv[0], pv[1], pv[2]);
-        uint16_t* ok = a.pieces + (int64_t)kh * 3 * pstride + (int64_t)pr * a.d;
-        uint16_t* ov = ok + (int64_t)a.nkv * 3 * pstride;
-        #pragma unroll
-        for (int pc = 0; pc < 3; ++pc) {
+        uint32_t pk[2], pv[3];
+        split2h(cached(r0[k], ks), cached(r1[k], ks), kshift, pk[0], pk[1]);
+        split3x2(cached(v0[k], vs), cached(v1[k], vs), pv[0], pv[1], pv[2]);
+#pragma unroll
+        for (int pc = 0; pc < 2; ++pc) {
           ok[pc * pstride + j] = (uint16_t)(pk[pc] & 0xFFFF);
           ok[pc * pstride + j + half] = (uint16_t)(pk[pc] >> 16);
+        }
+#pragma unroll
+        for (int pc = 0; pc < 3; ++pc) {
           ov[pc * pstride + j] = (uint16_t)(pv[pc] & 0xFFFF);
           ov[pc * pstride + j + half] = (uint16_t)(pv[pc] >> 16);
         }
@@ -2193,6 +2231,12 @@ __device__ __forceinline__ f32x4 mfma_bf16(bf16x8_t a, bf16x8_t b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4 mfma_f16(f16x8_t a, f16x8_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 // 16 int8 codes -> 16 bf16 (exact: |code| <= 127), bytes 0-7 into lo, 8-15
 // into hi, each in memory order.  One v_cvt_pk_bf16_f32 per pair (its
 // rounding is the identity on these values).
@@ -2782,7 +2826,7 @@ struct PfArgs {
   int dh;  // head dim as stored (< D: the launch runs padded to D, through the pieces)
   int page_shift;
   float scale;
-  // the attended keys [T0, T0 + R) of every KV head split into bf16 pieces
+  // the attended keys [T0, T0 + R) of every KV head split into 16-bit pieces
   // once for the launch (pf_split_kernel): [K, V][nkv][3 pieces][R][D]; NULL:
   // the kernel splits each staged tile itself
   const uint16_t* pieces;
@@ -2824,10 +2868,12 @@ __device__ __forceinline__ int64_t pf_row_off(const PfArgs& a, int h, int t, int
   }
 }
 
-// K and V of the keys [T0, T0 + R) as three bf16 pieces (split3x2, the
-// values the prefill kernel would split per tile: fp32 rows, or Q8 code * s),
-// into [K, V][nkv][3][R][D].  Thread: one 8-element unit of one row; grid
-// (units / 256, nkv, 2).
+// K and V of the keys [T0, T0 + R) as pieces (the values the prefill kernel
+// would split per tile: fp32 rows, or Q8 code * s), into [K, V][nkv][3][R][D]
+// (16-bit elements): K as two fp16 pieces of the row scaled by a power of two
+// (split2h) with the row's unit (a float) at the start of the third, V as
+// three bf16 pieces (split3x2).  Thread: one 8-element unit of one row, a
+// row's D/8 units in consecutive lanes; grid (units / 256, nkv, 2).
 template <int D, typename T, bool PAGED>
 __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) {
   constexpr bool Q8 = std::is_same<T, q8_t>::value;
@@ -2859,13 +2905,24 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
       x[4 + e] = x1[e];
     }
   }
+  auto row = [&](int p) { return out + ((((int64_t)kv * a.nkv + h) * 3 + p) * a.R + r) * D; };
   uint32_t pc[3][4];
+  if (kv == 0) {  // K: two fp16 pieces, the row scaled by a power of two (split2h)
+    float xm = 0.f;
 #pragma unroll
-  for (int e = 0; e < 8; e += 2) split3x2(x[e], x[e + 1], pc[0][e / 2], pc[1][e / 2], pc[2][e / 2]);
+    for (int e = 0; e < 8; ++e) xm = fmaxf(xm, fabsf(x[e]));
+    const int shift = f16_row_shift(group_max<D / 8>(xm));  // the row's UPR lanes
 #pragma unroll
-  for (int p = 0; p < 3; ++p)
-    *reinterpret_cast<u32x4*>(out + ((((int64_t)kv * a.nkv + h) * 3 + p) * a.R + r) * D + 8 * j) =
-        u32x4{pc[p][0], pc[p][1], pc[p][2], pc[p][3]};
+    for (int e = 0; e < 8; e += 2) split2h(x[e], x[e + 1], shift, pc[0][e / 2], pc[1][e / 2]);
+    if (j == 0) *reinterpret_cast<float*>(row(2)) = f16_row_unit(shift);
+  } else {  // V: three bf16 pieces
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) split3x2(x[e], x[e + 1], pc[0][e / 2], pc[1][e / 2], pc[2][e / 2]);
+    *reinterpret_cast<u32x4*>(row(2) + 8 * j) = u32x4{pc[2][0], pc[2][1], pc[2][2], pc[2][3]};
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+    *reinterpret_cast<u32x4*>(row(p) + 8 * j) = u32x4{pc[p][0], pc[p][1], pc[p][2], pc[p][3]};
 }
 
 // One 16-byte global -> LDS copy per lane (global_load_lds_dwordx4, scalar
@@ -2894,17 +2951,23 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
 // after 16384 cached tokens: 1452 us on 8 waves, 1414 on 4).
 constexpr int kPfWaves = 8;
 
-// The kernel: every fp32 product is taken as bf16 pieces on
-// v_mfma_f32_16x16x32_bf16 (16x the fp32 matrix rate).  x = hi + mid + lo
+// The kernel: every fp32 product is taken as 16-bit pieces on the dense
+// matrix cores (16x the fp32 matrix rate).  PV: x = hi + mid + lo in bf16
 // (split3) carries x's 24-bit significand; a product keeps the six piece
 // products down to 2^-16 of its size (hi*hi, hi*mid, mid*hi, hi*lo, lo*hi,
-// mid*mid), so the dropped ones are ~2^-24 of it, an fp32 rounding.  A bf16
-// cache needs one K/V piece (its values are exact): three products.  Tiles
-// of 32 keys are staged into LDS as pieces:
-//   K [KP][32 keys][D] bf16, 16-byte units XOR-swizzled by key (kt_off),
+// mid*mid) on v_mfma_f32_16x16x32_bf16, so the dropped ones are ~2^-24 of
+// it, an fp32 rounding.  Scores over fp32 and Q8 values: q and K rows as two
+// fp16 pieces of the row scaled by a power of two (split2h), three products
+// (lo*hi, hi*lo, hi*hi) on v_mfma_f32_16x16x32_f16, the dropped lo*lo within
+// 2^-22 of the term, then times the two rows' units (2500 TFLOP/s over 4.5
+// products a term on average instead of 6: 2048-token prompt 194 -> 176 us).
+// A bf16 cache needs one K/V piece (its values are exact): three bf16
+// products each.  Tiles of 32 keys are staged into LDS as pieces:
+//   K [KP][32 keys][D] 16-bit, 16-byte units XOR-swizzled by key (kt_off),
 //     read as the A operand of S^T = K . Q^T: lane l key 16u + l%16,
 //     elements 32s + 8(l/16) .. +7, Q^T in the same element order in
-//     registers;
+//     registers; fp32 and Q8 values: pieces 0 and 1 fp16 hi and lo, piece
+//     2 the row's unit (a float at its start, f16_row_unit);
 //   V [KP][32 keys][D] bf16, 16-byte units XOR-swizzled by key (vt_off),
 //     read as V^T by ds_read_b64_tr_b16 as in attn_mfma_kernel: the A
 //     operand of O^T += V^T . P^T, with P in the registers the score
@@ -2977,32 +3040,70 @@ void prefill_mfma16_kernel(PfArgs a) {
   const int64_t qoff = ((int64_t)m * a.nq + h * G + g) * a.dh;  // q and O rows of dh elements
 
   // Q^T pieces (B operand): lane l row c16, elements 32s + 8*g4 + e, scaled
-  // by scale*log2(e) (base-2 scores)
+  // by scale*log2(e) (base-2 scores).  Against a bf16 cache (KP = 1, exact
+  // K) three bf16 pieces; against fp32 and Q8 values (KP = 3) two fp16
+  // pieces of the row scaled by a power of two (split2h; the row's 4 lanes
+  // share its largest |q|), as K: three products per score term instead of
+  // six bf16 ones, and the scores take the q and K row units back.
   const float qsc = a.scale * kLog2e;
-  bf16x8_t qh[QS], qm[QS], ql[QS];
+  [[maybe_unused]] bf16x8_t qh[QS], qm[QS], ql[QS];
+  [[maybe_unused]] f16x8_t fqh[QS], fql[QS];
+  [[maybe_unused]] float qunit = 1.f;
+  float qx[QS][8];
 #pragma unroll
   for (int s = 0; s < QS; ++s) {
     const float* qp = a.q + qoff + 32 * s + 8 * g4;
     const bool qin = rv && 32 * s + 8 * g4 < a.dh;  // zero padding past dh (a multiple of 8)
     const f32x4 x0 = qin ? *reinterpret_cast<const f32x4*>(qp) : f32x4{0.f, 0.f, 0.f, 0.f};
     const f32x4 x1 = qin ? *reinterpret_cast<const f32x4*>(qp + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
-    uint32_t h4[4], m4[4], l4[4];
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const float xa = (e < 4 ? x0[e] : x1[e - 4]) * qsc, xb = (e < 4 ? x0[e + 1] : x1[e - 3]) * qsc;
-      split3x2(xa, xb, h4[e / 2], m4[e / 2], l4[e / 2]);
+    for (int e = 0; e < 4; ++e) {
+      qx[s][e] = x0[e] * qsc;
+      qx[s][4 + e] = x1[e] * qsc;
     }
-    qh[s] = __builtin_bit_cast(bf16x8_t, u32x4{h4[0], h4[1], h4[2], h4[3]});
-    qm[s] = __builtin_bit_cast(bf16x8_t, u32x4{m4[0], m4[1], m4[2], m4[3]});
-    ql[s] = __builtin_bit_cast(bf16x8_t, u32x4{l4[0], l4[1], l4[2], l4[3]});
+  }
+  if constexpr (KP == 3) {
+    float qm8 = 0.f;
+#pragma unroll
+    for (int s = 0; s < QS; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qm8 = fmaxf(qm8, fabsf(qx[s][e]));
+    const int qshift = f16_row_shift(max_xor32(max_xor16(qm8)));
+    qunit = f16_row_unit(qshift);
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      uint32_t h4[4], l4[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) split2h(qx[s][e], qx[s][e + 1], qshift, h4[e / 2], l4[e / 2]);
+      fqh[s] = __builtin_bit_cast(f16x8_t, u32x4{h4[0], h4[1], h4[2], h4[3]});
+      fql[s] = __builtin_bit_cast(f16x8_t, u32x4{l4[0], l4[1], l4[2], l4[3]});
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      uint32_t h4[4], m4[4], l4[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) split3x2(qx[s][e], qx[s][e + 1], h4[e / 2], m4[e / 2], l4[e / 2]);
+      qh[s] = __builtin_bit_cast(bf16x8_t, u32x4{h4[0], h4[1], h4[2], h4[3]});
+      qm[s] = __builtin_bit_cast(bf16x8_t, u32x4{m4[0], m4[1], m4[2], m4[3]});
+      ql[s] = __builtin_bit_cast(bf16x8_t, u32x4{l4[0], l4[1], l4[2], l4[3]});
+    }
   }
 
   // tile loads: chunk c (16 bytes of the cache type) is key c%8 of its
-  // key octet, column (c/8) % (D/VW) of the row, octet c / (8*D/VW)
+  // key octet, column (c/8) % (D/VW) of the row, octet c / (8*D/VW).  KP = 3
+  // (K split by rows, below): row-major, key c / (D/VW), column c % (D/VW),
+  // so a row's D/VW chunks sit in consecutive lanes of one wave.
+  constexpr int NCR = D / VW;  // chunks per row
+  static_assert(KP != 3 || (NCR <= 64 && 64 % NCR == 0 && NT % NCR == 0), "rows within waves");
   auto chunk_of = [&](int c, int& key, int& e) {
-    constexpr int NCR = D / VW;  // chunks per row
-    key = (c & 7) + 8 * (c / (8 * NCR));
-    e = VW * ((c >> 3) % NCR);
+    if constexpr (KP == 3) {
+      key = c / NCR;
+      e = VW * (c % NCR);
+    } else {
+      key = (c & 7) + 8 * (c / (8 * NCR));
+      e = VW * ((c >> 3) % NCR);
+    }
   };
   const T* Kb = reinterpret_cast<const T*>(a.k);
   const T* Vb = reinterpret_cast<const T*>(a.v);
@@ -3085,7 +3186,9 @@ void prefill_mfma16_kernel(PfArgs a) {
       }
     }
   };
-  // the chunk's values as KP bf16 pieces, 4 elements (8 bytes) at a time
+  // the chunk's values as KP pieces (K of fp32 and Q8 values: two fp16 of
+  // the row scaled by a power of two, its unit in the third), 4 elements
+  // (8 bytes) at a time
   auto store_tile = [&](char* kp_s, char* vp_s) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -3103,6 +3206,16 @@ void prefill_mfma16_kernel(PfArgs a) {
           vx[j] *= vsc[i];
         }
       }
+      [[maybe_unused]] int kshift = 0;
+      if constexpr (KP == 3) {  // the K row's scale: its largest |k| over its NCR lanes
+        float km = 0.f;
+#pragma unroll
+        for (int j = 0; j < VW; ++j) km = fmaxf(km, fabsf(kx[j]));
+        kshift = f16_row_shift(group_max<NCR>(km));
+        if (e == 0)
+          *reinterpret_cast<float*>(kp_s + 2 * KT * KRB + key * KRB + 16 * kt_f<D>(key)) =
+              f16_row_unit(kshift);
+      }
 #pragma unroll
       for (int j4 = 0; j4 < VW; j4 += 4) {
         const int ej = e + j4;
@@ -3110,7 +3223,7 @@ void prefill_mfma16_kernel(PfArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; j += 2) {
           if constexpr (KP == 3) {
-            split3x2(kx[j4 + j], kx[j4 + j + 1], kpc[0][j / 2], kpc[1][j / 2], kpc[2][j / 2]);
+            split2h(kx[j4 + j], kx[j4 + j + 1], kshift, kpc[0][j / 2], kpc[1][j / 2]);
             split3x2(vx[j4 + j], vx[j4 + j + 1], vpc[0][j / 2], vpc[1][j / 2], vpc[2][j / 2]);
           } else {  // exact bf16 values
             kpc[0][j / 2] = bf16_pair(kx[j4 + j], kx[j4 + j + 1]);
@@ -3121,7 +3234,8 @@ void prefill_mfma16_kernel(PfArgs a) {
         const int vofs = vt_off<D>(key, ej >> 3) + 8 * ((ej >> 2) & 1);
 #pragma unroll
         for (int p = 0; p < KP; ++p) {
-          *reinterpret_cast<u32x2*>(kp_s + p * KT * KRB + kofs) = u32x2{kpc[p][0], kpc[p][1]};
+          if (KP != 3 || p < 2)  // K's third piece holds the row's unit only
+            *reinterpret_cast<u32x2*>(kp_s + p * KT * KRB + kofs) = u32x2{kpc[p][0], kpc[p][1]};
           *reinterpret_cast<u32x2*>(vp_s + p * KT * VRB + vofs) = u32x2{vpc[p][0], vpc[p][1]};
         }
       }
@@ -3152,35 +3266,75 @@ void prefill_mfma16_kernel(PfArgs a) {
   // matrix instructions are independent; each accumulator takes its
   // products in the same order as one at a time.  The two step parities are
   // added at the end.
+  // KP = 3 (fp32 and Q8 values): K and q as two fp16 pieces each, three
+  // products per term (lo*hi, hi*lo, hi*hi; the dropped lo*lo is within
+  // 2^-22 of the term), then the q and K row units multiply each score.
+  constexpr int FPK[3] = {1, 0, 0};
+  constexpr int FPQ[3] = {0, 1, 0};
   auto scores = [&](const char* kp_s, f32x4 (&sacc)[KH]) {
     f32x4 sacc2[KH][2];
 #pragma unroll
     for (int u = 0; u < KH; ++u) sacc2[u][0] = sacc2[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s0 = 0; s0 < QS; s0 += SJ) {
-      bf16x8_t kk[SJ][KH][KP];
-#pragma unroll
-      for (int j = 0; j < SJ; ++j)
-#pragma unroll
-        for (int u = 0; u < KH; ++u) {
-          const char* kb = kp_s + kt_off<D>(16 * u + c16, 4 * (s0 + j) + g4);
-#pragma unroll
-          for (int p = 0; p < KP; ++p)
-            kk[j][u][p] = *reinterpret_cast<const bf16x8_t*>(kb + p * KT * KRB);
-        }
-#pragma unroll
-      for (int t = 0; t < NPR; ++t)
+      if constexpr (KP == 3) {
+        f16x8_t kk[SJ][KH][2];
 #pragma unroll
         for (int j = 0; j < SJ; ++j)
 #pragma unroll
           for (int u = 0; u < KH; ++u) {
-            const bf16x8_t& qp = PRQ[t] == 0 ? qh[s0 + j] : PRQ[t] == 1 ? qm[s0 + j] : ql[s0 + j];
-            f32x4& acc = sacc2[u][(s0 + j) & 1];
-            acc = mfma_bf16(kk[j][u][PRK[t]], qp, acc);
+            const char* kb = kp_s + kt_off<D>(16 * u + c16, 4 * (s0 + j) + g4);
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+              kk[j][u][p] = *reinterpret_cast<const f16x8_t*>(kb + p * KT * KRB);
           }
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+          for (int j = 0; j < SJ; ++j)
+#pragma unroll
+            for (int u = 0; u < KH; ++u) {
+              f32x4& acc = sacc2[u][(s0 + j) & 1];
+              acc = mfma_f16(kk[j][u][FPK[t]], FPQ[t] == 0 ? fqh[s0 + j] : fql[s0 + j], acc);
+            }
+      } else {
+        bf16x8_t kk[SJ][KH][KP];
+#pragma unroll
+        for (int j = 0; j < SJ; ++j)
+#pragma unroll
+          for (int u = 0; u < KH; ++u) {
+            const char* kb = kp_s + kt_off<D>(16 * u + c16, 4 * (s0 + j) + g4);
+#pragma unroll
+            for (int p = 0; p < KP; ++p)
+              kk[j][u][p] = *reinterpret_cast<const bf16x8_t*>(kb + p * KT * KRB);
+          }
+#pragma unroll
+        for (int t = 0; t < NPR; ++t)
+#pragma unroll
+          for (int j = 0; j < SJ; ++j)
+#pragma unroll
+            for (int u = 0; u < KH; ++u) {
+              const bf16x8_t& qp = PRQ[t] == 0 ? qh[s0 + j] : PRQ[t] == 1 ? qm[s0 + j] : ql[s0 + j];
+              f32x4& acc = sacc2[u][(s0 + j) & 1];
+              acc = mfma_bf16(kk[j][u][PRK[t]], qp, acc);
+            }
+      }
     }
 #pragma unroll
     for (int u = 0; u < KH; ++u) sacc[u] = sacc2[u][0] + sacc2[u][1];
+    if constexpr (KP == 3) {
+      // key 16u + 4*g4 + r's unit: the float at the start of its row of the
+      // third K piece (unit 0 of a staged row sits at unit kt_f(row))
+#pragma unroll
+      for (int u = 0; u < KH; ++u)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * u + 4 * g4 + r;
+          const float ku =
+              *reinterpret_cast<const float*>(kp_s + 2 * KT * KRB + key * KRB + 16 * kt_f<D>(key));
+          sacc[u][r] *= qunit * ku;
+        }
+    }
   };
   // online softmax (base 2) of this lane's row over its 8 keys of the tile
   // at tk.  Lazy rescale, as in the decode kernel: the running max moves
@@ -4885,7 +5039,7 @@ static int rope_append_paged_impl(float* q, const float* k_new, const float* v_n
 }
 
 // The attended keys of a prefill: [T0, N) with T0 the window start of its
-// first query (pos0), split into bf16 pieces once per launch for fp32 and
+// first query (pos0), split into 16-bit pieces once per launch for fp32 and
 // Q8 caches when the pieces fit (kMaxPiecesBytes) and the workspace need not
 // grow under capture.  Returns the pieces buffer (NULL: the attention kernel
 // splits each staged tile itself) and sets T0 and R.
@@ -5034,7 +5188,7 @@ static int attn_prefill_impl(const float* Qm, const void* K, const void* V, floa
   }
   PfFn pk = pieces_only ? nullptr : pf_kernel(D, kv_dtype, block_row != nullptr, pw);
   if (!pk && !pieces_only) return MOLOT_ENOTSUP;
-  // fp32 and Q8 caches: split the attended keys into bf16 pieces once
+  // fp32 and Q8 caches: split the attended keys into 16-bit pieces once
   // (pf_split_kernel), and let the attention kernel copy them into LDS.
   // Every query attends keys in [t0(query 0), N).  Not under stream capture
   // when the workspace would have to grow, nor past kMaxPiecesBytes: the
