@@ -341,6 +341,42 @@ def test_prefill_split_merge_widths(gpu, d, M, splits):
     assert err < TOL
 
 
+@pytest.mark.parametrize("kv", ["f32", "q8"])
+@pytest.mark.parametrize("presplit", [True, False])
+def test_prefill_row_scales(gpu, kv, presplit):
+    """The scores over fp32 and Q8 values take q and K rows as two fp16
+    pieces of the row scaled by a power of two.  K rows 2^-30 .. 2^30 apart
+    and q rows with three channels 1000x the rest, scaled so that the
+    largest scores stay near 5 and the softmax mixes rows of every scale,
+    on both splits of the keys, against the oracle."""
+    announce(f"prefill row scales kv={kv} presplit={presplit}")
+    nq, nkv, d, M, N, pos0 = 16, 4, 128, 64, 1064, 1000
+    st = Stream(950 + (kv == "q8") + 2 * presplit)
+    e = np.random.default_rng(951).integers(-30, 31, size=N)
+    K = (st.normal((N, nkv * d)) * np.exp2(e)[:, None]).astype(np.float32)
+    V = st.normal((N, nkv * d))
+    Q = st.normal((M, nq, d))
+    Q[:, :, [5, 40, 99]] *= 1000.0
+    Q = (Q * 2.0 ** -30 / 30).astype(np.float32)
+    if kv == "q8":
+        K, V = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
+        Kd = torch.from_numpy(np.ascontiguousarray(K, dtype=np.uint8)).cuda()
+        Vd = torch.from_numpy(np.ascontiguousarray(V, dtype=np.uint8)).cuda()
+    else:
+        Kd, Vd = dev(K), dev(V)
+    s = 1 / math.sqrt(d)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.set_prefill_presplit(presplit)
+    try:
+        attn.attn_prefill_gqa(dev(Q), Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)
+    finally:
+        attn.set_prefill_presplit(True)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, 0)
+    err = normwise_err(host(O), R)
+    print(f"row scales normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
 def test_prefill_2k_prompt(gpu):
     """A 2048-token prompt at the headline head shape (the bench workload)."""
     announce("prefill 32q/8kv/d128 M=2048 fresh")
