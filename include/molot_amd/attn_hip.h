@@ -334,8 +334,10 @@ void molot_hip_set_tuning(int wgs_per_cu);
  * its merged output would be NaN rather than a stale merge. */
 void molot_hip_set_merge(int in_launch);
 
-/* How the prefill entries feed fp32 and Q8 caches to the matrix cores.
- * on = 1 (default): the attended keys of every KV head are split into bf16
+/* How the prefill entries feed fp32 and Q8 caches to the matrix cores: K
+ * as two fp16 pieces of each row scaled by a power of two (the scores),
+ * V as three bf16 pieces (PV), both exact to fp32 rounding.
+ * on = 1 (default): the attended keys of every KV head are split into
  * pieces once per launch, into a per-stream workspace of
  * 12 * nkv * (N - t0) * d bytes (at most 1 GiB; it grows outside stream
  * capture only, and the buffers it outgrows stay allocated, under 1 GiB in
