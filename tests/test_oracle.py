@@ -341,7 +341,7 @@ def test_decode_step_shared_golden(name):
     np.testing.assert_array_equal(K, g["K"])  # nothing appended
     # d = 512 at scale 1 with a normed q and unnormed keys: scores ~ N(0, d),
     # |s - max| up to ~60, where one fp32 ulp of a score moves its weight by
-    # ~4e-6 relative; the survey's 1e-5 bar applies there
+    # ~4e-6 relative; the path's 1e-5 normwise parity bar applies there
     assert normwise_err(O, g["O"]) < (2e-6 if d <= 256 else 1e-5)
 
 
