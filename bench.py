@@ -639,6 +639,36 @@ def main() -> int:
     except (OSError, ValueError, AttributeError):
         pass
 
+    # The boundary with host buffers (never `value`): the C++ drop-in given
+    # host q and o pointers copies q in and o out on the step's stream every
+    # call and returns when o is there.  Pageable host memory, synchronous
+    # calls, the same layers cycled.
+    host_io = None
+    if not wl.paged:
+        qd, od = wl.keep[2], wl.keep[6]
+        q_host = qd.cpu().clone()
+        o_host = torch.empty(tuple(od.shape), dtype=od.dtype)
+        n_io = min(args.steps, 200)
+        with torch.cuda.stream(s):
+            for i in range(5):
+                qd.copy_(q_host)
+                step(i, sp)
+                o_host.copy_(od)
+            torch.cuda.synchronize()
+            t_io = time.perf_counter()
+            for i in range(n_io):
+                qd.copy_(q_host)
+                step(i, sp)
+                o_host.copy_(od)
+            t_io = time.perf_counter() - t_io
+        us_io = t_io / n_io * 1e6
+        host_io = {"us_per_step": round(us_io, 2),
+                   "kv_gbps": round(kv_bytes / (us_io * 1e-6) / 1e9, 1),
+                   "timing": f"{n_io} synchronous calls, host wall clock",
+                   "buffers": "q in and o out as pageable host memory each call"}
+        log(args, f"with host q/o (pageable, synchronous calls): {us_io:.1f} us/step -> "
+            f"{kv_bytes / (us_io * 1e-6) / 1e9:.0f} GB/s")
+
     config = {"workload": DESCR[args.config], "config": args.config}
     config.update(wl.config)
     config.update({"kv_layers_cycled": wl.layers, "timing": mode, "split_chunks": nch,
@@ -683,6 +713,8 @@ def main() -> int:
         },
     }
 
+    if host_io is not None:
+        out["host_io"] = host_io
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = wl.cpu(args)
     print(json.dumps(out), flush=True)
