@@ -640,33 +640,37 @@ def main() -> int:
         pass
 
     # The boundary with host buffers (never `value`): the C++ drop-in given
-    # host q and o pointers copies q in and o out on the step's stream every
-    # call and returns when o is there.  Pageable host memory, synchronous
-    # calls, the same layers cycled.
+    # host q, k, v and o pointers copies q and the new k and v rows in and o
+    # out on the step's stream every call and returns when o is there.
+    # Pageable host memory, synchronous calls, the same layers cycled.
     host_io = None
     if not wl.paged:
-        qd, od = wl.keep[2], wl.keep[6]
-        q_host = qd.cpu().clone()
+        dev_in = (wl.keep[2], wl.keep[3], wl.keep[4])  # q, k_new, v_new
+        od = wl.keep[6]
+        host_in = [t.cpu().clone() for t in dev_in]
         o_host = torch.empty(tuple(od.shape), dtype=od.dtype)
         n_io = min(args.steps, 200)
+
+        def io_call(i):
+            for dv, hv in zip(dev_in, host_in):
+                dv.copy_(hv)
+            step(i, sp)
+            o_host.copy_(od)
+
         with torch.cuda.stream(s):
             for i in range(5):
-                qd.copy_(q_host)
-                step(i, sp)
-                o_host.copy_(od)
+                io_call(i)
             torch.cuda.synchronize()
             t_io = time.perf_counter()
             for i in range(n_io):
-                qd.copy_(q_host)
-                step(i, sp)
-                o_host.copy_(od)
+                io_call(i)
             t_io = time.perf_counter() - t_io
         us_io = t_io / n_io * 1e6
         host_io = {"us_per_step": round(us_io, 2),
                    "kv_gbps": round(kv_bytes / (us_io * 1e-6) / 1e9, 1),
                    "timing": f"{n_io} synchronous calls, host wall clock",
-                   "buffers": "q in and o out as pageable host memory each call"}
-        log(args, f"with host q/o (pageable, synchronous calls): {us_io:.1f} us/step -> "
+                   "buffers": "q, k_new, v_new in and o out as pageable host memory each call"}
+        log(args, f"with host q/k/v/o (pageable, synchronous calls): {us_io:.1f} us/step -> "
             f"{kv_bytes / (us_io * 1e-6) / 1e9:.0f} GB/s")
 
     config = {"workload": DESCR[args.config], "config": args.config}
