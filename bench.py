@@ -639,39 +639,30 @@ def main() -> int:
     except (OSError, ValueError, AttributeError):
         pass
 
-    # The boundary with host buffers (never `value`): the C++ drop-in given
-    # host q, k, v and o pointers copies q and the new k and v rows in and o
-    # out on the step's stream every call and returns when o is there.
-    # Pageable host memory, synchronous calls, the same layers cycled.
+    # The boundary with host buffers (never `value`): the C++ drop-in's
+    # decode call (DeviceKV::decode) given the reference's host vectors, which
+    # it stages through a pinned mirror (q, k_new, v_new in one copy, q and o
+    # back in one) and synchronizes, timed by tests/cpp/host_io_time against
+    # the same call with device vectors (fp32 caches; built by build()).
     host_io = None
-    if not wl.paged:
-        dev_in = (wl.keep[2], wl.keep[3], wl.keep[4])  # q, k_new, v_new
-        od = wl.keep[6]
-        host_in = [t.cpu().clone() for t in dev_in]
-        o_host = torch.empty(tuple(od.shape), dtype=od.dtype)
-        n_io = min(args.steps, 200)
-
-        def io_call(i):
-            for dv, hv in zip(dev_in, host_in):
-                dv.copy_(hv)
-            step(i, sp)
-            o_host.copy_(od)
-
-        with torch.cuda.stream(s):
-            for i in range(5):
-                io_call(i)
-            torch.cuda.synchronize()
-            t_io = time.perf_counter()
-            for i in range(n_io):
-                io_call(i)
-            t_io = time.perf_counter() - t_io
-        us_io = t_io / n_io * 1e6
-        host_io = {"us_per_step": round(us_io, 2),
-                   "kv_gbps": round(kv_bytes / (us_io * 1e-6) / 1e9, 1),
-                   "timing": f"{n_io} synchronous calls, host wall clock",
-                   "buffers": "q, k_new, v_new in and o out as pageable host memory each call"}
-        log(args, f"with host q/k/v/o (pageable, synchronous calls): {us_io:.1f} us/step -> "
-            f"{kv_bytes / (us_io * 1e-6) / 1e9:.0f} GB/s")
+    timer = os.path.join(ROOT, "tests", "cpp", "host_io_time")
+    if not wl.paged and kvd == 0 and not args.norms and os.path.exists(timer):
+        import subprocess
+        cmd = [timer, str(cfg["nq"]), str(cfg["nkv"]), str(cfg["d"]), str(cfg["pos"]),
+               str(cfg["window"]), "200", str(wl.layers)]
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+        vals = dict(kv.split("=") for kv in r.stdout.split()) if r.returncode == 0 else {}
+        if "host_us" in vals:
+            us_io, us_dev = float(vals["host_us"]), float(vals["device_us"])
+            host_io = {"us_per_step": round(us_io, 2),
+                       "kv_gbps": round(kv_bytes / (us_io * 1e-6) / 1e9, 1),
+                       "device_vectors_us_per_step": round(us_dev, 2),
+                       "timing": "200 synchronous DeviceKV::decode calls, host wall clock, "
+                                 f"{wl.layers} layer caches cycled (tests/cpp/host_io_time)",
+                       "buffers": "the reference's host q, k_new, v_new, ao, staged by the "
+                                  "C++ drop-in through a pinned mirror"}
+            log(args, f"C++ drop-in with host vectors: {us_io:.1f} us/call "
+                f"({us_dev:.1f} with device vectors, synchronous calls)")
 
     config = {"workload": DESCR[args.config], "config": args.config}
     config.update(wl.config)

@@ -22,6 +22,7 @@
 
 #include <cmath>
 #include <cstddef>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -52,64 +53,112 @@ inline bool is_device_ptr(const void* p) {
   return attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged;
 }
 
-// Per-thread device staging for host-side q / o (small: nq * d floats).
+// Per-thread staging for host-side vectors (small: q, the new k and v rows,
+// o): a device buffer and a pinned host mirror of the same size, grown when
+// a call needs more (calls are synchronous, so nothing is in flight then).
 class Staging {
  public:
   ~Staging() {
-    if (buf_) (void)hipFree(buf_);
+    if (dev_) (void)hipFree(dev_);
+    if (host_) (void)hipHostFree(host_);
   }
-  float* get(size_t floats) {
-    if (floats > cap_) {
-      if (buf_) check_hip(hipFree(buf_), "hipFree");
-      buf_ = nullptr;
-      check_hip(hipMalloc(&buf_, floats * sizeof(float)), "hipMalloc");
-      cap_ = floats;
-    }
-    return static_cast<float*>(buf_);
+  void reserve(size_t floats) {
+    if (floats <= cap_) return;
+    if (dev_) check_hip(hipFree(dev_), "hipFree");
+    if (host_) check_hip(hipHostFree(host_), "hipHostFree");
+    dev_ = host_ = nullptr;
+    cap_ = 0;
+    check_hip(hipMalloc(&dev_, floats * sizeof(float)), "hipMalloc");
+    check_hip(hipHostMalloc(&host_, floats * sizeof(float), hipHostMallocDefault),
+              "hipHostMalloc");
+    cap_ = floats;
   }
+  float* dev() { return static_cast<float*>(dev_); }
+  float* host() { return static_cast<float*>(host_); }
   static Staging& local() {
     static thread_local Staging s;
     return s;
   }
 
  private:
-  void* buf_ = nullptr;
+  void* dev_ = nullptr;
+  void* host_ = nullptr;
   size_t cap_ = 0;
 };
 
-// Device view of q and o: the caller's pointers if they are device memory,
-// staged copies otherwise.  `sync_out` copies o back and waits.
-struct QOView {
-  const float* q;
+// Device views of one call's vectors: the caller's pointers where they are
+// device memory; host ones packed into the thread's pinned mirror as
+// [k | v | q | o] (the host ones only, each slot on 16 bytes), so that the
+// inputs go over in one copy and q (rotated, for a decode step) and o come
+// back in one.  `finish` copies back, waits and unpacks.
+struct CallStage {
+  float* q;  // device views
   float* o;
-  float* q_host_rot = nullptr;  // host q to receive the rotated q (decode step)
-  const float* q_in;
-  float* o_out;
-  size_t qn, on;
-  bool q_dev, o_dev;
-  float* stage = nullptr;
+  const float* k = nullptr;
+  const float* v = nullptr;
 
-  QOView(const float* Q, float* O, size_t qfloats, size_t ofloats, hipStream_t s)
-      : q_in(Q), o_out(O), qn(qfloats), on(ofloats) {
-    q_dev = is_device_ptr(Q);
-    o_dev = is_device_ptr(O);
-    q = Q;
-    o = O;
-    if (!q_dev || !o_dev) stage = Staging::local().get(qfloats + ofloats);
-    if (!q_dev) {
-      check_hip(hipMemcpyAsync(stage, Q, qn * sizeof(float), hipMemcpyHostToDevice, s), "H2D q");
-      q = stage;
+  CallStage(float* Q, bool q_rotated, float* O, size_t qn, size_t on, hipStream_t s,
+            const float* K = nullptr, const float* V = nullptr, size_t kn = 0)
+      : q(Q), o(O), k(K), v(V), s_(s), q_user_(Q), o_user_(O), qn_(qn), on_(on) {
+    const bool kh = K && !is_device_ptr(K), vh = V && !is_device_ptr(V);
+    qh_ = !is_device_ptr(Q);
+    oh_ = !is_device_ptr(O);
+    q_back_ = qh_ && q_rotated;
+    // every slot starts on 16 bytes (the C ABI's alignment of its vectors)
+    auto up4 = [](size_t n) { return (n + 3) & ~size_t(3); };
+    const size_t in = (kh ? up4(kn) : 0) + (vh ? up4(kn) : 0) + (qh_ ? up4(qn) : 0);
+    const size_t total = in + (oh_ ? up4(on) : 0);
+    if (total == 0) return;
+    staged_ = true;
+    Staging& st = Staging::local();
+    st.reserve(total);
+    float* hb = st.host();
+    float* db = st.dev();
+    size_t off = 0;
+    auto pack = [&](const float* src, size_t n) {
+      std::memcpy(hb + off, src, n * sizeof(float));
+      off += up4(n);
+      return db + off - up4(n);
+    };
+    if (kh) k = pack(K, kn);
+    if (vh) v = pack(V, kn);
+    if (qh_) {
+      q_off_ = off;
+      q = pack(Q, qn);
     }
-    if (!o_dev) o = stage + qfloats;
+    if (in) check_hip(hipMemcpyAsync(db, hb, in * sizeof(float), hipMemcpyHostToDevice, s), "H2D");
+    if (oh_) {
+      o_off_ = off;
+      o = db + off;
+    }
+    // what comes back: q (when rotated) and o, adjacent in the mirror
+    back_beg_ = q_back_ ? q_off_ : o_off_;
+    back_end_ = oh_ ? o_off_ + on : (q_back_ ? q_off_ + qn : back_beg_);
   }
-  void finish(hipStream_t s) {
-    if (!o_dev)
-      check_hip(hipMemcpyAsync(o_out, o, on * sizeof(float), hipMemcpyDeviceToHost, s), "D2H o");
-    if (q_host_rot)
-      check_hip(hipMemcpyAsync(q_host_rot, q, qn * sizeof(float), hipMemcpyDeviceToHost, s),
-                "D2H q");
-    check_hip(hipStreamSynchronize(s), "hipStreamSynchronize");
+  // a call that threw before finish: nothing may still read the mirror when
+  // the next call packs it
+  ~CallStage() {
+    if (staged_ && !finished_) (void)hipStreamSynchronize(s_);
   }
+  void finish() {
+    finished_ = true;
+    Staging& st = Staging::local();
+    if ((oh_ || q_back_) && back_end_ > back_beg_)
+      check_hip(hipMemcpyAsync(st.host() + back_beg_, st.dev() + back_beg_,
+                               (back_end_ - back_beg_) * sizeof(float), hipMemcpyDeviceToHost, s_),
+                "D2H");
+    check_hip(hipStreamSynchronize(s_), "hipStreamSynchronize");
+    if (q_back_) std::memcpy(q_user_, st.host() + q_off_, qn_ * sizeof(float));
+    if (oh_) std::memcpy(o_user_, st.host() + o_off_, on_ * sizeof(float));
+  }
+
+ private:
+  hipStream_t s_;
+  float* q_user_;
+  float* o_user_;
+  size_t qn_, on_;
+  bool qh_ = false, oh_ = false, q_back_ = false, staged_ = false, finished_ = false;
+  size_t q_off_ = 0, o_off_ = 0, back_beg_ = 0, back_end_ = 0;
 };
 
 // attn.h:31-33
@@ -125,21 +174,21 @@ inline void rope_apply(float* x, int d, int pos, const float* inv_freq, hipStrea
 inline void attn_decode_gqa_cache(const float* Q, const float* K, const float* V, float* O, int nq,
                                   int nkv, int n, int qhd, float scale, int pos_cur, int window,
                                   ThreadPool& /*pool*/, hipStream_t s = nullptr) {
-  QOView v(Q, O, (size_t)nq * qhd, (size_t)nq * qhd, s);
+  CallStage v(const_cast<float*>(Q), false, O, (size_t)nq * qhd, (size_t)nq * qhd, s);
   check(molot_hip_attn_decode_gqa_cache(v.q, K, V, v.o, nq, nkv, n, qhd, scale, pos_cur, window,
                                         MOLOT_KV_F32, s),
         "attn_decode_gqa_cache");
-  v.finish(s);
+  v.finish();
 }
 
 // attn.h:111-113: head-major [nkv][n][d] device K, V.
 inline void attn_decode_gqa(const float* Q, const float* K, const float* V, float* O, int nq,
                             int nkv, int n, int d, float scale, ThreadPool& /*pool*/,
                             hipStream_t s = nullptr) {
-  QOView v(Q, O, (size_t)nq * d, (size_t)nq * d, s);
+  CallStage v(const_cast<float*>(Q), false, O, (size_t)nq * d, (size_t)nq * d, s);
   check(molot_hip_attn_decode_gqa(v.q, K, V, v.o, nq, nkv, n, d, scale, MOLOT_KV_F32, s),
         "attn_decode_gqa");
-  v.finish(s);
+  v.finish();
 }
 
 // The layer's norms of the fresh q, k, v (forward.h:554, 562-563): the
@@ -199,29 +248,18 @@ class DeviceKV {
               hipStream_t s = nullptr) {
     if (n >= cap) throw std::runtime_error("fwd: KV cache full");  // forward.h:570
     const size_t qf = (size_t)nq * hd, kf = (size_t)nkv * hd;
-    QOView view(q, ao, qf, qf, s);
-    if (!view.q_dev) view.q_host_rot = q;
-    const float* kd = knew;
-    const float* vd = vnew;
-    float* kv_stage = nullptr;
-    if (!is_device_ptr(knew) || !is_device_ptr(vnew)) {
-      kv_stage = kv_staging_.get(2 * kf);
-      check_hip(hipMemcpyAsync(kv_stage, knew, kf * 4, hipMemcpyHostToDevice, s), "H2D k");
-      check_hip(hipMemcpyAsync(kv_stage + kf, vnew, kf * 4, hipMemcpyHostToDevice, s), "H2D v");
-      kd = kv_stage;
-      vd = kv_stage + kf;
-    }
+    CallStage view(q, true, ao, qf, qf, s, knew, vnew, kf);
     if (nm.q_norm || nm.k_norm || nm.v_norm)
-      check(molot_hip_decode_step_norm(const_cast<float*>(view.q), kd, vd, k, v, view.o, nq, nkv,
-                                       hd, n, pos, nm.q_norm, nm.k_norm, nm.v_norm ? 1 : 0,
-                                       nm.eps, inv_freq, scale, window, kv_dtype, s),
+      check(molot_hip_decode_step_norm(view.q, view.k, view.v, k, v, view.o, nq, nkv, hd, n, pos,
+                                       nm.q_norm, nm.k_norm, nm.v_norm ? 1 : 0, nm.eps, inv_freq,
+                                       scale, window, kv_dtype, s),
             "decode_step_norm");
     else
-      check(molot_hip_decode_step(const_cast<float*>(view.q), kd, vd, k, v, view.o, nq, nkv, hd,
-                                  n, pos, inv_freq, scale, window, kv_dtype, s),
+      check(molot_hip_decode_step(view.q, view.k, view.v, k, v, view.o, nq, nkv, hd, n, pos,
+                                  inv_freq, scale, window, kv_dtype, s),
             "decode_step");
     ++n;
-    view.finish(s);
+    view.finish();
   }
 
   // forward.h:554-558 and 578-591 for a layer without its own KV (L.has_kv
@@ -233,13 +271,11 @@ class DeviceKV {
                      int window, const LayerNorms& nm = LayerNorms{},
                      hipStream_t s = nullptr) const {
     if (n == 0) throw std::runtime_error("fwd: shared KV empty");  // forward.h:580
-    QOView view(q, ao, (size_t)nq * hd, (size_t)nq * hd, s);
-    if (!view.q_dev) view.q_host_rot = q;
-    check(molot_hip_decode_step_shared(const_cast<float*>(view.q), k, v, view.o, nq, nkv, hd, n,
-                                       pos, nm.q_norm, nm.eps, inv_freq, scale, window, kv_dtype,
-                                       s),
+    CallStage view(q, true, ao, (size_t)nq * hd, (size_t)nq * hd, s);
+    check(molot_hip_decode_step_shared(view.q, k, v, view.o, nq, nkv, hd, n, pos, nm.q_norm,
+                                       nm.eps, inv_freq, scale, window, kv_dtype, s),
           "decode_step_shared");
-    view.finish(s);
+    view.finish();
   }
 
   // forward.h:367-399 for a layer that owns this cache: M prompt tokens'
@@ -274,15 +310,13 @@ class DeviceKV {
   void attend(const float* q, float* ao, int nq, float scale, int pos_cur, int window,
               hipStream_t s = nullptr) const {
     if (n == 0) throw std::runtime_error("fwd: shared KV empty");  // forward.h:580
-    QOView view(q, ao, (size_t)nq * hd, (size_t)nq * hd, s);
+    CallStage view(const_cast<float*>(q), false, ao, (size_t)nq * hd, (size_t)nq * hd, s);
     check(molot_hip_attn_decode_gqa_cache(view.q, k, v, view.o, nq, nkv, n, hd, scale, pos_cur,
                                           window, kv_dtype, s),
           "attn_decode_gqa_cache");
-    view.finish(s);
+    view.finish();
   }
 
- private:
-  Staging kv_staging_;
 };
 
 }  // namespace molot::amd

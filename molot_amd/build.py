@@ -7,6 +7,8 @@
   tests/cpp/test_paged_kv      C++ self-check of the paged-KV manager
                               (include/molot_amd/attn.hpp), linked to the above
                               and to the oracle (its checker)
+  tests/cpp/host_io_time       time of the C++ drop-in's decode call with host
+                              vectors against device ones (bench.py's host_io)
 The oracle (oracle/Makefile) is test infrastructure and is built by
 ``__graft_entry__.build()`` next to these, never by the product path.
 """
@@ -81,7 +83,7 @@ def build_cpp_test(name: str = "test_attn_cpp") -> str:
     return out
 
 
-CPP_TESTS = ("test_attn_cpp", "test_paged_kv")
+CPP_TESTS = ("test_attn_cpp", "test_paged_kv", "host_io_time")
 
 
 def build_all() -> None:

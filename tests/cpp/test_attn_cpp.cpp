@@ -214,6 +214,53 @@ int main() {
     (void)hipFree(inv_d);
   }
 
+  // ---- 5. host vectors whose sizes are not multiples of 4 floats (3 q heads
+  // and 1 KV head of d = 34: 102 and 34 floats), staged through the pinned
+  // mirror on 16-byte slots; then the same step with q and ao on the device
+  // and k, v on the host (a mixed call) ----
+  {
+    const int nq = 3, nkv = 1, d = 34, cap = 24, steps = 20;
+    const float scale = 1.0f / std::sqrt((float)d);
+    std::vector<float> inv(d / 2);
+    molot::amd::rope_inv_freq(10000.0f, d, inv.data());
+    float* inv_d = nullptr;
+    molot::amd::check_hip(hipMalloc(&inv_d, inv.size() * 4), "hipMalloc");
+    molot::amd::check_hip(hipMemcpy(inv_d, inv.data(), inv.size() * 4, hipMemcpyHostToDevice), "");
+    molot::amd::DeviceKV kv(cap, nkv, d);
+    std::vector<float> Kref((size_t)cap * nkv * d, 0.f), Vref((size_t)cap * nkv * d, 0.f);
+    Rng rng(7);
+    double worst = 0, qworst = 0;
+    float *q_dev = nullptr, *ao_dev = nullptr;
+    molot::amd::check_hip(hipMalloc(&q_dev, nq * d * 4), "hipMalloc");
+    molot::amd::check_hip(hipMalloc(&ao_dev, nq * d * 4), "hipMalloc");
+    for (int pos = 0; pos < steps; ++pos) {
+      std::vector<float> q(nq * d), k(nkv * d), v(nkv * d), ao(nq * d), ao_ref(nq * d);
+      rng.normal(q);
+      rng.normal(k);
+      rng.normal(v);
+      std::vector<float> q_ref = q, k_ref = k;
+      if (pos % 2 == 0) {
+        kv.decode(q.data(), k.data(), v.data(), ao.data(), nq, pos, inv_d, scale, 0);
+      } else {
+        molot::amd::check_hip(hipMemcpy(q_dev, q.data(), nq * d * 4, hipMemcpyHostToDevice), "");
+        kv.decode(q_dev, k.data(), v.data(), ao_dev, nq, pos, inv_d, scale, 0);
+        molot::amd::check_hip(hipMemcpy(q.data(), q_dev, nq * d * 4, hipMemcpyDeviceToHost), "");
+        molot::amd::check_hip(hipMemcpy(ao.data(), ao_dev, nq * d * 4, hipMemcpyDeviceToHost), "");
+      }
+      orc_decode_step(q_ref.data(), k_ref.data(), v.data(), Kref.data(), Vref.data(),
+                      ao_ref.data(), nq, nkv, d, pos, pos, inv.data(), scale, 0, ORC_KV_F32, 1);
+      worst = std::fmax(worst, normwise(ao, ao_ref));
+      qworst = std::fmax(qworst, normwise(q, q_ref));
+    }
+    CHECK(worst < 1e-5, "d = 34 host/device decode normwise err %g", worst);
+    CHECK(qworst < 1e-6, "d = 34 rotated q err %g", qworst);
+    std::printf("[%s] DeviceKV 3q/1kv/d34, host and mixed pointers, %d steps: %.2e (q %.2e)\n",
+                worst < 1e-5 && qworst < 1e-6 ? "ok" : "FAIL", steps, worst, qworst);
+    (void)hipFree(q_dev);
+    (void)hipFree(ao_dev);
+    (void)hipFree(inv_d);
+  }
+
   // ---- 4. an unsupported (odd) head dim surfaces as std::runtime_error ----
   {
     bool threw = false;
