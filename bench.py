@@ -643,10 +643,13 @@ def main() -> int:
     # decode call (DeviceKV::decode) given the reference's host vectors, which
     # it stages through a pinned mirror (q, k_new, v_new in one copy, q and o
     # back in one) and synchronizes, timed by tests/cpp/host_io_time against
-    # the same call with device vectors (fp32 caches; built by build()).
+    # the same call with device vectors (fp32 caches; built by build()).  Full
+    # runs only (with the CPU baseline): under a profiler (--cpu-seconds 0)
+    # its launches would join the trace.
     host_io = None
     timer = os.path.join(ROOT, "tests", "cpp", "host_io_time")
-    if not wl.paged and kvd == 0 and not args.norms and os.path.exists(timer):
+    if (not wl.paged and kvd == 0 and not args.norms and args.cpu_seconds > 0
+            and os.path.exists(timer)):
         import subprocess
         cmd = [timer, str(cfg["nq"]), str(cfg["nkv"]), str(cfg["d"]), str(cfg["pos"]),
                str(cfg["window"]), "200", str(wl.layers)]
