@@ -142,11 +142,10 @@ CONFIGS = {
 }
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
 BF16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 matrix, published
-# the prefill's fp32-exact products on the dense fp16/bf16 matrix cores
-# (fp32 and Q8 caches): a score term as three fp16 piece products (two
-# row-scaled fp16 pieces of q and of K), a PV term as six bf16 piece
-# products (three bf16 pieces of P and of V), 4.5 a term on average
-PIECE_PRODUCTS = 4.5
+# the prefill's fp32-exact products on the dense fp16 matrix cores (fp32
+# and Q8 caches): a score term and a PV term each as three fp16 piece
+# products (two row-scaled fp16 pieces of q and K, of P and V)
+PIECE_PRODUCTS = 3.0
 PIECE_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / PIECE_PRODUCTS
 SIX_PRODUCT_PEAK_TFLOPS = BF16_MFMA_PEAK_TFLOPS / 6  # six bf16 products per term, both halves
 DESCR = {
@@ -779,7 +778,7 @@ def run_prefill(args, cfg, lib, L, torch, np):
     ms = start.elapsed_time(end) / steps
     value = flops / (ms * 1e-3) / 1e12
     log(args, f"eager: {steps} steps, {ms * 1e3:.1f} us/step -> {value:.1f} TFLOP/s "
-        f"({100 * value / PIECE_PEAK_TFLOPS:.1f}% of the 4.5-product matrix ceiling, "
+        f"({100 * value / PIECE_PEAK_TFLOPS:.1f}% of the 3-product matrix ceiling, "
         f"{100 * value / FP32_MFMA_PEAK_TFLOPS:.1f}% of the fp32 MFMA peak)")
     with torch.cuda.stream(s):
         L.check(lib.molot_hip_profile_begin(steps), "profile_begin")
@@ -811,17 +810,17 @@ def run_prefill(args, cfg, lib, L, torch, np):
                    "rope_theta": theta, "timing": "eager"},
         "flops_per_step": flops,
         # peak: the ceiling of the instructions the kernel issues.  It takes
-        # a score term as three fp16 and a PV term as six bf16 piece products
-        # on the 2500 TFLOP/s dense matrix cores, so 2500 / 4.5
-        # fp32-equivalent TFLOP/s; beside it the ceiling of six bf16 products
-        # for both (the kernel before the fp16 scores) and the fp32 matrix
-        # peak (the precision the products keep).
+        # a score term and a PV term each as three fp16 piece products on the
+        # 2500 TFLOP/s dense matrix cores, so 2500 / 3 fp32-equivalent
+        # TFLOP/s; beside it the ceiling of six bf16 products for both (the
+        # kernel before its fp16 pieces) and the fp32 matrix peak (the
+        # precision the products keep).
         "roofline": {"bound": "mfma", "kernel": "%s<%d,float>" % (kname, d),
                      "achieved": round(achieved, 2), "peak": round(PIECE_PEAK_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(achieved / PIECE_PEAK_TFLOPS, 4),
                      "traffic": None, "launch_us": round(k_us, 2),
-                     "peak_basis": "dense fp16/bf16 MFMA 2500 TFLOP/s / 4.5 piece products "
-                                   "(scores: 3 fp16, PV: 6 bf16)",
+                     "peak_basis": "dense fp16 MFMA 2500 TFLOP/s / 3 piece products "
+                                   "(scores and PV: 3 fp16 each)",
                      "six_product_peak": round(SIX_PRODUCT_PEAK_TFLOPS, 1),
                      "frac_of_six_product_peak": round(achieved / SIX_PRODUCT_PEAK_TFLOPS, 4),
                      "fp32_mfma_peak": FP32_MFMA_PEAK_TFLOPS,

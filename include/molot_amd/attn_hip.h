@@ -335,8 +335,8 @@ void molot_hip_set_tuning(int wgs_per_cu);
 void molot_hip_set_merge(int in_launch);
 
 /* How the prefill entries feed fp32 and Q8 caches to the matrix cores: K
- * as two fp16 pieces of each row scaled by a power of two (the scores),
- * V as three bf16 pieces (PV), both exact to fp32 rounding.
+ * and V as two fp16 pieces of each row scaled by a power of two (the scores
+ * and PV), exact to fp32 rounding.
  * on = 1 (default): the attended keys of every KV head are split into
  * pieces once per launch, into a per-stream workspace of
  * 12 * nkv * (N - t0) * d bytes (at most 1 GiB; it grows outside stream

@@ -330,6 +330,14 @@ __device__ __forceinline__ void split2h(float a, float b, int shift, uint32_t& h
   const float rb = yb - (float)__builtin_bit_cast(_Float16, (uint16_t)(hi >> 16));
   lo = f16_pair(ra, rb);
 }
+// V rows (the prefill's PV operand): the same split, with the unit kept a
+// normal float (shift <= 120: 2^-120 and up; rows below 2^-106 keep fewer
+// bits, as fp32 denormals would) and 0 for a row of zeros, which then
+// weighs nothing and never sets a tile's largest unit.
+__device__ __forceinline__ int f16_vrow_shift(float amax) { return min(f16_row_shift(amax), 120); }
+__device__ __forceinline__ float f16_vrow_unit(float amax, int shift) {
+  return amax > 0.f ? f16_row_unit(shift) : 0.f;
+}
 
 // ---------------------------------------------------------------------------
 // RoPE + append.
@@ -680,42 +688,45 @@ __global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeAr
       *(float*)((char*)a.V + soff) = vs;
     }
     // the row's pieces for the prefill (of the cached values: fp32 as
-    // stored, Q8 as code * scale), the bits pf_split_kernel writes: K as
-    // two fp16 pieces of the row scaled by a power of two (split2h, the
-    // row's unit in the first 4 bytes of the third piece), V as three bf16
-    // pieces (split3x2)
+    // stored, Q8 as code * scale), the bits pf_split_kernel writes: K and
+    // V as two fp16 pieces of the row scaled by a power of two (split2h,
+    // the row's unit in the first 4 bytes of the third piece)
     const int pr = slot - a.pc_T0;
     if (a.pieces && a.kv_dtype != MOLOT_KV_BF16 && pr >= 0 && pr < a.pc_R) {
       const int64_t pstride = (int64_t)a.pc_R * a.d;  // one piece of one head
       auto cached = [&](float x, float sc) {
         return a.kv_dtype == MOLOT_KV_Q8 ? (float)q8_code(x, sc) * sc : x;
       };
-      float kpm = 0.f;  // the row's largest |k| as cached
+      float kpm = 0.f, vpm = 0.f;  // the rows' largest |k| and |v| as cached
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
         if (k >= nk) break;
-        if (lane + 64 * k < half)
+        if (lane + 64 * k < half) {
           kpm = fmaxf(kpm, fmaxf(fabsf(cached(r0[k], ks)), fabsf(cached(r1[k], ks))));
+          vpm = fmaxf(vpm, fmaxf(fabsf(cached(v0[k], vs)), fabsf(cached(v1[k], vs))));
+        }
       }
       const int kshift = f16_row_shift(group_max<64>(kpm));
+      vpm = group_max<64>(vpm);
+      const int vshift = f16_vrow_shift(vpm);
       uint16_t* ok = a.pieces + (int64_t)kh * 3 * pstride + (int64_t)pr * a.d;
       uint16_t* ov = ok + (int64_t)a.nkv * 3 * pstride;
-      if (lane == 0) *reinterpret_cast<float*>(ok + 2 * pstride) = f16_row_unit(kshift);
+      if (lane == 0) {
+        *reinterpret_cast<float*>(ok + 2 * pstride) = f16_row_unit(kshift);
+        *reinterpret_cast<float*>(ov + 2 * pstride) = f16_vrow_unit(vpm, vshift);
+      }
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
         if (k >= nk) break;
         const int j = lane + 64 * k;
         if (j >= half) continue;
-        uint32_t pk[2], pv[3];
+        uint32_t pk[2], pv[2];
         split2h(cached(r0[k], ks), cached(r1[k], ks), kshift, pk[0], pk[1]);
-        split3x2(cached(v0[k], vs), cached(v1[k], vs), pv[0], pv[1], pv[2]);
+        split2h(cached(v0[k], vs), cached(v1[k], vs), vshift, pv[0], pv[1]);
 #pragma unroll
         for (int pc = 0; pc < 2; ++pc) {
           ok[pc * pstride + j] = (uint16_t)(pk[pc] & 0xFFFF);
           ok[pc * pstride + j + half] = (uint16_t)(pk[pc] >> 16);
-        }
-#pragma unroll
-        for (int pc = 0; pc < 3; ++pc) {
           ov[pc * pstride + j] = (uint16_t)(pv[pc] & 0xFFFF);
           ov[pc * pstride + j + half] = (uint16_t)(pv[pc] >> 16);
         }
@@ -2870,10 +2881,10 @@ __device__ __forceinline__ int64_t pf_row_off(const PfArgs& a, int h, int t, int
 
 // K and V of the keys [T0, T0 + R) as pieces (the values the prefill kernel
 // would split per tile: fp32 rows, or Q8 code * s), into [K, V][nkv][3][R][D]
-// (16-bit elements): K as two fp16 pieces of the row scaled by a power of two
-// (split2h) with the row's unit (a float) at the start of the third, V as
-// three bf16 pieces (split3x2).  Thread: one 8-element unit of one row, a
-// row's D/8 units in consecutive lanes; grid (units / 256, nkv, 2).
+// (16-bit elements): K and V rows as two fp16 pieces of the row scaled by a
+// power of two (split2h) with the row's unit (a float) at the start of the
+// third.  Thread: one 8-element unit of one row, a row's D/8 units in
+// consecutive lanes; grid (units / 256, nkv, 2).
 template <int D, typename T, bool PAGED>
 __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) {
   constexpr bool Q8 = std::is_same<T, q8_t>::value;
@@ -2906,20 +2917,17 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
     }
   }
   auto row = [&](int p) { return out + ((((int64_t)kv * a.nkv + h) * 3 + p) * a.R + r) * D; };
-  uint32_t pc[3][4];
-  if (kv == 0) {  // K: two fp16 pieces, the row scaled by a power of two (split2h)
-    float xm = 0.f;
+  // two fp16 pieces of the row scaled by a power of two (split2h), the
+  // row's unit (a float) at the start of the third piece
+  uint32_t pc[2][4];
+  float xm = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) xm = fmaxf(xm, fabsf(x[e]));
-    const int shift = f16_row_shift(group_max<D / 8>(xm));  // the row's UPR lanes
+  for (int e = 0; e < 8; ++e) xm = fmaxf(xm, fabsf(x[e]));
+  xm = group_max<D / 8>(xm);  // the row's UPR lanes
+  const int shift = kv ? f16_vrow_shift(xm) : f16_row_shift(xm);
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) split2h(x[e], x[e + 1], shift, pc[0][e / 2], pc[1][e / 2]);
-    if (j == 0) *reinterpret_cast<float*>(row(2)) = f16_row_unit(shift);
-  } else {  // V: three bf16 pieces
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) split3x2(x[e], x[e + 1], pc[0][e / 2], pc[1][e / 2], pc[2][e / 2]);
-    *reinterpret_cast<u32x4*>(row(2) + 8 * j) = u32x4{pc[2][0], pc[2][1], pc[2][2], pc[2][3]};
-  }
+  for (int e = 0; e < 8; e += 2) split2h(x[e], x[e + 1], shift, pc[0][e / 2], pc[1][e / 2]);
+  if (j == 0) *reinterpret_cast<float*>(row(2)) = kv ? f16_vrow_unit(xm, shift) : f16_row_unit(shift);
 #pragma unroll
   for (int p = 0; p < 2; ++p)
     *reinterpret_cast<u32x4*>(row(p) + 8 * j) = u32x4{pc[p][0], pc[p][1], pc[p][2], pc[p][3]};
@@ -2952,26 +2960,29 @@ __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t l
 constexpr int kPfWaves = 8;
 
 // The kernel: every fp32 product is taken as 16-bit pieces on the dense
-// matrix cores (16x the fp32 matrix rate).  PV: x = hi + mid + lo in bf16
-// (split3) carries x's 24-bit significand; a product keeps the six piece
-// products down to 2^-16 of its size (hi*hi, hi*mid, mid*hi, hi*lo, lo*hi,
-// mid*mid) on v_mfma_f32_16x16x32_bf16, so the dropped ones are ~2^-24 of
-// it, an fp32 rounding.  Scores over fp32 and Q8 values: q and K rows as two
-// fp16 pieces of the row scaled by a power of two (split2h), three products
-// (lo*hi, hi*lo, hi*hi) on v_mfma_f32_16x16x32_f16, the dropped lo*lo within
-// 2^-22 of the term, then times the two rows' units (2500 TFLOP/s over 4.5
-// products a term on average instead of 6: 2048-token prompt 194 -> 176 us).
-// A bf16 cache needs one K/V piece (its values are exact): three bf16
-// products each.  Tiles of 32 keys are staged into LDS as pieces:
+// matrix cores (16x the fp32 matrix rate).  Over fp32 and Q8 values both
+// products take two fp16 pieces of each operand (split2h: hi = fp16(y),
+// lo = fp16(y - hi) of y scaled by a power of two below 2^14) and three
+// products (lo*hi, hi*lo, hi*hi) on v_mfma_f32_16x16x32_f16, the dropped
+// lo*lo within 2^-22 of the term.  Scores: q and K rows scaled by their own
+// powers of two, the score then times the two rows' units.  PV: V rows
+// scaled the same way; each key's V unit folds into its p, and each query
+// row's y = p * u_key stays below 2^14 through a running power of two that
+// o carries (3 products a term instead of six bf16 ones: 2048-token prompt
+// 194 -> 176 us with the scores' pieces, 173 -> 162 us with PV's).  A bf16
+// cache needs one K/V piece (its values are exact) and q and P as three
+// bf16 pieces (split3): three bf16 products each.  Tiles of 32 keys are
+// staged into LDS as pieces:
 //   K [KP][32 keys][D] 16-bit, 16-byte units XOR-swizzled by key (kt_off),
 //     read as the A operand of S^T = K . Q^T: lane l key 16u + l%16,
 //     elements 32s + 8(l/16) .. +7, Q^T in the same element order in
 //     registers; fp32 and Q8 values: pieces 0 and 1 fp16 hi and lo, piece
 //     2 the row's unit (a float at its start, f16_row_unit);
-//   V [KP][32 keys][D] bf16, 16-byte units XOR-swizzled by key (vt_off),
+//   V [KP][32 keys][D] 16-bit, 16-byte units XOR-swizzled by key (vt_off),
 //     read as V^T by ds_read_b64_tr_b16 as in attn_mfma_kernel: the A
 //     operand of O^T += V^T . P^T, with P in the registers the score
-//     accumulator left it in (key 16u + 4(l/16) + r of lane l, slot 4u + r).
+//     accumulator left it in (key 16u + 4(l/16) + r of lane l, slot 4u + r);
+//     fp32 and Q8 values as K (f16_vrow_unit).
 // A tile's loads put keys 0..7 of one 16-byte column in lanes 0..7 and the
 // next column in lanes 8..15 (128 contiguous bytes of each of 8 rows per 64
 // lanes), so every LDS store of a piece is conflict-free too.
@@ -2979,7 +2990,7 @@ constexpr int kPfWaves = 8;
 template <int D, typename T, bool PAGED, int PW, bool PRE = false>
 __global__ __launch_bounds__(64 * PW, PW == 4 && D < 256 ? 2 : 1)
 void prefill_mfma16_kernel(PfArgs a) {
-  static_assert(D == 64 || D == 128 || D == 256, "bf16-piece prefill: D = 64, 128, 256");
+  static_assert(D == 64 || D == 128 || D == 256, "16-bit-piece prefill: D = 64, 128, 256");
   static_assert(PW == 4 || PW == 8, "4 or 8 waves");
   static_assert(!PRE || (sizeof(T) == 4 && !PAGED), "PRE: one instance per D and PW (pieces)");
   constexpr int NT = 64 * PW, QB = NT / 4;
@@ -3206,15 +3217,23 @@ void prefill_mfma16_kernel(PfArgs a) {
           vx[j] *= vsc[i];
         }
       }
-      [[maybe_unused]] int kshift = 0;
-      if constexpr (KP == 3) {  // the K row's scale: its largest |k| over its NCR lanes
-        float km = 0.f;
+      [[maybe_unused]] int kshift = 0, vshift = 0;
+      if constexpr (KP == 3) {  // the K and V rows' scales: largest |x| over the row's NCR lanes
+        float km = 0.f, vm = 0.f;
 #pragma unroll
-        for (int j = 0; j < VW; ++j) km = fmaxf(km, fabsf(kx[j]));
+        for (int j = 0; j < VW; ++j) {
+          km = fmaxf(km, fabsf(kx[j]));
+          vm = fmaxf(vm, fabsf(vx[j]));
+        }
         kshift = f16_row_shift(group_max<NCR>(km));
-        if (e == 0)
+        vm = group_max<NCR>(vm);
+        vshift = f16_vrow_shift(vm);
+        if (e == 0) {
           *reinterpret_cast<float*>(kp_s + 2 * KT * KRB + key * KRB + 16 * kt_f<D>(key)) =
               f16_row_unit(kshift);
+          *reinterpret_cast<float*>(vp_s + 2 * KT * VRB + key * VRB + 16 * vt_f<D>(key)) =
+              f16_vrow_unit(vm, vshift);
+        }
       }
 #pragma unroll
       for (int j4 = 0; j4 < VW; j4 += 4) {
@@ -3224,7 +3243,7 @@ void prefill_mfma16_kernel(PfArgs a) {
         for (int j = 0; j < 4; j += 2) {
           if constexpr (KP == 3) {
             split2h(kx[j4 + j], kx[j4 + j + 1], kshift, kpc[0][j / 2], kpc[1][j / 2]);
-            split3x2(vx[j4 + j], vx[j4 + j + 1], vpc[0][j / 2], vpc[1][j / 2], vpc[2][j / 2]);
+            split2h(vx[j4 + j], vx[j4 + j + 1], vshift, vpc[0][j / 2], vpc[1][j / 2]);
           } else {  // exact bf16 values
             kpc[0][j / 2] = bf16_pair(kx[j4 + j], kx[j4 + j + 1]);
             vpc[0][j / 2] = bf16_pair(vx[j4 + j], vx[j4 + j + 1]);
@@ -3233,9 +3252,8 @@ void prefill_mfma16_kernel(PfArgs a) {
         const int kofs = kt_off<D>(key, ej >> 3) + 8 * ((ej >> 2) & 1);
         const int vofs = vt_off<D>(key, ej >> 3) + 8 * ((ej >> 2) & 1);
 #pragma unroll
-        for (int p = 0; p < KP; ++p) {
-          if (KP != 3 || p < 2)  // K's third piece holds the row's unit only
-            *reinterpret_cast<u32x2*>(kp_s + p * KT * KRB + kofs) = u32x2{kpc[p][0], kpc[p][1]};
+        for (int p = 0; p < (KP == 3 ? 2 : 1); ++p) {  // the third piece holds the row's unit only
+          *reinterpret_cast<u32x2*>(kp_s + p * KT * KRB + kofs) = u32x2{kpc[p][0], kpc[p][1]};
           *reinterpret_cast<u32x2*>(vp_s + p * KT * VRB + vofs) = u32x2{vpc[p][0], vpc[p][1]};
         }
       }
@@ -3339,14 +3357,14 @@ void prefill_mfma16_kernel(PfArgs a) {
   // online softmax (base 2) of this lane's row over its 8 keys of the tile
   // at tk.  Lazy rescale, as in the decode kernel: the running max moves
   // only when a score exceeds it by more than kLazyMax (p <= 2^8 otherwise);
-  // o and l always share the max they were formed with.  Leaves P^T as
-  // pieces (B operand: slot 4u + r holds key 16u + 4*g4 + r), the factor
-  // alpha that o and l take before P is added (1 unless the max moved) and
-  // the tile's row sum.
+  // o and l always share the max they were formed with.  Leaves P^T (the
+  // B operand's order: pv[4u + r] is key 16u + 4*g4 + r), the factor alpha
+  // that o and l take before P is added (1 unless the max moved) and the
+  // tile's row sum.
   // FULL (a std::integral_constant): every key of the tile is in every
   // row's range, so no key is masked and every probability is an exp.
-  auto softmax = [&](auto FULL, const f32x4 (&sacc)[KH], int tk, bf16x8_t& ph, bf16x8_t& pm,
-                     bf16x8_t& pl, float& alpha, bool& grow, float& ps) {
+  auto softmax = [&](auto FULL, const f32x4 (&sacc)[KH], int tk, float (&pv)[4 * KH],
+                     float& alpha, bool& grow, int& gsh, float& ps) {
     constexpr bool full = decltype(FULL)::value;
     float sv[KH][4];
     float tmax = -INFINITY;
@@ -3362,8 +3380,9 @@ void prefill_mfma16_kernel(PfArgs a) {
     grow = tmax > m_run + kLazyMax;  // false while the row has no key (-inf)
     const float mn = grow ? fmaxf(m_run, tmax) : m_run;
     alpha = m_run == -INFINITY ? 1.f : exp2_hw(m_run - mn);  // exp2(0) = 1 exactly
+    // floor(log2(1 / alpha)) (> 8, at most 1000) when a finite max moved
+    gsh = (grow && m_run != -INFINITY) ? (int)fminf(floorf(mn - m_run), 1000.f) : 0;
     m_run = mn;
-    float pv[4 * KH];
     ps = 0.f;
 #pragma unroll
     for (int u = 0; u < KH; ++u)
@@ -3372,45 +3391,102 @@ void prefill_mfma16_kernel(PfArgs a) {
         pv[4 * u + r] = (!full && sv[u][r] == -INFINITY) ? 0.f : exp2_hw(sv[u][r] - m_run);
         ps += pv[4 * u + r];
       }
-    uint32_t ph4[4], pm4[4], pl4[4];
-#pragma unroll
-    for (int e = 0; e < 8; e += 2) split3x2(pv[e], pv[e + 1], ph4[e / 2], pm4[e / 2], pl4[e / 2]);
-    ph = __builtin_bit_cast(bf16x8_t, u32x4{ph4[0], ph4[1], ph4[2], ph4[3]});
-    pm = __builtin_bit_cast(bf16x8_t, u32x4{pm4[0], pm4[1], pm4[2], pm4[3]});
-    pl = __builtin_bit_cast(bf16x8_t, u32x4{pl4[0], pl4[1], pl4[2], pl4[3]});
   };
-  // o += P V over the tile at vp_s: V^T of the 16-row block dt by two
-  // transposed reads per piece, NDT blocks at a time: their operands first,
-  // then the piece products piece by piece across the NDT accumulators
-  // (each in the same order as one block at a time)
-  auto pv_acc = [&](const char* vp_s, const bf16x8_t& ph, const bf16x8_t& pm,
-                    const bf16x8_t& pl) {
+  // V^T of the 16-row blocks dt0 .. dt0 + NDT - 1 (A operands of PV), piece
+  // p of the staged tile at vp_s: two transposed reads per block
+  auto read_vt = [&](const char* vp_s, int dt0, int p, auto& av) {
 #pragma unroll
-    for (int dt0 = 0; dt0 < DT; dt0 += NDT) {
-      bf16x8_t av[NDT][KP];
+    for (int j = 0; j < NDT; ++j) {
+      i16x4_t t2[2];
 #pragma unroll
-      for (int j = 0; j < NDT; ++j)
+      for (int u = 0; u < 2; ++u) {
+        const int r = (lane >> 2) + 16 * u;
+        t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(
+                vp_s + p * KT * VRB + vt_off<D>(r, 2 * (dt0 + j) + ((lane & 3) >> 1)) +
+                8 * (lane & 1)));
+      }
+      av[j][p] = __builtin_bit_cast(typename std::remove_reference<decltype(av[j][p])>::type,
+                                    __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+  };
+  // fp32 and Q8 values (KP = 3): PV takes y = p * u_key * 2^wsh as two fp16
+  // pieces, u_key the key's V row unit (V's pieces are the row over u_key),
+  // so that o = 2^wsh * sum p v.  wsh (per query row: this lane's column of
+  // O^T) keeps y below 2^14: it follows the largest p * u_key of the row's
+  // keys so far, and when the running max moves (o and l scaled by alpha)
+  // it may grow by floor(log2(1 / alpha)), so that the unit follows o down.
+  // Each term is then held to 2^-22 of itself, or to 2^-25 of the
+  // row's unit 2^(14 - wsh) (2^-37 of its largest p * |v| term) below.
+  constexpr int kNoShift = 1 << 20;  // no key yet (o = 0)
+  [[maybe_unused]] int wsh = kNoShift;
+  // o += P V over the tile at vp_s.  bf16 caches (exact V): P as three bf16
+  // pieces, V^T of NDT 16-row blocks at a time, their operands first, then
+  // the piece products piece by piece across the NDT accumulators (each in
+  // the same order as one block at a time).  fp32 and Q8 values: y and V as
+  // two fp16 pieces each, three products per term (lo*hi, hi*lo, hi*hi; the
+  // dropped lo*lo is within 2^-22 of the term), as the scores.  gsh: the
+  // softmax's floor(log2(1 / alpha)) when the running max moved, else 0.
+  auto pv_acc = [&](const char* vp_s, const float (&pv)[4 * KH], int gsh) {
+    if constexpr (KP == 3) {
+      float z[4 * KH];  // p * u_key, u_key from the key row's third piece
+      float zt = 0.f;
 #pragma unroll
-        for (int p = 0; p < KP; ++p) {
-          i16x4_t t2[2];
+      for (int u = 0; u < KH; ++u)
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int r = (lane >> 2) + 16 * u;
-            t2[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4_t*)(
-                    vp_s + p * KT * VRB + vt_off<D>(r, 2 * (dt0 + j) + ((lane & 3) >> 1)) +
-                    8 * (lane & 1)));
+        for (int r = 0; r < 4; ++r) {
+          const int key = 16 * u + 4 * g4 + r;
+          const float uk =
+              *reinterpret_cast<const float*>(vp_s + 2 * KT * VRB + key * VRB + 16 * vt_f<D>(key));
+          z[4 * u + r] = pv[4 * u + r] * uk;
+          zt = fmaxf(zt, z[4 * u + r]);
+        }
+      zt = max_xor32(max_xor16(zt));  // the row's 32 keys (its column's 4 lanes)
+      const int ns = min(min(wsh + gsh, kNoShift), zt > 0.f ? f16_row_shift(zt) : kNoShift);
+      if (__builtin_amdgcn_ballot_w64(ns != wsh) != 0) {  // o into the new unit (exact)
+        const int dsh = ns - wsh;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[dt][i] = ldexpf(o[dt][i], dsh);
+      }
+      wsh = ns;
+      uint32_t h4[4], l4[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) split2h(z[e], z[e + 1], ns, h4[e / 2], l4[e / 2]);
+      const f16x8_t yh = __builtin_bit_cast(f16x8_t, u32x4{h4[0], h4[1], h4[2], h4[3]});
+      const f16x8_t yl = __builtin_bit_cast(f16x8_t, u32x4{l4[0], l4[1], l4[2], l4[3]});
+#pragma unroll
+      for (int dt0 = 0; dt0 < DT; dt0 += NDT) {
+        f16x8_t av[NDT][2];
+        read_vt(vp_s, dt0, 0, av);
+        read_vt(vp_s, dt0, 1, av);
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+          for (int j = 0; j < NDT; ++j)
+            o[dt0 + j] = mfma_f16(av[j][FPK[t]], FPQ[t] == 0 ? yh : yl, o[dt0 + j]);
+      }
+    } else {
+      uint32_t ph4[4], pm4[4], pl4[4];
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) split3x2(pv[e], pv[e + 1], ph4[e / 2], pm4[e / 2], pl4[e / 2]);
+      const bf16x8_t ph = __builtin_bit_cast(bf16x8_t, u32x4{ph4[0], ph4[1], ph4[2], ph4[3]});
+      const bf16x8_t pm = __builtin_bit_cast(bf16x8_t, u32x4{pm4[0], pm4[1], pm4[2], pm4[3]});
+      const bf16x8_t pl = __builtin_bit_cast(bf16x8_t, u32x4{pl4[0], pl4[1], pl4[2], pl4[3]});
+#pragma unroll
+      for (int dt0 = 0; dt0 < DT; dt0 += NDT) {
+        bf16x8_t av[NDT][KP];
+#pragma unroll
+        for (int p = 0; p < KP; ++p) read_vt(vp_s, dt0, p, av);
+#pragma unroll
+        for (int t = 0; t < NPR; ++t)
+#pragma unroll
+          for (int j = 0; j < NDT; ++j) {
+            const bf16x8_t& pp = PRQ[t] == 0 ? ph : PRQ[t] == 1 ? pm : pl;
+            o[dt0 + j] = mfma_bf16(av[j][PRK[t]], pp, o[dt0 + j]);
           }
-          av[j][p] = __builtin_bit_cast(
-              bf16x8_t, __builtin_shufflevector(t2[0], t2[1], 0, 1, 2, 3, 4, 5, 6, 7));
-        }
-#pragma unroll
-      for (int t = 0; t < NPR; ++t)
-#pragma unroll
-        for (int j = 0; j < NDT; ++j) {
-          const bf16x8_t& pp = PRQ[t] == 0 ? ph : PRQ[t] == 1 ? pm : pl;
-          o[dt0 + j] = mfma_bf16(av[j][PRK[t]], pp, o[dt0 + j]);
-        }
+      }
     }
   };
   // o and l take alpha, then l the tile's sum (two roundings, as the
@@ -3443,13 +3519,14 @@ void prefill_mfma16_kernel(PfArgs a) {
       if (more) dload1(tk + KT, kp_buf[(it + 1) & 1], 0);
       f32x4 sacc[KH];
       scores(kp_buf[it & 1], sacc);
-      bf16x8_t ph, pm, pl;
+      float pv[4 * KH];
       float alpha, ps;
       bool grow;
+      int gsh;
       if (__builtin_amdgcn_ballot_w64(!(rv && tk >= rt0 && tk + KT <= rnn)) == 0)
-        softmax(std::true_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+        softmax(std::true_type{}, sacc, tk, pv, alpha, grow, gsh, ps);
       else
-        softmax(std::false_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+        softmax(std::false_type{}, sacc, tk, pv, alpha, grow, gsh, ps);
       rescale(alpha, grow, ps);
       // V(it) is in LDS (K(it+1), copied after it, may still be in flight)
       if (more)
@@ -3457,7 +3534,7 @@ void prefill_mfma16_kernel(PfArgs a) {
       else
         wait_vmcnt<0>();
       lds_barrier();
-      pv_acc(vp_buf[0], ph, pm, pl);
+      pv_acc(vp_buf[0], pv, gsh);
       if (more) {
         lds_barrier();  // every wave is past PV(it)
         dload1(tk + KT, vp_buf[0], 1);
@@ -3490,16 +3567,17 @@ void prefill_mfma16_kernel(PfArgs a) {
       }
       f32x4 sacc[KH];
       scores(kp_s, sacc);
-      bf16x8_t ph, pm, pl;
+      float pv[4 * KH];
       float alpha, ps;
       bool grow;
+      int gsh;
       // interior tile: every row of the wave attends all of its keys
       if (__builtin_amdgcn_ballot_w64(!(rv && tk >= rt0 && tk + KT <= rnn)) == 0)
-        softmax(std::true_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+        softmax(std::true_type{}, sacc, tk, pv, alpha, grow, gsh, ps);
       else
-        softmax(std::false_type{}, sacc, tk, ph, pm, pl, alpha, grow, ps);
+        softmax(std::false_type{}, sacc, tk, pv, alpha, grow, gsh, ps);
       rescale(alpha, grow, ps);
-      pv_acc(vp_s, ph, pm, pl);
+      pv_acc(vp_s, pv, gsh);
       if constexpr (PRE) {
         if constexpr (NBUF == 1) {
           __syncthreads();  // every wave is done with the buffer
@@ -3513,6 +3591,12 @@ void prefill_mfma16_kernel(PfArgs a) {
     }
   }
   l_run = sum_xor32(sum_xor16(l_run));
+  if constexpr (KP == 3) {  // o back from 2^wsh * sum p v (a power of two; no key: o = 0)
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dt][i] = ldexpf(o[dt][i], -wsh);
+  }
   if (rv && a.nsplit > 1) {  // the split's partial: unnormalised o, max in natural units, sum
     const int64_t ps = ((int64_t)m * a.nq + h * G + g) * a.nsplit + sp;
     float* po = a.part_o + ps * D;

@@ -377,6 +377,47 @@ def test_prefill_row_scales(gpu, kv, presplit):
     assert err < TOL
 
 
+@pytest.mark.parametrize("kv", ["f32", "q8"])
+@pytest.mark.parametrize("presplit", [True, False])
+def test_prefill_v_row_scales(gpu, kv, presplit):
+    """PV over fp32 and Q8 values takes V rows as two fp16 pieces of the row
+    scaled by a power of two, the rows' units folded into P, keys more than
+    2^7 below a tile's largest unit in further bands.  V rows 2^-20 .. 2^20
+    apart, with each key's score lowered by its row's exponent (q channel 0
+    times K channel 0 adds -e ln 2), so that every scale contributes to O
+    alike and a band dropped or misweighted shows; against the oracle."""
+    announce(f"prefill V row scales kv={kv} presplit={presplit}")
+    nq, nkv, d, M, N, pos0 = 16, 4, 128, 64, 1064, 1000
+    st = Stream(960 + (kv == "q8") + 2 * presplit)
+    e = np.random.default_rng(961).integers(-20, 21, size=N)
+    s = 1 / math.sqrt(d)
+    c = 8.0
+    V = (st.normal((N, nkv * d)) * np.exp2(e)[:, None]).astype(np.float32)
+    K = st.normal((N, nkv * d))
+    for h in range(nkv):
+        K[:, h * d] = -e * math.log(2) / (c * s)
+    K = K.astype(np.float32)
+    Q = st.normal((M, nq, d))
+    Q[:, :, 0] = c
+    Q = Q.astype(np.float32)
+    if kv == "q8":
+        K, V = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
+        Kd = torch.from_numpy(np.ascontiguousarray(K, dtype=np.uint8)).cuda()
+        Vd = torch.from_numpy(np.ascontiguousarray(V, dtype=np.uint8)).cuda()
+    else:
+        Kd, Vd = dev(K), dev(V)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.set_prefill_presplit(presplit)
+    try:
+        attn.attn_prefill_gqa(dev(Q), Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)
+    finally:
+        attn.set_prefill_presplit(True)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, 0)
+    err = normwise_err(host(O), R)
+    print(f"V row scales normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
 def test_prefill_2k_prompt(gpu):
     """A 2048-token prompt at the headline head shape (the bench workload)."""
     announce("prefill 32q/8kv/d128 M=2048 fresh")
