@@ -690,7 +690,7 @@ __global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeAr
     // the row's pieces for the prefill (of the cached values: fp32 as
     // stored, Q8 as code * scale), the bits pf_split_kernel writes: K and
     // V as two fp16 pieces of the row scaled by a power of two (split2h,
-    // the row's unit in the first 4 bytes of the third piece)
+    // the row's unit at float pr of the head's third piece)
     const int pr = slot - a.pc_T0;
     if (a.pieces && a.kv_dtype != MOLOT_KV_BF16 && pr >= 0 && pr < a.pc_R) {
       const int64_t pstride = (int64_t)a.pc_R * a.d;  // one piece of one head
@@ -711,9 +711,10 @@ __global__ __launch_bounds__(kRopeTokThreads) void rope_append_tok_kernel(RopeAr
       const int vshift = f16_vrow_shift(vpm);
       uint16_t* ok = a.pieces + (int64_t)kh * 3 * pstride + (int64_t)pr * a.d;
       uint16_t* ov = ok + (int64_t)a.nkv * 3 * pstride;
-      if (lane == 0) {
-        *reinterpret_cast<float*>(ok + 2 * pstride) = f16_row_unit(kshift);
-        *reinterpret_cast<float*>(ov + 2 * pstride) = f16_vrow_unit(vpm, vshift);
+      if (lane == 0) {  // the units of a head's rows side by side in its third piece
+        reinterpret_cast<float*>(ok - (int64_t)pr * a.d + 2 * pstride)[pr] = f16_row_unit(kshift);
+        reinterpret_cast<float*>(ov - (int64_t)pr * a.d + 2 * pstride)[pr] =
+            f16_vrow_unit(vpm, vshift);
       }
 #pragma unroll
       for (int k = 0; k < KMAX; ++k) {
@@ -2882,8 +2883,8 @@ __device__ __forceinline__ int64_t pf_row_off(const PfArgs& a, int h, int t, int
 // K and V of the keys [T0, T0 + R) as pieces (the values the prefill kernel
 // would split per tile: fp32 rows, or Q8 code * s), into [K, V][nkv][3][R][D]
 // (16-bit elements): K and V rows as two fp16 pieces of the row scaled by a
-// power of two (split2h) with the row's unit (a float) at the start of the
-// third.  Thread: one 8-element unit of one row, a row's D/8 units in
+// power of two (split2h), the rows' units (floats) side by side at the start
+// of the third.  Thread: one 8-element unit of one row, a row's D/8 units in
 // consecutive lanes; grid (units / 256, nkv, 2).
 template <int D, typename T, bool PAGED>
 __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) {
@@ -2918,7 +2919,7 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
   }
   auto row = [&](int p) { return out + ((((int64_t)kv * a.nkv + h) * 3 + p) * a.R + r) * D; };
   // two fp16 pieces of the row scaled by a power of two (split2h), the
-  // row's unit (a float) at the start of the third piece
+  // row's unit (a float) at float r of the head's third piece
   uint32_t pc[2][4];
   float xm = 0.f;
 #pragma unroll
@@ -2927,7 +2928,9 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
   const int shift = kv ? f16_vrow_shift(xm) : f16_row_shift(xm);
 #pragma unroll
   for (int e = 0; e < 8; e += 2) split2h(x[e], x[e + 1], shift, pc[0][e / 2], pc[1][e / 2]);
-  if (j == 0) *reinterpret_cast<float*>(row(2)) = kv ? f16_vrow_unit(xm, shift) : f16_row_unit(shift);
+  if (j == 0)  // the units of a head's rows side by side in its third piece: row r's at float r
+    reinterpret_cast<float*>(out + (((int64_t)kv * a.nkv + h) * 3 + 2) * a.R * D)[r] =
+        kv ? f16_vrow_unit(xm, shift) : f16_row_unit(shift);
 #pragma unroll
   for (int p = 0; p < 2; ++p)
     *reinterpret_cast<u32x4*>(row(p) + 8 * j) = u32x4{pc[p][0], pc[p][1], pc[p][2], pc[p][3]};
@@ -2945,6 +2948,14 @@ __global__ __launch_bounds__(256) void pf_split_kernel(PfArgs a, uint16_t* out) 
 // between that write and the copy.
 __device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :
+               : "v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+// The same with 4 bytes a lane (global_load_lds_dword): lane l's 4 bytes
+// land at LDS address lds + 4*l.
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
                :
                : "v"(off), "s"(base), "{m0}"(lds)
                : "memory");
@@ -2976,8 +2987,8 @@ constexpr int kPfWaves = 8;
 //   K [KP][32 keys][D] 16-bit, 16-byte units XOR-swizzled by key (kt_off),
 //     read as the A operand of S^T = K . Q^T: lane l key 16u + l%16,
 //     elements 32s + 8(l/16) .. +7, Q^T in the same element order in
-//     registers; fp32 and Q8 values: pieces 0 and 1 fp16 hi and lo, piece
-//     2 the row's unit (a float at its start, f16_row_unit);
+//     registers; fp32 and Q8 values: pieces 0 and 1 fp16 hi and lo, the
+//     third slot the tile's 32 row units side by side (floats, f16_row_unit);
 //   V [KP][32 keys][D] 16-bit, 16-byte units XOR-swizzled by key (vt_off),
 //     read as V^T by ds_read_b64_tr_b16 as in attn_mfma_kernel: the A
 //     operand of O^T += V^T . P^T, with P in the registers the score
@@ -3129,19 +3140,31 @@ void prefill_mfma16_kernel(PfArgs a) {
   // The source is a wave-uniform row base (the tile's first key) plus a
   // 32-bit lane offset (key within the tile, clamped to the range's last
   // key, and its unit), so the loads take a scalar base and the per-tile
-  // address arithmetic stays off the vector ALU.
+  // address arithmetic stays off the vector ALU.  The two pieces, then the
+  // tile's 32 row units (128 bytes, dma4) to the start of the third piece
+  // slot
+  // (all 64 lanes: lanes 32..63 repeat the last key's unit into the unused
+  // bytes 128..255 of the slot, so no lane is masked off)
+  auto dunits = [&](int tk, char* buf, int kv) {
+    const char* units = reinterpret_cast<const char*>(
+        a.pieces + (((int64_t)kv * a.nkv + h) * 3 + 2) * a.R * D) + 4 * (int64_t)(tk - a.T0);
+    const uint32_t lo = (uint32_t)(4 * min(min(lane, KT - 1), kt_hi - 1 - tk));
+    dma4(units, lo, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)(
+                        buf + 2 * KT * (2 * D)));
+  };
   auto dload = [&](int tk, char* kbuf, char* vbuf) {
     constexpr int UPR = D / 8;             // 16-byte units per row
     constexpr int KPB = 64 / UPR;          // keys per 1 KB block
     constexpr int BPP = KT / KPB;          // blocks per piece
-    constexpr int NBL = 2 * 3 * BPP;       // blocks per tile (K, V; 3 pieces)
+    constexpr int NBL = 2 * 2 * BPP;       // blocks per tile (K, V; 2 pieces)
     const int r_in = lane / UPR, jpos = lane % UPR;
     const int lastr = kt_hi - 1 - tk;      // the range's last key, from the tile's first
+    if (w < 2) dunits(tk, w ? vbuf : kbuf, w);
 #pragma unroll
     for (int bi0 = 0; bi0 < NBL; bi0 += PW) {
       const int bi = bi0 + w;  // wave-uniform
       if (NBL % PW != 0 && bi >= NBL) break;
-      const int kv = bi / (3 * BPP), rem = bi - kv * 3 * BPP;
+      const int kv = bi / (2 * BPP), rem = bi - kv * 2 * BPP;
       const int pc = rem / BPP, kb = rem - pc * BPP;
       const int r = kb * KPB + r_in;
       const int ch = jpos ^ (kv ? vt_f<D>(r) : kt_f<D>(r));
@@ -3152,15 +3175,18 @@ void prefill_mfma16_kernel(PfArgs a) {
       dma16(rows, lo, (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)dst);
     }
   };
-  // K (kv = 0) or V (kv = 1) of a tile alone: NL copies a wave
-  constexpr int NL = 3 * (KT / (64 / (D / 8))) / PW;
+  // K (kv = 0) or V (kv = 1) of a tile alone: NL copies a wave (every wave
+  // copies the units, the same bytes to the same place, so that the waves
+  // count alike)
+  constexpr int NL = 2 * (KT / (64 / (D / 8))) / PW + 1;
   auto dload1 = [&](int tk, char* buf, int kv) {
     constexpr int UPR = D / 8, KPB = 64 / UPR, BPP = KT / KPB;
-    static_assert(!KKV || (3 * BPP) % PW == 0, "the same copies in every wave");
+    static_assert(!KKV || (2 * BPP) % PW == 0, "the same copies in every wave");
     const int r_in = lane / UPR, jpos = lane % UPR;
     const int lastr = kt_hi - 1 - tk;
+    dunits(tk, buf, kv);
 #pragma unroll
-    for (int bi0 = 0; bi0 < 3 * BPP; bi0 += PW) {
+    for (int bi0 = 0; bi0 < 2 * BPP; bi0 += PW) {
       const int bi = bi0 + w;  // wave-uniform
       const int pc = bi / BPP, kb = bi - pc * BPP;
       const int r = kb * KPB + r_in;
@@ -3228,11 +3254,9 @@ void prefill_mfma16_kernel(PfArgs a) {
         kshift = f16_row_shift(group_max<NCR>(km));
         vm = group_max<NCR>(vm);
         vshift = f16_vrow_shift(vm);
-        if (e == 0) {
-          *reinterpret_cast<float*>(kp_s + 2 * KT * KRB + key * KRB + 16 * kt_f<D>(key)) =
-              f16_row_unit(kshift);
-          *reinterpret_cast<float*>(vp_s + 2 * KT * VRB + key * VRB + 16 * vt_f<D>(key)) =
-              f16_vrow_unit(vm, vshift);
+        if (e == 0) {  // the tile's row units side by side in the third slot
+          reinterpret_cast<float*>(kp_s + 2 * KT * KRB)[key] = f16_row_unit(kshift);
+          reinterpret_cast<float*>(vp_s + 2 * KT * VRB)[key] = f16_vrow_unit(vm, vshift);
         }
       }
 #pragma unroll
@@ -3341,17 +3365,13 @@ void prefill_mfma16_kernel(PfArgs a) {
 #pragma unroll
     for (int u = 0; u < KH; ++u) sacc[u] = sacc2[u][0] + sacc2[u][1];
     if constexpr (KP == 3) {
-      // key 16u + 4*g4 + r's unit: the float at the start of its row of the
-      // third K piece (unit 0 of a staged row sits at unit kt_f(row))
+      // keys 16u + 4*g4 .. +3's units: floats 16u + 4*g4 .. of the third slot
 #pragma unroll
-      for (int u = 0; u < KH; ++u)
+      for (int u = 0; u < KH; ++u) {
+        const f32x4 ku = *reinterpret_cast<const f32x4*>(kp_s + 2 * KT * KRB + 4 * (16 * u + 4 * g4));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = 16 * u + 4 * g4 + r;
-          const float ku =
-              *reinterpret_cast<const float*>(kp_s + 2 * KT * KRB + key * KRB + 16 * kt_f<D>(key));
-          sacc[u][r] *= qunit * ku;
-        }
+        for (int r = 0; r < 4; ++r) sacc[u][r] *= qunit * ku[r];
+      }
     }
   };
   // online softmax (base 2) of this lane's row over its 8 keys of the tile
@@ -3429,18 +3449,17 @@ void prefill_mfma16_kernel(PfArgs a) {
   // softmax's floor(log2(1 / alpha)) when the running max moved, else 0.
   auto pv_acc = [&](const char* vp_s, const float (&pv)[4 * KH], int gsh) {
     if constexpr (KP == 3) {
-      float z[4 * KH];  // p * u_key, u_key from the key row's third piece
+      float z[4 * KH];  // p * u_key, u_key from the tile's units in the third slot
       float zt = 0.f;
 #pragma unroll
-      for (int u = 0; u < KH; ++u)
+      for (int u = 0; u < KH; ++u) {
+        const f32x4 uk = *reinterpret_cast<const f32x4*>(vp_s + 2 * KT * VRB + 4 * (16 * u + 4 * g4));
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = 16 * u + 4 * g4 + r;
-          const float uk =
-              *reinterpret_cast<const float*>(vp_s + 2 * KT * VRB + key * VRB + 16 * vt_f<D>(key));
-          z[4 * u + r] = pv[4 * u + r] * uk;
+          z[4 * u + r] = pv[4 * u + r] * uk[r];
           zt = fmaxf(zt, z[4 * u + r]);
         }
+      }
       zt = max_xor32(max_xor16(zt));  // the row's 32 keys (its column's 4 lanes)
       const int ns = min(min(wsh + gsh, kNoShift), zt > 0.f ? f16_row_shift(zt) : kNoShift);
       if (__builtin_amdgcn_ballot_w64(ns != wsh) != 0) {  // o into the new unit (exact)
