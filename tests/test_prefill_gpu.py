@@ -418,6 +418,46 @@ def test_prefill_v_row_scales(gpu, kv, presplit):
     assert err < TOL
 
 
+@pytest.mark.parametrize("kv", ["f32", "q8"])
+@pytest.mark.parametrize("presplit", [True, False])
+def test_prefill_ramp_scales(gpu, kv, presplit):
+    """Scores that rise along the keys by 40 (log2 units) while the V rows
+    fall by 2^-40, so that p * v stays alike: the running max keeps moving,
+    and each query row's PV unit has to follow o down with it (a unit kept
+    at the early keys' scale would hold the late keys' terms to 2^-40 of
+    it).  Prompt rows see the whole ramp; against the oracle."""
+    announce(f"prefill ramp scales kv={kv} presplit={presplit}")
+    nq, nkv, d, M, N, pos0 = 16, 4, 128, 64, 1064, 1000
+    st = Stream(970 + (kv == "q8") + 2 * presplit)
+    e = np.round(np.arange(N) * 40.0 / N) - 20.0
+    s = 1 / math.sqrt(d)
+    c = 8.0
+    V = (st.normal((N, nkv * d)) * np.exp2(-e)[:, None]).astype(np.float32)
+    K = st.normal((N, nkv * d))
+    for h in range(nkv):
+        K[:, h * d] = e * math.log(2) / (c * s)
+    K = K.astype(np.float32)
+    Q = st.normal((M, nq, d))
+    Q[:, :, 0] = c
+    Q = Q.astype(np.float32)
+    if kv == "q8":
+        K, V = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
+        Kd = torch.from_numpy(np.ascontiguousarray(K, dtype=np.uint8)).cuda()
+        Vd = torch.from_numpy(np.ascontiguousarray(V, dtype=np.uint8)).cuda()
+    else:
+        Kd, Vd = dev(K), dev(V)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.set_prefill_presplit(presplit)
+    try:
+        attn.attn_prefill_gqa(dev(Q), Kd, Vd, O, nq, nkv, M, N, d, s, pos0, 0)
+    finally:
+        attn.set_prefill_presplit(True)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, 0)
+    err = normwise_err(host(O), R)
+    print(f"ramp scales normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
 def test_prefill_2k_prompt(gpu):
     """A 2048-token prompt at the headline head shape (the bench workload)."""
     announce("prefill 32q/8kv/d128 M=2048 fresh")
