@@ -3366,11 +3366,13 @@ void prefill_mfma16_kernel(PfArgs a) {
     for (int u = 0; u < KH; ++u) sacc[u] = sacc2[u][0] + sacc2[u][1];
     if constexpr (KP == 3) {
       // keys 16u + 4*g4 .. +3's units: floats 16u + 4*g4 .. of the third slot
+      // (the q row's unit, the same for the row's every score, is the
+      // softmax's: its max and exponent arguments take it)
 #pragma unroll
       for (int u = 0; u < KH; ++u) {
         const f32x4 ku = *reinterpret_cast<const f32x4*>(kp_s + 2 * KT * KRB + 4 * (16 * u + 4 * g4));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sacc[u][r] *= qunit * ku[r];
+        for (int r = 0; r < 4; ++r) sacc[u][r] *= ku[r];
       }
     }
   };
@@ -3396,7 +3398,10 @@ void prefill_mfma16_kernel(PfArgs a) {
         sv[u][r] = (full || (t >= rt0 && t < rnn)) ? sacc[u][r] : -INFINITY;
         tmax = fmaxf(tmax, sv[u][r]);
       }
-    tmax = max_xor32(max_xor16(tmax));
+    // the scores over fp32 and Q8 values still lack the q row's unit qunit
+    // (a power of two): tmax takes it, and each exponent argument as one fma,
+    // s * qunit - m, rounded once as the difference of the scaled score was
+    tmax = max_xor32(max_xor16(tmax)) * qunit;
     grow = tmax > m_run + kLazyMax;  // false while the row has no key (-inf)
     const float mn = grow ? fmaxf(m_run, tmax) : m_run;
     alpha = m_run == -INFINITY ? 1.f : exp2_hw(m_run - mn);  // exp2(0) = 1 exactly
@@ -3408,7 +3413,8 @@ void prefill_mfma16_kernel(PfArgs a) {
     for (int u = 0; u < KH; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        pv[4 * u + r] = (!full && sv[u][r] == -INFINITY) ? 0.f : exp2_hw(sv[u][r] - m_run);
+        pv[4 * u + r] =
+            (!full && sv[u][r] == -INFINITY) ? 0.f : exp2_hw(fmaf(sv[u][r], qunit, -m_run));
         ps += pv[4 * u + r];
       }
   };
