@@ -458,6 +458,38 @@ def test_prefill_ramp_scales(gpu, kv, presplit):
     assert err < TOL
 
 
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("kv", ["f32", "q8"])
+@pytest.mark.parametrize("window", [0, 200])
+def test_prefill_random_row_scales(gpu, d, kv, window):
+    """K and V rows each scaled by their own 2^U(-12, 12), q rows by
+    2^U(-6, 6), at every head dim the matrix-core prefill tiles, with and
+    without a window: the row units of the scores and of PV, and the query
+    rows' PV shifts, over scales that move from row to row; against the
+    oracle."""
+    announce(f"prefill random row scales d={d} kv={kv} window={window}")
+    nq, nkv, M, N, pos0 = 8, 2, 70, 600, 530
+    rng = np.random.default_rng(980 + d + (kv == "q8") + window)
+    st = Stream(981 + d + (kv == "q8") + window)
+    K = (st.normal((N, nkv * d)) * np.exp2(rng.uniform(-12, 12, size=N))[:, None]).astype(np.float32)
+    V = (st.normal((N, nkv * d)) * np.exp2(rng.uniform(-12, 12, size=N))[:, None]).astype(np.float32)
+    Q = (st.normal((M, nq, d)) * np.exp2(rng.uniform(-6, 6, size=(M, nq)))[:, :, None])
+    Q = Q.astype(np.float32)
+    if kv == "q8":
+        K, V = oracle.q8_cache(K, nkv, d), oracle.q8_cache(V, nkv, d)
+        Kd = torch.from_numpy(np.ascontiguousarray(K, dtype=np.uint8)).cuda()
+        Vd = torch.from_numpy(np.ascontiguousarray(V, dtype=np.uint8)).cuda()
+    else:
+        Kd, Vd = dev(K), dev(V)
+    s = 2.0 ** -12 / math.sqrt(d)
+    O = torch.empty((M, nq, d), device="cuda")
+    attn.attn_prefill_gqa(dev(Q), Kd, Vd, O, nq, nkv, M, N, d, s, pos0, window)
+    R = oracle.attn_prefill(Q, K, V, nq, nkv, M, N, d, s, pos0, window)
+    err = normwise_err(host(O), R)
+    print(f"random row scales normwise err {err:.3e}", flush=True)
+    assert err < TOL
+
+
 def test_prefill_2k_prompt(gpu):
     """A 2048-token prompt at the headline head shape (the bench workload)."""
     announce("prefill 32q/8kv/d128 M=2048 fresh")
